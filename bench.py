@@ -1,0 +1,156 @@
+"""Benchmark: 40-step Joint-CFG RF sampling of a 750-frame latent on
+one MI355X through libirodori_hip, plus the roofline of the dominant kernel and the CPU
+oracle timed on the host's cores.
+
+A bench "step" is one whole RF run (40 Euler steps, each one B=2 DiT forward + CFG
+combine + Euler update), with its inputs already resident in HBM.  Prints one JSON line.
+
+    python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--cpu-threads N]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "irodori-tts-burn_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "RF ms per 40 steps @750 frames, B=2 joint CFG; attn/MLP MFMA util %"
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0
+
+
+def log(msg):
+    print("[bench] " + msg, file=sys.stderr, flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--profile-iters", type=int, default=50)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only (the RF step of one model instance "
+              "runs on one MI355X; multi-GPU sharding is by utterance and is not part of this "
+              "build). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import irodori_hip as ih
+
+    cfg = ih.cfg_full_rf()
+    U, S, Tt, Ts, N, SCALE = 1, 750, 256, 375, 40, 3.0
+    log("generating seeded random-init weights (12 x d1024) and inputs")
+    w = ih.DitWeights.random(cfg, 0)
+    ctx = ih.make_context_kv(cfg, U, Tt, Ts, seed=1)
+    x0 = ih.make_noise(U, S, cfg.latent_dim, 2)
+    g = ih.GuidanceConfig(mode=ih.CfgGuidanceMode.JOINT, scale_text=SCALE, scale_speaker=SCALE,
+                          min_t=0.0, max_t=1.0)
+    params = ih.SamplerParams(num_steps=N, guidance=g)
+
+    log("creating HIP context and ingesting weights")
+    eng = ih.HipInferenceEngine(cfg, ih.InferenceBackendKind.HIP_BF16, max_rows=2 * U,
+                                max_seq=S, max_ctx=Tt + Ts)
+    eng.load_weights(w)
+    eng.set_context_kv(ctx)
+    d_x0 = torch.from_numpy(x0).to("cuda")
+    d_out = torch.empty_like(d_x0)
+    torch.cuda.synchronize()
+
+    for i in range(args.warmup):
+        eng.sample_device(d_x0.data_ptr(), d_out.data_ptr(), U, S, params)
+    torch.cuda.synchronize()
+    log("warmup done (%d runs); timing %d runs" % (args.warmup, args.steps))
+    times = []
+    for i in range(args.steps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        eng.sample_device(d_x0.data_ptr(), d_out.data_ptr(), U, S, params)
+        torch.cuda.synchronize()
+        times.append((time.perf_counter() - t0) * 1e3)
+    ms = float(np.mean(times))
+    log("RF run: mean %.2f ms, p50 %.2f ms, min %.2f ms" % (ms, float(np.median(times)), min(times)))
+    out = d_out.cpu().numpy()
+    assert np.all(np.isfinite(out)), "non-finite sampler output"
+
+    # Per-kernel device time (HIP events on the context's stream) for one block.
+    kt = eng.profile_layer(2 * U, S, args.profile_iters)
+    log("kernel us: " + ", ".join("%s=%.1f" % (k, v) for k, v in kt.items()))
+    M, D, F, H, Dh = 2 * U * S, cfg.model_dim, cfg.mlp_hidden, cfg.num_heads, cfg.head_dim
+    flops = {
+        "qkvg_gemm": 2.0 * M * D * 4 * D,
+        "wo_gemm": 2.0 * M * D * D,
+        "w13_gemm": 2.0 * M * D * 2 * F,
+        "w2_gemm": 2.0 * M * F * D,
+        "attention": 4.0 * 2 * U * H * S * (S + Tt + Ts) * Dh,
+    }
+    util = {k: flops[k] / (kt[k + "_us"] * 1e-6) / (PEAK_BF16_TFLOPS * 1e12) for k in flops}
+    mlp_util = (flops["w13_gemm"] + flops["w2_gemm"]) / (
+        (kt["w13_gemm_us"] + kt["w2_gemm_us"]) * 1e-6) / (PEAK_BF16_TFLOPS * 1e12)
+    dom = "w13_gemm"  # largest single kernel of the step (SwiGLU up-projection)
+    achieved = flops[dom] / (kt[dom + "_us"] * 1e-6) / 1e12
+    norm_bytes = M * D * 4 + M * D * 2  # read x f32, write h bf16
+    norm_gbs = norm_bytes / (kt["norm_mod_us"] * 1e-6) / 1e9
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle.oracle import Oracle, get_threads, set_threads
+        if args.cpu_threads:
+            set_threads(args.cpu_threads)
+        c, u = ctx.rows([0]), ctx.rows([1])
+        log("timing the CPU oracle (f32, %d threads): 1 of 40 Euler steps" % get_threads())
+        t0 = time.perf_counter()
+        Oracle("f32").sample_joint_cfg(cfg, w, x0, (c.k, c.v, c.mask), (u.k, u.v, u.mask), N,
+                                       SCALE, 0.0, 1.0, max_steps_run=1)
+        step_s = time.perf_counter() - t0
+        cpu = {"value": round(step_s * N * 1e3, 1), "unit": "ms (extrapolated 40-step RF run)",
+               "cores": get_threads(), "kind": "port",
+               "sample": "1 of 40 Joint-CFG Euler steps at config 4 (cond + uncond forward, "
+                         "B=1 each, f32 C oracle, OpenMP), measured %.2f s, x40" % step_s}
+        log("CPU oracle: %.2f s per step -> %.0f ms per RF run" % (step_s, step_s * N * 1e3))
+
+    rec = {
+        "metric": METRIC,
+        "value": round(ms, 3),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 3),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded random-init DiT (all Linear N(0,0.02)), N(0,1) noise and "
+                "context K/V, text valid length U[32,256]",
+        "config": {"workload": "BASELINE config 4: 12-layer d1024 DiT, 16x64 heads, SwiGLU 2816, "
+                               "latent 32; B=2 Joint CFG (scale 3, min_t 0), 750 frames, 256 "
+                               "text + 375 speaker context keys, 40 Euler steps, hipGraph step",
+                   "global_batch": 2, "seq_len": S, "rf_steps": N, "parallelism": "none"},
+        "tokens_per_s": round(S * N * 2 / (ms * 1e-3), 1),
+        "latent_frames_per_s": round(S * N / (ms * 1e-3), 1),
+        "mfma_util": {"attention": round(util["attention"], 4), "mlp": round(mlp_util, 4),
+                      "qkvg_gemm": round(util["qkvg_gemm"], 4), "wo_gemm": round(util["wo_gemm"], 4),
+                      "w13_gemm": round(util["w13_gemm"], 4), "w2_gemm": round(util["w2_gemm"], 4)},
+        "kernel_us": {k: round(v, 2) for k, v in kt.items()},
+        "norm_mod_gbs": round(norm_gbs, 1),
+        "roofline": {"kernel": "w13_gemm (SwiGLU up-projection, 1500x1024x5632)", "bound": "mfma",
+                     "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+    }
+    eng.close()
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()

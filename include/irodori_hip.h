@@ -1,0 +1,208 @@
+/*
+ * libirodori_hip — MI355X (gfx950) implementation of the Irodori-TTS rectified-flow DiT
+ * step, behind a plain C ABI (no HIP or torch types in any signature).
+ *
+ * What it replaces in the reference (Sanzentyo/Irodori-TTS-burn):
+ *   - the per-step DiT forward InferenceOptimizedModel::forward_with_cond_cached
+ *     (src/model/optimized.rs:102-113 -> src/model/dit/model.rs:249-262, 354-393);
+ *   - the Joint-CFG Euler loop of sample_euler_rf_cfg
+ *     (src/rf/euler_sampler.rs:132-718, Joint branch :435-469, update :714);
+ *   - the per-layer context KV cache CondKvCache (src/model/attention.rs:24-45);
+ *   - the operator entry points of src/kernels (rms_norm_wgsl rms_norm.rs:70-142,
+ *     fused_adaln_wgsl fused_adaln.rs:92-205, native_fa_sdpa_wgsl
+ *     fused_sdpa_native.rs:220-302, native_fa_sdpa_f16_in fused_sdpa_native_f16.rs:181).
+ *
+ * Conventions
+ *   - Every call returns an int status (IRODORI_OK or an IRODORI_ERR_* code) and never
+ *     aborts; irodori_last_error() returns the calling thread's last message.  This
+ *     replaces the reference's assert!-panics and maps onto IrodoriError
+ *     (src/error.rs:4-60).
+ *   - Host weight pointers are float32 in Burn "row" layout [d_in, d_out], y = x @ W + b
+ *     (src/weights/record_builders.rs:37-66).  The library copies and re-lays them out
+ *     in device memory; the caller keeps ownership of every host buffer.
+ *   - A context owns one HIP stream, its device buffers and its captured graphs.  It is
+ *     single-threaded (not re-entrant); use one context per thread.
+ *   - Joint CFG rows: for utterance u, batch row 2u is the conditioned row and row
+ *     2u+1 the unconditioned row (EncodedCondition::zeros_like, condition.rs:144-154).
+ */
+#ifndef IRODORI_HIP_H
+#define IRODORI_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes (IrodoriError variants, src/error.rs:4-60) ---------------------- */
+#define IRODORI_OK 0
+#define IRODORI_ERR_INVALID_ARG 1 /* null pointer, out-of-range index */
+#define IRODORI_ERR_SHAPE 2       /* dimension mismatch / unsupported shape */
+#define IRODORI_ERR_DTYPE 3       /* unsupported dtype */
+#define IRODORI_ERR_HIP 4         /* HIP runtime error */
+#define IRODORI_ERR_OOM 5         /* device allocation failed */
+#define IRODORI_ERR_NOT_LOADED 6  /* weights / context KV missing */
+#define IRODORI_ERR_CONFIG 7      /* invalid sampler / model configuration */
+
+#define IRODORI_DTYPE_F32 0
+#define IRODORI_DTYPE_BF16 1
+
+#define IRODORI_CFG_INDEPENDENT 0 /* CfgGuidanceMode (src/config/sampling.rs:100-108) */
+#define IRODORI_CFG_JOINT 1
+#define IRODORI_CFG_ALTERNATING 2
+
+#define IRODORI_METHOD_EULER 0 /* SamplerMethod (src/config/sampling.rs:8-20) */
+#define IRODORI_METHOD_HEUN 1
+#define IRODORI_METHOD_PLMS4 2
+
+typedef struct irodori_ctx irodori_ctx;
+
+/* Model dimensions: the ModelConfig fields the DiT forward reads
+ * (src/config/model.rs:8-44), plus device sizing. */
+typedef struct irodori_dit_config {
+    int32_t latent_dim;         /* patched latent dim P (latent_dim * latent_patch_size) */
+    int32_t model_dim;          /* D */
+    int32_t num_layers;         /* L */
+    int32_t num_heads;          /* H (head_dim = D / H must be 64) */
+    int32_t head_dim;           /* Dh */
+    int32_t mlp_hidden;         /* F = floor(D * mlp_ratio) (diffusion.rs:32), multiple of 16 */
+    int32_t adaln_rank;         /* r (norm.rs:101-104) */
+    int32_t timestep_embed_dim; /* t_dim */
+    float norm_eps;             /* norm_eps (config/model.rs:78) */
+    float rope_theta;           /* 10000 (dit/model.rs:216) */
+    int32_t compute_dtype;      /* IRODORI_DTYPE_BF16 (MFMA bf16) or IRODORI_DTYPE_F32 */
+    int32_t max_rows;           /* max batch rows in one forward (2 per utterance) */
+    int32_t max_seq;            /* max latent frames S */
+    int32_t max_ctx;            /* max context keys T = text + speaker */
+} irodori_dit_config;
+
+/* One DiffusionBlock (src/model/diffusion.rs:21-28) in the fused inference layout
+ * (attention.rs:514-523, feed_forward.rs:96-103).  adaLN index [0] = attention_adaln,
+ * [1] = mlp_adaln; chunk index [0] = shift, [1] = scale, [2] = gate (norm.rs:141-157). */
+typedef struct irodori_block_weights {
+    const float* w_qkv;          /* [D, 3*H*Dh] = [Wq | Wk | Wv] */
+    const float* w_gate;         /* [D, D] attention output gate */
+    const float* w_o;            /* [H*Dh, D] */
+    const float* q_norm;         /* [H, Dh] */
+    const float* k_norm;         /* [H, Dh] */
+    const float* w13;            /* [D, 2F] = [W1 | W3] */
+    const float* w2;             /* [F, D] */
+    const float* ada_down[2][3]; /* [D, r], no bias */
+    const float* ada_up[2][3];   /* [r, D] */
+    const float* ada_up_b[2][3]; /* [D] */
+} irodori_block_weights;
+
+/* Per-forward weights outside the blocks (src/model/dit/model.rs:104-125). */
+typedef struct irodori_io_weights {
+    const float* cond_w0;    /* cond_module.0 [t_dim, D] */
+    const float* cond_w1;    /* cond_module.2 [D, D] */
+    const float* cond_w2;    /* cond_module.4 [D, 3D] */
+    const float* in_w;       /* in_proj [P, D] */
+    const float* in_b;       /* [D] */
+    const float* out_norm_w; /* out_norm [D] */
+    const float* out_w;      /* out_proj [D, P] */
+    const float* out_b;      /* [P] */
+} irodori_io_weights;
+
+/* SamplerParams + GuidanceConfig (src/rf/params.rs:9-35, :61-92). */
+typedef struct irodori_sampler_params {
+    int32_t num_steps;
+    int32_t method;   /* IRODORI_METHOD_* (Euler implemented) */
+    int32_t cfg_mode; /* IRODORI_CFG_* (Joint implemented) */
+    float scale_text;
+    float scale_caption;
+    float scale_speaker;
+    float min_t;
+    float max_t;
+    int32_t has_truncation;
+    float truncation_factor;
+    int32_t has_speaker; /* model uses speaker conditioning (affects the Joint scale set) */
+} irodori_sampler_params;
+
+/* ---- errors ----------------------------------------------------------------------- */
+const char* irodori_last_error(void);
+const char* irodori_version(void);
+
+/* SamplerParams::validate (params.rs:99-183) plus the Joint equal-scale rule
+ * (euler_sampler.rs:209-228).  Pure host logic: no device needed. */
+int irodori_sampler_params_validate(const irodori_sampler_params* params);
+
+/* ---- context ---------------------------------------------------------------------- */
+/* Creates a context on HIP device `device`; allocates every device buffer up front for
+ * cfg->max_rows / max_seq / max_ctx.  Replaces InferenceBuilder::build
+ * (src/inference.rs:83-196) for the HIP backend. */
+int irodori_ctx_create(int device, const irodori_dit_config* cfg, irodori_ctx** out);
+int irodori_ctx_destroy(irodori_ctx* ctx);
+/* Bytes of device memory the context holds. */
+int irodori_ctx_device_bytes(const irodori_ctx* ctx, uint64_t* bytes);
+
+/* Weight ingest (load_model -> InferenceOptimizedModel::from, inference.rs:107-116,
+ * :187-195): host f32 in Burn layout -> device compute dtype, fused layouts. */
+int irodori_load_io_weights(irodori_ctx* ctx, const irodori_io_weights* w);
+int irodori_load_block_weights(irodori_ctx* ctx, int layer, const irodori_block_weights* w);
+
+/* Context KV for one layer and one batch row: the CondKvCache contents
+ * (attention.rs:24-45; built by build_kv_cache :431-501).  k, v: [t_ctx, H, Dh] f32,
+ * k already k-normed and not rotated; mask: [t_ctx] (nonzero = attend).  Every row and
+ * layer must use the same t_ctx (<= max_ctx); irodori_clear_ctx_kv resets it. */
+int irodori_set_ctx_kv(irodori_ctx* ctx, int layer, int row, int t_ctx, const float* k,
+                       const float* v, const uint8_t* mask);
+int irodori_clear_ctx_kv(irodori_ctx* ctx);
+
+/* One DiT forward, forward_with_cond_cached (optimized.rs:102-113): x_t [B,S,P],
+ * t [B] -> v [B,S,P].  debug (nullable): [L+1,B,S,D] after in_proj and after each block
+ * (BlockDebugOutputs, dit/model.rs:92-102).  Host pointers; synchronous. */
+int irodori_forward(irodori_ctx* ctx, int batch, int seq, const float* x_t, const float* t,
+                    float* v_out, float* debug);
+
+/* One DiffusionBlock::forward_fused (diffusion.rs:62-105) on host data:
+ * x [B,S,D] updated in place; cond [B,3D] is the cond_module output. */
+int irodori_block_forward(irodori_ctx* ctx, int layer, int batch, int seq, float* x,
+                          const float* cond);
+
+/* Joint-CFG RF sampling (sample_euler_rf_cfg, euler_sampler.rs:132-718): U utterances,
+ * rows 2u / 2u+1 as above, x0 [U,S,P] -> x_out [U,S,P].  Host pointers; one hipGraph
+ * replayed per step.  Truncation (params.rs:146-155) is applied to x0 when set. */
+int irodori_sample(irodori_ctx* ctx, const irodori_sampler_params* params, int utterances,
+                   int seq, const float* x0, float* x_out);
+/* Same with x0 / x_out already in device memory (HBM-resident timing). */
+int irodori_sample_device(irodori_ctx* ctx, const irodori_sampler_params* params,
+                          int utterances, int seq, const float* d_x0, float* d_x_out);
+
+/* Average device time of each kernel of one DiT block at (batch, seq), measured with HIP
+ * events on the context's stream over `iters` back-to-back launches per kernel (the
+ * reference's NVTX per-call timings, docs/benchmarks/rtx-a6000.md:131-138, as a
+ * measurement entry point).  Weights and context KV must be loaded.  Microseconds. */
+typedef struct irodori_kernel_times {
+    float norm_mod_us;   /* RMSNorm + adaLN modulation (one of the two per block) */
+    float qkvg_gemm_us;  /* QKV + gate projection with head norm / RoPE epilogue */
+    float attention_us;  /* joint flash attention + sigmoid gate */
+    float wo_gemm_us;    /* output projection + gated residual */
+    float w13_gemm_us;   /* SwiGLU up-projection with silu(a)*b epilogue */
+    float w2_gemm_us;    /* SwiGLU down-projection + gated residual */
+    float final_us;      /* out_norm + out_proj + CFG combine + Euler update */
+} irodori_kernel_times;
+int irodori_profile_layer(irodori_ctx* ctx, int batch, int seq, int iters,
+                          irodori_kernel_times* out);
+
+/* ---- operator entry points (device pointers; stream may be NULL) ------------------- */
+/* rms_norm_wgsl (rms_norm.rs:70-142): y = x / sqrt(mean(x^2)+eps) * w, x [rows, dim]. */
+int irodori_op_rms_norm(const float* x, const float* w, int rows, int dim, float eps,
+                        float* y, void* stream);
+/* fused_adaln_wgsl (fused_adaln.rs:92-205): y = x/rms * (1 + scale[b]) + shift[b],
+ * x [batch*seq, dim], scale/shift [batch, dim]. */
+int irodori_op_fused_adaln(const float* x, const float* scale, const float* shift, int batch,
+                           int seq, int dim, float eps, float* y, void* stream);
+/* native_fa_sdpa_wgsl / native_fa_sdpa_f16_in (fused_sdpa_native.rs:220-302,
+ * fused_sdpa_native_f16.rs:181): out = softmax(q k^T * scale + mask) v.
+ * q [B,H,Sq,Dh], k/v [B,H,Skv,Dh] in `dtype` (F32 or BF16), mask [B,Skv] f32 with
+ * 1.0 = attend (may be NULL), out [B,H,Sq,Dh] f32.  Dh in {64, 128}.  A fully masked
+ * query row yields 0. */
+int irodori_op_sdpa(int dtype, const void* q, const void* k, const void* v, const float* mask,
+                    int batch, int heads, int seq_q, int seq_kv, int head_dim, float scale,
+                    float* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* IRODORI_HIP_H */

@@ -1,0 +1,128 @@
+// Shared device/host helpers for the gfx950 (CDNA4) kernels of libirodori_hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+namespace irodori {
+
+// ---------------------------------------------------------------------------------
+// Element types.  bf16 is clang's __bf16 storage type; arithmetic is always f32.
+// ---------------------------------------------------------------------------------
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+// Raw 16-byte register chunk (native vector type, so arrays of it stay in VGPRs).
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(bf16 v) { return static_cast<float>(v); }
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float v);
+template <>
+__device__ __forceinline__ float from_f32<float>(float v) { return v; }
+template <>
+__device__ __forceinline__ bf16 from_f32<bf16>(float v) { return static_cast<bf16>(v); }
+
+// A "k32 fragment": the 8 consecutive reduction-dim elements one lane feeds to the
+// matrix core per 32-wide slice of K.  For bf16 that is one v_mfma_f32_16x16x32_bf16
+// operand; for f32 it is the operands of eight v_mfma_f32_16x16x4_f32 (element j goes
+// to the j-th instruction).  Both operands of a product use the same element order, so
+// the k index each element stands for only has to agree between A and B.
+template <typename T>
+struct Frag;
+template <>
+struct Frag<bf16> {
+    bf16x8 v;
+};
+template <>
+struct Frag<float> {
+    f32x8 v;
+};
+
+__device__ __forceinline__ void mma16(f32x4& acc, const Frag<bf16>& a, const Frag<bf16>& b) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, acc, 0, 0, 0);
+}
+__device__ __forceinline__ void mma16(f32x4& acc, const Frag<float>& a, const Frag<float>& b) {
+#pragma unroll
+    for (int j = 0; j < 8; j++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.v[j], b.v[j], acc, 0, 0, 0);
+}
+
+// 16-byte vector loads/stores.
+template <typename V>
+__device__ __forceinline__ V ld_vec(const void* p) {
+    return *reinterpret_cast<const V*>(p);
+}
+template <typename V>
+__device__ __forceinline__ void st_vec(void* p, const V& v) {
+    *reinterpret_cast<V*>(p) = v;
+}
+
+// Load a k32 fragment (8 contiguous elements) from LDS or global memory.
+template <typename T>
+__device__ __forceinline__ Frag<T> load_frag(const T* p);
+template <>
+__device__ __forceinline__ Frag<bf16> load_frag<bf16>(const bf16* p) {
+    Frag<bf16> f;
+    f.v = *reinterpret_cast<const bf16x8*>(p);
+    return f;
+}
+template <>
+__device__ __forceinline__ Frag<float> load_frag<float>(const float* p) {
+    Frag<float> f;
+    f.v = *reinterpret_cast<const f32x8*>(p);
+    return f;
+}
+
+// ---------------------------------------------------------------------------------
+// Wavefront (64 lanes) reductions.
+// ---------------------------------------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+__device__ __forceinline__ float silu_f(float v) { return v / (1.0f + __expf(-v)); }
+__device__ __forceinline__ float sigmoid_f(float v) { return 1.0f / (1.0f + __expf(-v)); }
+
+// Map a linear workgroup id so that consecutive ids land on the same XCD.  Workgroups
+// are dispatched round-robin over the 8 XCDs (id % 8); when the grid is a multiple of
+// 8 this returns an id such that XCD x owns the contiguous range [x*n/8, (x+1)*n/8).
+__device__ __forceinline__ int xcd_remap(int id, int n) {
+    if (n % 8) return id;
+    return (id % 8) * (n / 8) + id / 8;
+}
+
+// ---------------------------------------------------------------------------------
+// Host-side error plumbing (thread-local last error, status codes of irodori_hip.h).
+// ---------------------------------------------------------------------------------
+void set_last_error(const std::string& msg);
+
+}  // namespace irodori
+
+#define IRO_HIP_CHECK(expr)                                                                 \
+    do {                                                                                    \
+        hipError_t _e = (expr);                                                             \
+        if (_e != hipSuccess) {                                                             \
+            ::irodori::set_last_error(std::string(#expr) + ": " + hipGetErrorString(_e));   \
+            return _e == hipErrorOutOfMemory ? IRODORI_ERR_OOM : IRODORI_ERR_HIP;          \
+        }                                                                                   \
+    } while (0)
+
+#define IRO_REQUIRE(cond, code, msg)                                                        \
+    do {                                                                                    \
+        if (!(cond)) {                                                                      \
+            ::irodori::set_last_error(msg);                                                 \
+            return code;                                                                    \
+        }                                                                                   \
+    } while (0)

@@ -1,0 +1,1065 @@
+// libirodori_hip host side: the C ABI of include/irodori_hip.h.
+//
+// A context owns every device buffer of one model instance, sized once at creation:
+//   weights   bf16 (or f32) K-major [N, K] for the four projection GEMMs, f32 for the
+//             norms / conditioning MLPs;
+//   context   per layer K/V [rows, H, max_ctx, Dh] + mask + per-64-key-tile "any valid"
+//             flags (the CondKvCache of attention.rs:24-45, laid out for the attention
+//             kernel's second key segment);
+//   work      residual x f32 [rows*S, D], modulated h, Q/K/V of the latent keys,
+//             sigmoid gate, gated attention output, SwiGLU product;
+//   tables    RoPE cos/sin [max_seq, Dh/2], adaLN modulation vectors per (step, layer).
+// One RF step is recorded once into a hipGraph and replayed num_steps times; the step
+// index lives in device memory and is advanced by the last node of the graph.
+#include <math.h>
+#include <string.h>
+
+#include <map>
+#include <memory>
+#include <new>
+#include <string>
+#include <tuple>
+#include <vector>
+
+#include "../../include/irodori_hip.h"
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace irodori {
+
+static thread_local std::string g_last_error;
+void set_last_error(const std::string& msg) { g_last_error = msg; }
+
+namespace {
+
+// ---------------------------------------------------------------------------------------
+// Weight ingest kernels: Burn [K, N] f32 -> K-major [N, K] compute dtype.
+// mode 0: dst row n = source column n.
+// mode 1: SwiGLU interleave — dst rows 32g..32g+15 = W1 columns 16g.., rows 32g+16..32g+31 =
+//         W3 columns 16g.. (W3 starts at source column N/2).
+// ---------------------------------------------------------------------------------------
+template <typename T>
+__global__ void transpose_kmajor_kernel(const float* __restrict__ src, int K, int N, int mode,
+                                        T* __restrict__ dst) {
+    __shared__ float tile[32][33];
+    int k0 = blockIdx.x * 32, n0 = blockIdx.y * 32;
+    int tx = threadIdx.x, ty = threadIdx.y;  // 32 x 8
+    for (int r = ty; r < 32; r += 8) {
+        int k = k0 + r, n = n0 + tx;
+        int sc = n;
+        if (mode == 1 && n < N) {
+            int half = N / 2, g = n / 32, w = n % 32;
+            sc = w < 16 ? 16 * g + w : half + 16 * g + (w - 16);
+        }
+        tile[r][tx] = (k < K && n < N) ? src[(size_t)k * N + sc] : 0.f;
+    }
+    __syncthreads();
+    for (int r = ty; r < 32; r += 8) {
+        int n = n0 + r, k = k0 + tx;
+        if (n < N && k < K) dst[(size_t)n * K + k] = from_f32<T>(tile[tx][r]);
+    }
+}
+
+template <typename T>
+void launch_transpose(const float* src, int K, int N, int mode, T* dst, hipStream_t st) {
+    dim3 grid((K + 31) / 32, (N + 31) / 32), block(32, 8);
+    transpose_kmajor_kernel<T><<<grid, block, 0, st>>>(src, K, N, mode, dst);
+}
+
+}  // namespace
+}  // namespace irodori
+
+using namespace irodori;
+
+struct LayerBufs {
+    void* w_qkvg = nullptr;  // [4D, D]
+    void* w_o = nullptr;     // [D, HD]
+    void* w13 = nullptr;     // [2F, D] interleaved per 16
+    void* w2 = nullptr;      // [D, F]
+    float* q_norm = nullptr;
+    float* k_norm = nullptr;
+    float* ada_down[2][3] = {};
+    float* ada_up[2][3] = {};
+    float* ada_up_b[2][3] = {};
+    void* ctx_k = nullptr;   // [rows, H, max_ctx, Dh]
+    void* ctx_v = nullptr;
+    float* ctx_mask = nullptr;  // [rows, max_ctx]
+    int* tile_on = nullptr;     // [rows, ceil(max_ctx / 64)]
+    bool loaded = false;
+    std::vector<char> row_set;
+};
+
+// A captured RF step is specific to the batch shape, the context length and the CFG
+// scale (a kernel argument baked into the graph).
+struct GraphKey {
+    int B, S, T;
+    uint32_t scale_bits;
+    bool operator<(const GraphKey& o) const {
+        return std::tie(B, S, T, scale_bits) < std::tie(o.B, o.S, o.T, o.scale_bits);
+    }
+};
+
+struct irodori_ctx {
+    int device = 0;
+    irodori_dit_config cfg{};
+    bool bf16 = true;
+    size_t esz = 2;  // compute element size
+    hipStream_t stream = nullptr;
+    std::vector<void*> allocs;
+    uint64_t dev_bytes = 0;
+
+    std::vector<LayerBufs> layers;
+    bool io_loaded = false;
+    float *cond_w0 = nullptr, *cond_w1 = nullptr, *cond_w2 = nullptr;
+    float *in_w = nullptr, *in_b = nullptr, *out_norm_w = nullptr, *out_wT = nullptr,
+          *out_b = nullptr;
+    int t_ctx = -1;
+
+    // work buffers
+    float* x = nullptr;   // [rows*S, D]
+    void* h = nullptr;    // [rows*S, D]
+    void* q = nullptr;    // [rows, H, S, Dh]
+    void* ks = nullptr;
+    void* vs = nullptr;
+    void* gate = nullptr;  // [rows*S, D]
+    void* o = nullptr;     // [rows*S, D]
+    void* u = nullptr;     // [rows*S, F]
+    float* rope_cos = nullptr;
+    float* rope_sin = nullptr;
+    float* xt = nullptr;    // [rows, S, P] sampler state / forward input
+    float* vout = nullptr;  // [rows, S, P]
+    int* step = nullptr;    // device step counter
+    int* zero_step = nullptr;
+
+    // conditioning precompute
+    int nvec_cap = 0;
+    float* tvec = nullptr;
+    float* emb = nullptr;
+    float* h0 = nullptr;
+    float* h1 = nullptr;
+    float* cond = nullptr;
+    float* mid = nullptr;
+    float* tab = nullptr;
+    float* t_sched = nullptr;
+    int* cfg_on = nullptr;
+    int sched_cap = 0;
+    VecLinJob* d_jobs_mlp = nullptr;   // 3 jobs
+    VecLinJob* d_jobs_down = nullptr;  // L*6 jobs
+    VecLinJob* d_jobs_up = nullptr;    // L*6 jobs
+
+    std::map<GraphKey, hipGraphExec_t> graphs;
+};
+
+namespace {
+
+int dev_alloc(irodori_ctx* c, void** p, size_t bytes) {
+    if (bytes == 0) bytes = 16;
+    hipError_t e = hipMalloc(p, bytes);
+    if (e != hipSuccess) {
+        set_last_error(std::string("hipMalloc(") + std::to_string(bytes) + "): " + hipGetErrorString(e));
+        return e == hipErrorOutOfMemory ? IRODORI_ERR_OOM : IRODORI_ERR_HIP;
+    }
+    c->allocs.push_back(*p);
+    c->dev_bytes += bytes;
+    return IRODORI_OK;
+}
+
+template <typename P>
+int dalloc(irodori_ctx* c, P** p, size_t bytes) {
+    return dev_alloc(c, reinterpret_cast<void**>(p), bytes);
+}
+
+#define IRO_TRY(expr)                   \
+    do {                                \
+        int _rc = (expr);               \
+        if (_rc != IRODORI_OK) return _rc; \
+    } while (0)
+
+int check_launch(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        set_last_error(std::string(what) + ": " + hipGetErrorString(e));
+        return IRODORI_ERR_HIP;
+    }
+    return IRODORI_OK;
+}
+
+// rope.rs:24-63 in f32: freq_i = 1 / theta^(2i/Dh), angle = pos * freq_i.
+void host_rope_tables(int S, int Dh, float theta, std::vector<float>& cs, std::vector<float>& sn) {
+    int half = Dh / 2;
+    cs.resize((size_t)S * half);
+    sn.resize((size_t)S * half);
+    for (int s = 0; s < S; s++)
+        for (int i = 0; i < half; i++) {
+            float freq = 1.0f / powf(theta, 2.0f * (float)i / (float)Dh);
+            float a = (float)s * freq;
+            cs[(size_t)s * half + i] = cosf(a);
+            sn[(size_t)s * half + i] = sinf(a);
+        }
+}
+
+int upload(irodori_ctx* c, void* dst, const void* src, size_t bytes) {
+    IRO_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream));
+    return IRODORI_OK;
+}
+
+// Host f32 [K, N] -> device compute-dtype [N, K] at dst (row offset applied by caller).
+int ingest_kmajor(irodori_ctx* c, const float* host, int K, int N, int mode, void* dst) {
+    float* stage = nullptr;
+    size_t bytes = sizeof(float) * (size_t)K * N;
+    IRO_HIP_CHECK(hipMalloc(&stage, bytes));
+    hipError_t e = hipMemcpyAsync(stage, host, bytes, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) {
+        if (c->bf16)
+            launch_transpose<bf16>(stage, K, N, mode, static_cast<bf16*>(dst), c->stream);
+        else
+            launch_transpose<float>(stage, K, N, mode, static_cast<float*>(dst), c->stream);
+        e = hipGetLastError();
+    }
+    hipError_t e2 = hipStreamSynchronize(c->stream);
+    (void)hipFree(stage);
+    if (e == hipSuccess) e = e2;
+    if (e != hipSuccess) {
+        set_last_error(std::string("weight ingest: ") + hipGetErrorString(e));
+        return IRODORI_ERR_HIP;
+    }
+    return IRODORI_OK;
+}
+
+int ensure_nvec(irodori_ctx* c, int nvec) {
+    if (nvec <= c->nvec_cap) return IRODORI_OK;
+    const auto& g = c->cfg;
+    int D = g.model_dim, L = g.num_layers, r = g.adaln_rank;
+    int cap = nvec < 64 ? 64 : nvec;
+    IRO_HIP_CHECK(hipStreamSynchronize(c->stream));
+    IRO_TRY(dalloc(c, &c->tvec, sizeof(float) * cap));
+    IRO_TRY(dalloc(c, &c->emb, sizeof(float) * (size_t)cap * g.timestep_embed_dim));
+    IRO_TRY(dalloc(c, &c->h0, sizeof(float) * (size_t)cap * D));
+    IRO_TRY(dalloc(c, &c->h1, sizeof(float) * (size_t)cap * D));
+    IRO_TRY(dalloc(c, &c->cond, sizeof(float) * (size_t)cap * 3 * D));
+    IRO_TRY(dalloc(c, &c->mid, sizeof(float) * (size_t)L * 6 * cap * r));
+    IRO_TRY(dalloc(c, &c->tab, sizeof(float) * (size_t)cap * L * 6 * D));
+    c->nvec_cap = cap;
+
+    // Job tables (pointers depend on the buffers above).
+    std::vector<VecLinJob> mlp(3), down(L * 6), up(L * 6);
+    mlp[0] = {c->emb, c->cond_w0, nullptr, nullptr, c->h0, g.timestep_embed_dim, 0, D,
+              g.timestep_embed_dim, D, 0, 1};
+    mlp[1] = {c->h0, c->cond_w1, nullptr, nullptr, c->h1, D, 0, D, D, D, 0, 1};
+    mlp[2] = {c->h1, c->cond_w2, nullptr, nullptr, c->cond, D, 0, 3 * D, D, 3 * D, 0, 0};
+    for (int l = 0; l < L; l++)
+        for (int k = 0; k < 2; k++)
+            for (int ch = 0; ch < 3; ch++) {
+                int j = (l * 2 + k) * 3 + ch;
+                float* midj = c->mid + (size_t)j * cap * r;
+                auto& lb = c->layers[l];
+                down[j] = {c->cond + ch * D, lb.ada_down[k][ch], nullptr, nullptr, midj, 3 * D, 0, r,
+                           D, r, 1, 0};
+                up[j] = {midj, lb.ada_up[k][ch], lb.ada_up_b[k][ch], c->cond + ch * D,
+                         c->tab + (size_t)(l * 6 + k * 3 + ch) * D, r, 3 * D, L * 6 * D, r, D, 0,
+                         ch == 2 ? 2 : 0};
+            }
+    if (!c->d_jobs_mlp) {
+        IRO_TRY(dalloc(c, &c->d_jobs_mlp, sizeof(VecLinJob) * 3));
+        IRO_TRY(dalloc(c, &c->d_jobs_down, sizeof(VecLinJob) * L * 6));
+        IRO_TRY(dalloc(c, &c->d_jobs_up, sizeof(VecLinJob) * L * 6));
+    }
+    IRO_HIP_CHECK(hipMemcpy(c->d_jobs_mlp, mlp.data(), sizeof(VecLinJob) * 3, hipMemcpyHostToDevice));
+    IRO_HIP_CHECK(hipMemcpy(c->d_jobs_down, down.data(), sizeof(VecLinJob) * L * 6, hipMemcpyHostToDevice));
+    IRO_HIP_CHECK(hipMemcpy(c->d_jobs_up, up.data(), sizeof(VecLinJob) * L * 6, hipMemcpyHostToDevice));
+    // Cached graphs captured the old table pointers.
+    for (auto& kv : c->graphs) (void)hipGraphExecDestroy(kv.second);
+    c->graphs.clear();
+    return IRODORI_OK;
+}
+
+// Modulation table for nvec timesteps already in c->tvec (or, when skip_mlp, for cond
+// vectors already in c->cond): tab[v][l][k][ch][:].
+int enqueue_mod_table(irodori_ctx* c, int nvec, bool skip_mlp) {
+    const auto& g = c->cfg;
+    int D = g.model_dim, L = g.num_layers, r = g.adaln_rank;
+    if (!skip_mlp) {
+        launch_timestep_embedding(c->tvec, nvec, g.timestep_embed_dim, c->emb, c->stream);
+        for (int j = 0; j < 3; j++)
+            launch_vec_linear(c->d_jobs_mlp + j, 1, nvec, j == 2 ? 3 * D : D, c->stream);
+    }
+    launch_vec_linear(c->d_jobs_down, L * 6, nvec, r, c->stream);
+    launch_vec_linear(c->d_jobs_up, L * 6, nvec, D, c->stream);
+    return check_launch("modulation table");
+}
+
+template <typename T>
+int enqueue_layer(irodori_ctx* c, int l, int B, int S, const ModTable& mt, bool last_norm) {
+    const auto& g = c->cfg;
+    int D = g.model_dim, H = g.num_heads, F = g.mlp_hidden, M = B * S;
+    auto& lb = c->layers[l];
+    hipStream_t st = c->stream;
+    T* h = static_cast<T*>(c->h);
+
+    GemmArgs<T> ga{};
+    ga.mt = mt;
+    ga.S = S;
+    ga.layer = l;
+    ga.H = H;
+    ga.D = D;
+    ga.eps = g.norm_eps;
+    ga.M = M;
+
+    // QKV + gate projection with head norms and half RoPE (attention.rs:293-345, :423).
+    ga.A = h;
+    ga.W = static_cast<const T*>(lb.w_qkvg);
+    ga.N = 4 * D;
+    ga.K = D;
+    ga.Q = static_cast<T*>(c->q);
+    ga.Kd = static_cast<T*>(c->ks);
+    ga.Vd = static_cast<T*>(c->vs);
+    ga.G = static_cast<T*>(c->gate);
+    ga.q_norm = lb.q_norm;
+    ga.k_norm = lb.k_norm;
+    ga.rope_cos = c->rope_cos;
+    ga.rope_sin = c->rope_sin;
+    if (launch_gemm<T>(EPI_QKVG, ga, st)) { set_last_error("qkvg gemm shape"); return IRODORI_ERR_SHAPE; }
+
+    // Joint attention over [latent self | cached ctx] (attention.rs:349-425).
+    AttnArgs<T> aa{};
+    aa.Q = static_cast<const T*>(c->q);
+    aa.K0 = static_cast<const T*>(c->ks);
+    aa.V0 = static_cast<const T*>(c->vs);
+    aa.len0 = S;
+    aa.stride0 = S;
+    if (c->t_ctx > 0) {
+        aa.K1 = static_cast<const T*>(lb.ctx_k);
+        aa.V1 = static_cast<const T*>(lb.ctx_v);
+        aa.len1 = c->t_ctx;
+        aa.stride1 = g.max_ctx;
+        aa.mask1 = lb.ctx_mask;
+        aa.tile_on1 = lb.tile_on;
+    }
+    aa.B = B;
+    aa.H = H;
+    aa.Sq = S;
+    aa.scale = 1.0f / sqrtf((float)g.head_dim);
+    aa.out_mode = 0;
+    aa.G = static_cast<const T*>(c->gate);
+    aa.O = static_cast<T*>(c->o);
+    if (launch_attention<T, 64>(aa, st)) { set_last_error("attention shape"); return IRODORI_ERR_SHAPE; }
+
+    // x += g_attn * (o @ Wo) (attention.rs:424, diffusion.rs:98).
+    ga.A = static_cast<const T*>(c->o);
+    ga.W = static_cast<const T*>(lb.w_o);
+    ga.N = D;
+    ga.K = D;
+    ga.x = c->x;
+    ga.kind = 0;
+    if (launch_gemm<T>(EPI_RESID, ga, st)) { set_last_error("wo gemm shape"); return IRODORI_ERR_SHAPE; }
+
+    // h2 = mlp adaLN(x) (diffusion.rs:101-102).
+    launch_norm_mod<T>(c->x, h, M, S, D, g.norm_eps, mt, l, 1, st);
+
+    // m = silu(h2 W1) * (h2 W3) (feed_forward.rs:76-84).
+    ga.A = h;
+    ga.W = static_cast<const T*>(lb.w13);
+    ga.N = 2 * F;
+    ga.K = D;
+    ga.U = static_cast<T*>(c->u);
+    if (launch_gemm<T>(EPI_SWIGLU, ga, st)) { set_last_error("w13 gemm shape"); return IRODORI_ERR_SHAPE; }
+
+    // x += g_mlp * (m @ W2) (diffusion.rs:104).
+    ga.A = static_cast<const T*>(c->u);
+    ga.W = static_cast<const T*>(lb.w2);
+    ga.N = D;
+    ga.K = F;
+    ga.kind = 1;
+    if (launch_gemm<T>(EPI_RESID, ga, st)) { set_last_error("w2 gemm shape"); return IRODORI_ERR_SHAPE; }
+
+    // Next block's attention adaLN.
+    if (!last_norm) launch_norm_mod<T>(c->x, h, M, S, D, g.norm_eps, mt, l + 1, 0, st);
+    return check_launch("layer");
+}
+
+int enqueue_layer_any(irodori_ctx* c, int l, int B, int S, const ModTable& mt, bool last) {
+    return c->bf16 ? enqueue_layer<bf16>(c, l, B, S, mt, last) : enqueue_layer<float>(c, l, B, S, mt, last);
+}
+
+int enqueue_inproj(irodori_ctx* c, int B, int S, int rows_per_src, const ModTable& mt) {
+    const auto& g = c->cfg;
+    if (c->bf16)
+        launch_inproj_norm<bf16>(c->xt, rows_per_src, c->in_w, c->in_b, c->x, static_cast<bf16*>(c->h),
+                                 B * S, S, g.latent_dim, g.model_dim, g.norm_eps, mt, c->stream);
+    else
+        launch_inproj_norm<float>(c->xt, rows_per_src, c->in_w, c->in_b, c->x, static_cast<float*>(c->h),
+                                  B * S, S, g.latent_dim, g.model_dim, g.norm_eps, mt, c->stream);
+    return check_launch("in_proj");
+}
+
+// All kernels of one RF step (Joint CFG, B = 2U rows): in_proj, L blocks, output head +
+// CFG combine + Euler update, step advance.
+int enqueue_rf_step(irodori_ctx* c, int B, int S, float scale) {
+    const auto& g = c->cfg;
+    ModTable mt{c->tab, c->step, 1, B, g.num_layers};
+    IRO_TRY(enqueue_inproj(c, B, S, 2, mt));
+    for (int l = 0; l < g.num_layers; l++) IRO_TRY(enqueue_layer_any(c, l, B, S, mt, l + 1 == g.num_layers));
+    FinalArgs fa{};
+    fa.x = c->x;
+    fa.norm_w = c->out_norm_w;
+    fa.out_wT = c->out_wT;
+    fa.out_b = c->out_b;
+    fa.B = B;
+    fa.S = S;
+    fa.D = g.model_dim;
+    fa.P = g.latent_dim;
+    fa.eps = g.norm_eps;
+    fa.mode = 1;
+    fa.xt = c->xt;
+    fa.t_sched = c->t_sched;
+    fa.cfg_on = c->cfg_on;
+    fa.step = c->step;
+    fa.scale = scale;
+    launch_final(fa, c->stream);
+    launch_step_advance(c->step, c->stream);
+    return check_launch("rf step tail");
+}
+
+int check_ready(irodori_ctx* c, int B) {
+    IRO_REQUIRE(c->io_loaded, IRODORI_ERR_NOT_LOADED, "io weights not loaded");
+    for (int l = 0; l < c->cfg.num_layers; l++) {
+        IRO_REQUIRE(c->layers[l].loaded, IRODORI_ERR_NOT_LOADED,
+                    "block weights of layer " + std::to_string(l) + " not loaded");
+        if (c->t_ctx > 0)
+            for (int r = 0; r < B; r++)
+                IRO_REQUIRE(c->layers[l].row_set[r], IRODORI_ERR_NOT_LOADED,
+                            "context KV of layer " + std::to_string(l) + " row " + std::to_string(r) +
+                                " not set");
+    }
+    return IRODORI_OK;
+}
+
+int validate_params(const irodori_sampler_params* p) {
+    IRO_REQUIRE(p != nullptr, IRODORI_ERR_INVALID_ARG, "params is null");
+    IRO_REQUIRE(p->num_steps > 0, IRODORI_ERR_CONFIG, "num_steps must be > 0");
+    const char* names[3] = {"guidance.scale_text", "guidance.scale_caption", "guidance.scale_speaker"};
+    float sc[3] = {p->scale_text, p->scale_caption, p->scale_speaker};
+    for (int i = 0; i < 3; i++)
+        IRO_REQUIRE(std::isfinite(sc[i]), IRODORI_ERR_CONFIG,
+                    std::string(names[i]) + " must be finite, got " + std::to_string(sc[i]));
+    IRO_REQUIRE(std::isfinite(p->min_t) && p->min_t >= 0.f && p->min_t <= 1.f, IRODORI_ERR_CONFIG,
+                "guidance.min_t must be finite and in [0, 1], got " + std::to_string(p->min_t));
+    IRO_REQUIRE(std::isfinite(p->max_t) && p->max_t >= 0.f && p->max_t <= 1.f, IRODORI_ERR_CONFIG,
+                "guidance.max_t must be finite and in [0, 1], got " + std::to_string(p->max_t));
+    IRO_REQUIRE(p->min_t <= p->max_t, IRODORI_ERR_CONFIG,
+                "guidance.min_t (" + std::to_string(p->min_t) + ") must not exceed guidance.max_t (" +
+                    std::to_string(p->max_t) + ")");
+    IRO_REQUIRE(!p->has_truncation || (std::isfinite(p->truncation_factor) && p->truncation_factor > 0.f),
+                IRODORI_ERR_CONFIG, "truncation_factor must be finite and > 0");
+    IRO_REQUIRE(!(p->method == IRODORI_METHOD_PLMS4 && p->cfg_mode == IRODORI_CFG_ALTERNATING),
+                IRODORI_ERR_CONFIG,
+                "sampler PLMS4 is not compatible with cfg_guidance_mode=Alternating; use Independent or "
+                "Joint instead");
+    IRO_REQUIRE(p->method >= 0 && p->method <= 2, IRODORI_ERR_CONFIG, "unknown sampler method");
+    IRO_REQUIRE(p->cfg_mode >= 0 && p->cfg_mode <= 2, IRODORI_ERR_CONFIG, "unknown cfg guidance mode");
+    if (p->cfg_mode == IRODORI_CFG_JOINT) {
+        // euler_sampler.rs:209-228: all active scales (text, speaker if used) must match.
+        float lo = INFINITY, hi = -INFINITY;
+        float act[2] = {p->scale_text, p->has_speaker ? p->scale_speaker : 0.f};
+        for (float s : act)
+            if (s > 0.f) { lo = fminf(lo, s); hi = fmaxf(hi, s); }
+        IRO_REQUIRE(!(hi - lo >= 1e-6f), IRODORI_ERR_CONFIG,
+                    "cfg_guidance_mode=Joint requires all active cfg scales to be equal, but got text=" +
+                        std::to_string(p->scale_text) + ", speaker=" + std::to_string(p->scale_speaker) +
+                        ", caption=" + std::to_string(p->scale_caption));
+    }
+    return IRODORI_OK;
+}
+
+float joint_scale(const irodori_sampler_params* p) {
+    if (p->scale_text > 0.f) return p->scale_text;
+    if (p->has_speaker && p->scale_speaker > 0.f) return p->scale_speaker;
+    return 0.f;
+}
+
+}  // namespace
+
+#define IRO_GUARD_BEGIN try {
+#define IRO_GUARD_END                                             \
+    }                                                             \
+    catch (const std::bad_alloc&) {                               \
+        set_last_error("host allocation failed");                 \
+        return IRODORI_ERR_OOM;                                   \
+    }                                                             \
+    catch (...) {                                                 \
+        set_last_error("unexpected C++ exception");               \
+        return IRODORI_ERR_HIP;                                   \
+    }
+
+extern "C" {
+
+const char* irodori_last_error(void) { return g_last_error.c_str(); }
+const char* irodori_version(void) { return "irodori_hip 0.1.0 (gfx950)"; }
+
+int irodori_sampler_params_validate(const irodori_sampler_params* params) {
+    IRO_GUARD_BEGIN
+    return validate_params(params);
+    IRO_GUARD_END
+}
+
+int irodori_ctx_destroy(irodori_ctx* c) {
+    if (!c) return IRODORI_OK;
+    (void)hipSetDevice(c->device);
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    for (auto& kv : c->graphs) (void)hipGraphExecDestroy(kv.second);
+    for (void* p : c->allocs) (void)hipFree(p);
+    if (c->stream) (void)hipStreamDestroy(c->stream);
+    delete c;
+    return IRODORI_OK;
+}
+
+int irodori_ctx_create(int device, const irodori_dit_config* cfg, irodori_ctx** out) {
+    IRO_GUARD_BEGIN
+    IRO_REQUIRE(cfg && out, IRODORI_ERR_INVALID_ARG, "null argument");
+    *out = nullptr;
+    const irodori_dit_config& g = *cfg;
+    IRO_REQUIRE(g.compute_dtype == IRODORI_DTYPE_BF16 || g.compute_dtype == IRODORI_DTYPE_F32,
+                IRODORI_ERR_DTYPE, "compute_dtype must be IRODORI_DTYPE_BF16 or IRODORI_DTYPE_F32");
+    IRO_REQUIRE(g.num_layers > 0 && g.num_heads > 0 && g.model_dim > 0 && g.latent_dim > 0,
+                IRODORI_ERR_SHAPE, "dimensions must be positive");
+    IRO_REQUIRE(g.head_dim == 64, IRODORI_ERR_SHAPE, "head_dim must be 64");
+    IRO_REQUIRE(g.num_heads * g.head_dim == g.model_dim, IRODORI_ERR_SHAPE, "num_heads * head_dim must equal model_dim");
+    IRO_REQUIRE(g.model_dim % 64 == 0 && g.model_dim <= 2048, IRODORI_ERR_SHAPE,
+                "model_dim must be a multiple of 64 and <= 2048");
+    IRO_REQUIRE(g.mlp_hidden > 0 && g.mlp_hidden % 64 == 0, IRODORI_ERR_SHAPE, "mlp_hidden must be a positive multiple of 64");
+    IRO_REQUIRE(g.latent_dim <= 64, IRODORI_ERR_SHAPE, "latent_dim must be <= 64");
+    IRO_REQUIRE(g.adaln_rank > 0 && g.timestep_embed_dim > 0 && g.timestep_embed_dim % 2 == 0,
+                IRODORI_ERR_SHAPE, "adaln_rank > 0 and even timestep_embed_dim required");
+    IRO_REQUIRE(g.norm_eps > 0.f && std::isfinite(g.norm_eps), IRODORI_ERR_CONFIG, "norm_eps must be > 0");
+    IRO_REQUIRE(g.max_rows > 0 && g.max_seq > 0 && g.max_ctx >= 0, IRODORI_ERR_SHAPE, "max sizes must be positive");
+
+    int ndev = 0;
+    hipError_t e = hipGetDeviceCount(&ndev);
+    IRO_REQUIRE(e == hipSuccess && ndev > 0, IRODORI_ERR_HIP,
+                std::string("no HIP device available: ") + (e == hipSuccess ? "0 devices" : hipGetErrorString(e)));
+    IRO_REQUIRE(device >= 0 && device < ndev, IRODORI_ERR_INVALID_ARG, "device index out of range");
+    IRO_HIP_CHECK(hipSetDevice(device));
+
+    std::unique_ptr<irodori_ctx, int (*)(irodori_ctx*)> c(new irodori_ctx(), irodori_ctx_destroy);
+    c->device = device;
+    c->cfg = g;
+    c->bf16 = g.compute_dtype == IRODORI_DTYPE_BF16;
+    c->esz = c->bf16 ? 2 : 4;
+    IRO_HIP_CHECK(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
+
+    int D = g.model_dim, F = g.mlp_hidden, H = g.num_heads, Dh = g.head_dim, L = g.num_layers;
+    int R = g.max_rows, S = g.max_seq, T = g.max_ctx > 0 ? g.max_ctx : 1, P = g.latent_dim;
+    size_t es = c->esz, M = (size_t)R * S;
+    c->layers.resize(L);
+    int ntl = (T + 63) / 64;
+    for (int l = 0; l < L; l++) {
+        auto& lb = c->layers[l];
+        IRO_TRY(dev_alloc(c.get(), &lb.w_qkvg, es * 4 * D * D));
+        IRO_TRY(dev_alloc(c.get(), &lb.w_o, es * D * D));
+        IRO_TRY(dev_alloc(c.get(), &lb.w13, es * 2 * (size_t)F * D));
+        IRO_TRY(dev_alloc(c.get(), &lb.w2, es * (size_t)D * F));
+        IRO_TRY(dalloc(c.get(), &lb.q_norm, sizeof(float) * H * Dh));
+        IRO_TRY(dalloc(c.get(), &lb.k_norm, sizeof(float) * H * Dh));
+        for (int k = 0; k < 2; k++)
+            for (int ch = 0; ch < 3; ch++) {
+                IRO_TRY(dalloc(c.get(), &lb.ada_down[k][ch], sizeof(float) * (size_t)D * g.adaln_rank));
+                IRO_TRY(dalloc(c.get(), &lb.ada_up[k][ch], sizeof(float) * (size_t)g.adaln_rank * D));
+                IRO_TRY(dalloc(c.get(), &lb.ada_up_b[k][ch], sizeof(float) * D));
+            }
+        IRO_TRY(dev_alloc(c.get(), &lb.ctx_k, es * (size_t)R * H * T * Dh));
+        IRO_TRY(dev_alloc(c.get(), &lb.ctx_v, es * (size_t)R * H * T * Dh));
+        IRO_TRY(dalloc(c.get(), &lb.ctx_mask, sizeof(float) * (size_t)R * T));
+        IRO_TRY(dalloc(c.get(), &lb.tile_on, sizeof(int) * (size_t)R * ntl));
+        lb.row_set.assign(R, 0);
+    }
+    IRO_TRY(dalloc(c.get(), &c->cond_w0, sizeof(float) * (size_t)g.timestep_embed_dim * D));
+    IRO_TRY(dalloc(c.get(), &c->cond_w1, sizeof(float) * (size_t)D * D));
+    IRO_TRY(dalloc(c.get(), &c->cond_w2, sizeof(float) * (size_t)D * 3 * D));
+    IRO_TRY(dalloc(c.get(), &c->in_w, sizeof(float) * (size_t)P * D));
+    IRO_TRY(dalloc(c.get(), &c->in_b, sizeof(float) * D));
+    IRO_TRY(dalloc(c.get(), &c->out_norm_w, sizeof(float) * D));
+    IRO_TRY(dalloc(c.get(), &c->out_wT, sizeof(float) * (size_t)P * D));
+    IRO_TRY(dalloc(c.get(), &c->out_b, sizeof(float) * P));
+
+    IRO_TRY(dalloc(c.get(), &c->x, sizeof(float) * M * D));
+    IRO_TRY(dev_alloc(c.get(), &c->h, es * M * D));
+    IRO_TRY(dev_alloc(c.get(), &c->q, es * M * D));
+    IRO_TRY(dev_alloc(c.get(), &c->ks, es * M * D));
+    IRO_TRY(dev_alloc(c.get(), &c->vs, es * M * D));
+    IRO_TRY(dev_alloc(c.get(), &c->gate, es * M * D));
+    IRO_TRY(dev_alloc(c.get(), &c->o, es * M * D));
+    IRO_TRY(dev_alloc(c.get(), &c->u, es * M * F));
+    IRO_TRY(dalloc(c.get(), &c->rope_cos, sizeof(float) * (size_t)S * Dh / 2));
+    IRO_TRY(dalloc(c.get(), &c->rope_sin, sizeof(float) * (size_t)S * Dh / 2));
+    IRO_TRY(dalloc(c.get(), &c->xt, sizeof(float) * M * P));
+    IRO_TRY(dalloc(c.get(), &c->vout, sizeof(float) * M * P));
+    IRO_TRY(dalloc(c.get(), &c->step, sizeof(int)));
+    IRO_TRY(dalloc(c.get(), &c->zero_step, sizeof(int)));
+    IRO_HIP_CHECK(hipMemsetAsync(c->zero_step, 0, sizeof(int), c->stream));
+
+    std::vector<float> cs, sn;
+    host_rope_tables(S, Dh, g.rope_theta, cs, sn);
+    IRO_TRY(upload(c.get(), c->rope_cos, cs.data(), sizeof(float) * cs.size()));
+    IRO_TRY(upload(c.get(), c->rope_sin, sn.data(), sizeof(float) * sn.size()));
+    IRO_HIP_CHECK(hipStreamSynchronize(c->stream));
+    *out = c.release();
+    return IRODORI_OK;
+    IRO_GUARD_END
+}
+
+int irodori_ctx_device_bytes(const irodori_ctx* c, uint64_t* bytes) {
+    IRO_REQUIRE(c && bytes, IRODORI_ERR_INVALID_ARG, "null argument");
+    *bytes = c->dev_bytes;
+    return IRODORI_OK;
+}
+
+int irodori_load_io_weights(irodori_ctx* c, const irodori_io_weights* w) {
+    IRO_GUARD_BEGIN
+    IRO_REQUIRE(c && w, IRODORI_ERR_INVALID_ARG, "null argument");
+    IRO_REQUIRE(w->cond_w0 && w->cond_w1 && w->cond_w2 && w->in_w && w->in_b && w->out_norm_w &&
+                    w->out_w && w->out_b,
+                IRODORI_ERR_INVALID_ARG, "null io weight pointer");
+    IRO_HIP_CHECK(hipSetDevice(c->device));
+    const auto& g = c->cfg;
+    int D = g.model_dim, P = g.latent_dim;
+    IRO_TRY(upload(c, c->cond_w0, w->cond_w0, sizeof(float) * (size_t)g.timestep_embed_dim * D));
+    IRO_TRY(upload(c, c->cond_w1, w->cond_w1, sizeof(float) * (size_t)D * D));
+    IRO_TRY(upload(c, c->cond_w2, w->cond_w2, sizeof(float) * (size_t)D * 3 * D));
+    IRO_TRY(upload(c, c->in_w, w->in_w, sizeof(float) * (size_t)P * D));
+    IRO_TRY(upload(c, c->in_b, w->in_b, sizeof(float) * D));
+    IRO_TRY(upload(c, c->out_norm_w, w->out_norm_w, sizeof(float) * D));
+    std::vector<float> wt((size_t)P * D);
+    for (int d = 0; d < D; d++)
+        for (int p = 0; p < P; p++) wt[(size_t)p * D + d] = w->out_w[(size_t)d * P + p];
+    IRO_TRY(upload(c, c->out_wT, wt.data(), sizeof(float) * wt.size()));
+    IRO_TRY(upload(c, c->out_b, w->out_b, sizeof(float) * P));
+    IRO_HIP_CHECK(hipStreamSynchronize(c->stream));
+    c->io_loaded = true;
+    return IRODORI_OK;
+    IRO_GUARD_END
+}
+
+int irodori_load_block_weights(irodori_ctx* c, int layer, const irodori_block_weights* w) {
+    IRO_GUARD_BEGIN
+    IRO_REQUIRE(c && w, IRODORI_ERR_INVALID_ARG, "null argument");
+    IRO_REQUIRE(layer >= 0 && layer < c->cfg.num_layers, IRODORI_ERR_INVALID_ARG, "layer index out of range");
+    IRO_REQUIRE(w->w_qkv && w->w_gate && w->w_o && w->q_norm && w->k_norm && w->w13 && w->w2,
+                IRODORI_ERR_INVALID_ARG, "null block weight pointer");
+    for (int k = 0; k < 2; k++)
+        for (int ch = 0; ch < 3; ch++)
+            IRO_REQUIRE(w->ada_down[k][ch] && w->ada_up[k][ch] && w->ada_up_b[k][ch], IRODORI_ERR_INVALID_ARG,
+                        "null adaLN weight pointer");
+    IRO_HIP_CHECK(hipSetDevice(c->device));
+    const auto& g = c->cfg;
+    int D = g.model_dim, F = g.mlp_hidden, HD = g.num_heads * g.head_dim, r = g.adaln_rank;
+    auto& lb = c->layers[layer];
+    char* qkvg = static_cast<char*>(lb.w_qkvg);
+    IRO_TRY(ingest_kmajor(c, w->w_qkv, D, 3 * HD, 0, qkvg));
+    IRO_TRY(ingest_kmajor(c, w->w_gate, D, D, 0, qkvg + c->esz * (size_t)3 * HD * D));
+    IRO_TRY(ingest_kmajor(c, w->w_o, HD, D, 0, lb.w_o));
+    IRO_TRY(ingest_kmajor(c, w->w13, D, 2 * F, 1, lb.w13));
+    IRO_TRY(ingest_kmajor(c, w->w2, F, D, 0, lb.w2));
+    IRO_TRY(upload(c, lb.q_norm, w->q_norm, sizeof(float) * HD));
+    IRO_TRY(upload(c, lb.k_norm, w->k_norm, sizeof(float) * HD));
+    for (int k = 0; k < 2; k++)
+        for (int ch = 0; ch < 3; ch++) {
+            IRO_TRY(upload(c, lb.ada_down[k][ch], w->ada_down[k][ch], sizeof(float) * (size_t)D * r));
+            IRO_TRY(upload(c, lb.ada_up[k][ch], w->ada_up[k][ch], sizeof(float) * (size_t)r * D));
+            IRO_TRY(upload(c, lb.ada_up_b[k][ch], w->ada_up_b[k][ch], sizeof(float) * D));
+        }
+    IRO_HIP_CHECK(hipStreamSynchronize(c->stream));
+    lb.loaded = true;
+    return IRODORI_OK;
+    IRO_GUARD_END
+}
+
+int irodori_clear_ctx_kv(irodori_ctx* c) {
+    IRO_REQUIRE(c, IRODORI_ERR_INVALID_ARG, "null context");
+    c->t_ctx = -1;
+    for (auto& lb : c->layers) std::fill(lb.row_set.begin(), lb.row_set.end(), 0);
+    for (auto& kv : c->graphs) (void)hipGraphExecDestroy(kv.second);
+    c->graphs.clear();
+    return IRODORI_OK;
+}
+
+int irodori_set_ctx_kv(irodori_ctx* c, int layer, int row, int t_ctx, const float* k, const float* v,
+                       const uint8_t* mask) {
+    IRO_GUARD_BEGIN
+    IRO_REQUIRE(c, IRODORI_ERR_INVALID_ARG, "null context");
+    const auto& g = c->cfg;
+    IRO_REQUIRE(layer >= 0 && layer < g.num_layers, IRODORI_ERR_INVALID_ARG, "layer index out of range");
+    IRO_REQUIRE(row >= 0 && row < g.max_rows, IRODORI_ERR_INVALID_ARG, "row index out of range");
+    IRO_REQUIRE(t_ctx >= 0 && t_ctx <= g.max_ctx, IRODORI_ERR_SHAPE,
+                "t_ctx " + std::to_string(t_ctx) + " exceeds max_ctx " + std::to_string(g.max_ctx));
+    IRO_REQUIRE(c->t_ctx < 0 || c->t_ctx == t_ctx, IRODORI_ERR_SHAPE,
+                "t_ctx must match the context length already set (" + std::to_string(c->t_ctx) +
+                    "); call irodori_clear_ctx_kv first");
+    IRO_REQUIRE(t_ctx == 0 || (k && v && mask), IRODORI_ERR_INVALID_ARG, "null k/v/mask");
+    IRO_HIP_CHECK(hipSetDevice(c->device));
+    auto& lb = c->layers[layer];
+    int H = g.num_heads, Dh = g.head_dim, T = g.max_ctx > 0 ? g.max_ctx : 1;
+    if (t_ctx > 0) {
+        // [t, H, Dh] f32 -> [H, T(max), Dh] compute dtype for this row; pad keys masked.
+        size_t n = (size_t)H * T * Dh;
+        std::vector<uint16_t> kb, vb;
+        std::vector<float> kf, vf;
+        if (c->bf16) { kb.assign(n, 0); vb.assign(n, 0); } else { kf.assign(n, 0.f); vf.assign(n, 0.f); }
+        for (int j = 0; j < t_ctx; j++)
+            for (int hh = 0; hh < H; hh++)
+                for (int d = 0; d < Dh; d++) {
+                    size_t src = ((size_t)j * H + hh) * Dh + d, dst = ((size_t)hh * T + j) * Dh + d;
+                    if (c->bf16) {
+                        auto cvt = [](float f) -> uint16_t {
+                            uint32_t u;
+                            memcpy(&u, &f, 4);
+                            if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+                            u += 0x7fffu + ((u >> 16) & 1u);
+                            return (uint16_t)(u >> 16);
+                        };
+                        kb[dst] = cvt(k[src]);
+                        vb[dst] = cvt(v[src]);
+                    } else {
+                        kf[dst] = k[src];
+                        vf[dst] = v[src];
+                    }
+                }
+        size_t off = (size_t)row * n * c->esz;
+        IRO_TRY(upload(c, static_cast<char*>(lb.ctx_k) + off, c->bf16 ? (const void*)kb.data() : kf.data(), n * c->esz));
+        IRO_TRY(upload(c, static_cast<char*>(lb.ctx_v) + off, c->bf16 ? (const void*)vb.data() : vf.data(), n * c->esz));
+        std::vector<float> m(T, 0.f);
+        int ntl = (T + 63) / 64;
+        std::vector<int> on(ntl, 0);
+        for (int j = 0; j < t_ctx; j++) {
+            m[j] = mask[j] ? 1.f : 0.f;
+            if (mask[j]) on[j / 64] = 1;
+        }
+        IRO_TRY(upload(c, lb.ctx_mask + (size_t)row * T, m.data(), sizeof(float) * T));
+        IRO_TRY(upload(c, lb.tile_on + (size_t)row * ntl, on.data(), sizeof(int) * ntl));
+        IRO_HIP_CHECK(hipStreamSynchronize(c->stream));
+    }
+    if (c->t_ctx != t_ctx) {
+        for (auto& kv : c->graphs) (void)hipGraphExecDestroy(kv.second);
+        c->graphs.clear();
+    }
+    c->t_ctx = t_ctx;
+    lb.row_set[row] = 1;
+    return IRODORI_OK;
+    IRO_GUARD_END
+}
+
+int irodori_forward(irodori_ctx* c, int B, int S, const float* x_t, const float* t, float* v_out, float* debug) {
+    IRO_GUARD_BEGIN
+    IRO_REQUIRE(c && x_t && t && v_out, IRODORI_ERR_INVALID_ARG, "null argument");
+    const auto& g = c->cfg;
+    IRO_REQUIRE(B > 0 && B <= g.max_rows, IRODORI_ERR_SHAPE, "batch out of range [1, max_rows]");
+    IRO_REQUIRE(S > 0 && S <= g.max_seq, IRODORI_ERR_SHAPE, "seq out of range [1, max_seq]");
+    IRO_TRY(check_ready(c, B));
+    IRO_HIP_CHECK(hipSetDevice(c->device));
+    int D = g.model_dim, P = g.latent_dim, L = g.num_layers;
+    IRO_TRY(ensure_nvec(c, B));
+    IRO_TRY(upload(c, c->tvec, t, sizeof(float) * B));
+    IRO_TRY(upload(c, c->xt, x_t, sizeof(float) * (size_t)B * S * P));
+    IRO_TRY(enqueue_mod_table(c, B, false));
+    ModTable mt{c->tab, c->zero_step, 0, 1, L};
+    IRO_TRY(enqueue_inproj(c, B, S, 1, mt));
+    size_t n = (size_t)B * S * D;
+    if (debug) IRO_HIP_CHECK(hipMemcpyAsync(debug, c->x, sizeof(float) * n, hipMemcpyDeviceToHost, c->stream));
+    for (int l = 0; l < L; l++) {
+        IRO_TRY(enqueue_layer_any(c, l, B, S, mt, l + 1 == L));
+        if (debug)
+            IRO_HIP_CHECK(hipMemcpyAsync(debug + (size_t)(l + 1) * n, c->x, sizeof(float) * n, hipMemcpyDeviceToHost,
+                                         c->stream));
+    }
+    FinalArgs fa{};
+    fa.x = c->x;
+    fa.norm_w = c->out_norm_w;
+    fa.out_wT = c->out_wT;
+    fa.out_b = c->out_b;
+    fa.B = B;
+    fa.S = S;
+    fa.D = D;
+    fa.P = P;
+    fa.eps = g.norm_eps;
+    fa.mode = 0;
+    fa.v_out = c->vout;
+    launch_final(fa, c->stream);
+    IRO_TRY(check_launch("output head"));
+    IRO_HIP_CHECK(hipMemcpyAsync(v_out, c->vout, sizeof(float) * (size_t)B * S * P, hipMemcpyDeviceToHost, c->stream));
+    IRO_HIP_CHECK(hipStreamSynchronize(c->stream));
+    return IRODORI_OK;
+    IRO_GUARD_END
+}
+
+int irodori_block_forward(irodori_ctx* c, int layer, int B, int S, float* x, const float* cond) {
+    IRO_GUARD_BEGIN
+    IRO_REQUIRE(c && x && cond, IRODORI_ERR_INVALID_ARG, "null argument");
+    const auto& g = c->cfg;
+    IRO_REQUIRE(layer >= 0 && layer < g.num_layers, IRODORI_ERR_INVALID_ARG, "layer index out of range");
+    IRO_REQUIRE(B > 0 && B <= g.max_rows && S > 0 && S <= g.max_seq, IRODORI_ERR_SHAPE, "batch/seq out of range");
+    IRO_REQUIRE(c->layers[layer].loaded, IRODORI_ERR_NOT_LOADED, "block weights not loaded");
+    if (c->t_ctx > 0)
+        for (int r = 0; r < B; r++)
+            IRO_REQUIRE(c->layers[layer].row_set[r], IRODORI_ERR_NOT_LOADED, "context KV not set for a row");
+    IRO_HIP_CHECK(hipSetDevice(c->device));
+    int D = g.model_dim, L = g.num_layers;
+    IRO_TRY(ensure_nvec(c, B));
+    IRO_TRY(upload(c, c->cond, cond, sizeof(float) * (size_t)B * 3 * D));
+    IRO_TRY(enqueue_mod_table(c, B, true));
+    ModTable mt{c->tab, c->zero_step, 0, 1, L};
+    size_t n = (size_t)B * S * D;
+    IRO_TRY(upload(c, c->x, x, sizeof(float) * n));
+    if (c->bf16)
+        launch_norm_mod<bf16>(c->x, static_cast<bf16*>(c->h), B * S, S, D, g.norm_eps, mt, layer, 0, c->stream);
+    else
+        launch_norm_mod<float>(c->x, static_cast<float*>(c->h), B * S, S, D, g.norm_eps, mt, layer, 0, c->stream);
+    IRO_TRY(enqueue_layer_any(c, layer, B, S, mt, true));
+    IRO_HIP_CHECK(hipMemcpyAsync(x, c->x, sizeof(float) * n, hipMemcpyDeviceToHost, c->stream));
+    IRO_HIP_CHECK(hipStreamSynchronize(c->stream));
+    return IRODORI_OK;
+    IRO_GUARD_END
+}
+
+int irodori_sample_device(irodori_ctx* c, const irodori_sampler_params* p, int U, int S, const float* d_x0,
+                          float* d_x_out) {
+    IRO_GUARD_BEGIN
+    IRO_REQUIRE(c && p && d_x0 && d_x_out, IRODORI_ERR_INVALID_ARG, "null argument");
+    IRO_TRY(validate_params(p));
+    IRO_REQUIRE(p->cfg_mode == IRODORI_CFG_JOINT, IRODORI_ERR_CONFIG,
+                "the HIP sampler implements cfg_guidance_mode=Joint");
+    IRO_REQUIRE(p->method == IRODORI_METHOD_EULER, IRODORI_ERR_CONFIG, "the HIP sampler implements the Euler method");
+    const auto& g = c->cfg;
+    int B = 2 * U;
+    IRO_REQUIRE(U > 0 && B <= g.max_rows, IRODORI_ERR_SHAPE, "2 * utterances must be in [2, max_rows]");
+    IRO_REQUIRE(S > 0 && S <= g.max_seq, IRODORI_ERR_SHAPE, "seq out of range [1, max_seq]");
+    IRO_TRY(check_ready(c, B));
+    IRO_HIP_CHECK(hipSetDevice(c->device));
+    int N = p->num_steps, P = g.latent_dim;
+
+    // Schedule (euler_sampler.rs:325-328, f32) and per-step CFG window (:379).
+    std::vector<float> ts(N + 1);
+    std::vector<int> on(N);
+    for (int i = 0; i <= N; i++) ts[i] = 0.999f * (1.0f - (float)i / (float)N);
+    float scale = joint_scale(p);
+    for (int i = 0; i < N; i++) on[i] = (scale > 0.f && p->min_t <= ts[i] && ts[i] <= p->max_t) ? 1 : 0;
+    IRO_TRY(ensure_nvec(c, N));
+    if (N + 1 > c->sched_cap) {
+        IRO_HIP_CHECK(hipStreamSynchronize(c->stream));
+        IRO_TRY(dalloc(c, &c->t_sched, sizeof(float) * (N + 1)));
+        IRO_TRY(dalloc(c, &c->cfg_on, sizeof(int) * (N + 1)));
+        c->sched_cap = N + 1;
+        for (auto& kv : c->graphs) (void)hipGraphExecDestroy(kv.second);
+        c->graphs.clear();
+    }
+    IRO_TRY(upload(c, c->t_sched, ts.data(), sizeof(float) * (N + 1)));
+    IRO_TRY(upload(c, c->cfg_on, on.data(), sizeof(int) * N));
+    IRO_TRY(upload(c, c->tvec, ts.data(), sizeof(float) * N));
+    IRO_TRY(enqueue_mod_table(c, N, false));
+    launch_scale_copy(d_x0, c->xt, U * S * P, p->has_truncation ? p->truncation_factor : 1.0f, c->stream);
+    IRO_HIP_CHECK(hipMemsetAsync(c->step, 0, sizeof(int), c->stream));
+    IRO_TRY(check_launch("sampler setup"));
+
+    // One captured RF step, replayed N times.
+    uint32_t sbits;
+    memcpy(&sbits, &scale, 4);
+    GraphKey key{B, S, c->t_ctx, sbits};
+    hipGraphExec_t exec = nullptr;
+    auto it = c->graphs.find(key);
+    if (it != c->graphs.end()) {
+        exec = it->second;
+    } else {
+        hipGraph_t graph = nullptr;
+        IRO_HIP_CHECK(hipStreamSynchronize(c->stream));
+        IRO_HIP_CHECK(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+        int rc = enqueue_rf_step(c, B, S, scale);
+        hipError_t ee = hipStreamEndCapture(c->stream, &graph);
+        if (rc != IRODORI_OK) {
+            if (graph) (void)hipGraphDestroy(graph);
+            return rc;
+        }
+        if (ee != hipSuccess) {
+            set_last_error(std::string("graph capture: ") + hipGetErrorString(ee));
+            return IRODORI_ERR_HIP;
+        }
+        ee = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        if (ee != hipSuccess) {
+            set_last_error(std::string("graph instantiate: ") + hipGetErrorString(ee));
+            return IRODORI_ERR_HIP;
+        }
+        c->graphs[key] = exec;
+    }
+    for (int i = 0; i < N; i++) IRO_HIP_CHECK(hipGraphLaunch(exec, c->stream));
+    IRO_HIP_CHECK(hipMemcpyAsync(d_x_out, c->xt, sizeof(float) * (size_t)U * S * P, hipMemcpyDeviceToDevice, c->stream));
+    IRO_HIP_CHECK(hipStreamSynchronize(c->stream));
+    return IRODORI_OK;
+    IRO_GUARD_END
+}
+
+int irodori_sample(irodori_ctx* c, const irodori_sampler_params* p, int U, int S, const float* x0, float* x_out) {
+    IRO_GUARD_BEGIN
+    IRO_REQUIRE(c && p && x0 && x_out, IRODORI_ERR_INVALID_ARG, "null argument");
+    IRO_TRY(validate_params(p));
+    const auto& g = c->cfg;
+    IRO_REQUIRE(U > 0 && 2 * U <= g.max_rows && S > 0 && S <= g.max_seq, IRODORI_ERR_SHAPE, "utterances/seq out of range");
+    IRO_HIP_CHECK(hipSetDevice(c->device));
+    size_t n = (size_t)U * S * g.latent_dim;
+    // Stage through the forward-output buffer (unused by the sampler).
+    IRO_TRY(upload(c, c->vout, x0, sizeof(float) * n));
+    int rc = irodori_sample_device(c, p, U, S, c->vout, c->vout);
+    if (rc != IRODORI_OK) return rc;
+    IRO_HIP_CHECK(hipMemcpy(x_out, c->vout, sizeof(float) * n, hipMemcpyDeviceToHost));
+    return IRODORI_OK;
+    IRO_GUARD_END
+}
+
+int irodori_profile_layer(irodori_ctx* c, int B, int S, int iters, irodori_kernel_times* out) {
+    IRO_GUARD_BEGIN
+    IRO_REQUIRE(c && out, IRODORI_ERR_INVALID_ARG, "null argument");
+    const auto& g = c->cfg;
+    IRO_REQUIRE(B > 0 && B <= g.max_rows && B % 2 == 0 && S > 0 && S <= g.max_seq, IRODORI_ERR_SHAPE,
+                "batch must be even and <= max_rows, seq <= max_seq");
+    IRO_REQUIRE(iters > 0, IRODORI_ERR_INVALID_ARG, "iters must be > 0");
+    IRO_TRY(check_ready(c, B));
+    IRO_HIP_CHECK(hipSetDevice(c->device));
+    int D = g.model_dim, H = g.num_heads, F = g.mlp_hidden, M = B * S, L = g.num_layers;
+    // Modulation vectors for t = 0.5 on every row; state from one in_proj of zeros + 1.
+    std::vector<float> t(B, 0.5f), x0((size_t)B * S * g.latent_dim, 1.0f);
+    IRO_TRY(ensure_nvec(c, B));
+    IRO_TRY(upload(c, c->tvec, t.data(), sizeof(float) * B));
+    IRO_TRY(upload(c, c->xt, x0.data(), sizeof(float) * x0.size()));
+    IRO_TRY(enqueue_mod_table(c, B, false));
+    ModTable mt{c->tab, c->zero_step, 0, 1, L};
+    IRO_TRY(enqueue_inproj(c, B, S, 1, mt));
+    IRO_TRY(enqueue_layer_any(c, 0, B, S, mt, false));  // fills q/k/v/gate/o/u
+    IRO_HIP_CHECK(hipStreamSynchronize(c->stream));
+
+    hipEvent_t e0, e1;
+    IRO_HIP_CHECK(hipEventCreate(&e0));
+    IRO_HIP_CHECK(hipEventCreate(&e1));
+    float* outs[7] = {&out->norm_mod_us, &out->qkvg_gemm_us, &out->attention_us, &out->wo_gemm_us,
+                      &out->w13_gemm_us, &out->w2_gemm_us, &out->final_us};
+    auto& lb = c->layers[0];
+    int rc = IRODORI_OK;
+    for (int kidx = 0; kidx < 7 && rc == IRODORI_OK; kidx++) {
+        (void)hipEventRecord(e0, c->stream);
+        for (int it = 0; it < iters; it++) {
+            if (kidx == 6) {
+                FinalArgs fa{};
+                fa.x = c->x; fa.norm_w = c->out_norm_w; fa.out_wT = c->out_wT; fa.out_b = c->out_b;
+                fa.B = B; fa.S = S; fa.D = D; fa.P = g.latent_dim; fa.eps = g.norm_eps;
+                fa.mode = 0; fa.v_out = c->vout;
+                launch_final(fa, c->stream);
+                continue;
+            }
+            if (c->bf16) {
+                using T = bf16;
+                if (kidx == 0) { launch_norm_mod<T>(c->x, static_cast<T*>(c->h), M, S, D, g.norm_eps, mt, 0, 1, c->stream); continue; }
+                if (kidx == 2) {
+                    AttnArgs<T> aa{};
+                    aa.Q = static_cast<const T*>(c->q); aa.K0 = static_cast<const T*>(c->ks);
+                    aa.V0 = static_cast<const T*>(c->vs); aa.len0 = S; aa.stride0 = S;
+                    if (c->t_ctx > 0) {
+                        aa.K1 = static_cast<const T*>(lb.ctx_k); aa.V1 = static_cast<const T*>(lb.ctx_v);
+                        aa.len1 = c->t_ctx; aa.stride1 = g.max_ctx; aa.mask1 = lb.ctx_mask; aa.tile_on1 = lb.tile_on;
+                    }
+                    aa.B = B; aa.H = H; aa.Sq = S; aa.scale = 1.0f / sqrtf((float)g.head_dim);
+                    aa.out_mode = 0; aa.G = static_cast<const T*>(c->gate); aa.O = static_cast<T*>(c->o);
+                    launch_attention<T, 64>(aa, c->stream);
+                    continue;
+                }
+                GemmArgs<T> ga{};
+                ga.mt = mt; ga.S = S; ga.layer = 0; ga.H = H; ga.D = D; ga.eps = g.norm_eps; ga.M = M;
+                ga.x = c->x;
+                if (kidx == 1) {
+                    ga.A = static_cast<const T*>(c->h); ga.W = static_cast<const T*>(lb.w_qkvg); ga.N = 4 * D; ga.K = D;
+                    ga.Q = static_cast<T*>(c->q); ga.Kd = static_cast<T*>(c->ks); ga.Vd = static_cast<T*>(c->vs);
+                    ga.G = static_cast<T*>(c->gate); ga.q_norm = lb.q_norm; ga.k_norm = lb.k_norm;
+                    ga.rope_cos = c->rope_cos; ga.rope_sin = c->rope_sin;
+                    launch_gemm<T>(EPI_QKVG, ga, c->stream);
+                } else if (kidx == 3) {
+                    ga.A = static_cast<const T*>(c->o); ga.W = static_cast<const T*>(lb.w_o); ga.N = D; ga.K = D; ga.kind = 0;
+                    launch_gemm<T>(EPI_RESID, ga, c->stream);
+                } else if (kidx == 4) {
+                    ga.A = static_cast<const T*>(c->h); ga.W = static_cast<const T*>(lb.w13); ga.N = 2 * F; ga.K = D;
+                    ga.U = static_cast<T*>(c->u);
+                    launch_gemm<T>(EPI_SWIGLU, ga, c->stream);
+                } else {
+                    ga.A = static_cast<const T*>(c->u); ga.W = static_cast<const T*>(lb.w2); ga.N = D; ga.K = F; ga.kind = 1;
+                    launch_gemm<T>(EPI_RESID, ga, c->stream);
+                }
+            } else {
+                rc = IRODORI_ERR_DTYPE;
+                set_last_error("irodori_profile_layer times the bf16 path");
+                break;
+            }
+        }
+        (void)hipEventRecord(e1, c->stream);
+        hipError_t se = hipEventSynchronize(e1);
+        float ms = 0.f;
+        if (se == hipSuccess) se = hipEventElapsedTime(&ms, e0, e1);
+        if (se != hipSuccess && rc == IRODORI_OK) {
+            set_last_error(std::string("profile events: ") + hipGetErrorString(se));
+            rc = IRODORI_ERR_HIP;
+        }
+        *outs[kidx] = ms * 1000.f / (float)iters;
+    }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (rc != IRODORI_OK) return rc;
+    return check_launch("profile");
+    IRO_GUARD_END
+}
+
+// ---- operator entry points ------------------------------------------------------------
+
+int irodori_op_rms_norm(const float* x, const float* w, int rows, int dim, float eps, float* y, void* stream) {
+    IRO_GUARD_BEGIN
+    IRO_REQUIRE(x && w && y, IRODORI_ERR_INVALID_ARG, "null argument");
+    IRO_REQUIRE(rows > 0 && dim > 0, IRODORI_ERR_SHAPE, "RMSNorm requires rows > 0 and dim > 0");
+    launch_rms_norm_op(x, w, rows, dim, eps, y, static_cast<hipStream_t>(stream));
+    return check_launch("rms_norm");
+    IRO_GUARD_END
+}
+
+int irodori_op_fused_adaln(const float* x, const float* scale, const float* shift, int batch, int seq, int dim,
+                           float eps, float* y, void* stream) {
+    IRO_GUARD_BEGIN
+    IRO_REQUIRE(x && scale && shift && y, IRODORI_ERR_INVALID_ARG, "null argument");
+    IRO_REQUIRE(batch > 0 && seq > 0 && dim > 0, IRODORI_ERR_SHAPE, "fused AdaLN requires positive dims");
+    launch_fused_adaln_op(x, scale, shift, batch, seq, dim, eps, y, static_cast<hipStream_t>(stream));
+    return check_launch("fused_adaln");
+    IRO_GUARD_END
+}
+
+int irodori_op_sdpa(int dtype, const void* q, const void* k, const void* v, const float* mask, int B, int H, int Sq,
+                    int Skv, int Dh, float scale, float* out, void* stream) {
+    IRO_GUARD_BEGIN
+    IRO_REQUIRE(q && k && v && out, IRODORI_ERR_INVALID_ARG, "null argument");
+    IRO_REQUIRE(B > 0 && H > 0 && Sq > 0 && Skv > 0, IRODORI_ERR_SHAPE, "SDPA dims must be positive");
+    IRO_REQUIRE(Dh == 64 || Dh == 128, IRODORI_ERR_SHAPE, "head_dim must be 64 or 128");
+    IRO_REQUIRE(dtype == IRODORI_DTYPE_F32 || dtype == IRODORI_DTYPE_BF16, IRODORI_ERR_DTYPE, "dtype must be F32 or BF16");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    int rc;
+    if (dtype == IRODORI_DTYPE_BF16) {
+        AttnArgs<bf16> a{};
+        a.Q = static_cast<const bf16*>(q);
+        a.K0 = static_cast<const bf16*>(k);
+        a.V0 = static_cast<const bf16*>(v);
+        a.len0 = Skv; a.stride0 = Skv; a.mask0 = mask;
+        a.B = B; a.H = H; a.Sq = Sq; a.scale = scale; a.out_mode = 1; a.Of = out;
+        rc = Dh == 64 ? launch_attention<bf16, 64>(a, st) : launch_attention<bf16, 128>(a, st);
+    } else {
+        AttnArgs<float> a{};
+        a.Q = static_cast<const float*>(q);
+        a.K0 = static_cast<const float*>(k);
+        a.V0 = static_cast<const float*>(v);
+        a.len0 = Skv; a.stride0 = Skv; a.mask0 = mask;
+        a.B = B; a.H = H; a.Sq = Sq; a.scale = scale; a.out_mode = 1; a.Of = out;
+        rc = Dh == 64 ? launch_attention<float, 64>(a, st) : launch_attention<float, 128>(a, st);
+    }
+    IRO_REQUIRE(rc == 0, IRODORI_ERR_SHAPE, "sdpa launch rejected the shape");
+    return check_launch("sdpa");
+    IRO_GUARD_END
+}
+
+}  // extern "C"

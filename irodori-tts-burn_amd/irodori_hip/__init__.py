@@ -1,0 +1,17 @@
+"""irodori_hip — MI355X (gfx950) RF-step DiT forward for Irodori-TTS behind a C ABI.
+
+Host-side mirror of the reference's inference API for the HIP backend:
+`InferenceBackendKind.HIP_BF16 / HIP_F32`, `SamplerParams`, `GuidanceConfig`, and
+`HipInferenceEngine` (forward_with_cond_cached / sample over libirodori_hip.so).
+"""
+from .config import (CfgGuidanceMode, DitConfig, GuidanceConfig, InferenceBackendKind,
+                     IrodoriError, SamplerMethod, SamplerParams, cfg_cpu_plumbing, cfg_full_rf,
+                     cfg_tiny)
+from .engine import HipInferenceEngine, ops
+from .synthetic import ContextKV, DitWeights, make_context_kv, make_noise
+
+__all__ = [
+    "CfgGuidanceMode", "DitConfig", "GuidanceConfig", "InferenceBackendKind", "IrodoriError",
+    "SamplerMethod", "SamplerParams", "cfg_cpu_plumbing", "cfg_full_rf", "cfg_tiny",
+    "HipInferenceEngine", "ops", "ContextKV", "DitWeights", "make_context_kv", "make_noise",
+]

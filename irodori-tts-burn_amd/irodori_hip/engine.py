@@ -1,0 +1,186 @@
+"""HipInferenceEngine: the HIP backend's InferenceEngine over libirodori_hip.so.
+
+Mirrors the reference's API for the hot path:
+  - construction + load_weights  ~ InferenceBuilder -> InferenceEngine
+    (src/inference.rs:83-196) with InferenceOptimizedModel fusion (optimized.rs:37-62);
+  - set_context_kv               ~ build_kv_caches / CondKvCache (dit/model.rs:444-472);
+  - forward_with_cond_cached     ~ optimized.rs:102-113 (one DiT forward);
+  - sample                       ~ InferenceEngine::sample -> sample_euler_rf_cfg
+    (inference.rs:222-227, euler_sampler.rs:132-718), Joint CFG.
+Errors map the C status codes onto IrodoriError variants (src/error.rs:4-60).
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import _lib as L
+from .config import (CfgGuidanceMode, DitConfig, InferenceBackendKind, IrodoriError,
+                     SamplerMethod, SamplerParams)
+from .synthetic import ContextKV, DitWeights
+
+_f32p = C.POINTER(C.c_float)
+
+
+def _check(rc: int) -> None:
+    if rc != L.OK:
+        raise IrodoriError(L.ERR_NAMES.get(rc, "Unknown(%d)" % rc), L.last_error())
+
+
+def _fp(a: np.ndarray):
+    assert a.dtype == np.float32 and a.flags.c_contiguous
+    return a.ctypes.data_as(_f32p)
+
+
+def _c32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def sampler_params_c(p: SamplerParams, has_speaker: bool = True) -> L.SamplerParamsC:
+    mode = {CfgGuidanceMode.INDEPENDENT: L.CFG_INDEPENDENT, CfgGuidanceMode.JOINT: L.CFG_JOINT,
+            CfgGuidanceMode.ALTERNATING: L.CFG_ALTERNATING}[p.guidance.mode]
+    method = {SamplerMethod.EULER: L.METHOD_EULER, SamplerMethod.HEUN: L.METHOD_HEUN,
+              SamplerMethod.PLMS4: L.METHOD_PLMS4}[p.method]
+    g = p.guidance
+    return L.SamplerParamsC(p.num_steps, method, mode, g.scale_text, g.scale_caption,
+                            g.scale_speaker, g.min_t, g.max_t,
+                            1 if p.truncation_factor is not None else 0,
+                            p.truncation_factor if p.truncation_factor is not None else 0.0,
+                            1 if has_speaker else 0)
+
+
+def validate_sampler_params(p: SamplerParams, has_speaker: bool = True) -> None:
+    """SamplerParams::validate (params.rs:99-183), evaluated by the library."""
+    c = sampler_params_c(p, has_speaker)
+    _check(L.load().irodori_sampler_params_validate(C.byref(c)))
+
+
+class HipInferenceEngine:
+    def __init__(self, cfg: DitConfig, backend: InferenceBackendKind = InferenceBackendKind.HIP_BF16,
+                 max_rows: int = 2, max_seq: int = 750, max_ctx: int = 631, device: int = 0):
+        cfg.validate()
+        self.cfg = cfg
+        self.backend = backend
+        self.lib = L.load()
+        c = L.DitConfigC(cfg.latent_dim, cfg.model_dim, cfg.num_layers, cfg.num_heads,
+                         cfg.head_dim, cfg.mlp_hidden, cfg.adaln_rank, cfg.timestep_embed_dim,
+                         cfg.norm_eps, cfg.rope_theta,
+                         L.DTYPE_BF16 if backend is InferenceBackendKind.HIP_BF16 else L.DTYPE_F32,
+                         max_rows, max_seq, max_ctx)
+        h = C.c_void_p()
+        _check(self.lib.irodori_ctx_create(device, C.byref(c), C.byref(h)))
+        self.ctx = h
+        self.max_rows, self.max_seq, self.max_ctx = max_rows, max_seq, max_ctx
+
+    def close(self) -> None:
+        if getattr(self, "ctx", None):
+            self.lib.irodori_ctx_destroy(self.ctx)
+            self.ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def device_bytes(self) -> int:
+        n = C.c_uint64()
+        _check(self.lib.irodori_ctx_device_bytes(self.ctx, C.byref(n)))
+        return int(n.value)
+
+    # ---- weights / context --------------------------------------------------------------
+    def load_weights(self, w: DitWeights) -> None:
+        io = L.IoWeightsC(*[_fp(w.io[k]) for k in ("cond_w0", "cond_w1", "cond_w2", "in_w",
+                                                     "in_b", "out_norm_w", "out_w", "out_b")])
+        _check(self.lib.irodori_load_io_weights(self.ctx, C.byref(io)))
+        for l, b in enumerate(w.blocks):
+            s = L.BlockWeightsC()
+            for k in ("w_qkv", "w_gate", "w_o", "q_norm", "k_norm", "w13", "w2"):
+                setattr(s, k, _fp(b[k]))
+            for i in range(2):
+                for ch in range(3):
+                    s.ada_down[i][ch] = _fp(b["ada_down"][i][ch])
+                    s.ada_up[i][ch] = _fp(b["ada_up"][i][ch])
+                    s.ada_up_b[i][ch] = _fp(b["ada_up_b"][i][ch])
+            _check(self.lib.irodori_load_block_weights(self.ctx, l, C.byref(s)))
+
+    def set_context_kv(self, ctx: ContextKV) -> None:
+        _check(self.lib.irodori_clear_ctx_kv(self.ctx))
+        Lc, B, T = ctx.k.shape[:3]
+        for l in range(Lc):
+            for r in range(B):
+                k = _c32(ctx.k[l, r])
+                v = _c32(ctx.v[l, r])
+                m = np.ascontiguousarray(ctx.mask[r], np.uint8)
+                _check(self.lib.irodori_set_ctx_kv(self.ctx, l, r, T, _fp(k), _fp(v),
+                                                   m.ctypes.data_as(C.POINTER(C.c_uint8))))
+
+    # ---- compute ------------------------------------------------------------------------
+    def forward_with_cond_cached(self, x_t: np.ndarray, t: np.ndarray, debug: bool = False):
+        """x_t [B,S,P], t [B] -> v [B,S,P] (and [L+1,B,S,D] block outputs if debug)."""
+        x_t = _c32(x_t)
+        t = _c32(t)
+        B, S, P = x_t.shape
+        v = np.empty_like(x_t)
+        dbg = (np.empty((self.cfg.num_layers + 1, B, S, self.cfg.model_dim), np.float32)
+               if debug else None)
+        _check(self.lib.irodori_forward(self.ctx, B, S, _fp(x_t), _fp(t), _fp(v),
+                                        _fp(dbg) if debug else None))
+        return (v, dbg) if debug else v
+
+    def block_forward(self, layer: int, x: np.ndarray, cond: np.ndarray) -> np.ndarray:
+        """One DiffusionBlock::forward_fused on x [B,S,D] with cond_module output [B,3D]."""
+        x = _c32(x).copy()
+        B, S, _ = x.shape
+        _check(self.lib.irodori_block_forward(self.ctx, layer, B, S, _fp(x), _fp(_c32(cond))))
+        return x
+
+    def sample(self, x0: np.ndarray, params: SamplerParams, has_speaker: bool = True) -> np.ndarray:
+        """Joint-CFG RF sampling of U utterances: x0 [U,S,P] -> x [U,S,P]."""
+        x0 = _c32(x0)
+        U, S, P = x0.shape
+        out = np.empty_like(x0)
+        pc = sampler_params_c(params, has_speaker)
+        _check(self.lib.irodori_sample(self.ctx, C.byref(pc), U, S, _fp(x0), _fp(out)))
+        return out
+
+    def sample_device(self, d_x0: int, d_out: int, utterances: int, seq: int,
+                      params: SamplerParams, has_speaker: bool = True) -> None:
+        """Same as sample() on device pointers (inputs/outputs resident in HBM)."""
+        pc = sampler_params_c(params, has_speaker)
+        _check(self.lib.irodori_sample_device(self.ctx, C.byref(pc), utterances, seq,
+                                              C.c_void_p(d_x0), C.c_void_p(d_out)))
+
+
+    def profile_layer(self, batch: int, seq: int, iters: int = 20) -> dict:
+        """Average microseconds per kernel of one block (HIP events on the context stream)."""
+        kt = L.KernelTimesC()
+        _check(self.lib.irodori_profile_layer(self.ctx, batch, seq, iters, C.byref(kt)))
+        return {n: float(getattr(kt, n)) for n, _ in L.KernelTimesC._fields_}
+
+
+class ops:
+    """Operator entry points (src/kernels analogues) on device pointers."""
+
+    @staticmethod
+    def rms_norm(d_x: int, d_w: int, rows: int, dim: int, eps: float, d_y: int,
+                 stream: int = 0) -> None:
+        _check(L.load().irodori_op_rms_norm(d_x, d_w, rows, dim, eps, d_y, stream or None))
+
+    @staticmethod
+    def fused_adaln(d_x, d_scale, d_shift, batch, seq, dim, eps, d_y, stream: int = 0) -> None:
+        _check(L.load().irodori_op_fused_adaln(d_x, d_scale, d_shift, batch, seq, dim, eps, d_y,
+                                               stream or None))
+
+    @staticmethod
+    def sdpa(dtype: int, d_q, d_k, d_v, d_mask, batch, heads, seq_q, seq_kv, head_dim, scale,
+             d_out, stream: int = 0) -> None:
+        _check(L.load().irodori_op_sdpa(dtype, d_q, d_k, d_v, d_mask or None, batch, heads, seq_q,
+                                        seq_kv, head_dim, scale, d_out, stream or None))

@@ -1,0 +1,136 @@
+"""Seeded synthetic inputs for the RF-step DiT: random-init weights, context KV, noise.
+
+The reference's random-init constructors zero out_proj and every adaLN up-projection
+(src/model/dit/model.rs:28-43, src/model/norm.rs:107-119), which would make v == 0; the
+benchmark configurations instead draw EVERY Linear weight and bias from N(0, std) and
+set norm weights to 1 (optionally 1 + N(0, norm_jitter) so tests see the norm weights).
+Arrays are float32 in Burn row layout [d_in, d_out] (src/weights/record_builders.rs:37-66).
+Draw order is fixed, so a (cfg, seed) pair always yields the same arrays.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+
+from .config import DitConfig
+
+
+class _Draw:
+    def __init__(self, seed: int, std: float, norm_jitter: float):
+        self.rng = np.random.default_rng(seed)
+        self.std = np.float32(std)
+        self.jit = np.float32(norm_jitter)
+
+    def lin(self, *shape):
+        return (self.rng.standard_normal(shape, dtype=np.float32) * self.std).astype(np.float32)
+
+    def norm(self, *shape):
+        w = np.ones(shape, np.float32)
+        if self.jit:
+            w += self.rng.standard_normal(shape, dtype=np.float32) * self.jit
+        return w
+
+
+@dataclass
+class DitWeights:
+    io: dict
+    blocks: list
+
+    @staticmethod
+    def random(cfg: DitConfig, seed: int = 0, std: float = 0.02,
+               norm_jitter: float = 0.0) -> "DitWeights":
+        d = _Draw(seed, std, norm_jitter)
+        D, P, F, r, H, Dh = (cfg.model_dim, cfg.latent_dim, cfg.mlp_hidden, cfg.adaln_rank,
+                             cfg.num_heads, cfg.head_dim)
+        HD = H * Dh
+        io = {
+            "cond_w0": d.lin(cfg.timestep_embed_dim, D),
+            "cond_w1": d.lin(D, D),
+            "cond_w2": d.lin(D, 3 * D),
+            "in_w": d.lin(P, D),
+            "in_b": d.lin(D),
+            "out_norm_w": d.norm(D),
+            "out_w": d.lin(D, P),
+            "out_b": d.lin(P),
+        }
+        blocks = []
+        for _ in range(cfg.num_layers):
+            b = {
+                "w_qkv": d.lin(D, 3 * HD),
+                "w_gate": d.lin(D, D),
+                "w_o": d.lin(HD, D),
+                "q_norm": d.norm(H, Dh),
+                "k_norm": d.norm(H, Dh),
+                "w13": d.lin(D, 2 * F),
+                "w2": d.lin(F, D),
+                "ada_down": [[d.lin(D, r) for _ in range(3)] for _ in range(2)],
+                "ada_up": [[d.lin(r, D) for _ in range(3)] for _ in range(2)],
+                "ada_up_b": [[d.lin(D) for _ in range(3)] for _ in range(2)],
+            }
+            blocks.append(b)
+        return DitWeights(io, blocks)
+
+    def nbytes(self) -> int:
+        n = sum(a.nbytes for a in self.io.values())
+        for b in self.blocks:
+            for k, v in b.items():
+                if isinstance(v, list):
+                    n += sum(x.nbytes for row in v for x in row)
+                else:
+                    n += v.nbytes
+        return n
+
+
+@dataclass
+class ContextKV:
+    """Per-layer cached context K/V for every batch row (CondKvCache, attention.rs:24-45):
+    k, v [L, B, T, H, Dh] (k already k-normed, not rotated), mask [B, T] (1 = attend)."""
+
+    k: np.ndarray
+    v: np.ndarray
+    mask: np.ndarray
+
+    @property
+    def t_ctx(self) -> int:
+        return self.k.shape[2]
+
+    def rows(self, idx) -> "ContextKV":
+        return ContextKV(np.ascontiguousarray(self.k[:, idx]), np.ascontiguousarray(self.v[:, idx]),
+                         np.ascontiguousarray(self.mask[idx]))
+
+
+def make_context_kv(cfg: DitConfig, utterances: int, t_text: int, t_spk: int, seed: int = 1,
+                    text_valid=None, joint_cfg: bool = True, kv_std: float = 1.0) -> ContextKV:
+    """Synthetic cached context for `utterances` utterances.
+
+    Conditioned rows: K/V ~ N(0, kv_std); text keys valid up to a per-utterance length
+    (default uniform in [min(32, t_text), t_text]), speaker keys all valid.
+    With joint_cfg, each utterance u occupies rows (2u, 2u+1) and row 2u+1 is the
+    unconditioned row of EncodedCondition::zeros_like (condition.rs:144-154): zero states
+    project to zero K/V and every context key is masked out.
+    """
+    rng = np.random.default_rng(seed)
+    L, H, Dh = cfg.num_layers, cfg.num_heads, cfg.head_dim
+    T = t_text + t_spk
+    rows = 2 * utterances if joint_cfg else utterances
+    k = np.zeros((L, rows, T, H, Dh), np.float32)
+    v = np.zeros_like(k)
+    mask = np.zeros((rows, T), np.uint8)
+    for u in range(utterances):
+        r = 2 * u if joint_cfg else u
+        k[:, r] = rng.standard_normal((L, T, H, Dh), dtype=np.float32) * np.float32(kv_std)
+        v[:, r] = rng.standard_normal((L, T, H, Dh), dtype=np.float32) * np.float32(kv_std)
+        if text_valid is not None:
+            tv = int(text_valid[u])
+        else:
+            tv = int(rng.integers(min(32, t_text), t_text + 1)) if t_text > 0 else 0
+        mask[r, :tv] = 1
+        mask[r, t_text:] = 1
+    return ContextKV(k, v, mask)
+
+
+def make_noise(utterances: int, seq: int, latent_dim: int, seed: int = 2) -> np.ndarray:
+    """Initial RF noise x_0 ~ N(0, 1), [U, S, P] (euler_sampler.rs:146-152)."""
+    rng = np.random.default_rng(seed)
+    return rng.standard_normal((utterances, seq, latent_dim), dtype=np.float32)

@@ -1,0 +1,125 @@
+/*
+ * CPU oracle for the Irodori-TTS RF-step DiT forward — TEST INFRASTRUCTURE ONLY.
+ *
+ * This is a plain-C restatement of the reference's Burn NdArray f32 semantics for the
+ * hot path (one DiT forward and the Joint-CFG Euler sampler).  It is used only by
+ * tests/, __graft_entry__.smoke() and the cpu_baseline leg of bench.py, as the
+ * checker and as the timed CPU baseline.  The product (libirodori_hip.so) never
+ * links, loads or calls it.
+ *
+ * Every function is compiled twice from oracle_body.h: once with float arithmetic
+ * (orc_f32_*, the NdArray<f32> analogue) and once with double arithmetic
+ * (orc_f64_*, the reference of record).  Inputs and outputs are always float, and so are
+ * the buffers between operators: the f64 variant rounds to f32 only at operator
+ * boundaries (relative ~1e-7), far below every tolerance it is used for.
+ *
+ * Layouts follow the reference at the Burn boundary: every Linear weight is
+ * [d_in, d_out] row-major with y = x @ W + b (src/weights/record_builders.rs:37-66).
+ */
+#ifndef IRODORI_ORACLE_H
+#define IRODORI_ORACLE_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct orc_cfg {
+    int32_t latent_dim;   /* patched latent dim P */
+    int32_t model_dim;    /* D */
+    int32_t num_layers;   /* L */
+    int32_t num_heads;    /* H */
+    int32_t head_dim;     /* Dh */
+    int32_t mlp_hidden;   /* F */
+    int32_t adaln_rank;   /* r */
+    int32_t t_dim;        /* timestep embedding dim */
+    float norm_eps;
+    float rope_theta;
+} orc_cfg;
+
+/* One DiffusionBlock (src/model/diffusion.rs:21-28), fused inference layout
+ * (attention.rs:514-523, feed_forward.rs:96-103).  adaln index: [0]=attention_adaln,
+ * [1]=mlp_adaln; chunk index: [0]=shift, [1]=scale, [2]=gate (norm.rs:141-157). */
+typedef struct orc_block {
+    const float* w_qkv;   /* [D, 3*H*Dh] = [Wq | Wk | Wv] */
+    const float* w_gate;  /* [D, D] */
+    const float* w_o;     /* [H*Dh, D] */
+    const float* q_norm;  /* [H, Dh] */
+    const float* k_norm;  /* [H, Dh] */
+    const float* w13;     /* [D, 2F] = [W1 | W3] */
+    const float* w2;      /* [F, D] */
+    const float* ada_down[2][3]; /* [D, r], no bias */
+    const float* ada_up[2][3];   /* [r, D] */
+    const float* ada_up_b[2][3]; /* [D] */
+} orc_block;
+
+/* Non-block weights of TextToLatentRfDiT used per forward (dit/model.rs:140-170). */
+typedef struct orc_io {
+    const float* cond_w0;    /* [t_dim, D], no bias */
+    const float* cond_w1;    /* [D, D], no bias */
+    const float* cond_w2;    /* [D, 3D], no bias */
+    const float* in_w;       /* [P, D] */
+    const float* in_b;       /* [D] */
+    const float* out_norm_w; /* [D] */
+    const float* out_w;      /* [D, P] */
+    const float* out_b;      /* [P] */
+} orc_io;
+
+/* Number of OpenMP threads the oracle uses (0 = runtime default). */
+void orc_set_threads(int n);
+int orc_get_threads(void);
+
+#define ORC_DECLARE(P)                                                                      \
+    void P##timestep_embedding(const float* t, int B, int t_dim, float* out);              \
+    void P##rope_tables(int S, int Dh, float theta, float* cos_out, float* sin_out);       \
+    void P##linear(const float* x, const float* w, const float* b, int M, int K, int N,    \
+                   float* y);                                                               \
+    void P##rms_norm(const float* x, const float* w, int rows, int D, float eps, float* y);\
+    void P##fused_adaln(const float* x, const float* scale, const float* shift, int B,     \
+                        int S, int D, float eps, float* y);                                 \
+    void P##head_rms_norm(const float* x, const float* w, int N, int H, int Dh, float eps, \
+                          float* y);                                                        \
+    void P##rope_half(const float* x, const float* cos_t, const float* sin_t, int B,       \
+                      int S, int H, int Dh, float* y);                                      \
+    void P##rope_full(const float* x, const float* cos_t, const float* sin_t, int B,       \
+                      int S, int H, int Dh, float* y);                                      \
+    void P##sdpa(const float* q, const float* k, const float* v, const float* mask, int B, \
+                 int H, int Sq, int Skv, int Dh, float scale, float* out);                  \
+    void P##cond_module(const orc_cfg* c, const orc_io* io, const float* t, int B,         \
+                        float* cond_out);                                                   \
+    void P##adaln_vectors(const orc_cfg* c, const orc_block* blk, int which,               \
+                          const float* cond, int B, float* shift, float* scale,            \
+                          float* gate);                                                     \
+    void P##swiglu(const float* h, const float* w13, const float* w2, int M, int D, int F, \
+                   float* out);                                                             \
+    void P##joint_attention(const orc_cfg* c, const orc_block* blk, const float* h, int B, \
+                            int S, int T, const float* ctx_k, const float* ctx_v,          \
+                            const uint8_t* ctx_mask, const float* cos_t,                   \
+                            const float* sin_t, float* out);                                \
+    void P##block_forward(const orc_cfg* c, const orc_block* blk, float* x,                \
+                          const float* cond, int B, int S, int T, const float* ctx_k,      \
+                          const float* ctx_v, const uint8_t* ctx_mask, const float* cos_t, \
+                          const float* sin_t);                                              \
+    void P##forward(const orc_cfg* c, const orc_io* io, const orc_block* blocks, int B,    \
+                    int S, const float* x_t, const float* t, int T, const float* ctx_k,    \
+                    const float* ctx_v, const uint8_t* ctx_mask, float* v_out,             \
+                    float* debug);                                                          \
+    void P##build_kv_cache(const orc_cfg* c, const float* k_norm, int B, const float* text,\
+                           const uint8_t* text_mask, int Tt, int Dt, const float* wk_text,  \
+                           const float* wv_text, const float* aux, const uint8_t* aux_mask,\
+                           int Ta, int Da, const float* wk_aux, const float* wv_aux,       \
+                           float* ctx_k, float* ctx_v, uint8_t* ctx_mask);                  \
+    int P##sample_joint_cfg(const orc_cfg* c, const orc_io* io, const orc_block* blocks,   \
+                            int U, int S, const float* x0, int T, const float* ctx_k_cond, \
+                            const float* ctx_v_cond, const uint8_t* mask_cond,             \
+                            const float* ctx_k_unc, const float* ctx_v_unc,                \
+                            const uint8_t* mask_unc, int num_steps, float scale,           \
+                            float min_t, float max_t, int max_steps_run, float* x_out);
+
+ORC_DECLARE(orc_f32_)
+ORC_DECLARE(orc_f64_)
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,288 @@
+"""ctypes wrapper for the CPU oracle — TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this
+module, as the checker and as the timed CPU baseline.  The product path
+(libirodori_hip.so and the irodori_hip package) never imports it.
+
+`Oracle("f32")` mirrors the reference's Burn NdArray<f32> arithmetic;
+`Oracle("f64")` is the same restatement in double precision.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "_build", "liboracle.so")
+
+_f32p = C.POINTER(C.c_float)
+_u8p = C.POINTER(C.c_uint8)
+
+
+class OrcCfg(C.Structure):
+    _fields_ = [
+        ("latent_dim", C.c_int32), ("model_dim", C.c_int32), ("num_layers", C.c_int32),
+        ("num_heads", C.c_int32), ("head_dim", C.c_int32), ("mlp_hidden", C.c_int32),
+        ("adaln_rank", C.c_int32), ("t_dim", C.c_int32), ("norm_eps", C.c_float),
+        ("rope_theta", C.c_float),
+    ]
+
+
+class OrcBlock(C.Structure):
+    _fields_ = [
+        ("w_qkv", _f32p), ("w_gate", _f32p), ("w_o", _f32p), ("q_norm", _f32p),
+        ("k_norm", _f32p), ("w13", _f32p), ("w2", _f32p),
+        ("ada_down", (_f32p * 3) * 2), ("ada_up", (_f32p * 3) * 2), ("ada_up_b", (_f32p * 3) * 2),
+    ]
+
+
+class OrcIo(C.Structure):
+    _fields_ = [
+        ("cond_w0", _f32p), ("cond_w1", _f32p), ("cond_w2", _f32p), ("in_w", _f32p),
+        ("in_b", _f32p), ("out_norm_w", _f32p), ("out_w", _f32p), ("out_b", _f32p),
+    ]
+
+
+def build() -> None:
+    """Compile liboracle.so with the Makefile beside this file."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+_lib = None
+
+
+def _load():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        _lib = C.CDLL(_LIB_PATH)
+    return _lib
+
+
+def _f(a: np.ndarray):
+    assert a.dtype == np.float32 and a.flags.c_contiguous, (a.dtype, a.flags)
+    return a.ctypes.data_as(_f32p)
+
+
+def _u8(a: np.ndarray):
+    assert a.dtype == np.uint8 and a.flags.c_contiguous
+    return a.ctypes.data_as(_u8p)
+
+
+def _c32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def set_threads(n: int) -> None:
+    _load().orc_set_threads(int(n))
+
+
+def get_threads() -> int:
+    return int(_load().orc_get_threads())
+
+
+class Oracle:
+    """Oracle entry points; arrays are numpy float32 (masks uint8), shapes as in oracle.h."""
+
+    def __init__(self, precision: str = "f32"):
+        assert precision in ("f32", "f64")
+        self.lib = _load()
+        self.p = "orc_%s_" % precision
+
+    def _fn(self, name):
+        return getattr(self.lib, self.p + name)
+
+    # ---- structs -------------------------------------------------------------------
+    @staticmethod
+    def cfg_struct(cfg) -> OrcCfg:
+        return OrcCfg(cfg.latent_dim, cfg.model_dim, cfg.num_layers, cfg.num_heads,
+                      cfg.head_dim, cfg.mlp_hidden, cfg.adaln_rank, cfg.timestep_embed_dim,
+                      cfg.norm_eps, cfg.rope_theta)
+
+    @staticmethod
+    def block_struct(b) -> OrcBlock:
+        s = OrcBlock()
+        for k in ("w_qkv", "w_gate", "w_o", "q_norm", "k_norm", "w13", "w2"):
+            setattr(s, k, _f(b[k]))
+        for w in range(2):
+            for ch in range(3):
+                s.ada_down[w][ch] = _f(b["ada_down"][w][ch])
+                s.ada_up[w][ch] = _f(b["ada_up"][w][ch])
+                s.ada_up_b[w][ch] = _f(b["ada_up_b"][w][ch])
+        return s
+
+    @staticmethod
+    def io_struct(io) -> OrcIo:
+        return OrcIo(*[_f(io[k]) for k in ("cond_w0", "cond_w1", "cond_w2", "in_w", "in_b",
+                                            "out_norm_w", "out_w", "out_b")])
+
+    # ---- operators -----------------------------------------------------------------
+    def timestep_embedding(self, t, t_dim):
+        t = _c32(t)
+        out = np.empty((t.shape[0], t_dim), np.float32)
+        self._fn("timestep_embedding")(_f(t), t.shape[0], t_dim, _f(out))
+        return out
+
+    def rope_tables(self, S, Dh, theta=10000.0):
+        cs = np.empty((S, Dh // 2), np.float32)
+        sn = np.empty((S, Dh // 2), np.float32)
+        self._fn("rope_tables")(S, Dh, C.c_float(theta), _f(cs), _f(sn))
+        return cs, sn
+
+    def linear(self, x, w, b=None):
+        x, w = _c32(x), _c32(w)
+        M, K = x.shape
+        N = w.shape[1]
+        y = np.empty((M, N), np.float32)
+        bb = _c32(b) if b is not None else None
+        self._fn("linear")(_f(x), _f(w), _f(bb) if bb is not None else None, M, K, N, _f(y))
+        return y
+
+    def rms_norm(self, x, w, eps):
+        x, w = _c32(x), _c32(w)
+        y = np.empty_like(x)
+        rows, D = x.reshape(-1, x.shape[-1]).shape
+        self._fn("rms_norm")(_f(x), _f(w), rows, D, C.c_float(eps), _f(y))
+        return y
+
+    def fused_adaln(self, x, scale, shift, B, S, eps):
+        x, scale, shift = _c32(x), _c32(scale), _c32(shift)
+        D = x.shape[-1]
+        y = np.empty_like(x)
+        self._fn("fused_adaln")(_f(x), _f(scale), _f(shift), B, S, D, C.c_float(eps), _f(y))
+        return y
+
+    def head_rms_norm(self, x, w, eps):
+        x, w = _c32(x), _c32(w)
+        H, Dh = w.shape
+        N = x.size // (H * Dh)
+        y = np.empty_like(x)
+        self._fn("head_rms_norm")(_f(x), _f(w), N, H, Dh, C.c_float(eps), _f(y))
+        return y
+
+    def rope_half(self, x, cs, sn):
+        x = _c32(x)
+        B, S, H, Dh = x.shape
+        y = np.empty_like(x)
+        self._fn("rope_half")(_f(x), _f(_c32(cs)), _f(_c32(sn)), B, S, H, Dh, _f(y))
+        return y
+
+    def rope_full(self, x, cs, sn):
+        x = _c32(x)
+        B, S, H, Dh = x.shape
+        y = np.empty_like(x)
+        self._fn("rope_full")(_f(x), _f(_c32(cs)), _f(_c32(sn)), B, S, H, Dh, _f(y))
+        return y
+
+    def sdpa(self, q, k, v, mask, scale):
+        q, k, v = _c32(q), _c32(k), _c32(v)
+        B, H, Sq, Dh = q.shape
+        Skv = k.shape[2]
+        m = _c32(mask) if mask is not None else None
+        out = np.empty_like(q)
+        self._fn("sdpa")(_f(q), _f(k), _f(v), _f(m) if m is not None else None, B, H, Sq, Skv,
+                         Dh, C.c_float(scale), _f(out))
+        return out
+
+    def cond_module(self, cfg, io, t):
+        t = _c32(t)
+        out = np.empty((t.shape[0], 3 * cfg.model_dim), np.float32)
+        self._fn("cond_module")(C.byref(self.cfg_struct(cfg)), C.byref(self.io_struct(io)),
+                                _f(t), t.shape[0], _f(out))
+        return out
+
+    def adaln_vectors(self, cfg, blk, which, cond):
+        cond = _c32(cond)
+        B, D = cond.shape[0], cfg.model_dim
+        sh, sc, g = (np.empty((B, D), np.float32) for _ in range(3))
+        self._fn("adaln_vectors")(C.byref(self.cfg_struct(cfg)), C.byref(self.block_struct(blk)),
+                                  which, _f(cond), B, _f(sh), _f(sc), _f(g))
+        return sh, sc, g
+
+    def swiglu(self, h, w13, w2):
+        h = _c32(h)
+        M, D = h.shape
+        F = w2.shape[0]
+        out = np.empty((M, D), np.float32)
+        self._fn("swiglu")(_f(h), _f(_c32(w13)), _f(_c32(w2)), M, D, F, _f(out))
+        return out
+
+    def joint_attention(self, cfg, blk, h, ctx_k, ctx_v, ctx_mask, cs, sn):
+        h = _c32(h)
+        B, S, _ = h.shape
+        T = ctx_k.shape[1]
+        out = np.empty_like(h)
+        self._fn("joint_attention")(C.byref(self.cfg_struct(cfg)), C.byref(self.block_struct(blk)),
+                                    _f(h), B, S, T, _f(_c32(ctx_k)), _f(_c32(ctx_v)),
+                                    _u8(np.ascontiguousarray(ctx_mask, np.uint8)),
+                                    _f(_c32(cs)), _f(_c32(sn)), _f(out))
+        return out
+
+    def build_kv_cache(self, cfg, k_norm, text, text_mask, wk_text, wv_text,
+                       aux=None, aux_mask=None, wk_aux=None, wv_aux=None):
+        text = _c32(text)
+        B, Tt, Dt = text.shape
+        Ta, Da = (aux.shape[1], aux.shape[2]) if aux is not None else (0, 0)
+        T = Tt + Ta
+        HD = cfg.num_heads * cfg.head_dim
+        ck = np.empty((B, T, cfg.num_heads, cfg.head_dim), np.float32)
+        cv = np.empty_like(ck)
+        cm = np.empty((B, T), np.uint8)
+        auxp = _f(_c32(aux)) if aux is not None else None
+        amp = _u8(np.ascontiguousarray(aux_mask, np.uint8)) if aux_mask is not None else None
+        self._fn("build_kv_cache")(
+            C.byref(self.cfg_struct(cfg)), _f(_c32(k_norm)), B, _f(text),
+            _u8(np.ascontiguousarray(text_mask, np.uint8)), Tt, Dt, _f(_c32(wk_text)),
+            _f(_c32(wv_text)), auxp, amp, Ta, Da,
+            _f(_c32(wk_aux)) if wk_aux is not None else None,
+            _f(_c32(wv_aux)) if wv_aux is not None else None, _f(ck), _f(cv), _u8(cm))
+        assert HD == cfg.num_heads * cfg.head_dim
+        return ck, cv, cm
+
+    def block_forward(self, cfg, blk, x, cond, ctx_k, ctx_v, ctx_mask):
+        """One DiffusionBlock on x [B,S,D] with cond [B,3D]; ctx_* of this layer [B,T,H,Dh]."""
+        x = _c32(x).copy()
+        B, S, _ = x.shape
+        T = ctx_k.shape[1]
+        cs, sn = self.rope_tables(S, cfg.head_dim, cfg.rope_theta)
+        self._fn("block_forward")(C.byref(self.cfg_struct(cfg)), C.byref(self.block_struct(blk)),
+                                  _f(x), _f(_c32(cond)), B, S, T, _f(_c32(ctx_k)), _f(_c32(ctx_v)),
+                                  _u8(np.ascontiguousarray(ctx_mask, np.uint8)), _f(cs), _f(sn))
+        return x
+
+    # ---- model ---------------------------------------------------------------------
+    def forward(self, cfg, weights, x_t, t, ctx_k, ctx_v, ctx_mask, debug=False):
+        """x_t [B,S,P]; t [B]; ctx_k/ctx_v [L,B,T,H,Dh]; ctx_mask [B,T] -> v [B,S,P]
+        (and [L+1,B,S,D] block outputs when debug)."""
+        x_t = _c32(x_t)
+        B, S, Pd = x_t.shape
+        T = ctx_k.shape[2]
+        blocks = (OrcBlock * cfg.num_layers)(*[self.block_struct(b) for b in weights.blocks])
+        v = np.empty_like(x_t)
+        dbg = np.empty((cfg.num_layers + 1, B, S, cfg.model_dim), np.float32) if debug else None
+        self._fn("forward")(C.byref(self.cfg_struct(cfg)), C.byref(self.io_struct(weights.io)),
+                            blocks, B, S, _f(x_t), _f(_c32(t)), T, _f(_c32(ctx_k)),
+                            _f(_c32(ctx_v)), _u8(np.ascontiguousarray(ctx_mask, np.uint8)),
+                            _f(v), _f(dbg) if debug else None)
+        return (v, dbg) if debug else v
+
+    def sample_joint_cfg(self, cfg, weights, x0, ctx_cond, ctx_unc, num_steps, scale,
+                         min_t=0.0, max_t=1.0, max_steps_run=0):
+        """x0 [U,S,P]; ctx_* = (k [L,U,T,H,Dh], v, mask [U,T]).  Returns (x_out, steps_run)."""
+        x0 = _c32(x0)
+        U, S, Pd = x0.shape
+        kc, vc, mc = ctx_cond
+        ku, vu, mu = ctx_unc
+        T = kc.shape[2]
+        blocks = (OrcBlock * cfg.num_layers)(*[self.block_struct(b) for b in weights.blocks])
+        out = np.empty_like(x0)
+        run = self._fn("sample_joint_cfg")(
+            C.byref(self.cfg_struct(cfg)), C.byref(self.io_struct(weights.io)), blocks, U, S,
+            _f(x0), T, _f(_c32(kc)), _f(_c32(vc)), _u8(np.ascontiguousarray(mc, np.uint8)),
+            _f(_c32(ku)), _f(_c32(vu)), _u8(np.ascontiguousarray(mu, np.uint8)), num_steps,
+            C.c_float(scale), C.c_float(min_t), C.c_float(max_t), max_steps_run, _f(out))
+        return out, int(run)

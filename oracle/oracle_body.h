@@ -1,0 +1,451 @@
+/*
+ * Body of the CPU oracle — TEST INFRASTRUCTURE ONLY (see oracle.h).
+ * Included twice by oracle.c with R = float / double and P(name) = orc_f32_name /
+ * orc_f64_name.  Each function cites the reference lines whose semantics it restates.
+ */
+
+/* rope.rs:141-165 — emb = [cos(t*f_i) | sin(t*f_i)], f_i = 1000*exp(-ln(1e4)*i/half).
+ * The reference computes the frequencies in f32; the f64 variant computes them in f64. */
+void P(timestep_embedding)(const float* t, int B, int t_dim, float* out) {
+    int half = t_dim / 2;
+    R log_10000 = LOG(R_C(10000.0));
+    for (int b = 0; b < B; b++) {
+        for (int i = 0; i < half; i++) {
+            R f = R_C(1000.0) * EXP((-log_10000 * (R)i) / (R)half);
+            R a = (R)t[b] * f;
+            out[b * t_dim + i] = (float)COS(a);
+            out[b * t_dim + half + i] = (float)SIN(a);
+        }
+    }
+}
+
+/* rope.rs:24-63 — cos/sin tables [S, Dh/2], freq_i = 1/theta^(2i/Dh), angle = pos*freq_i. */
+void P(rope_tables)(int S, int Dh, float theta, float* cos_out, float* sin_out) {
+    int half = Dh / 2;
+    for (int s = 0; s < S; s++) {
+        for (int i = 0; i < half; i++) {
+            R freq = R_C(1.0) / POW((R)theta, R_C(2.0) * (R)i / (R)Dh);
+            R a = (R)s * freq;
+            cos_out[s * half + i] = (float)COS(a);
+            sin_out[s * half + i] = (float)SIN(a);
+        }
+    }
+}
+
+/* Burn Linear::forward in row layout: y[M,N] = x[M,K] @ w[K,N] (+ b[N]).
+ * Blocked over rows and columns so each weight row streamed from cache serves
+ * ORC_IB output rows. */
+#define ORC_IB 16
+#define ORC_JB 128
+void P(linear)(const float* x, const float* w, const float* b, int M, int K, int N, float* y) {
+    int nib = (M + ORC_IB - 1) / ORC_IB, njb = (N + ORC_JB - 1) / ORC_JB;
+    #pragma omp parallel for schedule(dynamic, 1)
+    for (int blk = 0; blk < nib * njb; blk++) {
+        int i0 = (blk / njb) * ORC_IB, j0 = (blk % njb) * ORC_JB;
+        int ni = M - i0 < ORC_IB ? M - i0 : ORC_IB;
+        int nj = N - j0 < ORC_JB ? N - j0 : ORC_JB;
+        R acc[ORC_IB][ORC_JB];
+        for (int r = 0; r < ni; r++)
+            for (int j = 0; j < nj; j++) acc[r][j] = b ? (R)b[j0 + j] : R_C(0.0);
+        for (int k = 0; k < K; k++) {
+            const float* wr = w + (size_t)k * N + j0;
+            for (int r = 0; r < ni; r++) {
+                R a = (R)x[(size_t)(i0 + r) * K + k];
+                R* ar = acc[r];
+                for (int j = 0; j < nj; j++) ar[j] += a * (R)wr[j];
+            }
+        }
+        for (int r = 0; r < ni; r++)
+            for (int j = 0; j < nj; j++) y[(size_t)(i0 + r) * N + j0 + j] = (float)acc[r][j];
+    }
+}
+
+/* norm.rs:25-39 (RmsNorm::forward) and rms_norm.rs:161-175 (reference_rms_norm):
+ * y = x / sqrt(mean(x^2) + eps) * w. */
+void P(rms_norm)(const float* x, const float* w, int rows, int D, float eps, float* y) {
+    #pragma omp parallel for schedule(static)
+    for (int i = 0; i < rows; i++) {
+        const float* xr = x + (size_t)i * D;
+        R ss = 0;
+        for (int d = 0; d < D; d++) ss += (R)xr[d] * (R)xr[d];
+        R rms = SQRT(ss / (R)D + (R)eps);
+        for (int d = 0; d < D; d++) y[(size_t)i * D + d] = (float)((R)xr[d] / rms * (R)w[d]);
+    }
+}
+
+/* norm.rs:160-169 and fused_adaln.rs:223-251 (reference_fused_adaln):
+ * y = x / sqrt(mean(x^2)+eps) * (1 + scale[b]) + shift[b]; no learnable norm weight. */
+void P(fused_adaln)(const float* x, const float* scale, const float* shift, int B, int S, int D,
+                    float eps, float* y) {
+    #pragma omp parallel for schedule(static)
+    for (int i = 0; i < B * S; i++) {
+        int b = i / S;
+        const float* xr = x + (size_t)i * D;
+        R ss = 0;
+        for (int d = 0; d < D; d++) ss += (R)xr[d] * (R)xr[d];
+        R rms = SQRT(ss / (R)D + (R)eps);
+        for (int d = 0; d < D; d++)
+            y[(size_t)i * D + d] =
+                (float)((R)xr[d] / rms * (R_C(1.0) + (R)scale[b * D + d]) + (R)shift[b * D + d]);
+    }
+}
+
+/* norm.rs:60-74 (HeadRmsNorm::forward): per (token, head) over Dh, times w[h, :]. */
+void P(head_rms_norm)(const float* x, const float* w, int N, int H, int Dh, float eps, float* y) {
+    #pragma omp parallel for schedule(static)
+    for (int i = 0; i < N * H; i++) {
+        int h = i % H;
+        const float* xr = x + (size_t)i * Dh;
+        R ss = 0;
+        for (int d = 0; d < Dh; d++) ss += (R)xr[d] * (R)xr[d];
+        R rms = SQRT(ss / (R)Dh + (R)eps);
+        for (int d = 0; d < Dh; d++)
+            y[(size_t)i * Dh + d] = (float)((R)xr[d] / rms * (R)w[h * Dh + d]);
+    }
+}
+
+/* rope.rs:82-113 (apply_rotary_emb) restricted to heads [h_lo, h_hi): interleaved pairs
+ * (x[2k], x[2k+1]) rotated as a complex product by (cos[s,k], sin[s,k]). */
+static void P(rope_heads)(const float* x, const float* cos_t, const float* sin_t, int B, int S,
+                          int H, int Dh, int h_hi, float* y) {
+    int half = Dh / 2;
+    #pragma omp parallel for schedule(static)
+    for (int i = 0; i < B * S; i++) {
+        int s = i % S;
+        for (int h = 0; h < H; h++) {
+            const float* xr = x + ((size_t)i * H + h) * Dh;
+            float* yr = y + ((size_t)i * H + h) * Dh;
+            if (h >= h_hi) {
+                for (int d = 0; d < Dh; d++) yr[d] = xr[d];
+                continue;
+            }
+            for (int k = 0; k < half; k++) {
+                R c = (R)cos_t[s * half + k], sn = (R)sin_t[s * half + k];
+                R re = (R)xr[2 * k], im = (R)xr[2 * k + 1];
+                yr[2 * k] = (float)(re * c - im * sn);
+                yr[2 * k + 1] = (float)(re * sn + im * c);
+            }
+        }
+    }
+}
+
+/* rope.rs:119-135 (apply_rotary_half): RoPE on heads [0, H/2), heads [H/2, H) pass through. */
+void P(rope_half)(const float* x, const float* cos_t, const float* sin_t, int B, int S, int H,
+                  int Dh, float* y) {
+    P(rope_heads)(x, cos_t, sin_t, B, S, H, Dh, H / 2, y);
+}
+
+/* rope.rs:82-113 on all heads (SelfAttention's full RoPE; used to pin the half variant). */
+void P(rope_full)(const float* x, const float* cos_t, const float* sin_t, int B, int S, int H,
+                  int Dh, float* y) {
+    P(rope_heads)(x, cos_t, sin_t, B, S, H, Dh, H, y);
+}
+
+/* softmax(q k^T * scale + mask) v over [B, H, S, Dh] tensors; mask [B, Skv] with
+ * value < 0.5 meaning masked-out, and a fully masked row yields exactly 0.
+ * Follows reference_sdpa (fused_sdpa_native.rs:329-388) and the all-masked => 0 contract
+ * of manual_sdpa (attention.rs:686-716, test attention.rs:770-787). */
+void P(sdpa)(const float* q, const float* k, const float* v, const float* mask, int B, int H,
+             int Sq, int Skv, int Dh, float scale, float* out) {
+    #pragma omp parallel
+    {
+        R* sc = (R*)malloc(sizeof(R) * (size_t)(Skv > 0 ? Skv : 1));
+        R* acc = (R*)malloc(sizeof(R) * (size_t)Dh);
+        #pragma omp for schedule(static)
+        for (int i = 0; i < B * H * Sq; i++) {
+            int b = i / (H * Sq), bh = i / Sq;
+            const float* qr = q + (size_t)i * Dh;
+            R mx = -INFINITY;
+            for (int j = 0; j < Skv; j++) {
+                if (mask && mask[(size_t)b * Skv + j] < 0.5f) { sc[j] = -INFINITY; continue; }
+                const float* kr = k + ((size_t)bh * Skv + j) * Dh;
+                R dot = 0;
+                for (int d = 0; d < Dh; d++) dot += (R)qr[d] * (R)kr[d];
+                sc[j] = dot * (R)scale;
+                if (sc[j] > mx) mx = sc[j];
+            }
+            R sum = 0;
+            for (int d = 0; d < Dh; d++) acc[d] = 0;
+            if (mx != -INFINITY) {
+                for (int j = 0; j < Skv; j++) {
+                    if (sc[j] == -INFINITY) continue;
+                    R e = EXP(sc[j] - mx);
+                    sum += e;
+                    const float* vr = v + ((size_t)bh * Skv + j) * Dh;
+                    for (int d = 0; d < Dh; d++) acc[d] += e * (R)vr[d];
+                }
+            }
+            float* o = out + (size_t)i * Dh;
+            for (int d = 0; d < Dh; d++) o[d] = sum > 0 ? (float)(acc[d] / sum) : 0.0f;
+        }
+        free(sc);
+        free(acc);
+    }
+}
+
+static R P(silu)(R v) { return v / (R_C(1.0) + EXP(-v)); }
+static R P(sigmoid)(R v) { return R_C(1.0) / (R_C(1.0) + EXP(-v)); }
+
+/* dit/model.rs:80-85 (CondModule::forward) after get_timestep_embedding (rope.rs:141-165):
+ * c = L2(silu(L1(silu(L0(emb))))), no biases.  cond_out: [B, 3D]. */
+void P(cond_module)(const orc_cfg* c, const orc_io* io, const float* t, int B, float* cond_out) {
+    int D = c->model_dim, td = c->t_dim;
+    float* emb = (float*)malloc(sizeof(float) * (size_t)B * td);
+    float* h0 = (float*)malloc(sizeof(float) * (size_t)B * D);
+    float* h1 = (float*)malloc(sizeof(float) * (size_t)B * D);
+    P(timestep_embedding)(t, B, td, emb);
+    P(linear)(emb, io->cond_w0, NULL, B, td, D, h0);
+    for (int i = 0; i < B * D; i++) h0[i] = (float)P(silu)((R)h0[i]);
+    P(linear)(h0, io->cond_w1, NULL, B, D, D, h1);
+    for (int i = 0; i < B * D; i++) h1[i] = (float)P(silu)((R)h1[i]);
+    P(linear)(h1, io->cond_w2, NULL, B, D, 3 * D, cond_out);
+    free(emb); free(h0); free(h1);
+}
+
+/* norm.rs:141-157 + :170 (LowRankAdaLn::forward, the modulation vectors):
+ * (shift, scale, gate) = chunk(cond, 3); each += up(down(silu(.))) + b_up; gate -> tanh.
+ * which: 0 = attention_adaln, 1 = mlp_adaln.  Outputs [B, D] each. */
+void P(adaln_vectors)(const orc_cfg* c, const orc_block* blk, int which, const float* cond, int B,
+                      float* shift, float* scale, float* gate) {
+    int D = c->model_dim, r = c->adaln_rank;
+    float* in = (float*)malloc(sizeof(float) * (size_t)B * D);
+    float* mid = (float*)malloc(sizeof(float) * (size_t)B * r);
+    float* up = (float*)malloc(sizeof(float) * (size_t)B * D);
+    float* outs[3] = {shift, scale, gate};
+    for (int ch = 0; ch < 3; ch++) {
+        for (int b = 0; b < B; b++)
+            for (int d = 0; d < D; d++)
+                in[b * D + d] = (float)P(silu)((R)cond[(size_t)b * 3 * D + ch * D + d]);
+        P(linear)(in, blk->ada_down[which][ch], NULL, B, D, r, mid);
+        P(linear)(mid, blk->ada_up[which][ch], blk->ada_up_b[which][ch], B, r, D, up);
+        for (int b = 0; b < B; b++)
+            for (int d = 0; d < D; d++) {
+                R v = (R)up[b * D + d] + (R)cond[(size_t)b * 3 * D + ch * D + d];
+                outs[ch][b * D + d] = (float)(ch == 2 ? TANH(v) : v);
+            }
+    }
+    free(in); free(mid); free(up);
+}
+
+/* feed_forward.rs:76-85 (SwiGlu::forward_fused): u = h @ [W1|W3];
+ * out = (silu(u[:, :F]) * u[:, F:]) @ W2. */
+void P(swiglu)(const float* h, const float* w13, const float* w2, int M, int D, int F,
+               float* out) {
+    float* u = (float*)malloc(sizeof(float) * (size_t)M * 2 * F);
+    float* m = (float*)malloc(sizeof(float) * (size_t)M * F);
+    P(linear)(h, w13, NULL, M, D, 2 * F, u);
+    #pragma omp parallel for schedule(static)
+    for (int i = 0; i < M; i++)
+        for (int j = 0; j < F; j++)
+            m[(size_t)i * F + j] =
+                (float)(P(silu)((R)u[(size_t)i * 2 * F + j]) * (R)u[(size_t)i * 2 * F + F + j]);
+    P(linear)(m, w2, NULL, M, F, D, out);
+    free(u); free(m);
+}
+
+/* attention.rs:272-425 (JointAttention::forward_fused with a KV cache):
+ *   [q|k|v] = h @ W_qkv; q = rope_half(q_norm(q)); k = rope_half(k_norm(k));
+ *   K = [k | ctx_k], V = [v | ctx_v], mask = [1]*S ++ ctx_mask;
+ *   o = SDPA(q, K, V, mask, Dh^-0.5); out = (sigmoid(h @ W_gate) * o) @ W_o.
+ * ctx_k/ctx_v: [B, T, H, Dh] (already k-normed, not rotated); ctx_mask: [B, T] (1 = attend). */
+void P(joint_attention)(const orc_cfg* c, const orc_block* blk, const float* h, int B, int S,
+                        int T, const float* ctx_k, const float* ctx_v, const uint8_t* ctx_mask,
+                        const float* cos_t, const float* sin_t, float* out) {
+    int D = c->model_dim, H = c->num_heads, Dh = c->head_dim, HD = H * Dh;
+    int M = B * S, Skv = S + T;
+    size_t szq = (size_t)M * HD;
+    float* qkv = (float*)malloc(sizeof(float) * (size_t)M * 3 * HD);
+    float* q = (float*)malloc(sizeof(float) * szq);
+    float* kk = (float*)malloc(sizeof(float) * szq);
+    float* vv = (float*)malloc(sizeof(float) * szq);
+    float* tmp = (float*)malloc(sizeof(float) * szq);
+    P(linear)(h, blk->w_qkv, NULL, M, D, 3 * HD, qkv);
+    for (int i = 0; i < M; i++)
+        for (int j = 0; j < HD; j++) {
+            q[(size_t)i * HD + j] = qkv[(size_t)i * 3 * HD + j];
+            kk[(size_t)i * HD + j] = qkv[(size_t)i * 3 * HD + HD + j];
+            vv[(size_t)i * HD + j] = qkv[(size_t)i * 3 * HD + 2 * HD + j];
+        }
+    P(head_rms_norm)(q, blk->q_norm, M, H, Dh, c->norm_eps, tmp);
+    P(rope_half)(tmp, cos_t, sin_t, B, S, H, Dh, q);
+    P(head_rms_norm)(kk, blk->k_norm, M, H, Dh, c->norm_eps, tmp);
+    P(rope_half)(tmp, cos_t, sin_t, B, S, H, Dh, kk);
+
+    /* Rearrange to [B, H, S(kv), Dh] (attention.rs:629-633 swap_dims). */
+    float* qh = (float*)malloc(sizeof(float) * szq);
+    float* kh = (float*)malloc(sizeof(float) * (size_t)B * H * Skv * Dh);
+    float* vh = (float*)malloc(sizeof(float) * (size_t)B * H * Skv * Dh);
+    float* mk = (float*)malloc(sizeof(float) * (size_t)B * Skv);
+    float* oh = (float*)malloc(sizeof(float) * szq);
+    for (int b = 0; b < B; b++)
+        for (int hh = 0; hh < H; hh++) {
+            for (int s = 0; s < S; s++)
+                for (int d = 0; d < Dh; d++) {
+                    size_t src = (((size_t)b * S + s) * H + hh) * Dh + d;
+                    qh[(((size_t)b * H + hh) * S + s) * Dh + d] = q[src];
+                    kh[(((size_t)b * H + hh) * Skv + s) * Dh + d] = kk[src];
+                    vh[(((size_t)b * H + hh) * Skv + s) * Dh + d] = vv[src];
+                }
+            for (int j = 0; j < T; j++)
+                for (int d = 0; d < Dh; d++) {
+                    size_t src = (((size_t)b * T + j) * H + hh) * Dh + d;
+                    kh[(((size_t)b * H + hh) * Skv + S + j) * Dh + d] = ctx_k[src];
+                    vh[(((size_t)b * H + hh) * Skv + S + j) * Dh + d] = ctx_v[src];
+                }
+        }
+    for (int b = 0; b < B; b++) {
+        for (int s = 0; s < S; s++) mk[(size_t)b * Skv + s] = 1.0f;
+        for (int j = 0; j < T; j++) mk[(size_t)b * Skv + S + j] = ctx_mask[(size_t)b * T + j] ? 1.0f : 0.0f;
+    }
+    P(sdpa)(qh, kh, vh, mk, B, H, S, Skv, Dh, (float)(R_C(1.0) / SQRT((R)Dh)), oh);
+
+    /* gated = sigmoid(h @ W_gate) * o  (o back to [B, S, H*Dh]); out = gated @ W_o. */
+    P(linear)(h, blk->w_gate, NULL, M, D, D, tmp);
+    for (int b = 0; b < B; b++)
+        for (int s = 0; s < S; s++)
+            for (int hh = 0; hh < H; hh++)
+                for (int d = 0; d < Dh; d++) {
+                    size_t dst = (((size_t)b * S + s) * H + hh) * Dh + d;
+                    R o = (R)oh[(((size_t)b * H + hh) * S + s) * Dh + d];
+                    q[dst] = (float)(P(sigmoid)((R)tmp[dst]) * o);
+                }
+    P(linear)(q, blk->w_o, NULL, M, HD, D, out);
+    free(qkv); free(q); free(kk); free(vv); free(tmp);
+    free(qh); free(kh); free(vh); free(mk); free(oh);
+}
+
+/* diffusion.rs:62-105 (DiffusionBlock::forward_fused), dropout = identity:
+ *   (h1, g1) = attention_adaln(x, c); x += g1 * JointAttention(h1)
+ *   (h2, g2) = mlp_adaln(x, c);       x += g2 * SwiGLU(h2)
+ * x: [B, S, D] updated in place; cond: [B, 3D]. */
+void P(block_forward)(const orc_cfg* c, const orc_block* blk, float* x, const float* cond, int B,
+                      int S, int T, const float* ctx_k, const float* ctx_v,
+                      const uint8_t* ctx_mask, const float* cos_t, const float* sin_t) {
+    int D = c->model_dim, F = c->mlp_hidden, M = B * S;
+    size_t n = (size_t)M * D;
+    float* shift = (float*)malloc(sizeof(float) * (size_t)B * D);
+    float* scale = (float*)malloc(sizeof(float) * (size_t)B * D);
+    float* gate = (float*)malloc(sizeof(float) * (size_t)B * D);
+    float* h = (float*)malloc(sizeof(float) * n);
+    float* y = (float*)malloc(sizeof(float) * n);
+
+    P(adaln_vectors)(c, blk, 0, cond, B, shift, scale, gate);
+    P(fused_adaln)(x, scale, shift, B, S, D, c->norm_eps, h);
+    P(joint_attention)(c, blk, h, B, S, T, ctx_k, ctx_v, ctx_mask, cos_t, sin_t, y);
+    for (size_t i = 0; i < n; i++) {
+        int b = (int)(i / ((size_t)S * D)), d = (int)(i % D);
+        x[i] = (float)((R)x[i] + (R)gate[b * D + d] * (R)y[i]);
+    }
+    P(adaln_vectors)(c, blk, 1, cond, B, shift, scale, gate);
+    P(fused_adaln)(x, scale, shift, B, S, D, c->norm_eps, h);
+    P(swiglu)(h, blk->w13, blk->w2, M, D, F, y);
+    for (size_t i = 0; i < n; i++) {
+        int b = (int)(i / ((size_t)S * D)), d = (int)(i % D);
+        x[i] = (float)((R)x[i] + (R)gate[b * D + d] * (R)y[i]);
+    }
+    free(shift); free(scale); free(gate); free(h); free(y);
+}
+
+/* dit/model.rs:354-393 (forward_backbone_fused) with per-layer cached context KV
+ * (dit/model.rs:229-262):  c = cond_module(t); x = in_proj(x_t); 12 blocks;
+ * v = out_proj(out_norm(x)).
+ * ctx_k/ctx_v: [L][B][T][H][Dh]; ctx_mask: [B][T].
+ * debug (nullable): [L+1][B][S][D] = after_in_proj then each block output
+ * (BlockDebugOutputs, dit/model.rs:92-102). */
+void P(forward)(const orc_cfg* c, const orc_io* io, const orc_block* blocks, int B, int S,
+                const float* x_t, const float* t, int T, const float* ctx_k, const float* ctx_v,
+                const uint8_t* ctx_mask, float* v_out, float* debug) {
+    int D = c->model_dim, Pd = c->latent_dim, L = c->num_layers, H = c->num_heads,
+        Dh = c->head_dim;
+    size_t n = (size_t)B * S * D, lay = (size_t)B * T * H * Dh;
+    float* cond = (float*)malloc(sizeof(float) * (size_t)B * 3 * D);
+    float* x = (float*)malloc(sizeof(float) * n);
+    float* xn = (float*)malloc(sizeof(float) * n);
+    float* cs = (float*)malloc(sizeof(float) * (size_t)S * (Dh / 2));
+    float* sn = (float*)malloc(sizeof(float) * (size_t)S * (Dh / 2));
+    P(rope_tables)(S, Dh, c->rope_theta, cs, sn);
+    P(cond_module)(c, io, t, B, cond);
+    P(linear)(x_t, io->in_w, io->in_b, B * S, Pd, D, x);
+    if (debug) memcpy(debug, x, sizeof(float) * n);
+    for (int l = 0; l < L; l++) {
+        P(block_forward)(c, &blocks[l], x, cond, B, S, T, ctx_k + l * lay, ctx_v + l * lay,
+                         ctx_mask, cs, sn);
+        if (debug) memcpy(debug + (size_t)(l + 1) * n, x, sizeof(float) * n);
+    }
+    P(rms_norm)(x, io->out_norm_w, B * S, D, c->norm_eps, xn);
+    P(linear)(xn, io->out_w, io->out_b, B * S, D, Pd, v_out);
+    free(cond); free(x); free(xn); free(cs); free(sn);
+}
+
+/* attention.rs:431-501 (JointAttention::build_kv_cache): k_text = k_norm(text @ Wk_text),
+ * v_text = text @ Wv_text, same for the aux (speaker) state; ctx = [text | aux] along seq,
+ * ctx_mask = [text_mask | aux_mask].  aux may be NULL (Ta = 0).  Outputs [B, Tt+Ta, H, Dh]. */
+void P(build_kv_cache)(const orc_cfg* c, const float* k_norm, int B, const float* text,
+                       const uint8_t* text_mask, int Tt, int Dt, const float* wk_text,
+                       const float* wv_text, const float* aux, const uint8_t* aux_mask, int Ta,
+                       int Da, const float* wk_aux, const float* wv_aux, float* ctx_k,
+                       float* ctx_v, uint8_t* ctx_mask) {
+    int H = c->num_heads, Dh = c->head_dim, HD = H * Dh, T = Tt + (aux ? Ta : 0);
+    for (int seg = 0; seg < 2; seg++) {
+        const float* st = seg == 0 ? text : aux;
+        int Ts = seg == 0 ? Tt : Ta, Ds = seg == 0 ? Dt : Da, off = seg == 0 ? 0 : Tt;
+        const float* wk = seg == 0 ? wk_text : wk_aux;
+        const float* wv = seg == 0 ? wv_text : wv_aux;
+        const uint8_t* ms = seg == 0 ? text_mask : aux_mask;
+        if (!st || Ts == 0) continue;
+        float* kr = (float*)malloc(sizeof(float) * (size_t)B * Ts * HD);
+        float* kn = (float*)malloc(sizeof(float) * (size_t)B * Ts * HD);
+        float* vr = (float*)malloc(sizeof(float) * (size_t)B * Ts * HD);
+        P(linear)(st, wk, NULL, B * Ts, Ds, HD, kr);
+        P(head_rms_norm)(kr, k_norm, B * Ts, H, Dh, c->norm_eps, kn);
+        P(linear)(st, wv, NULL, B * Ts, Ds, HD, vr);
+        for (int b = 0; b < B; b++)
+            for (int j = 0; j < Ts; j++) {
+                memcpy(ctx_k + ((size_t)b * T + off + j) * HD, kn + ((size_t)b * Ts + j) * HD,
+                       sizeof(float) * HD);
+                memcpy(ctx_v + ((size_t)b * T + off + j) * HD, vr + ((size_t)b * Ts + j) * HD,
+                       sizeof(float) * HD);
+                ctx_mask[(size_t)b * T + off + j] = ms ? ms[(size_t)b * Ts + j] : 1;
+            }
+        free(kr); free(kn); free(vr);
+    }
+}
+
+/* euler_sampler.rs:132-718, Joint-CFG Euler branch (:325-328, :379, :435-469, :565-566, :714):
+ *   t_i = 0.999 (1 - i/N);  CFG iff min_t <= t_i <= max_t;
+ *   v_c = forward(x, t_i, cond KV); v_u = forward(x, t_i, uncond KV);
+ *   v = v_c + scale (v_c - v_u);  x += v (t_{i+1} - t_i).
+ * Two separate B=U forwards, exactly as the reference runs them.  Runs at most
+ * max_steps_run steps (<= 0: all); returns the number of steps run. */
+int P(sample_joint_cfg)(const orc_cfg* c, const orc_io* io, const orc_block* blocks, int U,
+                        int S, const float* x0, int T, const float* ctx_k_cond,
+                        const float* ctx_v_cond, const uint8_t* mask_cond,
+                        const float* ctx_k_unc, const float* ctx_v_unc, const uint8_t* mask_unc,
+                        int num_steps, float scale, float min_t, float max_t, int max_steps_run,
+                        float* x_out) {
+    int Pd = c->latent_dim;
+    size_t n = (size_t)U * S * Pd;
+    float* vc = (float*)malloc(sizeof(float) * n);
+    float* vu = (float*)malloc(sizeof(float) * n);
+    float* tt = (float*)malloc(sizeof(float) * (size_t)U);
+    memcpy(x_out, x0, sizeof(float) * n);
+    int run = (max_steps_run > 0 && max_steps_run < num_steps) ? max_steps_run : num_steps;
+    for (int i = 0; i < run; i++) {
+        /* The schedule is computed in f32 in the reference (euler_sampler.rs:326-328). */
+        float t = 0.999f * (1.0f - (float)i / (float)num_steps);
+        float tn = 0.999f * (1.0f - (float)(i + 1) / (float)num_steps);
+        for (int u = 0; u < U; u++) tt[u] = t;
+        int use_cfg = (min_t <= t) && (t <= max_t);
+        P(forward)(c, io, blocks, U, S, x_out, tt, T, ctx_k_cond, ctx_v_cond, mask_cond, vc, NULL);
+        if (use_cfg)
+            P(forward)(c, io, blocks, U, S, x_out, tt, T, ctx_k_unc, ctx_v_unc, mask_unc, vu, NULL);
+        float dt = tn - t;
+        for (size_t j = 0; j < n; j++) {
+            R v = (R)vc[j];
+            if (use_cfg) v = v + ((R)vc[j] - (R)vu[j]) * (R)scale;
+            x_out[j] = (float)((R)x_out[j] + v * (R)dt);
+        }
+    }
+    free(vc); free(vu); free(tt);
+    return run;
+}

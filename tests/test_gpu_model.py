@@ -1,0 +1,179 @@
+"""GPU parity of the whole RF-step DiT path (libirodori_hip through the C ABI) against the
+CPU oracle, on identical seeded inputs and random-init weights.
+
+Bars: f32 HIP path within 1e-4 relative L2 per block, bf16 within
+1e-2 per block and 2e-2 on the final sampled latent.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import irodori_hip as ih
+from conftest import rel_l2
+
+pytestmark = pytest.mark.gpu
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+BF16, F32 = ih.InferenceBackendKind.HIP_BF16, ih.InferenceBackendKind.HIP_F32
+TOL_BLOCK = {BF16: 1e-2, F32: 1e-4}
+TOL_FINAL = {BF16: 2e-2, F32: 1e-4}
+
+
+def joint_params(steps, scale=3.0, **kw):
+    g = ih.GuidanceConfig(mode=ih.CfgGuidanceMode.JOINT, scale_text=scale, scale_speaker=scale,
+                          min_t=kw.pop("min_t", 0.0), max_t=kw.pop("max_t", 1.0))
+    return ih.SamplerParams(num_steps=steps, guidance=g, **kw)
+
+
+def make_engine(cfg, backend, w, ctx, rows, seq):
+    e = ih.HipInferenceEngine(cfg, backend, max_rows=rows, max_seq=seq, max_ctx=max(ctx.t_ctx, 1))
+    e.load_weights(w)
+    e.set_context_kv(ctx)
+    return e
+
+
+SMALL = {
+    # name: (cfg factory, seq, text, speaker, weight std, norm jitter)
+    "tiny": (ih.cfg_tiny, 40, 20, 13, 0.05, 0.1),
+    "cfg1": (ih.cfg_cpu_plumbing, 64, 16, 32, 0.02, 0.0),
+}
+
+
+@pytest.mark.parametrize("backend", [F32, BF16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("name", list(SMALL))
+def test_forward_per_block(oracle64, name, backend):
+    make_cfg, S, tt, ts, std, jit = SMALL[name]
+    cfg = make_cfg()
+    w = ih.DitWeights.random(cfg, 0, std=std, norm_jitter=jit)
+    ctx = ih.make_context_kv(cfg, 1, tt, ts, seed=1)
+    x = ih.make_noise(2, S, cfg.latent_dim, 2)
+    t = np.array([0.9, 0.35], np.float32)
+    with make_engine(cfg, backend, w, ctx, 2, S) as e:
+        v, dbg = e.forward_with_cond_cached(x, t, debug=True)
+    v_ref, dbg_ref = oracle64.forward(cfg, w, x, t, ctx.k, ctx.v, ctx.mask, debug=True)
+    errs = [rel_l2(dbg[i], dbg_ref[i]) for i in range(dbg.shape[0])]
+    print(name, backend.value, "per-block rel L2:", ["%.2e" % x for x in errs],
+          "v: %.2e" % rel_l2(v, v_ref))
+    assert max(errs) < TOL_BLOCK[backend]
+    assert rel_l2(v, v_ref) < TOL_BLOCK[backend]
+
+
+@pytest.mark.parametrize("backend", [F32, BF16], ids=["f32", "bf16"])
+def test_block_forward_matches_oracle(oracle64, backend):
+    cfg = ih.cfg_cpu_plumbing()
+    w = ih.DitWeights.random(cfg, 5, norm_jitter=0.05)
+    ctx = ih.make_context_kv(cfg, 1, 16, 32, seed=6)
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((2, 64, cfg.model_dim)).astype(np.float32)
+    cond = (0.5 * rng.standard_normal((2, 3 * cfg.model_dim))).astype(np.float32)
+    with make_engine(cfg, backend, w, ctx, 2, 64) as e:
+        got = e.block_forward(1, x, cond)
+    ref = oracle64.block_forward(cfg, w.blocks[1], x, cond, ctx.k[1], ctx.v[1], ctx.mask)
+    assert rel_l2(got, ref) < TOL_BLOCK[backend]
+
+
+@pytest.mark.parametrize("backend", [F32, BF16], ids=["f32", "bf16"])
+def test_sample_joint_cfg_cfg1(oracle64, backend):
+    # BASELINE config 1 sampled for 4 Euler steps (Joint CFG, scale 3, min_t 0).
+    cfg = ih.cfg_cpu_plumbing()
+    w = ih.DitWeights.random(cfg, 0)
+    ctx = ih.make_context_kv(cfg, 1, 16, 32, seed=1)
+    x0 = ih.make_noise(1, 64, cfg.latent_dim, 2)
+    p = joint_params(4)
+    with make_engine(cfg, backend, w, ctx, 2, 64) as e:
+        got = e.sample(x0, p)
+        again = e.sample(x0, p)
+    c, u = ctx.rows([0]), ctx.rows([1])
+    ref, _ = oracle64.sample_joint_cfg(cfg, w, x0, (c.k, c.v, c.mask), (u.k, u.v, u.mask), 4, 3.0)
+    print(backend.value, "final rel L2 %.2e" % rel_l2(got, ref))
+    assert rel_l2(got, ref) < TOL_FINAL[backend]
+    assert np.array_equal(got, again)  # graph replay is deterministic
+
+
+def test_sample_two_utterances_rows_independent(oracle64):
+    # Two utterances in one batch (rows 0..3) equal each utterance sampled alone.
+    cfg = ih.cfg_tiny()
+    w = ih.DitWeights.random(cfg, 3, std=0.05, norm_jitter=0.1)
+    ctx = ih.make_context_kv(cfg, 2, 12, 9, seed=4)
+    x0 = ih.make_noise(2, 24, cfg.latent_dim, 5)
+    p = joint_params(3, scale=2.0)
+    with make_engine(cfg, F32, w, ctx, 4, 24) as e:
+        both = e.sample(x0, p)
+    for u in range(2):
+        c, un = ctx.rows([2 * u]), ctx.rows([2 * u + 1])
+        ref, _ = oracle64.sample_joint_cfg(cfg, w, x0[u:u + 1], (c.k, c.v, c.mask),
+                                           (un.k, un.v, un.mask), 3, 2.0)
+        assert rel_l2(both[u:u + 1], ref) < 1e-4
+
+
+def test_sample_cfg_window_off_equals_scale_zero():
+    # min_t above every t_i disables CFG (euler_sampler.rs:379) == scale 0.
+    cfg = ih.cfg_tiny()
+    w = ih.DitWeights.random(cfg, 8, std=0.05)
+    ctx = ih.make_context_kv(cfg, 1, 8, 8, seed=9)
+    x0 = ih.make_noise(1, 16, cfg.latent_dim, 10)
+    with make_engine(cfg, F32, w, ctx, 2, 16) as e:
+        a = e.sample(x0, joint_params(3, min_t=1.0, max_t=1.0))
+        b = e.sample(x0, joint_params(3, scale=0.0))
+        c = e.sample(x0, joint_params(3))
+    assert np.array_equal(a, b)
+    assert rel_l2(c, b) > 1e-3
+
+
+def test_forward_errors_are_reported():
+    cfg = ih.cfg_tiny()
+    e = ih.HipInferenceEngine(cfg, F32, max_rows=2, max_seq=16, max_ctx=8)
+    x = np.zeros((2, 16, cfg.latent_dim), np.float32)
+    with pytest.raises(ih.IrodoriError) as ei:
+        e.forward_with_cond_cached(x, np.zeros(2, np.float32))
+    assert ei.value.kind == "NotLoaded"
+    e.load_weights(ih.DitWeights.random(cfg, 0))
+    with pytest.raises(ih.IrodoriError) as ei:
+        e.forward_with_cond_cached(np.zeros((2, 17, cfg.latent_dim), np.float32),
+                                   np.zeros(2, np.float32))
+    assert ei.value.kind == "Shape"
+    with pytest.raises(ih.IrodoriError) as ei:
+        e.sample(x[:1], joint_params(0))
+    assert ei.value.kind == "Config"
+    e.close()
+
+
+# ---- BASELINE config 4 (12 layers, d=1024, 750 frames, 631 context keys) ------------------
+def cfg4_inputs():
+    cfg = ih.cfg_full_rf()
+    w = ih.DitWeights.random(cfg, 0)
+    ctx = ih.make_context_kv(cfg, 1, 256, 375, seed=1)
+    x0 = ih.make_noise(1, 750, cfg.latent_dim, 2)
+    return cfg, w, ctx, x0
+
+
+@pytest.fixture(scope="module")
+def cfg4():
+    return cfg4_inputs()
+
+
+def test_cfg4_forward_per_block_bf16(oracle32, cfg4):
+    cfg, w, ctx, x0 = cfg4
+    x = np.concatenate([x0, x0])
+    t = np.array([0.999, 0.999], np.float32)
+    with make_engine(cfg, BF16, w, ctx, 2, 750) as e:
+        v, dbg = e.forward_with_cond_cached(x, t, debug=True)
+    v_ref, dbg_ref = oracle32.forward(cfg, w, x, t, ctx.k, ctx.v, ctx.mask, debug=True)
+    errs = [rel_l2(dbg[i], dbg_ref[i]) for i in range(dbg.shape[0])]
+    print("cfg4 bf16 per-block rel L2:", ["%.2e" % e_ for e_ in errs], "v %.2e" % rel_l2(v, v_ref))
+    assert max(errs) < 1e-2 and rel_l2(v, v_ref) < 1e-2
+
+
+def test_cfg4_sample_40_steps_bf16_vs_golden(cfg4):
+    # Final 40-step latent against the f32 oracle's, committed by tests/golden/make_golden.py.
+    path = os.path.join(HERE, "golden", "cfg4_joint40_final_latent.npy")
+    if not os.path.exists(path):
+        pytest.skip("golden fixture not generated")
+    cfg, w, ctx, x0 = cfg4
+    with make_engine(cfg, BF16, w, ctx, 2, 750) as e:
+        got = e.sample(x0, joint_params(40))
+    ref = np.load(path)
+    err = rel_l2(got, ref)
+    print("cfg4 bf16 40-step final latent rel L2 %.3e" % err)
+    assert err < 2e-2

@@ -1,0 +1,117 @@
+"""Independent restatement of the RF-step DiT forward with torch.nn.functional library
+routines (F.linear, F.silu, F.scaled_dot_product_attention, torch.tanh/sigmoid/rsqrt),
+in float64 on the CPU.  Test infrastructure: it pins the C oracle's composition (index
+order, transposes, chunk order, mask polarity) against code that shares none of its
+loops.  Follows the reference's structure: src/model/dit/model.rs:354-393 (backbone),
+src/model/diffusion.rs:62-105 (block), src/model/attention.rs:272-425 (joint attention),
+src/model/norm.rs:25-173, src/model/rope.rs:24-165, src/model/feed_forward.rs:76-85.
+"""
+import math
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+DT = torch.float64
+
+
+def T(a):
+    return torch.as_tensor(np.asarray(a), dtype=DT)
+
+
+def lin(x, w, b=None):
+    # Burn row layout w [d_in, d_out]: y = x @ w + b == F.linear(x, w^T, b)
+    return F.linear(x, T(w).t(), None if b is None else T(b))
+
+
+def rms(x, eps):
+    return torch.sqrt(x.pow(2).mean(-1, keepdim=True) + eps)
+
+
+def timestep_embedding(t, dim):
+    half = dim // 2
+    i = torch.arange(half, dtype=DT)
+    f = 1000.0 * torch.exp(-math.log(10000.0) * i / half)
+    a = T(t)[:, None] * f[None]
+    return torch.cat([torch.cos(a), torch.sin(a)], dim=1)
+
+
+def rope_tables(S, Dh, theta=10000.0):
+    half = Dh // 2
+    freq = 1.0 / theta ** (2.0 * torch.arange(half, dtype=DT) / Dh)
+    ang = torch.arange(S, dtype=DT)[:, None] * freq[None]
+    return torch.cos(ang), torch.sin(ang)
+
+
+def rope(x, cos, sin):
+    # x [B, S, H, Dh]: complex rotation of interleaved pairs via torch.view_as_complex.
+    B, S, H, Dh = x.shape
+    xc = torch.view_as_complex(x.reshape(B, S, H, Dh // 2, 2).contiguous())
+    rot = torch.polar(torch.ones_like(cos), torch.atan2(sin, cos))  # cos + i sin
+    y = xc * rot[None, :, None, :]
+    return torch.view_as_real(y).reshape(B, S, H, Dh)
+
+
+def adaln(x, cond_chunks, blk, which, eps):
+    outs = []
+    for ch in range(3):
+        raw = cond_chunks[ch]
+        v = lin(lin(F.silu(raw), blk["ada_down"][which][ch]), blk["ada_up"][which][ch],
+                blk["ada_up_b"][which][ch]) + raw
+        outs.append(v)
+    shift, scale, gate = outs
+    h = x / rms(x, eps) * (1 + scale[:, None, :]) + shift[:, None, :]
+    return h, torch.tanh(gate)[:, None, :]
+
+
+def joint_attention(h, blk, ctx_k, ctx_v, ctx_mask, cos, sin, H, Dh, eps):
+    B, S, D = h.shape
+    HD = H * Dh
+    qkv = lin(h, blk["w_qkv"])
+    q, k, v = qkv[..., :HD], qkv[..., HD:2 * HD], qkv[..., 2 * HD:]
+    q = q.reshape(B, S, H, Dh)
+    k = k.reshape(B, S, H, Dh)
+    v = v.reshape(B, S, H, Dh)
+    qn = T(blk["q_norm"])
+    kn = T(blk["k_norm"])
+    q = q / rms(q, eps) * qn
+    k = k / rms(k, eps) * kn
+    hh = H // 2
+    q = torch.cat([rope(q[:, :, :hh], cos, sin), q[:, :, hh:]], dim=2)
+    k = torch.cat([rope(k[:, :, :hh], cos, sin), k[:, :, hh:]], dim=2)
+    K = torch.cat([k, T(ctx_k)], dim=1).transpose(1, 2)
+    V = torch.cat([v, T(ctx_v)], dim=1).transpose(1, 2)
+    valid = torch.cat([torch.ones(B, S, dtype=torch.bool), T(ctx_mask) > 0], dim=1)
+    o = F.scaled_dot_product_attention(q.transpose(1, 2), K, V,
+                                       attn_mask=valid[:, None, None, :])
+    o = o.transpose(1, 2).reshape(B, S, HD)
+    return lin(torch.sigmoid(lin(h, blk["w_gate"])) * o, blk["w_o"])
+
+
+def swiglu(h, w13, w2):
+    Fh = np.asarray(w2).shape[0]
+    u = lin(h, w13)
+    return lin(F.silu(u[..., :Fh]) * u[..., Fh:], w2)
+
+
+def forward(cfg, weights, x_t, t, ctx_k, ctx_v, ctx_mask, debug=False):
+    io = weights.io
+    D, H, Dh, eps = cfg.model_dim, cfg.num_heads, cfg.head_dim, cfg.norm_eps
+    x_t = T(x_t)
+    B, S, _ = x_t.shape
+    cos, sin = rope_tables(S, Dh, cfg.rope_theta)
+    c = lin(F.silu(lin(F.silu(lin(timestep_embedding(t, cfg.timestep_embed_dim), io["cond_w0"])),
+                       io["cond_w1"])), io["cond_w2"])
+    chunks = [c[:, 0:D], c[:, D:2 * D], c[:, 2 * D:3 * D]]
+    x = lin(x_t, io["in_w"], io["in_b"])
+    outs = [x.clone()]
+    for l, blk in enumerate(weights.blocks):
+        h1, g1 = adaln(x, chunks, blk, 0, eps)
+        x = x + g1 * joint_attention(h1, blk, ctx_k[l], ctx_v[l], ctx_mask, cos, sin, H, Dh, eps)
+        h2, g2 = adaln(x, chunks, blk, 1, eps)
+        x = x + g2 * swiglu(h2, blk["w13"], blk["w2"])
+        outs.append(x.clone())
+    v = lin(x / rms(x, eps) * T(io["out_norm_w"]), io["out_w"], io["out_b"])
+    if debug:
+        return v.numpy(), torch.stack(outs).numpy()
+    return v.numpy()
