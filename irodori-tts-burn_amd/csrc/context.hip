@@ -19,6 +19,7 @@
 #include <new>
 #include <string>
 #include <tuple>
+#include <type_traits>
 #include <vector>
 
 #include "../../include/irodori_hip.h"
@@ -35,8 +36,8 @@ namespace {
 // ---------------------------------------------------------------------------------------
 // Weight ingest kernels: Burn [K, N] f32 -> K-major [N, K] compute dtype.
 // mode 0: dst row n = source column n.
-// mode 1: SwiGLU interleave — dst rows 32g..32g+15 = W1 columns 16g.., rows 32g+16..32g+31 =
-//         W3 columns 16g.. (W3 starts at source column N/2).
+// mode 1: SwiGLU interleave — dst rows 64g..64g+31 = W1 columns 32g.., rows 64g+32..64g+63 =
+//         W3 columns 32g.. (W3 starts at source column N/2).
 // ---------------------------------------------------------------------------------------
 template <typename T>
 __global__ void transpose_kmajor_kernel(const float* __restrict__ src, int K, int N, int mode,
@@ -48,8 +49,8 @@ __global__ void transpose_kmajor_kernel(const float* __restrict__ src, int K, in
         int k = k0 + r, n = n0 + tx;
         int sc = n;
         if (mode == 1 && n < N) {
-            int half = N / 2, g = n / 32, w = n % 32;
-            sc = w < 16 ? 16 * g + w : half + 16 * g + (w - 16);
+            int half = N / 2, g = n / 64, w = n % 64;
+            sc = w < 32 ? 32 * g + w : half + 32 * g + (w - 32);
         }
         tile[r][tx] = (k < K && n < N) ? src[(size_t)k * N + sc] : 0.f;
     }
@@ -74,7 +75,7 @@ using namespace irodori;
 struct LayerBufs {
     void* w_qkvg = nullptr;  // [4D, D]
     void* w_o = nullptr;     // [D, HD]
-    void* w13 = nullptr;     // [2F, D] interleaved per 16
+    void* w13 = nullptr;     // [2F, D], W1/W3 rows interleaved per 32
     void* w2 = nullptr;      // [D, F]
     float* q_norm = nullptr;
     float* k_norm = nullptr;
@@ -82,7 +83,7 @@ struct LayerBufs {
     float* ada_up[2][3] = {};
     float* ada_up_b[2][3] = {};
     void* ctx_k = nullptr;   // [rows, H, max_ctx, Dh]
-    void* ctx_v = nullptr;
+    void* ctx_v = nullptr;      // V^T [rows, H, Dh, Tp] (Tp = max_ctx rounded up to 64), keys permuted
     float* ctx_mask = nullptr;  // [rows, max_ctx]
     int* tile_on = nullptr;     // [rows, ceil(max_ctx / 64)]
     bool loaded = false;
@@ -120,7 +121,7 @@ struct irodori_ctx {
     void* h = nullptr;    // [rows*S, D]
     void* q = nullptr;    // [rows, H, S, Dh]
     void* ks = nullptr;
-    void* vs = nullptr;
+    void* vs = nullptr;   // V^T [rows, H, Dh, S'] (S' = S rounded up to 64), keys permuted
     void* gate = nullptr;  // [rows*S, D]
     void* o = nullptr;     // [rows*S, D]
     void* u = nullptr;     // [rows*S, F]
@@ -318,6 +319,8 @@ int enqueue_layer(irodori_ctx* c, int l, int B, int S, const ModTable& mt, bool 
     ga.k_norm = lb.k_norm;
     ga.rope_cos = c->rope_cos;
     ga.rope_sin = c->rope_sin;
+    ga.vt_stride = (S + 63) / 64 * 64;
+    ga.q_scale = 1.4426950408889634f / sqrtf((float)g.head_dim);
     if (launch_gemm<T>(EPI_QKVG, ga, st)) { set_last_error("qkvg gemm shape"); return IRODORI_ERR_SHAPE; }
 
     // Joint attention over [latent self | cached ctx] (attention.rs:349-425).
@@ -327,11 +330,15 @@ int enqueue_layer(irodori_ctx* c, int l, int B, int S, const ModTable& mt, bool 
     aa.V0 = static_cast<const T*>(c->vs);
     aa.len0 = S;
     aa.stride0 = S;
+    aa.v_transposed = true;
+    aa.prescaled = true;
+    aa.vstride0 = (S + 63) / 64 * 64;
     if (c->t_ctx > 0) {
         aa.K1 = static_cast<const T*>(lb.ctx_k);
         aa.V1 = static_cast<const T*>(lb.ctx_v);
         aa.len1 = c->t_ctx;
         aa.stride1 = g.max_ctx;
+        aa.vstride1 = (g.max_ctx + 63) / 64 * 64;
         aa.mask1 = lb.ctx_mask;
         aa.tile_on1 = lb.tile_on;
     }
@@ -342,7 +349,12 @@ int enqueue_layer(irodori_ctx* c, int l, int B, int S, const ModTable& mt, bool 
     aa.out_mode = 0;
     aa.G = static_cast<const T*>(c->gate);
     aa.O = static_cast<T*>(c->o);
-    if (launch_attention<T, 64>(aa, st)) { set_last_error("attention shape"); return IRODORI_ERR_SHAPE; }
+    int arc;
+    if constexpr (std::is_same<T, bf16>::value)
+        arc = launch_attention32(aa, st);
+    else
+        arc = launch_attention<T, 64>(aa, st);
+    if (arc) { set_last_error("attention launch rejected the shape"); return IRODORI_ERR_SHAPE; }
 
     // x += g_attn * (o @ Wo) (attention.rs:424, diffusion.rs:98).
     ga.A = static_cast<const T*>(c->o);
@@ -552,6 +564,7 @@ int irodori_ctx_create(int device, const irodori_dit_config* cfg, irodori_ctx** 
     size_t es = c->esz, M = (size_t)R * S;
     c->layers.resize(L);
     int ntl = (T + 63) / 64;
+    int Tp = ntl * 64, Sp = (S + 63) / 64 * 64;
     for (int l = 0; l < L; l++) {
         auto& lb = c->layers[l];
         IRO_TRY(dev_alloc(c.get(), &lb.w_qkvg, es * 4 * D * D));
@@ -567,7 +580,8 @@ int irodori_ctx_create(int device, const irodori_dit_config* cfg, irodori_ctx** 
                 IRO_TRY(dalloc(c.get(), &lb.ada_up_b[k][ch], sizeof(float) * D));
             }
         IRO_TRY(dev_alloc(c.get(), &lb.ctx_k, es * (size_t)R * H * T * Dh));
-        IRO_TRY(dev_alloc(c.get(), &lb.ctx_v, es * (size_t)R * H * T * Dh));
+        IRO_TRY(dev_alloc(c.get(), &lb.ctx_v, es * (size_t)R * H * Dh * Tp));
+        IRO_HIP_CHECK(hipMemsetAsync(lb.ctx_v, 0, es * (size_t)R * H * Dh * Tp, c->stream));
         IRO_TRY(dalloc(c.get(), &lb.ctx_mask, sizeof(float) * (size_t)R * T));
         IRO_TRY(dalloc(c.get(), &lb.tile_on, sizeof(int) * (size_t)R * ntl));
         lb.row_set.assign(R, 0);
@@ -585,7 +599,8 @@ int irodori_ctx_create(int device, const irodori_dit_config* cfg, irodori_ctx** 
     IRO_TRY(dev_alloc(c.get(), &c->h, es * M * D));
     IRO_TRY(dev_alloc(c.get(), &c->q, es * M * D));
     IRO_TRY(dev_alloc(c.get(), &c->ks, es * M * D));
-    IRO_TRY(dev_alloc(c.get(), &c->vs, es * M * D));
+    IRO_TRY(dev_alloc(c.get(), &c->vs, es * (size_t)R * H * Dh * Sp));
+    IRO_HIP_CHECK(hipMemsetAsync(c->vs, 0, es * (size_t)R * H * Dh * Sp, c->stream));
     IRO_TRY(dev_alloc(c.get(), &c->gate, es * M * D));
     IRO_TRY(dev_alloc(c.get(), &c->o, es * M * D));
     IRO_TRY(dev_alloc(c.get(), &c->u, es * M * F));
@@ -628,9 +643,10 @@ int irodori_load_io_weights(irodori_ctx* c, const irodori_io_weights* w) {
     IRO_TRY(upload(c, c->in_w, w->in_w, sizeof(float) * (size_t)P * D));
     IRO_TRY(upload(c, c->in_b, w->in_b, sizeof(float) * D));
     IRO_TRY(upload(c, c->out_norm_w, w->out_norm_w, sizeof(float) * D));
+    // Output head weight with the out_norm weight folded in, transposed to [P, D].
     std::vector<float> wt((size_t)P * D);
     for (int d = 0; d < D; d++)
-        for (int p = 0; p < P; p++) wt[(size_t)p * D + d] = w->out_w[(size_t)d * P + p];
+        for (int p = 0; p < P; p++) wt[(size_t)p * D + d] = w->out_w[(size_t)d * P + p] * w->out_norm_w[d];
     IRO_TRY(upload(c, c->out_wT, wt.data(), sizeof(float) * wt.size()));
     IRO_TRY(upload(c, c->out_b, w->out_b, sizeof(float) * P));
     IRO_HIP_CHECK(hipStreamSynchronize(c->stream));
@@ -699,33 +715,40 @@ int irodori_set_ctx_kv(irodori_ctx* c, int layer, int row, int t_ctx, const floa
     auto& lb = c->layers[layer];
     int H = g.num_heads, Dh = g.head_dim, T = g.max_ctx > 0 ? g.max_ctx : 1;
     if (t_ctx > 0) {
-        // [t, H, Dh] f32 -> [H, T(max), Dh] compute dtype for this row; pad keys masked.
-        size_t n = (size_t)H * T * Dh;
-        std::vector<uint16_t> kb, vb;
-        std::vector<float> kf, vf;
-        if (c->bf16) { kb.assign(n, 0); vb.assign(n, 0); } else { kf.assign(n, 0.f); vf.assign(n, 0.f); }
-        for (int j = 0; j < t_ctx; j++)
+        // k: [t, H, Dh] f32 -> [H, T, Dh];  v: [t, H, Dh] f32 -> V^T [H, Dh, Tp] with keys in
+        // the attention kernel's A-operand order (vt_pos_bf16 / vt_pos_f32).
+        int Tp = (T + 63) / 64 * 64;
+        size_t nk = (size_t)H * T * Dh, nv = (size_t)H * Dh * Tp;
+        auto cvt = [](float f) -> uint16_t {
+            uint32_t u;
+            memcpy(&u, &f, 4);
+            if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+            u += 0x7fffu + ((u >> 16) & 1u);
+            return (uint16_t)(u >> 16);
+        };
+        std::vector<float> kf(nk, 0.f), vf(nv, 0.f);
+        for (int j = 0; j < t_ctx; j++) {
+            int pos = c->bf16 ? vt_pos_bf16(j) : vt_pos_f32(j);
             for (int hh = 0; hh < H; hh++)
                 for (int d = 0; d < Dh; d++) {
-                    size_t src = ((size_t)j * H + hh) * Dh + d, dst = ((size_t)hh * T + j) * Dh + d;
-                    if (c->bf16) {
-                        auto cvt = [](float f) -> uint16_t {
-                            uint32_t u;
-                            memcpy(&u, &f, 4);
-                            if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
-                            u += 0x7fffu + ((u >> 16) & 1u);
-                            return (uint16_t)(u >> 16);
-                        };
-                        kb[dst] = cvt(k[src]);
-                        vb[dst] = cvt(v[src]);
-                    } else {
-                        kf[dst] = k[src];
-                        vf[dst] = v[src];
-                    }
+                    size_t src = ((size_t)j * H + hh) * Dh + d;
+                    kf[((size_t)hh * T + j) * Dh + d] = k[src];
+                    vf[((size_t)hh * Dh + d) * Tp + pos] = v[src];
                 }
-        size_t off = (size_t)row * n * c->esz;
-        IRO_TRY(upload(c, static_cast<char*>(lb.ctx_k) + off, c->bf16 ? (const void*)kb.data() : kf.data(), n * c->esz));
-        IRO_TRY(upload(c, static_cast<char*>(lb.ctx_v) + off, c->bf16 ? (const void*)vb.data() : vf.data(), n * c->esz));
+        }
+        std::vector<uint16_t> kb, vb;
+        const void* kp = kf.data();
+        const void* vp = vf.data();
+        if (c->bf16) {
+            kb.resize(nk);
+            vb.resize(nv);
+            for (size_t i = 0; i < nk; i++) kb[i] = cvt(kf[i]);
+            for (size_t i = 0; i < nv; i++) vb[i] = cvt(vf[i]);
+            kp = kb.data();
+            vp = vb.data();
+        }
+        IRO_TRY(upload(c, static_cast<char*>(lb.ctx_k) + (size_t)row * nk * c->esz, kp, nk * c->esz));
+        IRO_TRY(upload(c, static_cast<char*>(lb.ctx_v) + (size_t)row * nv * c->esz, vp, nv * c->esz));
         std::vector<float> m(T, 0.f);
         int ntl = (T + 63) / 64;
         std::vector<int> on(ntl, 0);
@@ -958,13 +981,15 @@ int irodori_profile_layer(irodori_ctx* c, int B, int S, int iters, irodori_kerne
                     AttnArgs<T> aa{};
                     aa.Q = static_cast<const T*>(c->q); aa.K0 = static_cast<const T*>(c->ks);
                     aa.V0 = static_cast<const T*>(c->vs); aa.len0 = S; aa.stride0 = S;
+                    aa.v_transposed = true; aa.prescaled = true; aa.vstride0 = (S + 63) / 64 * 64;
                     if (c->t_ctx > 0) {
                         aa.K1 = static_cast<const T*>(lb.ctx_k); aa.V1 = static_cast<const T*>(lb.ctx_v);
-                        aa.len1 = c->t_ctx; aa.stride1 = g.max_ctx; aa.mask1 = lb.ctx_mask; aa.tile_on1 = lb.tile_on;
+                        aa.len1 = c->t_ctx; aa.stride1 = g.max_ctx; aa.vstride1 = (g.max_ctx + 63) / 64 * 64;
+                        aa.mask1 = lb.ctx_mask; aa.tile_on1 = lb.tile_on;
                     }
                     aa.B = B; aa.H = H; aa.Sq = S; aa.scale = 1.0f / sqrtf((float)g.head_dim);
                     aa.out_mode = 0; aa.G = static_cast<const T*>(c->gate); aa.O = static_cast<T*>(c->o);
-                    launch_attention<T, 64>(aa, c->stream);
+                    launch_attention32(aa, c->stream);
                     continue;
                 }
                 GemmArgs<T> ga{};
@@ -975,6 +1000,8 @@ int irodori_profile_layer(irodori_ctx* c, int B, int S, int iters, irodori_kerne
                     ga.Q = static_cast<T*>(c->q); ga.Kd = static_cast<T*>(c->ks); ga.Vd = static_cast<T*>(c->vs);
                     ga.G = static_cast<T*>(c->gate); ga.q_norm = lb.q_norm; ga.k_norm = lb.k_norm;
                     ga.rope_cos = c->rope_cos; ga.rope_sin = c->rope_sin;
+                    ga.vt_stride = (S + 63) / 64 * 64;
+                    ga.q_scale = 1.4426950408889634f / sqrtf((float)g.head_dim);
                     launch_gemm<T>(EPI_QKVG, ga, c->stream);
                 } else if (kidx == 3) {
                     ga.A = static_cast<const T*>(c->o); ga.W = static_cast<const T*>(lb.w_o); ga.N = D; ga.K = D; ga.kind = 0;

@@ -19,6 +19,15 @@ struct ModTable {
     int layers;
 };
 
+// Position of latent/context key s inside a V^T row.  bf16 path (32x32x16 attention):
+// bits 2 and 3 of the key index swapped; f32 path (16x16 attention): keys permuted inside
+// each 32-key group.  Both are involutions on aligned groups, so padding stays in place.
+__host__ __device__ inline int vt_pos_bf16(int s) { return (s & ~12) | ((s & 4) << 1) | ((s & 8) >> 1); }
+__host__ __device__ inline int vt_pos_f32(int s) {
+    int kk = s & 31;
+    return (s & ~31) | (((kk & 15) >> 2) * 8 + (kk >> 4) * 4 + (kk & 3));
+}
+
 // ---- kernels_norm.hip ------------------------------------------------------------------
 void launch_rms_norm_op(const float* x, const float* w, int rows, int D, float eps, float* y,
                         hipStream_t st);
@@ -40,7 +49,7 @@ void launch_inproj_norm(const float* x_src, int rows_per_src, const float* in_w,
 struct FinalArgs {
     const float* x;
     const float* norm_w;
-    const float* out_wT;  // [P, D]
+    const float* out_wT;  // [P, D] = (out_norm.weight (.) W_out)^T
     const float* out_b;   // [P]
     int B, S, D, P;
     float eps;
@@ -84,12 +93,14 @@ struct GemmArgs {
     ModTable mt;
     int layer, kind;
     int S;
-    // EPI_SWIGLU: U [M, N/2] = silu(acc_1) * acc_3 (W rows interleaved in 16-row groups)
+    // EPI_SWIGLU: U [M, N/2] = silu(acc_1) * acc_3 (W rows interleaved in 32-row groups)
     T* U;
     // EPI_QKVG: N = 4 * D; q/k head-normed (+ half RoPE), v raw, gate sigmoid.
     T* Q;  // [B, H, S, Dh]
     T* Kd; // [B, H, S, Dh]
-    T* Vd; // [B, H, S, Dh]
+    T* Vd; // V^T [B, H, Dh, vt_stride], key s at vt_pos_bf16 / vt_pos_f32 by dtype
+    int vt_stride;  // multiple of 64, >= S
+    float q_scale;  // q multiplier (Dh^-1/2 * log2 e) applied after norm + RoPE
     T* G;  // [M, D]
     const float* q_norm;  // [H, Dh]
     const float* k_norm;
@@ -118,6 +129,13 @@ struct AttnArgs {
     const int* tile_on1;  // [B, ceil(stride1/64)] nonzero if the 64-key tile has a valid key
     int B, H, Sq;
     float scale;
+    // v_transposed: V0/V1 hold V^T [B, H, Dh, vstride] with keys at vt_pos_f32 (this
+    // kernel) or vt_pos_bf16 (launch_attention32); vstride is a multiple of 64 and padding
+    // columns hold finite values.
+    bool v_transposed;
+    int vstride0, vstride1;
+    // prescaled: Q already multiplied by scale * log2(e) (the QKV epilogue does this).
+    bool prescaled;
     // epilogue: out_mode 0 -> O [B*Sq, H*Dh] (T) = gate[m, h*Dh+d] * attn;
     //           out_mode 1 -> Of [B, H, Sq, Dh] f32
     int out_mode;
@@ -127,5 +145,7 @@ struct AttnArgs {
 };
 template <typename T, int DH>
 int launch_attention(const AttnArgs<T>& a, hipStream_t st);
+// bf16, Dh = 64, V^T in vt_pos_bf16 order, Q pre-scaled (kernels_attn32.hip).
+int launch_attention32(const AttnArgs<bf16>& a, hipStream_t st);
 
 }  // namespace irodori

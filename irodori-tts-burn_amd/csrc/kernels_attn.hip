@@ -9,9 +9,12 @@
 // accumulator layout lane l holds keys 4*(l/16)+i (+16 per block) of query column l%16,
 // so the online-softmax max/sum of a query reduce over only 4 lanes (l, l^16, l^32,
 // l^48), and the probabilities P^T are already in B-operand layout for O^T = V^T P^T —
-// no LDS round trip for P.  V is staged transposed in LDS with keys permuted inside
-// each 32-key group so that a lane's 8 keys are one contiguous 16-byte read.
-// Workgroup = 4 wavefronts x WQ queries of one (batch row, head); K/V tiles are double
+// no LDS round trip for P.  The A operand of that product is V^T with the keys of each
+// 32-key group permuted so that a lane's 8 keys are one contiguous 16-byte read.  In the
+// model path V is stored that way in HBM (by the QKV epilogue and at context ingest), so
+// K and V^T tiles both move HBM -> registers -> LDS as plain 16-byte rows; the operator
+// entry point (V given as [key][d]) transposes while staging instead.
+// Workgroup = 4 wavefronts x 16*QB queries of one (batch row, head); K/V tiles are double
 // buffered in LDS with register prefetch; context tiles with no valid key are skipped.
 #include "common.hpp"
 #include "kernels.hpp"
@@ -51,8 +54,7 @@ __device__ __forceinline__ bf16 vec_elem<bf16>(const u32x4& v, int e) {
 }
 template <>
 __device__ __forceinline__ float vec_elem<float>(const u32x4& v, int e) {
-    unsigned w = v[e];
-    return __builtin_bit_cast(float, w);
+    return __builtin_bit_cast(float, v[e]);
 }
 
 // Position of key k (0..63) of a tile inside the transposed V tile.
@@ -61,14 +63,16 @@ __device__ __forceinline__ int vperm(int k) {
     return c * 32 + ((kk & 15) >> 2) * 8 + (kk >> 4) * 4 + (kk & 3);
 }
 
-template <typename T, int DH, int WQ>
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+template <typename T, int DH, int QB, bool VT, bool PRESCALED>
 __global__ __launch_bounds__(256) void attn_kernel(AttnArgs<T> a) {
     constexpr int VEC = 16 / sizeof(T);
     constexpr int LDK = DH + 16 / sizeof(T);   // K tile row stride
     constexpr int LDV = KT + 16 / sizeof(T);   // V^T tile row stride
-    constexpr int CHUNKS = KT * DH / VEC;      // 16-byte chunks per K (or V) tile
-    constexpr int LOADS = CHUNKS / 256;
-    constexpr int QB = WQ / 16, DC = DH / 32, DB = DH / 16;
+    constexpr int LOADS = KT * DH / VEC / 256; // 16-byte chunks per thread per K (or V) tile
+    constexpr int DC = DH / 32, DB = DH / 16;
+    constexpr int WQ = 16 * QB;
     static_assert(LOADS >= 1, "tile");
 
     __shared__ __attribute__((aligned(16))) T Ks[2][KT * LDK];
@@ -79,7 +83,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs<T> a) {
     const int b = blockIdx.z, h = blockIdx.y;
     const int q0 = blockIdx.x * (4 * WQ) + wave * WQ;
     const int fr = lane & 15, g = lane >> 4;
-    const float sl2 = a.scale * kLog2e;
+    const float sl2 = PRESCALED ? 1.0f : a.scale * kLog2e;
 
     // Q^T fragments (B operand): query q0 + 16*qb + fr, dims 32*dc + 8*g .. +8.
     Frag<T> qf[QB][DC];
@@ -98,14 +102,18 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs<T> a) {
     const int* tile_on = a.tile_on1 ? a.tile_on1 + b * ((a.stride1 + KT - 1) / KT) : nullptr;
     const size_t bh = (size_t)b * a.H + h;
     const T* K0b = a.K0 + bh * a.stride0 * DH;
-    const T* V0b = a.V0 + bh * a.stride0 * DH;
     const T* K1b = a.K1 ? a.K1 + bh * a.stride1 * DH : nullptr;
-    const T* V1b = a.V1 ? a.V1 + bh * a.stride1 * DH : nullptr;
+    // V: [key][d] rows (VT = false) or V^T rows of vstride permuted keys (VT = true).
+    const T* V0b = a.V0 + bh * (VT ? (size_t)DH * a.vstride0 : (size_t)a.stride0 * DH);
+    const T* V1b = a.V1 ? a.V1 + bh * (VT ? (size_t)DH * a.vstride1 : (size_t)a.stride1 * DH) : nullptr;
     const float* M0b = a.mask0 ? a.mask0 + (size_t)b * a.len0 : nullptr;
     const float* M1b = a.mask1 ? a.mask1 + (size_t)b * a.stride1 : nullptr;
-    // Chunk c = tid + 256 i of a tile: key c / (DH/VEC), elements (c % (DH/VEC)) * VEC..
+    // K chunk c = tid + 256 i: key c / (DH/VEC), elements (c % (DH/VEC)) * VEC..
     const int ckey = tid / (DH / VEC), ccol = (tid % (DH / VEC)) * VEC;
     constexpr int KEY_STEP = 256 / (DH / VEC);
+    // V^T chunk c = tid + 256 i: dim c / (KT/VEC), keys (c % (KT/VEC)) * VEC..
+    const int vdim = tid / (KT / VEC), vkey = (tid % (KT / VEC)) * VEC;
+    constexpr int DIM_STEP = 256 / (KT / VEC);
 
     u32x4 rk[LOADS], rv[LOADS];
     float rm = 0.f;
@@ -126,7 +134,13 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs<T> a) {
             int key = key0 + ckey + KEY_STEP * i;                                          \
             key = key < len ? key : len - 1;                                               \
             rk[i] = *reinterpret_cast<const u32x4*>(kb + (size_t)key * DH + ccol);         \
-            rv[i] = *reinterpret_cast<const u32x4*>(vb + (size_t)key * DH + ccol);         \
+            if constexpr (VT) {                                                            \
+                const size_t vs = s0 ? a.vstride0 : a.vstride1;                            \
+                rv[i] = *reinterpret_cast<const u32x4*>(                                   \
+                    vb + (size_t)(vdim + DIM_STEP * i) * vs + key0 + vkey);                \
+            } else {                                                                       \
+                rv[i] = *reinterpret_cast<const u32x4*>(vb + (size_t)key * DH + ccol);     \
+            }                                                                              \
         }                                                                                  \
         if (tid < KT) {                                                                    \
             int key = key0 + tid;                                                          \
@@ -139,9 +153,14 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs<T> a) {
         _Pragma("unroll") for (int i = 0; i < LOADS; i++) {                                \
             int key = ckey + KEY_STEP * i;                                                 \
             *reinterpret_cast<u32x4*>(&Ks[buf][key * LDK + ccol]) = rk[i];                 \
-            int pk = vperm(key);                                                           \
-            _Pragma("unroll") for (int e = 0; e < VEC; e++) Vt[buf][(ccol + e) * LDV + pk] = \
-                vec_elem<T>(rv[i], e);                                                     \
+            if constexpr (VT) {                                                            \
+                *reinterpret_cast<u32x4*>(&Vt[buf][(vdim + DIM_STEP * i) * LDV + vkey]) =  \
+                    rv[i];                                                                 \
+            } else {                                                                       \
+                int pk = vperm(key);                                                       \
+                _Pragma("unroll") for (int e = 0; e < VEC; e++)                            \
+                    Vt[buf][(ccol + e) * LDV + pk] = vec_elem<T>(rv[i], e);                \
+            }                                                                              \
         }                                                                                  \
         if (tid < KT) Ms[buf][tid] = rm;                                                   \
     } while (0)
@@ -183,12 +202,16 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs<T> a) {
                 for (int qb = 0; qb < QB; qb++) mma16(s[kb][qb], kf, qf[qb][dc]);
             }
         }
-        // Online softmax over this tile (log2 domain), per query column.
+        // Online softmax over this tile (log2 domain), per query column.  Latent self
+        // tiles are never masked except past the segment end (last tile only).
+        const bool masked = t >= nt0 || (t + 1) * KT > a.len0 || M0b != nullptr;
         float bias[4][4];
+        if (masked) {
 #pragma unroll
-        for (int kb = 0; kb < 4; kb++)
+            for (int kb = 0; kb < 4; kb++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) bias[kb][i] = Ms[buf][kb * 16 + 4 * g + i];
+                for (int i = 0; i < 4; i++) bias[kb][i] = Ms[buf][kb * 16 + 4 * g + i];
+        }
 #pragma unroll
         for (int qb = 0; qb < QB; qb++) {
             float mx = -INFINITY;
@@ -196,7 +219,8 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs<T> a) {
             for (int kb = 0; kb < 4; kb++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    float v = s[kb][qb][i] * sl2 + bias[kb][i];
+                    float v = PRESCALED ? s[kb][qb][i] : s[kb][qb][i] * sl2;
+                    if (masked) v += bias[kb][i];
                     s[kb][qb][i] = v;
                     mx = fmaxf(mx, v);
                 }
@@ -204,13 +228,13 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs<T> a) {
             mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
             float m_new = fmaxf(m_run[qb], mx);
             float m_use = m_new == -INFINITY ? 0.f : m_new;
-            float corr = exp2f(m_run[qb] - m_use);
+            float corr = fast_exp2(m_run[qb] - m_use);
             float psum = 0.f;
 #pragma unroll
             for (int kb = 0; kb < 4; kb++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    float p = exp2f(s[kb][qb][i] - m_use);
+                    float p = fast_exp2(s[kb][qb][i] - m_use);
                     s[kb][qb][i] = p;
                     psum += p;
                 }
@@ -242,7 +266,6 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs<T> a) {
         buf ^= 1;
         t = tn;
     }
-
 #undef ATTN_NEXT
 #undef ATTN_GLOAD
 #undef ATTN_LSTORE
@@ -275,15 +298,30 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs<T> a) {
     }
 }
 
+template <typename T, int DH, bool VT, bool PRE>
+int launch_q(const AttnArgs<T>& a, int qb, hipStream_t st) {
+    int wq = 16 * qb;
+    dim3 grid((a.Sq + 4 * wq - 1) / (4 * wq), a.H, a.B);
+    if (qb == 1)
+        attn_kernel<T, DH, 1, VT, PRE><<<grid, 256, 0, st>>>(a);
+    else
+        attn_kernel<T, DH, 2, VT, PRE><<<grid, 256, 0, st>>>(a);
+    return 0;
+}
+
 }  // namespace
 
+// 32 queries per wavefront (better K/V reuse) when that still gives >= 2 workgroups per
+// CU of the 256-CU chip; 16 otherwise.
 template <typename T, int DH>
 int launch_attention(const AttnArgs<T>& a, hipStream_t st) {
-    constexpr int WQ = 32;
     if (a.Sq <= 0 || a.len0 <= 0) return -1;
-    dim3 grid((a.Sq + 4 * WQ - 1) / (4 * WQ), a.H, a.B);
-    attn_kernel<T, DH, WQ><<<grid, 256, 0, st>>>(a);
-    return 0;
+    if (a.v_transposed && ((a.vstride0 % KT) || (a.K1 && (a.vstride1 % KT)))) return -1;
+    long wgs32 = (long)((a.Sq + 127) / 128) * a.H * a.B;
+    int qb = wgs32 >= 512 ? 2 : 1;
+    if (a.v_transposed)
+        return a.prescaled ? launch_q<T, DH, true, true>(a, qb, st) : launch_q<T, DH, true, false>(a, qb, st);
+    return a.prescaled ? launch_q<T, DH, false, true>(a, qb, st) : launch_q<T, DH, false, false>(a, qb, st);
 }
 
 template int launch_attention<bf16, 64>(const AttnArgs<bf16>&, hipStream_t);

@@ -147,47 +147,70 @@ __global__ __launch_bounds__(256) void inproj_norm_kernel(
     }
 }
 
-// Output head: one wavefront per latent frame s handles every batch row of that frame,
-// so the Joint-CFG combine of rows (2u, 2u+1) and the Euler update happen in registers.
-// v[b, s, p] = sum_d (x[b,s,d] / rms * w[d]) * W_out[d, p] + b_out[p]   (norm.rs:25-39,
-// dit/model.rs:391-392); P <= 64 outputs, lane p owns output p after an LDS reduction.
+// Output head: one wavefront per latent frame s handles every batch row of that frame, two
+// rows at a time, so the Joint-CFG combine of rows (2u, 2u+1) and the Euler update happen
+// in registers.  v[b,s,p] = (sum_d x[b,s,d] * W'[p,d]) / rms(x[b,s,:]) + b_out[p] with
+// W' = out_norm.weight (.) W_out^T folded at ingest — the same product as
+// out_proj(out_norm(x)) (norm.rs:25-39, dit/model.rs:391-392).  Each lane accumulates its
+// D/64 columns for all PT outputs in registers; the cross-lane sums go through a padded
+// [row][p][65] LDS tile (conflict-free writes and reads).
+template <int PT>
 __global__ __launch_bounds__(64) void final_kernel(FinalArgs a) {
-    extern __shared__ float red[];  // [64 lanes][P]
-    int s = blockIdx.x, lane = threadIdx.x;
-    int D = a.D, P = a.P;
-    int step = a.step ? *a.step : 0;
-    float dt = 0.f, vc_keep = 0.f;
+    __shared__ float red[2][PT][65];
+    const int s = blockIdx.x, lane = threadIdx.x;
+    const int D = a.D, P = a.P;
+    const int step = a.step ? *a.step : 0;
+    float dt = 0.f;
     int cfg_on = 0;
     if (a.mode == 1) {
         dt = a.t_sched[step + 1] - a.t_sched[step];
         cfg_on = a.cfg_on[step];
     }
-    for (int b = 0; b < a.B; b++) {
-        const float* xr = a.x + ((size_t)b * a.S + s) * D;
-        float ss = 0.f;
-        for (int d = lane; d < D; d += 64) ss += xr[d] * xr[d];
-        ss = wave_sum(ss);
-        float rms = sqrtf(ss / (float)D + a.eps);
-        for (int p = 0; p < P; p++) red[lane * P + p] = 0.f;
+    for (int b0 = 0; b0 < a.B; b0 += 2) {
+        const bool two = b0 + 1 < a.B;
+        const float* x0 = a.x + ((size_t)b0 * a.S + s) * D;
+        const float* x1 = a.x + ((size_t)(two ? b0 + 1 : b0) * a.S + s) * D;
+        float part0[PT], part1[PT];
+#pragma unroll
+        for (int p = 0; p < PT; p++) { part0[p] = 0.f; part1[p] = 0.f; }
+        float ss0 = 0.f, ss1 = 0.f;
         for (int d = lane; d < D; d += 64) {
-            float xn = xr[d] / rms * a.norm_w[d];
-            for (int p = 0; p < P; p++) red[lane * P + p] += xn * a.out_wT[(size_t)p * D + d];
+            float u0 = x0[d], u1 = x1[d];
+            ss0 += u0 * u0;
+            ss1 += u1 * u1;
+#pragma unroll
+            for (int p = 0; p < PT; p++) {
+                float w = p < P ? a.out_wT[(size_t)p * D + d] : 0.f;
+                part0[p] += u0 * w;
+                part1[p] += u1 * w;
+            }
+        }
+        ss0 = wave_sum(ss0);
+        ss1 = wave_sum(ss1);
+#pragma unroll
+        for (int p = 0; p < PT; p++) {
+            red[0][p][lane] = part0[p];
+            red[1][p][lane] = part1[p];
         }
         __syncthreads();
-        float v = 0.f;
+        float v0 = 0.f, v1 = 0.f;
         if (lane < P) {
-            v = a.out_b[lane];
-            for (int l = 0; l < 64; l++) v += red[l * P + lane];
+            for (int l = 0; l < 64; l++) {
+                v0 += red[0][lane][l];
+                v1 += red[1][lane][l];
+            }
+            v0 = v0 / sqrtf(ss0 / (float)D + a.eps) + a.out_b[lane];
+            v1 = v1 / sqrtf(ss1 / (float)D + a.eps) + a.out_b[lane];
         }
         __syncthreads();
+        if (lane >= P) continue;
         if (a.mode == 0) {
-            if (lane < P) a.v_out[((size_t)b * a.S + s) * P + lane] = v;
-        } else if ((b & 1) == 0) {
-            vc_keep = v;  // conditioned row of utterance b/2
-        } else if (lane < P) {
-            // euler_sampler.rs:467 (v_c + (v_c - v_u) * s) and :714 (x += v * dt)
-            float vv = cfg_on ? vc_keep + (vc_keep - v) * a.scale : vc_keep;
-            float* xt = a.xt + ((size_t)(b / 2) * a.S + s) * P + lane;
+            a.v_out[((size_t)b0 * a.S + s) * P + lane] = v0;
+            if (two) a.v_out[((size_t)(b0 + 1) * a.S + s) * P + lane] = v1;
+        } else {
+            // euler_sampler.rs:467 (v_c + (v_c - v_u) * scale) and :714 (x += v * dt)
+            float vv = cfg_on ? v0 + (v0 - v1) * a.scale : v0;
+            float* xt = a.xt + ((size_t)(b0 / 2) * a.S + s) * P + lane;
             *xt = *xt + vv * dt;
         }
     }
@@ -259,7 +282,10 @@ template void launch_inproj_norm<bf16>(const float*, int, const float*, const fl
                                        bf16*, int, int, int, int, float, ModTable, hipStream_t);
 
 void launch_final(const FinalArgs& a, hipStream_t st) {
-    final_kernel<<<a.S, 64, sizeof(float) * 64 * a.P, st>>>(a);
+    if (a.P <= 8) final_kernel<8><<<a.S, 64, 0, st>>>(a);
+    else if (a.P <= 16) final_kernel<16><<<a.S, 64, 0, st>>>(a);
+    else if (a.P <= 32) final_kernel<32><<<a.S, 64, 0, st>>>(a);
+    else final_kernel<64><<<a.S, 64, 0, st>>>(a);
 }
 
 void launch_step_advance(int* step, hipStream_t st) { step_advance_kernel<<<1, 64, 0, st>>>(step); }
