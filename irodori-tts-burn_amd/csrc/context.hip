@@ -86,6 +86,7 @@ struct LayerBufs {
     void* ctx_v = nullptr;      // V^T [rows, H, Dh, Tp] (Tp = max_ctx rounded up to 64), keys permuted
     float* ctx_mask = nullptr;  // [rows, max_ctx]
     int* tile_on = nullptr;     // [rows, ceil(max_ctx / 64)]
+    unsigned long long* tile_bits = nullptr;  // [rows, ceil(max_ctx / 64)], bit k: key 64 t + k valid
     bool loaded = false;
     std::vector<char> row_set;
 };
@@ -341,6 +342,7 @@ int enqueue_layer(irodori_ctx* c, int l, int B, int S, const ModTable& mt, bool 
         aa.vstride1 = (g.max_ctx + 63) / 64 * 64;
         aa.mask1 = lb.ctx_mask;
         aa.tile_on1 = lb.tile_on;
+        aa.bits1 = lb.tile_bits;
     }
     aa.B = B;
     aa.H = H;
@@ -584,6 +586,7 @@ int irodori_ctx_create(int device, const irodori_dit_config* cfg, irodori_ctx** 
         IRO_HIP_CHECK(hipMemsetAsync(lb.ctx_v, 0, es * (size_t)R * H * Dh * Tp, c->stream));
         IRO_TRY(dalloc(c.get(), &lb.ctx_mask, sizeof(float) * (size_t)R * T));
         IRO_TRY(dalloc(c.get(), &lb.tile_on, sizeof(int) * (size_t)R * ntl));
+        IRO_TRY(dalloc(c.get(), &lb.tile_bits, sizeof(unsigned long long) * (size_t)R * ntl));
         lb.row_set.assign(R, 0);
     }
     IRO_TRY(dalloc(c.get(), &c->cond_w0, sizeof(float) * (size_t)g.timestep_embed_dim * D));
@@ -752,12 +755,17 @@ int irodori_set_ctx_kv(irodori_ctx* c, int layer, int row, int t_ctx, const floa
         std::vector<float> m(T, 0.f);
         int ntl = (T + 63) / 64;
         std::vector<int> on(ntl, 0);
+        std::vector<unsigned long long> bits(ntl, 0ull);
         for (int j = 0; j < t_ctx; j++) {
             m[j] = mask[j] ? 1.f : 0.f;
-            if (mask[j]) on[j / 64] = 1;
+            if (mask[j]) {
+                on[j / 64] = 1;
+                bits[j / 64] |= 1ull << (j % 64);
+            }
         }
         IRO_TRY(upload(c, lb.ctx_mask + (size_t)row * T, m.data(), sizeof(float) * T));
         IRO_TRY(upload(c, lb.tile_on + (size_t)row * ntl, on.data(), sizeof(int) * ntl));
+        IRO_TRY(upload(c, lb.tile_bits + (size_t)row * ntl, bits.data(), sizeof(unsigned long long) * ntl));
         IRO_HIP_CHECK(hipStreamSynchronize(c->stream));
     }
     if (c->t_ctx != t_ctx) {
@@ -985,7 +993,7 @@ int irodori_profile_layer(irodori_ctx* c, int B, int S, int iters, irodori_kerne
                     if (c->t_ctx > 0) {
                         aa.K1 = static_cast<const T*>(lb.ctx_k); aa.V1 = static_cast<const T*>(lb.ctx_v);
                         aa.len1 = c->t_ctx; aa.stride1 = g.max_ctx; aa.vstride1 = (g.max_ctx + 63) / 64 * 64;
-                        aa.mask1 = lb.ctx_mask; aa.tile_on1 = lb.tile_on;
+                        aa.mask1 = lb.ctx_mask; aa.tile_on1 = lb.tile_on; aa.bits1 = lb.tile_bits;
                     }
                     aa.B = B; aa.H = H; aa.Sq = S; aa.scale = 1.0f / sqrtf((float)g.head_dim);
                     aa.out_mode = 0; aa.G = static_cast<const T*>(c->gate); aa.O = static_cast<T*>(c->o);

@@ -127,6 +127,8 @@ struct AttnArgs {
     int len1, stride1;
     const float* mask1;   // optional [B, stride1]; value < 0.5 = masked out
     const int* tile_on1;  // [B, ceil(stride1/64)] nonzero if the 64-key tile has a valid key
+    // [B, ceil(stride1/64)]: bit k of tile t set iff key 64 t + k is valid (launch_attention32)
+    const unsigned long long* bits1;
     int B, H, Sq;
     float scale;
     // v_transposed: V0/V1 hold V^T [B, H, Dh, vstride] with keys at vt_pos_f32 (this

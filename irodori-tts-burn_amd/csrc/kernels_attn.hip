@@ -54,7 +54,10 @@ __device__ __forceinline__ bf16 vec_elem<bf16>(const u32x4& v, int e) {
 }
 template <>
 __device__ __forceinline__ float vec_elem<float>(const u32x4& v, int e) {
-    return __builtin_bit_cast(float, v[e]);
+    // Copy the element into a scalar first: bit-casting the vector-element lvalue
+    // directly reads element 0.
+    unsigned w = v[e];
+    return __builtin_bit_cast(float, w);
 }
 
 // Position of key k (0..63) of a tile inside the transposed V tile.

@@ -31,10 +31,6 @@ typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 constexpr int KT = 64;
 constexpr int TILE_BYTES = KT * 128;  // 64 rows x 128 bytes (bf16 Dh = 64)
 
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
 __device__ __forceinline__ void raw_barrier() { asm volatile("s_barrier" ::: "memory"); }
 __device__ __forceinline__ void load_lds16(const void* g, void* lds) {
     __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
@@ -45,51 +41,74 @@ __device__ __forceinline__ bf16x8 frag(const unsigned char* tile, int r, int chu
 }
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-template <int QB, int KVS>
-__global__ __launch_bounds__(64 * QB * KVS) void attn32_kernel(AttnArgs<bf16> a) {
+// Tile list of one (row, head): entry i < nact of the list is held by lane i as the tile
+// index and its 64-bit key-validity mask.  Latent tiles are valid up to len0; context
+// tiles carry the host-computed bits of the row and tiles without a valid key are dropped.
+struct TileList {
+    int t, lo, hi;  // per lane
+    int nact;       // wave-uniform
+};
+
+__device__ __forceinline__ TileList build_tile_list(const AttnArgs<bf16>& a, int b, int lane, int nt0, int nt1) {
+    unsigned long long bits = 0ull;
+    if (lane < nt0) {
+        const int rem = a.len0 & (KT - 1);
+        bits = (lane == nt0 - 1 && rem) ? ((1ull << rem) - 1ull) : ~0ull;
+    } else if (lane < nt0 + nt1) {
+        bits = a.bits1[(size_t)b * ((a.stride1 + KT - 1) / KT) + (lane - nt0)];
+    }
+    const bool on = bits != 0ull;
+    const unsigned long long act = __ballot(on);
+    TileList tl;
+    tl.nact = __popcll(act);
+    const int below = __popcll(act & ((1ull << lane) - 1ull));
+    // Active lanes go to their rank; the others to distinct slots past the active ones.
+    const int dest = 4 * (on ? below : tl.nact + (lane - below));
+    tl.t = __builtin_amdgcn_ds_permute(dest, lane);
+    tl.lo = __builtin_amdgcn_ds_permute(dest, (int)(unsigned)bits);
+    tl.hi = __builtin_amdgcn_ds_permute(dest, (int)(unsigned)(bits >> 32));
+    return tl;
+}
+
+// QB query blocks of 32 x KVS key parities = QB*KVS wavefronts per workgroup, ST-stage
+// HBM -> LDS pipeline.  Workgroup id -> (query block, head, row) with the query block
+// fastest and the XCD-aware remap on top, so each XCD keeps whole (row, head) K/V sets
+// in its L2.
+template <int QB, int KVS, int ST>
+__global__ __launch_bounds__(64 * QB * KVS) void attn32_kernel(AttnArgs<bf16> a, int nqb) {
     constexpr int NW = QB * KVS;
     constexpr int STAGE_BYTES = KVS * 2 * TILE_BYTES;
     constexpr int LPW = KVS * 2 * 8 / NW;  // load instructions per wave per stage
     static_assert(LPW * NW == KVS * 2 * 8, "tiles must split over the waves");
+    static_assert((KVS - 1) * QB * 34 * 64 * 4 <= ST * STAGE_BYTES, "merge buffer must fit the stages");
     extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
-    __shared__ int tlist[64];
-    __shared__ int ntl;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int qb = wave % QB, par = wave / QB;
-    const int b = blockIdx.z, hh = blockIdx.y;
-    const int q0 = blockIdx.x * (32 * QB) + 32 * qb;
+    const int pid = xcd_remap(blockIdx.x, gridDim.x);
+    const int qblk = pid % nqb, bhid = pid / nqb;
+    const int hh = bhid % a.H, b = bhid / a.H;
+    const int q0 = qblk * (32 * QB) + 32 * qb;
     const int fr = lane & 31, fh = lane >> 5;
     const size_t bh = (size_t)b * a.H + hh;
 
     const int nt0 = (a.len0 + KT - 1) / KT;
     const int nt1 = a.K1 ? (a.len1 + KT - 1) / KT : 0;
-    const int ntiles = nt0 + nt1;
-    const int* tile_on = a.tile_on1 ? a.tile_on1 + b * ((a.stride1 + KT - 1) / KT) : nullptr;
-    if (wave == 0) {
-        int t = lane;
-        bool act = t < ntiles && (t < nt0 || tile_on == nullptr || tile_on[t - nt0] != 0);
-        unsigned long long bal = __ballot(act);
-        int pos = __popcll(bal & ((1ull << lane) - 1ull));
-        if (act) tlist[pos] = t;
-        if (lane == 0) ntl = __popcll(bal);
-    }
-    __syncthreads();
-    const int nact = ntl;
+    const TileList tl = build_tile_list(a, b, lane, nt0, nt1);
+    const int nact = tl.nact;
     const int niter = (nact + KVS - 1) / KVS;
 
     const bf16* K0b = a.K0 + bh * a.stride0 * 64;
     const bf16* K1b = a.K1 ? a.K1 + bh * a.stride1 * 64 : nullptr;
     const bf16* V0b = a.V0 + bh * 64 * (size_t)a.vstride0;
     const bf16* V1b = a.V1 ? a.V1 + bh * 64 * (size_t)a.vstride1 : nullptr;
-    const float* M0b = a.mask0 ? a.mask0 + (size_t)b * a.len0 : nullptr;
-    const float* M1b = a.mask1 ? a.mask1 + (size_t)b * a.stride1 : nullptr;
 
     // Issue the loads of iteration j into stage buffer sb: tile list entries j*KVS + p
-    // (clamped, so every wave always issues LPW loads per stage and the vmcnt accounting
-    // holds).  Instruction ii of this wave: global index gi = wave*LPW + ii -> tile slot
-    // gi / 8 = 2 p + kind (kind 0 = K rows = keys, kind 1 = V^T rows = dims), rows
-    // 8 (gi % 8) .. +7, lane -> row + lane / 8, physical chunk lane % 8.
+    // (clamped to the last entry, so every wave issues LPW loads per stage).  Instruction
+    // ii of this wave: gi = wave*LPW + ii -> tile slot gi / 8 = 2 p + kind (kind 0 = K
+    // rows = keys, kind 1 = V^T rows = dims), rows 8 (gi % 8) .. +7, lane -> row
+    // + lane / 8, physical chunk lane % 8.  Everything but the lane part is wave-uniform.
 #define ATT_ISSUE(j_, sb_)                                                                    \
     do {                                                                                      \
         _Pragma("unroll") for (int ii = 0; ii < LPW; ii++) {                                  \
@@ -97,7 +116,7 @@ __global__ __launch_bounds__(64 * QB * KVS) void attn32_kernel(AttnArgs<bf16> a)
             const int p = gi / 16, kind = (gi / 8) & 1;                                       \
             int li = (j_) * KVS + p;                                                          \
             li = li < nact ? li : nact - 1;                                                   \
-            const int t = tlist[li];                                                          \
+            const int t = __builtin_amdgcn_readlane(tl.t, li);                                \
             const bool s0 = t < nt0;                                                          \
             const int key0 = s0 ? t * KT : (t - nt0) * KT;                                    \
             const int r = (gi % 8) * 8 + lane / 8;                                            \
@@ -132,16 +151,24 @@ __global__ __launch_bounds__(64 * QB * KVS) void attn32_kernel(AttnArgs<bf16> a)
         for (int e = 0; e < 16; e++) o[db][e] = 0.f;
     float m_run = -INFINITY, l_run = 0.f;
 
-    if (niter > 0) ATT_ISSUE(0, 0);
+#pragma unroll
+    for (int st = 0; st < ST - 1; st++)
+        if (st < niter) ATT_ISSUE(st, st);
     for (int j = 0; j < niter; j++) {
-        if (j + 1 < niter) wait_vmcnt<LPW>();
-        else wait_vmcnt<0>();
+        // Stages issued so far: 0 .. min(j + ST - 2, niter - 1); stage j must have landed.
+        const int ahead = min(ST - 2, niter - 1 - j);
+        if constexpr (ST >= 3) {
+            if (ahead >= 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LPW) : "memory");
+            else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        } else {
+            (void)ahead;
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
         raw_barrier();
-        if (j + 1 < niter) ATT_ISSUE(j + 1, (j + 1) & 1);
+        if (j + ST - 1 < niter) ATT_ISSUE(j + ST - 1, (j + ST - 1) % ST);
         const int li = j * KVS + par;
         if (li >= nact) continue;  // this parity has no tile in the last iteration
-        const int t = tlist[li];
-        const unsigned char* kt = smem + (j & 1) * STAGE_BYTES + (2 * par) * TILE_BYTES;
+        const unsigned char* kt = smem + (j % ST) * STAGE_BYTES + (2 * par) * TILE_BYTES;
         const unsigned char* vt = kt + TILE_BYTES;
 
         // S^T for the 64 keys of the tile: two 32-key blocks.
@@ -154,22 +181,18 @@ __global__ __launch_bounds__(64 * QB * KVS) void attn32_kernel(AttnArgs<bf16> a)
             for (int ks = 0; ks < 4; ks++)
                 s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag(kt, 32 * kb + fr, 2 * ks + fh), qf[ks], s[kb], 0, 0, 0);
         }
-        // Mask: context tiles, a masked latent segment, or the partial last latent tile.
-        const bool s0 = t < nt0;
-        const int key0 = s0 ? t * KT : (t - nt0) * KT;
-        const int len = s0 ? a.len0 : a.len1;
-        const float* mk = s0 ? M0b : M1b;
-        if (mk != nullptr || key0 + KT > len) {
+        // Mask: keys 32 kb + 8 g4 + 4 fh + c of this lane, from the tile's validity bits.
+        const unsigned long long vm = ((unsigned long long)(unsigned)__builtin_amdgcn_readlane(tl.hi, li) << 32) |
+                                      (unsigned)__builtin_amdgcn_readlane(tl.lo, li);
+        if (vm != ~0ull) {
 #pragma unroll
             for (int kb = 0; kb < 2; kb++)
 #pragma unroll
                 for (int g4 = 0; g4 < 4; g4++) {
-                    const int k = key0 + 32 * kb + 8 * g4 + 4 * fh;  // keys k .. k+3
+                    const unsigned nib = (unsigned)(vm >> (32 * kb + 8 * g4 + 4 * fh)) & 15u;
 #pragma unroll
-                    for (int c = 0; c < 4; c++) {
-                        bool ok = k + c < len && (mk == nullptr || mk[k + c] >= 0.5f);
-                        if (!ok) s[kb][4 * g4 + c] = -INFINITY;
-                    }
+                    for (int c = 0; c < 4; c++)
+                        if (!((nib >> c) & 1u)) s[kb][4 * g4 + c] = -INFINITY;
                 }
         }
         float mx = -INFINITY;
@@ -204,31 +227,36 @@ __global__ __launch_bounds__(64 * QB * KVS) void attn32_kernel(AttnArgs<bf16> a)
     }
 #undef ATT_ISSUE
 
-    // Merge the KVS parities through LDS (reusing the tile buffers).
-    if (KVS > 1) {
+    // Merge the KVS parities through LDS (reusing the stage buffers; every load has
+    // landed since the last iteration waits for all of them): [parity-1][QB][34][64 lanes].
+    if constexpr (KVS > 1) {
         __syncthreads();
-        float* comb = reinterpret_cast<float*>(smem);  // [QB][64 lanes][34]
-        if (par == 1) {
-            float* c = comb + ((size_t)qb * 64 + lane) * 34;
+        float* comb = reinterpret_cast<float*>(smem);
+        if (par > 0) {
+            float* c = comb + ((size_t)(par - 1) * QB + qb) * 34 * 64 + lane;
 #pragma unroll
             for (int db = 0; db < 2; db++)
 #pragma unroll
-                for (int e = 0; e < 16; e++) c[16 * db + e] = o[db][e];
-            c[32] = m_run;
-            c[33] = l_run;
+                for (int e = 0; e < 16; e++) c[(16 * db + e) * 64] = o[db][e];
+            c[32 * 64] = m_run;
+            c[33 * 64] = l_run;
         }
         __syncthreads();
-        if (par == 1) return;
-        const float* c = comb + ((size_t)qb * 64 + lane) * 34;
-        const float m1 = c[32], l1 = c[33];
-        const float mt = fmaxf(m_run, m1);
-        const float mu = mt == -INFINITY ? 0.f : mt;
-        const float c0 = fast_exp2(m_run - mu), c1 = fast_exp2(m1 - mu);
+        if (par > 0) return;
 #pragma unroll
-        for (int db = 0; db < 2; db++)
+        for (int pp = 1; pp < KVS; pp++) {
+            const float* c = comb + ((size_t)(pp - 1) * QB + qb) * 34 * 64 + lane;
+            const float m1 = c[32 * 64], l1 = c[33 * 64];
+            const float mt = fmaxf(m_run, m1);
+            const float mu = mt == -INFINITY ? 0.f : mt;
+            const float c0 = fast_exp2(m_run - mu), c1 = fast_exp2(m1 - mu);
 #pragma unroll
-            for (int e = 0; e < 16; e++) o[db][e] = o[db][e] * c0 + c[16 * db + e] * c1;
-        l_run = l_run * c0 + l1 * c1;
+            for (int db = 0; db < 2; db++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) o[db][e] = o[db][e] * c0 + c[(16 * db + e) * 64] * c1;
+            l_run = l_run * c0 + l1 * c1;
+            m_run = mt;
+        }
     }
 
     // Normalise, gate, store.  o[db][e] = O[q0 + fr][32 db + 8 (e / 4) + 4 fh + e % 4].
@@ -256,25 +284,30 @@ __global__ __launch_bounds__(64 * QB * KVS) void attn32_kernel(AttnArgs<bf16> a)
         }
 }
 
-}  // namespace
-
-int launch_attention32(const AttnArgs<bf16>& a, hipStream_t st) {
-    constexpr int QB = 2, KVS = 2;
-    if (a.Sq <= 0 || a.len0 <= 0 || !a.v_transposed || !a.prescaled) return -1;
-    if ((a.vstride0 % KT) || (a.K1 && (a.vstride1 % KT))) return -1;
-    const int ntiles = (a.len0 + KT - 1) / KT + (a.K1 ? (a.len1 + KT - 1) / KT : 0);
-    if (ntiles > 64) return -1;  // tile list holds 64 entries (4096 keys)
-    const size_t lds = (size_t)2 * KVS * 2 * TILE_BYTES;
+template <int QB, int KVS, int ST>
+int launch_attn32_cfg(const AttnArgs<bf16>& a, hipStream_t st) {
+    const size_t lds = (size_t)ST * KVS * 2 * TILE_BYTES;
     static bool attr_set = false;
     if (!attr_set) {
-        if (hipFuncSetAttribute((const void*)attn32_kernel<QB, KVS>, hipFuncAttributeMaxDynamicSharedMemorySize,
+        if (hipFuncSetAttribute((const void*)attn32_kernel<QB, KVS, ST>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)lds) != hipSuccess)
             return -2;
         attr_set = true;
     }
-    dim3 grid((a.Sq + 32 * QB - 1) / (32 * QB), a.H, a.B);
-    attn32_kernel<QB, KVS><<<grid, 64 * QB * KVS, lds, st>>>(a);
+    const int nqb = (a.Sq + 32 * QB - 1) / (32 * QB);
+    attn32_kernel<QB, KVS, ST><<<dim3(nqb * a.H * a.B), 64 * QB * KVS, lds, st>>>(a, nqb);
     return 0;
+}
+
+}  // namespace
+
+int launch_attention32(const AttnArgs<bf16>& a, hipStream_t st) {
+    if (a.Sq <= 0 || a.len0 <= 0 || !a.v_transposed || !a.prescaled || a.mask0) return -1;
+    if (a.K1 && !a.bits1) return -1;
+    if ((a.vstride0 % KT) || (a.K1 && (a.vstride1 % KT))) return -1;
+    const int ntiles = (a.len0 + KT - 1) / KT + (a.K1 ? (a.len1 + KT - 1) / KT : 0);
+    if (ntiles > 64) return -1;  // the tile list holds one entry per lane (4096 keys)
+    return launch_attn32_cfg<2, 2, 2>(a, st);
 }
 
 }  // namespace irodori
