@@ -6,18 +6,26 @@
 // Context tiles without a valid key are dropped from the tile list up front.
 //
 // Per tile and wavefront (32 queries):
-//   S^T = K Q^T      8 MFMAs; K tile from LDS (A operand), Q^T in registers (B operand).
-//                    Lane l ends up holding query l%32 and keys 8a + 4(l/32) + c of every
-//                    16-key group, so a query's max / sum reduce over lanes l and l^32.
-//   online softmax   in the log2 domain (Q is pre-scaled by Dh^-1/2 log2 e).
-//   O^T += V^T P^T   8 MFMAs; P^T is the S^T accumulator itself, 8 consecutive values per
+//   S'^T = K Q^T - m  10 MFMAs; K tile from LDS (A operand), Q^T in registers (B operand).
+//                    The running reference m of every query is subtracted by one more
+//                    k16 step per 32-key block: a constant A fragment holding a single 1
+//                    (k = 0) against a B fragment holding -m (bf16) at k = 0.  Lane l
+//                    ends up holding query l%32 and keys 8a + 4(l/32) + c of every 16-key
+//                    group, so a query's max / sum reduce over lanes l and l^32.
+//   online softmax   in the log2 domain (Q is pre-scaled by Dh^-1/2 log2 e), with a lazy
+//                    reference: m (a bf16 value) moves only on the wavefront's first tile
+//                    or when a score exceeds it by more than 2^TAU, so the O / l rescale
+//                    is off the common path and p = exp2(S') <= 2^TAU.
+//   O^T += V^T P^T   8 MFMAs; P^T is the S'^T accumulator itself, 8 consecutive values per
 //                    k16 step, and V^T is stored with bits 2 and 3 of every key index
 //                    swapped so that the matching 8 keys are one 16-byte LDS read.
-// Workgroup: QB query blocks x KVS key parities = 4 wavefronts; tiles are dealt to the
-// parities round-robin and the partial (m, l, O) of the two parities are merged through
-// LDS at the end.  K and V^T tiles move HBM -> LDS with global_load_lds_dwordx4 into
-// unpadded 128-byte rows whose 16-byte chunks are xor-swizzled by (row >> 1) & 7, double
-// buffered, with raw barriers so the next tile's loads stay in flight.
+// Workgroup: QB query blocks x KVS key parities; tiles are dealt to the parities
+// round-robin and the partial (m, l, O) of the parities are merged through LDS at the
+// end.  K and V^T tiles move HBM -> LDS with buffer_load_dwordx4 ... lds (one SGPR
+// resource per tile, so rows past the segment end read as zero and need no clamping)
+// into unpadded 128-byte rows whose 16-byte chunks are xor-swizzled by (row >> 1) & 7.
+// K streams one tile ahead of V so that the score MFMAs of the next tile overlap the
+// softmax of the current one.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -30,16 +38,22 @@ typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 
 constexpr int KT = 64;
 constexpr int TILE_BYTES = KT * 128;  // 64 rows x 128 bytes (bf16 Dh = 64)
+constexpr float TAU = 8.0f;           // lazy-reference slack, log2 units
 
 __device__ __forceinline__ void raw_barrier() { asm volatile("s_barrier" ::: "memory"); }
-__device__ __forceinline__ void load_lds16(const void* g, void* lds) {
-    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, unsigned bytes) {
+    // Raw (stride 0) buffer; dword3 0x00020000 is the gfx9-family data format for raw access.
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ void buf_load_lds16(__amdgpu_buffer_rsrc_t r, unsigned voff, void* lds) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 0);
 }
 __device__ __forceinline__ int swz(int r, int c) { return c ^ ((r >> 1) & 7); }
 __device__ __forceinline__ bf16x8 frag(const unsigned char* tile, int r, int chunk) {
     return *reinterpret_cast<const bf16x8*>(tile + r * 128 + (swz(r, chunk) << 4));
 }
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float bf16_round(float x) { return static_cast<float>(static_cast<bf16>(x)); }
 
 // Tile list of one (row, head): entry i < nact of the list is held by lane i as the tile
 // index and its 64-bit key-validity mask.  Latent tiles are valid up to len0; context
@@ -70,18 +84,40 @@ __device__ __forceinline__ TileList build_tile_list(const AttnArgs<bf16>& a, int
     return tl;
 }
 
-// QB query blocks of 32 x KVS key parities = QB*KVS wavefronts per workgroup, ST-stage
-// HBM -> LDS pipeline.  Workgroup id -> (query block, head, row) with the query block
-// fastest and the XCD-aware remap on top, so each XCD keeps whole (row, head) K/V sets
-// in its L2.
-template <int QB, int KVS, int ST>
+// S'^T of one 64-key tile (two 32-key blocks): the reference step, then 4 k16 steps.
+__device__ __forceinline__ void score_tile(f32x16 (&s)[2], const unsigned char* kt, int fr, int fh,
+                                           const bf16x8 (&qf)[4], bf16x8 ones, bf16x8 qbias) {
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++) {
+        f32x16 z;
+#pragma unroll
+        for (int e = 0; e < 16; e++) z[e] = 0.f;
+        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ones, qbias, z, 0, 0, 0);
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++)
+            s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag(kt, 32 * kb + fr, 2 * ks + fh), qf[ks], s[kb], 0, 0, 0);
+    }
+}
+
+// QB query blocks of 32 x KVS key parities = QB*KVS wavefronts per workgroup.
+// Workgroup id -> (query block, head, row) with the query block fastest and the
+// XCD-aware remap on top, so each XCD keeps whole (row, head) K/V sets in its L2.
+//
+// Software pipeline per wavefront: while the softmax of tile j runs on the VALU, the
+// score MFMAs of tile j + 1 run on the matrix core (interleaved by scheduling groups),
+// then P_j V_j.  K therefore streams one tile ahead of V: at the barrier of iteration j
+// the K tiles of iteration j + 1 and the V tiles of iteration j have landed, and the
+// loads of K_{j+2} / V_{j+1} are issued into the slots freed by iteration j - 1.  LDS:
+// K ring [2][KVS] tiles + V ring [2][KVS] tiles.
+template <int QB, int KVS>
 __global__ __launch_bounds__(64 * QB * KVS) void attn32_kernel(AttnArgs<bf16> a, int nqb) {
     constexpr int NW = QB * KVS;
-    constexpr int STAGE_BYTES = KVS * 2 * TILE_BYTES;
-    constexpr int LPW = KVS * 2 * 8 / NW;  // load instructions per wave per stage
-    static_assert(LPW * NW == KVS * 2 * 8, "tiles must split over the waves");
-    static_assert((KVS - 1) * QB * 34 * 64 * 4 <= ST * STAGE_BYTES, "merge buffer must fit the stages");
+    constexpr int LPK = KVS * 8 / NW;  // load instructions per wave per K (or V) stage
+    static_assert(LPK * NW == KVS * 8, "tiles must split over the waves");
+    static_assert((KVS - 1) * QB * 34 * 64 * 4 <= 4 * KVS * TILE_BYTES, "merge buffer must fit the rings");
     extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
+    unsigned char* kring = smem;                        // [2][KVS][TILE_BYTES]
+    unsigned char* vring = smem + 2 * KVS * TILE_BYTES;  // [2][KVS][TILE_BYTES]
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -104,33 +140,41 @@ __global__ __launch_bounds__(64 * QB * KVS) void attn32_kernel(AttnArgs<bf16> a,
     const bf16* V0b = a.V0 + bh * 64 * (size_t)a.vstride0;
     const bf16* V1b = a.V1 ? a.V1 + bh * 64 * (size_t)a.vstride1 : nullptr;
 
-    // Issue the loads of iteration j into stage buffer sb: tile list entries j*KVS + p
-    // (clamped to the last entry, so every wave issues LPW loads per stage).  Instruction
-    // ii of this wave: gi = wave*LPW + ii -> tile slot gi / 8 = 2 p + kind (kind 0 = K
-    // rows = keys, kind 1 = V^T rows = dims), rows 8 (gi % 8) .. +7, lane -> row
-    // + lane / 8, physical chunk lane % 8.  Everything but the lane part is wave-uniform.
-#define ATT_ISSUE(j_, sb_)                                                                    \
+    // Load instruction ii of this wave within a K (or V) stage: gi = wave*LPK + ii ->
+    // parity tile gi / 8, rows 8 (gi % 8) .. +7; lane -> row + lane / 8, physical chunk
+    // lane % 8.  The lane byte offsets are fixed per ii (and per segment for V^T rows).
+    unsigned voK[LPK], voV0[LPK], voV1[LPK];
+#pragma unroll
+    for (int ii = 0; ii < LPK; ii++) {
+        const int gi = wave * LPK + ii;
+        const int r = (gi % 8) * 8 + lane / 8;
+        const unsigned cb = (unsigned)swz(r, lane % 8) * 16u;
+        voK[ii] = (unsigned)r * 128u + cb;
+        voV0[ii] = (unsigned)r * (unsigned)a.vstride0 * 2u + cb;
+        voV1[ii] = (unsigned)r * (unsigned)a.vstride1 * 2u + cb;
+    }
+
+    // Issue the K (kind 0) or V^T (kind 1) tiles of iteration j into ring slot sl: tile
+    // list entries j*KVS + p, clamped to the last entry so every wave issues LPK loads.
+#define ATT_ISSUE(kind_, j_, sl_)                                                             \
     do {                                                                                      \
-        _Pragma("unroll") for (int ii = 0; ii < LPW; ii++) {                                  \
-            const int gi = wave * LPW + ii;                                                   \
-            const int p = gi / 16, kind = (gi / 8) & 1;                                       \
-            int li = (j_) * KVS + p;                                                          \
+        _Pragma("unroll") for (int ii = 0; ii < LPK; ii++) {                                  \
+            const int gi = wave * LPK + ii;                                                   \
+            int li = (j_) * KVS + gi / 8;                                                     \
             li = li < nact ? li : nact - 1;                                                   \
             const int t = __builtin_amdgcn_readlane(tl.t, li);                                \
             const bool s0 = t < nt0;                                                          \
             const int key0 = s0 ? t * KT : (t - nt0) * KT;                                    \
-            const int r = (gi % 8) * 8 + lane / 8;                                            \
-            const int lc = swz(r, lane % 8);                                                  \
-            const bf16* src;                                                                  \
-            if (kind == 0) {                                                                  \
+            unsigned char* dst = ((kind_) ? vring : kring) + ((sl_) * KVS + gi / 8) * TILE_BYTES + (gi % 8) * 1024; \
+            if ((kind_) == 0) {                                                               \
                 const int len = s0 ? a.len0 : a.len1;                                         \
-                int key = key0 + r;                                                           \
-                key = key < len ? key : len - 1;                                              \
-                src = (s0 ? K0b : K1b) + (size_t)key * 64 + lc * 8;                           \
+                buf_load_lds16(make_rsrc((s0 ? K0b : K1b) + (size_t)key0 * 64, (unsigned)(len - key0) * 128u), \
+                               voK[ii], dst);                                                 \
             } else {                                                                          \
-                src = (s0 ? V0b : V1b) + (size_t)r * (s0 ? a.vstride0 : a.vstride1) + key0 + lc * 8; \
+                const int vs = s0 ? a.vstride0 : a.vstride1;                                  \
+                buf_load_lds16(make_rsrc((s0 ? V0b : V1b) + key0, (unsigned)(64 * vs - key0) * 2u), \
+                               s0 ? voV0[ii] : voV1[ii], dst);                                \
             }                                                                                 \
-            load_lds16(src, smem + (sb_) * STAGE_BYTES + (gi / 8) * TILE_BYTES + (gi % 8) * 1024); \
         }                                                                                     \
     } while (0)
 
@@ -143,57 +187,58 @@ __global__ __launch_bounds__(64 * QB * KVS) void attn32_kernel(AttnArgs<bf16> a,
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) qf[ks] = *reinterpret_cast<const bf16x8*>(qp + 16 * ks);
     }
+    // Reference subtraction fragments: A = 1 at k = 0 for every key row, B = -m at k = 0.
+    bf16x8 ones, qbias;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        ones[e] = static_cast<bf16>(0.f);
+        qbias[e] = static_cast<bf16>(0.f);
+    }
+    if (fh == 0) ones[0] = static_cast<bf16>(1.f);
 
     f32x16 o[2];
 #pragma unroll
     for (int db = 0; db < 2; db++)
 #pragma unroll
         for (int e = 0; e < 16; e++) o[db][e] = 0.f;
-    float m_run = -INFINITY, l_run = 0.f;
+    float m_ref = 0.f, l_run = 0.f;
+    bool first = true;  // wave-uniform: no tile processed yet
 
-#pragma unroll
-    for (int st = 0; st < ST - 1; st++)
-        if (st < niter) ATT_ISSUE(st, st);
+    // Prologue: K_0, V_0, then K_1 in flight; scores of tile 0.
+    ATT_ISSUE(0, 0, 0);
+    ATT_ISSUE(1, 0, 0);
+    if (niter > 1) {
+        ATT_ISSUE(0, 1, 1);
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LPK) : "memory");
+    } else {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    raw_barrier();
+    f32x16 s[2];
+    if (par < nact) score_tile(s, kring + par * TILE_BYTES, fr, fh, qf, ones, qbias);
+
     for (int j = 0; j < niter; j++) {
-        // Stages issued so far: 0 .. min(j + ST - 2, niter - 1); stage j must have landed.
-        const int ahead = min(ST - 2, niter - 1 - j);
-        if constexpr (ST >= 3) {
-            if (ahead >= 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LPW) : "memory");
-            else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        } else {
-            (void)ahead;
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        }
+        // K_{j+1} and V_j have landed once this wave's loads are done and all waves met.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         raw_barrier();
-        if (j + ST - 1 < niter) ATT_ISSUE(j + ST - 1, (j + ST - 1) % ST);
+        if (j + 1 < niter) ATT_ISSUE(1, j + 1, (j + 1) & 1);
+        if (j + 2 < niter) ATT_ISSUE(0, j + 2, j & 1);
         const int li = j * KVS + par;
         if (li >= nact) continue;  // this parity has no tile in the last iteration
-        const unsigned char* kt = smem + (j % ST) * STAGE_BYTES + (2 * par) * TILE_BYTES;
-        const unsigned char* vt = kt + TILE_BYTES;
 
-        // S^T for the 64 keys of the tile: two 32-key blocks.
-        f32x16 s[2];
+        // Mask (partial tiles only): keys 32 kb + 8 g4 + 4 fh + c of this lane.
+        const unsigned vlo = (unsigned)__builtin_amdgcn_readlane(tl.lo, li);
+        const unsigned vhi = (unsigned)__builtin_amdgcn_readlane(tl.hi, li);
+        if ((vlo & vhi) != 0xffffffffu) {
 #pragma unroll
-        for (int kb = 0; kb < 2; kb++) {
+            for (int kb = 0; kb < 2; kb++) {
+                const unsigned w = (kb ? vhi : vlo) >> (4 * fh);
 #pragma unroll
-            for (int e = 0; e < 16; e++) s[kb][e] = 0.f;
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++)
-                s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag(kt, 32 * kb + fr, 2 * ks + fh), qf[ks], s[kb], 0, 0, 0);
-        }
-        // Mask: keys 32 kb + 8 g4 + 4 fh + c of this lane, from the tile's validity bits.
-        const unsigned long long vm = ((unsigned long long)(unsigned)__builtin_amdgcn_readlane(tl.hi, li) << 32) |
-                                      (unsigned)__builtin_amdgcn_readlane(tl.lo, li);
-        if (vm != ~0ull) {
-#pragma unroll
-            for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-                for (int g4 = 0; g4 < 4; g4++) {
-                    const unsigned nib = (unsigned)(vm >> (32 * kb + 8 * g4 + 4 * fh)) & 15u;
+                for (int g4 = 0; g4 < 4; g4++)
 #pragma unroll
                     for (int c = 0; c < 4; c++)
-                        if (!((nib >> c) & 1u)) s[kb][4 * g4 + c] = -INFINITY;
-                }
+                        if (!((w >> (8 * g4 + c)) & 1u)) s[kb][4 * g4 + c] = -INFINITY;
+            }
         }
         float mx = -INFINITY;
 #pragma unroll
@@ -201,31 +246,59 @@ __global__ __launch_bounds__(64 * QB * KVS) void attn32_kernel(AttnArgs<bf16> a,
 #pragma unroll
             for (int e = 0; e < 16; e++) mx = fmaxf(mx, s[kb][e]);
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float m_new = fmaxf(m_run, mx);
-        const float m_use = m_new == -INFINITY ? 0.f : m_new;
-        const float corr = fast_exp2(m_run - m_use);
+        // Move the reference on the first tile or when a score exceeds it by 2^TAU.
+        const bool need = first || mx > TAU;
+        if (__ballot(need)) {
+            const float nref = need ? bf16_round(m_ref + mx) : m_ref;
+            const float delta = nref - m_ref;
+            const float corr = first ? 0.f : fast_exp2(-delta);
+            m_ref = nref;
+#pragma unroll
+            for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) s[kb][e] -= delta;
+#pragma unroll
+            for (int db = 0; db < 2; db++) o[db] *= corr;
+            l_run *= corr;
+            if (fh == 0) qbias[0] = static_cast<bf16>(-m_ref);
+        }
+        first = false;
+
+        // Scores of tile j + 1 on the matrix core, softmax of tile j on the VALU.
+        // (Computed unconditionally to keep one scheduling region; without a next tile the
+        // slot holds stale data and the result is dropped.)
+        f32x16 sn[2];
+        score_tile(sn, kring + (((j + 1) & 1) * KVS + par) * TILE_BYTES, fr, fh, qf, ones, qbias);
         float psum = 0.f;
         bf16x8 pf[4];
 #pragma unroll
         for (int kb = 0; kb < 2; kb++)
 #pragma unroll
             for (int e = 0; e < 16; e++) {
-                float p = fast_exp2(s[kb][e] - m_use);
+                const float p = fast_exp2(s[kb][e]);
                 psum += p;
                 pf[2 * kb + (e >> 3)][e & 7] = static_cast<bf16>(p);
             }
-        l_run = l_run * corr + psum;
-        m_run = m_new;
+        l_run += psum;
+        // 8 K-fragment reads, then each score MFMA followed by a slice of the softmax.
+        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
 #pragma unroll
-        for (int db = 0; db < 2; db++) o[db] *= corr;
+        for (int i = 0; i < 10; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);
+        }
         // O^T += V^T P^T over the 4 16-key groups of the tile.
+        const unsigned char* vt = vring + ((j & 1) * KVS + par) * TILE_BYTES;
 #pragma unroll
         for (int db = 0; db < 2; db++)
 #pragma unroll
             for (int g = 0; g < 4; g++)
                 o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag(vt, 32 * db + fr, 2 * g + fh), pf[g], o[db], 0, 0, 0);
+        s[0] = sn[0];
+        s[1] = sn[1];
     }
 #undef ATT_ISSUE
+    float m_run = first ? -INFINITY : m_ref;
 
     // Merge the KVS parities through LDS (reusing the stage buffers; every load has
     // landed since the last iteration waits for all of them): [parity-1][QB][34][64 lanes].
@@ -284,18 +357,18 @@ __global__ __launch_bounds__(64 * QB * KVS) void attn32_kernel(AttnArgs<bf16> a,
         }
 }
 
-template <int QB, int KVS, int ST>
+template <int QB, int KVS>
 int launch_attn32_cfg(const AttnArgs<bf16>& a, hipStream_t st) {
-    const size_t lds = (size_t)ST * KVS * 2 * TILE_BYTES;
+    const size_t lds = (size_t)4 * KVS * TILE_BYTES;
     static bool attr_set = false;
     if (!attr_set) {
-        if (hipFuncSetAttribute((const void*)attn32_kernel<QB, KVS, ST>, hipFuncAttributeMaxDynamicSharedMemorySize,
+        if (hipFuncSetAttribute((const void*)attn32_kernel<QB, KVS>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)lds) != hipSuccess)
             return -2;
         attr_set = true;
     }
     const int nqb = (a.Sq + 32 * QB - 1) / (32 * QB);
-    attn32_kernel<QB, KVS, ST><<<dim3(nqb * a.H * a.B), 64 * QB * KVS, lds, st>>>(a, nqb);
+    attn32_kernel<QB, KVS><<<dim3(nqb * a.H * a.B), 64 * QB * KVS, lds, st>>>(a, nqb);
     return 0;
 }
 
@@ -307,7 +380,7 @@ int launch_attention32(const AttnArgs<bf16>& a, hipStream_t st) {
     if ((a.vstride0 % KT) || (a.K1 && (a.vstride1 % KT))) return -1;
     const int ntiles = (a.len0 + KT - 1) / KT + (a.K1 ? (a.len1 + KT - 1) / KT : 0);
     if (ntiles > 64) return -1;  // the tile list holds one entry per lane (4096 keys)
-    return launch_attn32_cfg<2, 2, 2>(a, st);
+    return launch_attn32_cfg<4, 2>(a, st);
 }
 
 }  // namespace irodori
