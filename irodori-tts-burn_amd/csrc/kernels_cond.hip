@@ -22,8 +22,10 @@ __global__ void timestep_embedding_kernel(const float* __restrict__ t, int nvec,
     out[(size_t)v * t_dim + half + i] = sinf(a);
 }
 
-constexpr int kVecChunk = 32;  // vectors accumulated per thread per pass
-constexpr int kKTile = 64;
+constexpr int kVecChunk = 32;  // vectors per workgroup (blockIdx.z chunks the rest)
+constexpr int kCols = 64;      // output columns per workgroup
+constexpr int kKGroups = 4;    // k-slices per workgroup, reduced through LDS
+constexpr int kKTile = 256;    // staged X columns per pass
 
 __device__ __forceinline__ float apply_act(float v, int act) {
     if (act == 1) return silu_f(v);
@@ -32,45 +34,73 @@ __device__ __forceinline__ float apply_act(float v, int act) {
 }
 
 // Y[v, n] = act_out(act_in(X[v, :]) @ W[:, n] + bias[n] + R[v, n]) for every job
-// (blockIdx.y) and column block (blockIdx.x).  Each thread owns one column n and
-// accumulates up to kVecChunk vectors, so W (the dominant traffic) is streamed once per
-// kVecChunk vectors with coalesced row reads; the X tile is staged in LDS.
+// (blockIdx.y), 64-column block (blockIdx.x) and 32-vector chunk (blockIdx.z).  Thread
+// (kg, c) owns column n = 64 blockIdx.x + c and the k-slice k = kg (mod 4), accumulating
+// all vectors of the chunk in registers; a wavefront reads one 256-byte row segment of
+// W per k, so W is streamed once per vector chunk.  The X tile (activation applied) is
+// staged in LDS and the 4 k-slices are summed through LDS at the end.
 __global__ __launch_bounds__(256) void vec_linear_kernel(const VecLinJob* __restrict__ jobs,
                                                          int nvec) {
-    __shared__ float xs[kVecChunk][kKTile];
+    __shared__ __attribute__((aligned(16))) float xs[kKTile][kVecChunk];  // transposed: one k = 32 vectors
+    __shared__ float red[kKGroups - 1][kVecChunk][kCols];
     const VecLinJob jb = jobs[blockIdx.y];
-    int n = blockIdx.x * 256 + threadIdx.x;
-    bool active = n < jb.N;
-    for (int v0 = 0; v0 < nvec; v0 += kVecChunk) {
-        int nv = nvec - v0 < kVecChunk ? nvec - v0 : kVecChunk;
-        float acc[kVecChunk];
+    if (blockIdx.x * kCols >= jb.N) return;  // uniform: this job has fewer columns
+    const int c = threadIdx.x % kCols, kg = threadIdx.x / kCols;
+    const int n = blockIdx.x * kCols + c;
+    const bool active = n < jb.N;
+    const int v0 = blockIdx.z * kVecChunk;
+    const int nv = nvec - v0 < kVecChunk ? nvec - v0 : kVecChunk;
+    float acc[kVecChunk];
 #pragma unroll
-        for (int v = 0; v < kVecChunk; v++) acc[v] = 0.f;
-        for (int k0 = 0; k0 < jb.K; k0 += kKTile) {
-            int kt = jb.K - k0 < kKTile ? jb.K - k0 : kKTile;
-            __syncthreads();
-            for (int e = threadIdx.x; e < kVecChunk * kKTile; e += 256) {
-                int v = e / kKTile, k = e % kKTile;
-                float val = 0.f;
-                if (v < nv && k < kt) val = apply_act(jb.X[(size_t)(v0 + v) * jb.ldx + k0 + k], jb.act_in);
-                xs[v][k] = val;
-            }
-            __syncthreads();
-            if (active) {
-                for (int k = 0; k < kt; k++) {
-                    float w = jb.W[(size_t)(k0 + k) * jb.N + n];
+    for (int v = 0; v < kVecChunk; v++) acc[v] = 0.f;
+    for (int k0 = 0; k0 < jb.K; k0 += kKTile) {
+        const int kt = jb.K - k0 < kKTile ? jb.K - k0 : kKTile;
+        __syncthreads();
+        for (int e = threadIdx.x; e < kVecChunk * kKTile; e += 256) {
+            const int v = e % kVecChunk, k = e / kVecChunk;  // conflict-free LDS writes
+            float val = 0.f;
+            if (v < nv && k < kt) val = apply_act(jb.X[(size_t)(v0 + v) * jb.ldx + k0 + k], jb.act_in);
+            xs[k][v] = val;
+        }
+        __syncthreads();
+        if (active) {
+            // 16 W values (k = kg, kg + 4, ...) are loaded together so their latencies
+            // overlap; each k's 32 vector values are 8 broadcast 16-byte LDS reads.
+            for (int kb = 0; kb < kt; kb += 16 * kKGroups) {
+                float wv[16];
 #pragma unroll
-                    for (int v = 0; v < kVecChunk; v++) acc[v] += xs[v][k] * w;
+                for (int i = 0; i < 16; i++) {
+                    const int k = kb + kg + kKGroups * i;
+                    wv[i] = k < kt ? jb.W[(size_t)(k0 + k) * jb.N + n] : 0.f;
+                }
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const int k = kb + kg + kKGroups * i;
+                    if (k >= kt) break;
+                    const float4* xr = reinterpret_cast<const float4*>(&xs[k][0]);
+#pragma unroll
+                    for (int q = 0; q < kVecChunk / 4; q++) {
+                        const float4 xv = xr[q];
+                        acc[4 * q] += xv.x * wv[i];
+                        acc[4 * q + 1] += xv.y * wv[i];
+                        acc[4 * q + 2] += xv.z * wv[i];
+                        acc[4 * q + 3] += xv.w * wv[i];
+                    }
                 }
             }
         }
-        if (active) {
-            for (int v = 0; v < nv; v++) {
-                float y = acc[v];
-                if (jb.bias) y += jb.bias[n];
-                if (jb.R) y += jb.R[(size_t)(v0 + v) * jb.ldr + n];
-                jb.Y[(size_t)(v0 + v) * jb.ldy + n] = apply_act(y, jb.act_out);
-            }
+    }
+    if (kg > 0) {
+#pragma unroll
+        for (int v = 0; v < kVecChunk; v++) red[kg - 1][v][c] = acc[v];
+    }
+    __syncthreads();
+    if (kg == 0 && active) {
+        for (int v = 0; v < nv; v++) {
+            float y = acc[v] + red[0][v][c] + red[1][v][c] + red[2][v][c];
+            if (jb.bias) y += jb.bias[n];
+            if (jb.R) y += jb.R[(size_t)(v0 + v) * jb.ldr + n];
+            jb.Y[(size_t)(v0 + v) * jb.ldy + n] = apply_act(y, jb.act_out);
         }
     }
 }
@@ -83,7 +113,7 @@ void launch_timestep_embedding(const float* t, int nvec, int t_dim, float* out, 
 }
 
 void launch_vec_linear(const VecLinJob* d_jobs, int njobs, int nvec, int max_n, hipStream_t st) {
-    dim3 grid((max_n + 255) / 256, njobs);
+    dim3 grid((max_n + kCols - 1) / kCols, njobs, (nvec + kVecChunk - 1) / kVecChunk);
     vec_linear_kernel<<<grid, 256, 0, st>>>(d_jobs, nvec);
 }
 

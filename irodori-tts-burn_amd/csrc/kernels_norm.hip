@@ -102,63 +102,131 @@ __global__ __launch_bounds__(256) void norm_mod_kernel(const float* __restrict__
     }
 }
 
-// in_proj (x = x_src @ W_in + b_in, dit/model.rs:370) fused with the first adaLN.
+// in_proj (x = x_src @ W_in + b_in, dit/model.rs:370) fused with the first adaLN.  A
+// 256-thread block owns kInRows rows; thread t owns the column quads 4 t + 1024 j (j <
+// NCH) of every row, so each W_in quad is loaded once per block and applied to all its
+// rows (W_in stays in L2 and is streamed M / kInRows times).  The source rows are staged
+// in LDS 64 latent channels at a time; the row RMS reduces over lanes, then over the 4
+// wavefronts through LDS.
+constexpr int kInRows = 8;
+
 template <typename T, int NCH>
 __global__ __launch_bounds__(256) void inproj_norm_kernel(
     const float* __restrict__ x_src, int rows_per_src, const float* __restrict__ in_w,
     const float* __restrict__ in_b, float* __restrict__ x, T* __restrict__ h, int M, int S, int P,
     int D, float eps, ModTable mt) {
-    int row = blockIdx.x * kRowsPerBlock + threadIdx.x / 64, lane = threadIdx.x % 64;
-    if (row >= M) return;
-    int b = row / S, s = row % S;
-    const float* src = x_src + ((size_t)(b / rows_per_src) * S + s) * P;
-    float4 v[NCH];
-    float ss = 0.f;
+    __shared__ float xs[kInRows][64];
+    __shared__ float red[kInRows][4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int row0 = blockIdx.x * kInRows;
+    float4 acc[kInRows][NCH];
 #pragma unroll
     for (int j = 0; j < NCH; j++) {
-        int d = lane * 4 + 256 * j;
-        float4 acc = make_float4(0, 0, 0, 0);
-        if (d < D) {
-            acc = *reinterpret_cast<const float4*>(in_b + d);
-            for (int p = 0; p < P; p++) {
-                float a = src[p];
-                float4 wv = *reinterpret_cast<const float4*>(in_w + (size_t)p * D + d);
-                acc.x += a * wv.x; acc.y += a * wv.y; acc.z += a * wv.z; acc.w += a * wv.w;
-            }
-            *reinterpret_cast<float4*>(x + (size_t)row * D + d) = acc;
-        }
-        v[j] = acc;
-        ss += acc.x * acc.x + acc.y * acc.y + acc.z * acc.z + acc.w * acc.w;
+        const int d = 4 * tid + 1024 * j;
+        const float4 bv = d < D ? *reinterpret_cast<const float4*>(in_b + d) : make_float4(0, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < kInRows; r++) acc[r][j] = bv;
     }
-    ss = wave_sum(ss);
-    float rms = sqrtf(ss / (float)D + eps);
-    const float* base = mod_base(mt, b, 0, 0, D);
-    const float* shift = base;
-    const float* scale = base + D;
+    for (int p0 = 0; p0 < P; p0 += 64) {
+        const int pn = P - p0 < 64 ? P - p0 : 64;
+        __syncthreads();
+        for (int e = tid; e < kInRows * 64; e += 256) {
+            const int r = e / 64, pp = e % 64, row = row0 + r;
+            float v = 0.f;
+            if (row < M && pp < pn) {
+                const int b = row / S, sq = row % S;
+                v = x_src[((size_t)(b / rows_per_src) * S + sq) * P + p0 + pp];
+            }
+            xs[r][pp] = v;
+        }
+        __syncthreads();
+        // 16 W_in quads per column chunk are loaded together so their latencies overlap.
 #pragma unroll
-    for (int j = 0; j < NCH; j++) {
-        int d = lane * 4 + 256 * j;
-        if (d >= D) break;
-        float4 sc = *reinterpret_cast<const float4*>(scale + d);
-        float4 sh = *reinterpret_cast<const float4*>(shift + d);
-        store4<T>(h + (size_t)row * D + d, v[j].x / rms * (1.f + sc.x) + sh.x,
-                  v[j].y / rms * (1.f + sc.y) + sh.y, v[j].z / rms * (1.f + sc.z) + sh.z,
-                  v[j].w / rms * (1.f + sc.w) + sh.w);
+        for (int j = 0; j < NCH; j++) {
+            const int d = 4 * tid + 1024 * j;
+            if (d >= D) break;
+            for (int c0 = 0; c0 < pn; c0 += 16) {
+                float4 wv[16];
+#pragma unroll
+                for (int i = 0; i < 16; i++)
+                    wv[i] = c0 + i < pn ? *reinterpret_cast<const float4*>(in_w + (size_t)(p0 + c0 + i) * D + d)
+                                        : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+#pragma unroll
+                    for (int r = 0; r < kInRows; r++) {
+                        const float a = xs[r][(c0 + i) & 63];
+                        acc[r][j].x += a * wv[i].x;
+                        acc[r][j].y += a * wv[i].y;
+                        acc[r][j].z += a * wv[i].z;
+                        acc[r][j].w += a * wv[i].w;
+                    }
+                }
+            }
+        }
+    }
+    // Store x and reduce the per-row sums of squares.
+#pragma unroll
+    for (int r = 0; r < kInRows; r++) {
+        const int row = row0 + r;
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < NCH; j++) {
+            const int d = 4 * tid + 1024 * j;
+            if (d >= D) break;
+            const float4 v = acc[r][j];
+            if (row < M) *reinterpret_cast<float4*>(x + (size_t)row * D + d) = v;
+            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) red[r][wave] = ss;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kInRows; r++) {
+        const int row = row0 + r;
+        if (row >= M) break;
+        const float rms = sqrtf((red[r][0] + red[r][1] + red[r][2] + red[r][3]) / (float)D + eps);
+        const float* base = mod_base(mt, row / S, 0, 0, D);
+        const float* shift = base;
+        const float* scale = base + D;
+#pragma unroll
+        for (int j = 0; j < NCH; j++) {
+            const int d = 4 * tid + 1024 * j;
+            if (d >= D) break;
+            const float4 sc = *reinterpret_cast<const float4*>(scale + d);
+            const float4 sh = *reinterpret_cast<const float4*>(shift + d);
+            const float4 v = acc[r][j];
+            store4<T>(h + (size_t)row * D + d, v.x / rms * (1.f + sc.x) + sh.x, v.y / rms * (1.f + sc.y) + sh.y,
+                      v.z / rms * (1.f + sc.z) + sh.z, v.w / rms * (1.f + sc.w) + sh.w);
+        }
     }
 }
 
-// Output head: one wavefront per latent frame s handles every batch row of that frame, two
-// rows at a time, so the Joint-CFG combine of rows (2u, 2u+1) and the Euler update happen
-// in registers.  v[b,s,p] = (sum_d x[b,s,d] * W'[p,d]) / rms(x[b,s,:]) + b_out[p] with
-// W' = out_norm.weight (.) W_out^T folded at ingest — the same product as
-// out_proj(out_norm(x)) (norm.rs:25-39, dit/model.rs:391-392).  Each lane accumulates its
-// D/64 columns for all PT outputs in registers; the cross-lane sums go through a padded
-// [row][p][65] LDS tile (conflict-free writes and reads).
+// Output head: one 256-thread block per kFinFrames latent frames handles every batch row
+// of those frames, two rows at a time, so the Joint-CFG combine of rows (2u, 2u+1) and the
+// Euler update happen in the block.  v[b,s,p] = (sum_d x[b,s,d] * W'[p,d]) / rms(x[b,s,:])
+// + b_out[p] with W' = out_norm.weight (.) W_out^T folded at ingest — the same product as
+// out_proj(out_norm(x)) (norm.rs:25-39, dit/model.rs:391-392).  The block's rows are staged
+// in LDS; thread (ks, p) computes output p over the k-slice ks for every staged row
+// (reading its own W' row once per block), and the KS slices are summed through LDS.
+constexpr int kFinFrames = 4;
+
 template <int PT>
-__global__ __launch_bounds__(64) void final_kernel(FinalArgs a) {
-    __shared__ float red[2][PT][65];
-    const int s = blockIdx.x, lane = threadIdx.x;
+__global__ __launch_bounds__(256) void final_kernel(FinalArgs a) {
+    constexpr int KS = 256 / PT;
+    constexpr int R = 2 * kFinFrames;
+    extern __shared__ __attribute__((aligned(16))) float fsm[];
     const int D = a.D, P = a.P;
+    float* xs = fsm;                  // [R][D]
+    float* red = xs + R * D;          // [KS][R][PT]
+    float* vals = red + KS * R * PT;  // [R][PT]
+    float* rinv = vals + R * PT;      // [R]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int p = tid % PT, ks = tid / PT;
+    const int s0 = blockIdx.x * kFinFrames;
+    const int nf = a.S - s0 < kFinFrames ? a.S - s0 : kFinFrames;
+    const int kper = D / KS;
     const int step = a.step ? *a.step : 0;
     float dt = 0.f;
     int cfg_on = 0;
@@ -168,50 +236,73 @@ __global__ __launch_bounds__(64) void final_kernel(FinalArgs a) {
     }
     for (int b0 = 0; b0 < a.B; b0 += 2) {
         const bool two = b0 + 1 < a.B;
-        const float* x0 = a.x + ((size_t)b0 * a.S + s) * D;
-        const float* x1 = a.x + ((size_t)(two ? b0 + 1 : b0) * a.S + s) * D;
-        float part0[PT], part1[PT];
-#pragma unroll
-        for (int p = 0; p < PT; p++) { part0[p] = 0.f; part1[p] = 0.f; }
-        float ss0 = 0.f, ss1 = 0.f;
-        for (int d = lane; d < D; d += 64) {
-            float u0 = x0[d], u1 = x1[d];
-            ss0 += u0 * u0;
-            ss1 += u1 * u1;
-#pragma unroll
-            for (int p = 0; p < PT; p++) {
-                float w = p < P ? a.out_wT[(size_t)p * D + d] : 0.f;
-                part0[p] += u0 * w;
-                part1[p] += u1 * w;
+        __syncthreads();
+        // Stage row r = 2 f + i = x[b0 + i, s0 + f, :] (the second row repeats the first when
+        // B is odd; frames past S are zero).
+        for (int e = tid * 4; e < R * D; e += 1024) {
+            const int r = e / D, d = e % D, f = r >> 1, i = r & 1;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (f < nf) {
+                const int b = (i && two) ? b0 + 1 : b0;
+                v = *reinterpret_cast<const float4*>(a.x + ((size_t)b * a.S + s0 + f) * D + d);
             }
-        }
-        ss0 = wave_sum(ss0);
-        ss1 = wave_sum(ss1);
-#pragma unroll
-        for (int p = 0; p < PT; p++) {
-            red[0][p][lane] = part0[p];
-            red[1][p][lane] = part1[p];
+            *reinterpret_cast<float4*>(xs + r * D + d) = v;
         }
         __syncthreads();
-        float v0 = 0.f, v1 = 0.f;
-        if (lane < P) {
-            for (int l = 0; l < 64; l++) {
-                v0 += red[0][lane][l];
-                v1 += red[1][lane][l];
+        for (int r = wave; r < R; r += 4) {
+            float ss = 0.f;
+            for (int d = lane; d < D; d += 64) ss += xs[r * D + d] * xs[r * D + d];
+            ss = wave_sum(ss);
+            if (lane == 0) rinv[r] = 1.f / sqrtf(ss / (float)D + a.eps);
+        }
+        float acc[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) acc[r] = 0.f;
+        if (p < P) {
+            // 16 W' quads are loaded together so their latencies overlap (kper % 8 == 0).
+            const float* wr = a.out_wT + (size_t)p * D;
+            const int kend = (ks + 1) * kper;
+            for (int k0 = ks * kper; k0 < kend; k0 += 64) {
+                float4 w[16];
+#pragma unroll
+                for (int i = 0; i < 16; i++)
+                    w[i] = k0 + 4 * i < kend ? *reinterpret_cast<const float4*>(wr + k0 + 4 * i)
+                                             : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    if (k0 + 4 * i >= kend) break;
+#pragma unroll
+                    for (int r = 0; r < R; r++) {
+                        const float4 xv = *reinterpret_cast<const float4*>(xs + r * D + k0 + 4 * i);
+                        acc[r] += xv.x * w[i].x + xv.y * w[i].y + xv.z * w[i].z + xv.w * w[i].w;
+                    }
+                }
             }
-            v0 = v0 / sqrtf(ss0 / (float)D + a.eps) + a.out_b[lane];
-            v1 = v1 / sqrtf(ss1 / (float)D + a.eps) + a.out_b[lane];
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) red[(ks * R + r) * PT + p] = acc[r];
+        __syncthreads();
+        if (tid < R * PT) {
+            const int r = tid / PT, pp = tid % PT;
+            float v = 0.f;
+#pragma unroll
+            for (int k2 = 0; k2 < KS; k2++) v += red[(k2 * R + r) * PT + pp];
+            vals[r * PT + pp] = pp < P ? v * rinv[r] + a.out_b[pp] : 0.f;
         }
         __syncthreads();
-        if (lane >= P) continue;
-        if (a.mode == 0) {
-            a.v_out[((size_t)b0 * a.S + s) * P + lane] = v0;
-            if (two) a.v_out[((size_t)(b0 + 1) * a.S + s) * P + lane] = v1;
-        } else {
-            // euler_sampler.rs:467 (v_c + (v_c - v_u) * scale) and :714 (x += v * dt)
-            float vv = cfg_on ? v0 + (v0 - v1) * a.scale : v0;
-            float* xt = a.xt + ((size_t)(b0 / 2) * a.S + s) * P + lane;
-            *xt = *xt + vv * dt;
+        for (int e = tid; e < nf * PT; e += 256) {
+            const int f = e / PT, pp = e % PT, sq = s0 + f;
+            if (pp >= P) continue;
+            const float v0 = vals[(2 * f) * PT + pp], v1 = vals[(2 * f + 1) * PT + pp];
+            if (a.mode == 0) {
+                a.v_out[((size_t)b0 * a.S + sq) * P + pp] = v0;
+                if (two) a.v_out[((size_t)(b0 + 1) * a.S + sq) * P + pp] = v1;
+            } else {
+                // euler_sampler.rs:467 (v_c + (v_c - v_u) * scale) and :714 (x += v * dt)
+                const float vv = cfg_on ? v0 + (v0 - v1) * a.scale : v0;
+                float* xt = a.xt + ((size_t)(b0 / 2) * a.S + sq) * P + pp;
+                *xt = *xt + vv * dt;
+            }
         }
     }
 }
@@ -259,15 +350,14 @@ template <typename T>
 void launch_inproj_norm(const float* x_src, int rows_per_src, const float* in_w,
                         const float* in_b, float* x, T* h, int M, int S, int P, int D, float eps,
                         ModTable mt, hipStream_t st) {
-    int grid = (M + kRowsPerBlock - 1) / kRowsPerBlock;
-    int nch = (D + 255) / 256;
+    int grid = (M + kInRows - 1) / kInRows;
+    int nch = (D + 1023) / 1024;
 #define IRO_INPROJ(N)                                                                      \
     inproj_norm_kernel<T, N><<<grid, 256, 0, st>>>(x_src, rows_per_src, in_w, in_b, x, h, M, \
                                                    S, P, D, eps, mt)
     if (nch <= 1) IRO_INPROJ(1);
     else if (nch <= 2) IRO_INPROJ(2);
-    else if (nch <= 4) IRO_INPROJ(4);
-    else IRO_INPROJ(8);
+    else IRO_INPROJ(4);
 #undef IRO_INPROJ
 }
 
@@ -281,11 +371,23 @@ template void launch_inproj_norm<float>(const float*, int, const float*, const f
 template void launch_inproj_norm<bf16>(const float*, int, const float*, const float*, float*,
                                        bf16*, int, int, int, int, float, ModTable, hipStream_t);
 
+template <int PT>
+static void launch_final_pt(const FinalArgs& a, hipStream_t st) {
+    constexpr int KS = 256 / PT, R = 2 * kFinFrames;
+    const size_t lds = sizeof(float) * ((size_t)R * a.D + (size_t)KS * R * PT + (size_t)R * PT + R);
+    static bool attr_set = false;
+    if (!attr_set) {
+        // Sized for the largest model width the context accepts (D <= 2048).
+        constexpr int kMax = (int)sizeof(float) * (R * 2048 + KS * R * PT + R * PT + R);
+        (void)hipFuncSetAttribute((const void*)final_kernel<PT>, hipFuncAttributeMaxDynamicSharedMemorySize, kMax);
+        attr_set = true;
+    }
+    final_kernel<PT><<<(a.S + kFinFrames - 1) / kFinFrames, 256, lds, st>>>(a);
+}
+
 void launch_final(const FinalArgs& a, hipStream_t st) {
-    if (a.P <= 8) final_kernel<8><<<a.S, 64, 0, st>>>(a);
-    else if (a.P <= 16) final_kernel<16><<<a.S, 64, 0, st>>>(a);
-    else if (a.P <= 32) final_kernel<32><<<a.S, 64, 0, st>>>(a);
-    else final_kernel<64><<<a.S, 64, 0, st>>>(a);
+    if (a.P <= 32) launch_final_pt<32>(a, st);
+    else launch_final_pt<64>(a, st);
 }
 
 void launch_step_advance(int* step, hipStream_t st) { step_advance_kernel<<<1, 64, 0, st>>>(step); }
