@@ -35,6 +35,10 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--profile-iters", type=int, default=50)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run one 1 GiB device-to-device copy (the known-size kernel that "
+                         "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings; 32x the L2, so "
+                         "cache residency does not skew it)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the RF step of one model instance "
@@ -84,6 +88,13 @@ def main():
 
     # Per-kernel device time (HIP events on the context's stream) for one block.
     kt = eng.profile_layer(2 * U, S, args.profile_iters)
+    if args.copy_calibration:
+        src = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     log("kernel us: " + ", ".join("%s=%.1f" % (k, v) for k, v in kt.items()))
     M, D, F, H, Dh = 2 * U * S, cfg.model_dim, cfg.mlp_hidden, cfg.num_heads, cfg.head_dim
     flops = {
