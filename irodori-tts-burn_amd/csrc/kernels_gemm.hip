@@ -38,9 +38,14 @@ __device__ __forceinline__ void wait_vmcnt() {
 // load, including the prefetched slices).
 __device__ __forceinline__ void raw_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-// 16 bytes per lane from global memory straight into LDS (lane i lands at lds + 16 i).
-__device__ __forceinline__ void load_lds16(const void* g, void* lds) {
-    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+// 16 bytes per lane from a raw buffer straight into LDS (lane i lands at lds + 16 i).
+// Offsets at or past the resource's byte count read as zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, unsigned bytes) {
+    // Raw (stride 0) buffer; dword3 0x00020000 is the gfx9-family data format for raw access.
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ void buf_load_lds16(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff, void* lds) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
 }
 
 __device__ __forceinline__ int swz(int r, int c) { return c ^ ((r >> 1) & 7); }
@@ -84,6 +89,20 @@ __device__ __forceinline__ Frag32<float> read_frag<float>(const unsigned char* s
     return f;
 }
 
+// Sum over the 32 lanes of each half-wave (lanes 0-31 and 32-63 separately): DPP
+// rotations within 16-lane rows, then one swizzle across the two rows of each half.
+#define IRO_DPP(v, ctrl)                                                                        \
+    __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, (v)), (ctrl), 0xF, 0xF, false))
+__device__ __forceinline__ float half_wave_sum(float v) {
+    v += IRO_DPP(v, 0x128);  // row_ror:8
+    v += IRO_DPP(v, 0x124);  // row_ror:4
+    v += IRO_DPP(v, 0x4E);   // quad_perm [2,3,0,1]
+    v += IRO_DPP(v, 0xB1);   // quad_perm [1,0,3,2]
+    // swizzle (bit mode, and 0x1f, xor 0x10): lane ^ 16 within each 32-lane group
+    v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+    return v;
+}
+
 __device__ __forceinline__ const float* gate_vec(const ModTable& mt, int b, int layer, int kind,
                                                 int D) {
     int step = mt.step ? *mt.step : 0;
@@ -91,9 +110,9 @@ __device__ __forceinline__ const float* gate_vec(const ModTable& mt, int b, int 
     return mt.tab + ((size_t)vec * mt.layers * 6 + (size_t)layer * 6 + kind * 3 + 2) * D;
 }
 
-template <typename T, int BM, int BN, int STAGES, int EPI>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs<T> a) {
-    constexpr int WAVES_M = 2, WAVES_N = 2, NW = 4;
+template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int EPI>
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T> a) {
+    constexpr int NW = WAVES_M * WAVES_N;
     constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
     constexpr int FM = WM / 32, FN = WN / 32;
     constexpr int ROWS = BM + BN;
@@ -102,11 +121,14 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs<T> a) {
     constexpr int BK = 128 / sizeof(T);  // elements per slice
     constexpr int KS = BK / 16;          // k16 steps per slice
     static_assert(LPW * 8 * NW == ROWS, "rows per slice must split over the waves");
+    static_assert(FM * 32 == WM && FN * 32 == WN, "wave tiles are whole 32x32 blocks");
+    static_assert(BM % 8 == 0, "a load instruction covers A rows or W rows, not both");
     static_assert(EPI != EPI_QKVG || WN == 64, "QKVG epilogue needs one head per wave");
     static_assert(EPI != EPI_SWIGLU || FN % 2 == 0, "SWIGLU epilogue needs column pairs");
 
     extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int tiles_m = (a.M + BM - 1) / BM;
     const int pid = xcd_remap(blockIdx.x, gridDim.x);
     const int tile_m = pid % tiles_m, tile_n = pid / tiles_m;
@@ -114,28 +136,27 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs<T> a) {
     const int wm0 = (wave / WAVES_N) * WM, wn0 = (wave % WAVES_N) * WN;
     const int K = a.K;
 
-    // Source of each of this wave's load instructions: stage row r = 8 * (instr) + lane/8,
-    // physical chunk lane % 8 <- logical chunk swz(r, lane % 8).  A rows past M are
-    // clamped into range (their results are never stored).
-    const T* src[LPW];
+    // Load instruction i of this wave fills stage rows 8 (wave*LPW + i) .. +7: lane -> row
+    // r = 8 (wave*LPW + i) + lane / 8, physical chunk lane % 8 <- logical chunk
+    // swz(r, lane % 8).  One SGPR resource per operand tile; A rows past M fall outside
+    // the A resource and read as zero.  The slice offset kt * 128 bytes rides in soffset.
+    const int mrows = a.M - m0 < BM ? a.M - m0 : BM;
+    const __amdgpu_buffer_rsrc_t rA = make_rsrc(a.A + (size_t)m0 * K, (unsigned)(mrows * K * sizeof(T)));
+    const __amdgpu_buffer_rsrc_t rW = make_rsrc(a.W + (size_t)n0 * K, (unsigned)(BN * K * sizeof(T)));
+    unsigned voff[LPW];
 #pragma unroll
     for (int i = 0; i < LPW; i++) {
-        int r = (wave * LPW + i) * 8 + lane / 8;
-        int lc = swz(r, lane % 8);
-        const T* base;
-        if (r < BM) {
-            int gr = m0 + r < a.M ? m0 + r : a.M - 1;
-            base = a.A + (size_t)gr * K;
-        } else {
-            base = a.W + (size_t)(n0 + r - BM) * K;
-        }
-        src[i] = base + lc * (16 / sizeof(T));
+        const int r = (wave * LPW + i) * 8 + lane / 8;
+        const int rr = r < BM ? r : r - BM;
+        voff[i] = (unsigned)rr * (unsigned)(K * sizeof(T)) + (unsigned)swz(r, lane % 8) * 16u;
     }
 #define GEMM_ISSUE(kt_, stage_)                                                            \
     do {                                                                                   \
         unsigned char* dst_ = smem + (stage_) * STAGE_BYTES + wave * LPW * 1024;           \
-        _Pragma("unroll") for (int i_ = 0; i_ < LPW; i_++)                                 \
-            load_lds16(src[i_] + (size_t)(kt_) * BK, dst_ + i_ * 1024);                    \
+        _Pragma("unroll") for (int i_ = 0; i_ < LPW; i_++) {                               \
+            const bool isA = (wave * LPW + i_) * 8 < BM;                                   \
+            buf_load_lds16(isA ? rA : rW, voff[i_], (unsigned)(kt_) * 128u, dst_ + i_ * 1024); \
+        }                                                                                  \
     } while (0)
 
     f32x16 acc[FM][FN];
@@ -153,8 +174,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs<T> a) {
     const int fr = lane & 31, fh = lane >> 5;
     for (int kt = 0; kt < nk; kt++) {
         // Slice kt has landed (later slices may still be in flight); make it visible.
-        if (STAGES == 3 && kt + 1 < nk) wait_vmcnt<LPW>();
-        else if (STAGES == 4 && kt + 2 < nk) wait_vmcnt<2 * LPW>();
+        if (STAGES >= 4 && kt + 2 < nk) wait_vmcnt<2 * LPW>();
+        else if (STAGES >= 3 && kt + 1 < nk) wait_vmcnt<LPW>();
         else wait_vmcnt<0>();
         raw_barrier();
         if (kt + STAGES - 1 < nk) GEMM_ISSUE(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
@@ -222,58 +243,117 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs<T> a) {
                 }
             }
     } else if constexpr (EPI == EPI_QKVG) {
+        // Each wave owns WM rows x one 64-column head of one region (q | k | v | gate).
+        // The stage buffers are free once every wave is past the main loop; each wave then
+        // uses its own 16 KB LDS slot (RoPE table rows, or the V^T transpose).
+        static_assert(STAGES * STAGE_BYTES >= NW * 16384, "QKVG epilogue needs 16 KB of LDS per wave");
+        static_assert(WM == 64, "QKVG epilogue stages 64 rows per wave");
         const int D = a.D, Dh = 64;
         const int col0 = n0 + wn0;  // first column of this wave's head
         const int region = col0 / D;
         const int h = (col0 % D) / Dh;
         const int half_heads = a.H / 2;
+        __syncthreads();
+        unsigned char* slot = smem + wave * 16384;
+        const int rw0 = m0 + wm0;  // first row of this wave
         if (region <= 1) {
-            const float* nw = (region == 0 ? a.q_norm : a.k_norm) + h * Dh;
+            const float* nwp = (region == 0 ? a.q_norm : a.k_norm) + h * Dh;
+            const float nw0 = nwp[cl], nw1 = nwp[32 + cl];
             T* dst = region == 0 ? a.Q : a.Kd;
+            const bool rope = h < half_heads;
+            float* rt = reinterpret_cast<float*>(slot);  // [64 rows][cos 32 | sin 32]
+            if (rope) {
+#pragma unroll
+                for (int it = 0; it < 16; it++) {
+                    const int idx = it * 64 + lane, r = idx >> 4, q4 = idx & 15;
+                    int row = rw0 + r;
+                    row = row < a.M ? row : a.M - 1;
+                    const int sq = row % a.S;
+                    const float* tb = (q4 < 8 ? a.rope_cos : a.rope_sin) + (size_t)sq * (Dh / 2) + (q4 & 7) * 4;
+                    *reinterpret_cast<float4*>(rt + r * 64 + q4 * 4) = *reinterpret_cast<const float4*>(tb);
+                }
+            }
 #pragma unroll
             for (int i = 0; i < FM; i++)
 #pragma unroll
                 for (int e = 0; e < 16; e++) {
-                    int row = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
-                    float ss = acc[i][0][e] * acc[i][0][e] + acc[i][1][e] * acc[i][1][e];
-                    ss += __shfl_xor(ss, 1, 64);
-                    ss += __shfl_xor(ss, 2, 64);
-                    ss += __shfl_xor(ss, 4, 64);
-                    ss += __shfl_xor(ss, 8, 64);
-                    ss += __shfl_xor(ss, 16, 64);
-                    float rms = sqrtf(ss / (float)Dh + a.eps);
-                    int rr = row < a.M ? row : a.M - 1;
-                    int b = rr / a.S, s = rr % a.S;
-#pragma unroll
-                    for (int j = 0; j < 2; j++) {
-                        int d = 32 * j + cl;
-                        float y = acc[i][j][e] / rms * nw[d];
-                        float partner = __shfl_xor(y, 1, 64);
-                        if (h < half_heads) {
-                            int k = d >> 1;
-                            float c = a.rope_cos[s * (Dh / 2) + k], sn = a.rope_sin[s * (Dh / 2) + k];
-                            y = (d & 1) ? (partner * sn + y * c) : (y * c - partner * sn);
-                        }
-                        if (region == 0) y *= a.q_scale;
-                        if (row < a.M) dst[(((size_t)b * a.H + h) * a.S + s) * Dh + d] = from_f32<T>(y);
+                    const int rl = 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);  // row within the wave
+                    const int row = rw0 + rl;
+                    const float y0 = acc[i][0][e], y1 = acc[i][1][e];
+                    const float ss = half_wave_sum(y0 * y0 + y1 * y1);
+                    const float inv = 1.f / sqrtf(ss / (float)Dh + a.eps);
+                    float ya = y0 * inv * nw0, yb = y1 * inv * nw1;
+                    if (rope) {
+                        // interleaved pairs (2k, 2k+1) sit in neighbouring lanes
+                        const float pa = IRO_DPP(ya, 0xB1), pb = IRO_DPP(yb, 0xB1);
+                        const int k0 = cl >> 1, k1 = 16 + (cl >> 1);
+                        const float c0 = rt[rl * 64 + k0], s0 = rt[rl * 64 + 32 + k0];
+                        const float c1 = rt[rl * 64 + k1], s1 = rt[rl * 64 + 32 + k1];
+                        ya = (cl & 1) ? (pa * s0 + ya * c0) : (ya * c0 - pa * s0);
+                        yb = (cl & 1) ? (pb * s1 + yb * c1) : (yb * c1 - pb * s1);
+                    }
+                    if (region == 0) {
+                        ya *= a.q_scale;
+                        yb *= a.q_scale;
+                    }
+                    if (row < a.M) {
+                        const int b = row / a.S, sq = row % a.S;
+                        T* o = dst + (((size_t)b * a.H + h) * a.S + sq) * Dh;
+                        o[cl] = from_f32<T>(ya);
+                        o[32 + cl] = from_f32<T>(yb);
                     }
                 }
         } else if (region == 2) {
+            // V^T [B,H,Dh,S'] in the key order the attention kernel's A operand wants.
+            if constexpr (sizeof(T) == 2) {
+                // The wave's 64 x 64 block is transposed through LDS (row stride 66 elements
+                // keeps both passes conflict-free), then each lane stores a token pair (s, s+1)
+                // — adjacent under the key permutation — as one 4-byte word.
+                T* vt = reinterpret_cast<T*>(slot);  // [64 dims][66]
 #pragma unroll
-            for (int i = 0; i < FM; i++)
+                for (int i = 0; i < FM; i++)
 #pragma unroll
-                for (int e = 0; e < 16; e++) {
-                    int row = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
+                    for (int e = 0; e < 16; e++) {
+                        const int rl = 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+#pragma unroll
+                        for (int j = 0; j < 2; j++) vt[(32 * j + cl) * 66 + rl] = from_f32<T>(acc[i][j][e]);
+                    }
+#pragma unroll
+                for (int it = 0; it < 32; it++) {
+                    const int d = 2 * it + (lane >> 5), p = lane & 31;  // dim d, token pair p
+                    const int row = rw0 + 2 * p;
                     if (row >= a.M) continue;
-                    int b = row / a.S, s = row % a.S;
-                    // V^T in the key order the attention kernel's A operand wants.
-                    int pos = sizeof(T) == 2 ? vt_pos_bf16(s) : vt_pos_f32(s);
+                    const int b = row / a.S, sq = row % a.S;
+                    if (sq + 1 < a.S && row + 1 < a.M) {  // both tokens in one batch row
+                        T* o = a.Vd + (((size_t)b * a.H + h) * Dh + d) * a.vt_stride;
+                        *reinterpret_cast<unsigned*>(o + vt_pos_bf16(sq)) =
+                            *reinterpret_cast<const unsigned*>(vt + d * 66 + 2 * p);
+                    } else {
 #pragma unroll
-                    for (int j = 0; j < 2; j++) {
-                        int d = 32 * j + cl;
-                        a.Vd[(((size_t)b * a.H + h) * Dh + d) * a.vt_stride + pos] = from_f32<T>(acc[i][j][e]);
+                        for (int u = 0; u < 2; u++) {
+                            const int r2 = row + u;
+                            if (r2 >= a.M) break;
+                            const int b2 = r2 / a.S, s2 = r2 % a.S;
+                            a.Vd[(((size_t)b2 * a.H + h) * Dh + d) * a.vt_stride + vt_pos_bf16(s2)] = vt[d * 66 + 2 * p + u];
+                        }
                     }
                 }
+            } else {
+#pragma unroll
+                for (int i = 0; i < FM; i++)
+#pragma unroll
+                    for (int e = 0; e < 16; e++) {
+                        int row = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
+                        if (row >= a.M) continue;
+                        int b = row / a.S, sq = row % a.S;
+                        int pos = vt_pos_f32(sq);
+#pragma unroll
+                        for (int j = 0; j < 2; j++) {
+                            int d = 32 * j + cl;
+                            a.Vd[(((size_t)b * a.H + h) * Dh + d) * a.vt_stride + pos] = from_f32<T>(acc[i][j][e]);
+                        }
+                    }
+            }
         } else {
 #pragma unroll
             for (int i = 0; i < FM; i++)
@@ -291,20 +371,21 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs<T> a) {
     }
 }
 
-template <typename T, int BM, int BN, int STAGES, int EPI>
+template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int EPI>
 int launch_cfg(const GemmArgs<T>& a, hipStream_t st) {
     constexpr int BK = 128 / sizeof(T);
     if (a.M <= 0 || a.N % BN != 0 || a.K % BK != 0 || a.K <= 0) return -1;
+    if ((size_t)BN * a.K * sizeof(T) > 0xffffffffull || (size_t)BM * a.K * sizeof(T) > 0xffffffffull) return -1;
     int tiles = ((a.M + BM - 1) / BM) * (a.N / BN);
     size_t lds = (size_t)STAGES * (BM + BN) * 128;
     static bool attr_set = false;  // per instantiation; the attribute is process-wide
     if (!attr_set) {
-        if (hipFuncSetAttribute((const void*)gemm_kernel<T, BM, BN, STAGES, EPI>,
+        if (hipFuncSetAttribute((const void*)gemm_kernel<T, BM, BN, WAVES_M, WAVES_N, STAGES, EPI>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
             return -2;
         attr_set = true;
     }
-    gemm_kernel<T, BM, BN, STAGES, EPI><<<tiles, 256, lds, st>>>(a);
+    gemm_kernel<T, BM, BN, WAVES_M, WAVES_N, STAGES, EPI><<<tiles, 64 * WAVES_M * WAVES_N, lds, st>>>(a);
     return 0;
 }
 
@@ -316,10 +397,10 @@ int launch_cfg(const GemmArgs<T>& a, hipStream_t st) {
 template <typename T>
 int launch_gemm(int epi, const GemmArgs<T>& a, hipStream_t st) {
     switch (epi) {
-        case EPI_STORE: return launch_cfg<T, 64, 64, 4, EPI_STORE>(a, st);
-        case EPI_RESID: return launch_cfg<T, 64, 64, 4, EPI_RESID>(a, st);
-        case EPI_SWIGLU: return launch_cfg<T, 128, 128, 2, EPI_SWIGLU>(a, st);
-        case EPI_QKVG: return launch_cfg<T, 128, 128, 2, EPI_QKVG>(a, st);
+        case EPI_STORE: return launch_cfg<T, 64, 64, 2, 2, 4, EPI_STORE>(a, st);
+        case EPI_RESID: return launch_cfg<T, 64, 64, 2, 2, 4, EPI_RESID>(a, st);
+        case EPI_SWIGLU: return launch_cfg<T, 128, 128, 2, 2, 2, EPI_SWIGLU>(a, st);
+        case EPI_QKVG: return launch_cfg<T, 128, 128, 2, 2, 2, EPI_QKVG>(a, st);
     }
     return -1;
 }

@@ -36,6 +36,8 @@ def make_engine(cfg, backend, w, ctx, rows, seq):
 SMALL = {
     # name: (cfg factory, seq, text, speaker, weight std, norm jitter)
     "tiny": (ih.cfg_tiny, 40, 20, 13, 0.05, 0.1),
+    # odd S: the V^T token pair at the batch-row boundary straddles two rows
+    "tiny_odd": (ih.cfg_tiny, 37, 11, 9, 0.05, 0.1),
     "cfg1": (ih.cfg_cpu_plumbing, 64, 16, 32, 0.02, 0.0),
 }
 
