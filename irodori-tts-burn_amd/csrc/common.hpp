@@ -92,8 +92,21 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
-__device__ __forceinline__ float silu_f(float v) { return v / (1.0f + __expf(-v)); }
-__device__ __forceinline__ float sigmoid_f(float v) { return 1.0f / (1.0f + __expf(-v)); }
+// v_rcp_f32 (1 ulp) instead of an IEEE division: these feed bf16 operands or are far
+// inside the f32 tolerance, and the precise divide is ~10 instructions per element.
+__device__ __forceinline__ float silu_f(float v) { return v * __builtin_amdgcn_rcpf(1.0f + __expf(-v)); }
+__device__ __forceinline__ float sigmoid_f(float v) { return __builtin_amdgcn_rcpf(1.0f + __expf(-v)); }
+
+// (b, s) = divmod(row, S) without an integer division: a float-reciprocal quotient
+// (exact to within one for row < 2^24) and a one-step correction.
+__device__ __forceinline__ void row_bs(int row, int S, float inv_s, int& b, int& s) {
+    int q = (int)((float)row * inv_s);
+    int r = row - q * S;
+    if (r < 0) { q--; r += S; }
+    if (r >= S) { q++; r -= S; }
+    b = q;
+    s = r;
+}
 
 // Map a linear workgroup id so that consecutive ids land on the same XCD.  Workgroups
 // are dispatched round-robin over the 8 XCDs (id % 8); when the grid is a multiple of

@@ -200,6 +200,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
     //      col = n0 + wn0 + 32 j + lane % 32.
     const int rbase = m0 + wm0 + 4 * (lane >> 5);
     const int cl = lane & 31;
+    const float inv_s = 1.f / (float)a.S;
     if constexpr (EPI == EPI_STORE) {
 #pragma unroll
         for (int i = 0; i < FM; i++)
@@ -211,20 +212,62 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
                 for (int j = 0; j < FN; j++) a.C[(size_t)row * a.N + n0 + wn0 + 32 * j + cl] = acc[i][j][e];
             }
     } else if constexpr (EPI == EPI_RESID) {
+        // x[row, col] += gate[b(row), col] * C.  The gate rows of the (at most two) batch
+        // rows a 32-row block touches are loaded once; x is read for a whole 32-row block
+        // before any of it is written.
+        float* __restrict__ xg = a.x;
+        const int step = a.mt.step ? *a.mt.step : 0;
+        if (a.S < 32) {  // a 32-row block may span more than two batch rows
 #pragma unroll
-        for (int i = 0; i < FM; i++)
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const int row = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
+                    if (row >= a.M) continue;
+                    const float* g = gate_vec(a.mt, row / a.S, a.layer, a.kind, a.N);
+#pragma unroll
+                    for (int j = 0; j < FN; j++) {
+                        const int col = n0 + wn0 + 32 * j + cl;
+                        xg[(size_t)row * a.N + col] += g[col] * acc[i][j][e];
+                    }
+                }
+        } else
+#pragma unroll
+        for (int i = 0; i < FM; i++) {
+            const int r0 = rbase + 32 * i;
+            int b_lo, s_lo;
+            row_bs(r0 < a.M ? r0 : a.M - 1, a.S, inv_s, b_lo, s_lo);
+            const int b_hi = b_lo + 1;
+            const float* g_lo = a.mt.tab + ((size_t)(step * a.mt.step_stride + b_lo / a.mt.rows_per_vec) * a.mt.layers * 6 +
+                                            (size_t)a.layer * 6 + a.kind * 3 + 2) * a.N;
+            const float* g_hi = a.mt.tab + ((size_t)(step * a.mt.step_stride + b_hi / a.mt.rows_per_vec) * a.mt.layers * 6 +
+                                            (size_t)a.layer * 6 + a.kind * 3 + 2) * a.N;
+            float glo[FN], ghi[FN];
+            const bool need_hi = s_lo + 28 >= a.S && b_hi * a.S < a.M;  // block may cross into b_hi
+#pragma unroll
+            for (int j = 0; j < FN; j++) {
+                const int col = n0 + wn0 + 32 * j + cl;
+                glo[j] = g_lo[col];
+                ghi[j] = need_hi ? g_hi[col] : 0.f;
+            }
+            float xv[16][FN];
 #pragma unroll
             for (int e = 0; e < 16; e++) {
-                int row = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
-                if (row >= a.M) continue;
-                const float* g = gate_vec(a.mt, row / a.S, a.layer, a.kind, a.N);
+                const int row = r0 + 8 * (e >> 2) + (e & 3);
 #pragma unroll
-                for (int j = 0; j < FN; j++) {
-                    int col = n0 + wn0 + 32 * j + cl;
-                    float* xp = a.x + (size_t)row * a.N + col;
-                    *xp = *xp + g[col] * acc[i][j][e];
-                }
+                for (int j = 0; j < FN; j++)
+                    xv[e][j] = row < a.M ? xg[(size_t)row * a.N + n0 + wn0 + 32 * j + cl] : 0.f;
             }
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const int row = r0 + 8 * (e >> 2) + (e & 3);
+                if (row >= a.M) continue;
+                const bool hi = row >= b_hi * a.S;
+#pragma unroll
+                for (int j = 0; j < FN; j++)
+                    xg[(size_t)row * a.N + n0 + wn0 + 32 * j + cl] = xv[e][j] + (hi ? ghi[j] : glo[j]) * acc[i][j][e];
+            }
+        }
     } else if constexpr (EPI == EPI_SWIGLU) {
         // W rows come in 32-row groups alternating W1 / W3 columns: block j even holds
         // u1 and block j+1 the matching u3 for output columns 32 * pair + lane % 32.
@@ -268,7 +311,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
                     const int idx = it * 64 + lane, r = idx >> 4, q4 = idx & 15;
                     int row = rw0 + r;
                     row = row < a.M ? row : a.M - 1;
-                    const int sq = row % a.S;
+                    int bq, sq;
+                    row_bs(row, a.S, inv_s, bq, sq);
                     const float* tb = (q4 < 8 ? a.rope_cos : a.rope_sin) + (size_t)sq * (Dh / 2) + (q4 & 7) * 4;
                     *reinterpret_cast<float4*>(rt + r * 64 + q4 * 4) = *reinterpret_cast<const float4*>(tb);
                 }
@@ -281,7 +325,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
                     const int row = rw0 + rl;
                     const float y0 = acc[i][0][e], y1 = acc[i][1][e];
                     const float ss = half_wave_sum(y0 * y0 + y1 * y1);
-                    const float inv = 1.f / sqrtf(ss / (float)Dh + a.eps);
+                    const float inv = __builtin_amdgcn_rsqf(ss * (1.f / (float)Dh) + a.eps);
                     float ya = y0 * inv * nw0, yb = y1 * inv * nw1;
                     if (rope) {
                         // interleaved pairs (2k, 2k+1) sit in neighbouring lanes
@@ -297,7 +341,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
                         yb *= a.q_scale;
                     }
                     if (row < a.M) {
-                        const int b = row / a.S, sq = row % a.S;
+                        int b, sq;
+                        row_bs(row, a.S, inv_s, b, sq);
                         T* o = dst + (((size_t)b * a.H + h) * a.S + sq) * Dh;
                         o[cl] = from_f32<T>(ya);
                         o[32 + cl] = from_f32<T>(yb);
@@ -323,7 +368,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
                     const int d = 2 * it + (lane >> 5), p = lane & 31;  // dim d, token pair p
                     const int row = rw0 + 2 * p;
                     if (row >= a.M) continue;
-                    const int b = row / a.S, sq = row % a.S;
+                    int b, sq;
+                    row_bs(row, a.S, inv_s, b, sq);
                     if (sq + 1 < a.S && row + 1 < a.M) {  // both tokens in one batch row
                         T* o = a.Vd + (((size_t)b * a.H + h) * Dh + d) * a.vt_stride;
                         *reinterpret_cast<unsigned*>(o + vt_pos_bf16(sq)) =
@@ -333,7 +379,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
                         for (int u = 0; u < 2; u++) {
                             const int r2 = row + u;
                             if (r2 >= a.M) break;
-                            const int b2 = r2 / a.S, s2 = r2 % a.S;
+                            int b2, s2;
+                            row_bs(r2, a.S, inv_s, b2, s2);
                             a.Vd[(((size_t)b2 * a.H + h) * Dh + d) * a.vt_stride + vt_pos_bf16(s2)] = vt[d * 66 + 2 * p + u];
                         }
                     }
@@ -345,7 +392,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
                     for (int e = 0; e < 16; e++) {
                         int row = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
                         if (row >= a.M) continue;
-                        int b = row / a.S, sq = row % a.S;
+                        int b, sq;
+                        row_bs(row, a.S, inv_s, b, sq);
                         int pos = vt_pos_f32(sq);
 #pragma unroll
                         for (int j = 0; j < 2; j++) {
