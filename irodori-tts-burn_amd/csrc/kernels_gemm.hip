@@ -288,26 +288,28 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
     } else if constexpr (EPI == EPI_QKVG) {
         // Each wave owns WM rows x one 64-column head of one region (q | k | v | gate).
         // The stage buffers are free once every wave is past the main loop; each wave then
-        // uses its own 16 KB LDS slot (RoPE table rows, or the V^T transpose).
-        static_assert(STAGES * STAGE_BYTES >= NW * 16384, "QKVG epilogue needs 16 KB of LDS per wave");
-        static_assert(WM == 64, "QKVG epilogue stages 64 rows per wave");
+        // uses its own LDS slot: RoPE table rows (WM x 64 f32) or the V^T transpose
+        // (64 x (WM + 2) elements; an odd word stride keeps both passes conflict-free).
+        constexpr int VT_BYTES = sizeof(T) == 2 ? 64 * (WM + 2) * 2 : 0;  // f32 scatters V^T directly
+        constexpr int SLOT = WM * 256 > VT_BYTES ? WM * 256 : VT_BYTES;
+        static_assert(STAGES * STAGE_BYTES >= NW * SLOT, "QKVG epilogue needs one LDS slot per wave");
         const int D = a.D, Dh = 64;
         const int col0 = n0 + wn0;  // first column of this wave's head
         const int region = col0 / D;
         const int h = (col0 % D) / Dh;
         const int half_heads = a.H / 2;
         __syncthreads();
-        unsigned char* slot = smem + wave * 16384;
+        unsigned char* slot = smem + wave * SLOT;
         const int rw0 = m0 + wm0;  // first row of this wave
         if (region <= 1) {
             const float* nwp = (region == 0 ? a.q_norm : a.k_norm) + h * Dh;
             const float nw0 = nwp[cl], nw1 = nwp[32 + cl];
             T* dst = region == 0 ? a.Q : a.Kd;
             const bool rope = h < half_heads;
-            float* rt = reinterpret_cast<float*>(slot);  // [64 rows][cos 32 | sin 32]
+            float* rt = reinterpret_cast<float*>(slot);  // [WM rows][cos 32 | sin 32]
             if (rope) {
 #pragma unroll
-                for (int it = 0; it < 16; it++) {
+                for (int it = 0; it < WM / 4; it++) {
                     const int idx = it * 64 + lane, r = idx >> 4, q4 = idx & 15;
                     int row = rw0 + r;
                     row = row < a.M ? row : a.M - 1;
@@ -351,21 +353,22 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
         } else if (region == 2) {
             // V^T [B,H,Dh,S'] in the key order the attention kernel's A operand wants.
             if constexpr (sizeof(T) == 2) {
-                // The wave's 64 x 64 block is transposed through LDS (row stride 66 elements
-                // keeps both passes conflict-free), then each lane stores a token pair (s, s+1)
-                // — adjacent under the key permutation — as one 4-byte word.
-                T* vt = reinterpret_cast<T*>(slot);  // [64 dims][66]
+                // The wave's WM x 64 block is transposed through LDS, then each lane stores
+                // a token pair (s, s+1) — adjacent under the key permutation — as one word.
+                constexpr int VS = WM + 2;  // row stride (elements) of the transpose
+                T* vt = reinterpret_cast<T*>(slot);  // [64 dims][VS]
 #pragma unroll
                 for (int i = 0; i < FM; i++)
 #pragma unroll
                     for (int e = 0; e < 16; e++) {
                         const int rl = 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
 #pragma unroll
-                        for (int j = 0; j < 2; j++) vt[(32 * j + cl) * 66 + rl] = from_f32<T>(acc[i][j][e]);
+                        for (int j = 0; j < 2; j++) vt[(32 * j + cl) * VS + rl] = from_f32<T>(acc[i][j][e]);
                     }
 #pragma unroll
-                for (int it = 0; it < 32; it++) {
-                    const int d = 2 * it + (lane >> 5), p = lane & 31;  // dim d, token pair p
+                for (int it = 0; it < WM / 2; it++) {
+                    const int t = it * 64 + lane;
+                    const int d = t / (WM / 2), p = t % (WM / 2);  // dim d, token pair p
                     const int row = rw0 + 2 * p;
                     if (row >= a.M) continue;
                     int b, sq;
@@ -373,7 +376,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
                     if (sq + 1 < a.S && row + 1 < a.M) {  // both tokens in one batch row
                         T* o = a.Vd + (((size_t)b * a.H + h) * Dh + d) * a.vt_stride;
                         *reinterpret_cast<unsigned*>(o + vt_pos_bf16(sq)) =
-                            *reinterpret_cast<const unsigned*>(vt + d * 66 + 2 * p);
+                            *reinterpret_cast<const unsigned*>(vt + d * VS + 2 * p);
                     } else {
 #pragma unroll
                         for (int u = 0; u < 2; u++) {
@@ -381,7 +384,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
                             if (r2 >= a.M) break;
                             int b2, s2;
                             row_bs(r2, a.S, inv_s, b2, s2);
-                            a.Vd[(((size_t)b2 * a.H + h) * Dh + d) * a.vt_stride + vt_pos_bf16(s2)] = vt[d * 66 + 2 * p + u];
+                            a.Vd[(((size_t)b2 * a.H + h) * Dh + d) * a.vt_stride + vt_pos_bf16(s2)] = vt[d * VS + 2 * p + u];
                         }
                     }
                 }

@@ -175,6 +175,10 @@ def test_cfg4_sample_40_steps_bf16_vs_golden(cfg4):
     cfg, w, ctx, x0 = cfg4
     with make_engine(cfg, BF16, w, ctx, 2, 750) as e:
         got = e.sample(x0, joint_params(40))
+        # At this shape the GEMMs split their tail tiles over K; the fixed-order
+        # reduction keeps replays bit-identical.
+        again = e.sample(x0, joint_params(40))
+    assert np.array_equal(got, again)
     ref = np.load(path)
     err = rel_l2(got, ref)
     print("cfg4 bf16 40-step final latent rel L2 %.3e" % err)
