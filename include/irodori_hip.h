@@ -155,6 +155,13 @@ int irodori_clear_ctx_kv(irodori_ctx* ctx);
 int irodori_forward(irodori_ctx* ctx, int batch, int seq, const float* x_t, const float* t,
                     float* v_out, float* debug);
 
+/* forward_with_cond_cached with a latent mask (optimized.rs:102-113 latent_mask;
+ * build_joint_mask, attention.rs:730-750): latent_mask [B,S] (nonzero = the latent key
+ * attends; NULL = all attend) masks latent keys in every block's joint attention.  Query
+ * rows are computed for every frame; a row with no valid key gets a zero attention output. */
+int irodori_forward_masked(irodori_ctx* ctx, int batch, int seq, const float* x_t, const float* t,
+                           const uint8_t* latent_mask, float* v_out, float* debug);
+
 /* One DiffusionBlock::forward_fused (diffusion.rs:62-105) on host data:
  * x [B,S,D] updated in place; cond [B,3D] is the cond_module output. */
 int irodori_block_forward(irodori_ctx* ctx, int layer, int batch, int seq, float* x,
@@ -165,6 +172,12 @@ int irodori_block_forward(irodori_ctx* ctx, int layer, int batch, int seq, float
  * replayed per step.  Truncation (params.rs:146-155) is applied to x0 when set. */
 int irodori_sample(irodori_ctx* ctx, const irodori_sampler_params* params, int utterances,
                    int seq, const float* x0, float* x_out);
+/* Joint-CFG sampling of a padded variable-length batch: utterance u attends to its first
+ * lengths[u] latent frames (both CFG rows), so frames below lengths[u] match an unpadded
+ * run of that utterance (BASELINE config 5's padded batches; the reference sampler always
+ * passes latent_mask = None, euler_sampler.rs:410-523).  lengths: host int32 [U]. */
+int irodori_sample_masked(irodori_ctx* ctx, const irodori_sampler_params* params, int utterances,
+                          int seq, const int32_t* lengths, const float* x0, float* x_out);
 /* Same with x0 / x_out already in device memory (HBM-resident timing). */
 int irodori_sample_device(irodori_ctx* ctx, const irodori_sampler_params* params,
                           int utterances, int seq, const float* d_x0, float* d_x_out);

@@ -96,8 +96,9 @@ struct LayerBufs {
 struct GraphKey {
     int B, S, T;
     uint32_t scale_bits;
+    int latent_masked;  // the captured attention reads the latent key masks
     bool operator<(const GraphKey& o) const {
-        return std::tie(B, S, T, scale_bits) < std::tie(o.B, o.S, o.T, o.scale_bits);
+        return std::tie(B, S, T, scale_bits, latent_masked) < std::tie(o.B, o.S, o.T, o.scale_bits, o.latent_masked);
     }
 };
 
@@ -132,6 +133,12 @@ struct irodori_ctx {
     float* vout = nullptr;  // [rows, S, P]
     int* step = nullptr;    // device step counter
     int* zero_step = nullptr;
+    // Latent key mask of the current call (build_joint_mask's self part,
+    // attention.rs:730-750): per row and 64-key tile a validity word (bf16 attention)
+    // and the float mask (f32 attention).  lat_on routes them to the attention launches.
+    unsigned long long* lat_bits = nullptr;  // [rows, ceil(S / 64)] for the call's S
+    float* lat_mask_f = nullptr;             // [rows, S]
+    bool lat_on = false;
 
     // conditioning precompute
     int nvec_cap = 0;
@@ -343,6 +350,10 @@ int enqueue_layer(irodori_ctx* c, int l, int B, int S, const ModTable& mt, bool 
         aa.mask1 = lb.ctx_mask;
         aa.tile_on1 = lb.tile_on;
         aa.bits1 = lb.tile_bits;
+    }
+    if (c->lat_on) {
+        aa.mask0 = c->lat_mask_f;
+        aa.bits0 = c->lat_bits;
     }
     aa.B = B;
     aa.H = H;
@@ -611,6 +622,8 @@ int irodori_ctx_create(int device, const irodori_dit_config* cfg, irodori_ctx** 
     IRO_TRY(dalloc(c.get(), &c->rope_sin, sizeof(float) * (size_t)S * Dh / 2));
     IRO_TRY(dalloc(c.get(), &c->xt, sizeof(float) * M * P));
     IRO_TRY(dalloc(c.get(), &c->vout, sizeof(float) * M * P));
+    IRO_TRY(dalloc(c.get(), &c->lat_bits, sizeof(unsigned long long) * (size_t)R * ((S + 63) / 64)));
+    IRO_TRY(dalloc(c.get(), &c->lat_mask_f, sizeof(float) * (size_t)R * S));
     IRO_TRY(dalloc(c.get(), &c->step, sizeof(int)));
     IRO_TRY(dalloc(c.get(), &c->zero_step, sizeof(int)));
     IRO_HIP_CHECK(hipMemsetAsync(c->zero_step, 0, sizeof(int), c->stream));
@@ -778,7 +791,44 @@ int irodori_set_ctx_kv(irodori_ctx* c, int layer, int row, int t_ctx, const floa
     IRO_GUARD_END
 }
 
+// Upload a latent key mask [B, S] (nonzero = the key attends) as per-row tile validity
+// words and a float mask, and route it to the attention launches until the guard ends.
+static int upload_latent_mask(irodori_ctx* c, int B, int S, const uint8_t* mask) {
+    const int ntl = (S + 63) / 64;
+    std::vector<unsigned long long> bits((size_t)B * ntl, 0ull);
+    std::vector<float> mf((size_t)B * S, 0.f);
+    for (int b = 0; b < B; b++)
+        for (int s = 0; s < S; s++)
+            if (mask[(size_t)b * S + s]) {
+                bits[(size_t)b * ntl + s / 64] |= 1ull << (s % 64);
+                mf[(size_t)b * S + s] = 1.f;
+            }
+    IRO_TRY(upload(c, c->lat_bits, bits.data(), sizeof(unsigned long long) * bits.size()));
+    IRO_TRY(upload(c, c->lat_mask_f, mf.data(), sizeof(float) * mf.size()));
+    IRO_HIP_CHECK(hipStreamSynchronize(c->stream));  // the host staging vectors end here
+    return IRODORI_OK;
+}
+
+struct LatentMaskScope {
+    irodori_ctx* c;
+    LatentMaskScope(irodori_ctx* ctx, bool on) : c(ctx) { c->lat_on = on; }
+    ~LatentMaskScope() { c->lat_on = false; }
+};
+
+static int forward_impl(irodori_ctx* c, int B, int S, const float* x_t, const float* t, const uint8_t* latent_mask,
+                 float* v_out, float* debug);
+
 int irodori_forward(irodori_ctx* c, int B, int S, const float* x_t, const float* t, float* v_out, float* debug) {
+    return forward_impl(c, B, S, x_t, t, nullptr, v_out, debug);
+}
+
+int irodori_forward_masked(irodori_ctx* c, int B, int S, const float* x_t, const float* t, const uint8_t* latent_mask,
+                           float* v_out, float* debug) {
+    return forward_impl(c, B, S, x_t, t, latent_mask, v_out, debug);
+}
+
+static int forward_impl(irodori_ctx* c, int B, int S, const float* x_t, const float* t, const uint8_t* latent_mask,
+                 float* v_out, float* debug) {
     IRO_GUARD_BEGIN
     IRO_REQUIRE(c && x_t && t && v_out, IRODORI_ERR_INVALID_ARG, "null argument");
     const auto& g = c->cfg;
@@ -787,6 +837,8 @@ int irodori_forward(irodori_ctx* c, int B, int S, const float* x_t, const float*
     IRO_TRY(check_ready(c, B));
     IRO_HIP_CHECK(hipSetDevice(c->device));
     int D = g.model_dim, P = g.latent_dim, L = g.num_layers;
+    if (latent_mask) IRO_TRY(upload_latent_mask(c, B, S, latent_mask));
+    LatentMaskScope lms(c, latent_mask != nullptr);
     IRO_TRY(ensure_nvec(c, B));
     IRO_TRY(upload(c, c->tvec, t, sizeof(float) * B));
     IRO_TRY(upload(c, c->xt, x_t, sizeof(float) * (size_t)B * S * P));
@@ -850,8 +902,18 @@ int irodori_block_forward(irodori_ctx* c, int layer, int B, int S, float* x, con
     IRO_GUARD_END
 }
 
+static int sample_device_impl(irodori_ctx* c, const irodori_sampler_params* p, int U, int S, const int32_t* lengths,
+                       const float* d_x0, float* d_x_out);
+
 int irodori_sample_device(irodori_ctx* c, const irodori_sampler_params* p, int U, int S, const float* d_x0,
                           float* d_x_out) {
+    return sample_device_impl(c, p, U, S, nullptr, d_x0, d_x_out);
+}
+
+// lengths (nullable, host [U]): utterance u attends to its first lengths[u] latent keys
+// in both CFG rows (padded variable-length batches).
+static int sample_device_impl(irodori_ctx* c, const irodori_sampler_params* p, int U, int S, const int32_t* lengths,
+                       const float* d_x0, float* d_x_out) {
     IRO_GUARD_BEGIN
     IRO_REQUIRE(c && p && d_x0 && d_x_out, IRODORI_ERR_INVALID_ARG, "null argument");
     IRO_TRY(validate_params(p));
@@ -865,6 +927,16 @@ int irodori_sample_device(irodori_ctx* c, const irodori_sampler_params* p, int U
     IRO_TRY(check_ready(c, B));
     IRO_HIP_CHECK(hipSetDevice(c->device));
     int N = p->num_steps, P = g.latent_dim;
+    if (lengths) {
+        std::vector<uint8_t> m((size_t)B * S, 0);
+        for (int u = 0; u < U; u++) {
+            IRO_REQUIRE(lengths[u] >= 1 && lengths[u] <= S, IRODORI_ERR_SHAPE, "utterance length must be in [1, seq]");
+            for (int r = 0; r < 2; r++)
+                for (int s = 0; s < lengths[u]; s++) m[(size_t)(2 * u + r) * S + s] = 1;
+        }
+        IRO_TRY(upload_latent_mask(c, B, S, m.data()));
+    }
+    LatentMaskScope lms(c, lengths != nullptr);
 
     // Schedule (euler_sampler.rs:325-328, f32) and per-step CFG window (:379).
     std::vector<float> ts(N + 1);
@@ -892,7 +964,7 @@ int irodori_sample_device(irodori_ctx* c, const irodori_sampler_params* p, int U
     // One captured RF step, replayed N times.
     uint32_t sbits;
     memcpy(&sbits, &scale, 4);
-    GraphKey key{B, S, c->t_ctx, sbits};
+    GraphKey key{B, S, c->t_ctx, sbits, lengths ? 1 : 0};
     hipGraphExec_t exec = nullptr;
     auto it = c->graphs.find(key);
     if (it != c->graphs.end()) {
@@ -926,7 +998,24 @@ int irodori_sample_device(irodori_ctx* c, const irodori_sampler_params* p, int U
     IRO_GUARD_END
 }
 
+static int sample_host(irodori_ctx* c, const irodori_sampler_params* p, int U, int S, const int32_t* lengths,
+                const float* x0, float* x_out);
+
 int irodori_sample(irodori_ctx* c, const irodori_sampler_params* p, int U, int S, const float* x0, float* x_out) {
+    return sample_host(c, p, U, S, nullptr, x0, x_out);
+}
+
+int irodori_sample_masked(irodori_ctx* c, const irodori_sampler_params* p, int U, int S, const int32_t* lengths,
+                          const float* x0, float* x_out) {
+    if (!lengths) {
+        set_last_error("null lengths");
+        return IRODORI_ERR_INVALID_ARG;
+    }
+    return sample_host(c, p, U, S, lengths, x0, x_out);
+}
+
+static int sample_host(irodori_ctx* c, const irodori_sampler_params* p, int U, int S, const int32_t* lengths,
+                const float* x0, float* x_out) {
     IRO_GUARD_BEGIN
     IRO_REQUIRE(c && p && x0 && x_out, IRODORI_ERR_INVALID_ARG, "null argument");
     IRO_TRY(validate_params(p));
@@ -936,7 +1025,7 @@ int irodori_sample(irodori_ctx* c, const irodori_sampler_params* p, int U, int S
     size_t n = (size_t)U * S * g.latent_dim;
     // Stage through the forward-output buffer (unused by the sampler).
     IRO_TRY(upload(c, c->vout, x0, sizeof(float) * n));
-    int rc = irodori_sample_device(c, p, U, S, c->vout, c->vout);
+    int rc = sample_device_impl(c, p, U, S, lengths, c->vout, c->vout);
     if (rc != IRODORI_OK) return rc;
     IRO_HIP_CHECK(hipMemcpy(x_out, c->vout, sizeof(float) * n, hipMemcpyDeviceToHost));
     return IRODORI_OK;

@@ -121,6 +121,9 @@ struct AttnArgs {
     const T* V0;
     int len0, stride0;
     const float* mask0;  // optional [B, len0]; value < 0.5 = masked out
+    // optional [B, ceil(len0/64)]: bit k of tile t set iff latent key 64 t + k attends
+    // (launch_attention32; required there together with mask0)
+    const unsigned long long* bits0;
     // segment 1 (cached context keys): [B, H, stride1, Dh], len1 keys
     const T* K1;
     const T* V1;

@@ -56,8 +56,9 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 __device__ __forceinline__ float bf16_round(float x) { return static_cast<float>(static_cast<bf16>(x)); }
 
 // Tile list of one (row, head): entry i < nact of the list is held by lane i as the tile
-// index and its 64-bit key-validity mask.  Latent tiles are valid up to len0; context
-// tiles carry the host-computed bits of the row and tiles without a valid key are dropped.
+// index and its 64-bit key-validity mask.  Latent tiles are valid up to len0 (or carry the
+// host-computed latent mask bits); context tiles carry the host-computed bits of the row;
+// tiles without a valid key are dropped.
 struct TileList {
     int t, lo, hi;  // per lane
     int nact;       // wave-uniform
@@ -67,7 +68,7 @@ __device__ __forceinline__ TileList build_tile_list(const AttnArgs<bf16>& a, int
     unsigned long long bits = 0ull;
     if (lane < nt0) {
         const int rem = a.len0 & (KT - 1);
-        bits = (lane == nt0 - 1 && rem) ? ((1ull << rem) - 1ull) : ~0ull;
+        bits = a.bits0 ? a.bits0[(size_t)b * nt0 + lane] : (lane == nt0 - 1 && rem) ? ((1ull << rem) - 1ull) : ~0ull;
     } else if (lane < nt0 + nt1) {
         bits = a.bits1[(size_t)b * ((a.stride1 + KT - 1) / KT) + (lane - nt0)];
     }
@@ -375,7 +376,7 @@ int launch_attn32_cfg(const AttnArgs<bf16>& a, hipStream_t st) {
 }  // namespace
 
 int launch_attention32(const AttnArgs<bf16>& a, hipStream_t st) {
-    if (a.Sq <= 0 || a.len0 <= 0 || !a.v_transposed || !a.prescaled || a.mask0) return -1;
+    if (a.Sq <= 0 || a.len0 <= 0 || !a.v_transposed || !a.prescaled || (a.mask0 && !a.bits0)) return -1;
     if (a.K1 && !a.bits1) return -1;
     if ((a.vstride0 % KT) || (a.K1 && (a.vstride1 % KT))) return -1;
     const int ntiles = (a.len0 + KT - 1) / KT + (a.K1 ? (a.len1 + KT - 1) / KT : 0);

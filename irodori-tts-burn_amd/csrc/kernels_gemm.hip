@@ -373,7 +373,10 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
                     if (row >= a.M) continue;
                     int b, sq;
                     row_bs(row, a.S, inv_s, b, sq);
-                    if (sq + 1 < a.S && row + 1 < a.M) {  // both tokens in one batch row
+                    // One word only for an even token with its successor in the same batch
+                    // row: (s, s+1) are then adjacent and 4-byte aligned under the key
+                    // permutation.  With odd S, odd batch rows start on an odd token.
+                    if (!(sq & 1) && sq + 1 < a.S && row + 1 < a.M) {
                         T* o = a.Vd + (((size_t)b * a.H + h) * Dh + d) * a.vt_stride;
                         *reinterpret_cast<unsigned*>(o + vt_pos_bf16(sq)) =
                             *reinterpret_cast<const unsigned*>(vt + d * VS + 2 * p);

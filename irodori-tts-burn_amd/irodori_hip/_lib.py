@@ -87,9 +87,13 @@ SIGNATURES = {
                                      C.POINTER(C.c_uint8)]),
     "irodori_clear_ctx_kv": (C.c_int, [_vp]),
     "irodori_forward": (C.c_int, [_vp, C.c_int, C.c_int, _f32p, _f32p, _f32p, _f32p]),
+    "irodori_forward_masked": (C.c_int, [_vp, C.c_int, C.c_int, _f32p, _f32p,
+                                         C.POINTER(C.c_uint8), _f32p, _f32p]),
     "irodori_block_forward": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _f32p, _f32p]),
     "irodori_sample": (C.c_int, [_vp, C.POINTER(SamplerParamsC), C.c_int, C.c_int, _f32p,
                                  _f32p]),
+    "irodori_sample_masked": (C.c_int, [_vp, C.POINTER(SamplerParamsC), C.c_int, C.c_int,
+                                        C.POINTER(C.c_int32), _f32p, _f32p]),
     "irodori_sample_device": (C.c_int, [_vp, C.POINTER(SamplerParamsC), C.c_int, C.c_int,
                                         _vp, _vp]),
     "irodori_profile_layer": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.POINTER(KernelTimesC)]),

@@ -123,16 +123,27 @@ class HipInferenceEngine:
                                                    m.ctypes.data_as(C.POINTER(C.c_uint8))))
 
     # ---- compute ------------------------------------------------------------------------
-    def forward_with_cond_cached(self, x_t: np.ndarray, t: np.ndarray, debug: bool = False):
-        """x_t [B,S,P], t [B] -> v [B,S,P] (and [L+1,B,S,D] block outputs if debug)."""
+    def forward_with_cond_cached(self, x_t: np.ndarray, t: np.ndarray, debug: bool = False,
+                                 latent_mask: np.ndarray = None):
+        """x_t [B,S,P], t [B] -> v [B,S,P] (and [L+1,B,S,D] block outputs if debug).
+        latent_mask [B,S] (nonzero = the latent key attends) masks latent keys
+        (optimized.rs:102-113, attention.rs:730-750); None = every key attends."""
         x_t = _c32(x_t)
         t = _c32(t)
         B, S, P = x_t.shape
         v = np.empty_like(x_t)
         dbg = (np.empty((self.cfg.num_layers + 1, B, S, self.cfg.model_dim), np.float32)
                if debug else None)
-        _check(self.lib.irodori_forward(self.ctx, B, S, _fp(x_t), _fp(t), _fp(v),
-                                        _fp(dbg) if debug else None))
+        if latent_mask is None:
+            _check(self.lib.irodori_forward(self.ctx, B, S, _fp(x_t), _fp(t), _fp(v),
+                                            _fp(dbg) if debug else None))
+        else:
+            m = np.ascontiguousarray(latent_mask, np.uint8)
+            if m.shape != (B, S):
+                raise IrodoriError("Shape", "latent_mask must be [B, S]")
+            _check(self.lib.irodori_forward_masked(self.ctx, B, S, _fp(x_t), _fp(t),
+                                                   m.ctypes.data_as(C.POINTER(C.c_uint8)), _fp(v),
+                                                   _fp(dbg) if debug else None))
         return (v, dbg) if debug else v
 
     def block_forward(self, layer: int, x: np.ndarray, cond: np.ndarray) -> np.ndarray:
@@ -142,13 +153,24 @@ class HipInferenceEngine:
         _check(self.lib.irodori_block_forward(self.ctx, layer, B, S, _fp(x), _fp(_c32(cond))))
         return x
 
-    def sample(self, x0: np.ndarray, params: SamplerParams, has_speaker: bool = True) -> np.ndarray:
-        """Joint-CFG RF sampling of U utterances: x0 [U,S,P] -> x [U,S,P]."""
+    def sample(self, x0: np.ndarray, params: SamplerParams, has_speaker: bool = True,
+               lengths=None) -> np.ndarray:
+        """Joint-CFG RF sampling of U utterances: x0 [U,S,P] -> x [U,S,P].  lengths [U]
+        (optional): utterance u attends to its first lengths[u] latent frames (padded
+        variable-length batch)."""
         x0 = _c32(x0)
         U, S, P = x0.shape
         out = np.empty_like(x0)
         pc = sampler_params_c(params, has_speaker)
-        _check(self.lib.irodori_sample(self.ctx, C.byref(pc), U, S, _fp(x0), _fp(out)))
+        if lengths is None:
+            _check(self.lib.irodori_sample(self.ctx, C.byref(pc), U, S, _fp(x0), _fp(out)))
+        else:
+            ln = np.ascontiguousarray(lengths, np.int32)
+            if ln.shape != (U,):
+                raise IrodoriError("Shape", "lengths must be [U]")
+            _check(self.lib.irodori_sample_masked(self.ctx, C.byref(pc), U, S,
+                                                  ln.ctypes.data_as(C.POINTER(C.c_int32)),
+                                                  _fp(x0), _fp(out)))
         return out
 
     def sample_device(self, d_x0: int, d_out: int, utterances: int, seq: int,

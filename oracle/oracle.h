@@ -94,16 +94,16 @@ int orc_get_threads(void);
                    float* out);                                                             \
     void P##joint_attention(const orc_cfg* c, const orc_block* blk, const float* h, int B, \
                             int S, int T, const float* ctx_k, const float* ctx_v,          \
-                            const uint8_t* ctx_mask, const float* cos_t,                   \
-                            const float* sin_t, float* out);                                \
+                            const uint8_t* ctx_mask, const uint8_t* lat_mask,              \
+                            const float* cos_t, const float* sin_t, float* out);            \
     void P##block_forward(const orc_cfg* c, const orc_block* blk, float* x,                \
                           const float* cond, int B, int S, int T, const float* ctx_k,      \
-                          const float* ctx_v, const uint8_t* ctx_mask, const float* cos_t, \
-                          const float* sin_t);                                              \
+                          const float* ctx_v, const uint8_t* ctx_mask,                      \
+                          const uint8_t* lat_mask, const float* cos_t, const float* sin_t); \
     void P##forward(const orc_cfg* c, const orc_io* io, const orc_block* blocks, int B,    \
                     int S, const float* x_t, const float* t, int T, const float* ctx_k,    \
-                    const float* ctx_v, const uint8_t* ctx_mask, float* v_out,             \
-                    float* debug);                                                          \
+                    const float* ctx_v, const uint8_t* ctx_mask, const uint8_t* lat_mask,  \
+                    float* v_out, float* debug);                                            \
     void P##build_kv_cache(const orc_cfg* c, const float* k_norm, int B, const float* text,\
                            const uint8_t* text_mask, int Tt, int Dt, const float* wk_text,  \
                            const float* wv_text, const float* aux, const uint8_t* aux_mask,\
@@ -113,8 +113,9 @@ int orc_get_threads(void);
                             int U, int S, const float* x0, int T, const float* ctx_k_cond, \
                             const float* ctx_v_cond, const uint8_t* mask_cond,             \
                             const float* ctx_k_unc, const float* ctx_v_unc,                \
-                            const uint8_t* mask_unc, int num_steps, float scale,           \
-                            float min_t, float max_t, int max_steps_run, float* x_out);
+                            const uint8_t* mask_unc, const uint8_t* lat_mask,              \
+                            int num_steps, float scale, float min_t, float max_t,          \
+                            int max_steps_run, float* x_out);
 
 ORC_DECLARE(orc_f32_)
 ORC_DECLARE(orc_f64_)

@@ -73,6 +73,11 @@ def _u8(a: np.ndarray):
     return a.ctypes.data_as(_u8p)
 
 
+def _lat(mask):
+    """Optional latent key mask -> uint8 pointer (None = every latent key attends)."""
+    return None if mask is None else _u8(np.ascontiguousarray(mask, np.uint8))
+
+
 def _c32(a) -> np.ndarray:
     return np.ascontiguousarray(a, dtype=np.float32)
 
@@ -211,14 +216,14 @@ class Oracle:
         self._fn("swiglu")(_f(h), _f(_c32(w13)), _f(_c32(w2)), M, D, F, _f(out))
         return out
 
-    def joint_attention(self, cfg, blk, h, ctx_k, ctx_v, ctx_mask, cs, sn):
+    def joint_attention(self, cfg, blk, h, ctx_k, ctx_v, ctx_mask, cs, sn, latent_mask=None):
         h = _c32(h)
         B, S, _ = h.shape
         T = ctx_k.shape[1]
         out = np.empty_like(h)
         self._fn("joint_attention")(C.byref(self.cfg_struct(cfg)), C.byref(self.block_struct(blk)),
                                     _f(h), B, S, T, _f(_c32(ctx_k)), _f(_c32(ctx_v)),
-                                    _u8(np.ascontiguousarray(ctx_mask, np.uint8)),
+                                    _u8(np.ascontiguousarray(ctx_mask, np.uint8)), _lat(latent_mask),
                                     _f(_c32(cs)), _f(_c32(sn)), _f(out))
         return out
 
@@ -243,7 +248,7 @@ class Oracle:
         assert HD == cfg.num_heads * cfg.head_dim
         return ck, cv, cm
 
-    def block_forward(self, cfg, blk, x, cond, ctx_k, ctx_v, ctx_mask):
+    def block_forward(self, cfg, blk, x, cond, ctx_k, ctx_v, ctx_mask, latent_mask=None):
         """One DiffusionBlock on x [B,S,D] with cond [B,3D]; ctx_* of this layer [B,T,H,Dh]."""
         x = _c32(x).copy()
         B, S, _ = x.shape
@@ -251,13 +256,15 @@ class Oracle:
         cs, sn = self.rope_tables(S, cfg.head_dim, cfg.rope_theta)
         self._fn("block_forward")(C.byref(self.cfg_struct(cfg)), C.byref(self.block_struct(blk)),
                                   _f(x), _f(_c32(cond)), B, S, T, _f(_c32(ctx_k)), _f(_c32(ctx_v)),
-                                  _u8(np.ascontiguousarray(ctx_mask, np.uint8)), _f(cs), _f(sn))
+                                  _u8(np.ascontiguousarray(ctx_mask, np.uint8)), _lat(latent_mask),
+                                  _f(cs), _f(sn))
         return x
 
     # ---- model ---------------------------------------------------------------------
-    def forward(self, cfg, weights, x_t, t, ctx_k, ctx_v, ctx_mask, debug=False):
+    def forward(self, cfg, weights, x_t, t, ctx_k, ctx_v, ctx_mask, debug=False, latent_mask=None):
         """x_t [B,S,P]; t [B]; ctx_k/ctx_v [L,B,T,H,Dh]; ctx_mask [B,T] -> v [B,S,P]
-        (and [L+1,B,S,D] block outputs when debug)."""
+        (and [L+1,B,S,D] block outputs when debug).  latent_mask [B,S] (nonzero = key
+        attends) masks latent keys (attention.rs:730-750)."""
         x_t = _c32(x_t)
         B, S, Pd = x_t.shape
         T = ctx_k.shape[2]
@@ -267,12 +274,13 @@ class Oracle:
         self._fn("forward")(C.byref(self.cfg_struct(cfg)), C.byref(self.io_struct(weights.io)),
                             blocks, B, S, _f(x_t), _f(_c32(t)), T, _f(_c32(ctx_k)),
                             _f(_c32(ctx_v)), _u8(np.ascontiguousarray(ctx_mask, np.uint8)),
-                            _f(v), _f(dbg) if debug else None)
+                            _lat(latent_mask), _f(v), _f(dbg) if debug else None)
         return (v, dbg) if debug else v
 
     def sample_joint_cfg(self, cfg, weights, x0, ctx_cond, ctx_unc, num_steps, scale,
-                         min_t=0.0, max_t=1.0, max_steps_run=0):
-        """x0 [U,S,P]; ctx_* = (k [L,U,T,H,Dh], v, mask [U,T]).  Returns (x_out, steps_run)."""
+                         min_t=0.0, max_t=1.0, max_steps_run=0, latent_mask=None):
+        """x0 [U,S,P]; ctx_* = (k [L,U,T,H,Dh], v, mask [U,T]); latent_mask [U,S] or None.
+        Returns (x_out, steps_run)."""
         x0 = _c32(x0)
         U, S, Pd = x0.shape
         kc, vc, mc = ctx_cond
@@ -283,6 +291,7 @@ class Oracle:
         run = self._fn("sample_joint_cfg")(
             C.byref(self.cfg_struct(cfg)), C.byref(self.io_struct(weights.io)), blocks, U, S,
             _f(x0), T, _f(_c32(kc)), _f(_c32(vc)), _u8(np.ascontiguousarray(mc, np.uint8)),
-            _f(_c32(ku)), _f(_c32(vu)), _u8(np.ascontiguousarray(mu, np.uint8)), num_steps,
+            _f(_c32(ku)), _f(_c32(vu)), _u8(np.ascontiguousarray(mu, np.uint8)),
+            _lat(latent_mask), num_steps,
             C.c_float(scale), C.c_float(min_t), C.c_float(max_t), max_steps_run, _f(out))
         return out, int(run)

@@ -245,12 +245,13 @@ void P(swiglu)(const float* h, const float* w13, const float* w2, int M, int D, 
 
 /* attention.rs:272-425 (JointAttention::forward_fused with a KV cache):
  *   [q|k|v] = h @ W_qkv; q = rope_half(q_norm(q)); k = rope_half(k_norm(k));
- *   K = [k | ctx_k], V = [v | ctx_v], mask = [1]*S ++ ctx_mask;
+ *   K = [k | ctx_k], V = [v | ctx_v], mask = latent_mask ++ ctx_mask with latent_mask all
+ *   ones when absent (build_joint_mask, attention.rs:730-750);
  *   o = SDPA(q, K, V, mask, Dh^-0.5); out = (sigmoid(h @ W_gate) * o) @ W_o.
  * ctx_k/ctx_v: [B, T, H, Dh] (already k-normed, not rotated); ctx_mask: [B, T] (1 = attend). */
 void P(joint_attention)(const orc_cfg* c, const orc_block* blk, const float* h, int B, int S,
                         int T, const float* ctx_k, const float* ctx_v, const uint8_t* ctx_mask,
-                        const float* cos_t, const float* sin_t, float* out) {
+                        const uint8_t* lat_mask, const float* cos_t, const float* sin_t, float* out) {
     int D = c->model_dim, H = c->num_heads, Dh = c->head_dim, HD = H * Dh;
     int M = B * S, Skv = S + T;
     size_t szq = (size_t)M * HD;
@@ -294,7 +295,8 @@ void P(joint_attention)(const orc_cfg* c, const orc_block* blk, const float* h, 
                 }
         }
     for (int b = 0; b < B; b++) {
-        for (int s = 0; s < S; s++) mk[(size_t)b * Skv + s] = 1.0f;
+        for (int s = 0; s < S; s++)
+            mk[(size_t)b * Skv + s] = (lat_mask && !lat_mask[(size_t)b * S + s]) ? 0.0f : 1.0f;
         for (int j = 0; j < T; j++) mk[(size_t)b * Skv + S + j] = ctx_mask[(size_t)b * T + j] ? 1.0f : 0.0f;
     }
     P(sdpa)(qh, kh, vh, mk, B, H, S, Skv, Dh, (float)(R_C(1.0) / SQRT((R)Dh)), oh);
@@ -320,7 +322,8 @@ void P(joint_attention)(const orc_cfg* c, const orc_block* blk, const float* h, 
  * x: [B, S, D] updated in place; cond: [B, 3D]. */
 void P(block_forward)(const orc_cfg* c, const orc_block* blk, float* x, const float* cond, int B,
                       int S, int T, const float* ctx_k, const float* ctx_v,
-                      const uint8_t* ctx_mask, const float* cos_t, const float* sin_t) {
+                      const uint8_t* ctx_mask, const uint8_t* lat_mask, const float* cos_t,
+                      const float* sin_t) {
     int D = c->model_dim, F = c->mlp_hidden, M = B * S;
     size_t n = (size_t)M * D;
     float* shift = (float*)malloc(sizeof(float) * (size_t)B * D);
@@ -331,7 +334,7 @@ void P(block_forward)(const orc_cfg* c, const orc_block* blk, float* x, const fl
 
     P(adaln_vectors)(c, blk, 0, cond, B, shift, scale, gate);
     P(fused_adaln)(x, scale, shift, B, S, D, c->norm_eps, h);
-    P(joint_attention)(c, blk, h, B, S, T, ctx_k, ctx_v, ctx_mask, cos_t, sin_t, y);
+    P(joint_attention)(c, blk, h, B, S, T, ctx_k, ctx_v, ctx_mask, lat_mask, cos_t, sin_t, y);
     for (size_t i = 0; i < n; i++) {
         int b = (int)(i / ((size_t)S * D)), d = (int)(i % D);
         x[i] = (float)((R)x[i] + (R)gate[b * D + d] * (R)y[i]);
@@ -354,7 +357,7 @@ void P(block_forward)(const orc_cfg* c, const orc_block* blk, float* x, const fl
  * (BlockDebugOutputs, dit/model.rs:92-102). */
 void P(forward)(const orc_cfg* c, const orc_io* io, const orc_block* blocks, int B, int S,
                 const float* x_t, const float* t, int T, const float* ctx_k, const float* ctx_v,
-                const uint8_t* ctx_mask, float* v_out, float* debug) {
+                const uint8_t* ctx_mask, const uint8_t* lat_mask, float* v_out, float* debug) {
     int D = c->model_dim, Pd = c->latent_dim, L = c->num_layers, H = c->num_heads,
         Dh = c->head_dim;
     size_t n = (size_t)B * S * D, lay = (size_t)B * T * H * Dh;
@@ -369,7 +372,7 @@ void P(forward)(const orc_cfg* c, const orc_io* io, const orc_block* blocks, int
     if (debug) memcpy(debug, x, sizeof(float) * n);
     for (int l = 0; l < L; l++) {
         P(block_forward)(c, &blocks[l], x, cond, B, S, T, ctx_k + l * lay, ctx_v + l * lay,
-                         ctx_mask, cs, sn);
+                         ctx_mask, lat_mask, cs, sn);
         if (debug) memcpy(debug + (size_t)(l + 1) * n, x, sizeof(float) * n);
     }
     P(rms_norm)(x, io->out_norm_w, B * S, D, c->norm_eps, xn);
@@ -415,14 +418,15 @@ void P(build_kv_cache)(const orc_cfg* c, const float* k_norm, int B, const float
  *   t_i = 0.999 (1 - i/N);  CFG iff min_t <= t_i <= max_t;
  *   v_c = forward(x, t_i, cond KV); v_u = forward(x, t_i, uncond KV);
  *   v = v_c + scale (v_c - v_u);  x += v (t_{i+1} - t_i).
- * Two separate B=U forwards, exactly as the reference runs them.  Runs at most
+ * Two separate B=U forwards, exactly as the reference runs them.  lat_mask (nullable,
+ * [U, S]) masks latent keys of both forwards of utterance u (padded batches).  Runs at most
  * max_steps_run steps (<= 0: all); returns the number of steps run. */
 int P(sample_joint_cfg)(const orc_cfg* c, const orc_io* io, const orc_block* blocks, int U,
                         int S, const float* x0, int T, const float* ctx_k_cond,
                         const float* ctx_v_cond, const uint8_t* mask_cond,
                         const float* ctx_k_unc, const float* ctx_v_unc, const uint8_t* mask_unc,
-                        int num_steps, float scale, float min_t, float max_t, int max_steps_run,
-                        float* x_out) {
+                        const uint8_t* lat_mask, int num_steps, float scale, float min_t,
+                        float max_t, int max_steps_run, float* x_out) {
     int Pd = c->latent_dim;
     size_t n = (size_t)U * S * Pd;
     float* vc = (float*)malloc(sizeof(float) * n);
@@ -436,9 +440,9 @@ int P(sample_joint_cfg)(const orc_cfg* c, const orc_io* io, const orc_block* blo
         float tn = 0.999f * (1.0f - (float)(i + 1) / (float)num_steps);
         for (int u = 0; u < U; u++) tt[u] = t;
         int use_cfg = (min_t <= t) && (t <= max_t);
-        P(forward)(c, io, blocks, U, S, x_out, tt, T, ctx_k_cond, ctx_v_cond, mask_cond, vc, NULL);
+        P(forward)(c, io, blocks, U, S, x_out, tt, T, ctx_k_cond, ctx_v_cond, mask_cond, lat_mask, vc, NULL);
         if (use_cfg)
-            P(forward)(c, io, blocks, U, S, x_out, tt, T, ctx_k_unc, ctx_v_unc, mask_unc, vu, NULL);
+            P(forward)(c, io, blocks, U, S, x_out, tt, T, ctx_k_unc, ctx_v_unc, mask_unc, lat_mask, vu, NULL);
         float dt = tn - t;
         for (size_t j = 0; j < n; j++) {
             R v = (R)vc[j];

@@ -109,6 +109,25 @@ def test_sample_two_utterances_rows_independent(oracle64):
         assert rel_l2(both[u:u + 1], ref) < 1e-4
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("backend", [F32, BF16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("S", [37, 41, 64])
+def test_forward_identical_rows_are_bit_identical(backend, S):
+    # Every batch row computes the same function of its own inputs, so identical rows give
+    # identical outputs in any precision.  Odd S puts odd batch rows on odd token offsets
+    # (the V^T pair stores of the QKV epilogue once scrambled them there).
+    cfg = ih.cfg_tiny()
+    w = ih.DitWeights.random(cfg, 6, std=0.05, norm_jitter=0.1)
+    ctx = ih.make_context_kv(cfg, 1, 12, 9, seed=7).rows([0, 0, 0])
+    x = np.repeat(ih.make_noise(1, S, cfg.latent_dim, 8), 3, axis=0)
+    t = np.full(3, 0.6, np.float32)
+    with make_engine(cfg, backend, w, ctx, 3, S) as e:
+        v, dbg = e.forward_with_cond_cached(x, t, debug=True)
+    for b in (1, 2):
+        assert np.array_equal(dbg[:, b], dbg[:, 0]), f"row {b} differs from row 0"
+        assert np.array_equal(v[b], v[0])
+
+
 def test_sample_cfg_window_off_equals_scale_zero():
     # min_t above every t_i disables CFG (euler_sampler.rs:379) == scale 0.
     cfg = ih.cfg_tiny()
@@ -175,11 +194,67 @@ def test_cfg4_sample_40_steps_bf16_vs_golden(cfg4):
     cfg, w, ctx, x0 = cfg4
     with make_engine(cfg, BF16, w, ctx, 2, 750) as e:
         got = e.sample(x0, joint_params(40))
-        # At this shape the GEMMs split their tail tiles over K; the fixed-order
-        # reduction keeps replays bit-identical.
-        again = e.sample(x0, joint_params(40))
+        again = e.sample(x0, joint_params(40))  # graph replays are bit-identical
     assert np.array_equal(got, again)
     ref = np.load(path)
     err = rel_l2(got, ref)
     print("cfg4 bf16 40-step final latent rel L2 %.3e" % err)
     assert err < 2e-2
+
+
+# ---- latent key mask (attention.rs:730-750; config 5's padded batches) -------------------
+
+def _latent_mask(B, S, lengths, holes=()):
+    m = np.zeros((B, S), np.uint8)
+    for b, n in enumerate(lengths):
+        m[b, :n] = 1
+    for b, s in holes:
+        m[b, s] = 0
+    return m
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("backend", [F32, BF16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("name", ["tiny", "cfg1"])
+def test_forward_latent_mask_vs_oracle(oracle64, name, backend):
+    make_cfg, S, tt, ts, std, jit = SMALL[name]
+    cfg = make_cfg()
+    w = ih.DitWeights.random(cfg, 3, std=std, norm_jitter=jit)
+    ctx = ih.make_context_kv(cfg, 1, tt, ts, seed=4)
+    x = ih.make_noise(2, S, cfg.latent_dim, 5)
+    t = np.array([0.8, 0.45], np.float32)
+    # row 0: isolated masked keys (first, middle, last tile positions); row 1: a masked
+    # tail of 19 keys plus one hole
+    m = _latent_mask(2, S, [S, S - 19], holes=[(0, 1), (0, S // 2), (0, S - 1), (1, 7)])
+    with make_engine(cfg, backend, w, ctx, 2, S) as e:
+        v, dbg = e.forward_with_cond_cached(x, t, debug=True, latent_mask=m)
+        v_plain = e.forward_with_cond_cached(x, t)
+    v_ref, dbg_ref = oracle64.forward(cfg, w, x, t, ctx.k, ctx.v, ctx.mask, debug=True, latent_mask=m)
+    errs = [rel_l2(dbg[i], dbg_ref[i]) for i in range(dbg.shape[0])]
+    print(name, backend.value, "masked per-block rel L2:", ["%.2e" % x for x in errs])
+    assert max(errs) < TOL_BLOCK[backend]
+    assert rel_l2(v, v_ref) < TOL_BLOCK[backend]
+    assert rel_l2(v, v_plain) > 1e-3  # the mask reached the attention
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("backend", [F32, BF16], ids=["f32", "bf16"])
+def test_sample_padded_batch_matches_unpadded(backend):
+    # Two utterances padded to 64 frames, the second only 41 long: its first 41 frames
+    # equal an unpadded 41-frame run of that utterance alone.
+    cfg = ih.cfg_cpu_plumbing()
+    w = ih.DitWeights.random(cfg, 0)
+    ctx = ih.make_context_kv(cfg, 2, 16, 32, seed=1)
+    x0 = ih.make_noise(2, 64, cfg.latent_dim, 2)
+    p = joint_params(4)
+    n = 41
+    with make_engine(cfg, backend, w, ctx, 4, 64) as e:
+        padded = e.sample(x0, p, lengths=[64, n])
+        full = e.sample(x0, p)
+    with make_engine(cfg, backend, w, ctx.rows([2, 3]), 2, 64) as e:
+        short = e.sample(x0[1:2, :n], p)
+    assert rel_l2(padded[1:2, :n], short) < 1e-6
+    assert rel_l2(padded[0:1], full[0:1]) < 1e-6  # full-length utterance unaffected
+    with pytest.raises(ih.IrodoriError):
+        with make_engine(cfg, backend, w, ctx, 4, 64) as e:
+            e.sample(x0, p, lengths=[64, 65])

@@ -306,3 +306,54 @@ def test_sampler_one_step_is_cfg_euler(oracle64):
                                        (unc.k, unc.v, unc.mask), 1, 2.0)
     want = x0 + (vc + 2.0 * (vc - vu)) * (0.0 - 0.999)
     assert np.allclose(out, want, atol=1e-6)
+
+
+# ---- latent key mask (build_joint_mask, attention.rs:730-750) ---------------------------
+
+def _latent_mask(B, S, lengths, holes=()):
+    m = np.zeros((B, S), np.uint8)
+    for b, n in enumerate(lengths):
+        m[b, :n] = 1
+    for b, s in holes:
+        m[b, s] = 0
+    return m
+
+
+def test_latent_mask_matches_torch_library(oracle64):
+    # Masked latent keys via torch's scaled_dot_product_attention attn_mask (an independent
+    # library route) — a dropped or inverted mask fails here.
+    cfg, w, ctx, x = _tiny_setup(seed=11, S=24)
+    t = np.array([0.7, 0.3], np.float32)
+    m = _latent_mask(2, 24, [24, 17], holes=[(0, 3), (0, 20), (1, 5)])
+    v64 = oracle64.forward(cfg, w, x, t, ctx.k, ctx.v, ctx.mask, latent_mask=m)
+    vt = tref.forward(cfg, w, x, t, ctx.k, ctx.v, ctx.mask, latent_mask=m)
+    assert rel_l2(v64, vt) < 1e-6
+    # and it changes the result (the mask is not ignored)
+    v_nomask = oracle64.forward(cfg, w, x, t, ctx.k, ctx.v, ctx.mask)
+    assert rel_l2(v64, v_nomask) > 1e-3
+
+
+def test_latent_mask_equals_dropping_the_padding(oracle64):
+    # A padded row with its padding masked equals the unpadded row on its valid frames:
+    # masked keys contribute exp(-inf) = 0 exactly, every other operator is per frame.
+    cfg, w, ctx, x = _tiny_setup(seed=12, S=24)
+    t = np.array([0.6, 0.6], np.float32)
+    n = 15
+    m = _latent_mask(2, 24, [24, n])
+    padded = oracle64.forward(cfg, w, x, t, ctx.k, ctx.v, ctx.mask, latent_mask=m)
+    c = ctx.rows([1])
+    short = oracle64.forward(cfg, w, x[1:2, :n], t[1:2], c.k, c.v, c.mask)
+    assert np.array_equal(padded[1:2, :n], short)
+
+
+def test_sampler_latent_mask_equals_unpadded(oracle64):
+    cfg, w, ctx, x = _tiny_setup(seed=13, S=20)
+    cond, unc = ctx.rows([0]), ctx.rows([1])
+    n = 13
+    m = _latent_mask(1, 20, [n])
+    x0 = x[:1]
+    padded, _ = oracle64.sample_joint_cfg(cfg, w, x0, (cond.k, cond.v, cond.mask),
+                                          (unc.k, unc.v, unc.mask), 4, 2.0, latent_mask=m)
+    short, _ = oracle64.sample_joint_cfg(cfg, w, x0[:, :n], (cond.k, cond.v, cond.mask),
+                                         (unc.k, unc.v, unc.mask), 4, 2.0)
+    assert np.array_equal(padded[:, :n], short)

@@ -64,7 +64,7 @@ def adaln(x, cond_chunks, blk, which, eps):
     return h, torch.tanh(gate)[:, None, :]
 
 
-def joint_attention(h, blk, ctx_k, ctx_v, ctx_mask, cos, sin, H, Dh, eps):
+def joint_attention(h, blk, ctx_k, ctx_v, ctx_mask, cos, sin, H, Dh, eps, latent_mask=None):
     B, S, D = h.shape
     HD = H * Dh
     qkv = lin(h, blk["w_qkv"])
@@ -81,7 +81,8 @@ def joint_attention(h, blk, ctx_k, ctx_v, ctx_mask, cos, sin, H, Dh, eps):
     k = torch.cat([rope(k[:, :, :hh], cos, sin), k[:, :, hh:]], dim=2)
     K = torch.cat([k, T(ctx_k)], dim=1).transpose(1, 2)
     V = torch.cat([v, T(ctx_v)], dim=1).transpose(1, 2)
-    valid = torch.cat([torch.ones(B, S, dtype=torch.bool), T(ctx_mask) > 0], dim=1)
+    lat = torch.ones(B, S, dtype=torch.bool) if latent_mask is None else T(latent_mask) > 0
+    valid = torch.cat([lat, T(ctx_mask) > 0], dim=1)
     o = F.scaled_dot_product_attention(q.transpose(1, 2), K, V,
                                        attn_mask=valid[:, None, None, :])
     o = o.transpose(1, 2).reshape(B, S, HD)
@@ -94,7 +95,7 @@ def swiglu(h, w13, w2):
     return lin(F.silu(u[..., :Fh]) * u[..., Fh:], w2)
 
 
-def forward(cfg, weights, x_t, t, ctx_k, ctx_v, ctx_mask, debug=False):
+def forward(cfg, weights, x_t, t, ctx_k, ctx_v, ctx_mask, debug=False, latent_mask=None):
     io = weights.io
     D, H, Dh, eps = cfg.model_dim, cfg.num_heads, cfg.head_dim, cfg.norm_eps
     x_t = T(x_t)
@@ -107,7 +108,8 @@ def forward(cfg, weights, x_t, t, ctx_k, ctx_v, ctx_mask, debug=False):
     outs = [x.clone()]
     for l, blk in enumerate(weights.blocks):
         h1, g1 = adaln(x, chunks, blk, 0, eps)
-        x = x + g1 * joint_attention(h1, blk, ctx_k[l], ctx_v[l], ctx_mask, cos, sin, H, Dh, eps)
+        x = x + g1 * joint_attention(h1, blk, ctx_k[l], ctx_v[l], ctx_mask, cos, sin, H, Dh, eps,
+                                     latent_mask)
         h2, g2 = adaln(x, chunks, blk, 1, eps)
         x = x + g2 * swiglu(h2, blk["w13"], blk["w2"])
         outs.append(x.clone())
