@@ -23,8 +23,69 @@ PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "w13_gemm_config4_hbm_traffic.txt")
+W13_KERNEL = "gemm_kernelIDF16bLi128ELi128ELi2ELi2ELi2ELi2E"  # bf16 128x128, EPI_SWIGLU
+COPY_BYTES = 1 << 30  # the --copy-calibration copy: reads and writes 1 GiB
+
+
 def log(msg):
     print("[bench] " + msg, file=sys.stderr, flush=True)
+
+
+def pmc_summary(fetch_csv, write_csv):
+    """Text summary of two rocprofv3 --pmc runs of this script (FETCH_SIZE, then
+    WRITE_SIZE, with --copy-calibration): per-kernel KiB per dispatch, the scale factors
+    that make the 1 GiB copy read 1 GiB and write 1 GiB, and the calibrated HBM bytes per
+    launch of the SwiGLU up-projection GEMM."""
+    import csv
+    per = {}
+    for counter, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
+        for r in csv.DictReader(open(path)):
+            if r["Counter_Name"] != counter:
+                continue
+            per.setdefault(counter, {}).setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+    lines, factor = [], {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        copies = per[counter].get("__amd_rocclr_copyBuffer", [])
+        kib = max(copies) if copies else 0.0
+        if kib < 0.25 * COPY_BYTES / 1024:
+            raise SystemExit("no 1 GiB calibration copy in %s (run with --copy-calibration)" % counter)
+        factor[counter] = COPY_BYTES / (kib * 1024.0)
+        lines.append("%s calibration: the 1 GiB copy counts %.1f KiB -> factor %.4f bytes per counted byte"
+                     % (counter, kib, factor[counter]))
+    lines.append("")
+    lines.append("%-72s %6s %14s %14s %12s" % ("kernel", "calls", "FETCH KiB/disp", "WRITE KiB/disp", "MB/disp cal."))
+    names = sorted(set(per["FETCH_SIZE"]) | set(per["WRITE_SIZE"]),
+                   key=lambda n: -sum(per["FETCH_SIZE"].get(n, [0.0])) / max(len(per["FETCH_SIZE"].get(n, [1])), 1))
+    w13 = None
+    for n in names:
+        f = per["FETCH_SIZE"].get(n, [0.0])
+        wv = per["WRITE_SIZE"].get(n, [0.0])
+        fa, wa = sum(f) / len(f), sum(wv) / len(wv)
+        cal = (fa * factor["FETCH_SIZE"] + wa * factor["WRITE_SIZE"]) * 1024.0
+        short = n.replace("_ZN7irodori12_GLOBAL__N_1", "").replace("irodori::(anonymous namespace)::", "")
+        short = short if len(short) <= 72 else short[:69] + "..."
+        lines.append("%-72s %6d %14.1f %14.1f %12.2f" % (short, len(f), fa, wa, cal / 1e6))
+        if W13_KERNEL in n:
+            w13 = (fa * factor["FETCH_SIZE"] * 1024.0, wa * factor["WRITE_SIZE"] * 1024.0)
+    if w13 is None:
+        raise SystemExit("SwiGLU GEMM kernel %s not found in the counter files" % W13_KERNEL)
+    lines.append("")
+    lines.append("w13_fetch_bytes_per_launch: %d" % round(w13[0]))
+    lines.append("w13_write_bytes_per_launch: %d" % round(w13[1]))
+    lines.append("traffic_bytes_per_launch: %d" % round(w13[0] + w13[1]))
+    return "\n".join(lines)
+
+
+def read_traffic():
+    """Calibrated HBM bytes per w13 launch from the committed PMC summary, or None."""
+    try:
+        for line in open(TRAFFIC_FILE):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
 
 
 def main():
@@ -39,7 +100,13 @@ def main():
                     help="also run one 1 GiB device-to-device copy (the known-size kernel that "
                          "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings; 32x the L2, so "
                          "cache residency does not skew it)")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="print the calibrated traffic summary of two rocprofv3 --pmc "
+                         "counter_collection.csv files of this script and exit")
     args = ap.parse_args()
+    if args.pmc_summary:
+        print(pmc_summary(*args.pmc_summary))
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the RF step of one model instance "
               "runs on one MI355X; multi-GPU sharding is by utterance and is not part of this "
@@ -109,6 +176,7 @@ def main():
         (kt["w13_gemm_us"] + kt["w2_gemm_us"]) * 1e-6) / (PEAK_BF16_TFLOPS * 1e12)
     dom = "w13_gemm"  # largest single kernel of the step (SwiGLU up-projection)
     achieved = flops[dom] / (kt[dom + "_us"] * 1e-6) / 1e12
+    w13_bytes = 2 * (M * D + 2 * F * D + M * F)  # bf16 h, W13, U once each
     norm_bytes = M * D * 4 + M * D * 2  # read x f32, write h bf16
     norm_gbs = norm_bytes / (kt["norm_mod_us"] * 1e-6) / 1e9
 
@@ -156,7 +224,10 @@ def main():
         "norm_mod_gbs": round(norm_gbs, 1),
         "roofline": {"kernel": "w13_gemm (SwiGLU up-projection, 1500x1024x5632)", "bound": "mfma",
                      "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None},
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": read_traffic(),
+                     "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, "
+                                     "copy-calibrated; profiles/w13_gemm_config4_hbm_traffic.txt)",
+                     "algorithmic_bytes": w13_bytes},
         "cpu_baseline": cpu,
     }
     eng.close()
