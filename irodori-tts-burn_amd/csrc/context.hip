@@ -108,6 +108,10 @@ struct irodori_ctx {
     bool bf16 = true;
     size_t esz = 2;  // compute element size
     hipStream_t stream = nullptr;
+    // Second capture stream and fork/join events: a captured RF step runs the two halves
+    // of the batch rows as independent chains of kernels until the output head.
+    hipStream_t stream2 = nullptr;
+    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
     std::vector<void*> allocs;
     uint64_t dev_bytes = 0;
 
@@ -297,13 +301,26 @@ int enqueue_mod_table(irodori_ctx* c, int nvec, bool skip_mlp) {
     return check_launch("modulation table");
 }
 
+// One DiT block over batch rows [r0, r0 + B) of the context's buffers, on stream st.
+// Every row-indexed buffer is offset to row r0; mt must map the slice's local row b to
+// the vector of global row r0 + b (rows_per_vec == 1 with the table offset, or all rows
+// sharing one vector).
 template <typename T>
-int enqueue_layer(irodori_ctx* c, int l, int B, int S, const ModTable& mt, bool last_norm) {
+int enqueue_layer(irodori_ctx* c, int l, int B, int S, const ModTable& mt, bool last_norm, int r0,
+                  hipStream_t st) {
     const auto& g = c->cfg;
-    int D = g.model_dim, H = g.num_heads, F = g.mlp_hidden, M = B * S;
+    int D = g.model_dim, H = g.num_heads, F = g.mlp_hidden, M = B * S, Dh = g.head_dim;
     auto& lb = c->layers[l];
-    hipStream_t st = c->stream;
-    T* h = static_cast<T*>(c->h);
+    const int vt_stride = (S + 63) / 64 * 64;
+    const size_t tok0 = (size_t)r0 * S;  // first token row of the slice
+    T* h = static_cast<T*>(c->h) + tok0 * D;
+    float* x = c->x + tok0 * D;
+    T* q = static_cast<T*>(c->q) + (size_t)r0 * H * S * Dh;
+    T* ks = static_cast<T*>(c->ks) + (size_t)r0 * H * S * Dh;
+    T* vs = static_cast<T*>(c->vs) + (size_t)r0 * H * Dh * vt_stride;
+    T* gate = static_cast<T*>(c->gate) + tok0 * D;
+    T* o = static_cast<T*>(c->o) + tok0 * D;
+    T* u = static_cast<T*>(c->u) + tok0 * F;
 
     GemmArgs<T> ga{};
     ga.mt = mt;
@@ -319,49 +336,50 @@ int enqueue_layer(irodori_ctx* c, int l, int B, int S, const ModTable& mt, bool 
     ga.W = static_cast<const T*>(lb.w_qkvg);
     ga.N = 4 * D;
     ga.K = D;
-    ga.Q = static_cast<T*>(c->q);
-    ga.Kd = static_cast<T*>(c->ks);
-    ga.Vd = static_cast<T*>(c->vs);
-    ga.G = static_cast<T*>(c->gate);
+    ga.Q = q;
+    ga.Kd = ks;
+    ga.Vd = vs;
+    ga.G = gate;
     ga.q_norm = lb.q_norm;
     ga.k_norm = lb.k_norm;
     ga.rope_cos = c->rope_cos;
     ga.rope_sin = c->rope_sin;
-    ga.vt_stride = (S + 63) / 64 * 64;
+    ga.vt_stride = vt_stride;
     ga.q_scale = 1.4426950408889634f / sqrtf((float)g.head_dim);
     if (launch_gemm<T>(EPI_QKVG, ga, st)) { set_last_error("qkvg gemm shape"); return IRODORI_ERR_SHAPE; }
 
     // Joint attention over [latent self | cached ctx] (attention.rs:349-425).
     AttnArgs<T> aa{};
-    aa.Q = static_cast<const T*>(c->q);
-    aa.K0 = static_cast<const T*>(c->ks);
-    aa.V0 = static_cast<const T*>(c->vs);
+    aa.Q = q;
+    aa.K0 = ks;
+    aa.V0 = vs;
     aa.len0 = S;
     aa.stride0 = S;
     aa.v_transposed = true;
     aa.prescaled = true;
-    aa.vstride0 = (S + 63) / 64 * 64;
+    aa.vstride0 = vt_stride;
     if (c->t_ctx > 0) {
-        aa.K1 = static_cast<const T*>(lb.ctx_k);
-        aa.V1 = static_cast<const T*>(lb.ctx_v);
+        const int T1 = g.max_ctx, vs1 = (g.max_ctx + 63) / 64 * 64, nt1 = (g.max_ctx + 63) / 64;
+        aa.K1 = static_cast<const T*>(lb.ctx_k) + (size_t)r0 * H * T1 * Dh;
+        aa.V1 = static_cast<const T*>(lb.ctx_v) + (size_t)r0 * H * Dh * vs1;
         aa.len1 = c->t_ctx;
-        aa.stride1 = g.max_ctx;
-        aa.vstride1 = (g.max_ctx + 63) / 64 * 64;
-        aa.mask1 = lb.ctx_mask;
-        aa.tile_on1 = lb.tile_on;
-        aa.bits1 = lb.tile_bits;
+        aa.stride1 = T1;
+        aa.vstride1 = vs1;
+        aa.mask1 = lb.ctx_mask + (size_t)r0 * T1;
+        aa.tile_on1 = lb.tile_on + (size_t)r0 * nt1;
+        aa.bits1 = lb.tile_bits + (size_t)r0 * nt1;
     }
     if (c->lat_on) {
-        aa.mask0 = c->lat_mask_f;
-        aa.bits0 = c->lat_bits;
+        aa.mask0 = c->lat_mask_f + tok0;
+        aa.bits0 = c->lat_bits + (size_t)r0 * ((S + 63) / 64);
     }
     aa.B = B;
     aa.H = H;
     aa.Sq = S;
     aa.scale = 1.0f / sqrtf((float)g.head_dim);
     aa.out_mode = 0;
-    aa.G = static_cast<const T*>(c->gate);
-    aa.O = static_cast<T*>(c->o);
+    aa.G = gate;
+    aa.O = o;
     int arc;
     if constexpr (std::is_same<T, bf16>::value)
         arc = launch_attention32(aa, st);
@@ -370,27 +388,27 @@ int enqueue_layer(irodori_ctx* c, int l, int B, int S, const ModTable& mt, bool 
     if (arc) { set_last_error("attention launch rejected the shape"); return IRODORI_ERR_SHAPE; }
 
     // x += g_attn * (o @ Wo) (attention.rs:424, diffusion.rs:98).
-    ga.A = static_cast<const T*>(c->o);
+    ga.A = o;
     ga.W = static_cast<const T*>(lb.w_o);
     ga.N = D;
     ga.K = D;
-    ga.x = c->x;
+    ga.x = x;
     ga.kind = 0;
     if (launch_gemm<T>(EPI_RESID, ga, st)) { set_last_error("wo gemm shape"); return IRODORI_ERR_SHAPE; }
 
     // h2 = mlp adaLN(x) (diffusion.rs:101-102).
-    launch_norm_mod<T>(c->x, h, M, S, D, g.norm_eps, mt, l, 1, st);
+    launch_norm_mod<T>(x, h, M, S, D, g.norm_eps, mt, l, 1, st);
 
     // m = silu(h2 W1) * (h2 W3) (feed_forward.rs:76-84).
     ga.A = h;
     ga.W = static_cast<const T*>(lb.w13);
     ga.N = 2 * F;
     ga.K = D;
-    ga.U = static_cast<T*>(c->u);
+    ga.U = u;
     if (launch_gemm<T>(EPI_SWIGLU, ga, st)) { set_last_error("w13 gemm shape"); return IRODORI_ERR_SHAPE; }
 
     // x += g_mlp * (m @ W2) (diffusion.rs:104).
-    ga.A = static_cast<const T*>(c->u);
+    ga.A = u;
     ga.W = static_cast<const T*>(lb.w2);
     ga.N = D;
     ga.K = F;
@@ -398,12 +416,15 @@ int enqueue_layer(irodori_ctx* c, int l, int B, int S, const ModTable& mt, bool 
     if (launch_gemm<T>(EPI_RESID, ga, st)) { set_last_error("w2 gemm shape"); return IRODORI_ERR_SHAPE; }
 
     // Next block's attention adaLN.
-    if (!last_norm) launch_norm_mod<T>(c->x, h, M, S, D, g.norm_eps, mt, l + 1, 0, st);
+    if (!last_norm) launch_norm_mod<T>(x, h, M, S, D, g.norm_eps, mt, l + 1, 0, st);
     return check_launch("layer");
 }
 
-int enqueue_layer_any(irodori_ctx* c, int l, int B, int S, const ModTable& mt, bool last) {
-    return c->bf16 ? enqueue_layer<bf16>(c, l, B, S, mt, last) : enqueue_layer<float>(c, l, B, S, mt, last);
+int enqueue_layer_any(irodori_ctx* c, int l, int B, int S, const ModTable& mt, bool last, int r0 = 0,
+                      hipStream_t st = nullptr) {
+    if (!st) st = c->stream;
+    return c->bf16 ? enqueue_layer<bf16>(c, l, B, S, mt, last, r0, st)
+                   : enqueue_layer<float>(c, l, B, S, mt, last, r0, st);
 }
 
 int enqueue_inproj(irodori_ctx* c, int B, int S, int rows_per_src, const ModTable& mt) {
@@ -418,12 +439,26 @@ int enqueue_inproj(irodori_ctx* c, int B, int S, int rows_per_src, const ModTabl
 }
 
 // All kernels of one RF step (Joint CFG, B = 2U rows): in_proj, L blocks, output head +
-// CFG combine + Euler update, step advance.
+// CFG combine + Euler update, step advance.  Rows never interact inside the blocks, so
+// the L blocks run as two independent chains, rows [0, B/2) on the context's stream and
+// rows [B/2, B) on the second stream, forked after in_proj and joined before the head:
+// in a captured graph the two chains overlap each other's launch gaps, tails and uneven
+// attention work (the conditioned row attends to the context, the unconditioned one does
+// not).  Every row shares the step's modulation vector.
 int enqueue_rf_step(irodori_ctx* c, int B, int S, float scale) {
     const auto& g = c->cfg;
     ModTable mt{c->tab, c->step, 1, B, g.num_layers};
     IRO_TRY(enqueue_inproj(c, B, S, 2, mt));
-    for (int l = 0; l < g.num_layers; l++) IRO_TRY(enqueue_layer_any(c, l, B, S, mt, l + 1 == g.num_layers));
+    const int half = B / 2;
+    IRO_HIP_CHECK(hipEventRecord(c->ev_fork, c->stream));
+    IRO_HIP_CHECK(hipStreamWaitEvent(c->stream2, c->ev_fork, 0));
+    for (int l = 0; l < g.num_layers; l++) {
+        const bool last = l + 1 == g.num_layers;
+        IRO_TRY(enqueue_layer_any(c, l, half, S, mt, last, 0, c->stream));
+        IRO_TRY(enqueue_layer_any(c, l, B - half, S, mt, last, half, c->stream2));
+    }
+    IRO_HIP_CHECK(hipEventRecord(c->ev_join, c->stream2));
+    IRO_HIP_CHECK(hipStreamWaitEvent(c->stream, c->ev_join, 0));
     FinalArgs fa{};
     fa.x = c->x;
     fa.norm_w = c->out_norm_w;
@@ -533,6 +568,10 @@ int irodori_ctx_destroy(irodori_ctx* c) {
     if (c->stream) (void)hipStreamSynchronize(c->stream);
     for (auto& kv : c->graphs) (void)hipGraphExecDestroy(kv.second);
     for (void* p : c->allocs) (void)hipFree(p);
+    if (c->stream2) (void)hipStreamSynchronize(c->stream2);
+    if (c->ev_fork) (void)hipEventDestroy(c->ev_fork);
+    if (c->ev_join) (void)hipEventDestroy(c->ev_join);
+    if (c->stream2) (void)hipStreamDestroy(c->stream2);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
     return IRODORI_OK;
@@ -571,6 +610,9 @@ int irodori_ctx_create(int device, const irodori_dit_config* cfg, irodori_ctx** 
     c->bf16 = g.compute_dtype == IRODORI_DTYPE_BF16;
     c->esz = c->bf16 ? 2 : 4;
     IRO_HIP_CHECK(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
+    IRO_HIP_CHECK(hipStreamCreateWithFlags(&c->stream2, hipStreamNonBlocking));
+    IRO_HIP_CHECK(hipEventCreateWithFlags(&c->ev_fork, hipEventDisableTiming));
+    IRO_HIP_CHECK(hipEventCreateWithFlags(&c->ev_join, hipEventDisableTiming));
 
     int D = g.model_dim, F = g.mlp_hidden, H = g.num_heads, Dh = g.head_dim, L = g.num_layers;
     int R = g.max_rows, S = g.max_seq, T = g.max_ctx > 0 ? g.max_ctx : 1, P = g.latent_dim;
