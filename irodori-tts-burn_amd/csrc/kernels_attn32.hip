@@ -381,6 +381,12 @@ int launch_attention32(const AttnArgs<bf16>& a, hipStream_t st) {
     if ((a.vstride0 % KT) || (a.K1 && (a.vstride1 % KT))) return -1;
     const int ntiles = (a.len0 + KT - 1) / KT + (a.K1 ? (a.len1 + KT - 1) / KT : 0);
     if (ntiles > 64) return -1;  // the tile list holds one entry per lane (4096 keys)
+    // Latency vs throughput: when 2 query blocks x 2 key parities (4 waves, 64 KB LDS)
+    // need at most one workgroup per CU, the smaller workgroups finish sooner (one CFG row
+    // of 750 frames: 18.2 vs 21.1 us with context keys, 12.3 vs 14.5 us without); larger
+    // launches keep 4 x 2.
+    const long wg22 = (long)((a.Sq + 63) / 64) * a.H * a.B;
+    if (wg22 <= 256) return launch_attn32_cfg<2, 2>(a, st);
     return launch_attn32_cfg<4, 2>(a, st);
 }
 
