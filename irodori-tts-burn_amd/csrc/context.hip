@@ -301,15 +301,30 @@ int enqueue_mod_table(irodori_ctx* c, int nvec, bool skip_mlp) {
     return check_launch("modulation table");
 }
 
-// One DiT block over batch rows [r0, r0 + B) of the context's buffers, on stream st.
-// Every row-indexed buffer is offset to row r0; mt must map the slice's local row b to
-// the vector of global row r0 + b (rows_per_vec == 1 with the table offset, or all rows
-// sharing one vector).
+// The kernels of one DiT block (diffusion.rs:62-105), in launch order.  The block's
+// first adaLN (attention modulation) is launched by the previous block's PART_NORM_NEXT
+// or by in_proj.
+enum LayerPart {
+    PART_QKVG = 0,       // QKV + gate projection, head norms, half RoPE, V^T
+    PART_ATTN = 1,       // joint attention + output gate
+    PART_WO = 2,         // x += g_attn * (o @ W_o)
+    PART_NORM_MLP = 3,   // mlp adaLN
+    PART_W13 = 4,        // SwiGLU up-projection
+    PART_W2 = 5,         // x += g_mlp * (m @ W2)
+    PART_NORM_NEXT = 6,  // next block's attention adaLN (none after the last block)
+    PART_COUNT = 7
+};
+
+// One kernel of a DiT block over batch rows [r0, r0 + B) of the context's buffers, on
+// stream st.  Every row-indexed buffer is offset to row r0; mt must map the slice's local
+// row b to the vector of global row r0 + b (rows_per_vec == 1 with the table offset, or
+// all rows sharing one vector).
 template <typename T>
-int enqueue_layer(irodori_ctx* c, int l, int B, int S, const ModTable& mt, bool last_norm, int r0,
-                  hipStream_t st) {
+int enqueue_part(irodori_ctx* c, int l, int B, int S, const ModTable& mt, int part, int r0,
+                 hipStream_t st) {
     const auto& g = c->cfg;
-    int D = g.model_dim, H = g.num_heads, F = g.mlp_hidden, M = B * S, Dh = g.head_dim;
+    const int D = g.model_dim, H = g.num_heads, F = g.mlp_hidden, M = B * S, Dh = g.head_dim;
+    const bool last = l + 1 == g.num_layers;
     auto& lb = c->layers[l];
     const int vt_stride = (S + 63) / 64 * 64;
     const size_t tok0 = (size_t)r0 * S;  // first token row of the slice
@@ -330,101 +345,132 @@ int enqueue_layer(irodori_ctx* c, int l, int B, int S, const ModTable& mt, bool 
     ga.D = D;
     ga.eps = g.norm_eps;
     ga.M = M;
-
-    // QKV + gate projection with head norms and half RoPE (attention.rs:293-345, :423).
-    ga.A = h;
-    ga.W = static_cast<const T*>(lb.w_qkvg);
-    ga.N = 4 * D;
-    ga.K = D;
-    ga.Q = q;
-    ga.Kd = ks;
-    ga.Vd = vs;
-    ga.G = gate;
-    ga.q_norm = lb.q_norm;
-    ga.k_norm = lb.k_norm;
-    ga.rope_cos = c->rope_cos;
-    ga.rope_sin = c->rope_sin;
-    ga.vt_stride = vt_stride;
-    ga.q_scale = 1.4426950408889634f / sqrtf((float)g.head_dim);
-    if (launch_gemm<T>(EPI_QKVG, ga, st)) { set_last_error("qkvg gemm shape"); return IRODORI_ERR_SHAPE; }
-
-    // Joint attention over [latent self | cached ctx] (attention.rs:349-425).
-    AttnArgs<T> aa{};
-    aa.Q = q;
-    aa.K0 = ks;
-    aa.V0 = vs;
-    aa.len0 = S;
-    aa.stride0 = S;
-    aa.v_transposed = true;
-    aa.prescaled = true;
-    aa.vstride0 = vt_stride;
-    if (c->t_ctx > 0) {
-        const int T1 = g.max_ctx, vs1 = (g.max_ctx + 63) / 64 * 64, nt1 = (g.max_ctx + 63) / 64;
-        aa.K1 = static_cast<const T*>(lb.ctx_k) + (size_t)r0 * H * T1 * Dh;
-        aa.V1 = static_cast<const T*>(lb.ctx_v) + (size_t)r0 * H * Dh * vs1;
-        aa.len1 = c->t_ctx;
-        aa.stride1 = T1;
-        aa.vstride1 = vs1;
-        aa.mask1 = lb.ctx_mask + (size_t)r0 * T1;
-        aa.tile_on1 = lb.tile_on + (size_t)r0 * nt1;
-        aa.bits1 = lb.tile_bits + (size_t)r0 * nt1;
-    }
-    if (c->lat_on) {
-        aa.mask0 = c->lat_mask_f + tok0;
-        aa.bits0 = c->lat_bits + (size_t)r0 * ((S + 63) / 64);
-    }
-    aa.B = B;
-    aa.H = H;
-    aa.Sq = S;
-    aa.scale = 1.0f / sqrtf((float)g.head_dim);
-    aa.out_mode = 0;
-    aa.G = gate;
-    aa.O = o;
-    int arc;
-    if constexpr (std::is_same<T, bf16>::value)
-        arc = launch_attention32(aa, st);
-    else
-        arc = launch_attention<T, 64>(aa, st);
-    if (arc) { set_last_error("attention launch rejected the shape"); return IRODORI_ERR_SHAPE; }
-
-    // x += g_attn * (o @ Wo) (attention.rs:424, diffusion.rs:98).
-    ga.A = o;
-    ga.W = static_cast<const T*>(lb.w_o);
-    ga.N = D;
-    ga.K = D;
     ga.x = x;
-    ga.kind = 0;
-    if (launch_gemm<T>(EPI_RESID, ga, st)) { set_last_error("wo gemm shape"); return IRODORI_ERR_SHAPE; }
 
-    // h2 = mlp adaLN(x) (diffusion.rs:101-102).
-    launch_norm_mod<T>(x, h, M, S, D, g.norm_eps, mt, l, 1, st);
+    switch (part) {
+        case PART_QKVG: {
+            // QKV + gate projection with head norms and half RoPE (attention.rs:293-345, :423).
+            ga.A = h;
+            ga.W = static_cast<const T*>(lb.w_qkvg);
+            ga.N = 4 * D;
+            ga.K = D;
+            ga.Q = q;
+            ga.Kd = ks;
+            ga.Vd = vs;
+            ga.G = gate;
+            ga.q_norm = lb.q_norm;
+            ga.k_norm = lb.k_norm;
+            ga.rope_cos = c->rope_cos;
+            ga.rope_sin = c->rope_sin;
+            ga.vt_stride = vt_stride;
+            ga.q_scale = 1.4426950408889634f / sqrtf((float)g.head_dim);
+            if (launch_gemm<T>(EPI_QKVG, ga, st)) { set_last_error("qkvg gemm shape"); return IRODORI_ERR_SHAPE; }
+            break;
+        }
+        case PART_ATTN: {
+            // Joint attention over [latent self | cached ctx] (attention.rs:349-425).
+            AttnArgs<T> aa{};
+            aa.Q = q;
+            aa.K0 = ks;
+            aa.V0 = vs;
+            aa.len0 = S;
+            aa.stride0 = S;
+            aa.v_transposed = true;
+            aa.prescaled = true;
+            aa.vstride0 = vt_stride;
+            if (c->t_ctx > 0) {
+                const int T1 = g.max_ctx, vs1 = (g.max_ctx + 63) / 64 * 64, nt1 = (g.max_ctx + 63) / 64;
+                aa.K1 = static_cast<const T*>(lb.ctx_k) + (size_t)r0 * H * T1 * Dh;
+                aa.V1 = static_cast<const T*>(lb.ctx_v) + (size_t)r0 * H * Dh * vs1;
+                aa.len1 = c->t_ctx;
+                aa.stride1 = T1;
+                aa.vstride1 = vs1;
+                aa.mask1 = lb.ctx_mask + (size_t)r0 * T1;
+                aa.tile_on1 = lb.tile_on + (size_t)r0 * nt1;
+                aa.bits1 = lb.tile_bits + (size_t)r0 * nt1;
+            }
+            if (c->lat_on) {
+                aa.mask0 = c->lat_mask_f + tok0;
+                aa.bits0 = c->lat_bits + (size_t)r0 * ((S + 63) / 64);
+            }
+            aa.B = B;
+            aa.H = H;
+            aa.Sq = S;
+            aa.scale = 1.0f / sqrtf((float)g.head_dim);
+            aa.out_mode = 0;
+            aa.G = gate;
+            aa.O = o;
+            int arc;
+            if constexpr (std::is_same<T, bf16>::value)
+                arc = launch_attention32(aa, st);
+            else
+                arc = launch_attention<T, 64>(aa, st);
+            if (arc) { set_last_error("attention launch rejected the shape"); return IRODORI_ERR_SHAPE; }
+            break;
+        }
+        case PART_WO: {
+            // x += g_attn * (o @ Wo) (attention.rs:424, diffusion.rs:98).
+            ga.A = o;
+            ga.W = static_cast<const T*>(lb.w_o);
+            ga.N = D;
+            ga.K = D;
+            ga.kind = 0;
+            if (launch_gemm<T>(EPI_RESID, ga, st)) { set_last_error("wo gemm shape"); return IRODORI_ERR_SHAPE; }
+            break;
+        }
+        case PART_NORM_MLP: {
+            // h2 = mlp adaLN(x) (diffusion.rs:101-102).
+            launch_norm_mod<T>(x, h, M, S, D, g.norm_eps, mt, l, 1, st);
+            break;
+        }
+        case PART_W13: {
+            // m = silu(h2 W1) * (h2 W3) (feed_forward.rs:76-84).
+            ga.A = h;
+            ga.W = static_cast<const T*>(lb.w13);
+            ga.N = 2 * F;
+            ga.K = D;
+            ga.U = u;
+            if (launch_gemm<T>(EPI_SWIGLU, ga, st)) { set_last_error("w13 gemm shape"); return IRODORI_ERR_SHAPE; }
+            break;
+        }
+        case PART_W2: {
+            // x += g_mlp * (m @ W2) (diffusion.rs:104).
+            ga.A = u;
+            ga.W = static_cast<const T*>(lb.w2);
+            ga.N = D;
+            ga.K = F;
+            ga.kind = 1;
+            if (launch_gemm<T>(EPI_RESID, ga, st)) { set_last_error("w2 gemm shape"); return IRODORI_ERR_SHAPE; }
+            break;
+        }
+        case PART_NORM_NEXT: {
+            // Next block's attention adaLN.
+            if (!last) launch_norm_mod<T>(x, h, M, S, D, g.norm_eps, mt, l + 1, 0, st);
+            break;
+        }
+        default:
+            set_last_error("unknown layer part");
+            return IRODORI_ERR_INVALID_ARG;
+    }
+    return IRODORI_OK;
+}
 
-    // m = silu(h2 W1) * (h2 W3) (feed_forward.rs:76-84).
-    ga.A = h;
-    ga.W = static_cast<const T*>(lb.w13);
-    ga.N = 2 * F;
-    ga.K = D;
-    ga.U = u;
-    if (launch_gemm<T>(EPI_SWIGLU, ga, st)) { set_last_error("w13 gemm shape"); return IRODORI_ERR_SHAPE; }
-
-    // x += g_mlp * (m @ W2) (diffusion.rs:104).
-    ga.A = u;
-    ga.W = static_cast<const T*>(lb.w2);
-    ga.N = D;
-    ga.K = F;
-    ga.kind = 1;
-    if (launch_gemm<T>(EPI_RESID, ga, st)) { set_last_error("w2 gemm shape"); return IRODORI_ERR_SHAPE; }
-
-    // Next block's attention adaLN.
-    if (!last_norm) launch_norm_mod<T>(x, h, M, S, D, g.norm_eps, mt, l + 1, 0, st);
+// One DiT block over batch rows [r0, r0 + B) on stream st (see enqueue_part).
+template <typename T>
+int enqueue_layer(irodori_ctx* c, int l, int B, int S, const ModTable& mt, int r0, hipStream_t st) {
+    for (int p = 0; p < PART_COUNT; p++) IRO_TRY(enqueue_part<T>(c, l, B, S, mt, p, r0, st));
     return check_launch("layer");
 }
 
-int enqueue_layer_any(irodori_ctx* c, int l, int B, int S, const ModTable& mt, bool last, int r0 = 0,
+int enqueue_layer_any(irodori_ctx* c, int l, int B, int S, const ModTable& mt, int r0 = 0,
                       hipStream_t st = nullptr) {
     if (!st) st = c->stream;
-    return c->bf16 ? enqueue_layer<bf16>(c, l, B, S, mt, last, r0, st)
-                   : enqueue_layer<float>(c, l, B, S, mt, last, r0, st);
+    return c->bf16 ? enqueue_layer<bf16>(c, l, B, S, mt, r0, st) : enqueue_layer<float>(c, l, B, S, mt, r0, st);
+}
+
+int enqueue_part_any(irodori_ctx* c, int l, int B, int S, const ModTable& mt, int part) {
+    return c->bf16 ? enqueue_part<bf16>(c, l, B, S, mt, part, 0, c->stream)
+                   : enqueue_part<float>(c, l, B, S, mt, part, 0, c->stream);
 }
 
 int enqueue_inproj(irodori_ctx* c, int B, int S, int rows_per_src, const ModTable& mt) {
@@ -453,9 +499,8 @@ int enqueue_rf_step(irodori_ctx* c, int B, int S, float scale) {
     IRO_HIP_CHECK(hipEventRecord(c->ev_fork, c->stream));
     IRO_HIP_CHECK(hipStreamWaitEvent(c->stream2, c->ev_fork, 0));
     for (int l = 0; l < g.num_layers; l++) {
-        const bool last = l + 1 == g.num_layers;
-        IRO_TRY(enqueue_layer_any(c, l, half, S, mt, last, 0, c->stream));
-        IRO_TRY(enqueue_layer_any(c, l, B - half, S, mt, last, half, c->stream2));
+        IRO_TRY(enqueue_layer_any(c, l, half, S, mt, 0, c->stream));
+        IRO_TRY(enqueue_layer_any(c, l, B - half, S, mt, half, c->stream2));
     }
     IRO_HIP_CHECK(hipEventRecord(c->ev_join, c->stream2));
     IRO_HIP_CHECK(hipStreamWaitEvent(c->stream, c->ev_join, 0));
@@ -890,7 +935,7 @@ static int forward_impl(irodori_ctx* c, int B, int S, const float* x_t, const fl
     size_t n = (size_t)B * S * D;
     if (debug) IRO_HIP_CHECK(hipMemcpyAsync(debug, c->x, sizeof(float) * n, hipMemcpyDeviceToHost, c->stream));
     for (int l = 0; l < L; l++) {
-        IRO_TRY(enqueue_layer_any(c, l, B, S, mt, l + 1 == L));
+        IRO_TRY(enqueue_layer_any(c, l, B, S, mt));
         if (debug)
             IRO_HIP_CHECK(hipMemcpyAsync(debug + (size_t)(l + 1) * n, c->x, sizeof(float) * n, hipMemcpyDeviceToHost,
                                          c->stream));
@@ -937,7 +982,7 @@ int irodori_block_forward(irodori_ctx* c, int layer, int B, int S, float* x, con
         launch_norm_mod<bf16>(c->x, static_cast<bf16*>(c->h), B * S, S, D, g.norm_eps, mt, layer, 0, c->stream);
     else
         launch_norm_mod<float>(c->x, static_cast<float*>(c->h), B * S, S, D, g.norm_eps, mt, layer, 0, c->stream);
-    IRO_TRY(enqueue_layer_any(c, layer, B, S, mt, true));
+    IRO_TRY(enqueue_layer_any(c, layer, B, S, mt));
     IRO_HIP_CHECK(hipMemcpyAsync(x, c->x, sizeof(float) * n, hipMemcpyDeviceToHost, c->stream));
     IRO_HIP_CHECK(hipStreamSynchronize(c->stream));
     return IRODORI_OK;
@@ -1083,7 +1128,7 @@ int irodori_profile_layer(irodori_ctx* c, int B, int S, int iters, irodori_kerne
     IRO_REQUIRE(iters > 0, IRODORI_ERR_INVALID_ARG, "iters must be > 0");
     IRO_TRY(check_ready(c, B));
     IRO_HIP_CHECK(hipSetDevice(c->device));
-    int D = g.model_dim, H = g.num_heads, F = g.mlp_hidden, M = B * S, L = g.num_layers;
+    int D = g.model_dim, L = g.num_layers;
     // Modulation vectors for t = 0.5 on every row; state from one in_proj of zeros + 1.
     std::vector<float> t(B, 0.5f), x0((size_t)B * S * g.latent_dim, 1.0f);
     IRO_TRY(ensure_nvec(c, B));
@@ -1092,7 +1137,7 @@ int irodori_profile_layer(irodori_ctx* c, int B, int S, int iters, irodori_kerne
     IRO_TRY(enqueue_mod_table(c, B, false));
     ModTable mt{c->tab, c->zero_step, 0, 1, L};
     IRO_TRY(enqueue_inproj(c, B, S, 1, mt));
-    IRO_TRY(enqueue_layer_any(c, 0, B, S, mt, false));  // fills q/k/v/gate/o/u
+    IRO_TRY(enqueue_layer_any(c, 0, B, S, mt));  // fills q/k/v/gate/o/u
     IRO_HIP_CHECK(hipStreamSynchronize(c->stream));
 
     hipEvent_t e0, e1;
@@ -1100,7 +1145,6 @@ int irodori_profile_layer(irodori_ctx* c, int B, int S, int iters, irodori_kerne
     IRO_HIP_CHECK(hipEventCreate(&e1));
     float* outs[7] = {&out->norm_mod_us, &out->qkvg_gemm_us, &out->attention_us, &out->wo_gemm_us,
                       &out->w13_gemm_us, &out->w2_gemm_us, &out->final_us};
-    auto& lb = c->layers[0];
     int rc = IRODORI_OK;
     for (int kidx = 0; kidx < 7 && rc == IRODORI_OK; kidx++) {
         (void)hipEventRecord(e0, c->stream);
@@ -1113,51 +1157,15 @@ int irodori_profile_layer(irodori_ctx* c, int B, int S, int iters, irodori_kerne
                 launch_final(fa, c->stream);
                 continue;
             }
-            if (c->bf16) {
-                using T = bf16;
-                if (kidx == 0) { launch_norm_mod<T>(c->x, static_cast<T*>(c->h), M, S, D, g.norm_eps, mt, 0, 1, c->stream); continue; }
-                if (kidx == 2) {
-                    AttnArgs<T> aa{};
-                    aa.Q = static_cast<const T*>(c->q); aa.K0 = static_cast<const T*>(c->ks);
-                    aa.V0 = static_cast<const T*>(c->vs); aa.len0 = S; aa.stride0 = S;
-                    aa.v_transposed = true; aa.prescaled = true; aa.vstride0 = (S + 63) / 64 * 64;
-                    if (c->t_ctx > 0) {
-                        aa.K1 = static_cast<const T*>(lb.ctx_k); aa.V1 = static_cast<const T*>(lb.ctx_v);
-                        aa.len1 = c->t_ctx; aa.stride1 = g.max_ctx; aa.vstride1 = (g.max_ctx + 63) / 64 * 64;
-                        aa.mask1 = lb.ctx_mask; aa.tile_on1 = lb.tile_on; aa.bits1 = lb.tile_bits;
-                    }
-                    aa.B = B; aa.H = H; aa.Sq = S; aa.scale = 1.0f / sqrtf((float)g.head_dim);
-                    aa.out_mode = 0; aa.G = static_cast<const T*>(c->gate); aa.O = static_cast<T*>(c->o);
-                    launch_attention32(aa, c->stream);
-                    continue;
-                }
-                GemmArgs<T> ga{};
-                ga.mt = mt; ga.S = S; ga.layer = 0; ga.H = H; ga.D = D; ga.eps = g.norm_eps; ga.M = M;
-                ga.x = c->x;
-                if (kidx == 1) {
-                    ga.A = static_cast<const T*>(c->h); ga.W = static_cast<const T*>(lb.w_qkvg); ga.N = 4 * D; ga.K = D;
-                    ga.Q = static_cast<T*>(c->q); ga.Kd = static_cast<T*>(c->ks); ga.Vd = static_cast<T*>(c->vs);
-                    ga.G = static_cast<T*>(c->gate); ga.q_norm = lb.q_norm; ga.k_norm = lb.k_norm;
-                    ga.rope_cos = c->rope_cos; ga.rope_sin = c->rope_sin;
-                    ga.vt_stride = (S + 63) / 64 * 64;
-                    ga.q_scale = 1.4426950408889634f / sqrtf((float)g.head_dim);
-                    launch_gemm<T>(EPI_QKVG, ga, c->stream);
-                } else if (kidx == 3) {
-                    ga.A = static_cast<const T*>(c->o); ga.W = static_cast<const T*>(lb.w_o); ga.N = D; ga.K = D; ga.kind = 0;
-                    launch_gemm<T>(EPI_RESID, ga, c->stream);
-                } else if (kidx == 4) {
-                    ga.A = static_cast<const T*>(c->h); ga.W = static_cast<const T*>(lb.w13); ga.N = 2 * F; ga.K = D;
-                    ga.U = static_cast<T*>(c->u);
-                    launch_gemm<T>(EPI_SWIGLU, ga, c->stream);
-                } else {
-                    ga.A = static_cast<const T*>(c->u); ga.W = static_cast<const T*>(lb.w2); ga.N = D; ga.K = F; ga.kind = 1;
-                    launch_gemm<T>(EPI_RESID, ga, c->stream);
-                }
-            } else {
+            if (!c->bf16) {
                 rc = IRODORI_ERR_DTYPE;
                 set_last_error("irodori_profile_layer times the bf16 path");
                 break;
             }
+            // The kernels exactly as a block launches them.
+            static const int part_of[6] = {PART_NORM_MLP, PART_QKVG, PART_ATTN, PART_WO, PART_W13, PART_W2};
+            rc = enqueue_part_any(c, 0, B, S, mt, part_of[kidx]);
+            if (rc != IRODORI_OK) break;
         }
         (void)hipEventRecord(e1, c->stream);
         hipError_t se = hipEventSynchronize(e1);

@@ -180,17 +180,31 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
         raw_barrier();
         if (kt + STAGES - 1 < nk) GEMM_ISSUE(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
         const unsigned char* st = smem + (kt % STAGES) * STAGE_BYTES;
+        // Fragments double-buffered in registers: the LDS reads of k16 step ks + 1 are
+        // issued ahead of the MFMAs of step ks, so their latency hides behind FM*FN MFMAs.
+        Frag32<T> af[2][FM], bfr[2][FN];
+#pragma unroll
+        for (int i = 0; i < FM; i++) af[0][i] = read_frag<T>(st, wm0 + 32 * i + fr, 0, fh);
+#pragma unroll
+        for (int j = 0; j < FN; j++) bfr[0][j] = read_frag<T>(st, BM + wn0 + 32 * j + fr, 0, fh);
+        if constexpr (sizeof(T) == 2) __builtin_amdgcn_sched_group_barrier(0x100, FM + FN, 0);
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
-            Frag32<T> af[FM], bfr[FN];
+            const int cur = ks & 1, nxt = cur ^ 1;
+            if (ks + 1 < KS) {
 #pragma unroll
-            for (int i = 0; i < FM; i++) af[i] = read_frag<T>(st, wm0 + 32 * i + fr, ks, fh);
+                for (int i = 0; i < FM; i++) af[nxt][i] = read_frag<T>(st, wm0 + 32 * i + fr, ks + 1, fh);
 #pragma unroll
-            for (int j = 0; j < FN; j++) bfr[j] = read_frag<T>(st, BM + wn0 + 32 * j + fr, ks, fh);
+                for (int j = 0; j < FN; j++) bfr[nxt][j] = read_frag<T>(st, BM + wn0 + 32 * j + fr, ks + 1, fh);
+            }
 #pragma unroll
             for (int i = 0; i < FM; i++)
 #pragma unroll
-                for (int j = 0; j < FN; j++) mma32(acc[i][j], af[i], bfr[j]);
+                for (int j = 0; j < FN; j++) mma32(acc[i][j], af[cur][i], bfr[cur][j]);
+            if constexpr (sizeof(T) == 2) {
+                if (ks + 1 < KS) __builtin_amdgcn_sched_group_barrier(0x100, FM + FN, 0);  // DS reads
+                __builtin_amdgcn_sched_group_barrier(0x008, FM * FN, 0);                   // MFMAs
+            }
         }
     }
 #undef GEMM_ISSUE
@@ -202,6 +216,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
     const int cl = lane & 31;
     const float inv_s = 1.f / (float)a.S;
     if constexpr (EPI == EPI_STORE) {
+        float* __restrict__ C = a.C;
 #pragma unroll
         for (int i = 0; i < FM; i++)
 #pragma unroll
@@ -209,7 +224,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
                 int row = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
                 if (row >= a.M) continue;
 #pragma unroll
-                for (int j = 0; j < FN; j++) a.C[(size_t)row * a.N + n0 + wn0 + 32 * j + cl] = acc[i][j][e];
+                for (int j = 0; j < FN; j++) C[(size_t)row * a.N + n0 + wn0 + 32 * j + cl] = acc[i][j][e];
             }
     } else if constexpr (EPI == EPI_RESID) {
         // x[row, col] += gate[b(row), col] * C.  The gate rows of the (at most two) batch
@@ -445,9 +460,12 @@ int launch_cfg(const GemmArgs<T>& a, hipStream_t st) {
 
 }  // namespace
 
-// Tile choice per epilogue: the wide projections (QKV+gate, W1|W3) use 128x128 tiles in
-// two stages (two workgroups per CU); the D-wide projections (Wo, W2) use 64x64 tiles in
-// four stages so that M = 1500 x N = 1024 still yields 384 workgroups for 256 CUs.
+// Tile choice per epilogue.  With 2x2 wavefronts of 32x32 blocks the main loop is bound by
+// LDS bandwidth (fragment reads + the DMA writes): 1.5x the MFMA time for 128x128 tiles,
+// 3x for 64x64.  The wide projections (QKV+gate, W1|W3) use 128x128 tiles in two stages
+// (two workgroups per CU); the D-wide projections (Wo, W2) use 64x64 tiles in four stages
+// so that N = 1024 still yields enough workgroups (split-K over larger tiles measured
+// slower: the f32 partial planes cost more HBM traffic than the LDS time they save).
 template <typename T>
 int launch_gemm(int epi, const GemmArgs<T>& a, hipStream_t st) {
     switch (epi) {
