@@ -90,7 +90,10 @@ __device__ __forceinline__ Frag32<float> read_frag<float>(const unsigned char* s
 }
 
 // Sum over the 32 lanes of each half-wave (lanes 0-31 and 32-63 separately): DPP
-// rotations within 16-lane rows, then one swizzle across the two rows of each half.
+// rotations within 16-lane rows, then v_permlane16_swap, which exchanges the odd 16-lane
+// rows of one operand with the even rows of the other.  With both operands equal to v the
+// two results hold, at every lane, the values of lane l and lane l ^ 16, so their sum is
+// the half-wave total (all on the VALU; no LDS-pipeline swizzle).
 #define IRO_DPP(v, ctrl)                                                                        \
     __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, (v)), (ctrl), 0xF, 0xF, false))
 __device__ __forceinline__ float half_wave_sum(float v) {
@@ -98,9 +101,18 @@ __device__ __forceinline__ float half_wave_sum(float v) {
     v += IRO_DPP(v, 0x124);  // row_ror:4
     v += IRO_DPP(v, 0x4E);   // quad_perm [2,3,0,1]
     v += IRO_DPP(v, 0xB1);   // quad_perm [1,0,3,2]
-    // swizzle (bit mode, and 0x1f, xor 0x10): lane ^ 16 within each 32-lane group
-    v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
-    return v;
+    const unsigned u = __builtin_bit_cast(unsigned, v);
+    const auto sw = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return __builtin_bit_cast(float, (unsigned)sw[0]) + __builtin_bit_cast(float, (unsigned)sw[1]);
+}
+
+// Staged bf16 wave tile of the QKVG epilogue: row r (< 64) of 64 columns lives at
+// slot + 256 r, its 16-byte chunk c at chunk position c ^ (4 * ((r >> 2 ^ r) & 1)).  The
+// column writes of an accumulator step touch rows r and r + 4 together and the 16-byte row
+// reads rows r and r + 1 together; the xor puts each pair on different banks.
+__device__ __forceinline__ int stage_off(int r, int col) {
+    const int c = col >> 3;
+    return r * 256 + ((c ^ (4 * (((r >> 2) ^ r) & 1))) << 4) + (col & 7) * 2;
 }
 
 __device__ __forceinline__ const float* gate_vec(const ModTable& mt, int b, int layer, int kind,
@@ -303,7 +315,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
     } else if constexpr (EPI == EPI_QKVG) {
         // Each wave owns WM rows x one 64-column head of one region (q | k | v | gate).
         // The stage buffers are free once every wave is past the main loop; each wave then
-        // uses its own LDS slot: RoPE table rows (WM x 64 f32) or the V^T transpose
+        // uses its own LDS slot: RoPE table rows (WM x 64 f32) and, for bf16, the staged
+        // q / k / gate tile (stage_off) written out with 16-byte stores; or the V^T transpose
         // (64 x (WM + 2) elements; an odd word stride keeps both passes conflict-free).
         constexpr int VT_BYTES = sizeof(T) == 2 ? 64 * (WM + 2) * 2 : 0;  // f32 scatters V^T directly
         constexpr int SLOT = WM * 256 > VT_BYTES ? WM * 256 : VT_BYTES;
@@ -357,7 +370,12 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
                         ya *= a.q_scale;
                         yb *= a.q_scale;
                     }
-                    if (row < a.M) {
+                    if constexpr (sizeof(T) == 2) {
+                        // Staged over the first half of row rl's table entries, which this
+                        // step has already read (each row is handled in exactly one step).
+                        *reinterpret_cast<T*>(slot + stage_off(rl, cl)) = from_f32<T>(ya);
+                        *reinterpret_cast<T*>(slot + stage_off(rl, 32 + cl)) = from_f32<T>(yb);
+                    } else if (row < a.M) {
                         int b, sq;
                         row_bs(row, a.S, inv_s, b, sq);
                         T* o = dst + (((size_t)b * a.H + h) * a.S + sq) * Dh;
@@ -365,6 +383,19 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
                         o[32 + cl] = from_f32<T>(yb);
                     }
                 }
+            if constexpr (sizeof(T) == 2) {
+                // 16-byte stores: 8 lanes per 128-byte head row of [B, H, S, Dh].
+#pragma unroll
+                for (int it = 0; it < WM / 8; it++) {
+                    const int r = it * 8 + (lane >> 3), c = lane & 7;
+                    const int row = rw0 + r;
+                    if (row >= a.M) continue;
+                    int b, sq;
+                    row_bs(row, a.S, inv_s, b, sq);
+                    const uint4 v = *reinterpret_cast<const uint4*>(slot + stage_off(r, 8 * c));
+                    *reinterpret_cast<uint4*>(dst + (((size_t)b * a.H + h) * a.S + sq) * Dh + 8 * c) = v;
+                }
+            }
         } else if (region == 2) {
             // V^T [B,H,Dh,S'] in the key order the attention kernel's A operand wants.
             if constexpr (sizeof(T) == 2) {
@@ -422,6 +453,26 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
                             a.Vd[(((size_t)b * a.H + h) * Dh + d) * a.vt_stride + pos] = from_f32<T>(acc[i][j][e]);
                         }
                     }
+            }
+        } else if constexpr (sizeof(T) == 2) {
+            // Gate: sigmoid staged in LDS, then 16-byte stores of the 128-byte row segments.
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const int rl = 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+#pragma unroll
+                    for (int j = 0; j < 2; j++)
+                        *reinterpret_cast<T*>(slot + stage_off(rl, 32 * j + cl)) = from_f32<T>(sigmoid_f(acc[i][j][e]));
+                }
+            T* gdst = a.G + (col0 - 3 * D);
+#pragma unroll
+            for (int it = 0; it < WM / 8; it++) {
+                const int r = it * 8 + (lane >> 3), c = lane & 7;
+                const int row = rw0 + r;
+                if (row >= a.M) continue;
+                const uint4 v = *reinterpret_cast<const uint4*>(slot + stage_off(r, 8 * c));
+                *reinterpret_cast<uint4*>(gdst + (size_t)row * D + 8 * c) = v;
             }
         } else {
 #pragma unroll
