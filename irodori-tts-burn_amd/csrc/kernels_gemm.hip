@@ -179,6 +179,48 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
 #pragma unroll
             for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
 
+    // Accumulator element (i, j, e) of this lane is C[row][col] with
+    //   row = rbase + 32 i + 8 (e / 4) + e % 4,  col = n0 + wn0 + 32 j + cl.
+    const int rbase = m0 + wm0 + 4 * (lane >> 5);
+    const int cl = lane & 31;
+    const float inv_s = 1.f / (float)a.S;
+
+    // EPI_RESID (S >= 32): the residual elements this lane updates and the gate rows of
+    // the (at most two) batch rows each 32-row block touches are loaded before the main
+    // loop, so their latency hides behind it (each element belongs to one lane only).
+    [[maybe_unused]] float xpre[FM][16][FN];
+    [[maybe_unused]] float gpre[FM][2][FN];
+    [[maybe_unused]] int hi_row[FM];  // first row of the upper batch row of block i
+    if constexpr (EPI == EPI_RESID) {
+        if (a.S >= 32) {
+            const int step = a.mt.step ? *a.mt.step : 0;
+#pragma unroll
+            for (int i = 0; i < FM; i++) {
+                const int r0 = rbase + 32 * i;
+                int b_lo, s_lo;
+                row_bs(r0 < a.M ? r0 : a.M - 1, a.S, inv_s, b_lo, s_lo);
+                const int b_hi = b_lo + 1;
+                hi_row[i] = b_hi * a.S;
+                const bool need_hi = s_lo + 28 >= a.S && hi_row[i] < a.M;  // block may cross into b_hi
+#pragma unroll
+                for (int u = 0; u < 2; u++) {
+                    const int bb = u ? b_hi : b_lo;
+                    const float* g = a.mt.tab + ((size_t)(step * a.mt.step_stride + bb / a.mt.rows_per_vec) * a.mt.layers * 6 +
+                                                 (size_t)a.layer * 6 + a.kind * 3 + 2) * a.N;
+#pragma unroll
+                    for (int j = 0; j < FN; j++) gpre[i][u][j] = (!u || need_hi) ? g[n0 + wn0 + 32 * j + cl] : 0.f;
+                }
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const int row = r0 + 8 * (e >> 2) + (e & 3);
+#pragma unroll
+                    for (int j = 0; j < FN; j++)
+                        xpre[i][e][j] = row < a.M ? a.x[(size_t)row * a.N + n0 + wn0 + 32 * j + cl] : 0.f;
+                }
+            }
+        }
+    }
+
     const int nk = K / BK;
 #pragma unroll
     for (int s = 0; s < STAGES - 1; s++)
@@ -221,12 +263,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
     }
 #undef GEMM_ISSUE
 
-    // ---- epilogues.  acc[i][j][e] = C[row][col] with
-    //      row = m0 + wm0 + 32 i + 8 (e / 4) + 4 (lane / 32) + e % 4,
-    //      col = n0 + wn0 + 32 j + lane % 32.
-    const int rbase = m0 + wm0 + 4 * (lane >> 5);
-    const int cl = lane & 31;
-    const float inv_s = 1.f / (float)a.S;
+    // ---- epilogues (acc layout: see rbase / cl above).
     if constexpr (EPI == EPI_STORE) {
         float* __restrict__ C = a.C;
 #pragma unroll
@@ -239,11 +276,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
                 for (int j = 0; j < FN; j++) C[(size_t)row * a.N + n0 + wn0 + 32 * j + cl] = acc[i][j][e];
             }
     } else if constexpr (EPI == EPI_RESID) {
-        // x[row, col] += gate[b(row), col] * C.  The gate rows of the (at most two) batch
-        // rows a 32-row block touches are loaded once; x is read for a whole 32-row block
-        // before any of it is written.
+        // x[row, col] += gate[b(row), col] * C, from the values loaded before the main loop.
         float* __restrict__ xg = a.x;
-        const int step = a.mt.step ? *a.mt.step : 0;
         if (a.S < 32) {  // a 32-row block may span more than two batch rows
 #pragma unroll
             for (int i = 0; i < FM; i++)
@@ -261,38 +295,14 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
         } else
 #pragma unroll
         for (int i = 0; i < FM; i++) {
-            const int r0 = rbase + 32 * i;
-            int b_lo, s_lo;
-            row_bs(r0 < a.M ? r0 : a.M - 1, a.S, inv_s, b_lo, s_lo);
-            const int b_hi = b_lo + 1;
-            const float* g_lo = a.mt.tab + ((size_t)(step * a.mt.step_stride + b_lo / a.mt.rows_per_vec) * a.mt.layers * 6 +
-                                            (size_t)a.layer * 6 + a.kind * 3 + 2) * a.N;
-            const float* g_hi = a.mt.tab + ((size_t)(step * a.mt.step_stride + b_hi / a.mt.rows_per_vec) * a.mt.layers * 6 +
-                                            (size_t)a.layer * 6 + a.kind * 3 + 2) * a.N;
-            float glo[FN], ghi[FN];
-            const bool need_hi = s_lo + 28 >= a.S && b_hi * a.S < a.M;  // block may cross into b_hi
-#pragma unroll
-            for (int j = 0; j < FN; j++) {
-                const int col = n0 + wn0 + 32 * j + cl;
-                glo[j] = g_lo[col];
-                ghi[j] = need_hi ? g_hi[col] : 0.f;
-            }
-            float xv[16][FN];
 #pragma unroll
             for (int e = 0; e < 16; e++) {
-                const int row = r0 + 8 * (e >> 2) + (e & 3);
-#pragma unroll
-                for (int j = 0; j < FN; j++)
-                    xv[e][j] = row < a.M ? xg[(size_t)row * a.N + n0 + wn0 + 32 * j + cl] : 0.f;
-            }
-#pragma unroll
-            for (int e = 0; e < 16; e++) {
-                const int row = r0 + 8 * (e >> 2) + (e & 3);
+                const int row = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
                 if (row >= a.M) continue;
-                const bool hi = row >= b_hi * a.S;
+                const int u = row >= hi_row[i] ? 1 : 0;
 #pragma unroll
                 for (int j = 0; j < FN; j++)
-                    xg[(size_t)row * a.N + n0 + wn0 + 32 * j + cl] = xv[e][j] + (hi ? ghi[j] : glo[j]) * acc[i][j][e];
+                    xg[(size_t)row * a.N + n0 + wn0 + 32 * j + cl] = xpre[i][e][j] + gpre[i][u][j] * acc[i][j][e];
             }
         }
     } else if constexpr (EPI == EPI_SWIGLU) {
