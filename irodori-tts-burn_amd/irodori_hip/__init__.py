@@ -8,10 +8,12 @@ from .config import (CfgGuidanceMode, DitConfig, GuidanceConfig, InferenceBacken
                      IrodoriError, SamplerMethod, SamplerParams, cfg_cpu_plumbing, cfg_full_rf,
                      cfg_tiny)
 from .engine import HipInferenceEngine, ops
-from .synthetic import ContextKV, DitWeights, make_context_kv, make_noise
+from .synthetic import (ROLE_COND, ROLE_NO_AUX, ROLE_NO_TEXT, ROLE_UNCOND, ContextKV,
+                        DitWeights, make_context_kv, make_noise, make_role_context)
 
 __all__ = [
     "CfgGuidanceMode", "DitConfig", "GuidanceConfig", "InferenceBackendKind", "IrodoriError",
     "SamplerMethod", "SamplerParams", "cfg_cpu_plumbing", "cfg_full_rf", "cfg_tiny",
     "HipInferenceEngine", "ops", "ContextKV", "DitWeights", "make_context_kv", "make_noise",
+    "make_role_context", "ROLE_COND", "ROLE_UNCOND", "ROLE_NO_TEXT", "ROLE_NO_AUX",
 ]

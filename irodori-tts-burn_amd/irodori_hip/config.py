@@ -110,6 +110,23 @@ class GuidanceConfig:
 
 
 @dataclass
+class TemporalRescaleConfig:
+    """src/rf/params.rs:37-45 (arxiv:2510.01184); k and sigma are set together."""
+
+    k: float
+    sigma: float
+
+
+@dataclass
+class SpeakerKvConfig:
+    """src/rf/params.rs:47-58: scale the speaker K/V of the context cache."""
+
+    scale: float
+    max_layers: int | None = None   # None = every layer
+    min_t: float | None = None      # revert once t drops below it; None = never
+
+
+@dataclass
 class SamplerParams:
     """src/rf/params.rs:61-92 (defaults :77-90)."""
 
@@ -117,9 +134,11 @@ class SamplerParams:
     method: SamplerMethod = SamplerMethod.EULER
     guidance: GuidanceConfig = field(default_factory=GuidanceConfig)
     truncation_factor: float | None = None
+    temporal_rescale: TemporalRescaleConfig | None = None
+    speaker_kv: SpeakerKvConfig | None = None
     use_context_kv_cache: bool = True
 
-    def validate(self, has_speaker: bool = True) -> None:
+    def validate(self, has_speaker: bool = True, has_caption: bool = False) -> None:
         """params.rs:99-183 and the Joint equal-scale rule (euler_sampler.rs:209-228)."""
         if self.num_steps == 0:
             raise IrodoriError("Config", "num_steps must be > 0")
@@ -129,15 +148,31 @@ class SamplerParams:
                         ("guidance.scale_speaker", g.scale_speaker)):
             if not math.isfinite(s):
                 raise IrodoriError("Config", "%s must be finite, got %s" % (name, s))
-        if not (math.isfinite(g.min_t) and math.isfinite(g.max_t)):
-            raise IrodoriError("Config", "guidance min_t/max_t must be finite")
+        for name, t in (("guidance.min_t", g.min_t), ("guidance.max_t", g.max_t)):
+            if not (math.isfinite(t) and 0.0 <= t <= 1.0):
+                raise IrodoriError("Config", "%s must be finite and in [0, 1], got %s" % (name, t))
         if g.min_t > g.max_t:
-            raise IrodoriError("Config", "guidance.min_t must be <= guidance.max_t")
+            raise IrodoriError("Config", "guidance.min_t (%s) must not exceed guidance.max_t (%s)"
+                               % (g.min_t, g.max_t))
         if self.truncation_factor is not None and not (
                 math.isfinite(self.truncation_factor) and self.truncation_factor > 0):
             raise IrodoriError("Config", "truncation_factor must be finite and > 0")
+        if self.temporal_rescale is not None:
+            if not math.isfinite(self.temporal_rescale.k):
+                raise IrodoriError("Config", "temporal_rescale.k must be finite")
+            if self.temporal_rescale.sigma == 0.0:
+                raise IrodoriError("Config", "temporal_rescale.sigma must not be zero")
+        if self.speaker_kv is not None:
+            skv = self.speaker_kv
+            if not (math.isfinite(skv.scale) and skv.scale > 0):
+                raise IrodoriError("Config", "speaker_kv.scale must be finite and > 0")
+            if skv.min_t is not None and not (math.isfinite(skv.min_t) and 0.0 <= skv.min_t <= 1.0):
+                raise IrodoriError("Config", "speaker_kv.min_t must be finite and in [0, 1]")
+        if self.method is SamplerMethod.PLMS4 and g.mode is CfgGuidanceMode.ALTERNATING:
+            raise IrodoriError("Config", "sampler PLMS4 is not compatible with "
+                                         "cfg_guidance_mode=Alternating; use Independent or Joint instead")
         if g.mode is CfgGuidanceMode.JOINT:
-            active = [s for s in (g.scale_text, g.scale_speaker if has_speaker else 0.0) if s > 0]
+            active = self.cfg_scales(has_speaker, has_caption)
             if active and max(active) - min(active) >= 1e-6:
                 raise IrodoriError(
                     "Config",
@@ -145,12 +180,38 @@ class SamplerParams:
                     "text=%s, speaker=%s, caption=%s" % (g.scale_text, g.scale_speaker,
                                                         g.scale_caption))
 
-    def joint_scale(self, has_speaker: bool = True) -> float:
+    def cfg_signals(self, has_speaker: bool = True, has_caption: bool = False) -> list[str]:
+        """Active CFG signals in the sampler's order (euler_sampler.rs:163-200): text if its
+        scale is > 0, speaker if the condition holds a speaker state and its scale is > 0,
+        caption if the condition holds a caption with a valid token and its scale is > 0."""
         g = self.guidance
-        for s in (g.scale_text, g.scale_speaker if has_speaker else 0.0):
-            if s > 0:
-                return s
-        return 0.0
+        out = []
+        if g.scale_text > 0:
+            out.append("text")
+        if has_speaker and g.scale_speaker > 0:
+            out.append("speaker")
+        if has_caption and g.scale_caption > 0:
+            out.append("caption")
+        return out
+
+    def cfg_scales(self, has_speaker: bool = True, has_caption: bool = False) -> list[float]:
+        g = self.guidance
+        by = {"text": g.scale_text, "speaker": g.scale_speaker, "caption": g.scale_caption}
+        return [by[n] for n in self.cfg_signals(has_speaker, has_caption)]
+
+    def joint_scale(self, has_speaker: bool = True, has_caption: bool = False) -> float:
+        sc = self.cfg_scales(has_speaker, has_caption)
+        return sc[0] if sc else 0.0
+
+    def cfg_roles(self, has_speaker: bool = True, has_caption: bool = False) -> list[str]:
+        """The context bundles irodori_sample reads, in role order (row r * U + u): the
+        conditioned bundle, then for Joint the fully unconditioned one, for Independent and
+        Alternating one bundle per active signal with that signal dropped (text ->
+        "no_text", speaker / caption -> "no_aux", euler_sampler.rs:41-85)."""
+        sig = self.cfg_signals(has_speaker, has_caption)
+        if self.guidance.mode is CfgGuidanceMode.JOINT:
+            return ["cond", "uncond"] if sig else ["cond"]
+        return ["cond"] + ["no_text" if s == "text" else "no_aux" for s in sig]
 
     def t_schedule(self) -> list[float]:
         """euler_sampler.rs:325-328, computed in f32: t_i = 0.999 * (1 - i/N), i = 0..N."""

@@ -100,34 +100,61 @@ class ContextKV:
                          np.ascontiguousarray(self.mask[idx]))
 
 
-def make_context_kv(cfg: DitConfig, utterances: int, t_text: int, t_spk: int, seed: int = 1,
-                    text_valid=None, joint_cfg: bool = True, kv_std: float = 1.0) -> ContextKV:
-    """Synthetic cached context for `utterances` utterances.
+# Context bundles of the CFG roles (euler_sampler.rs:41-85, condition.rs:144-154): the
+# conditioned bundle, the fully unconditioned one (Joint), and the bundles with the text or
+# the aux (speaker / caption) signal dropped.  A dropped signal has zero states, which
+# project to zero K/V, and every one of its keys masked out.
+ROLE_COND, ROLE_UNCOND, ROLE_NO_TEXT, ROLE_NO_AUX = "cond", "uncond", "no_text", "no_aux"
 
-    Conditioned rows: K/V ~ N(0, kv_std); text keys valid up to a per-utterance length
-    (default uniform in [min(32, t_text), t_text]), speaker keys all valid.
-    With joint_cfg, each utterance u occupies rows (2u, 2u+1) and row 2u+1 is the
-    unconditioned row of EncodedCondition::zeros_like (condition.rs:144-154): zero states
-    project to zero K/V and every context key is masked out.
-    """
+
+def make_role_context(cfg: DitConfig, utterances: int, t_text: int, t_aux: int, roles,
+                      seed: int = 1, text_valid=None, kv_std: float = 1.0) -> ContextKV:
+    """Synthetic cached context for the CFG roles of `utterances` utterances, role-major:
+    role r of utterance u is row r * U + u (the row layout of irodori_sample).
+
+    Utterance u draws text and aux K/V ~ N(0, kv_std) once; its text keys are valid up to
+    a per-utterance length (default uniform in [min(32, t_text), t_text]) and its aux keys
+    are all valid.  Each role keeps or drops the two segments (see the ROLE_* names)."""
     rng = np.random.default_rng(seed)
     L, H, Dh = cfg.num_layers, cfg.num_heads, cfg.head_dim
-    T = t_text + t_spk
-    rows = 2 * utterances if joint_cfg else utterances
-    k = np.zeros((L, rows, T, H, Dh), np.float32)
+    T, U, R = t_text + t_aux, utterances, len(roles)
+    k = np.zeros((L, R * U, T, H, Dh), np.float32)
     v = np.zeros_like(k)
-    mask = np.zeros((rows, T), np.uint8)
-    for u in range(utterances):
-        r = 2 * u if joint_cfg else u
-        k[:, r] = rng.standard_normal((L, T, H, Dh), dtype=np.float32) * np.float32(kv_std)
-        v[:, r] = rng.standard_normal((L, T, H, Dh), dtype=np.float32) * np.float32(kv_std)
+    mask = np.zeros((R * U, T), np.uint8)
+    for u in range(U):
+        ku = rng.standard_normal((L, T, H, Dh), dtype=np.float32) * np.float32(kv_std)
+        vu = rng.standard_normal((L, T, H, Dh), dtype=np.float32) * np.float32(kv_std)
         if text_valid is not None:
             tv = int(text_valid[u])
         else:
             tv = int(rng.integers(min(32, t_text), t_text + 1)) if t_text > 0 else 0
-        mask[r, :tv] = 1
-        mask[r, t_text:] = 1
+        for r, role in enumerate(roles):
+            row = r * U + u
+            keep_text = role in (ROLE_COND, ROLE_NO_AUX)
+            keep_aux = role in (ROLE_COND, ROLE_NO_TEXT)
+            if role not in (ROLE_COND, ROLE_UNCOND, ROLE_NO_TEXT, ROLE_NO_AUX):
+                raise ValueError("unknown role %r" % (role,))
+            if keep_text:
+                k[:, row, :t_text] = ku[:, :t_text]
+                v[:, row, :t_text] = vu[:, :t_text]
+                mask[row, :tv] = 1
+            if keep_aux:
+                k[:, row, t_text:] = ku[:, t_text:]
+                v[:, row, t_text:] = vu[:, t_text:]
+                mask[row, t_text:] = 1
     return ContextKV(k, v, mask)
+
+
+def make_context_kv(cfg: DitConfig, utterances: int, t_text: int, t_spk: int, seed: int = 1,
+                    text_valid=None, joint_cfg: bool = True, kv_std: float = 1.0) -> ContextKV:
+    """Synthetic cached context for `utterances` utterances: with joint_cfg the Joint-CFG
+    roles (rows [0, U) conditioned, rows [U, 2U) the unconditioned bundle of
+    EncodedCondition::zeros_like: zero K/V, every key masked out), else the conditioned
+    rows only.  Text keys are valid up to a per-utterance length (default uniform in
+    [min(32, t_text), t_text]); speaker keys are all valid."""
+    roles = (ROLE_COND, ROLE_UNCOND) if joint_cfg else (ROLE_COND,)
+    return make_role_context(cfg, utterances, t_text, t_spk, roles, seed=seed,
+                             text_valid=text_valid, kv_std=kv_std)
 
 
 def make_noise(utterances: int, seq: int, latent_dim: int, seed: int = 2) -> np.ndarray:

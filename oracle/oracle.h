@@ -65,6 +65,29 @@ typedef struct orc_io {
     const float* out_b;      /* [P] */
 } orc_io;
 
+/* SamplerParams + GuidanceConfig + TemporalRescaleConfig + SpeakerKvConfig
+ * (src/rf/params.rs:9-92) as the sampler consumes them, plus the request facts that
+ * select the active CFG signals (euler_sampler.rs:163-200). */
+typedef struct orc_sampler {
+    int32_t num_steps;
+    int32_t method;     /* 0 Euler, 1 Heun, 2 PLMS-4 (config/sampling.rs:8-20) */
+    int32_t cfg_mode;   /* 0 Independent, 1 Joint, 2 Alternating (config/sampling.rs:100-108) */
+    float scale_text, scale_caption, scale_speaker;
+    float min_t, max_t;
+    int32_t has_truncation;
+    float truncation_factor;
+    int32_t has_speaker;  /* the model uses speaker conditioning and the condition holds a speaker state */
+    int32_t has_caption;  /* the condition holds a caption with at least one valid token */
+    int32_t has_temporal_rescale;
+    float rescale_k, rescale_sigma;
+    int32_t has_speaker_kv;
+    float speaker_kv_scale;
+    int32_t speaker_kv_max_layers;  /* < 0: every layer */
+    int32_t speaker_kv_has_min_t;
+    float speaker_kv_min_t;
+    int32_t ctx_aux_start;  /* first aux (speaker) key of the context sequence */
+} orc_sampler;
+
 /* Number of OpenMP threads the oracle uses (0 = runtime default). */
 void orc_set_threads(int n);
 int orc_get_threads(void);
@@ -115,7 +138,11 @@ int orc_get_threads(void);
                             const float* ctx_k_unc, const float* ctx_v_unc,                \
                             const uint8_t* mask_unc, const uint8_t* lat_mask,              \
                             int num_steps, float scale, float min_t, float max_t,          \
-                            int max_steps_run, float* x_out);
+                            int max_steps_run, float* x_out);                              \
+    int P##sample_rf(const orc_cfg* c, const orc_io* io, const orc_block* blocks, int U,   \
+                     int S, const float* x0, int T, const float* ctx_k, const float* ctx_v,\
+                     const uint8_t* ctx_mask, const uint8_t* lat_mask,                      \
+                     const orc_sampler* sp, int max_steps_run, float* x_out);
 
 ORC_DECLARE(orc_f32_)
 ORC_DECLARE(orc_f64_)

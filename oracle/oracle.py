@@ -46,6 +46,39 @@ class OrcIo(C.Structure):
     ]
 
 
+class OrcSampler(C.Structure):
+    """orc_sampler (oracle.h): the sampler parameters and request facts."""
+    _fields_ = [
+        ("num_steps", C.c_int32), ("method", C.c_int32), ("cfg_mode", C.c_int32),
+        ("scale_text", C.c_float), ("scale_caption", C.c_float), ("scale_speaker", C.c_float),
+        ("min_t", C.c_float), ("max_t", C.c_float), ("has_truncation", C.c_int32),
+        ("truncation_factor", C.c_float), ("has_speaker", C.c_int32), ("has_caption", C.c_int32),
+        ("has_temporal_rescale", C.c_int32), ("rescale_k", C.c_float), ("rescale_sigma", C.c_float),
+        ("has_speaker_kv", C.c_int32), ("speaker_kv_scale", C.c_float),
+        ("speaker_kv_max_layers", C.c_int32), ("speaker_kv_has_min_t", C.c_int32),
+        ("speaker_kv_min_t", C.c_float), ("ctx_aux_start", C.c_int32),
+    ]
+
+
+# Defaults of a sampler request: Independent CFG, Euler, scales 3/3/5 over [0.5, 1]
+# (params.rs:22-33), no truncation, rescale or speaker-KV scaling.
+SAMPLER_DEFAULTS = dict(num_steps=40, method=0, cfg_mode=0, scale_text=3.0, scale_caption=3.0,
+                        scale_speaker=5.0, min_t=0.5, max_t=1.0, has_truncation=0,
+                        truncation_factor=1.0, has_speaker=0, has_caption=0,
+                        has_temporal_rescale=0, rescale_k=1.0, rescale_sigma=1.0,
+                        has_speaker_kv=0, speaker_kv_scale=1.0, speaker_kv_max_layers=-1,
+                        speaker_kv_has_min_t=0, speaker_kv_min_t=0.0, ctx_aux_start=0)
+
+
+def sampler_struct(**kw) -> OrcSampler:
+    """OrcSampler from SAMPLER_DEFAULTS overridden by keyword arguments."""
+    unknown = set(kw) - set(SAMPLER_DEFAULTS)
+    if unknown:
+        raise TypeError("unknown sampler fields: %s" % sorted(unknown))
+    d = dict(SAMPLER_DEFAULTS, **kw)
+    return OrcSampler(**d)
+
+
 def build() -> None:
     """Compile liboracle.so with the Makefile beside this file."""
     subprocess.run(["make", "-s", "-C", _HERE], check=True)
@@ -276,6 +309,22 @@ class Oracle:
                             _f(_c32(ctx_v)), _u8(np.ascontiguousarray(ctx_mask, np.uint8)),
                             _lat(latent_mask), _f(v), _f(dbg) if debug else None)
         return (v, dbg) if debug else v
+
+    def sample_rf(self, cfg, weights, x0, ctx, sampler, max_steps_run=0, latent_mask=None):
+        """x0 [U,S,P]; ctx = (k [L,R*U,T,H,Dh], v, mask [R*U,T]) role-major (row r*U + u);
+        sampler: an OrcSampler (sampler_struct); latent_mask [U,S] or None.
+        Returns (x_out, steps_run)."""
+        x0 = _c32(x0)
+        U, S, Pd = x0.shape
+        k, v, m = ctx
+        T = k.shape[2]
+        blocks = (OrcBlock * cfg.num_layers)(*[self.block_struct(b) for b in weights.blocks])
+        out = np.empty_like(x0)
+        run = self._fn("sample_rf")(
+            C.byref(self.cfg_struct(cfg)), C.byref(self.io_struct(weights.io)), blocks, U, S,
+            _f(x0), T, _f(_c32(k)), _f(_c32(v)), _u8(np.ascontiguousarray(m, np.uint8)),
+            _lat(latent_mask), C.byref(sampler), max_steps_run, _f(out))
+        return out, int(run)
 
     def sample_joint_cfg(self, cfg, weights, x0, ctx_cond, ctx_unc, num_steps, scale,
                          min_t=0.0, max_t=1.0, max_steps_run=0, latent_mask=None):

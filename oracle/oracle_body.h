@@ -453,3 +453,199 @@ int P(sample_joint_cfg)(const orc_cfg* c, const orc_io* io, const orc_block* blo
     free(vc); free(vu); free(tt);
     return run;
 }
+
+/* Active CFG signals in the reference's order (euler_sampler.rs:163-200): text if its
+ * scale is > 0; speaker if the model uses speaker conditioning, the condition holds a
+ * speaker state and its scale is > 0; caption if the condition holds a caption with a
+ * valid token and its scale is > 0.  scales[k] = scale of signal k; returns the count. */
+static int P(cfg_signals)(const orc_sampler* sp, float* scales) {
+    int n = 0;
+    if (sp->scale_text > 0.f) scales[n++] = sp->scale_text;
+    if (sp->has_speaker && sp->scale_speaker > 0.f) scales[n++] = sp->scale_speaker;
+    if (sp->has_caption && sp->scale_caption > 0.f) scales[n++] = sp->scale_caption;
+    return n;
+}
+
+/* kv_scaling.rs:10-60 on the role copies: the aux keys [aux_start, T) of K and V of every
+ * scaled role times s, in the first nl layers. */
+static void P(scale_aux_kv)(float* const* rk, float* const* rv, const int* roles, int nroles,
+                            int nl, int U, int T, int HD, int aux_start, float s) {
+    for (int ri = 0; ri < nroles; ri++)
+        for (int l = 0; l < nl; l++)
+            for (int u = 0; u < U; u++)
+                for (int j = aux_start; j < T; j++) {
+                    size_t o = (((size_t)l * U + u) * T + j) * HD;
+                    for (int e = 0; e < HD; e++) {
+                        rk[roles[ri]][o + e] = (float)((R)rk[roles[ri]][o + e] * (R)s);
+                        rv[roles[ri]][o + e] = (float)((R)rv[roles[ri]][o + e] * (R)s);
+                    }
+                }
+}
+
+/* math.rs:38-53 temporal_score_rescale (no-op for t >= 1): with 1-t = omt,
+ * snr = omt^2 / t^2, ratio = (snr sigma^2 + 1) / (snr sigma^2 / k + 1),
+ * v' = (v omt + x) ratio / omt - x / omt.  The scalars are f32, as in the reference. */
+static void P(temporal_rescale)(float* v, const float* x, size_t n, float t, float k, float sigma) {
+    if (t >= 1.0f) return;
+    float omt = 1.0f - t;
+    float snr = (omt * omt) / (t * t);
+    float sig2 = sigma * sigma;
+    float ratio = (snr * sig2 + 1.0f) / (snr * sig2 / k + 1.0f);
+    for (size_t j = 0; j < n; j++) {
+        R a = (R)v[j] * (R)omt + (R)x[j];
+        v[j] = (float)(a * (R)ratio / (R)omt - (R)x[j] / (R)omt);
+    }
+}
+
+/* The guided velocity at (x, t) (euler_sampler.rs:435-523 and the Heun corrector's copy
+ * :571-666): the conditioned forward (role 0), and when CFG is on
+ *   Independent  v = v_c; v += (v_c - v_k) s_k for every enabled signal k (role 1 + k),
+ *   Joint        v = v_c + (v_c - v_u) s_0 (role 1),
+ *   Alternating  a = i mod n: v = v_c + (v_c - v_a) s_a (role 1 + a).
+ * rk/rv/rm hold one [L, U, T, H, Dh] / [U, T] copy per role. */
+static void P(guided_velocity)(const orc_cfg* c, const orc_io* io, const orc_block* blocks,
+                               int U, int S, const float* x, float t, int use_cfg, int step,
+                               int mode, int n, const float* scales, int T,
+                               float* const* rk, float* const* rv, uint8_t* const* rm,
+                               const uint8_t* lat_mask, float* tt, float* vtmp, float* v) {
+    size_t nel = (size_t)U * S * c->latent_dim;
+    for (int u = 0; u < U; u++) tt[u] = t;
+    P(forward)(c, io, blocks, U, S, x, tt, T, rk[0], rv[0], rm[0], lat_mask, v, NULL);
+    if (!use_cfg) return;
+    if (mode == 0) {
+        float* vc = vtmp + nel * n;  /* keep v_c while v accumulates */
+        memcpy(vc, v, sizeof(float) * nel);
+        for (int k = 0; k < n; k++)
+            P(forward)(c, io, blocks, U, S, x, tt, T, rk[1 + k], rv[1 + k], rm[1 + k], lat_mask,
+                       vtmp + nel * k, NULL);
+        for (size_t j = 0; j < nel; j++) {
+            R acc = (R)vc[j];
+            for (int k = 0; k < n; k++) acc = acc + ((R)vc[j] - (R)vtmp[nel * k + j]) * (R)scales[k];
+            v[j] = (float)acc;
+        }
+    } else {
+        int a = mode == 1 ? 0 : step % n;
+        P(forward)(c, io, blocks, U, S, x, tt, T, rk[1 + a], rv[1 + a], rm[1 + a], lat_mask, vtmp, NULL);
+        for (size_t j = 0; j < nel; j++) v[j] = (float)((R)v[j] + ((R)v[j] - (R)vtmp[j]) * (R)scales[a]);
+    }
+}
+
+/* euler_sampler.rs:132-718 — the RF ODE loop with CFG, every mode and integrator:
+ *   x = noise (times truncation_factor); t_i = 0.999 (1 - i/N) in f32 (:325-328);
+ *   CFG at t iff a signal is enabled and min_t <= t <= max_t (:379);
+ *   v1 = guided velocity at (x, t_i) (guided_velocity), temporally rescaled (:525-530);
+ *   the speaker-KV scaling reverts once t_{i+1} < min_t <= t_i, before the corrector (:533-545);
+ *   Euler  x += v1 dt;
+ *   Heun   x_p = x + v1 dt, v2 = guided velocity at (x_p, t_{i+1}) with the same dropped
+ *          condition index i, rescaled at t_{i+1}; x += (v1 + v2) / 2 dt (:567-683);
+ *   PLMS-4 the newest-first history of v1 (at most 4) is cleared whenever (CFG on,
+ *          speaker KV active) changes between steps (:341-347, :383-390); Adams-Bashforth
+ *          orders 1-4 (:98-117); x += v_eff dt (:714).
+ * ctx_k/ctx_v [L, R*U, T, H, Dh], ctx_mask [R*U, T] are role-major: role r of utterance u
+ * is row r*U + u, with role 0 the conditioned bundle, Joint role 1 the unconditioned one,
+ * and Independent / Alternating role 1+k the bundle with enabled signal k dropped
+ * (make_single_uncond, :41-85).  Speaker-KV scaling (kv_scaling.rs:10-60) multiplies the
+ * aux keys of role 0, and of every role in Independent mode (the batched cache), in the
+ * first max_layers layers.  lat_mask (nullable, [U, S]) masks latent keys in every forward.
+ * Runs at most max_steps_run steps (<= 0: all); returns the number run. */
+int P(sample_rf)(const orc_cfg* c, const orc_io* io, const orc_block* blocks, int U, int S,
+                 const float* x0, int T, const float* ctx_k, const float* ctx_v,
+                 const uint8_t* ctx_mask, const uint8_t* lat_mask, const orc_sampler* sp,
+                 int max_steps_run, float* x_out) {
+    const int L = c->num_layers, HD = c->num_heads * c->head_dim, Pd = c->latent_dim;
+    const int N = sp->num_steps;
+    float scales[3];
+    const int n = P(cfg_signals)(sp, scales);
+    const int Rr = sp->cfg_mode == 1 ? (n > 0 ? 2 : 1) : 1 + n;  /* roles */
+    const size_t nel = (size_t)U * S * Pd, lay = (size_t)T * HD;
+    float* rk[4];
+    float* rv[4];
+    uint8_t* rm[4];
+    for (int r = 0; r < Rr; r++) {
+        rk[r] = (float*)malloc(sizeof(float) * L * U * lay);
+        rv[r] = (float*)malloc(sizeof(float) * L * U * lay);
+        rm[r] = (uint8_t*)malloc((size_t)U * T);
+        for (int l = 0; l < L; l++)
+            for (int u = 0; u < U; u++) {
+                size_t src = ((size_t)l * Rr * U + (size_t)r * U + u) * lay;
+                memcpy(rk[r] + ((size_t)l * U + u) * lay, ctx_k + src, sizeof(float) * lay);
+                memcpy(rv[r] + ((size_t)l * U + u) * lay, ctx_v + src, sizeof(float) * lay);
+            }
+        memcpy(rm[r], ctx_mask + (size_t)r * U * T, (size_t)U * T);
+    }
+    int scaled_roles[4], nsr = 0;
+    scaled_roles[nsr++] = 0;
+    if (sp->cfg_mode == 0)
+        for (int r = 1; r < Rr; r++) scaled_roles[nsr++] = r;
+    const int nl = sp->speaker_kv_max_layers < 0 || sp->speaker_kv_max_layers > L ? L : sp->speaker_kv_max_layers;
+    int spk_active = sp->has_speaker_kv != 0;
+    if (spk_active && sp->has_speaker)
+        P(scale_aux_kv)(rk, rv, scaled_roles, nsr, nl, U, T, HD, sp->ctx_aux_start, sp->speaker_kv_scale);
+
+    float* ts = (float*)malloc(sizeof(float) * (N + 1));
+    for (int i = 0; i <= N; i++) ts[i] = 0.999f * (1.0f - (float)i / (float)N);
+    float* v1 = (float*)malloc(sizeof(float) * nel);
+    float* v2 = (float*)malloc(sizeof(float) * nel);
+    float* xp = (float*)malloc(sizeof(float) * nel);
+    float* vtmp = (float*)malloc(sizeof(float) * nel * (n + 1 > 1 ? n + 1 : 1));
+    float* hist = (float*)malloc(sizeof(float) * nel * 4);  /* hist[k] = k-th newest */
+    float* tt = (float*)malloc(sizeof(float) * U);
+    int nhist = 0;
+    for (size_t j = 0; j < nel; j++) x_out[j] = sp->has_truncation ? (float)((R)x0[j] * (R)sp->truncation_factor) : x0[j];
+    int prev_cfg = n > 0 && sp->min_t <= ts[0] && ts[0] <= sp->max_t, prev_spk = spk_active;
+    const int run = (max_steps_run > 0 && max_steps_run < N) ? max_steps_run : N;
+    for (int i = 0; i < run; i++) {
+        const float t = ts[i], tn = ts[i + 1];
+        const int use_cfg = n > 0 && sp->min_t <= t && t <= sp->max_t;
+        if (sp->method == 2 && (use_cfg != prev_cfg || spk_active != prev_spk)) {
+            nhist = 0;
+            prev_cfg = use_cfg;
+            prev_spk = spk_active;
+        }
+        P(guided_velocity)(c, io, blocks, U, S, x_out, t, use_cfg, i, sp->cfg_mode, n, scales, T,
+                           rk, rv, rm, lat_mask, tt, vtmp, v1);
+        if (sp->has_temporal_rescale) P(temporal_rescale)(v1, x_out, nel, t, sp->rescale_k, sp->rescale_sigma);
+        if (spk_active && sp->has_speaker && sp->speaker_kv_has_min_t && tn < sp->speaker_kv_min_t &&
+            t >= sp->speaker_kv_min_t) {
+            P(scale_aux_kv)(rk, rv, scaled_roles, nsr, nl, U, T, HD, sp->ctx_aux_start, 1.0f / sp->speaker_kv_scale);
+            spk_active = 0;
+        }
+        const float dt = tn - t;
+        if (sp->method == 1) {
+            for (size_t j = 0; j < nel; j++) xp[j] = (float)((R)x_out[j] + (R)v1[j] * (R)dt);
+            const int use_cfg2 = n > 0 && sp->min_t <= tn && tn <= sp->max_t;
+            P(guided_velocity)(c, io, blocks, U, S, xp, tn, use_cfg2, i, sp->cfg_mode, n, scales, T,
+                               rk, rv, rm, lat_mask, tt, vtmp, v2);
+            if (sp->has_temporal_rescale) P(temporal_rescale)(v2, xp, nel, tn, sp->rescale_k, sp->rescale_sigma);
+            for (size_t j = 0; j < nel; j++) {
+                R ve = ((R)v1[j] + (R)v2[j]) / R_C(2.0);
+                x_out[j] = (float)((R)x_out[j] + ve * (R)dt);
+            }
+        } else if (sp->method == 2) {
+            for (int k = (nhist < 4 ? nhist : 3); k > 0; k--) memcpy(hist + nel * k, hist + nel * (k - 1), sizeof(float) * nel);
+            memcpy(hist, v1, sizeof(float) * nel);
+            nhist = nhist < 4 ? nhist + 1 : 4;
+            for (size_t j = 0; j < nel; j++) {
+                R ve;
+                const R h0 = (R)hist[j];
+                if (nhist == 1) {
+                    ve = h0;
+                } else if (nhist == 2) {
+                    ve = h0 * (R)1.5f + (R)hist[nel + j] * (R)-0.5f;
+                } else if (nhist == 3) {
+                    ve = h0 * (R)(23.0f / 12.0f) + (R)hist[nel + j] * (R)(-16.0f / 12.0f) +
+                         (R)hist[2 * nel + j] * (R)(5.0f / 12.0f);
+                } else {
+                    ve = h0 * (R)(55.0f / 24.0f) + (R)hist[nel + j] * (R)(-59.0f / 24.0f) +
+                         (R)hist[2 * nel + j] * (R)(37.0f / 24.0f) + (R)hist[3 * nel + j] * (R)(-9.0f / 24.0f);
+                }
+                x_out[j] = (float)((R)x_out[j] + ve * (R)dt);
+            }
+        } else {
+            for (size_t j = 0; j < nel; j++) x_out[j] = (float)((R)x_out[j] + (R)v1[j] * (R)dt);
+        }
+    }
+    for (int r = 0; r < Rr; r++) { free(rk[r]); free(rv[r]); free(rm[r]); }
+    free(ts); free(v1); free(v2); free(xp); free(vtmp); free(hist); free(tt);
+    return run;
+}
