@@ -20,10 +20,15 @@
  *   - Host weight pointers are float32 in Burn "row" layout [d_in, d_out], y = x @ W + b
  *     (src/weights/record_builders.rs:37-66).  The library copies and re-lays them out
  *     in device memory; the caller keeps ownership of every host buffer.
- *   - A context owns one HIP stream, its device buffers and its captured graphs.  It is
+ *   - A context owns its HIP streams, its device buffers and its captured graphs.  It is
  *     single-threaded (not re-entrant); use one context per thread.
- *   - Joint CFG rows: for utterance u, batch row 2u is the conditioned row and row
- *     2u+1 the unconditioned row (EncodedCondition::zeros_like, condition.rs:144-154).
+ *   - Sampler rows are role-major: role r of utterance u is batch row r * U + u.  Role 0
+ *     is the conditioned bundle; with cfg_mode Joint, role 1 is the unconditioned bundle
+ *     (EncodedCondition::zeros_like, condition.rs:144-154); with Independent or
+ *     Alternating, role 1 + k is the bundle with the k-th active CFG signal dropped
+ *     (make_single_uncond, euler_sampler.rs:41-85), the signals ordered text, speaker,
+ *     caption and active when their scale is > 0 (speaker: has_speaker; caption:
+ *     has_caption).  A dropped signal has zero K/V and all of its keys masked.
  */
 #ifndef IRODORI_HIP_H
 #define IRODORI_HIP_H
@@ -104,11 +109,13 @@ typedef struct irodori_io_weights {
     const float* out_b;      /* [P] */
 } irodori_io_weights;
 
-/* SamplerParams + GuidanceConfig (src/rf/params.rs:9-35, :61-92). */
+/* SamplerParams + GuidanceConfig + TemporalRescaleConfig + SpeakerKvConfig
+ * (src/rf/params.rs:9-92) and the request facts that select the active CFG signals
+ * (euler_sampler.rs:163-200). */
 typedef struct irodori_sampler_params {
     int32_t num_steps;
-    int32_t method;   /* IRODORI_METHOD_* (Euler implemented) */
-    int32_t cfg_mode; /* IRODORI_CFG_* (Joint implemented) */
+    int32_t method;   /* IRODORI_METHOD_* */
+    int32_t cfg_mode; /* IRODORI_CFG_* */
     float scale_text;
     float scale_caption;
     float scale_speaker;
@@ -116,7 +123,17 @@ typedef struct irodori_sampler_params {
     float max_t;
     int32_t has_truncation;
     float truncation_factor;
-    int32_t has_speaker; /* model uses speaker conditioning (affects the Joint scale set) */
+    int32_t has_speaker;  /* the model uses speaker conditioning and the condition holds a speaker state */
+    int32_t has_caption;  /* the condition holds a caption with at least one valid token */
+    int32_t has_temporal_rescale; /* temporal_score_rescale (math.rs:38-53) with k, sigma */
+    float rescale_k;
+    float rescale_sigma;
+    int32_t has_speaker_kv;       /* force-speaker KV scaling (kv_scaling.rs:10-60) */
+    float speaker_kv_scale;
+    int32_t speaker_kv_max_layers; /* < 0: every layer */
+    int32_t speaker_kv_has_min_t;  /* revert the scaling once t drops below speaker_kv_min_t */
+    float speaker_kv_min_t;
+    int32_t ctx_aux_start;         /* first aux (speaker) key of the context sequence (= text keys) */
 } irodori_sampler_params;
 
 /* ---- errors ----------------------------------------------------------------------- */
@@ -167,13 +184,17 @@ int irodori_forward_masked(irodori_ctx* ctx, int batch, int seq, const float* x_
 int irodori_block_forward(irodori_ctx* ctx, int layer, int batch, int seq, float* x,
                           const float* cond);
 
-/* Joint-CFG RF sampling (sample_euler_rf_cfg, euler_sampler.rs:132-718): U utterances,
- * rows 2u / 2u+1 as above, x0 [U,S,P] -> x_out [U,S,P].  Host pointers; one hipGraph
- * replayed per step.  Truncation (params.rs:146-155) is applied to x0 when set. */
+/* RF sampling (sample_euler_rf_cfg, euler_sampler.rs:132-718): U utterances, x0 [U,S,P]
+ * -> x_out [U,S,P], every cfg_mode (rows role-major, see the conventions above) and method
+ * (Euler; Heun at 2 forwards per step; PLMS-4), temporal score rescaling and speaker-KV
+ * scaling.  A step's forward runs only the roles it needs (the conditioned role alone
+ * outside the CFG window; Alternating the conditioned role and the role dropped at that
+ * step), each role as its own kernel chain of a captured hipGraph.  Host pointers.
+ * Truncation (params.rs:146-155) is applied to x0 when set. */
 int irodori_sample(irodori_ctx* ctx, const irodori_sampler_params* params, int utterances,
                    int seq, const float* x0, float* x_out);
-/* Joint-CFG sampling of a padded variable-length batch: utterance u attends to its first
- * lengths[u] latent frames (both CFG rows), so frames below lengths[u] match an unpadded
+/* Sampling of a padded variable-length batch: utterance u attends to its first
+ * lengths[u] latent frames (in every role), so frames below lengths[u] match an unpadded
  * run of that utterance (BASELINE config 5's padded batches; the reference sampler always
  * passes latent_mask = None, euler_sampler.rs:410-523).  lengths: host int32 [U]. */
 int irodori_sample_masked(irodori_ctx* ctx, const irodori_sampler_params* params, int utterances,

@@ -93,12 +93,17 @@ struct LayerBufs {
 
 // A captured RF step is specific to the batch shape, the context length and the CFG
 // scale (a kernel argument baked into the graph).
+// One captured sampler evaluation: the role chains it runs, the integrator phase, and
+// what the captured kernels read (context length, latent masks, scaled speaker KV).
 struct GraphKey {
-    int B, S, T;
-    uint32_t scale_bits;
+    int U, S, T;
+    int roles;          // bit r set: role r runs (rows r*U .. r*U + U - 1)
+    int method, phase;
     int latent_masked;  // the captured attention reads the latent key masks
+    int kv_scaled;      // the captured attention reads the speaker-scaled context copies
     bool operator<(const GraphKey& o) const {
-        return std::tie(B, S, T, scale_bits, latent_masked) < std::tie(o.B, o.S, o.T, o.scale_bits, o.latent_masked);
+        return std::tie(U, S, T, roles, method, phase, latent_masked, kv_scaled) <
+               std::tie(o.U, o.S, o.T, o.roles, o.method, o.phase, o.latent_masked, o.kv_scaled);
     }
 };
 
@@ -108,10 +113,11 @@ struct irodori_ctx {
     bool bf16 = true;
     size_t esz = 2;  // compute element size
     hipStream_t stream = nullptr;
-    // Second capture stream and fork/join events: a captured RF step runs the two halves
-    // of the batch rows as independent chains of kernels until the output head.
-    hipStream_t stream2 = nullptr;
-    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
+    // Side capture streams and fork/join events: a captured sampler evaluation runs each
+    // CFG role as an independent chain of kernels (role 0 on `stream`) until the update.
+    static constexpr int kMaxRoles = 3;
+    hipStream_t side[kMaxRoles - 1] = {};
+    hipEvent_t ev_fork = nullptr, ev_join[kMaxRoles - 1] = {};
     std::vector<void*> allocs;
     uint64_t dev_bytes = 0;
 
@@ -134,7 +140,17 @@ struct irodori_ctx {
     float* rope_cos = nullptr;
     float* rope_sin = nullptr;
     float* xt = nullptr;    // [rows, S, P] sampler state / forward input
-    float* vout = nullptr;  // [rows, S, P]
+    float* vout = nullptr;  // [rows, S, P] head outputs (role-major in the sampler)
+    float* xin = nullptr;   // [rows, S, P] Heun predictor state
+    float* hist = nullptr;  // [4][rows, S, P] Heun v1 / PLMS-4 history
+    RfEval* plan = nullptr; // sampler evaluations [2 * steps]
+    int plan_cap = 0;       // steps
+    // Speaker-KV scaling (kv_scaling.rs:10-60): per-layer copies of the context K / V^T
+    // with the aux keys of the scaled rows multiplied; the attention of layers < kvs_layers
+    // reads them while kvs_on.
+    std::vector<void*> act_k, act_v;
+    bool kvs_on = false;
+    int kvs_layers = 0;
     int* step = nullptr;    // device step counter
     int* zero_step = nullptr;
     // Latent key mask of the current call (build_joint_mask's self part,
@@ -153,9 +169,6 @@ struct irodori_ctx {
     float* cond = nullptr;
     float* mid = nullptr;
     float* tab = nullptr;
-    float* t_sched = nullptr;
-    int* cfg_on = nullptr;
-    int sched_cap = 0;
     VecLinJob* d_jobs_mlp = nullptr;   // 3 jobs
     VecLinJob* d_jobs_down = nullptr;  // L*6 jobs
     VecLinJob* d_jobs_up = nullptr;    // L*6 jobs
@@ -380,8 +393,11 @@ int enqueue_part(irodori_ctx* c, int l, int B, int S, const ModTable& mt, int pa
             aa.vstride0 = vt_stride;
             if (c->t_ctx > 0) {
                 const int T1 = g.max_ctx, vs1 = (g.max_ctx + 63) / 64 * 64, nt1 = (g.max_ctx + 63) / 64;
-                aa.K1 = static_cast<const T*>(lb.ctx_k) + (size_t)r0 * H * T1 * Dh;
-                aa.V1 = static_cast<const T*>(lb.ctx_v) + (size_t)r0 * H * Dh * vs1;
+                const bool kvs = c->kvs_on && l < c->kvs_layers;
+                const T* ck = static_cast<const T*>(kvs ? c->act_k[l] : lb.ctx_k);
+                const T* cv = static_cast<const T*>(kvs ? c->act_v[l] : lb.ctx_v);
+                aa.K1 = ck + (size_t)r0 * H * T1 * Dh;
+                aa.V1 = cv + (size_t)r0 * H * Dh * vs1;
                 aa.len1 = c->t_ctx;
                 aa.stride1 = T1;
                 aa.vstride1 = vs1;
@@ -473,39 +489,28 @@ int enqueue_part_any(irodori_ctx* c, int l, int B, int S, const ModTable& mt, in
                    : enqueue_part<float>(c, l, B, S, mt, part, 0, c->stream);
 }
 
-int enqueue_inproj(irodori_ctx* c, int B, int S, int rows_per_src, const ModTable& mt) {
+// in_proj + the first adaLN for batch rows [r0, r0 + B): row r0 + b reads source row
+// b mod src_batches of src [src_batches, S, P].
+int enqueue_inproj(irodori_ctx* c, int B, int S, const float* src, int src_batches, int r0, const ModTable& mt,
+                   hipStream_t st) {
     const auto& g = c->cfg;
+    const size_t tok0 = (size_t)r0 * S;
+    float* x = c->x + tok0 * g.model_dim;
     if (c->bf16)
-        launch_inproj_norm<bf16>(c->xt, rows_per_src, c->in_w, c->in_b, c->x, static_cast<bf16*>(c->h),
-                                 B * S, S, g.latent_dim, g.model_dim, g.norm_eps, mt, c->stream);
+        launch_inproj_norm<bf16>(src, src_batches, c->in_w, c->in_b, x, static_cast<bf16*>(c->h) + tok0 * g.model_dim,
+                                 B * S, S, g.latent_dim, g.model_dim, g.norm_eps, mt, st);
     else
-        launch_inproj_norm<float>(c->xt, rows_per_src, c->in_w, c->in_b, c->x, static_cast<float*>(c->h),
-                                  B * S, S, g.latent_dim, g.model_dim, g.norm_eps, mt, c->stream);
+        launch_inproj_norm<float>(src, src_batches, c->in_w, c->in_b, x,
+                                  static_cast<float*>(c->h) + tok0 * g.model_dim, B * S, S, g.latent_dim,
+                                  g.model_dim, g.norm_eps, mt, st);
     return check_launch("in_proj");
 }
 
-// All kernels of one RF step (Joint CFG, B = 2U rows): in_proj, L blocks, output head +
-// CFG combine + Euler update, step advance.  Rows never interact inside the blocks, so
-// the L blocks run as two independent chains, rows [0, B/2) on the context's stream and
-// rows [B/2, B) on the second stream, forked after in_proj and joined before the head:
-// in a captured graph the two chains overlap each other's launch gaps, tails and uneven
-// attention work (the conditioned row attends to the context, the unconditioned one does
-// not).  Every row shares the step's modulation vector.
-int enqueue_rf_step(irodori_ctx* c, int B, int S, float scale) {
+// Output head for batch rows [r0, r0 + B) into the matching rows of vout.
+int enqueue_head(irodori_ctx* c, int B, int S, int r0, hipStream_t st) {
     const auto& g = c->cfg;
-    ModTable mt{c->tab, c->step, 1, B, g.num_layers};
-    IRO_TRY(enqueue_inproj(c, B, S, 2, mt));
-    const int half = B / 2;
-    IRO_HIP_CHECK(hipEventRecord(c->ev_fork, c->stream));
-    IRO_HIP_CHECK(hipStreamWaitEvent(c->stream2, c->ev_fork, 0));
-    for (int l = 0; l < g.num_layers; l++) {
-        IRO_TRY(enqueue_layer_any(c, l, half, S, mt, 0, c->stream));
-        IRO_TRY(enqueue_layer_any(c, l, B - half, S, mt, half, c->stream2));
-    }
-    IRO_HIP_CHECK(hipEventRecord(c->ev_join, c->stream2));
-    IRO_HIP_CHECK(hipStreamWaitEvent(c->stream, c->ev_join, 0));
     FinalArgs fa{};
-    fa.x = c->x;
+    fa.x = c->x + (size_t)r0 * S * g.model_dim;
     fa.norm_w = c->out_norm_w;
     fa.out_wT = c->out_wT;
     fa.out_b = c->out_b;
@@ -514,15 +519,66 @@ int enqueue_rf_step(irodori_ctx* c, int B, int S, float scale) {
     fa.D = g.model_dim;
     fa.P = g.latent_dim;
     fa.eps = g.norm_eps;
-    fa.mode = 1;
-    fa.xt = c->xt;
-    fa.t_sched = c->t_sched;
-    fa.cfg_on = c->cfg_on;
-    fa.step = c->step;
-    fa.scale = scale;
+    fa.v_out = c->vout + (size_t)r0 * S * g.latent_dim;
+    launch_final(fa, st);
+    return check_launch("output head");
+}
+
+// All kernels of one sampler evaluation (one model forward per active role, then the
+// update): every active role r runs in_proj from src and the L blocks over its rows
+// [r U, r U + U) as an independent chain of kernels — the first on the context's stream,
+// the others on side streams forked from it and joined before the output head, which
+// computes every active role's velocity and applies the guided combine and the integrator
+// update in one kernel.  Rows never interact inside the forward, so in a captured graph the chains
+// overlap each other's launch gaps, tails and uneven attention work (the conditioned
+// role attends to the context, a dropped signal's keys are skipped).  Every row shares
+// the evaluation's modulation vector (mt.step_add selects t_{i+1} for the Heun
+// corrector).  The step counter advances after the step's last evaluation.
+int enqueue_eval(irodori_ctx* c, int U, int S, int roles, int method, int phase, const float* src) {
+    const auto& g = c->cfg;
+    // Every row of the evaluation (b < kMaxRoles U, chain-local or not) maps to vector step.
+    ModTable mt{c->tab, c->step, 1, U * irodori_ctx::kMaxRoles, g.num_layers, phase};
+    int active[irodori_ctx::kMaxRoles], na = 0;
+    for (int r = 0; r < irodori_ctx::kMaxRoles; r++)
+        if (roles & (1 << r)) active[na++] = r;
+    if (na == 0) { set_last_error("no role to evaluate"); return IRODORI_ERR_INVALID_ARG; }
+    // in_proj of every active row in one launch before the fork when the active roles are
+    // the first na (rows [0, na U)), else at the head of each chain.
+    const bool contiguous = active[na - 1] == na - 1;
+    if (contiguous) IRO_TRY(enqueue_inproj(c, na * U, S, src, U, 0, mt, c->stream));
+    if (na > 1) IRO_HIP_CHECK(hipEventRecord(c->ev_fork, c->stream));
+    for (int k = 0; k < na; k++) {
+        hipStream_t st = k == 0 ? c->stream : c->side[k - 1];
+        if (k > 0) IRO_HIP_CHECK(hipStreamWaitEvent(st, c->ev_fork, 0));
+        const int r0 = active[k] * U;
+        if (!contiguous) IRO_TRY(enqueue_inproj(c, U, S, src, U, r0, mt, st));
+        for (int l = 0; l < g.num_layers; l++) IRO_TRY(enqueue_layer_any(c, l, U, S, mt, r0, st));
+        if (k > 0) IRO_HIP_CHECK(hipEventRecord(c->ev_join[k - 1], st));
+    }
+    for (int k = 1; k < na; k++) IRO_HIP_CHECK(hipStreamWaitEvent(c->stream, c->ev_join[k - 1], 0));
+    FinalArgs fa{};
+    fa.x = c->x;
+    fa.norm_w = c->out_norm_w;
+    fa.out_wT = c->out_wT;
+    fa.out_b = c->out_b;
+    fa.B = U;
+    fa.S = S;
+    fa.D = g.model_dim;
+    fa.P = g.latent_dim;
+    fa.eps = g.norm_eps;
+    fa.nrole = na;
+    for (int k = 0; k < na; k++) fa.role[k] = active[k];
+    fa.rf.x = c->xt;
+    fa.rf.xin = c->xin;
+    fa.rf.hist = c->hist;
+    fa.rf.plan = c->plan;
+    fa.rf.step = c->step;
+    fa.rf.phase = phase;
+    fa.rf.method = method;
+    fa.rf.n = U * S * g.latent_dim;
     launch_final(fa, c->stream);
-    launch_step_advance(c->step, c->stream);
-    return check_launch("rf step tail");
+    if (method != IRODORI_METHOD_HEUN || phase == 1) launch_step_advance(c->step, c->stream);
+    return check_launch("sampler evaluation");
 }
 
 int check_ready(irodori_ctx* c, int B) {
@@ -537,6 +593,18 @@ int check_ready(irodori_ctx* c, int B) {
                                 " not set");
     }
     return IRODORI_OK;
+}
+
+// Active CFG signals in the sampler's order (euler_sampler.rs:163-200): text if its scale
+// is > 0, speaker if the condition holds a speaker state and its scale is > 0, caption if
+// the condition holds a caption with a valid token and its scale is > 0.  scales[k] = the
+// k-th active signal's scale; returns the count.
+int cfg_signals(const irodori_sampler_params* p, float* scales) {
+    int n = 0;
+    if (p->scale_text > 0.f) scales[n++] = p->scale_text;
+    if (p->has_speaker && p->scale_speaker > 0.f) scales[n++] = p->scale_speaker;
+    if (p->has_caption && p->scale_caption > 0.f) scales[n++] = p->scale_caption;
+    return n;
 }
 
 int validate_params(const irodori_sampler_params* p) {
@@ -562,12 +630,23 @@ int validate_params(const irodori_sampler_params* p) {
                 "Joint instead");
     IRO_REQUIRE(p->method >= 0 && p->method <= 2, IRODORI_ERR_CONFIG, "unknown sampler method");
     IRO_REQUIRE(p->cfg_mode >= 0 && p->cfg_mode <= 2, IRODORI_ERR_CONFIG, "unknown cfg guidance mode");
+    if (p->has_temporal_rescale) {
+        IRO_REQUIRE(std::isfinite(p->rescale_k), IRODORI_ERR_CONFIG, "temporal_rescale.k must be finite");
+        IRO_REQUIRE(p->rescale_sigma != 0.f, IRODORI_ERR_CONFIG, "temporal_rescale.sigma must not be zero");
+    }
+    if (p->has_speaker_kv) {
+        IRO_REQUIRE(std::isfinite(p->speaker_kv_scale) && p->speaker_kv_scale > 0.f, IRODORI_ERR_CONFIG,
+                    "speaker_kv.scale must be finite and > 0");
+        IRO_REQUIRE(!p->speaker_kv_has_min_t ||
+                        (std::isfinite(p->speaker_kv_min_t) && p->speaker_kv_min_t >= 0.f && p->speaker_kv_min_t <= 1.f),
+                    IRODORI_ERR_CONFIG, "speaker_kv.min_t must be finite and in [0, 1]");
+    }
     if (p->cfg_mode == IRODORI_CFG_JOINT) {
-        // euler_sampler.rs:209-228: all active scales (text, speaker if used) must match.
+        // euler_sampler.rs:209-228: all active scales must match.
+        float act[3];
+        const int n = cfg_signals(p, act);
         float lo = INFINITY, hi = -INFINITY;
-        float act[2] = {p->scale_text, p->has_speaker ? p->scale_speaker : 0.f};
-        for (float s : act)
-            if (s > 0.f) { lo = fminf(lo, s); hi = fmaxf(hi, s); }
+        for (int k = 0; k < n; k++) { lo = fminf(lo, act[k]); hi = fmaxf(hi, act[k]); }
         IRO_REQUIRE(!(hi - lo >= 1e-6f), IRODORI_ERR_CONFIG,
                     "cfg_guidance_mode=Joint requires all active cfg scales to be equal, but got text=" +
                         std::to_string(p->scale_text) + ", speaker=" + std::to_string(p->scale_speaker) +
@@ -576,10 +655,9 @@ int validate_params(const irodori_sampler_params* p) {
     return IRODORI_OK;
 }
 
-float joint_scale(const irodori_sampler_params* p) {
-    if (p->scale_text > 0.f) return p->scale_text;
-    if (p->has_speaker && p->scale_speaker > 0.f) return p->scale_speaker;
-    return 0.f;
+// Number of sampler roles (context bundles) for n active signals (role-major rows).
+int cfg_roles(const irodori_sampler_params* p, int n) {
+    return p->cfg_mode == IRODORI_CFG_JOINT ? (n > 0 ? 2 : 1) : 1 + n;
 }
 
 }  // namespace
@@ -613,10 +691,13 @@ int irodori_ctx_destroy(irodori_ctx* c) {
     if (c->stream) (void)hipStreamSynchronize(c->stream);
     for (auto& kv : c->graphs) (void)hipGraphExecDestroy(kv.second);
     for (void* p : c->allocs) (void)hipFree(p);
-    if (c->stream2) (void)hipStreamSynchronize(c->stream2);
+    for (auto sd : c->side)
+        if (sd) (void)hipStreamSynchronize(sd);
     if (c->ev_fork) (void)hipEventDestroy(c->ev_fork);
-    if (c->ev_join) (void)hipEventDestroy(c->ev_join);
-    if (c->stream2) (void)hipStreamDestroy(c->stream2);
+    for (auto ev : c->ev_join)
+        if (ev) (void)hipEventDestroy(ev);
+    for (auto sd : c->side)
+        if (sd) (void)hipStreamDestroy(sd);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
     return IRODORI_OK;
@@ -655,9 +736,11 @@ int irodori_ctx_create(int device, const irodori_dit_config* cfg, irodori_ctx** 
     c->bf16 = g.compute_dtype == IRODORI_DTYPE_BF16;
     c->esz = c->bf16 ? 2 : 4;
     IRO_HIP_CHECK(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
-    IRO_HIP_CHECK(hipStreamCreateWithFlags(&c->stream2, hipStreamNonBlocking));
     IRO_HIP_CHECK(hipEventCreateWithFlags(&c->ev_fork, hipEventDisableTiming));
-    IRO_HIP_CHECK(hipEventCreateWithFlags(&c->ev_join, hipEventDisableTiming));
+    for (int i = 0; i < irodori_ctx::kMaxRoles - 1; i++) {
+        IRO_HIP_CHECK(hipStreamCreateWithFlags(&c->side[i], hipStreamNonBlocking));
+        IRO_HIP_CHECK(hipEventCreateWithFlags(&c->ev_join[i], hipEventDisableTiming));
+    }
 
     int D = g.model_dim, F = g.mlp_hidden, H = g.num_heads, Dh = g.head_dim, L = g.num_layers;
     int R = g.max_rows, S = g.max_seq, T = g.max_ctx > 0 ? g.max_ctx : 1, P = g.latent_dim;
@@ -709,6 +792,8 @@ int irodori_ctx_create(int device, const irodori_dit_config* cfg, irodori_ctx** 
     IRO_TRY(dalloc(c.get(), &c->rope_sin, sizeof(float) * (size_t)S * Dh / 2));
     IRO_TRY(dalloc(c.get(), &c->xt, sizeof(float) * M * P));
     IRO_TRY(dalloc(c.get(), &c->vout, sizeof(float) * M * P));
+    IRO_TRY(dalloc(c.get(), &c->xin, sizeof(float) * M * P));
+    IRO_TRY(dalloc(c.get(), &c->hist, sizeof(float) * 4 * M * P));
     IRO_TRY(dalloc(c.get(), &c->lat_bits, sizeof(unsigned long long) * (size_t)R * ((S + 63) / 64)));
     IRO_TRY(dalloc(c.get(), &c->lat_mask_f, sizeof(float) * (size_t)R * S));
     IRO_TRY(dalloc(c.get(), &c->step, sizeof(int)));
@@ -931,7 +1016,7 @@ static int forward_impl(irodori_ctx* c, int B, int S, const float* x_t, const fl
     IRO_TRY(upload(c, c->xt, x_t, sizeof(float) * (size_t)B * S * P));
     IRO_TRY(enqueue_mod_table(c, B, false));
     ModTable mt{c->tab, c->zero_step, 0, 1, L};
-    IRO_TRY(enqueue_inproj(c, B, S, 1, mt));
+    IRO_TRY(enqueue_inproj(c, B, S, c->xt, B, 0, mt, c->stream));
     size_t n = (size_t)B * S * D;
     if (debug) IRO_HIP_CHECK(hipMemcpyAsync(debug, c->x, sizeof(float) * n, hipMemcpyDeviceToHost, c->stream));
     for (int l = 0; l < L; l++) {
@@ -940,20 +1025,7 @@ static int forward_impl(irodori_ctx* c, int B, int S, const float* x_t, const fl
             IRO_HIP_CHECK(hipMemcpyAsync(debug + (size_t)(l + 1) * n, c->x, sizeof(float) * n, hipMemcpyDeviceToHost,
                                          c->stream));
     }
-    FinalArgs fa{};
-    fa.x = c->x;
-    fa.norm_w = c->out_norm_w;
-    fa.out_wT = c->out_wT;
-    fa.out_b = c->out_b;
-    fa.B = B;
-    fa.S = S;
-    fa.D = D;
-    fa.P = P;
-    fa.eps = g.norm_eps;
-    fa.mode = 0;
-    fa.v_out = c->vout;
-    launch_final(fa, c->stream);
-    IRO_TRY(check_launch("output head"));
+    IRO_TRY(enqueue_head(c, B, S, 0, c->stream));
     IRO_HIP_CHECK(hipMemcpyAsync(v_out, c->vout, sizeof(float) * (size_t)B * S * P, hipMemcpyDeviceToHost, c->stream));
     IRO_HIP_CHECK(hipStreamSynchronize(c->stream));
     return IRODORI_OK;
@@ -997,70 +1069,180 @@ int irodori_sample_device(irodori_ctx* c, const irodori_sampler_params* p, int U
     return sample_device_impl(c, p, U, S, nullptr, d_x0, d_x_out);
 }
 
+// Restores the context's speaker-KV routing when a sampling call ends.
+struct KvsScope {
+    irodori_ctx* c;
+    ~KvsScope() { c->kvs_on = false; }
+};
+
 // lengths (nullable, host [U]): utterance u attends to its first lengths[u] latent keys
-// in both CFG rows (padded variable-length batches).
+// in every role (padded variable-length batches).
 static int sample_device_impl(irodori_ctx* c, const irodori_sampler_params* p, int U, int S, const int32_t* lengths,
                        const float* d_x0, float* d_x_out) {
     IRO_GUARD_BEGIN
     IRO_REQUIRE(c && p && d_x0 && d_x_out, IRODORI_ERR_INVALID_ARG, "null argument");
     IRO_TRY(validate_params(p));
-    IRO_REQUIRE(p->cfg_mode == IRODORI_CFG_JOINT, IRODORI_ERR_CONFIG,
-                "the HIP sampler implements cfg_guidance_mode=Joint");
-    IRO_REQUIRE(p->method == IRODORI_METHOD_EULER, IRODORI_ERR_CONFIG, "the HIP sampler implements the Euler method");
     const auto& g = c->cfg;
-    int B = 2 * U;
-    IRO_REQUIRE(U > 0 && B <= g.max_rows, IRODORI_ERR_SHAPE, "2 * utterances must be in [2, max_rows]");
+    float scales[3];
+    const int n = cfg_signals(p, scales);
+    const int R = cfg_roles(p, n);
+    const int B = R * U;
+    IRO_REQUIRE(U > 0 && B <= g.max_rows, IRODORI_ERR_SHAPE,
+                std::to_string(R) + " roles x " + std::to_string(U) + " utterances exceed max_rows");
     IRO_REQUIRE(S > 0 && S <= g.max_seq, IRODORI_ERR_SHAPE, "seq out of range [1, max_seq]");
     IRO_TRY(check_ready(c, B));
     IRO_HIP_CHECK(hipSetDevice(c->device));
-    int N = p->num_steps, P = g.latent_dim;
+    const int N = p->num_steps, P = g.latent_dim, L = g.num_layers;
+    const int method = p->method, mode = p->cfg_mode;
+    const bool heun = method == IRODORI_METHOD_HEUN, plms = method == IRODORI_METHOD_PLMS4;
     if (lengths) {
         std::vector<uint8_t> m((size_t)B * S, 0);
         for (int u = 0; u < U; u++) {
             IRO_REQUIRE(lengths[u] >= 1 && lengths[u] <= S, IRODORI_ERR_SHAPE, "utterance length must be in [1, seq]");
-            for (int r = 0; r < 2; r++)
-                for (int s = 0; s < lengths[u]; s++) m[(size_t)(2 * u + r) * S + s] = 1;
+            for (int r = 0; r < R; r++)
+                for (int s2 = 0; s2 < lengths[u]; s2++) m[(size_t)(r * U + u) * S + s2] = 1;
         }
         IRO_TRY(upload_latent_mask(c, B, S, m.data()));
     }
     LatentMaskScope lms(c, lengths != nullptr);
 
-    // Schedule (euler_sampler.rs:325-328, f32) and per-step CFG window (:379).
+    // Schedule t_i = 0.999 (1 - i/N) in f32 (euler_sampler.rs:325-328), the CFG window
+    // (:379), and one planned evaluation per step (two for Heun, the corrector at t_{i+1}).
     std::vector<float> ts(N + 1);
-    std::vector<int> on(N);
     for (int i = 0; i <= N; i++) ts[i] = 0.999f * (1.0f - (float)i / (float)N);
-    float scale = joint_scale(p);
-    for (int i = 0; i < N; i++) on[i] = (scale > 0.f && p->min_t <= ts[i] && ts[i] <= p->max_t) ? 1 : 0;
-    IRO_TRY(ensure_nvec(c, N));
-    if (N + 1 > c->sched_cap) {
+    auto cfg_at = [&](float t) { return n > 0 && p->min_t <= t && t <= p->max_t; };
+    std::vector<RfEval> plan((size_t)2 * N);
+    std::vector<int> roles_of((size_t)2 * N, 0);
+    auto fill = [&](int e, float t, float dt, bool on, int step) {
+        RfEval& ev = plan[e];
+        ev = RfEval{};
+        ev.dt = dt;
+        int roles = 1;
+        if (on) {
+            if (mode == IRODORI_CFG_JOINT) {
+                ev.nterm = 1; ev.role[0] = 1; ev.scale[0] = scales[0];
+            } else if (mode == IRODORI_CFG_INDEPENDENT) {
+                ev.nterm = n;
+                for (int k = 0; k < n; k++) { ev.role[k] = 1 + k; ev.scale[k] = scales[k]; }
+            } else {  // Alternating: the dropped signal cycles with the step (:472-473)
+                const int a = step % n;
+                ev.nterm = 1; ev.role[0] = 1 + a; ev.scale[0] = scales[a];
+            }
+            for (int k = 0; k < ev.nterm; k++) roles |= 1 << ev.role[k];
+        }
+        if (p->has_temporal_rescale && t < 1.0f) {
+            // math.rs:38-53, scalars in f32
+            const float omt = 1.0f - t;
+            const float snr = (omt * omt) / (t * t);
+            const float sig2 = p->rescale_sigma * p->rescale_sigma;
+            ev.rescale = 1;
+            ev.omt = omt;
+            ev.ratio = (snr * sig2 + 1.0f) / (snr * sig2 / p->rescale_k + 1.0f);
+        }
+        roles_of[e] = roles;
+    };
+    bool spk_active = p->has_speaker_kv != 0;  // speaker_kv.is_some() (:337)
+    int revert_step = -1, nhist = 0;
+    int prev_cfg = cfg_at(ts[0]), prev_spk = spk_active;
+    for (int i = 0; i < N; i++) {
+        const float t = ts[i], tn = ts[i + 1];
+        const bool on = cfg_at(t);
+        if (plms && (on != (bool)prev_cfg || spk_active != (bool)prev_spk)) {  // (:383-390)
+            nhist = 0;
+            prev_cfg = on;
+            prev_spk = spk_active;
+        }
+        fill(2 * i, t, tn - t, on, i);
+        if (spk_active && p->has_speaker && p->speaker_kv_has_min_t && tn < p->speaker_kv_min_t &&
+            t >= p->speaker_kv_min_t) {  // (:533-545), before the corrector
+            revert_step = i;
+            spk_active = false;
+        }
+        if (plms) {
+            nhist = nhist < 4 ? nhist + 1 : 4;
+            plan[2 * i].ab_order = nhist;
+        }
+        if (heun) fill(2 * i + 1, tn, tn - t, cfg_at(tn), i);
+    }
+
+    // Modulation vectors for every t_i (i <= N: the corrector's t_{i+1}), the plan.
+    IRO_TRY(ensure_nvec(c, N + 1));
+    if (N > c->plan_cap) {
         IRO_HIP_CHECK(hipStreamSynchronize(c->stream));
-        IRO_TRY(dalloc(c, &c->t_sched, sizeof(float) * (N + 1)));
-        IRO_TRY(dalloc(c, &c->cfg_on, sizeof(int) * (N + 1)));
-        c->sched_cap = N + 1;
+        IRO_TRY(dalloc(c, &c->plan, sizeof(RfEval) * 2 * (size_t)N));
+        c->plan_cap = N;
         for (auto& kv : c->graphs) (void)hipGraphExecDestroy(kv.second);
         c->graphs.clear();
     }
-    IRO_TRY(upload(c, c->t_sched, ts.data(), sizeof(float) * (N + 1)));
-    IRO_TRY(upload(c, c->cfg_on, on.data(), sizeof(int) * N));
-    IRO_TRY(upload(c, c->tvec, ts.data(), sizeof(float) * N));
-    IRO_TRY(enqueue_mod_table(c, N, false));
+    IRO_TRY(upload(c, c->plan, plan.data(), sizeof(RfEval) * plan.size()));
+    IRO_TRY(upload(c, c->tvec, ts.data(), sizeof(float) * (N + 1)));
+    IRO_TRY(enqueue_mod_table(c, N + 1, false));
+
+    // Speaker-KV scaling (euler_sampler.rs:258-264, :294-300): the conditioned rows, or in
+    // Independent mode every row of the batched cache, in the first max_layers layers.
+    const bool kvs = p->has_speaker_kv && p->has_speaker && c->t_ctx > 0;
+    const int nl = p->speaker_kv_max_layers < 0 || p->speaker_kv_max_layers > L ? L : p->speaker_kv_max_layers;
+    const int rows_scaled = mode == IRODORI_CFG_INDEPENDENT ? B : U;
+    const int T1 = g.max_ctx > 0 ? g.max_ctx : 1, vs1 = (T1 + 63) / 64 * 64;
+    KvsScope kscope{c};
+    auto scale_kv = [&](bool from_ctx, float factor) -> int {
+        for (int l = 0; l < nl; l++) {
+            auto& lb = c->layers[l];
+            const void* sk = from_ctx ? lb.ctx_k : c->act_k[l];
+            const void* sv = from_ctx ? lb.ctx_v : c->act_v[l];
+            if (c->bf16)
+                launch_scale_ctx_aux<bf16>(static_cast<const bf16*>(sk), static_cast<const bf16*>(sv),
+                                           static_cast<bf16*>(c->act_k[l]), static_cast<bf16*>(c->act_v[l]), B,
+                                           rows_scaled, g.num_heads, T1, vs1, c->t_ctx, p->ctx_aux_start, factor,
+                                           c->stream);
+            else
+                launch_scale_ctx_aux<float>(static_cast<const float*>(sk), static_cast<const float*>(sv),
+                                            static_cast<float*>(c->act_k[l]), static_cast<float*>(c->act_v[l]), B,
+                                            rows_scaled, g.num_heads, T1, vs1, c->t_ctx, p->ctx_aux_start, factor,
+                                            c->stream);
+        }
+        return check_launch("speaker kv scaling");
+    };
+    if (kvs) {
+        IRO_REQUIRE(p->ctx_aux_start >= 0 && p->ctx_aux_start <= c->t_ctx, IRODORI_ERR_CONFIG,
+                    "ctx_aux_start must be in [0, t_ctx]");
+        IRO_REQUIRE(g.head_dim == 64, IRODORI_ERR_CONFIG, "speaker KV scaling needs head_dim 64");
+        if ((int)c->act_k.size() < L) {
+            IRO_HIP_CHECK(hipStreamSynchronize(c->stream));
+            const size_t kb = (size_t)g.max_rows * g.num_heads * T1 * g.head_dim * c->esz;
+            const size_t vb = (size_t)g.max_rows * g.num_heads * g.head_dim * vs1 * c->esz;
+            c->act_k.assign(L, nullptr);
+            c->act_v.assign(L, nullptr);
+            // Zeroed once: the V^T padding columns past max_ctx (which the scaling never
+            // writes) must hold finite values, like the context buffers they mirror.
+            for (int l = 0; l < L; l++) {
+                IRO_TRY(dev_alloc(c, &c->act_k[l], kb));
+                IRO_TRY(dev_alloc(c, &c->act_v[l], vb));
+                IRO_HIP_CHECK(hipMemsetAsync(c->act_k[l], 0, kb, c->stream));
+                IRO_HIP_CHECK(hipMemsetAsync(c->act_v[l], 0, vb, c->stream));
+            }
+        }
+        IRO_TRY(scale_kv(true, p->speaker_kv_scale));
+        c->kvs_on = true;
+        c->kvs_layers = nl;
+    }
+
     launch_scale_copy(d_x0, c->xt, U * S * P, p->has_truncation ? p->truncation_factor : 1.0f, c->stream);
     IRO_HIP_CHECK(hipMemsetAsync(c->step, 0, sizeof(int), c->stream));
     IRO_TRY(check_launch("sampler setup"));
 
-    // One captured RF step, replayed N times.
-    uint32_t sbits;
-    memcpy(&sbits, &scale, 4);
-    GraphKey key{B, S, c->t_ctx, sbits, lengths ? 1 : 0};
-    hipGraphExec_t exec = nullptr;
-    auto it = c->graphs.find(key);
-    if (it != c->graphs.end()) {
-        exec = it->second;
-    } else {
+    // One captured graph per distinct evaluation (roles, phase), replayed per step.
+    auto graph_for = [&](int roles, int phase, hipGraphExec_t* out) -> int {
+        GraphKey key{U, S, c->t_ctx, roles, method, phase, lengths ? 1 : 0, c->kvs_on ? 1 : 0};
+        auto it = c->graphs.find(key);
+        if (it != c->graphs.end()) {
+            *out = it->second;
+            return IRODORI_OK;
+        }
         hipGraph_t graph = nullptr;
         IRO_HIP_CHECK(hipStreamSynchronize(c->stream));
         IRO_HIP_CHECK(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
-        int rc = enqueue_rf_step(c, B, S, scale);
+        int rc = enqueue_eval(c, U, S, roles, method, phase, phase == 1 ? c->xin : c->xt);
         hipError_t ee = hipStreamEndCapture(c->stream, &graph);
         if (rc != IRODORI_OK) {
             if (graph) (void)hipGraphDestroy(graph);
@@ -1070,6 +1252,7 @@ static int sample_device_impl(irodori_ctx* c, const irodori_sampler_params* p, i
             set_last_error(std::string("graph capture: ") + hipGetErrorString(ee));
             return IRODORI_ERR_HIP;
         }
+        hipGraphExec_t exec = nullptr;
         ee = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
         (void)hipGraphDestroy(graph);
         if (ee != hipSuccess) {
@@ -1077,8 +1260,19 @@ static int sample_device_impl(irodori_ctx* c, const irodori_sampler_params* p, i
             return IRODORI_ERR_HIP;
         }
         c->graphs[key] = exec;
+        *out = exec;
+        return IRODORI_OK;
+    };
+    for (int i = 0; i < N; i++) {
+        hipGraphExec_t ex = nullptr;
+        IRO_TRY(graph_for(roles_of[2 * i], 0, &ex));
+        IRO_HIP_CHECK(hipGraphLaunch(ex, c->stream));
+        if (i == revert_step && kvs) IRO_TRY(scale_kv(false, 1.0f / p->speaker_kv_scale));
+        if (heun) {
+            IRO_TRY(graph_for(roles_of[2 * i + 1], 1, &ex));
+            IRO_HIP_CHECK(hipGraphLaunch(ex, c->stream));
+        }
     }
-    for (int i = 0; i < N; i++) IRO_HIP_CHECK(hipGraphLaunch(exec, c->stream));
     IRO_HIP_CHECK(hipMemcpyAsync(d_x_out, c->xt, sizeof(float) * (size_t)U * S * P, hipMemcpyDeviceToDevice, c->stream));
     IRO_HIP_CHECK(hipStreamSynchronize(c->stream));
     return IRODORI_OK;
@@ -1107,14 +1301,15 @@ static int sample_host(irodori_ctx* c, const irodori_sampler_params* p, int U, i
     IRO_REQUIRE(c && p && x0 && x_out, IRODORI_ERR_INVALID_ARG, "null argument");
     IRO_TRY(validate_params(p));
     const auto& g = c->cfg;
-    IRO_REQUIRE(U > 0 && 2 * U <= g.max_rows && S > 0 && S <= g.max_seq, IRODORI_ERR_SHAPE, "utterances/seq out of range");
+    IRO_REQUIRE(U > 0 && U <= g.max_rows && S > 0 && S <= g.max_seq, IRODORI_ERR_SHAPE, "utterances/seq out of range");
     IRO_HIP_CHECK(hipSetDevice(c->device));
     size_t n = (size_t)U * S * g.latent_dim;
-    // Stage through the forward-output buffer (unused by the sampler).
-    IRO_TRY(upload(c, c->vout, x0, sizeof(float) * n));
-    int rc = sample_device_impl(c, p, U, S, lengths, c->vout, c->vout);
+    // Staged through the Heun predictor buffer: the sampler reads x0 before its first
+    // evaluation and writes x_out after its last.
+    IRO_TRY(upload(c, c->xin, x0, sizeof(float) * n));
+    int rc = sample_device_impl(c, p, U, S, lengths, c->xin, c->xin);
     if (rc != IRODORI_OK) return rc;
-    IRO_HIP_CHECK(hipMemcpy(x_out, c->vout, sizeof(float) * n, hipMemcpyDeviceToHost));
+    IRO_HIP_CHECK(hipMemcpy(x_out, c->xin, sizeof(float) * n, hipMemcpyDeviceToHost));
     return IRODORI_OK;
     IRO_GUARD_END
 }
@@ -1128,7 +1323,7 @@ int irodori_profile_layer(irodori_ctx* c, int B, int S, int iters, irodori_kerne
     IRO_REQUIRE(iters > 0, IRODORI_ERR_INVALID_ARG, "iters must be > 0");
     IRO_TRY(check_ready(c, B));
     IRO_HIP_CHECK(hipSetDevice(c->device));
-    int D = g.model_dim, L = g.num_layers;
+    int L = g.num_layers;
     // Modulation vectors for t = 0.5 on every row; state from one in_proj of zeros + 1.
     std::vector<float> t(B, 0.5f), x0((size_t)B * S * g.latent_dim, 1.0f);
     IRO_TRY(ensure_nvec(c, B));
@@ -1136,7 +1331,7 @@ int irodori_profile_layer(irodori_ctx* c, int B, int S, int iters, irodori_kerne
     IRO_TRY(upload(c, c->xt, x0.data(), sizeof(float) * x0.size()));
     IRO_TRY(enqueue_mod_table(c, B, false));
     ModTable mt{c->tab, c->zero_step, 0, 1, L};
-    IRO_TRY(enqueue_inproj(c, B, S, 1, mt));
+    IRO_TRY(enqueue_inproj(c, B, S, c->xt, B, 0, mt, c->stream));
     IRO_TRY(enqueue_layer_any(c, 0, B, S, mt));  // fills q/k/v/gate/o/u
     IRO_HIP_CHECK(hipStreamSynchronize(c->stream));
 
@@ -1150,11 +1345,8 @@ int irodori_profile_layer(irodori_ctx* c, int B, int S, int iters, irodori_kerne
         (void)hipEventRecord(e0, c->stream);
         for (int it = 0; it < iters; it++) {
             if (kidx == 6) {
-                FinalArgs fa{};
-                fa.x = c->x; fa.norm_w = c->out_norm_w; fa.out_wT = c->out_wT; fa.out_b = c->out_b;
-                fa.B = B; fa.S = S; fa.D = D; fa.P = g.latent_dim; fa.eps = g.norm_eps;
-                fa.mode = 0; fa.v_out = c->vout;
-                launch_final(fa, c->stream);
+                rc = enqueue_head(c, B, S, 0, c->stream);
+                if (rc != IRODORI_OK) break;
                 continue;
             }
             if (!c->bf16) {

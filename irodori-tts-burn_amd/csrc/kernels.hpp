@@ -10,14 +10,18 @@ namespace irodori {
 
 // Where the adaLN modulation vectors of a forward live: a table of rows
 // [vec][layer][kind(attn,mlp)][chunk(shift,scale,gate)][D] (gate already tanh'd).
-// Row index for batch row b: vec = (*step) * step_stride + (b / rows_per_vec).
+// Row index for batch row b: vec = (*step + step_add) * step_stride + (b / rows_per_vec).
 struct ModTable {
     const float* tab;
     const int* step;   // device step counter (0 for single forwards)
     int step_stride;   // vectors per step
     int rows_per_vec;  // batch rows sharing one vector
     int layers;
+    int step_add = 0;  // evaluation offset (1: the Heun corrector at t_{i+1})
 };
+__host__ __device__ inline int mod_vec_index(const ModTable& mt, int step, int b) {
+    return (step + mt.step_add) * mt.step_stride + b / mt.rows_per_vec;
+}
 
 // Position of latent/context key s inside a V^T row.  bf16 path (32x32x16 attention):
 // bits 2 and 3 of the key index swapped; f32 path (16x16 attention): keys permuted inside
@@ -37,15 +41,86 @@ void launch_fused_adaln_op(const float* x, const float* scale, const float* shif
 template <typename T>
 void launch_norm_mod(const float* x, T* h, int M, int S, int D, float eps, ModTable mt,
                      int layer, int kind, hipStream_t st);
-// x = x_src[row] @ in_w + in_b (in_proj), then h = norm_mod(x) for (layer 0, attn).
+// x[b] = x_src[b mod src_batches] @ in_w + in_b (in_proj), then h = norm_mod(x) for
+// (layer 0, attn); b is the batch row.
 template <typename T>
-void launch_inproj_norm(const float* x_src, int rows_per_src, const float* in_w,
+void launch_inproj_norm(const float* x_src, int src_batches, const float* in_w,
                         const float* in_b, float* x, T* h, int M, int S, int P, int D,
                         float eps, ModTable mt, hipStream_t st);
 
-// Output head.  mode 0: v[b,s,:] = out_proj(out_norm(x[b,s,:])).
-// mode 1 (Joint CFG + Euler): per utterance u, v = v_c + scale (v_c - v_u) when the step
-// is guided (else v_c), then x_t[u,s,:] += v * (t[step+1] - t[step]).
+
+// One model evaluation of the RF sampler, as the update kernel applies it
+// (euler_sampler.rs:435-714): the guided velocity v = v_0 + sum_k (v_0 - v_{role_k}) s_k
+// over the role-major head outputs, the temporal score rescale v = (v omt + x) ratio / omt
+// - x / omt (math.rs:38-53) at the evaluation's t when rescale != 0, then the integrator.
+struct RfEval {
+    float dt;          // t_{i+1} - t_i of the step
+    float omt, ratio;  // 1 - t and the rescale ratio at the evaluation's t
+    int rescale;
+    int nterm;         // CFG terms
+    int role[3];
+    float scale[3];
+    int ab_order;      // PLMS-4: history entries (newest first) after this step's push
+};
+enum RfMethod { RF_EULER = 0, RF_HEUN = 1, RF_PLMS4 = 2 };
+// Evaluation (step, phase) of the plan is plan[2 * (*step) + phase]; phase 1 is the Heun
+// corrector.  Euler: x += v dt.  Heun phase 0: hist = v, xin = x + v dt; phase 1:
+// x += (hist + v) / 2 dt (the evaluation state is xin).  PLMS-4: hist slot (step mod 4) =
+// v, x += sum of the Adams-Bashforth coefficients of order ab_order times the newest
+// entries (euler_sampler.rs:98-117).
+struct RfUpdateArgs {
+    float* x;     // [n] sampler state
+    float* xin;   // [n] Heun predictor state
+    float* hist;  // [4][n]
+    const RfEval* plan;  // null: no update (plain output head)
+    const int* step;
+    int phase, method;
+    int n;        // U * S * P
+};
+
+// Element j of the state after the guided velocity v of evaluation e (f32, in the
+// reference's operation order).
+__device__ inline void rf_apply(const RfUpdateArgs& a, const RfEval& e, int step, int j, float v) {
+    const bool corr = a.method == RF_HEUN && a.phase == 1;
+    const float xs = corr ? a.xin[j] : a.x[j];
+    if (e.rescale) v = (v * e.omt + xs) * e.ratio / e.omt - xs / e.omt;  // math.rs:38-53
+    const float x = a.x[j];
+    if (a.method == RF_EULER) {
+        a.x[j] = x + v * e.dt;
+    } else if (a.method == RF_HEUN) {
+        if (a.phase == 0) {
+            a.hist[j] = v;
+            a.xin[j] = x + v * e.dt;
+        } else {
+            a.x[j] = x + (a.hist[j] + v) / 2.0f * e.dt;
+        }
+    } else {
+        const size_t n = (size_t)a.n;
+        a.hist[(size_t)(step & 3) * n + j] = v;
+        float ve = v;
+        if (e.ab_order >= 2) {
+            const float h1 = a.hist[(size_t)((step - 1) & 3) * n + j];
+            if (e.ab_order == 2) {
+                ve = v * 1.5f + h1 * -0.5f;
+            } else {
+                const float h2 = a.hist[(size_t)((step - 2) & 3) * n + j];
+                if (e.ab_order == 3) {
+                    ve = v * (23.0f / 12.0f) + h1 * (-16.0f / 12.0f) + h2 * (5.0f / 12.0f);
+                } else {
+                    const float h3 = a.hist[(size_t)((step - 3) & 3) * n + j];
+                    ve = v * (55.0f / 24.0f) + h1 * (-59.0f / 24.0f) + h2 * (37.0f / 24.0f) + h3 * (-9.0f / 24.0f);
+                }
+            }
+        }
+        a.x[j] = x + ve * e.dt;
+    }
+}
+
+// Output head: v[b,s,:] = out_proj(out_norm(x[b,s,:])) into v_out [B,S,P]; or, with
+// rf.plan set, the sampler evaluation's head and update fused: for each of the B = U
+// utterances, the rows role[k] * U + u of its nrole active roles (role[0] = 0, increasing),
+// their velocities combined as v = v_0 + sum_k (v_0 - v_{role_k}) s_k per the plan, then
+// rf_apply.
 struct FinalArgs {
     const float* x;
     const float* norm_w;
@@ -53,15 +128,21 @@ struct FinalArgs {
     const float* out_b;   // [P]
     int B, S, D, P;
     float eps;
-    int mode;
-    float* v_out;        // mode 0: [B,S,P]
-    float* xt;           // mode 1: [U,S,P]
-    const float* t_sched;  // [steps+1]
-    const int* cfg_on;     // [steps]
-    const int* step;
-    float scale;
+    float* v_out;         // [B,S,P] (plain head)
+    int nrole;            // sampler evaluation: active roles
+    int role[3];
+    RfUpdateArgs rf;
 };
 void launch_final(const FinalArgs& a, hipStream_t st);
+
+// Speaker-KV scaling of cached context (kv_scaling.rs:10-60) on the device copies the
+// attention reads: for rows < rows_scaled, the keys [aux_start, t_ctx) of K
+// ([R, H, T1, Dh]) and V^T ([R, H, Dh, vs1], key order vt_pos_*) times factor; src == dst
+// scales in place, otherwise every other element is copied unchanged.
+template <typename T>
+void launch_scale_ctx_aux(const T* src_k, const T* src_v, T* dst_k, T* dst_v, int rows,
+                          int rows_scaled, int H, int T1, int vs1, int t_ctx, int aux_start,
+                          float factor, hipStream_t st);
 void launch_step_advance(int* step, hipStream_t st);
 void launch_scale_copy(const float* src, float* dst, int n, float s, hipStream_t st);
 

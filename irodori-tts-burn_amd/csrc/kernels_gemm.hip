@@ -117,8 +117,7 @@ __device__ __forceinline__ int stage_off(int r, int col) {
 
 __device__ __forceinline__ const float* gate_vec(const ModTable& mt, int b, int layer, int kind,
                                                 int D) {
-    int step = mt.step ? *mt.step : 0;
-    int vec = step * mt.step_stride + b / mt.rows_per_vec;
+    int vec = mod_vec_index(mt, mt.step ? *mt.step : 0, b);
     return mt.tab + ((size_t)vec * mt.layers * 6 + (size_t)layer * 6 + kind * 3 + 2) * D;
 }
 
@@ -205,7 +204,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
 #pragma unroll
                 for (int u = 0; u < 2; u++) {
                     const int bb = u ? b_hi : b_lo;
-                    const float* g = a.mt.tab + ((size_t)(step * a.mt.step_stride + bb / a.mt.rows_per_vec) * a.mt.layers * 6 +
+                    const float* g = a.mt.tab + ((size_t)mod_vec_index(a.mt, step, bb) * a.mt.layers * 6 +
                                                  (size_t)a.layer * 6 + a.kind * 3 + 2) * a.N;
 #pragma unroll
                     for (int j = 0; j < FN; j++) gpre[i][u][j] = (!u || need_hi) ? g[n0 + wn0 + 32 * j + cl] : 0.f;

@@ -1,5 +1,5 @@
-// HBM-bound row kernels: RMSNorm, adaLN modulation, in_proj + modulation, output head
-// with the Joint-CFG combine and Euler update.  One wavefront per row, 4 rows per
+// HBM-bound row kernels: RMSNorm, adaLN modulation, in_proj + modulation, output head.
+// One wavefront per row, 4 rows per
 // 256-thread workgroup; rows are read with 16-byte loads and reduced in registers with
 // cross-lane shuffles (no LDS), so each row is read from HBM exactly once.
 #include "common.hpp"
@@ -12,8 +12,7 @@ namespace {
 constexpr int kRowsPerBlock = 4;
 
 __device__ __forceinline__ int mod_vec(const ModTable& mt, int b) {
-    int step = mt.step ? *mt.step : 0;
-    return step * mt.step_stride + b / mt.rows_per_vec;
+    return mod_vec_index(mt, mt.step ? *mt.step : 0, b);
 }
 
 // Pointer to (shift, scale, gate) of (layer, kind) for batch row b.
@@ -112,7 +111,7 @@ constexpr int kInRows = 8;
 
 template <typename T, int NCH>
 __global__ __launch_bounds__(256) void inproj_norm_kernel(
-    const float* __restrict__ x_src, int rows_per_src, const float* __restrict__ in_w,
+    const float* __restrict__ x_src, int src_batches, const float* __restrict__ in_w,
     const float* __restrict__ in_b, float* __restrict__ x, T* __restrict__ h, int M, int S, int P,
     int D, float eps, ModTable mt) {
     __shared__ float xs[kInRows][64];
@@ -135,7 +134,7 @@ __global__ __launch_bounds__(256) void inproj_norm_kernel(
             float v = 0.f;
             if (row < M && pp < pn) {
                 const int b = row / S, sq = row % S;
-                v = x_src[((size_t)(b / rows_per_src) * S + sq) * P + p0 + pp];
+                v = x_src[((size_t)(b % src_batches) * S + sq) * P + p0 + pp];
             }
             xs[r][pp] = v;
         }
@@ -204,18 +203,21 @@ __global__ __launch_bounds__(256) void inproj_norm_kernel(
 }
 
 // Output head: one 256-thread block per kFinFrames latent frames handles every batch row
-// of those frames, two rows at a time, so the Joint-CFG combine of rows (2u, 2u+1) and the
-// Euler update happen in the block.  v[b,s,p] = (sum_d x[b,s,d] * W'[p,d]) / rms(x[b,s,:])
-// + b_out[p] with W' = out_norm.weight (.) W_out^T folded at ingest — the same product as
-// out_proj(out_norm(x)) (norm.rs:25-39, dit/model.rs:391-392).  The block's rows are staged
-// in LDS; thread (ks, p) computes output p over the k-slice ks for every staged row
-// (reading its own W' row once per block), and the KS slices are summed through LDS.
+// of those frames, NR rows (a group) at a time.  v[b,s,p] = (sum_d x[b,s,d] * W'[p,d]) /
+// rms(x[b,s,:]) + b_out[p] with W' = out_norm.weight (.) W_out^T folded at ingest — the
+// same product as out_proj(out_norm(x)) (norm.rs:25-39, dit/model.rs:391-392).  The group's
+// rows are staged in LDS; thread (ks, p) computes output p over the k-slice ks for every
+// staged row (reading its own W' row once per block), and the KS slices are summed through
+// LDS.  Plain head: groups are consecutive rows.  Sampler evaluation: group u holds the
+// active roles' rows of utterance u, and the block applies the guided combine and the
+// integrator update to them (euler_sampler.rs:460-467, :497-510, :683-714) — one kernel
+// after the role chains join.
 constexpr int kFinFrames = 4;
 
-template <int PT>
+template <int PT, int NR>
 __global__ __launch_bounds__(256) void final_kernel(FinalArgs a) {
     constexpr int KS = 256 / PT;
-    constexpr int R = 2 * kFinFrames;
+    constexpr int R = NR * kFinFrames;  // staged row slot f * NR + i
     extern __shared__ __attribute__((aligned(16))) float fsm[];
     const int D = a.D, P = a.P;
     float* xs = fsm;                  // [R][D]
@@ -227,25 +229,27 @@ __global__ __launch_bounds__(256) void final_kernel(FinalArgs a) {
     const int s0 = blockIdx.x * kFinFrames;
     const int nf = a.S - s0 < kFinFrames ? a.S - s0 : kFinFrames;
     const int kper = D / KS;
-    const int step = a.step ? *a.step : 0;
-    float dt = 0.f;
-    int cfg_on = 0;
-    if (a.mode == 1) {
-        dt = a.t_sched[step + 1] - a.t_sched[step];
-        cfg_on = a.cfg_on[step];
+    const bool rf = a.rf.plan != nullptr;
+    int step = 0;
+    RfEval ev{};
+    if (rf) {
+        step = *a.rf.step;
+        ev = a.rf.plan[2 * step + a.rf.phase];
     }
-    for (int b0 = 0; b0 < a.B; b0 += 2) {
-        const bool two = b0 + 1 < a.B;
+    const int ngroups = rf ? a.B : (a.B + NR - 1) / NR;
+    for (int g = 0; g < ngroups; g++) {
+        // Row of slot i: the group's i-th row (a plain head's short last group repeats its
+        // first row); frames past S stage zeros.
+        auto row_of = [&](int i) {
+            if (rf) return a.role[i] * a.B + g;
+            const int b = g * NR + i;
+            return b < a.B ? b : g * NR;
+        };
         __syncthreads();
-        // Stage row r = 2 f + i = x[b0 + i, s0 + f, :] (the second row repeats the first when
-        // B is odd; frames past S are zero).
         for (int e = tid * 4; e < R * D; e += 1024) {
-            const int r = e / D, d = e % D, f = r >> 1, i = r & 1;
+            const int r = e / D, d = e % D, f = r / NR, i = r % NR;
             float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (f < nf) {
-                const int b = (i && two) ? b0 + 1 : b0;
-                v = *reinterpret_cast<const float4*>(a.x + ((size_t)b * a.S + s0 + f) * D + d);
-            }
+            if (f < nf) v = *reinterpret_cast<const float4*>(a.x + ((size_t)row_of(i) * a.S + s0 + f) * D + d);
             *reinterpret_cast<float4*>(xs + r * D + d) = v;
         }
         __syncthreads();
@@ -282,8 +286,8 @@ __global__ __launch_bounds__(256) void final_kernel(FinalArgs a) {
 #pragma unroll
         for (int r = 0; r < R; r++) red[(ks * R + r) * PT + p] = acc[r];
         __syncthreads();
-        if (tid < R * PT) {
-            const int r = tid / PT, pp = tid % PT;
+        for (int idx = tid; idx < R * PT; idx += 256) {  // R * PT may exceed the block
+            const int r = idx / PT, pp = idx % PT;
             float v = 0.f;
 #pragma unroll
             for (int k2 = 0; k2 < KS; k2++) v += red[(k2 * R + r) * PT + pp];
@@ -293,16 +297,22 @@ __global__ __launch_bounds__(256) void final_kernel(FinalArgs a) {
         for (int e = tid; e < nf * PT; e += 256) {
             const int f = e / PT, pp = e % PT, sq = s0 + f;
             if (pp >= P) continue;
-            const float v0 = vals[(2 * f) * PT + pp], v1 = vals[(2 * f + 1) * PT + pp];
-            if (a.mode == 0) {
-                a.v_out[((size_t)b0 * a.S + sq) * P + pp] = v0;
-                if (two) a.v_out[((size_t)(b0 + 1) * a.S + sq) * P + pp] = v1;
-            } else {
-                // euler_sampler.rs:467 (v_c + (v_c - v_u) * scale) and :714 (x += v * dt)
-                const float vv = cfg_on ? v0 + (v0 - v1) * a.scale : v0;
-                float* xt = a.xt + ((size_t)(b0 / 2) * a.S + sq) * P + pp;
-                *xt = *xt + vv * dt;
+            if (!rf) {
+#pragma unroll
+                for (int i = 0; i < NR; i++)
+                    if (g * NR + i < a.B) a.v_out[((size_t)(g * NR + i) * a.S + sq) * P + pp] = vals[(f * NR + i) * PT + pp];
+                continue;
             }
+            const float v0 = vals[(f * NR) * PT + pp];
+            float v = v0;
+            for (int k = 0; k < ev.nterm; k++) {
+                int slot = 0;
+#pragma unroll
+                for (int i = 1; i < NR; i++)
+                    if (a.role[i] == ev.role[k]) slot = i;
+                v = v + (v0 - vals[(f * NR + slot) * PT + pp]) * ev.scale[k];
+            }
+            rf_apply(a.rf, ev, step, (g * a.S + sq) * P + pp, v);
         }
     }
 }
@@ -347,13 +357,13 @@ void launch_norm_mod(const float* x, T* h, int M, int S, int D, float eps, ModTa
 }
 
 template <typename T>
-void launch_inproj_norm(const float* x_src, int rows_per_src, const float* in_w,
+void launch_inproj_norm(const float* x_src, int src_batches, const float* in_w,
                         const float* in_b, float* x, T* h, int M, int S, int P, int D, float eps,
                         ModTable mt, hipStream_t st) {
     int grid = (M + kInRows - 1) / kInRows;
     int nch = (D + 1023) / 1024;
 #define IRO_INPROJ(N)                                                                      \
-    inproj_norm_kernel<T, N><<<grid, 256, 0, st>>>(x_src, rows_per_src, in_w, in_b, x, h, M, \
+    inproj_norm_kernel<T, N><<<grid, 256, 0, st>>>(x_src, src_batches, in_w, in_b, x, h, M, \
                                                    S, P, D, eps, mt)
     if (nch <= 1) IRO_INPROJ(1);
     else if (nch <= 2) IRO_INPROJ(2);
@@ -371,18 +381,26 @@ template void launch_inproj_norm<float>(const float*, int, const float*, const f
 template void launch_inproj_norm<bf16>(const float*, int, const float*, const float*, float*,
                                        bf16*, int, int, int, int, float, ModTable, hipStream_t);
 
-template <int PT>
-static void launch_final_pt(const FinalArgs& a, hipStream_t st) {
-    constexpr int KS = 256 / PT, R = 2 * kFinFrames;
+template <int PT, int NR>
+static void launch_final_cfg(const FinalArgs& a, hipStream_t st) {
+    constexpr int KS = 256 / PT, R = NR * kFinFrames;
     const size_t lds = sizeof(float) * ((size_t)R * a.D + (size_t)KS * R * PT + (size_t)R * PT + R);
     static bool attr_set = false;
     if (!attr_set) {
         // Sized for the largest model width the context accepts (D <= 2048).
         constexpr int kMax = (int)sizeof(float) * (R * 2048 + KS * R * PT + R * PT + R);
-        (void)hipFuncSetAttribute((const void*)final_kernel<PT>, hipFuncAttributeMaxDynamicSharedMemorySize, kMax);
+        (void)hipFuncSetAttribute((const void*)final_kernel<PT, NR>, hipFuncAttributeMaxDynamicSharedMemorySize, kMax);
         attr_set = true;
     }
-    final_kernel<PT><<<(a.S + kFinFrames - 1) / kFinFrames, 256, lds, st>>>(a);
+    final_kernel<PT, NR><<<(a.S + kFinFrames - 1) / kFinFrames, 256, lds, st>>>(a);
+}
+
+template <int PT>
+static void launch_final_pt(const FinalArgs& a, hipStream_t st) {
+    const int nr = a.rf.plan ? a.nrole : 2;
+    if (nr <= 1) launch_final_cfg<PT, 1>(a, st);
+    else if (nr == 2) launch_final_cfg<PT, 2>(a, st);
+    else launch_final_cfg<PT, 3>(a, st);
 }
 
 void launch_final(const FinalArgs& a, hipStream_t st) {

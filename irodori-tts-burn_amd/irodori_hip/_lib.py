@@ -63,7 +63,11 @@ class SamplerParamsC(C.Structure):
         ("num_steps", C.c_int32), ("method", C.c_int32), ("cfg_mode", C.c_int32),
         ("scale_text", C.c_float), ("scale_caption", C.c_float), ("scale_speaker", C.c_float),
         ("min_t", C.c_float), ("max_t", C.c_float), ("has_truncation", C.c_int32),
-        ("truncation_factor", C.c_float), ("has_speaker", C.c_int32),
+        ("truncation_factor", C.c_float), ("has_speaker", C.c_int32), ("has_caption", C.c_int32),
+        ("has_temporal_rescale", C.c_int32), ("rescale_k", C.c_float), ("rescale_sigma", C.c_float),
+        ("has_speaker_kv", C.c_int32), ("speaker_kv_scale", C.c_float),
+        ("speaker_kv_max_layers", C.c_int32), ("speaker_kv_has_min_t", C.c_int32),
+        ("speaker_kv_min_t", C.c_float), ("ctx_aux_start", C.c_int32),
     ]
 
 

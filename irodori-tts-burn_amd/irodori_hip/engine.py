@@ -37,22 +37,35 @@ def _c32(a) -> np.ndarray:
     return np.ascontiguousarray(a, dtype=np.float32)
 
 
-def sampler_params_c(p: SamplerParams, has_speaker: bool = True) -> L.SamplerParamsC:
+def sampler_params_c(p: SamplerParams, has_speaker: bool = True, has_caption: bool = False,
+                     ctx_aux_start: int = 0) -> L.SamplerParamsC:
+    """irodori_sampler_params from the params and the request facts: whether the condition
+    holds a speaker state (and the model uses it) or a caption with a valid token, and the
+    first aux key of the cached context (the text key count)."""
     mode = {CfgGuidanceMode.INDEPENDENT: L.CFG_INDEPENDENT, CfgGuidanceMode.JOINT: L.CFG_JOINT,
             CfgGuidanceMode.ALTERNATING: L.CFG_ALTERNATING}[p.guidance.mode]
     method = {SamplerMethod.EULER: L.METHOD_EULER, SamplerMethod.HEUN: L.METHOD_HEUN,
               SamplerMethod.PLMS4: L.METHOD_PLMS4}[p.method]
     g = p.guidance
-    return L.SamplerParamsC(p.num_steps, method, mode, g.scale_text, g.scale_caption,
-                            g.scale_speaker, g.min_t, g.max_t,
-                            1 if p.truncation_factor is not None else 0,
-                            p.truncation_factor if p.truncation_factor is not None else 0.0,
-                            1 if has_speaker else 0)
+    tr, skv = p.temporal_rescale, p.speaker_kv
+    return L.SamplerParamsC(
+        num_steps=p.num_steps, method=method, cfg_mode=mode, scale_text=g.scale_text,
+        scale_caption=g.scale_caption, scale_speaker=g.scale_speaker, min_t=g.min_t, max_t=g.max_t,
+        has_truncation=1 if p.truncation_factor is not None else 0,
+        truncation_factor=p.truncation_factor if p.truncation_factor is not None else 0.0,
+        has_speaker=1 if has_speaker else 0, has_caption=1 if has_caption else 0,
+        has_temporal_rescale=1 if tr is not None else 0, rescale_k=tr.k if tr else 1.0,
+        rescale_sigma=tr.sigma if tr else 1.0, has_speaker_kv=1 if skv is not None else 0,
+        speaker_kv_scale=skv.scale if skv else 1.0,
+        speaker_kv_max_layers=skv.max_layers if skv and skv.max_layers is not None else -1,
+        speaker_kv_has_min_t=1 if skv is not None and skv.min_t is not None else 0,
+        speaker_kv_min_t=skv.min_t if skv is not None and skv.min_t is not None else 0.0,
+        ctx_aux_start=ctx_aux_start)
 
 
-def validate_sampler_params(p: SamplerParams, has_speaker: bool = True) -> None:
+def validate_sampler_params(p: SamplerParams, has_speaker: bool = True, has_caption: bool = False) -> None:
     """SamplerParams::validate (params.rs:99-183), evaluated by the library."""
-    c = sampler_params_c(p, has_speaker)
+    c = sampler_params_c(p, has_speaker, has_caption)
     _check(L.load().irodori_sampler_params_validate(C.byref(c)))
 
 
@@ -154,14 +167,16 @@ class HipInferenceEngine:
         return x
 
     def sample(self, x0: np.ndarray, params: SamplerParams, has_speaker: bool = True,
-               lengths=None) -> np.ndarray:
-        """Joint-CFG RF sampling of U utterances: x0 [U,S,P] -> x [U,S,P].  lengths [U]
-        (optional): utterance u attends to its first lengths[u] latent frames (padded
-        variable-length batch)."""
+               lengths=None, has_caption: bool = False, ctx_aux_start: int = 0) -> np.ndarray:
+        """RF sampling of U utterances (sample_euler_rf_cfg): x0 [U,S,P] -> x [U,S,P], any
+        CFG mode and method.  The context rows must hold params.cfg_roles(has_speaker,
+        has_caption) role-major (row r * U + u).  lengths [U] (optional): utterance u
+        attends to its first lengths[u] latent frames (padded variable-length batch).
+        ctx_aux_start: first aux key of the context (used by speaker-KV scaling)."""
         x0 = _c32(x0)
         U, S, P = x0.shape
         out = np.empty_like(x0)
-        pc = sampler_params_c(params, has_speaker)
+        pc = sampler_params_c(params, has_speaker, has_caption, ctx_aux_start)
         if lengths is None:
             _check(self.lib.irodori_sample(self.ctx, C.byref(pc), U, S, _fp(x0), _fp(out)))
         else:
@@ -174,9 +189,10 @@ class HipInferenceEngine:
         return out
 
     def sample_device(self, d_x0: int, d_out: int, utterances: int, seq: int,
-                      params: SamplerParams, has_speaker: bool = True) -> None:
+                      params: SamplerParams, has_speaker: bool = True, has_caption: bool = False,
+                      ctx_aux_start: int = 0) -> None:
         """Same as sample() on device pointers (inputs/outputs resident in HBM)."""
-        pc = sampler_params_c(params, has_speaker)
+        pc = sampler_params_c(params, has_speaker, has_caption, ctx_aux_start)
         _check(self.lib.irodori_sample_device(self.ctx, C.byref(pc), utterances, seq,
                                               C.c_void_p(d_x0), C.c_void_p(d_out)))
 

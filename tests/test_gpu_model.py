@@ -4,6 +4,7 @@ CPU oracle, on identical seeded inputs and random-init weights.
 Bars: f32 HIP path within 1e-4 relative L2 per block, bf16 within
 1e-2 per block and 2e-2 on the final sampled latent.
 """
+import dataclasses
 import os
 
 import numpy as np
@@ -39,6 +40,9 @@ SMALL = {
     # odd S: the V^T token pair at the batch-row boundary straddles two rows
     "tiny_odd": (ih.cfg_tiny, 37, 11, 9, 0.05, 0.1),
     "cfg1": (ih.cfg_cpu_plumbing, 64, 16, 32, 0.02, 0.0),
+    # a 48-channel latent takes the output head's 64-wide tile path (more staged outputs
+    # than threads)
+    "tiny_p48": (lambda: dataclasses.replace(ih.cfg_tiny(), latent_dim=48), 40, 20, 13, 0.05, 0.1),
 }
 
 
@@ -94,7 +98,8 @@ def test_sample_joint_cfg_cfg1(oracle64, backend):
 
 
 def test_sample_two_utterances_rows_independent(oracle64):
-    # Two utterances in one batch (rows 0..3) equal each utterance sampled alone.
+    # Two utterances in one batch (role-major rows: conditioned 0, 1; unconditioned 2, 3)
+    # equal each utterance sampled alone.
     cfg = ih.cfg_tiny()
     w = ih.DitWeights.random(cfg, 3, std=0.05, norm_jitter=0.1)
     ctx = ih.make_context_kv(cfg, 2, 12, 9, seed=4)
@@ -103,7 +108,7 @@ def test_sample_two_utterances_rows_independent(oracle64):
     with make_engine(cfg, F32, w, ctx, 4, 24) as e:
         both = e.sample(x0, p)
     for u in range(2):
-        c, un = ctx.rows([2 * u]), ctx.rows([2 * u + 1])
+        c, un = ctx.rows([u]), ctx.rows([2 + u])
         ref, _ = oracle64.sample_joint_cfg(cfg, w, x0[u:u + 1], (c.k, c.v, c.mask),
                                            (un.k, un.v, un.mask), 3, 2.0)
         assert rel_l2(both[u:u + 1], ref) < 1e-4
@@ -251,7 +256,7 @@ def test_sample_padded_batch_matches_unpadded(backend):
     with make_engine(cfg, backend, w, ctx, 4, 64) as e:
         padded = e.sample(x0, p, lengths=[64, n])
         full = e.sample(x0, p)
-    with make_engine(cfg, backend, w, ctx.rows([2, 3]), 2, 64) as e:
+    with make_engine(cfg, backend, w, ctx.rows([1, 3]), 2, 64) as e:  # utterance 1's roles
         short = e.sample(x0[1:2, :n], p)
     assert rel_l2(padded[1:2, :n], short) < 1e-6
     assert rel_l2(padded[0:1], full[0:1]) < 1e-6  # full-length utterance unaffected
