@@ -166,6 +166,34 @@ int irodori_set_ctx_kv(irodori_ctx* ctx, int layer, int row, int t_ctx, const fl
                        const float* v, const uint8_t* mask);
 int irodori_clear_ctx_kv(irodori_ctx* ctx);
 
+/* Context projections of one layer, JointAttention wk_text / wv_text and wk_speaker /
+ * wv_speaker (or the caption pair) (attention.rs:142-147, :183-207): Burn [d_in, H*Dh],
+ * no bias.  aux pointers may be NULL when aux_dim is 0.  Every layer must use the same
+ * text_dim / aux_dim. */
+typedef struct irodori_ctx_proj_weights {
+    const float* wk_text; /* [text_dim, H*Dh] */
+    const float* wv_text;
+    const float* wk_aux;  /* [aux_dim, H*Dh] */
+    const float* wv_aux;
+} irodori_ctx_proj_weights;
+int irodori_load_ctx_proj_weights(irodori_ctx* ctx, int layer, int text_dim, int aux_dim,
+                                  const irodori_ctx_proj_weights* w);
+
+/* build_kv_cache (attention.rs:431-501) on the device for every layer and one batch row:
+ * K = k_norm(state @ Wk) (not rotated), V = state @ Wv for the text state [t_text, text_dim]
+ * and the aux state [t_aux, aux_dim] (nullable when t_aux = 0), concatenated [text | aux]
+ * with ctx_mask = [text_mask | aux_mask] (nonzero = attend).  Replaces irodori_set_ctx_kv
+ * for that row (same t_ctx rule: t_text + t_aux).  An unconditioned bundle is built from
+ * zero states with all-false masks (condition.rs:144-154).  Host pointers; synchronous. */
+int irodori_build_ctx_kv(irodori_ctx* ctx, int row, int t_text, const float* text_state,
+                         const uint8_t* text_mask, int t_aux, const float* aux_state,
+                         const uint8_t* aux_mask);
+
+/* Inspection (no counterpart in the reference, which keeps CondKvCache as tensors): copy
+ * the cached context of one layer and batch row back to the host as k, v [t_ctx, H, Dh]
+ * (k normed, not rotated) and mask [t_ctx], in the compute dtype's values.  Synchronous. */
+int irodori_read_ctx_kv(irodori_ctx* ctx, int layer, int row, float* k, float* v, uint8_t* mask);
+
 /* One DiT forward, forward_with_cond_cached (optimized.rs:102-113): x_t [B,S,P],
  * t [B] -> v [B,S,P].  debug (nullable): [L+1,B,S,D] after in_proj and after each block
  * (BlockDebugOutputs, dit/model.rs:92-102).  Host pointers; synchronous. */

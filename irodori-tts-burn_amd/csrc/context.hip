@@ -87,6 +87,10 @@ struct LayerBufs {
     float* ctx_mask = nullptr;  // [rows, max_ctx]
     int* tile_on = nullptr;     // [rows, ceil(max_ctx / 64)]
     unsigned long long* tile_bits = nullptr;  // [rows, ceil(max_ctx / 64)], bit k: key 64 t + k valid
+    // Context projections (wk/wv_text, wk/wv_speaker|caption, attention.rs:142-147): per
+    // segment (0 text, 1 aux) [2 H Dh, kpad] = [Wk ; Wv]^T, input dim zero-padded to 64.
+    void* w_ctx[2] = {};
+    bool ctx_proj_loaded = false;
     bool loaded = false;
     std::vector<char> row_set;
 };
@@ -145,6 +149,12 @@ struct irodori_ctx {
     float* hist = nullptr;  // [4][rows, S, P] Heun v1 / PLMS-4 history
     RfEval* plan = nullptr; // sampler evaluations [2 * steps]
     int plan_cap = 0;       // steps
+    // Context KV build on the device: projection input dims (0 text, 1 aux; 0 = absent),
+    // their 64-padded widths, and a staging buffer for the states in the compute dtype.
+    int ctx_dim[2] = {0, 0};
+    int ctx_kpad[2] = {0, 0};
+    void* ctx_state = nullptr;
+    size_t ctx_state_bytes = 0;
     // Speaker-KV scaling (kv_scaling.rs:10-60): per-layer copies of the context K / V^T
     // with the aux keys of the scaled rows multiplied; the attention of layers < kvs_layers
     // reads them while kvs_on.
@@ -886,6 +896,181 @@ int irodori_clear_ctx_kv(irodori_ctx* c) {
     return IRODORI_OK;
 }
 
+// The context key mask of one row of one layer (nonzero = attend) as the attention reads
+// it: a float mask [max_ctx], per-tile "any valid key" flags and 64-bit validity words.
+static int upload_row_mask(irodori_ctx* c, LayerBufs& lb, int row, int t_ctx, const uint8_t* mask) {
+    const int T = c->cfg.max_ctx > 0 ? c->cfg.max_ctx : 1;
+    std::vector<float> m(T, 0.f);
+    int ntl = (T + 63) / 64;
+    std::vector<int> on(ntl, 0);
+    std::vector<unsigned long long> bits(ntl, 0ull);
+    for (int j = 0; j < t_ctx; j++) {
+        m[j] = mask[j] ? 1.f : 0.f;
+        if (mask[j]) {
+            on[j / 64] = 1;
+            bits[j / 64] |= 1ull << (j % 64);
+        }
+    }
+    IRO_TRY(upload(c, lb.ctx_mask + (size_t)row * T, m.data(), sizeof(float) * T));
+    IRO_TRY(upload(c, lb.tile_on + (size_t)row * ntl, on.data(), sizeof(int) * ntl));
+    IRO_TRY(upload(c, lb.tile_bits + (size_t)row * ntl, bits.data(), sizeof(unsigned long long) * ntl));
+    IRO_HIP_CHECK(hipStreamSynchronize(c->stream));  // the host staging vectors end here
+    return IRODORI_OK;
+}
+
+// Round-to-nearest-even f32 -> bf16 bits (NaN kept quiet).
+static uint16_t bf16_bits(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+int irodori_load_ctx_proj_weights(irodori_ctx* c, int layer, int text_dim, int aux_dim,
+                                  const irodori_ctx_proj_weights* w) {
+    IRO_GUARD_BEGIN
+    IRO_REQUIRE(c && w && w->wk_text && w->wv_text, IRODORI_ERR_INVALID_ARG, "null argument");
+    const auto& g = c->cfg;
+    IRO_REQUIRE(layer >= 0 && layer < g.num_layers, IRODORI_ERR_INVALID_ARG, "layer index out of range");
+    IRO_REQUIRE(text_dim > 0 && aux_dim >= 0, IRODORI_ERR_SHAPE, "text_dim must be > 0 and aux_dim >= 0");
+    IRO_REQUIRE(aux_dim == 0 || (w->wk_aux && w->wv_aux), IRODORI_ERR_INVALID_ARG, "null aux projection");
+    IRO_REQUIRE(g.head_dim == 64, IRODORI_ERR_CONFIG, "the context KV build needs head_dim 64");
+    const int dims[2] = {text_dim, aux_dim};
+    for (int sgm = 0; sgm < 2; sgm++)
+        IRO_REQUIRE(c->ctx_dim[sgm] == 0 || c->ctx_dim[sgm] == dims[sgm], IRODORI_ERR_SHAPE,
+                    "context projection input dims must match the layers already loaded");
+    IRO_HIP_CHECK(hipSetDevice(c->device));
+    const int HD = g.num_heads * g.head_dim;
+    auto& lb = c->layers[layer];
+    for (int sgm = 0; sgm < 2; sgm++) {
+        const int K = dims[sgm];
+        if (K == 0) continue;
+        const int kpad = (K + 63) / 64 * 64;
+        if (!lb.w_ctx[sgm]) IRO_TRY(dev_alloc(c, &lb.w_ctx[sgm], c->esz * (size_t)2 * HD * kpad));
+        const float* src[2] = {sgm ? w->wk_aux : w->wk_text, sgm ? w->wv_aux : w->wv_text};
+        std::vector<float> padded((size_t)kpad * HD, 0.f);  // Burn [d_in, kv_dim], rows past d_in zero
+        for (int kv = 0; kv < 2; kv++) {
+            memcpy(padded.data(), src[kv], sizeof(float) * (size_t)K * HD);
+            IRO_TRY(ingest_kmajor(c, padded.data(), kpad, HD, 0,
+                                  static_cast<char*>(lb.w_ctx[sgm]) + c->esz * (size_t)kv * HD * kpad));
+        }
+        c->ctx_dim[sgm] = K;
+        c->ctx_kpad[sgm] = kpad;
+    }
+    lb.ctx_proj_loaded = true;
+    return IRODORI_OK;
+    IRO_GUARD_END
+}
+
+// build_kv_cache (attention.rs:431-501) of one batch row for every layer, on the device:
+// per segment (text, then aux) one GEMM of the states against [Wk ; Wv] whose epilogue
+// head-normalizes K and writes K and V^T into the row's context at the segment's key
+// offset; ctx_mask = [text_mask | aux_mask].
+int irodori_build_ctx_kv(irodori_ctx* c, int row, int t_text, const float* text_state, const uint8_t* text_mask,
+                         int t_aux, const float* aux_state, const uint8_t* aux_mask) {
+    IRO_GUARD_BEGIN
+    IRO_REQUIRE(c, IRODORI_ERR_INVALID_ARG, "null context");
+    const auto& g = c->cfg;
+    const int L = g.num_layers, H = g.num_heads, Dh = g.head_dim, HD = H * Dh;
+    IRO_REQUIRE(row >= 0 && row < g.max_rows, IRODORI_ERR_INVALID_ARG, "row index out of range");
+    IRO_REQUIRE(t_text >= 0 && t_aux >= 0, IRODORI_ERR_SHAPE, "segment lengths must be >= 0");
+    const int t_ctx = t_text + t_aux;
+    IRO_REQUIRE(t_ctx <= g.max_ctx, IRODORI_ERR_SHAPE,
+                "t_ctx " + std::to_string(t_ctx) + " exceeds max_ctx " + std::to_string(g.max_ctx));
+    IRO_REQUIRE(c->t_ctx < 0 || c->t_ctx == t_ctx, IRODORI_ERR_SHAPE,
+                "t_ctx must match the context length already set (" + std::to_string(c->t_ctx) +
+                    "); call irodori_clear_ctx_kv first");
+    IRO_REQUIRE(t_text == 0 || (text_state && text_mask), IRODORI_ERR_INVALID_ARG, "null text state / mask");
+    IRO_REQUIRE(t_aux == 0 || (aux_state && aux_mask), IRODORI_ERR_INVALID_ARG, "null aux state / mask");
+    for (int l = 0; l < L; l++) {
+        IRO_REQUIRE(c->layers[l].ctx_proj_loaded, IRODORI_ERR_NOT_LOADED,
+                    "context projections of layer " + std::to_string(l) + " not loaded");
+        IRO_REQUIRE(c->layers[l].loaded, IRODORI_ERR_NOT_LOADED,
+                    "block weights (k_norm) of layer " + std::to_string(l) + " not loaded");
+    }
+    IRO_REQUIRE(t_aux == 0 || c->ctx_dim[1] > 0, IRODORI_ERR_NOT_LOADED, "no aux context projection loaded");
+    IRO_HIP_CHECK(hipSetDevice(c->device));
+    const int T1 = g.max_ctx > 0 ? g.max_ctx : 1, vs1 = (T1 + 63) / 64 * 64;
+
+    // States -> compute dtype, input dim zero-padded, staged [text rows | aux rows].
+    const int lens[2] = {t_text, t_aux};
+    const float* states[2] = {text_state, aux_state};
+    size_t off[2], total = 0;
+    for (int sgm = 0; sgm < 2; sgm++) {
+        off[sgm] = total;
+        if (lens[sgm]) total += (size_t)lens[sgm] * c->ctx_kpad[sgm];
+    }
+    if (!c->ctx_state) {  // t_text + t_aux <= max_ctx rows of the wider padded input
+        const int kmax = c->ctx_kpad[0] > c->ctx_kpad[1] ? c->ctx_kpad[0] : c->ctx_kpad[1];
+        c->ctx_state_bytes = (size_t)T1 * kmax * c->esz;
+        IRO_TRY(dev_alloc(c, &c->ctx_state, c->ctx_state_bytes));
+    }
+    IRO_REQUIRE(total * c->esz <= c->ctx_state_bytes, IRODORI_ERR_SHAPE, "context states exceed the staging buffer");
+    std::vector<float> sf(total, 0.f);
+    for (int sgm = 0; sgm < 2; sgm++)
+        for (int j = 0; j < lens[sgm]; j++)
+            memcpy(sf.data() + off[sgm] + (size_t)j * c->ctx_kpad[sgm], states[sgm] + (size_t)j * c->ctx_dim[sgm],
+                   sizeof(float) * c->ctx_dim[sgm]);
+    std::vector<uint16_t> sb;
+    if (c->bf16) {
+        sb.resize(total);
+        for (size_t i = 0; i < total; i++) sb[i] = bf16_bits(sf[i]);
+        IRO_TRY(upload(c, c->ctx_state, sb.data(), total * 2));
+    } else if (total) {
+        IRO_TRY(upload(c, c->ctx_state, sf.data(), total * 4));
+    }
+    IRO_HIP_CHECK(hipStreamSynchronize(c->stream));  // the host staging vectors end here
+    std::vector<uint8_t> mask(t_ctx);
+    for (int j = 0; j < t_text; j++) mask[j] = text_mask[j] ? 1 : 0;
+    for (int j = 0; j < t_aux; j++) mask[t_text + j] = aux_mask[j] ? 1 : 0;
+
+    for (int l = 0; l < L; l++) {
+        auto& lb = c->layers[l];
+        const size_t nk = (size_t)H * T1 * Dh, nv = (size_t)H * Dh * vs1;
+        char* ck = static_cast<char*>(lb.ctx_k) + (size_t)row * nk * c->esz;
+        char* cv = static_cast<char*>(lb.ctx_v) + (size_t)row * nv * c->esz;
+        // Keys past t_ctx (and the V^T padding) hold zeros, as after irodori_set_ctx_kv.
+        IRO_HIP_CHECK(hipMemsetAsync(ck, 0, nk * c->esz, c->stream));
+        IRO_HIP_CHECK(hipMemsetAsync(cv, 0, nv * c->esz, c->stream));
+        for (int sgm = 0; sgm < 2; sgm++) {
+            if (lens[sgm] == 0) continue;
+            int rc;
+            if (c->bf16) {
+                GemmArgs<bf16> ga{};
+                ga.A = static_cast<const bf16*>(c->ctx_state) + off[sgm];
+                ga.W = static_cast<const bf16*>(lb.w_ctx[sgm]);
+                ga.M = lens[sgm]; ga.N = 2 * HD; ga.K = c->ctx_kpad[sgm]; ga.S = lens[sgm];
+                ga.H = H; ga.D = g.model_dim; ga.eps = g.norm_eps; ga.k_norm = lb.k_norm;
+                ga.Ck = reinterpret_cast<bf16*>(ck); ga.Cv = reinterpret_cast<bf16*>(cv);
+                ga.key_off = sgm ? t_text : 0; ga.ctx_stride = T1; ga.ctx_vstride = vs1;
+                rc = launch_gemm<bf16>(EPI_CTXKV, ga, c->stream);
+            } else {
+                GemmArgs<float> ga{};
+                ga.A = static_cast<const float*>(c->ctx_state) + off[sgm];
+                ga.W = static_cast<const float*>(lb.w_ctx[sgm]);
+                ga.M = lens[sgm]; ga.N = 2 * HD; ga.K = c->ctx_kpad[sgm]; ga.S = lens[sgm];
+                ga.H = H; ga.D = g.model_dim; ga.eps = g.norm_eps; ga.k_norm = lb.k_norm;
+                ga.Ck = reinterpret_cast<float*>(ck); ga.Cv = reinterpret_cast<float*>(cv);
+                ga.key_off = sgm ? t_text : 0; ga.ctx_stride = T1; ga.ctx_vstride = vs1;
+                rc = launch_gemm<float>(EPI_CTXKV, ga, c->stream);
+            }
+            if (rc) { set_last_error("context KV gemm shape"); return IRODORI_ERR_SHAPE; }
+        }
+        IRO_TRY(check_launch("context KV build"));
+        IRO_TRY(upload_row_mask(c, lb, row, t_ctx, mask.data()));
+        lb.row_set[row] = 1;
+    }
+    IRO_HIP_CHECK(hipStreamSynchronize(c->stream));
+    if (c->t_ctx != t_ctx) {
+        for (auto& kv : c->graphs) (void)hipGraphExecDestroy(kv.second);
+        c->graphs.clear();
+    }
+    c->t_ctx = t_ctx;
+    return IRODORI_OK;
+    IRO_GUARD_END
+}
+
 int irodori_set_ctx_kv(irodori_ctx* c, int layer, int row, int t_ctx, const float* k, const float* v,
                        const uint8_t* mask) {
     IRO_GUARD_BEGIN
@@ -907,13 +1092,7 @@ int irodori_set_ctx_kv(irodori_ctx* c, int layer, int row, int t_ctx, const floa
         // the attention kernel's A-operand order (vt_pos_bf16 / vt_pos_f32).
         int Tp = (T + 63) / 64 * 64;
         size_t nk = (size_t)H * T * Dh, nv = (size_t)H * Dh * Tp;
-        auto cvt = [](float f) -> uint16_t {
-            uint32_t u;
-            memcpy(&u, &f, 4);
-            if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
-            u += 0x7fffu + ((u >> 16) & 1u);
-            return (uint16_t)(u >> 16);
-        };
+        auto cvt = bf16_bits;
         std::vector<float> kf(nk, 0.f), vf(nv, 0.f);
         for (int j = 0; j < t_ctx; j++) {
             int pos = c->bf16 ? vt_pos_bf16(j) : vt_pos_f32(j);
@@ -937,21 +1116,7 @@ int irodori_set_ctx_kv(irodori_ctx* c, int layer, int row, int t_ctx, const floa
         }
         IRO_TRY(upload(c, static_cast<char*>(lb.ctx_k) + (size_t)row * nk * c->esz, kp, nk * c->esz));
         IRO_TRY(upload(c, static_cast<char*>(lb.ctx_v) + (size_t)row * nv * c->esz, vp, nv * c->esz));
-        std::vector<float> m(T, 0.f);
-        int ntl = (T + 63) / 64;
-        std::vector<int> on(ntl, 0);
-        std::vector<unsigned long long> bits(ntl, 0ull);
-        for (int j = 0; j < t_ctx; j++) {
-            m[j] = mask[j] ? 1.f : 0.f;
-            if (mask[j]) {
-                on[j / 64] = 1;
-                bits[j / 64] |= 1ull << (j % 64);
-            }
-        }
-        IRO_TRY(upload(c, lb.ctx_mask + (size_t)row * T, m.data(), sizeof(float) * T));
-        IRO_TRY(upload(c, lb.tile_on + (size_t)row * ntl, on.data(), sizeof(int) * ntl));
-        IRO_TRY(upload(c, lb.tile_bits + (size_t)row * ntl, bits.data(), sizeof(unsigned long long) * ntl));
-        IRO_HIP_CHECK(hipStreamSynchronize(c->stream));
+        IRO_TRY(upload_row_mask(c, lb, row, t_ctx, mask));
     }
     if (c->t_ctx != t_ctx) {
         for (auto& kv : c->graphs) (void)hipGraphExecDestroy(kv.second);
@@ -959,6 +1124,52 @@ int irodori_set_ctx_kv(irodori_ctx* c, int layer, int row, int t_ctx, const floa
     }
     c->t_ctx = t_ctx;
     lb.row_set[row] = 1;
+    return IRODORI_OK;
+    IRO_GUARD_END
+}
+
+int irodori_read_ctx_kv(irodori_ctx* c, int layer, int row, float* k, float* v, uint8_t* mask) {
+    IRO_GUARD_BEGIN
+    IRO_REQUIRE(c && k && v && mask, IRODORI_ERR_INVALID_ARG, "null argument");
+    const auto& g = c->cfg;
+    IRO_REQUIRE(layer >= 0 && layer < g.num_layers, IRODORI_ERR_INVALID_ARG, "layer index out of range");
+    IRO_REQUIRE(row >= 0 && row < g.max_rows, IRODORI_ERR_INVALID_ARG, "row index out of range");
+    IRO_REQUIRE(c->t_ctx >= 0 && c->layers[layer].row_set[row], IRODORI_ERR_NOT_LOADED,
+                "context KV of this layer / row not set");
+    IRO_HIP_CHECK(hipSetDevice(c->device));
+    auto& lb = c->layers[layer];
+    const int H = g.num_heads, Dh = g.head_dim, T = g.max_ctx > 0 ? g.max_ctx : 1, Tp = (T + 63) / 64 * 64;
+    const size_t nk = (size_t)H * T * Dh, nv = (size_t)H * Dh * Tp;
+    std::vector<unsigned char> kb(nk * c->esz), vb(nv * c->esz);
+    std::vector<float> mf(T);
+    IRO_HIP_CHECK(hipMemcpyAsync(kb.data(), static_cast<char*>(lb.ctx_k) + (size_t)row * nk * c->esz, kb.size(),
+                                 hipMemcpyDeviceToHost, c->stream));
+    IRO_HIP_CHECK(hipMemcpyAsync(vb.data(), static_cast<char*>(lb.ctx_v) + (size_t)row * nv * c->esz, vb.size(),
+                                 hipMemcpyDeviceToHost, c->stream));
+    IRO_HIP_CHECK(hipMemcpyAsync(mf.data(), lb.ctx_mask + (size_t)row * T, sizeof(float) * T,
+                                 hipMemcpyDeviceToHost, c->stream));
+    IRO_HIP_CHECK(hipStreamSynchronize(c->stream));
+    auto at = [&](const std::vector<unsigned char>& b, size_t i) -> float {
+        if (!c->bf16) {
+            float f;
+            memcpy(&f, b.data() + 4 * i, 4);
+            return f;
+        }
+        uint32_t u = (uint32_t)(b[2 * i] | (b[2 * i + 1] << 8)) << 16;
+        float f;
+        memcpy(&f, &u, 4);
+        return f;
+    };
+    for (int j = 0; j < c->t_ctx; j++) {
+        const int pos = c->bf16 ? vt_pos_bf16(j) : vt_pos_f32(j);
+        for (int hh = 0; hh < H; hh++)
+            for (int d = 0; d < Dh; d++) {
+                const size_t dst = ((size_t)j * H + hh) * Dh + d;
+                k[dst] = at(kb, ((size_t)hh * T + j) * Dh + d);
+                v[dst] = at(vb, ((size_t)hh * Dh + d) * Tp + pos);
+            }
+        mask[j] = mf[j] != 0.f;
+    }
     return IRODORI_OK;
     IRO_GUARD_END
 }

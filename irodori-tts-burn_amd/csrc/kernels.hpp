@@ -161,7 +161,7 @@ void launch_timestep_embedding(const float* t, int nvec, int t_dim, float* out, 
 void launch_vec_linear(const VecLinJob* d_jobs, int njobs, int nvec, int max_n, hipStream_t st);
 
 // ---- kernels_gemm.hip ------------------------------------------------------------------
-enum GemmEpi { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_QKVG = 3 };
+enum GemmEpi { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_QKVG = 3, EPI_CTXKV = 4 };
 template <typename T>
 struct GemmArgs {
     const T* A;   // [M, K] row-major
@@ -189,6 +189,12 @@ struct GemmArgs {
     const float* rope_sin;
     int H, D;
     float eps;
+    // EPI_CTXKV (context KV build, attention.rs:431-501): N = 2 H Dh columns [K | V] of the
+    // context rows key_off .. key_off + M - 1: K head-normed with k_norm into Ck
+    // [H, ctx_stride, Dh], V into Cv = V^T [H, Dh, ctx_vstride] at vt_pos_bf16 / vt_pos_f32.
+    T* Ck;
+    T* Cv;
+    int key_off, ctx_stride, ctx_vstride;
 };
 template <typename T>
 int launch_gemm(int epi, const GemmArgs<T>& a, hipStream_t st);

@@ -134,7 +134,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
     static_assert(LPW * 8 * NW == ROWS, "rows per slice must split over the waves");
     static_assert(FM * 32 == WM && FN * 32 == WN, "wave tiles are whole 32x32 blocks");
     static_assert(BM % 8 == 0, "a load instruction covers A rows or W rows, not both");
-    static_assert(EPI != EPI_QKVG || WN == 64, "QKVG epilogue needs one head per wave");
+    static_assert((EPI != EPI_QKVG && EPI != EPI_CTXKV) || WN == 64, "QKVG / CTXKV epilogues need one head per wave");
     static_assert(EPI != EPI_SWIGLU || FN % 2 == 0, "SWIGLU epilogue needs column pairs");
 
     extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
@@ -321,6 +321,42 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
                     a.U[(size_t)row * half_n + pair * 32 + cl] = from_f32<T>(silu_f(u1) * u3);
                 }
             }
+    } else if constexpr (EPI == EPI_CTXKV) {
+        // One 64-column head per wave: region 0 = K (head RMSNorm, norm.rs:60-74, no RoPE),
+        // region 1 = V (transposed scatter).  A setup-path epilogue: element stores.
+        const int Dh = 64, HD = a.H * Dh;
+        const int col0 = n0 + wn0;
+        const bool is_k = col0 < HD;
+        const int h = (is_k ? col0 : col0 - HD) / Dh;
+        if (is_k) {
+            const float nw0 = a.k_norm[h * Dh + cl], nw1 = a.k_norm[h * Dh + 32 + cl];
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const int row = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
+                    const float y0 = acc[i][0][e], y1 = acc[i][1][e];
+                    const float ss = half_wave_sum(y0 * y0 + y1 * y1);
+                    const float inv = __builtin_amdgcn_rsqf(ss * (1.f / (float)Dh) + a.eps);
+                    if (row >= a.M) continue;
+                    T* o = a.Ck + ((size_t)h * a.ctx_stride + a.key_off + row) * Dh;
+                    o[cl] = from_f32<T>(y0 * inv * nw0);
+                    o[32 + cl] = from_f32<T>(y1 * inv * nw1);
+                }
+        } else {
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const int row = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
+                    if (row >= a.M) continue;
+                    const int key = a.key_off + row;
+                    const int pos = sizeof(T) == 2 ? vt_pos_bf16(key) : vt_pos_f32(key);
+#pragma unroll
+                    for (int j = 0; j < 2; j++)
+                        a.Cv[((size_t)h * Dh + 32 * j + cl) * a.ctx_vstride + pos] = from_f32<T>(acc[i][j][e]);
+                }
+        }
     } else if constexpr (EPI == EPI_QKVG) {
         // Each wave owns WM rows x one 64-column head of one region (q | k | v | gate).
         // The stage buffers are free once every wave is past the main loop; each wave then
@@ -533,6 +569,9 @@ int launch_gemm(int epi, const GemmArgs<T>& a, hipStream_t st) {
         case EPI_RESID: return launch_cfg<T, 64, 64, 2, 2, 4, EPI_RESID>(a, st);
         case EPI_SWIGLU: return launch_cfg<T, 128, 128, 2, 2, 2, EPI_SWIGLU>(a, st);
         case EPI_QKVG: return launch_cfg<T, 128, 128, 2, 2, 2, EPI_QKVG>(a, st);
+        case EPI_CTXKV:
+            if (a.N != 2 * a.H * 64) return -1;
+            return launch_cfg<T, 128, 128, 2, 2, 2, EPI_CTXKV>(a, st);
     }
     return -1;
 }

@@ -9,11 +9,12 @@ from .config import (CfgGuidanceMode, DitConfig, GuidanceConfig, InferenceBacken
                      cfg_tiny)
 from .engine import HipInferenceEngine, ops
 from .synthetic import (ROLE_COND, ROLE_NO_AUX, ROLE_NO_TEXT, ROLE_UNCOND, ContextKV,
-                        DitWeights, make_context_kv, make_noise, make_role_context)
+                        CtxProjWeights, DitWeights, make_context_kv, make_noise,
+                        make_role_context)
 
 __all__ = [
     "CfgGuidanceMode", "DitConfig", "GuidanceConfig", "InferenceBackendKind", "IrodoriError",
     "SamplerMethod", "SamplerParams", "cfg_cpu_plumbing", "cfg_full_rf", "cfg_tiny",
-    "HipInferenceEngine", "ops", "ContextKV", "DitWeights", "make_context_kv", "make_noise",
+    "HipInferenceEngine", "ops", "ContextKV", "CtxProjWeights", "DitWeights", "make_context_kv", "make_noise",
     "make_role_context", "ROLE_COND", "ROLE_UNCOND", "ROLE_NO_TEXT", "ROLE_NO_AUX",
 ]

@@ -71,6 +71,10 @@ class SamplerParamsC(C.Structure):
     ]
 
 
+class CtxProjWeightsC(C.Structure):
+    _fields_ = [("wk_text", _f32p), ("wv_text", _f32p), ("wk_aux", _f32p), ("wv_aux", _f32p)]
+
+
 class KernelTimesC(C.Structure):
     _fields_ = [(n, C.c_float) for n in ("norm_mod_us", "qkvg_gemm_us", "attention_us",
                                           "wo_gemm_us", "w13_gemm_us", "w2_gemm_us", "final_us")]
@@ -90,6 +94,11 @@ SIGNATURES = {
     "irodori_set_ctx_kv": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _f32p, _f32p,
                                      C.POINTER(C.c_uint8)]),
     "irodori_clear_ctx_kv": (C.c_int, [_vp]),
+    "irodori_load_ctx_proj_weights": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int,
+                                                C.POINTER(CtxProjWeightsC)]),
+    "irodori_build_ctx_kv": (C.c_int, [_vp, C.c_int, C.c_int, _f32p, C.POINTER(C.c_uint8),
+                                       C.c_int, _f32p, C.POINTER(C.c_uint8)]),
+    "irodori_read_ctx_kv": (C.c_int, [_vp, C.c_int, C.c_int, _f32p, _f32p, C.POINTER(C.c_uint8)]),
     "irodori_forward": (C.c_int, [_vp, C.c_int, C.c_int, _f32p, _f32p, _f32p, _f32p]),
     "irodori_forward_masked": (C.c_int, [_vp, C.c_int, C.c_int, _f32p, _f32p,
                                          C.POINTER(C.c_uint8), _f32p, _f32p]),

@@ -18,7 +18,7 @@ import numpy as np
 from . import _lib as L
 from .config import (CfgGuidanceMode, DitConfig, InferenceBackendKind, IrodoriError,
                      SamplerMethod, SamplerParams)
-from .synthetic import ContextKV, DitWeights
+from .synthetic import ContextKV, CtxProjWeights, DitWeights
 
 _f32p = C.POINTER(C.c_float)
 
@@ -134,6 +134,39 @@ class HipInferenceEngine:
                 m = np.ascontiguousarray(ctx.mask[r], np.uint8)
                 _check(self.lib.irodori_set_ctx_kv(self.ctx, l, r, T, _fp(k), _fp(v),
                                                    m.ctypes.data_as(C.POINTER(C.c_uint8))))
+
+    def load_ctx_proj_weights(self, w: CtxProjWeights) -> None:
+        """Upload every layer's context projections (wk/wv_text, wk/wv_speaker|caption)."""
+        for l, lw in enumerate(w.layers):
+            s = L.CtxProjWeightsC(_fp(lw["wk_text"]), _fp(lw["wv_text"]),
+                                  _fp(lw["wk_aux"]) if w.aux_dim else None,
+                                  _fp(lw["wv_aux"]) if w.aux_dim else None)
+            _check(self.lib.irodori_load_ctx_proj_weights(self.ctx, l, w.text_dim, w.aux_dim,
+                                                          C.byref(s)))
+
+    def build_context_kv(self, row: int, text_state: np.ndarray, text_mask: np.ndarray,
+                         aux_state: np.ndarray = None, aux_mask: np.ndarray = None) -> None:
+        """build_kv_cache (attention.rs:431-501) of batch row `row` on the device, every layer:
+        text_state [t_text, text_dim], aux_state [t_aux, aux_dim] (None: no aux keys)."""
+        ts = _c32(text_state)
+        tm = np.ascontiguousarray(text_mask, np.uint8)
+        t_aux = 0 if aux_state is None else aux_state.shape[0]
+        a = _c32(aux_state) if t_aux else None
+        am = np.ascontiguousarray(aux_mask, np.uint8) if t_aux else None
+        u8 = C.POINTER(C.c_uint8)
+        _check(self.lib.irodori_build_ctx_kv(
+            self.ctx, row, ts.shape[0], _fp(ts), tm.ctypes.data_as(u8), t_aux,
+            _fp(a) if t_aux else None, am.ctypes.data_as(u8) if t_aux else None))
+
+    def read_context_kv(self, layer: int, row: int, t_ctx: int):
+        """The cached context of (layer, row): k, v [t_ctx, H, Dh], mask [t_ctx]."""
+        H, Dh = self.cfg.num_heads, self.cfg.head_dim
+        k = np.empty((t_ctx, H, Dh), np.float32)
+        v = np.empty_like(k)
+        m = np.empty(t_ctx, np.uint8)
+        _check(self.lib.irodori_read_ctx_kv(self.ctx, layer, row, _fp(k), _fp(v),
+                                            m.ctypes.data_as(C.POINTER(C.c_uint8))))
+        return k, v, m
 
     # ---- compute ------------------------------------------------------------------------
     def forward_with_cond_cached(self, x_t: np.ndarray, t: np.ndarray, debug: bool = False,

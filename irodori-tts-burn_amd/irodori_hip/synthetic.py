@@ -83,6 +83,31 @@ class DitWeights:
 
 
 @dataclass
+class CtxProjWeights:
+    """Per-layer context projections of JointAttention (attention.rs:142-147): wk_text /
+    wv_text [text_dim, H*Dh] and, when aux_dim > 0, wk_aux / wv_aux [aux_dim, H*Dh] (the
+    speaker or caption pair), Burn row layout, no bias."""
+
+    layers: list
+    text_dim: int
+    aux_dim: int
+
+    @staticmethod
+    def random(cfg: DitConfig, text_dim: int, aux_dim: int, seed: int = 0,
+               std: float = 0.02) -> "CtxProjWeights":
+        d = _Draw(seed, std, 0.0)
+        HD = cfg.num_heads * cfg.head_dim
+        layers = []
+        for _ in range(cfg.num_layers):
+            w = {"wk_text": d.lin(text_dim, HD), "wv_text": d.lin(text_dim, HD)}
+            if aux_dim:
+                w["wk_aux"] = d.lin(aux_dim, HD)
+                w["wv_aux"] = d.lin(aux_dim, HD)
+            layers.append(w)
+        return CtxProjWeights(layers, text_dim, aux_dim)
+
+
+@dataclass
 class ContextKV:
     """Per-layer cached context K/V for every batch row (CondKvCache, attention.rs:24-45):
     k, v [L, B, T, H, Dh] (k already k-normed, not rotated), mask [B, T] (1 = attend)."""
