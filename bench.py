@@ -96,6 +96,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--profile-iters", type=int, default=50)
+    ap.add_argument("--workload", choices=["cfg4", "cfg5"], default="cfg4",
+                    help="cfg4 (default): the headline B=2 Joint-CFG RF run; cfg5: batched "
+                         "throughput, 16 utterances x 2 CFG rows, lengths U[200,750] padded")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run one 1 GiB device-to-device copy (the known-size kernel that "
                          "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings; 32x the L2, so "
@@ -117,6 +120,10 @@ def main():
     import torch
 
     import irodori_hip as ih
+
+    if args.workload == "cfg5":
+        print(json.dumps(run_cfg5(args, np, torch, ih)), flush=True)
+        return
 
     cfg = ih.cfg_full_rf()
     U, S, Tt, Ts, N, SCALE = 1, 750, 256, 375, 40, 3.0
@@ -232,6 +239,80 @@ def main():
     }
     eng.close()
     print(json.dumps(rec), flush=True)
+
+
+def run_cfg5(args, np, torch, ih):
+    """BASELINE config 5 in bf16: 16 utterances x Joint CFG = 32 rows of the 12-layer d1024
+    DiT, latent lengths U[200,750] padded to 750 with the latent key mask, text valid lengths
+    U[32,256], 40 Euler steps.  Aggregate latent frames/s = sum(lengths) / RF-run seconds."""
+    cfg = ih.cfg_full_rf()
+    U, S, Tt, Ts, N, SCALE = 16, 750, 256, 375, 40, 3.0
+    rng = np.random.default_rng(5)
+    lengths = rng.integers(200, S + 1, U).astype(np.int32)
+    log("config 5: generating weights and inputs; lengths sum %d" % int(lengths.sum()))
+    w = ih.DitWeights.random(cfg, 0)
+    ctx = ih.make_context_kv(cfg, U, Tt, Ts, seed=1)
+    x0 = ih.make_noise(U, S, cfg.latent_dim, 2)
+    g = ih.GuidanceConfig(mode=ih.CfgGuidanceMode.JOINT, scale_text=SCALE, scale_speaker=SCALE,
+                          min_t=0.0, max_t=1.0)
+    params = ih.SamplerParams(num_steps=N, guidance=g)
+    eng = ih.HipInferenceEngine(cfg, ih.InferenceBackendKind.HIP_BF16, max_rows=2 * U,
+                                max_seq=S, max_ctx=Tt + Ts)
+    eng.load_weights(w)
+    eng.set_context_kv(ctx)
+    d_x0 = torch.from_numpy(x0).to("cuda")
+    d_out = torch.empty_like(d_x0)
+    torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        eng.sample_device(d_x0.data_ptr(), d_out.data_ptr(), U, S, params, lengths=lengths)
+    torch.cuda.synchronize()
+    log("warmup done (%d runs); timing %d runs" % (args.warmup, args.steps))
+    times = []
+    for _ in range(args.steps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        eng.sample_device(d_x0.data_ptr(), d_out.data_ptr(), U, S, params, lengths=lengths)
+        torch.cuda.synchronize()
+        times.append((time.perf_counter() - t0) * 1e3)
+    ms = float(np.mean(times))
+    out = d_out.cpu().numpy()
+    assert all(np.all(np.isfinite(out[u, :n])) for u, n in enumerate(lengths)), "non-finite output"
+    log("RF run: mean %.2f ms, min %.2f ms" % (ms, min(times)))
+    kt = eng.profile_layer(2 * U, S, max(5, args.profile_iters // 5))
+    log("kernel us (B=32): " + ", ".join("%s=%.1f" % (k, v) for k, v in kt.items()))
+    eng.close()
+    M, D, F = 2 * U * S, cfg.model_dim, cfg.mlp_hidden
+    w13_flops = 2.0 * M * D * 2 * F
+    achieved = w13_flops / (kt["w13_gemm_us"] * 1e-6) / 1e12
+    frames = int(lengths.sum())
+    H, Dh, T = cfg.num_heads, cfg.head_dim, Tt + Ts
+    per_tok = 2.0 * D * (4 * D + D + 2 * F) + 2.0 * F * D  # GEMM FLOP per token per block
+    useful = N * 2 * cfg.num_layers * sum(
+        n * per_tok + 4.0 * H * Dh * n * (n + T) for n in lengths)  # both CFG rows, valid frames
+    return {
+        "metric": "RF aggregate latent frames/s, 16 utterances x 2 CFG (BASELINE config 5)",
+        "value": round(frames / (ms * 1e-3), 1),
+        "unit": "latent frames/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded random-init DiT (all Linear N(0,0.02)), N(0,1) noise and "
+                "context K/V, latent lengths U[200,750] (seed 5), text valid length U[32,256]",
+        "config": {"workload": "BASELINE config 5 shape in bf16 (fp8 weights not built): "
+                               "12-layer d1024 DiT, 16 utterances x Joint CFG = 32 rows padded "
+                               "to 750 frames with the latent key mask, 256 text + 375 speaker "
+                               "keys, 40 Euler steps",
+                   "global_batch": 2 * U, "seq_len": S, "rf_steps": N, "parallelism": "none",
+                   "lengths_sum": frames},
+        "useful_tflops": round(useful / (ms * 1e-3) / 1e12, 1),
+        "kernel_us": {k: round(v, 2) for k, v in kt.items()},
+        "roofline": {"kernel": "w13_gemm (SwiGLU up-projection, %dx1024x5632)" % M,
+                     "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": None},
+        "cpu_baseline": None,
+    }
 
 
 if __name__ == "__main__":

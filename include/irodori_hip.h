@@ -230,6 +230,10 @@ int irodori_sample_masked(irodori_ctx* ctx, const irodori_sampler_params* params
 /* Same with x0 / x_out already in device memory (HBM-resident timing). */
 int irodori_sample_device(irodori_ctx* ctx, const irodori_sampler_params* params,
                           int utterances, int seq, const float* d_x0, float* d_x_out);
+/* irodori_sample_masked with x0 / x_out in device memory; lengths stays a host array. */
+int irodori_sample_device_masked(irodori_ctx* ctx, const irodori_sampler_params* params,
+                                 int utterances, int seq, const int32_t* lengths,
+                                 const float* d_x0, float* d_x_out);
 
 /* Average device time of each kernel of one DiT block at (batch, seq), measured with HIP
  * events on the context's stream over `iters` back-to-back launches per kernel (the

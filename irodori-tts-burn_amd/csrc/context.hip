@@ -1280,6 +1280,15 @@ int irodori_sample_device(irodori_ctx* c, const irodori_sampler_params* p, int U
     return sample_device_impl(c, p, U, S, nullptr, d_x0, d_x_out);
 }
 
+int irodori_sample_device_masked(irodori_ctx* c, const irodori_sampler_params* p, int U, int S,
+                                 const int32_t* lengths, const float* d_x0, float* d_x_out) {
+    if (!lengths) {
+        set_last_error("null lengths");
+        return IRODORI_ERR_INVALID_ARG;
+    }
+    return sample_device_impl(c, p, U, S, lengths, d_x0, d_x_out);
+}
+
 // Restores the context's speaker-KV routing when a sampling call ends.
 struct KvsScope {
     irodori_ctx* c;

@@ -561,12 +561,25 @@ int launch_cfg(const GemmArgs<T>& a, hipStream_t st) {
 // 3x for 64x64.  The wide projections (QKV+gate, W1|W3) use 128x128 tiles in two stages
 // (two workgroups per CU); the D-wide projections (Wo, W2) use 64x64 tiles in four stages
 // so that N = 1024 still yields enough workgroups (split-K over larger tiles measured
-// slower: the f32 partial planes cost more HBM traffic than the LDS time they save).
+// slower: the f32 partial planes cost more HBM traffic than the LDS time they save), unless
+// the batch is large enough for 128x128 tiles.
+// Large batches (many utterances) fill the chip with 128x128 tiles too: two full waves of
+// workgroups (two per CU) or more.  Tiles are the same MFMA sequence over k in either
+// shape, so the choice does not change a single output bit.
+template <typename T>
+static bool wide_enough(const GemmArgs<T>& a) {
+    return a.N % 128 == 0 && (long)((a.M + 127) / 128) * (a.N / 128) >= 512;
+}
+
 template <typename T>
 int launch_gemm(int epi, const GemmArgs<T>& a, hipStream_t st) {
     switch (epi) {
-        case EPI_STORE: return launch_cfg<T, 64, 64, 2, 2, 4, EPI_STORE>(a, st);
-        case EPI_RESID: return launch_cfg<T, 64, 64, 2, 2, 4, EPI_RESID>(a, st);
+        case EPI_STORE:
+            if (wide_enough(a)) return launch_cfg<T, 128, 128, 2, 2, 2, EPI_STORE>(a, st);
+            return launch_cfg<T, 64, 64, 2, 2, 4, EPI_STORE>(a, st);
+        case EPI_RESID:
+            if (wide_enough(a)) return launch_cfg<T, 128, 128, 2, 2, 2, EPI_RESID>(a, st);
+            return launch_cfg<T, 64, 64, 2, 2, 4, EPI_RESID>(a, st);
         case EPI_SWIGLU: return launch_cfg<T, 128, 128, 2, 2, 2, EPI_SWIGLU>(a, st);
         case EPI_QKVG: return launch_cfg<T, 128, 128, 2, 2, 2, EPI_QKVG>(a, st);
         case EPI_CTXKV:

@@ -202,8 +202,8 @@ __global__ __launch_bounds__(256) void inproj_norm_kernel(
     }
 }
 
-// Output head: one 256-thread block per kFinFrames latent frames handles every batch row
-// of those frames, NR rows (a group) at a time.  v[b,s,p] = (sum_d x[b,s,d] * W'[p,d]) /
+// Output head: one 256-thread block per kFinFrames latent frames and row group (NR rows;
+// blockIdx.y strides over the groups).  v[b,s,p] = (sum_d x[b,s,d] * W'[p,d]) /
 // rms(x[b,s,:]) + b_out[p] with W' = out_norm.weight (.) W_out^T folded at ingest — the
 // same product as out_proj(out_norm(x)) (norm.rs:25-39, dit/model.rs:391-392).  The group's
 // rows are staged in LDS; thread (ks, p) computes output p over the k-slice ks for every
@@ -237,7 +237,7 @@ __global__ __launch_bounds__(256) void final_kernel(FinalArgs a) {
         ev = a.rf.plan[2 * step + a.rf.phase];
     }
     const int ngroups = rf ? a.B : (a.B + NR - 1) / NR;
-    for (int g = 0; g < ngroups; g++) {
+    for (int g = blockIdx.y; g < ngroups; g += gridDim.y) {
         // Row of slot i: the group's i-th row (a plain head's short last group repeats its
         // first row); frames past S stage zeros.
         auto row_of = [&](int i) {
@@ -392,7 +392,9 @@ static void launch_final_cfg(const FinalArgs& a, hipStream_t st) {
         (void)hipFuncSetAttribute((const void*)final_kernel<PT, NR>, hipFuncAttributeMaxDynamicSharedMemorySize, kMax);
         attr_set = true;
     }
-    final_kernel<PT, NR><<<(a.S + kFinFrames - 1) / kFinFrames, 256, lds, st>>>(a);
+    const int ngroups = a.rf.plan ? a.B : (a.B + NR - 1) / NR;
+    const dim3 grid((a.S + kFinFrames - 1) / kFinFrames, ngroups < 65535 ? ngroups : 65535);
+    final_kernel<PT, NR><<<grid, 256, lds, st>>>(a);
 }
 
 template <int PT>

@@ -109,6 +109,8 @@ SIGNATURES = {
                                         C.POINTER(C.c_int32), _f32p, _f32p]),
     "irodori_sample_device": (C.c_int, [_vp, C.POINTER(SamplerParamsC), C.c_int, C.c_int,
                                         _vp, _vp]),
+    "irodori_sample_device_masked": (C.c_int, [_vp, C.POINTER(SamplerParamsC), C.c_int, C.c_int,
+                                               C.POINTER(C.c_int32), _vp, _vp]),
     "irodori_profile_layer": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.POINTER(KernelTimesC)]),
     "irodori_op_rms_norm": (C.c_int, [_vp, _vp, C.c_int, C.c_int, C.c_float, _vp, _vp]),
     "irodori_op_fused_adaln": (C.c_int, [_vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_float,

@@ -223,11 +223,19 @@ class HipInferenceEngine:
 
     def sample_device(self, d_x0: int, d_out: int, utterances: int, seq: int,
                       params: SamplerParams, has_speaker: bool = True, has_caption: bool = False,
-                      ctx_aux_start: int = 0) -> None:
+                      ctx_aux_start: int = 0, lengths=None) -> None:
         """Same as sample() on device pointers (inputs/outputs resident in HBM)."""
         pc = sampler_params_c(params, has_speaker, has_caption, ctx_aux_start)
-        _check(self.lib.irodori_sample_device(self.ctx, C.byref(pc), utterances, seq,
-                                              C.c_void_p(d_x0), C.c_void_p(d_out)))
+        if lengths is None:
+            _check(self.lib.irodori_sample_device(self.ctx, C.byref(pc), utterances, seq,
+                                                  C.c_void_p(d_x0), C.c_void_p(d_out)))
+            return
+        ln = np.ascontiguousarray(lengths, np.int32)
+        if ln.shape != (utterances,):
+            raise IrodoriError("Shape", "lengths must be [utterances]")
+        _check(self.lib.irodori_sample_device_masked(
+            self.ctx, C.byref(pc), utterances, seq, ln.ctypes.data_as(C.POINTER(C.c_int32)),
+            C.c_void_p(d_x0), C.c_void_p(d_out)))
 
 
     def profile_layer(self, batch: int, seq: int, iters: int = 20) -> dict:

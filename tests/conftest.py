@@ -2,6 +2,10 @@ import os
 import sys
 
 import pytest
+# torch first: it carries its own HIP runtime, and a process that has loaded
+# libirodori_hip.so (linked against /opt/rocm's runtime) before importing torch leaves
+# torch without devices ("No HIP GPUs are available").
+import torch  # noqa: F401
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 for p in (ROOT, os.path.join(ROOT, "irodori-tts-burn_amd")):

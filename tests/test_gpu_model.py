@@ -207,6 +207,22 @@ def test_cfg4_sample_40_steps_bf16_vs_golden(cfg4):
     assert err < 2e-2
 
 
+@pytest.mark.parametrize("backend", [F32, BF16], ids=["f32", "bf16"])
+def test_large_batch_tile_shapes_are_bit_identical(cfg4, backend):
+    # At 12 rows x 750 frames the W_o / W2 projections switch from 64x64 to 128x128 tiles;
+    # both run the same MFMA sequence over k, so rows shared with a 2-row forward (64x64
+    # tiles, checked against the oracle above) must agree to the bit.
+    cfg, w, _, _ = cfg4
+    ctx = ih.make_context_kv(cfg, 6, 256, 375, seed=3)
+    x = ih.make_noise(12, 750, cfg.latent_dim, 4)
+    t = np.linspace(0.1, 0.9, 12).astype(np.float32)
+    with make_engine(cfg, backend, w, ctx, 12, 750) as e:
+        v12 = e.forward_with_cond_cached(x, t)
+        v2 = e.forward_with_cond_cached(x[:2], t[:2])
+    assert np.all(np.isfinite(v12))
+    assert np.array_equal(v12[:2], v2)
+
+
 # ---- latent key mask (attention.rs:730-750; config 5's padded batches) -------------------
 
 def _latent_mask(B, S, lengths, holes=()):
@@ -260,6 +276,13 @@ def test_sample_padded_batch_matches_unpadded(backend):
         short = e.sample(x0[1:2, :n], p)
     assert rel_l2(padded[1:2, :n], short) < 1e-6
     assert rel_l2(padded[0:1], full[0:1]) < 1e-6  # full-length utterance unaffected
+    import torch
+    d_x0 = torch.from_numpy(x0).to("cuda")
+    d_out = torch.empty_like(d_x0)
+    with make_engine(cfg, backend, w, ctx, 4, 64) as e:  # device-pointer variant
+        e.sample_device(d_x0.data_ptr(), d_out.data_ptr(), 2, 64, p, lengths=[64, n])
+        torch.cuda.synchronize()
+    assert np.array_equal(d_out.cpu().numpy(), padded)
     with pytest.raises(ih.IrodoriError):
         with make_engine(cfg, backend, w, ctx, 4, 64) as e:
             e.sample(x0, p, lengths=[64, 65])
