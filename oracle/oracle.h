@@ -35,6 +35,8 @@ typedef struct orc_cfg {
     int32_t t_dim;        /* timestep embedding dim */
     float norm_eps;
     float rope_theta;
+    int32_t gemm_fp8;     /* 1: the block GEMMs take fp8 operands (orc_mx_quantize_rows /
+                             orc_quant_weight_cols), the HIP path's fp8 compute mode */
 } orc_cfg;
 
 /* One DiffusionBlock (src/model/diffusion.rs:21-28), fused inference layout
@@ -88,6 +90,14 @@ typedef struct orc_sampler {
     int32_t ctx_aux_start;  /* first aux (speaker) key of the context sequence */
 } orc_sampler;
 
+/* fp8 (e4m3fn) GEMM operands (oracle.c). */
+uint8_t orc_e4m3_encode(float x);
+float orc_e4m3_decode(uint8_t b);
+int orc_mx_scale_exp(float amax);
+void orc_mx_quantize_rows(const float* x, int M, int K, uint8_t* q, uint8_t* s);
+void orc_mx_dequantize_rows(const uint8_t* q, const uint8_t* s, int M, int K, float* y);
+void orc_quant_weight_cols(const float* w, int K, int N, uint8_t* q, float* scale);
+
 /* Number of OpenMP threads the oracle uses (0 = runtime default). */
 void orc_set_threads(int n);
 int orc_get_threads(void);
@@ -113,6 +123,7 @@ int orc_get_threads(void);
     void P##adaln_vectors(const orc_cfg* c, const orc_block* blk, int which,               \
                           const float* cond, int B, float* shift, float* scale,            \
                           float* gate);                                                     \
+    void P##gemm_fp8(const float* x, const float* w, int M, int K, int N, float* y);      \
     void P##swiglu(const float* h, const float* w13, const float* w2, int M, int D, int F, \
                    float* out);                                                             \
     void P##joint_attention(const orc_cfg* c, const orc_block* blk, const float* h, int B, \

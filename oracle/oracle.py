@@ -27,7 +27,7 @@ class OrcCfg(C.Structure):
         ("latent_dim", C.c_int32), ("model_dim", C.c_int32), ("num_layers", C.c_int32),
         ("num_heads", C.c_int32), ("head_dim", C.c_int32), ("mlp_hidden", C.c_int32),
         ("adaln_rank", C.c_int32), ("t_dim", C.c_int32), ("norm_eps", C.c_float),
-        ("rope_theta", C.c_float),
+        ("rope_theta", C.c_float), ("gemm_fp8", C.c_int32),
     ]
 
 
@@ -123,23 +123,77 @@ def get_threads() -> int:
     return int(_load().orc_get_threads())
 
 
-class Oracle:
-    """Oracle entry points; arrays are numpy float32 (masks uint8), shapes as in oracle.h."""
+def e4m3_encode(x) -> np.ndarray:
+    """float32 array -> e4m3fn codes (uint8), round to nearest even, saturating at 448."""
+    lib = _load()
+    lib.orc_e4m3_encode.restype = C.c_uint8
+    lib.orc_e4m3_encode.argtypes = [C.c_float]
+    x = _c32(x)
+    return np.array([lib.orc_e4m3_encode(float(v)) for v in x.ravel()], np.uint8).reshape(x.shape)
 
-    def __init__(self, precision: str = "f32"):
+
+def e4m3_decode(b) -> np.ndarray:
+    lib = _load()
+    lib.orc_e4m3_decode.restype = C.c_float
+    lib.orc_e4m3_decode.argtypes = [C.c_uint8]
+    b = np.ascontiguousarray(b, np.uint8)
+    return np.array([lib.orc_e4m3_decode(int(v)) for v in b.ravel()], np.float32).reshape(b.shape)
+
+
+def mx_scale_exp(amax: float) -> int:
+    lib = _load()
+    lib.orc_mx_scale_exp.restype = C.c_int
+    lib.orc_mx_scale_exp.argtypes = [C.c_float]
+    return int(lib.orc_mx_scale_exp(float(amax)))
+
+
+def mx_quantize_rows(x):
+    """x [M, K] (K % 32 == 0) -> (codes uint8 [M, K], E8M0 scale bytes uint8 [M, K/32])."""
+    x = _c32(x)
+    M, K = x.shape
+    q = np.empty((M, K), np.uint8)
+    sc = np.empty((M, K // 32), np.uint8)
+    _load().orc_mx_quantize_rows(_f(x), M, K, _u8(q), _u8(sc))
+    return q, sc
+
+
+def mx_dequantize_rows(q, sc) -> np.ndarray:
+    q = np.ascontiguousarray(q, np.uint8)
+    sc = np.ascontiguousarray(sc, np.uint8)
+    M, K = q.shape
+    y = np.empty((M, K), np.float32)
+    _load().orc_mx_dequantize_rows(_u8(q), _u8(sc), M, K, _f(y))
+    return y
+
+
+def quant_weight_cols(w):
+    """Burn w [K, N] -> (codes uint8 [K, N], per-output-channel f32 scales [N])."""
+    w = _c32(w)
+    K, N = w.shape
+    q = np.empty((K, N), np.uint8)
+    sc = np.empty(N, np.float32)
+    _load().orc_quant_weight_cols(_f(w), K, N, _u8(q), _f(sc))
+    return q, sc
+
+
+class Oracle:
+    """Oracle entry points; arrays are numpy float32 (masks uint8), shapes as in oracle.h.
+    gemm_fp8: the block GEMMs take fp8 operands (the HIP path's fp8 compute mode)."""
+
+    def __init__(self, precision: str = "f32", gemm_fp8: bool = False):
         assert precision in ("f32", "f64")
         self.lib = _load()
         self.p = "orc_%s_" % precision
+        self.fp8 = bool(gemm_fp8)
 
     def _fn(self, name):
         return getattr(self.lib, self.p + name)
 
     # ---- structs -------------------------------------------------------------------
-    @staticmethod
-    def cfg_struct(cfg) -> OrcCfg:
+    def cfg_struct(self, cfg) -> OrcCfg:
         return OrcCfg(cfg.latent_dim, cfg.model_dim, cfg.num_layers, cfg.num_heads,
                       cfg.head_dim, cfg.mlp_hidden, cfg.adaln_rank, cfg.timestep_embed_dim,
-                      cfg.norm_eps, cfg.rope_theta)
+                      cfg.norm_eps, cfg.rope_theta, int(self.fp8))
 
     @staticmethod
     def block_struct(b) -> OrcBlock:
@@ -240,6 +294,15 @@ class Oracle:
         self._fn("adaln_vectors")(C.byref(self.cfg_struct(cfg)), C.byref(self.block_struct(blk)),
                                   which, _f(cond), B, _f(sh), _f(sc), _f(g))
         return sh, sc, g
+
+    def gemm_fp8(self, x, w):
+        """The fp8-operand block GEMM: x [M, K] @ w [K, N] (oracle.h gemm_fp8)."""
+        x, w = _c32(x), _c32(w)
+        M, K = x.shape
+        N = w.shape[1]
+        y = np.empty((M, N), np.float32)
+        self._fn("gemm_fp8")(_f(x), _f(w), M, K, N, _f(y))
+        return y
 
     def swiglu(self, h, w13, w2):
         h = _c32(h)

@@ -227,20 +227,56 @@ void P(adaln_vectors)(const orc_cfg* c, const orc_block* blk, int which, const f
     free(in); free(mid); free(up);
 }
 
+/* A block GEMM y[M,N] = x[M,K] @ w[K,N] (no bias), in fp8 operands when c->gemm_fp8
+ * (oracle.c): x quantized per row and 32-wide k block, w per output channel; the product
+ * of the dequantized x and the unscaled weight codes, then times the channel scale. */
+static void P(glinear)(const orc_cfg* c, const float* x, const float* w, int M, int K, int N, float* y) {
+    if (!c || !c->gemm_fp8) {
+        P(linear)(x, w, NULL, M, K, N, y);
+        return;
+    }
+    uint8_t* qx = (uint8_t*)malloc((size_t)M * K);
+    uint8_t* sx = (uint8_t*)malloc((size_t)M * (K / 32));
+    uint8_t* qw = (uint8_t*)malloc((size_t)K * N);
+    float* xd = (float*)malloc(sizeof(float) * (size_t)M * K);
+    float* wd = (float*)malloc(sizeof(float) * (size_t)K * N);
+    float* sw = (float*)malloc(sizeof(float) * (size_t)N);
+    orc_mx_quantize_rows(x, M, K, qx, sx);
+    orc_mx_dequantize_rows(qx, sx, M, K, xd);
+    orc_quant_weight_cols(w, K, N, qw, sw);
+    for (size_t i = 0; i < (size_t)K * N; i++) wd[i] = orc_e4m3_decode(qw[i]);
+    P(linear)(xd, wd, NULL, M, K, N, y);
+    for (int i = 0; i < M; i++)
+        for (int n = 0; n < N; n++) y[(size_t)i * N + n] = (float)((R)y[(size_t)i * N + n] * (R)sw[n]);
+    free(qx); free(sx); free(qw); free(xd); free(wd); free(sw);
+}
+
+void P(gemm_fp8)(const float* x, const float* w, int M, int K, int N, float* y) {
+    orc_cfg c;
+    memset(&c, 0, sizeof c);
+    c.gemm_fp8 = 1;
+    P(glinear)(&c, x, w, M, K, N, y);
+}
+
 /* feed_forward.rs:76-85 (SwiGlu::forward_fused): u = h @ [W1|W3];
  * out = (silu(u[:, :F]) * u[:, F:]) @ W2. */
-void P(swiglu)(const float* h, const float* w13, const float* w2, int M, int D, int F,
-               float* out) {
+static void P(swiglu_c)(const orc_cfg* c, const float* h, const float* w13, const float* w2, int M, int D,
+                        int F, float* out) {
     float* u = (float*)malloc(sizeof(float) * (size_t)M * 2 * F);
     float* m = (float*)malloc(sizeof(float) * (size_t)M * F);
-    P(linear)(h, w13, NULL, M, D, 2 * F, u);
+    P(glinear)(c, h, w13, M, D, 2 * F, u);
     #pragma omp parallel for schedule(static)
     for (int i = 0; i < M; i++)
         for (int j = 0; j < F; j++)
             m[(size_t)i * F + j] =
                 (float)(P(silu)((R)u[(size_t)i * 2 * F + j]) * (R)u[(size_t)i * 2 * F + F + j]);
-    P(linear)(m, w2, NULL, M, F, D, out);
+    P(glinear)(c, m, w2, M, F, D, out);
     free(u); free(m);
+}
+
+void P(swiglu)(const float* h, const float* w13, const float* w2, int M, int D, int F,
+               float* out) {
+    P(swiglu_c)(NULL, h, w13, w2, M, D, F, out);
 }
 
 /* attention.rs:272-425 (JointAttention::forward_fused with a KV cache):
@@ -260,7 +296,7 @@ void P(joint_attention)(const orc_cfg* c, const orc_block* blk, const float* h, 
     float* kk = (float*)malloc(sizeof(float) * szq);
     float* vv = (float*)malloc(sizeof(float) * szq);
     float* tmp = (float*)malloc(sizeof(float) * szq);
-    P(linear)(h, blk->w_qkv, NULL, M, D, 3 * HD, qkv);
+    P(glinear)(c, h, blk->w_qkv, M, D, 3 * HD, qkv);
     for (int i = 0; i < M; i++)
         for (int j = 0; j < HD; j++) {
             q[(size_t)i * HD + j] = qkv[(size_t)i * 3 * HD + j];
@@ -302,7 +338,7 @@ void P(joint_attention)(const orc_cfg* c, const orc_block* blk, const float* h, 
     P(sdpa)(qh, kh, vh, mk, B, H, S, Skv, Dh, (float)(R_C(1.0) / SQRT((R)Dh)), oh);
 
     /* gated = sigmoid(h @ W_gate) * o  (o back to [B, S, H*Dh]); out = gated @ W_o. */
-    P(linear)(h, blk->w_gate, NULL, M, D, D, tmp);
+    P(glinear)(c, h, blk->w_gate, M, D, D, tmp);
     for (int b = 0; b < B; b++)
         for (int s = 0; s < S; s++)
             for (int hh = 0; hh < H; hh++)
@@ -311,7 +347,7 @@ void P(joint_attention)(const orc_cfg* c, const orc_block* blk, const float* h, 
                     R o = (R)oh[(((size_t)b * H + hh) * S + s) * Dh + d];
                     q[dst] = (float)(P(sigmoid)((R)tmp[dst]) * o);
                 }
-    P(linear)(q, blk->w_o, NULL, M, HD, D, out);
+    P(glinear)(c, q, blk->w_o, M, HD, D, out);
     free(qkv); free(q); free(kk); free(vv); free(tmp);
     free(qh); free(kh); free(vh); free(mk); free(oh);
 }
@@ -341,7 +377,7 @@ void P(block_forward)(const orc_cfg* c, const orc_block* blk, float* x, const fl
     }
     P(adaln_vectors)(c, blk, 1, cond, B, shift, scale, gate);
     P(fused_adaln)(x, scale, shift, B, S, D, c->norm_eps, h);
-    P(swiglu)(h, blk->w13, blk->w2, M, D, F, y);
+    P(swiglu_c)(c, h, blk->w13, blk->w2, M, D, F, y);
     for (size_t i = 0; i < n; i++) {
         int b = (int)(i / ((size_t)S * D)), d = (int)(i % D);
         x[i] = (float)((R)x[i] + (R)gate[b * D + d] * (R)y[i]);
