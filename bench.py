@@ -20,6 +20,7 @@ for _p in (ROOT, os.path.join(ROOT, "irodori-tts-burn_amd")):
 
 METRIC = "RF ms per 40 steps @750 frames, B=2 joint CFG; attn/MLP MFMA util %"
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_FP8_TFLOPS = 5000.0    # MI355X dense fp8 MFMA
 PEAK_HBM_GBS = 8000.0
 
 
@@ -96,6 +97,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--profile-iters", type=int, default=50)
+    ap.add_argument("--cfg5-dtype", choices=["fp8", "bf16"], default="fp8",
+                    help="compute mode of --workload cfg5 (config 5 names fp8 weights)")
     ap.add_argument("--workload", choices=["cfg4", "cfg5"], default="cfg4",
                     help="cfg4 (default): the headline B=2 Joint-CFG RF run; cfg5: batched "
                          "throughput, 16 utterances x 2 CFG rows, lengths U[200,750] padded")
@@ -242,9 +245,12 @@ def main():
 
 
 def run_cfg5(args, np, torch, ih):
-    """BASELINE config 5 in bf16: 16 utterances x Joint CFG = 32 rows of the 12-layer d1024
-    DiT, latent lengths U[200,750] padded to 750 with the latent key mask, text valid lengths
-    U[32,256], 40 Euler steps.  Aggregate latent frames/s = sum(lengths) / RF-run seconds."""
+    """16 utterances x Joint CFG = 32 rows of the 12-layer d1024 DiT, latent
+    lengths U[200,750] padded to 750 with the latent key mask, text valid lengths U[32,256],
+    40 Euler steps; fp8 (e4m3 weights with per-output-channel f32 scales, GEMM inputs with
+    power-of-two scales per 32 values, bf16 attention) or bf16.  Aggregate latent
+    frames/s = sum(lengths) / RF-run seconds."""
+    fp8 = args.cfg5_dtype == "fp8"
     cfg = ih.cfg_full_rf()
     U, S, Tt, Ts, N, SCALE = 16, 750, 256, 375, 40, 3.0
     rng = np.random.default_rng(5)
@@ -256,8 +262,8 @@ def run_cfg5(args, np, torch, ih):
     g = ih.GuidanceConfig(mode=ih.CfgGuidanceMode.JOINT, scale_text=SCALE, scale_speaker=SCALE,
                           min_t=0.0, max_t=1.0)
     params = ih.SamplerParams(num_steps=N, guidance=g)
-    eng = ih.HipInferenceEngine(cfg, ih.InferenceBackendKind.HIP_BF16, max_rows=2 * U,
-                                max_seq=S, max_ctx=Tt + Ts)
+    kind = ih.InferenceBackendKind.HIP_FP8 if fp8 else ih.InferenceBackendKind.HIP_BF16
+    eng = ih.HipInferenceEngine(cfg, kind, max_rows=2 * U, max_seq=S, max_ctx=Tt + Ts)
     eng.load_weights(w)
     eng.set_context_kv(ctx)
     d_x0 = torch.from_numpy(x0).to("cuda")
@@ -284,6 +290,7 @@ def run_cfg5(args, np, torch, ih):
     M, D, F = 2 * U * S, cfg.model_dim, cfg.mlp_hidden
     w13_flops = 2.0 * M * D * 2 * F
     achieved = w13_flops / (kt["w13_gemm_us"] * 1e-6) / 1e12
+    peak = PEAK_FP8_TFLOPS if fp8 else PEAK_BF16_TFLOPS
     frames = int(lengths.sum())
     H, Dh, T = cfg.num_heads, cfg.head_dim, Tt + Ts
     per_tok = 2.0 * D * (4 * D + D + 2 * F) + 2.0 * F * D  # GEMM FLOP per token per block
@@ -296,20 +303,20 @@ def run_cfg5(args, np, torch, ih):
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms, 3),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "fp8 (e4m3 block GEMMs; bf16 attention)" if fp8 else "bf16",
         "data": "synthetic: seeded random-init DiT (all Linear N(0,0.02)), N(0,1) noise and "
                 "context K/V, latent lengths U[200,750] (seed 5), text valid length U[32,256]",
-        "config": {"workload": "BASELINE config 5 shape in bf16 (fp8 weights not built): "
-                               "12-layer d1024 DiT, 16 utterances x Joint CFG = 32 rows padded "
-                               "to 750 frames with the latent key mask, 256 text + 375 speaker "
-                               "keys, 40 Euler steps",
+        "config": {"workload": "BASELINE config 5%s: 12-layer d1024 DiT, 16 utterances x Joint "
+                               "CFG = 32 rows padded to 750 frames with the latent key mask, 256 "
+                               "text + 375 speaker keys, 40 Euler steps"
+                               % ("" if fp8 else " shape in bf16"),
                    "global_batch": 2 * U, "seq_len": S, "rf_steps": N, "parallelism": "none",
                    "lengths_sum": frames},
         "useful_tflops": round(useful / (ms * 1e-3) / 1e12, 1),
         "kernel_us": {k: round(v, 2) for k, v in kt.items()},
         "roofline": {"kernel": "w13_gemm (SwiGLU up-projection, %dx1024x5632)" % M,
-                     "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "bound": "mfma", "achieved": round(achieved, 2), "peak": peak,
+                     "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
                      "traffic": None},
         "cpu_baseline": None,
     }

@@ -51,6 +51,11 @@ extern "C" {
 
 #define IRODORI_DTYPE_F32 0
 #define IRODORI_DTYPE_BF16 1
+/* bf16 activations and attention; the block GEMMs (QKV+gate, W_o, W1|W3, W2) on e4m3fn
+ * operands: weights with one f32 scale per output channel, GEMM inputs with one
+ * power-of-two scale per 32 values along k (the gfx950 scaled fp8 MFMA).  No counterpart in
+ * the reference (BASELINE config 5's fp8 weights); needs model_dim, mlp_hidden % 128 == 0. */
+#define IRODORI_DTYPE_FP8 2
 
 #define IRODORI_CFG_INDEPENDENT 0 /* CfgGuidanceMode (src/config/sampling.rs:100-108) */
 #define IRODORI_CFG_JOINT 1
@@ -75,7 +80,7 @@ typedef struct irodori_dit_config {
     int32_t timestep_embed_dim; /* t_dim */
     float norm_eps;             /* norm_eps (config/model.rs:78) */
     float rope_theta;           /* 10000 (dit/model.rs:216) */
-    int32_t compute_dtype;      /* IRODORI_DTYPE_BF16 (MFMA bf16) or IRODORI_DTYPE_F32 */
+    int32_t compute_dtype;      /* IRODORI_DTYPE_BF16 (MFMA bf16), _F32 or _FP8 */
     int32_t max_rows;           /* max batch rows in one forward (2 per utterance) */
     int32_t max_seq;            /* max latent frames S */
     int32_t max_ctx;            /* max context keys T = text + speaker */
@@ -267,6 +272,16 @@ int irodori_op_fused_adaln(const float* x, const float* scale, const float* shif
 int irodori_op_sdpa(int dtype, const void* q, const void* k, const void* v, const float* mask,
                     int batch, int heads, int seq_q, int seq_kv, int head_dim, float scale,
                     float* out, void* stream);
+/* The fp8 GEMM-operand form of the IRODORI_DTYPE_FP8 mode (no counterpart in the
+ * reference): x [rows, dim] f32 (dim % 32 == 0) -> e4m3 codes q [rows, dim] and E8M0 scale
+ * bytes s [rows, dim/32]; per 32-wide block, 2^e with e the smallest integer such that
+ * max |x| <= 448 * 2^e, codes = round-to-nearest-even e4m3(x * 2^-e). */
+int irodori_op_mx_quantize(const float* x, int rows, int dim, uint8_t* q, uint8_t* s, void* stream);
+/* The fp8 block GEMM of that mode: c[m, n] = w_scale[n] * sum_k a[m, k] 2^(a_scale[m, k/32] - 127)
+ * * w[n, k], with a [M, K] and w [N, K] e4m3 codes (K-contiguous, K % 128 == 0, N % 64 == 0),
+ * a_scale [M, K/32] E8M0 bytes, w_scale [N] f32; c [M, N] f32. */
+int irodori_op_gemm_fp8(const uint8_t* a, const uint8_t* a_scale, const uint8_t* w, const float* w_scale,
+                        int M, int N, int K, float* c, void* stream);
 
 #ifdef __cplusplus
 }

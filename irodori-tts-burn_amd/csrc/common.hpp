@@ -28,6 +28,41 @@ __device__ __forceinline__ float from_f32<float>(float v) { return v; }
 template <>
 __device__ __forceinline__ bf16 from_f32<bf16>(float v) { return static_cast<bf16>(v); }
 
+// ---------------------------------------------------------------------------------
+// fp8 (e4m3fn) GEMM operands: a 32-wide block of a row is stored as e4m3 codes of
+// x * 2^-e with e the smallest integer such that max |x| <= 448 * 2^e, and the E8M0 byte
+// 127 + e.  The codes then never exceed 448, where the hardware converter (round to
+// nearest even) is exact.
+// ---------------------------------------------------------------------------------
+// The block exponent from the bits of amax = (1 + f / 2^23) 2^(E - 127):
+// amax <= 448 2^e  <=>  e >= E - 135 when f <= 0.75 * 2^23, else e >= E - 134.
+__device__ __forceinline__ int mx_exp(float amax) {
+    const unsigned u = __float_as_uint(amax);
+    const int E = (int)(u >> 23);
+    if (E == 0) return amax > 0.f ? -127 : 0;
+    const int e = (u & 0x7fffffu) <= 0x600000u ? E - 135 : E - 134;
+    return e < -127 ? -127 : (e > 127 ? 127 : e);
+}
+// Four values -> four e4m3 bytes (little-endian in the word).
+__device__ __forceinline__ unsigned pack_e4m3(float v0, float v1, float v2, float v3) {
+    int w = __builtin_amdgcn_cvt_pk_fp8_f32(v0, v1, 0, false);
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(v2, v3, w, true);
+    return (unsigned)w;
+}
+// Quantize four consecutive values held by each lane of an aligned group of 8 lanes (one
+// 32-wide block): every lane of the group must call it.  Stores the lane's 4 codes at q
+// and, from the group's first lane, the block's scale byte at s.
+__device__ __forceinline__ void mx_store4_group8(float a, float b, float c, float d, uint8_t* q, uint8_t* s,
+                                                 int lane) {
+    float amax = fmaxf(fmaxf(fabsf(a), fabsf(b)), fmaxf(fabsf(c), fabsf(d)));
+    amax = fmaxf(amax, __shfl_xor(amax, 1));
+    amax = fmaxf(amax, __shfl_xor(amax, 2));
+    amax = fmaxf(amax, __shfl_xor(amax, 4));
+    const int e = mx_exp(amax);
+    *reinterpret_cast<unsigned*>(q) = pack_e4m3(ldexpf(a, -e), ldexpf(b, -e), ldexpf(c, -e), ldexpf(d, -e));
+    if ((lane & 7) == 0) *s = (uint8_t)(127 + e);
+}
+
 // A "k32 fragment": the 8 consecutive reduction-dim elements one lane feeds to the
 // matrix core per 32-wide slice of K.  For bf16 that is one v_mfma_f32_16x16x32_bf16
 // operand; for f32 it is the operands of eight v_mfma_f32_16x16x4_f32 (element j goes

@@ -77,6 +77,12 @@ struct LayerBufs {
     void* w_o = nullptr;     // [D, HD]
     void* w13 = nullptr;     // [2F, D], W1/W3 rows interleaved per 32
     void* w2 = nullptr;      // [D, F]
+    // fp8 compute: the four weights above hold e4m3 codes; their per-row (output channel)
+    // scales.
+    float* ws_qkvg = nullptr;
+    float* ws_o = nullptr;
+    float* ws_13 = nullptr;
+    float* ws_2 = nullptr;
     float* q_norm = nullptr;
     float* k_norm = nullptr;
     float* ada_down[2][3] = {};
@@ -115,7 +121,8 @@ struct irodori_ctx {
     int device = 0;
     irodori_dit_config cfg{};
     bool bf16 = true;
-    size_t esz = 2;  // compute element size
+    bool fp8 = false;  // block GEMMs on e4m3 operands (activations and attention stay bf16)
+    size_t esz = 2;    // compute element size
     hipStream_t stream = nullptr;
     // Side capture streams and fork/join events: a captured sampler evaluation runs each
     // CFG role as an independent chain of kernels (role 0 on `stream`) until the update.
@@ -141,6 +148,10 @@ struct irodori_ctx {
     void* gate = nullptr;  // [rows*S, D]
     void* o = nullptr;     // [rows*S, D]
     void* u = nullptr;     // [rows*S, F]
+    // fp8 compute: the GEMM inputs h, o and u as e4m3 codes with E8M0 scales per 32 values.
+    uint8_t *h8 = nullptr, *h8s = nullptr;  // [rows*S, D], [rows*S, D/32]
+    uint8_t *o8 = nullptr, *o8s = nullptr;  // [rows*S, D], [rows*S, D/32]
+    uint8_t *u8 = nullptr, *u8s = nullptr;  // [rows*S, F], [rows*S, F/32]
     float* rope_cos = nullptr;
     float* rope_sin = nullptr;
     float* xt = nullptr;    // [rows, S, P] sampler state / forward input
@@ -262,6 +273,30 @@ int ingest_kmajor(irodori_ctx* c, const float* host, int K, int N, int mode, voi
     return IRODORI_OK;
 }
 
+// Host f32 [K, N] -> device e4m3 codes [N, K] (row n = output channel, transpose mode as
+// ingest_kmajor) at dst_q, and the channel scales at dst_s.
+int ingest_fp8(irodori_ctx* c, const float* host, int K, int N, int mode, uint8_t* dst_q, float* dst_s) {
+    float *stage = nullptr, *kmaj = nullptr;
+    const size_t bytes = sizeof(float) * (size_t)K * N;
+    IRO_HIP_CHECK(hipMalloc(&stage, bytes));
+    hipError_t e = hipMalloc(&kmaj, bytes);
+    if (e == hipSuccess) e = hipMemcpyAsync(stage, host, bytes, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) {
+        launch_transpose<float>(stage, K, N, mode, kmaj, c->stream);
+        launch_quant_weight_rows(kmaj, N, K, dst_q, dst_s, c->stream);
+        e = hipGetLastError();
+    }
+    hipError_t e2 = hipStreamSynchronize(c->stream);
+    (void)hipFree(stage);
+    if (kmaj) (void)hipFree(kmaj);
+    if (e == hipSuccess) e = e2;
+    if (e != hipSuccess) {
+        set_last_error(std::string("fp8 weight ingest: ") + hipGetErrorString(e));
+        return IRODORI_ERR_HIP;
+    }
+    return IRODORI_OK;
+}
+
 int ensure_nvec(irodori_ctx* c, int nvec) {
     if (nvec <= c->nvec_cap) return IRODORI_OK;
     const auto& g = c->cfg;
@@ -359,6 +394,30 @@ int enqueue_part(irodori_ctx* c, int l, int B, int S, const ModTable& mt, int pa
     T* gate = static_cast<T*>(c->gate) + tok0 * D;
     T* o = static_cast<T*>(c->o) + tok0 * D;
     T* u = static_cast<T*>(c->u) + tok0 * F;
+    // fp8 compute: the e4m3 copies of h / o / u with their block scales (same row slice).
+    const bool f8 = c->fp8 && std::is_same<T, bf16>::value;
+    uint8_t* h8 = f8 ? c->h8 + tok0 * D : nullptr;
+    uint8_t* h8s = f8 ? c->h8s + tok0 * (D / 32) : nullptr;
+    uint8_t* o8 = f8 ? c->o8 + tok0 * D : nullptr;
+    uint8_t* o8s = f8 ? c->o8s + tok0 * (D / 32) : nullptr;
+    uint8_t* u8 = f8 ? c->u8 + tok0 * F : nullptr;
+    uint8_t* u8s = f8 ? c->u8s + tok0 * (F / 32) : nullptr;
+    // One projection: the bf16 / f32 GEMM on A and W, or the fp8 GEMM on their e4m3 forms.
+    auto gemm = [&](int epi, GemmArgs<T>& args, const T* A, const uint8_t* A8, const uint8_t* As,
+                    const void* W, const float* ws) -> int {
+        if constexpr (std::is_same<T, bf16>::value) {
+            if (f8) {
+                args.A8 = A8;
+                args.As = As;
+                args.W8 = static_cast<const uint8_t*>(W);
+                args.ws = ws;
+                return launch_gemm_fp8(epi, args, st);
+            }
+        }
+        args.A = A;
+        args.W = static_cast<const T*>(W);
+        return launch_gemm<T>(epi, args, st);
+    };
 
     GemmArgs<T> ga{};
     ga.mt = mt;
@@ -373,8 +432,6 @@ int enqueue_part(irodori_ctx* c, int l, int B, int S, const ModTable& mt, int pa
     switch (part) {
         case PART_QKVG: {
             // QKV + gate projection with head norms and half RoPE (attention.rs:293-345, :423).
-            ga.A = h;
-            ga.W = static_cast<const T*>(lb.w_qkvg);
             ga.N = 4 * D;
             ga.K = D;
             ga.Q = q;
@@ -387,7 +444,10 @@ int enqueue_part(irodori_ctx* c, int l, int B, int S, const ModTable& mt, int pa
             ga.rope_sin = c->rope_sin;
             ga.vt_stride = vt_stride;
             ga.q_scale = 1.4426950408889634f / sqrtf((float)g.head_dim);
-            if (launch_gemm<T>(EPI_QKVG, ga, st)) { set_last_error("qkvg gemm shape"); return IRODORI_ERR_SHAPE; }
+            if (gemm(EPI_QKVG, ga, h, h8, h8s, lb.w_qkvg, lb.ws_qkvg)) {
+                set_last_error("qkvg gemm shape");
+                return IRODORI_ERR_SHAPE;
+            }
             break;
         }
         case PART_ATTN: {
@@ -423,9 +483,11 @@ int enqueue_part(irodori_ctx* c, int l, int B, int S, const ModTable& mt, int pa
             aa.H = H;
             aa.Sq = S;
             aa.scale = 1.0f / sqrtf((float)g.head_dim);
-            aa.out_mode = 0;
+            aa.out_mode = f8 ? 2 : 0;  // fp8: o goes straight to the W_o operand form
             aa.G = gate;
             aa.O = o;
+            aa.O8 = o8;
+            aa.O8s = o8s;
             int arc;
             if constexpr (std::is_same<T, bf16>::value)
                 arc = launch_attention32(aa, st);
@@ -436,42 +498,49 @@ int enqueue_part(irodori_ctx* c, int l, int B, int S, const ModTable& mt, int pa
         }
         case PART_WO: {
             // x += g_attn * (o @ Wo) (attention.rs:424, diffusion.rs:98).
-            ga.A = o;
-            ga.W = static_cast<const T*>(lb.w_o);
             ga.N = D;
             ga.K = D;
             ga.kind = 0;
-            if (launch_gemm<T>(EPI_RESID, ga, st)) { set_last_error("wo gemm shape"); return IRODORI_ERR_SHAPE; }
+            if (gemm(EPI_RESID, ga, o, o8, o8s, lb.w_o, lb.ws_o)) {
+                set_last_error("wo gemm shape");
+                return IRODORI_ERR_SHAPE;
+            }
             break;
         }
         case PART_NORM_MLP: {
             // h2 = mlp adaLN(x) (diffusion.rs:101-102).
-            launch_norm_mod<T>(x, h, M, S, D, g.norm_eps, mt, l, 1, st);
+            launch_norm_mod<T>(x, f8 ? nullptr : h, M, S, D, g.norm_eps, mt, l, 1, st, h8, h8s);
             break;
         }
         case PART_W13: {
             // m = silu(h2 W1) * (h2 W3) (feed_forward.rs:76-84).
-            ga.A = h;
-            ga.W = static_cast<const T*>(lb.w13);
             ga.N = 2 * F;
             ga.K = D;
             ga.U = u;
-            if (launch_gemm<T>(EPI_SWIGLU, ga, st)) { set_last_error("w13 gemm shape"); return IRODORI_ERR_SHAPE; }
+            ga.U8 = u8;  // fp8: m goes straight to the W2 operand form
+            ga.U8s = u8s;
+            if (gemm(EPI_SWIGLU, ga, h, h8, h8s, lb.w13, lb.ws_13)) {
+                set_last_error("w13 gemm shape");
+                return IRODORI_ERR_SHAPE;
+            }
             break;
         }
         case PART_W2: {
             // x += g_mlp * (m @ W2) (diffusion.rs:104).
-            ga.A = u;
-            ga.W = static_cast<const T*>(lb.w2);
             ga.N = D;
             ga.K = F;
             ga.kind = 1;
-            if (launch_gemm<T>(EPI_RESID, ga, st)) { set_last_error("w2 gemm shape"); return IRODORI_ERR_SHAPE; }
+            if (gemm(EPI_RESID, ga, u, u8, u8s, lb.w2, lb.ws_2)) {
+                set_last_error("w2 gemm shape");
+                return IRODORI_ERR_SHAPE;
+            }
             break;
         }
         case PART_NORM_NEXT: {
             // Next block's attention adaLN.
-            if (!last) launch_norm_mod<T>(x, h, M, S, D, g.norm_eps, mt, l + 1, 0, st);
+            if (!last) {
+                launch_norm_mod<T>(x, f8 ? nullptr : h, M, S, D, g.norm_eps, mt, l + 1, 0, st, h8, h8s);
+            }
             break;
         }
         default:
@@ -506,9 +575,12 @@ int enqueue_inproj(irodori_ctx* c, int B, int S, const float* src, int src_batch
     const auto& g = c->cfg;
     const size_t tok0 = (size_t)r0 * S;
     float* x = c->x + tok0 * g.model_dim;
-    if (c->bf16)
-        launch_inproj_norm<bf16>(src, src_batches, c->in_w, c->in_b, x, static_cast<bf16*>(c->h) + tok0 * g.model_dim,
-                                 B * S, S, g.latent_dim, g.model_dim, g.norm_eps, mt, st);
+    if (c->bf16) {
+        bf16* h = c->fp8 ? nullptr : static_cast<bf16*>(c->h) + tok0 * g.model_dim;
+        launch_inproj_norm<bf16>(src, src_batches, c->in_w, c->in_b, x, h, B * S, S, g.latent_dim, g.model_dim,
+                                 g.norm_eps, mt, st, c->fp8 ? c->h8 + tok0 * g.model_dim : nullptr,
+                                 c->fp8 ? c->h8s + tok0 * (g.model_dim / 32) : nullptr);
+    }
     else
         launch_inproj_norm<float>(src, src_batches, c->in_w, c->in_b, x,
                                   static_cast<float*>(c->h) + tok0 * g.model_dim, B * S, S, g.latent_dim,
@@ -718,8 +790,11 @@ int irodori_ctx_create(int device, const irodori_dit_config* cfg, irodori_ctx** 
     IRO_REQUIRE(cfg && out, IRODORI_ERR_INVALID_ARG, "null argument");
     *out = nullptr;
     const irodori_dit_config& g = *cfg;
-    IRO_REQUIRE(g.compute_dtype == IRODORI_DTYPE_BF16 || g.compute_dtype == IRODORI_DTYPE_F32,
-                IRODORI_ERR_DTYPE, "compute_dtype must be IRODORI_DTYPE_BF16 or IRODORI_DTYPE_F32");
+    IRO_REQUIRE(g.compute_dtype == IRODORI_DTYPE_BF16 || g.compute_dtype == IRODORI_DTYPE_F32 ||
+                    g.compute_dtype == IRODORI_DTYPE_FP8,
+                IRODORI_ERR_DTYPE, "compute_dtype must be IRODORI_DTYPE_BF16, _F32 or _FP8");
+    IRO_REQUIRE(g.compute_dtype != IRODORI_DTYPE_FP8 || (g.model_dim % 128 == 0 && g.mlp_hidden % 128 == 0),
+                IRODORI_ERR_SHAPE, "fp8 compute needs model_dim and mlp_hidden multiples of 128");
     IRO_REQUIRE(g.num_layers > 0 && g.num_heads > 0 && g.model_dim > 0 && g.latent_dim > 0,
                 IRODORI_ERR_SHAPE, "dimensions must be positive");
     IRO_REQUIRE(g.head_dim == 64, IRODORI_ERR_SHAPE, "head_dim must be 64");
@@ -743,7 +818,8 @@ int irodori_ctx_create(int device, const irodori_dit_config* cfg, irodori_ctx** 
     std::unique_ptr<irodori_ctx, int (*)(irodori_ctx*)> c(new irodori_ctx(), irodori_ctx_destroy);
     c->device = device;
     c->cfg = g;
-    c->bf16 = g.compute_dtype == IRODORI_DTYPE_BF16;
+    c->fp8 = g.compute_dtype == IRODORI_DTYPE_FP8;
+    c->bf16 = g.compute_dtype == IRODORI_DTYPE_BF16 || c->fp8;
     c->esz = c->bf16 ? 2 : 4;
     IRO_HIP_CHECK(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
     IRO_HIP_CHECK(hipEventCreateWithFlags(&c->ev_fork, hipEventDisableTiming));
@@ -760,10 +836,17 @@ int irodori_ctx_create(int device, const irodori_dit_config* cfg, irodori_ctx** 
     int Tp = ntl * 64, Sp = (S + 63) / 64 * 64;
     for (int l = 0; l < L; l++) {
         auto& lb = c->layers[l];
-        IRO_TRY(dev_alloc(c.get(), &lb.w_qkvg, es * 4 * D * D));
-        IRO_TRY(dev_alloc(c.get(), &lb.w_o, es * D * D));
-        IRO_TRY(dev_alloc(c.get(), &lb.w13, es * 2 * (size_t)F * D));
-        IRO_TRY(dev_alloc(c.get(), &lb.w2, es * (size_t)D * F));
+        const size_t wes = c->fp8 ? 1 : es;  // weight element bytes
+        IRO_TRY(dev_alloc(c.get(), &lb.w_qkvg, wes * 4 * D * D));
+        IRO_TRY(dev_alloc(c.get(), &lb.w_o, wes * D * D));
+        IRO_TRY(dev_alloc(c.get(), &lb.w13, wes * 2 * (size_t)F * D));
+        IRO_TRY(dev_alloc(c.get(), &lb.w2, wes * (size_t)D * F));
+        if (c->fp8) {
+            IRO_TRY(dalloc(c.get(), &lb.ws_qkvg, sizeof(float) * 4 * D));
+            IRO_TRY(dalloc(c.get(), &lb.ws_o, sizeof(float) * D));
+            IRO_TRY(dalloc(c.get(), &lb.ws_13, sizeof(float) * 2 * F));
+            IRO_TRY(dalloc(c.get(), &lb.ws_2, sizeof(float) * D));
+        }
         IRO_TRY(dalloc(c.get(), &lb.q_norm, sizeof(float) * H * Dh));
         IRO_TRY(dalloc(c.get(), &lb.k_norm, sizeof(float) * H * Dh));
         for (int k = 0; k < 2; k++)
@@ -798,6 +881,14 @@ int irodori_ctx_create(int device, const irodori_dit_config* cfg, irodori_ctx** 
     IRO_TRY(dev_alloc(c.get(), &c->gate, es * M * D));
     IRO_TRY(dev_alloc(c.get(), &c->o, es * M * D));
     IRO_TRY(dev_alloc(c.get(), &c->u, es * M * F));
+    if (c->fp8) {
+        IRO_TRY(dalloc(c.get(), &c->h8, M * D));
+        IRO_TRY(dalloc(c.get(), &c->h8s, M * D / 32));
+        IRO_TRY(dalloc(c.get(), &c->o8, M * D));
+        IRO_TRY(dalloc(c.get(), &c->o8s, M * D / 32));
+        IRO_TRY(dalloc(c.get(), &c->u8, M * F));
+        IRO_TRY(dalloc(c.get(), &c->u8s, M * F / 32));
+    }
     IRO_TRY(dalloc(c.get(), &c->rope_cos, sizeof(float) * (size_t)S * Dh / 2));
     IRO_TRY(dalloc(c.get(), &c->rope_sin, sizeof(float) * (size_t)S * Dh / 2));
     IRO_TRY(dalloc(c.get(), &c->xt, sizeof(float) * M * P));
@@ -868,11 +959,20 @@ int irodori_load_block_weights(irodori_ctx* c, int layer, const irodori_block_we
     int D = g.model_dim, F = g.mlp_hidden, HD = g.num_heads * g.head_dim, r = g.adaln_rank;
     auto& lb = c->layers[layer];
     char* qkvg = static_cast<char*>(lb.w_qkvg);
-    IRO_TRY(ingest_kmajor(c, w->w_qkv, D, 3 * HD, 0, qkvg));
-    IRO_TRY(ingest_kmajor(c, w->w_gate, D, D, 0, qkvg + c->esz * (size_t)3 * HD * D));
-    IRO_TRY(ingest_kmajor(c, w->w_o, HD, D, 0, lb.w_o));
-    IRO_TRY(ingest_kmajor(c, w->w13, D, 2 * F, 1, lb.w13));
-    IRO_TRY(ingest_kmajor(c, w->w2, F, D, 0, lb.w2));
+    if (c->fp8) {
+        uint8_t* q8 = reinterpret_cast<uint8_t*>(qkvg);
+        IRO_TRY(ingest_fp8(c, w->w_qkv, D, 3 * HD, 0, q8, lb.ws_qkvg));
+        IRO_TRY(ingest_fp8(c, w->w_gate, D, D, 0, q8 + (size_t)3 * HD * D, lb.ws_qkvg + 3 * HD));
+        IRO_TRY(ingest_fp8(c, w->w_o, HD, D, 0, static_cast<uint8_t*>(lb.w_o), lb.ws_o));
+        IRO_TRY(ingest_fp8(c, w->w13, D, 2 * F, 1, static_cast<uint8_t*>(lb.w13), lb.ws_13));
+        IRO_TRY(ingest_fp8(c, w->w2, F, D, 0, static_cast<uint8_t*>(lb.w2), lb.ws_2));
+    } else {
+        IRO_TRY(ingest_kmajor(c, w->w_qkv, D, 3 * HD, 0, qkvg));
+        IRO_TRY(ingest_kmajor(c, w->w_gate, D, D, 0, qkvg + c->esz * (size_t)3 * HD * D));
+        IRO_TRY(ingest_kmajor(c, w->w_o, HD, D, 0, lb.w_o));
+        IRO_TRY(ingest_kmajor(c, w->w13, D, 2 * F, 1, lb.w13));
+        IRO_TRY(ingest_kmajor(c, w->w2, F, D, 0, lb.w2));
+    }
     IRO_TRY(upload(c, lb.q_norm, w->q_norm, sizeof(float) * HD));
     IRO_TRY(upload(c, lb.k_norm, w->k_norm, sizeof(float) * HD));
     for (int k = 0; k < 2; k++)
@@ -1261,9 +1361,10 @@ int irodori_block_forward(irodori_ctx* c, int layer, int B, int S, float* x, con
     ModTable mt{c->tab, c->zero_step, 0, 1, L};
     size_t n = (size_t)B * S * D;
     IRO_TRY(upload(c, c->x, x, sizeof(float) * n));
-    if (c->bf16)
-        launch_norm_mod<bf16>(c->x, static_cast<bf16*>(c->h), B * S, S, D, g.norm_eps, mt, layer, 0, c->stream);
-    else
+    if (c->bf16) {
+        launch_norm_mod<bf16>(c->x, c->fp8 ? nullptr : static_cast<bf16*>(c->h), B * S, S, D, g.norm_eps, mt, layer,
+                              0, c->stream, c->fp8 ? c->h8 : nullptr, c->fp8 ? c->h8s : nullptr);
+    } else
         launch_norm_mod<float>(c->x, static_cast<float*>(c->h), B * S, S, D, g.norm_eps, mt, layer, 0, c->stream);
     IRO_TRY(enqueue_layer_any(c, layer, B, S, mt));
     IRO_HIP_CHECK(hipMemcpyAsync(x, c->x, sizeof(float) * n, hipMemcpyDeviceToHost, c->stream));
@@ -1597,6 +1698,38 @@ int irodori_profile_layer(irodori_ctx* c, int B, int S, int iters, irodori_kerne
 }
 
 // ---- operator entry points ------------------------------------------------------------
+
+int irodori_op_mx_quantize(const float* x, int rows, int dim, uint8_t* q, uint8_t* s, void* stream) {
+    IRO_GUARD_BEGIN
+    IRO_REQUIRE(x && q && s, IRODORI_ERR_INVALID_ARG, "null argument");
+    IRO_REQUIRE(rows > 0 && dim > 0 && dim % 32 == 0, IRODORI_ERR_SHAPE, "mx_quantize requires rows > 0 and dim % 32 == 0");
+    launch_mx_quant_rows<float>(x, rows, dim, q, s, static_cast<hipStream_t>(stream));
+    return check_launch("mx_quantize");
+    IRO_GUARD_END
+}
+
+int irodori_op_gemm_fp8(const uint8_t* a8, const uint8_t* a_scale, const uint8_t* w8, const float* w_scale, int M,
+                        int N, int K, float* c, void* stream) {
+    IRO_GUARD_BEGIN
+    IRO_REQUIRE(a8 && a_scale && w8 && w_scale && c, IRODORI_ERR_INVALID_ARG, "null argument");
+    IRO_REQUIRE(M > 0 && N > 0 && N % 64 == 0 && K > 0 && K % 128 == 0 && K <= 8192, IRODORI_ERR_SHAPE,
+                "gemm_fp8 requires M > 0, N % 64 == 0 and K % 128 == 0 (K <= 8192)");
+    GemmArgs<bf16> ga{};
+    ga.A8 = a8;
+    ga.As = a_scale;
+    ga.W8 = w8;
+    ga.ws = w_scale;
+    ga.M = M;
+    ga.N = N;
+    ga.K = K;
+    ga.C = c;
+    if (launch_gemm_fp8(EPI_STORE, ga, static_cast<hipStream_t>(stream))) {
+        set_last_error("gemm_fp8 launch rejected the shape");
+        return IRODORI_ERR_SHAPE;
+    }
+    return check_launch("gemm_fp8");
+    IRO_GUARD_END
+}
 
 int irodori_op_rms_norm(const float* x, const float* w, int rows, int dim, float eps, float* y, void* stream) {
     IRO_GUARD_BEGIN

@@ -40,13 +40,16 @@ void launch_fused_adaln_op(const float* x, const float* scale, const float* shif
 // h = x / sqrt(mean(x^2)+eps) * (1 + scale) + shift for (layer, kind) of the table.
 template <typename T>
 void launch_norm_mod(const float* x, T* h, int M, int S, int D, float eps, ModTable mt,
-                     int layer, int kind, hipStream_t st);
+                     int layer, int kind, hipStream_t st, uint8_t* q8 = nullptr,
+                     uint8_t* q8s = nullptr);
 // x[b] = x_src[b mod src_batches] @ in_w + in_b (in_proj), then h = norm_mod(x) for
-// (layer 0, attn); b is the batch row.
+// (layer 0, attn); b is the batch row.  h is nullable; q8 / q8s (nullable) receive the fp8
+// GEMM-operand form of h (e4m3 codes, E8M0 scales per 32 values; D % 32 == 0).
 template <typename T>
 void launch_inproj_norm(const float* x_src, int src_batches, const float* in_w,
                         const float* in_b, float* x, T* h, int M, int S, int P, int D,
-                        float eps, ModTable mt, hipStream_t st);
+                        float eps, ModTable mt, hipStream_t st, uint8_t* q8 = nullptr,
+                        uint8_t* q8s = nullptr);
 
 
 // One model evaluation of the RF sampler, as the update kernel applies it
@@ -195,9 +198,29 @@ struct GemmArgs {
     T* Ck;
     T* Cv;
     int key_off, ctx_stride, ctx_vstride;
+    // fp8 operands (launch_gemm_fp8): A8 [M, K] e4m3 with As [M, K/32] E8M0 block scales
+    // (power-of-two scale of row m, k block kb = 2^(As - 127)); W8 [N, K] e4m3 with f32
+    // per-output-channel scales ws [N].  C = (A8 * 2^As) @ W8^T * ws.
+    const uint8_t* A8;
+    const uint8_t* As;
+    const uint8_t* W8;
+    const float* ws;
+    // EPI_SWIGLU over fp8 operands: U in the fp8 GEMM-operand form (e4m3 codes U8 [M, N/2],
+    // E8M0 scales U8s [M, N/64]) for the next projection, instead of U.
+    uint8_t* U8;
+    uint8_t* U8s;
 };
 template <typename T>
 int launch_gemm(int epi, const GemmArgs<T>& a, hipStream_t st);
+// The same epilogues over fp8 operands (K % 128 == 0); outputs in bf16 / f32 as above.
+int launch_gemm_fp8(int epi, const GemmArgs<bf16>& a, hipStream_t st);
+
+// ---- kernels_fp8.hip -------------------------------------------------------------------
+// Weights w [N, K] f32 (K-major, K % 4 == 0) -> e4m3 codes q [N, K], channel scales s [N].
+void launch_quant_weight_rows(const float* w, int N, int K, uint8_t* q, float* s, hipStream_t st);
+// Activations x [M, K] (K % 32 == 0) -> e4m3 codes q [M, K], E8M0 block scales s [M, K/32].
+template <typename T>
+void launch_mx_quant_rows(const T* x, int M, int K, uint8_t* q, uint8_t* s, hipStream_t st);
 
 // ---- kernels_attn.hip ------------------------------------------------------------------
 template <typename T>
@@ -229,11 +252,15 @@ struct AttnArgs {
     // prescaled: Q already multiplied by scale * log2(e) (the QKV epilogue does this).
     bool prescaled;
     // epilogue: out_mode 0 -> O [B*Sq, H*Dh] (T) = gate[m, h*Dh+d] * attn;
-    //           out_mode 1 -> Of [B, H, Sq, Dh] f32
+    //           out_mode 1 -> Of [B, H, Sq, Dh] f32;
+    //           out_mode 2 -> the out_mode 0 values in the fp8 GEMM-operand form: e4m3
+    //           codes O8 [B*Sq, H*Dh] and E8M0 scales O8s [B*Sq, H*Dh/32] (bf16 kernel only)
     int out_mode;
     const T* G;
     T* O;
     float* Of;
+    uint8_t* O8;
+    uint8_t* O8s;
 };
 template <typename T, int DH>
 int launch_attention(const AttnArgs<T>& a, hipStream_t st);

@@ -339,6 +339,34 @@ __global__ __launch_bounds__(64 * QB * KVS) void attn32_kernel(AttnArgs<bf16> a,
     const int q = q0 + fr;
     if (q >= a.Sq) return;
     const size_t m = (size_t)b * a.Sq + q;
+    if (a.out_mode == 2) {
+        // fp8 operand form: head dims 32 db .. 32 db + 31 of query q are one scale block,
+        // split between this lane and lane ^ 32.
+        const size_t ob = m * (a.H * 64) + hh * 64;
+#pragma unroll
+        for (int db = 0; db < 2; db++) {
+            float gv[16];
+            float amax = 0.f;
+#pragma unroll
+            for (int g4 = 0; g4 < 4; g4++) {
+                const bf16x4 gt = *reinterpret_cast<const bf16x4*>(a.G + ob + 32 * db + 8 * g4 + 4 * fh);
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    gv[4 * g4 + c] = o[db][4 * g4 + c] * inv * static_cast<float>(gt[c]);
+                    amax = fmaxf(amax, fabsf(gv[4 * g4 + c]));
+                }
+            }
+            amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+            const int ex = mx_exp(amax);
+#pragma unroll
+            for (int g4 = 0; g4 < 4; g4++)
+                *reinterpret_cast<unsigned*>(a.O8 + ob + 32 * db + 8 * g4 + 4 * fh) =
+                    pack_e4m3(ldexpf(gv[4 * g4], -ex), ldexpf(gv[4 * g4 + 1], -ex), ldexpf(gv[4 * g4 + 2], -ex),
+                              ldexpf(gv[4 * g4 + 3], -ex));
+            if (fh == 0) a.O8s[m * (a.H * 2) + hh * 2 + db] = (uint8_t)(127 + ex);
+        }
+        return;
+    }
 #pragma unroll
     for (int db = 0; db < 2; db++)
 #pragma unroll

@@ -89,6 +89,27 @@ __device__ __forceinline__ Frag32<float> read_frag<float>(const unsigned char* s
     return f;
 }
 
+// fp8 fragment of one 32x32x64 step: 32 bytes per lane, k = 16*(lane/32) + 0..15 (the
+// first 32-wide scale block) and 32 + 16*(lane/32) + 0..15 (the second), i.e. 16-byte
+// chunks 4*ks + h and 4*ks + 2 + h of the 128-byte row.  The E8M0 scale of row r, block b
+// is supplied by lane r + 32 b.
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+struct Frag8 {
+    i32x8 v;
+};
+__device__ __forceinline__ Frag8 read_frag8(const unsigned char* st, int r, int ks, int h) {
+    const int4 lo = *reinterpret_cast<const int4*>(st + r * 128 + (swz(r, 4 * ks + h) << 4));
+    const int4 hi = *reinterpret_cast<const int4*>(st + r * 128 + (swz(r, 4 * ks + 2 + h) << 4));
+    Frag8 f;
+    f.v[0] = lo.x; f.v[1] = lo.y; f.v[2] = lo.z; f.v[3] = lo.w;
+    f.v[4] = hi.x; f.v[5] = hi.y; f.v[6] = hi.z; f.v[7] = hi.w;
+    return f;
+}
+__device__ __forceinline__ void mma8(f32x16& acc, const Frag8& a, const Frag8& b, int scale_a) {
+    // cbsz = blgp = 0: both operands e4m3; B's block scale is 2^0 (E8M0 127).
+    acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a.v, b.v, acc, 0, 0, 0, scale_a, 0, 127);
+}
+
 // Sum over the 32 lanes of each half-wave (lanes 0-31 and 32-63 separately): DPP
 // rotations within 16-lane rows, then v_permlane16_swap, which exchanges the odd 16-lane
 // rows of one operand with the even rows of the other.  With both operands equal to v the
@@ -104,6 +125,16 @@ __device__ __forceinline__ float half_wave_sum(float v) {
     const unsigned u = __builtin_bit_cast(unsigned, v);
     const auto sw = __builtin_amdgcn_permlane16_swap(u, u, false, false);
     return __builtin_bit_cast(float, (unsigned)sw[0]) + __builtin_bit_cast(float, (unsigned)sw[1]);
+}
+// The same reduction with max.
+__device__ __forceinline__ float half_wave_max(float v) {
+    v = fmaxf(v, IRO_DPP(v, 0x128));  // row_ror:8
+    v = fmaxf(v, IRO_DPP(v, 0x124));  // row_ror:4
+    v = fmaxf(v, IRO_DPP(v, 0x4E));  // quad_perm [2,3,0,1]
+    v = fmaxf(v, IRO_DPP(v, 0xB1));  // quad_perm [1,0,3,2]
+    const unsigned u = __builtin_bit_cast(unsigned, v);
+    const auto sw = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return fmaxf(__builtin_bit_cast(float, (unsigned)sw[0]), __builtin_bit_cast(float, (unsigned)sw[1]));
 }
 
 // Staged bf16 wave tile of the QKVG epilogue: row r (< 64) of 64 columns lives at
@@ -121,7 +152,7 @@ __device__ __forceinline__ const float* gate_vec(const ModTable& mt, int b, int 
     return mt.tab + ((size_t)vec * mt.layers * 6 + (size_t)layer * 6 + kind * 3 + 2) * D;
 }
 
-template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int EPI>
+template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int EPI, bool F8 = false>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T> a) {
     constexpr int NW = WAVES_M * WAVES_N;
     constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
@@ -129,8 +160,10 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
     constexpr int ROWS = BM + BN;
     constexpr int LPW = ROWS / 8 / NW;  // load instructions per wave per slice
     constexpr int STAGE_BYTES = ROWS * 128;
-    constexpr int BK = 128 / sizeof(T);  // elements per slice
-    constexpr int KS = BK / 16;          // k16 steps per slice
+    constexpr int ES = F8 ? 1 : (int)sizeof(T);  // operand element bytes
+    constexpr int BK = 128 / ES;                  // elements per slice
+    constexpr int KS = BK / (F8 ? 64 : 16);       // MFMA k-steps per slice
+    static_assert(!F8 || sizeof(T) == 2, "fp8 operands produce bf16 / f32 outputs");
     static_assert(LPW * 8 * NW == ROWS, "rows per slice must split over the waves");
     static_assert(FM * 32 == WM && FN * 32 == WN, "wave tiles are whole 32x32 blocks");
     static_assert(BM % 8 == 0, "a load instruction covers A rows or W rows, not both");
@@ -152,14 +185,30 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
     // swz(r, lane % 8).  One SGPR resource per operand tile; A rows past M fall outside
     // the A resource and read as zero.  The slice offset kt * 128 bytes rides in soffset.
     const int mrows = a.M - m0 < BM ? a.M - m0 : BM;
-    const __amdgpu_buffer_rsrc_t rA = make_rsrc(a.A + (size_t)m0 * K, (unsigned)(mrows * K * sizeof(T)));
-    const __amdgpu_buffer_rsrc_t rW = make_rsrc(a.W + (size_t)n0 * K, (unsigned)(BN * K * sizeof(T)));
+    const unsigned char* Ab = F8 ? a.A8 : reinterpret_cast<const unsigned char*>(a.A);
+    const unsigned char* Wb = F8 ? a.W8 : reinterpret_cast<const unsigned char*>(a.W);
+    const __amdgpu_buffer_rsrc_t rA = make_rsrc(Ab + (size_t)m0 * K * ES, (unsigned)(mrows * K * ES));
+    const __amdgpu_buffer_rsrc_t rW = make_rsrc(Wb + (size_t)n0 * K * ES, (unsigned)(BN * K * ES));
     unsigned voff[LPW];
 #pragma unroll
     for (int i = 0; i < LPW; i++) {
         const int r = (wave * LPW + i) * 8 + lane / 8;
         const int rr = r < BM ? r : r - BM;
-        voff[i] = (unsigned)rr * (unsigned)(K * sizeof(T)) + (unsigned)swz(r, lane % 8) * 16u;
+        voff[i] = (unsigned)rr * (unsigned)(K * ES) + (unsigned)swz(r, lane % 8) * 16u;
+    }
+    // fp8: the tile's E8M0 block scales (BM rows x K/32 bytes) are staged in LDS past the
+    // operand stages before the main loop; rows past M read as 127 (2^0) over zero codes.
+    [[maybe_unused]] const int kb = K / 32;
+    [[maybe_unused]] unsigned char* sc_lds = smem + STAGES * STAGE_BYTES;
+    if constexpr (F8) {
+        const int words = BM * (kb / 4);
+        for (int idx = threadIdx.x; idx < words; idx += 64 * NW) {
+            const int r = idx / (kb / 4), c4 = idx % (kb / 4);
+            unsigned w = 0x7f7f7f7fu;
+            if (m0 + r < a.M) w = *reinterpret_cast<const unsigned*>(a.As + (size_t)(m0 + r) * kb + 4 * c4);
+            *reinterpret_cast<unsigned*>(sc_lds + r * kb + 4 * c4) = w;
+        }
+        __syncthreads();
     }
 #define GEMM_ISSUE(kt_, stage_)                                                            \
     do {                                                                                   \
@@ -233,6 +282,27 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
         raw_barrier();
         if (kt + STAGES - 1 < nk) GEMM_ISSUE(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
         const unsigned char* st = smem + (kt % STAGES) * STAGE_BYTES;
+        if constexpr (F8) {
+            // Scale bytes of this lane's rows for the slice's four k blocks.
+            unsigned scw[FM];
+#pragma unroll
+            for (int i = 0; i < FM; i++) scw[i] = *reinterpret_cast<const unsigned*>(sc_lds + (wm0 + 32 * i + fr) * kb + 4 * kt);
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) {
+                Frag8 af8[FM], bf8[FN];
+#pragma unroll
+                for (int i = 0; i < FM; i++) af8[i] = read_frag8(st, wm0 + 32 * i + fr, ks, fh);
+#pragma unroll
+                for (int j = 0; j < FN; j++) bf8[j] = read_frag8(st, BM + wn0 + 32 * j + fr, ks, fh);
+#pragma unroll
+                for (int i = 0; i < FM; i++) {
+                    const int sa = (int)((scw[i] >> (8 * (2 * ks + fh))) & 0xffu);
+#pragma unroll
+                    for (int j = 0; j < FN; j++) mma8(acc[i][j], af8[i], bf8[j], sa);
+                }
+            }
+            continue;
+        }
         // Fragments double-buffered in registers: the LDS reads of k16 step ks + 1 are
         // issued ahead of the MFMAs of step ks, so their latency hides behind FM*FN MFMAs.
         Frag32<T> af[2][FM], bfr[2][FN];
@@ -261,6 +331,17 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
         }
     }
 #undef GEMM_ISSUE
+
+    if constexpr (F8) {  // per-output-channel weight scales
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+            const float wsv = a.ws[n0 + wn0 + 32 * j + cl];
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) acc[i][j][e] *= wsv;
+        }
+    }
 
     // ---- epilogues (acc layout: see rbase / cl above).
     if constexpr (EPI == EPI_STORE) {
@@ -308,6 +389,26 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
         // W rows come in 32-row groups alternating W1 / W3 columns: block j even holds
         // u1 and block j+1 the matching u3 for output columns 32 * pair + lane % 32.
         const int half_n = a.N / 2;
+        if constexpr (F8) {
+            // fp8 output: a pair's 32 columns of a row are one scale block of the next
+            // projection's input; its max is a half-wave reduction (all lanes take part).
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const int row = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
+#pragma unroll
+                    for (int j = 0; j < FN; j += 2) {
+                        const int pair = (n0 + wn0) / 64 + j / 2;
+                        const float m = silu_f(acc[i][j][e]) * acc[i][j + 1][e];
+                        const int ex = mx_exp(half_wave_max(fabsf(m)));
+                        if (row >= a.M) continue;
+                        const unsigned code = (unsigned)__builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(m, -ex), 0.f, 0, false);
+                        a.U8[(size_t)row * half_n + pair * 32 + cl] = (uint8_t)(code & 0xffu);
+                        if (cl == 0) a.U8s[(size_t)row * (half_n / 32) + pair] = (uint8_t)(127 + ex);
+                    }
+                }
+        } else {
 #pragma unroll
         for (int i = 0; i < FM; i++)
 #pragma unroll
@@ -321,6 +422,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
                     a.U[(size_t)row * half_n + pair * 32 + cl] = from_f32<T>(silu_f(u1) * u3);
                 }
             }
+        }
     } else if constexpr (EPI == EPI_CTXKV) {
         // One 64-column head per wave: region 0 = K (head RMSNorm, norm.rs:60-74, no RoPE),
         // region 1 = V (transposed scatter).  A setup-path epilogue: element stores.
@@ -536,21 +638,24 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
     }
 }
 
-template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int EPI>
+template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int EPI, bool F8 = false>
 int launch_cfg(const GemmArgs<T>& a, hipStream_t st) {
-    constexpr int BK = 128 / sizeof(T);
-    if (a.M <= 0 || a.N % BN != 0 || a.K % BK != 0 || a.K <= 0) return -1;
-    if ((size_t)BN * a.K * sizeof(T) > 0xffffffffull || (size_t)BM * a.K * sizeof(T) > 0xffffffffull) return -1;
+    constexpr int ES = F8 ? 1 : (int)sizeof(T);
+    constexpr int BK = 128 / ES;
+    constexpr int kMaxK8 = 8192;  // fp8: the staged block scales take BM * K / 32 bytes of LDS
+    if (a.M <= 0 || a.N % BN != 0 || a.K % BK != 0 || a.K <= 0 || (F8 && a.K > kMaxK8)) return -1;
+    if ((size_t)BN * a.K * ES > 0xffffffffull || (size_t)BM * a.K * ES > 0xffffffffull) return -1;
     int tiles = ((a.M + BM - 1) / BM) * (a.N / BN);
-    size_t lds = (size_t)STAGES * (BM + BN) * 128;
+    const size_t lds = (size_t)STAGES * (BM + BN) * 128 + (F8 ? (size_t)BM * (a.K / 32) : 0);
     static bool attr_set = false;  // per instantiation; the attribute is process-wide
     if (!attr_set) {
-        if (hipFuncSetAttribute((const void*)gemm_kernel<T, BM, BN, WAVES_M, WAVES_N, STAGES, EPI>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+        const int lds_max = STAGES * (BM + BN) * 128 + (F8 ? BM * (kMaxK8 / 32) : 0);
+        if (hipFuncSetAttribute((const void*)gemm_kernel<T, BM, BN, WAVES_M, WAVES_N, STAGES, EPI, F8>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, lds_max) != hipSuccess)
             return -2;
         attr_set = true;
     }
-    gemm_kernel<T, BM, BN, WAVES_M, WAVES_N, STAGES, EPI><<<tiles, 64 * WAVES_M * WAVES_N, lds, st>>>(a);
+    gemm_kernel<T, BM, BN, WAVES_M, WAVES_N, STAGES, EPI, F8><<<tiles, 64 * WAVES_M * WAVES_N, lds, st>>>(a);
     return 0;
 }
 
@@ -585,6 +690,22 @@ int launch_gemm(int epi, const GemmArgs<T>& a, hipStream_t st) {
         case EPI_CTXKV:
             if (a.N != 2 * a.H * 64) return -1;
             return launch_cfg<T, 128, 128, 2, 2, 2, EPI_CTXKV>(a, st);
+    }
+    return -1;
+}
+
+// fp8 operands: the same tile choices; each 128-byte slice holds 128 k values.
+int launch_gemm_fp8(int epi, const GemmArgs<bf16>& a, hipStream_t st) {
+    if (!a.A8 || !a.As || !a.W8 || !a.ws || a.K % 128 != 0) return -1;
+    switch (epi) {
+        case EPI_STORE:
+            if (wide_enough(a)) return launch_cfg<bf16, 128, 128, 2, 2, 2, EPI_STORE, true>(a, st);
+            return launch_cfg<bf16, 64, 64, 2, 2, 4, EPI_STORE, true>(a, st);
+        case EPI_RESID:
+            if (wide_enough(a)) return launch_cfg<bf16, 128, 128, 2, 2, 2, EPI_RESID, true>(a, st);
+            return launch_cfg<bf16, 64, 64, 2, 2, 4, EPI_RESID, true>(a, st);
+        case EPI_SWIGLU: return launch_cfg<bf16, 128, 128, 2, 2, 2, EPI_SWIGLU, true>(a, st);
+        case EPI_QKVG: return launch_cfg<bf16, 128, 128, 2, 2, 2, EPI_QKVG, true>(a, st);
     }
     return -1;
 }

@@ -67,12 +67,14 @@ __global__ __launch_bounds__(256) void fused_adaln_op_kernel(
 }
 
 // Model adaLN modulation: h = x / rms * (1 + scale) + shift (norm.rs:160-169).
-// D % 4 == 0; each lane owns float4 chunks lane*4 + 256*j.
+// D % 4 == 0; each lane owns float4 chunks lane*4 + 256*j.  h (nullable) gets the values in
+// the compute dtype; q8 / q8s (nullable, D % 32 == 0) their fp8 GEMM-operand form.
 template <typename T, int NCH>
 __global__ __launch_bounds__(256) void norm_mod_kernel(const float* __restrict__ x,
                                                        T* __restrict__ h, int M, int S, int D,
                                                        float eps, ModTable mt, int layer,
-                                                       int kind) {
+                                                       int kind, uint8_t* __restrict__ q8,
+                                                       uint8_t* __restrict__ q8s) {
     int row = blockIdx.x * kRowsPerBlock + threadIdx.x / 64, lane = threadIdx.x % 64;
     if (row >= M) return;
     const float* xr = x + (size_t)row * D;
@@ -95,9 +97,10 @@ __global__ __launch_bounds__(256) void norm_mod_kernel(const float* __restrict__
         if (d >= D) break;
         float4 sc = *reinterpret_cast<const float4*>(scale + d);
         float4 sh = *reinterpret_cast<const float4*>(shift + d);
-        store4<T>(h + (size_t)row * D + d, v[j].x / rms * (1.f + sc.x) + sh.x,
-                  v[j].y / rms * (1.f + sc.y) + sh.y, v[j].z / rms * (1.f + sc.z) + sh.z,
-                  v[j].w / rms * (1.f + sc.w) + sh.w);
+        const float h0 = v[j].x / rms * (1.f + sc.x) + sh.x, h1 = v[j].y / rms * (1.f + sc.y) + sh.y;
+        const float h2 = v[j].z / rms * (1.f + sc.z) + sh.z, h3 = v[j].w / rms * (1.f + sc.w) + sh.w;
+        if (h) store4<T>(h + (size_t)row * D + d, h0, h1, h2, h3);
+        if (q8) mx_store4_group8(h0, h1, h2, h3, q8 + (size_t)row * D + d, q8s + (size_t)row * (D / 32) + d / 32, lane);
     }
 }
 
@@ -113,7 +116,7 @@ template <typename T, int NCH>
 __global__ __launch_bounds__(256) void inproj_norm_kernel(
     const float* __restrict__ x_src, int src_batches, const float* __restrict__ in_w,
     const float* __restrict__ in_b, float* __restrict__ x, T* __restrict__ h, int M, int S, int P,
-    int D, float eps, ModTable mt) {
+    int D, float eps, ModTable mt, uint8_t* __restrict__ q8, uint8_t* __restrict__ q8s) {
     __shared__ float xs[kInRows][64];
     __shared__ float red[kInRows][4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -196,8 +199,10 @@ __global__ __launch_bounds__(256) void inproj_norm_kernel(
             const float4 sc = *reinterpret_cast<const float4*>(scale + d);
             const float4 sh = *reinterpret_cast<const float4*>(shift + d);
             const float4 v = acc[r][j];
-            store4<T>(h + (size_t)row * D + d, v.x / rms * (1.f + sc.x) + sh.x, v.y / rms * (1.f + sc.y) + sh.y,
-                      v.z / rms * (1.f + sc.z) + sh.z, v.w / rms * (1.f + sc.w) + sh.w);
+            const float h0 = v.x / rms * (1.f + sc.x) + sh.x, h1 = v.y / rms * (1.f + sc.y) + sh.y;
+            const float h2 = v.z / rms * (1.f + sc.z) + sh.z, h3 = v.w / rms * (1.f + sc.w) + sh.w;
+            if (h) store4<T>(h + (size_t)row * D + d, h0, h1, h2, h3);
+            if (q8) mx_store4_group8(h0, h1, h2, h3, q8 + (size_t)row * D + d, q8s + (size_t)row * (D / 32) + d / 32, lane);
         }
     }
 }
@@ -343,28 +348,28 @@ void launch_fused_adaln_op(const float* x, const float* scale, const float* shif
 
 template <typename T>
 void launch_norm_mod(const float* x, T* h, int M, int S, int D, float eps, ModTable mt,
-                     int layer, int kind, hipStream_t st) {
+                     int layer, int kind, hipStream_t st, uint8_t* q8, uint8_t* q8s) {
     int grid = (M + kRowsPerBlock - 1) / kRowsPerBlock;
     int nch = (D + 255) / 256;
     if (nch <= 1)
-        norm_mod_kernel<T, 1><<<grid, 256, 0, st>>>(x, h, M, S, D, eps, mt, layer, kind);
+        norm_mod_kernel<T, 1><<<grid, 256, 0, st>>>(x, h, M, S, D, eps, mt, layer, kind, q8, q8s);
     else if (nch <= 2)
-        norm_mod_kernel<T, 2><<<grid, 256, 0, st>>>(x, h, M, S, D, eps, mt, layer, kind);
+        norm_mod_kernel<T, 2><<<grid, 256, 0, st>>>(x, h, M, S, D, eps, mt, layer, kind, q8, q8s);
     else if (nch <= 4)
-        norm_mod_kernel<T, 4><<<grid, 256, 0, st>>>(x, h, M, S, D, eps, mt, layer, kind);
+        norm_mod_kernel<T, 4><<<grid, 256, 0, st>>>(x, h, M, S, D, eps, mt, layer, kind, q8, q8s);
     else
-        norm_mod_kernel<T, 8><<<grid, 256, 0, st>>>(x, h, M, S, D, eps, mt, layer, kind);
+        norm_mod_kernel<T, 8><<<grid, 256, 0, st>>>(x, h, M, S, D, eps, mt, layer, kind, q8, q8s);
 }
 
 template <typename T>
 void launch_inproj_norm(const float* x_src, int src_batches, const float* in_w,
                         const float* in_b, float* x, T* h, int M, int S, int P, int D, float eps,
-                        ModTable mt, hipStream_t st) {
+                        ModTable mt, hipStream_t st, uint8_t* q8, uint8_t* q8s) {
     int grid = (M + kInRows - 1) / kInRows;
     int nch = (D + 1023) / 1024;
 #define IRO_INPROJ(N)                                                                      \
     inproj_norm_kernel<T, N><<<grid, 256, 0, st>>>(x_src, src_batches, in_w, in_b, x, h, M, \
-                                                   S, P, D, eps, mt)
+                                                   S, P, D, eps, mt, q8, q8s)
     if (nch <= 1) IRO_INPROJ(1);
     else if (nch <= 2) IRO_INPROJ(2);
     else IRO_INPROJ(4);
@@ -372,14 +377,15 @@ void launch_inproj_norm(const float* x_src, int src_batches, const float* in_w,
 }
 
 template void launch_norm_mod<float>(const float*, float*, int, int, int, float, ModTable, int,
-                                     int, hipStream_t);
+                                     int, hipStream_t, uint8_t*, uint8_t*);
 template void launch_norm_mod<bf16>(const float*, bf16*, int, int, int, float, ModTable, int,
-                                    int, hipStream_t);
+                                    int, hipStream_t, uint8_t*, uint8_t*);
 template void launch_inproj_norm<float>(const float*, int, const float*, const float*, float*,
                                         float*, int, int, int, int, float, ModTable,
-                                        hipStream_t);
+                                        hipStream_t, uint8_t*, uint8_t*);
 template void launch_inproj_norm<bf16>(const float*, int, const float*, const float*, float*,
-                                       bf16*, int, int, int, int, float, ModTable, hipStream_t);
+                                       bf16*, int, int, int, int, float, ModTable, hipStream_t,
+                                       uint8_t*, uint8_t*);
 
 template <int PT, int NR>
 static void launch_final_cfg(const FinalArgs& a, hipStream_t st) {

@@ -27,6 +27,7 @@ ERR_NAMES = {ERR_INVALID_ARG: "InvalidArg", ERR_SHAPE: "Shape", ERR_DTYPE: "Dtyp
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
+DTYPE_FP8 = 2
 CFG_INDEPENDENT, CFG_JOINT, CFG_ALTERNATING = 0, 1, 2
 METHOD_EULER, METHOD_HEUN, METHOD_PLMS4 = 0, 1, 2
 
@@ -117,6 +118,8 @@ SIGNATURES = {
                                          _vp, _vp]),
     "irodori_op_sdpa": (C.c_int, [C.c_int, _vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int,
                                   C.c_int, C.c_int, C.c_float, _vp, _vp]),
+    "irodori_op_mx_quantize": (C.c_int, [_vp, C.c_int, C.c_int, _vp, _vp, _vp]),
+    "irodori_op_gemm_fp8": (C.c_int, [_vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int, _vp, _vp]),
 }
 
 _lib = None

@@ -27,14 +27,17 @@ class InferenceBackendKind(enum.Enum):
 
     HIP_BF16 = "hip-bf16"
     HIP_F32 = "hip-f32"
+    # bf16 activations with the block GEMMs on e4m3 operands (no reference counterpart).
+    HIP_FP8 = "hip-fp8"
 
     @property
     def label(self) -> str:
-        return {"hip-bf16": "HIP bf16 (gfx950)", "hip-f32": "HIP f32 (gfx950)"}[self.value]
+        return {"hip-bf16": "HIP bf16 (gfx950)", "hip-f32": "HIP f32 (gfx950)",
+                "hip-fp8": "HIP fp8 GEMMs + bf16 (gfx950)"}[self.value]
 
     @property
     def is_reduced_precision(self) -> bool:
-        return self is InferenceBackendKind.HIP_BF16
+        return self is not InferenceBackendKind.HIP_F32
 
 
 class CfgGuidanceMode(enum.Enum):

@@ -79,7 +79,9 @@ class HipInferenceEngine:
         c = L.DitConfigC(cfg.latent_dim, cfg.model_dim, cfg.num_layers, cfg.num_heads,
                          cfg.head_dim, cfg.mlp_hidden, cfg.adaln_rank, cfg.timestep_embed_dim,
                          cfg.norm_eps, cfg.rope_theta,
-                         L.DTYPE_BF16 if backend is InferenceBackendKind.HIP_BF16 else L.DTYPE_F32,
+                         {InferenceBackendKind.HIP_BF16: L.DTYPE_BF16,
+                          InferenceBackendKind.HIP_F32: L.DTYPE_F32,
+                          InferenceBackendKind.HIP_FP8: L.DTYPE_FP8}[backend],
                          max_rows, max_seq, max_ctx)
         h = C.c_void_p()
         _check(self.lib.irodori_ctx_create(device, C.byref(c), C.byref(h)))
@@ -257,6 +259,14 @@ class ops:
     def fused_adaln(d_x, d_scale, d_shift, batch, seq, dim, eps, d_y, stream: int = 0) -> None:
         _check(L.load().irodori_op_fused_adaln(d_x, d_scale, d_shift, batch, seq, dim, eps, d_y,
                                                stream or None))
+
+    @staticmethod
+    def mx_quantize(d_x, rows, dim, d_q, d_s, stream: int = 0) -> None:
+        _check(L.load().irodori_op_mx_quantize(d_x, rows, dim, d_q, d_s, stream or None))
+
+    @staticmethod
+    def gemm_fp8(d_a, d_as, d_w, d_ws, M, N, K, d_c, stream: int = 0) -> None:
+        _check(L.load().irodori_op_gemm_fp8(d_a, d_as, d_w, d_ws, M, N, K, d_c, stream or None))
 
     @staticmethod
     def sdpa(dtype: int, d_q, d_k, d_v, d_mask, batch, heads, seq_q, seq_kv, head_dim, scale,
