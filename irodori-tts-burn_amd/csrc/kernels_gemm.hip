@@ -126,16 +126,6 @@ __device__ __forceinline__ float half_wave_sum(float v) {
     const auto sw = __builtin_amdgcn_permlane16_swap(u, u, false, false);
     return __builtin_bit_cast(float, (unsigned)sw[0]) + __builtin_bit_cast(float, (unsigned)sw[1]);
 }
-// The same reduction with max.
-__device__ __forceinline__ float half_wave_max(float v) {
-    v = fmaxf(v, IRO_DPP(v, 0x128));  // row_ror:8
-    v = fmaxf(v, IRO_DPP(v, 0x124));  // row_ror:4
-    v = fmaxf(v, IRO_DPP(v, 0x4E));  // quad_perm [2,3,0,1]
-    v = fmaxf(v, IRO_DPP(v, 0xB1));  // quad_perm [1,0,3,2]
-    const unsigned u = __builtin_bit_cast(unsigned, v);
-    const auto sw = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-    return fmaxf(__builtin_bit_cast(float, (unsigned)sw[0]), __builtin_bit_cast(float, (unsigned)sw[1]));
-}
 
 // Staged bf16 wave tile of the QKVG epilogue: row r (< 64) of 64 columns lives at
 // slot + 256 r, its 16-byte chunk c at chunk position c ^ (4 * ((r >> 2 ^ r) & 1)).  The
@@ -173,9 +163,17 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
     extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int tiles_m = (a.M + BM - 1) / BM;
+    // Tiles in groups of GM row tiles: consecutive ids (one XCD's, see xcd_remap) sweep
+    // the group's GM row tiles for one column tile, then the next column tile, so the
+    // workgroups an XCD runs together share GM A tiles and a few W tiles in its L2.  With
+    // at most GM row tiles this is the plain column-by-column order.
+    constexpr int GM = 8;
+    const int tiles_m = (a.M + BM - 1) / BM, tiles_n = a.N / BN;
     const int pid = xcd_remap(blockIdx.x, gridDim.x);
-    const int tile_m = pid % tiles_m, tile_n = pid / tiles_m;
+    const int per_group = GM * tiles_n, group = pid / per_group, first_m = group * GM;
+    const int gm = tiles_m - first_m < GM ? tiles_m - first_m : GM;
+    const int local = pid - group * per_group;
+    const int tile_m = first_m + local % gm, tile_n = local / gm;
     const int m0 = tile_m * BM, n0 = tile_n * BN;
     const int wm0 = (wave / WAVES_N) * WM, wn0 = (wave % WAVES_N) * WN;
     const int K = a.K;
@@ -197,16 +195,18 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
         voff[i] = (unsigned)rr * (unsigned)(K * ES) + (unsigned)swz(r, lane % 8) * 16u;
     }
     // fp8: the tile's E8M0 block scales (BM rows x K/32 bytes) are staged in LDS past the
-    // operand stages before the main loop; rows past M read as 127 (2^0) over zero codes.
+    // operand stages before the main loop, slice-major: the word of row r for slice kt (its
+    // four k blocks) at (kt * BM + r) * 4, so a wave's 32 rows read 32 consecutive words.
+    // Rows past M read as 127 (2^0) over zero codes.
     [[maybe_unused]] const int kb = K / 32;
     [[maybe_unused]] unsigned char* sc_lds = smem + STAGES * STAGE_BYTES;
     if constexpr (F8) {
         const int words = BM * (kb / 4);
         for (int idx = threadIdx.x; idx < words; idx += 64 * NW) {
-            const int r = idx / (kb / 4), c4 = idx % (kb / 4);
+            const int r = idx % BM, c4 = idx / BM;
             unsigned w = 0x7f7f7f7fu;
             if (m0 + r < a.M) w = *reinterpret_cast<const unsigned*>(a.As + (size_t)(m0 + r) * kb + 4 * c4);
-            *reinterpret_cast<unsigned*>(sc_lds + r * kb + 4 * c4) = w;
+            *reinterpret_cast<unsigned*>(sc_lds + (c4 * BM + r) * 4) = w;
         }
         __syncthreads();
     }
@@ -286,20 +286,32 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
             // Scale bytes of this lane's rows for the slice's four k blocks.
             unsigned scw[FM];
 #pragma unroll
-            for (int i = 0; i < FM; i++) scw[i] = *reinterpret_cast<const unsigned*>(sc_lds + (wm0 + 32 * i + fr) * kb + 4 * kt);
+            for (int i = 0; i < FM; i++) scw[i] = *reinterpret_cast<const unsigned*>(sc_lds + (kt * BM + wm0 + 32 * i + fr) * 4);
+            // Fragments double-buffered as in the bf16 loop: the reads of step ks + 1 go out
+            // ahead of the MFMAs of step ks (two 16-byte LDS reads per fragment).
+            Frag8 af8[2][FM], bf8[2][FN];
+#pragma unroll
+            for (int i = 0; i < FM; i++) af8[0][i] = read_frag8(st, wm0 + 32 * i + fr, 0, fh);
+#pragma unroll
+            for (int j = 0; j < FN; j++) bf8[0][j] = read_frag8(st, BM + wn0 + 32 * j + fr, 0, fh);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2 * (FM + FN), 0);
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) {
-                Frag8 af8[FM], bf8[FN];
+                const int cur = ks & 1, nxt = cur ^ 1;
+                if (ks + 1 < KS) {
 #pragma unroll
-                for (int i = 0; i < FM; i++) af8[i] = read_frag8(st, wm0 + 32 * i + fr, ks, fh);
+                    for (int i = 0; i < FM; i++) af8[nxt][i] = read_frag8(st, wm0 + 32 * i + fr, ks + 1, fh);
 #pragma unroll
-                for (int j = 0; j < FN; j++) bf8[j] = read_frag8(st, BM + wn0 + 32 * j + fr, ks, fh);
+                    for (int j = 0; j < FN; j++) bf8[nxt][j] = read_frag8(st, BM + wn0 + 32 * j + fr, ks + 1, fh);
+                }
 #pragma unroll
                 for (int i = 0; i < FM; i++) {
                     const int sa = (int)((scw[i] >> (8 * (2 * ks + fh))) & 0xffu);
 #pragma unroll
-                    for (int j = 0; j < FN; j++) mma8(acc[i][j], af8[i], bf8[j], sa);
+                    for (int j = 0; j < FN; j++) mma8(acc[i][j], af8[cur][i], bf8[cur][j], sa);
                 }
+                if (ks + 1 < KS) __builtin_amdgcn_sched_group_barrier(0x100, 2 * (FM + FN), 0);  // DS reads
+                __builtin_amdgcn_sched_group_barrier(0x008, FM * FN, 0);                         // MFMAs
             }
             continue;
         }
@@ -391,23 +403,50 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
         const int half_n = a.N / 2;
         if constexpr (F8) {
             // fp8 output: a pair's 32 columns of a row are one scale block of the next
-            // projection's input; its max is a half-wave reduction (all lanes take part).
+            // projection's input.  Each wave stages its WM x 32 block of m per pair in its own
+            // LDS slot (row stride 33 floats: both passes conflict-free); then lane r owns row
+            // r: the block max, the 32 codes as two 16-byte stores, and the scale byte.
+            static_assert(WM <= 64, "one staged row per lane");
+            constexpr int SLOT = WM * 33 * 4;
+            static_assert(STAGES * STAGE_BYTES >= NW * SLOT, "SwiGLU fp8 epilogue needs one LDS slot per wave");
+            __syncthreads();  // every wave is past its last read of the operand stages
+            float* slot = reinterpret_cast<float*>(smem + wave * SLOT);
 #pragma unroll
-            for (int i = 0; i < FM; i++)
+            for (int j = 0; j < FN; j += 2) {
+                const int pair = (n0 + wn0) / 64 + j / 2;
 #pragma unroll
-                for (int e = 0; e < 16; e++) {
-                    const int row = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
+                for (int i = 0; i < FM; i++)
 #pragma unroll
-                    for (int j = 0; j < FN; j += 2) {
-                        const int pair = (n0 + wn0) / 64 + j / 2;
-                        const float m = silu_f(acc[i][j][e]) * acc[i][j + 1][e];
-                        const int ex = mx_exp(half_wave_max(fabsf(m)));
-                        if (row >= a.M) continue;
-                        const unsigned code = (unsigned)__builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(m, -ex), 0.f, 0, false);
-                        a.U8[(size_t)row * half_n + pair * 32 + cl] = (uint8_t)(code & 0xffu);
-                        if (cl == 0) a.U8s[(size_t)row * (half_n / 32) + pair] = (uint8_t)(127 + ex);
+                    for (int e = 0; e < 16; e++) {
+                        const int r = 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+                        slot[r * 33 + cl] = silu_f(acc[i][j][e]) * acc[i][j + 1][e];
+                    }
+                __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's slot writes landed
+                __builtin_amdgcn_wave_barrier();
+                if (lane < WM) {
+                    float v[32];
+                    float amax = 0.f;
+#pragma unroll
+                    for (int c = 0; c < 32; c++) {
+                        v[c] = slot[lane * 33 + c];
+                        amax = fmaxf(amax, fabsf(v[c]));
+                    }
+                    const int ex = mx_exp(amax);
+                    const int row = m0 + wm0 + lane;
+                    if (row < a.M) {
+                        unsigned w[8];
+#pragma unroll
+                        for (int q = 0; q < 8; q++)
+                            w[q] = pack_e4m3(ldexpf(v[4 * q], -ex), ldexpf(v[4 * q + 1], -ex), ldexpf(v[4 * q + 2], -ex),
+                                             ldexpf(v[4 * q + 3], -ex));
+                        uint4* dst = reinterpret_cast<uint4*>(a.U8 + (size_t)row * half_n + pair * 32);
+                        dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
+                        dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+                        a.U8s[(size_t)row * (half_n / 32) + pair] = (uint8_t)(127 + ex);
                     }
                 }
+                __builtin_amdgcn_wave_barrier();  // the slot is rewritten by the next pair
+            }
         } else {
 #pragma unroll
         for (int i = 0; i < FM; i++)
