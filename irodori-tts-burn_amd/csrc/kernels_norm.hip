@@ -105,34 +105,33 @@ __global__ __launch_bounds__(256) void norm_mod_kernel(const float* __restrict__
 }
 
 // in_proj (x = x_src @ W_in + b_in, dit/model.rs:370) fused with the first adaLN.  A
-// 256-thread block owns kInRows rows; thread t owns the column quads 4 t + 1024 j (j <
+// 256-thread block owns ROWS rows (8, or 2 when that leaves too few blocks to fill the chip); thread t owns the column quads 4 t + 1024 j (j <
 // NCH) of every row, so each W_in quad is loaded once per block and applied to all its
-// rows (W_in stays in L2 and is streamed M / kInRows times).  The source rows are staged
+// rows (W_in stays in L2 and is streamed M / ROWS times).  The source rows are staged
 // in LDS 64 latent channels at a time; the row RMS reduces over lanes, then over the 4
 // wavefronts through LDS.
-constexpr int kInRows = 8;
 
-template <typename T, int NCH>
+template <typename T, int NCH, int ROWS>
 __global__ __launch_bounds__(256) void inproj_norm_kernel(
     const float* __restrict__ x_src, int src_batches, const float* __restrict__ in_w,
     const float* __restrict__ in_b, float* __restrict__ x, T* __restrict__ h, int M, int S, int P,
     int D, float eps, ModTable mt, uint8_t* __restrict__ q8, uint8_t* __restrict__ q8s) {
-    __shared__ float xs[kInRows][64];
-    __shared__ float red[kInRows][4];
+    __shared__ float xs[ROWS][64];
+    __shared__ float red[ROWS][4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int row0 = blockIdx.x * kInRows;
-    float4 acc[kInRows][NCH];
+    const int row0 = blockIdx.x * ROWS;
+    float4 acc[ROWS][NCH];
 #pragma unroll
     for (int j = 0; j < NCH; j++) {
         const int d = 4 * tid + 1024 * j;
         const float4 bv = d < D ? *reinterpret_cast<const float4*>(in_b + d) : make_float4(0, 0, 0, 0);
 #pragma unroll
-        for (int r = 0; r < kInRows; r++) acc[r][j] = bv;
+        for (int r = 0; r < ROWS; r++) acc[r][j] = bv;
     }
     for (int p0 = 0; p0 < P; p0 += 64) {
         const int pn = P - p0 < 64 ? P - p0 : 64;
         __syncthreads();
-        for (int e = tid; e < kInRows * 64; e += 256) {
+        for (int e = tid; e < ROWS * 64; e += 256) {
             const int r = e / 64, pp = e % 64, row = row0 + r;
             float v = 0.f;
             if (row < M && pp < pn) {
@@ -156,7 +155,7 @@ __global__ __launch_bounds__(256) void inproj_norm_kernel(
 #pragma unroll
                 for (int i = 0; i < 16; i++) {
 #pragma unroll
-                    for (int r = 0; r < kInRows; r++) {
+                    for (int r = 0; r < ROWS; r++) {
                         const float a = xs[r][(c0 + i) & 63];
                         acc[r][j].x += a * wv[i].x;
                         acc[r][j].y += a * wv[i].y;
@@ -169,7 +168,7 @@ __global__ __launch_bounds__(256) void inproj_norm_kernel(
     }
     // Store x and reduce the per-row sums of squares.
 #pragma unroll
-    for (int r = 0; r < kInRows; r++) {
+    for (int r = 0; r < ROWS; r++) {
         const int row = row0 + r;
         float ss = 0.f;
 #pragma unroll
@@ -185,7 +184,7 @@ __global__ __launch_bounds__(256) void inproj_norm_kernel(
     }
     __syncthreads();
 #pragma unroll
-    for (int r = 0; r < kInRows; r++) {
+    for (int r = 0; r < ROWS; r++) {
         const int row = row0 + r;
         if (row >= M) break;
         const float rms = sqrtf((red[r][0] + red[r][1] + red[r][2] + red[r][3]) / (float)D + eps);
@@ -207,7 +206,7 @@ __global__ __launch_bounds__(256) void inproj_norm_kernel(
     }
 }
 
-// Output head: one 256-thread block per kFinFrames latent frames and row group (NR rows;
+// Output head: one 256-thread block per FR latent frames and row group (NR rows;
 // blockIdx.y strides over the groups).  v[b,s,p] = (sum_d x[b,s,d] * W'[p,d]) /
 // rms(x[b,s,:]) + b_out[p] with W' = out_norm.weight (.) W_out^T folded at ingest — the
 // same product as out_proj(out_norm(x)) (norm.rs:25-39, dit/model.rs:391-392).  The group's
@@ -217,12 +216,10 @@ __global__ __launch_bounds__(256) void inproj_norm_kernel(
 // active roles' rows of utterance u, and the block applies the guided combine and the
 // integrator update to them (euler_sampler.rs:460-467, :497-510, :683-714) — one kernel
 // after the role chains join.
-constexpr int kFinFrames = 4;
-
-template <int PT, int NR>
+template <int PT, int NR, int FR>
 __global__ __launch_bounds__(256) void final_kernel(FinalArgs a) {
     constexpr int KS = 256 / PT;
-    constexpr int R = NR * kFinFrames;  // staged row slot f * NR + i
+    constexpr int R = NR * FR;  // staged row slot f * NR + i
     extern __shared__ __attribute__((aligned(16))) float fsm[];
     const int D = a.D, P = a.P;
     float* xs = fsm;                  // [R][D]
@@ -231,8 +228,8 @@ __global__ __launch_bounds__(256) void final_kernel(FinalArgs a) {
     float* rinv = vals + R * PT;      // [R]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int p = tid % PT, ks = tid / PT;
-    const int s0 = blockIdx.x * kFinFrames;
-    const int nf = a.S - s0 < kFinFrames ? a.S - s0 : kFinFrames;
+    const int s0 = blockIdx.x * FR;
+    const int nf = a.S - s0 < FR ? a.S - s0 : FR;
     const int kper = D / KS;
     const bool rf = a.rf.plan != nullptr;
     int step = 0;
@@ -365,14 +362,21 @@ template <typename T>
 void launch_inproj_norm(const float* x_src, int src_batches, const float* in_w,
                         const float* in_b, float* x, T* h, int M, int S, int P, int D, float eps,
                         ModTable mt, hipStream_t st, uint8_t* q8, uint8_t* q8s) {
-    int grid = (M + kInRows - 1) / kInRows;
-    int nch = (D + 1023) / 1024;
-#define IRO_INPROJ(N)                                                                      \
-    inproj_norm_kernel<T, N><<<grid, 256, 0, st>>>(x_src, src_batches, in_w, in_b, x, h, M, \
-                                                   S, P, D, eps, mt, q8, q8s)
-    if (nch <= 1) IRO_INPROJ(1);
-    else if (nch <= 2) IRO_INPROJ(2);
-    else IRO_INPROJ(4);
+    const int nch = (D + 1023) / 1024;
+    const bool fine = (M + 7) / 8 < 512;  // fewer than two blocks per CU at 8 rows
+    const int rows = fine ? 2 : 8, grid = (M + rows - 1) / rows;
+#define IRO_INPROJ(N, R)                                                                      \
+    inproj_norm_kernel<T, N, R><<<grid, 256, 0, st>>>(x_src, src_batches, in_w, in_b, x, h, M, \
+                                                      S, P, D, eps, mt, q8, q8s)
+    if (fine) {
+        if (nch <= 1) IRO_INPROJ(1, 2);
+        else if (nch <= 2) IRO_INPROJ(2, 2);
+        else IRO_INPROJ(4, 2);
+    } else {
+        if (nch <= 1) IRO_INPROJ(1, 8);
+        else if (nch <= 2) IRO_INPROJ(2, 8);
+        else IRO_INPROJ(4, 8);
+    }
 #undef IRO_INPROJ
 }
 
@@ -387,28 +391,37 @@ template void launch_inproj_norm<bf16>(const float*, int, const float*, const fl
                                        bf16*, int, int, int, int, float, ModTable, hipStream_t,
                                        uint8_t*, uint8_t*);
 
-template <int PT, int NR>
+template <int PT, int NR, int FR>
 static void launch_final_cfg(const FinalArgs& a, hipStream_t st) {
-    constexpr int KS = 256 / PT, R = NR * kFinFrames;
+    constexpr int KS = 256 / PT, R = NR * FR;
     const size_t lds = sizeof(float) * ((size_t)R * a.D + (size_t)KS * R * PT + (size_t)R * PT + R);
     static bool attr_set = false;
     if (!attr_set) {
         // Sized for the largest model width the context accepts (D <= 2048).
         constexpr int kMax = (int)sizeof(float) * (R * 2048 + KS * R * PT + R * PT + R);
-        (void)hipFuncSetAttribute((const void*)final_kernel<PT, NR>, hipFuncAttributeMaxDynamicSharedMemorySize, kMax);
+        (void)hipFuncSetAttribute((const void*)final_kernel<PT, NR, FR>, hipFuncAttributeMaxDynamicSharedMemorySize, kMax);
         attr_set = true;
     }
     const int ngroups = a.rf.plan ? a.B : (a.B + NR - 1) / NR;
-    const dim3 grid((a.S + kFinFrames - 1) / kFinFrames, ngroups < 65535 ? ngroups : 65535);
-    final_kernel<PT, NR><<<grid, 256, lds, st>>>(a);
+    const dim3 grid((a.S + FR - 1) / FR, ngroups < 65535 ? ngroups : 65535);
+    final_kernel<PT, NR, FR><<<grid, 256, lds, st>>>(a);
 }
 
+// Four frames per block, or one when that leaves too few blocks to fill the chip (each
+// block re-reads W' from L2, so coarser blocks win once there are enough of them).
+template <int PT, int FR>
+static void launch_final_fr(const FinalArgs& a, hipStream_t st) {
+    const int nr = a.rf.plan ? a.nrole : 2;
+    if (nr <= 1) launch_final_cfg<PT, 1, FR>(a, st);
+    else if (nr == 2) launch_final_cfg<PT, 2, FR>(a, st);
+    else launch_final_cfg<PT, 3, FR>(a, st);
+}
 template <int PT>
 static void launch_final_pt(const FinalArgs& a, hipStream_t st) {
     const int nr = a.rf.plan ? a.nrole : 2;
-    if (nr <= 1) launch_final_cfg<PT, 1>(a, st);
-    else if (nr == 2) launch_final_cfg<PT, 2>(a, st);
-    else launch_final_cfg<PT, 3>(a, st);
+    const int ngroups = a.rf.plan ? a.B : (a.B + nr - 1) / nr;
+    if ((long)((a.S + 3) / 4) * ngroups < 512) launch_final_fr<PT, 1>(a, st);
+    else launch_final_fr<PT, 4>(a, st);
 }
 
 void launch_final(const FinalArgs& a, hipStream_t st) {
