@@ -4,12 +4,13 @@ Host-side mirror of the reference's inference API for the HIP backend:
 `InferenceBackendKind.HIP_BF16 / HIP_F32`, `SamplerParams`, `GuidanceConfig`, and
 `HipInferenceEngine` (forward_with_cond_cached / sample over libirodori_hip.so).
 """
-from .config import (CfgGuidanceMode, DitConfig, GuidanceConfig, InferenceBackendKind,
-                     IrodoriError, SamplerMethod, SamplerParams, cfg_cpu_plumbing, cfg_full_rf,
-                     cfg_tiny)
+from .config import (CfgGuidanceMode, DitConfig, EncoderConfig, GuidanceConfig,
+                     InferenceBackendKind, IrodoriError, SamplerMethod, SamplerParams,
+                     cfg_cpu_plumbing, cfg_full_rf, cfg_tiny, enc_speaker_default,
+                     enc_speaker_tiny, enc_text_default, enc_text_tiny)
 from .engine import HipInferenceEngine, ops
 from .synthetic import (ROLE_COND, ROLE_NO_AUX, ROLE_NO_TEXT, ROLE_UNCOND, ContextKV,
-                        CtxProjWeights, DitWeights, make_context_kv, make_noise,
+                        CtxProjWeights, DitWeights, EncoderWeights, make_context_kv, make_noise,
                         make_role_context)
 
 __all__ = [
@@ -17,4 +18,6 @@ __all__ = [
     "SamplerMethod", "SamplerParams", "cfg_cpu_plumbing", "cfg_full_rf", "cfg_tiny",
     "HipInferenceEngine", "ops", "ContextKV", "CtxProjWeights", "DitWeights", "make_context_kv", "make_noise",
     "make_role_context", "ROLE_COND", "ROLE_UNCOND", "ROLE_NO_TEXT", "ROLE_NO_AUX",
+    "EncoderConfig", "EncoderWeights", "enc_text_default", "enc_speaker_default", "enc_text_tiny",
+    "enc_speaker_tiny",
 ]

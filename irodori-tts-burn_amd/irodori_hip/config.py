@@ -101,6 +101,51 @@ def cfg_tiny() -> DitConfig:
 
 
 @dataclass
+class EncoderConfig:
+    """A condition encoder and its conditioner norm: TextEncoder (text / caption,
+    text_encoder.rs:64-148) when vocab_size > 0, ReferenceLatentEncoder (speaker,
+    speaker_encoder.rs:85-162) when in_dim > 0; TextBlocks of width dim, num_heads heads of
+    dim / num_heads (64 or 128), SwiGLU hidden floor(dim * mlp_ratio) (text_encoder.rs:36).
+    mean_token: prepend the speaker conditioner's masked-mean token
+    (aux_conditioner.rs:150-185)."""
+
+    dim: int
+    num_layers: int
+    num_heads: int
+    mlp_hidden: int
+    norm_eps: float = 1e-5
+    vocab_size: int = 0
+    in_dim: int = 0
+    mean_token: bool = False
+
+    @property
+    def head_dim(self) -> int:
+        return self.dim // self.num_heads
+
+
+def enc_text_default() -> EncoderConfig:
+    """The reference's default text encoder (config/model.rs:46-80): 1280 wide, 14 layers,
+    10 heads, mlp ratio 2.6, vocab 102400."""
+    return EncoderConfig(dim=1280, num_layers=14, num_heads=10, mlp_hidden=int(1280 * 2.6),
+                         vocab_size=102400)
+
+
+def enc_speaker_default(latent_dim: int = 32) -> EncoderConfig:
+    """The default speaker encoder over latent_dim-channel reference latents (patch 1)."""
+    return EncoderConfig(dim=1280, num_layers=14, num_heads=10, mlp_hidden=int(1280 * 2.6),
+                         in_dim=latent_dim, mean_token=True)
+
+
+def enc_text_tiny() -> EncoderConfig:
+    return EncoderConfig(dim=256, num_layers=2, num_heads=2, mlp_hidden=640, vocab_size=1000)
+
+
+def enc_speaker_tiny() -> EncoderConfig:
+    return EncoderConfig(dim=256, num_layers=2, num_heads=4, mlp_hidden=640, in_dim=32,
+                         mean_token=True)
+
+
+@dataclass
 class GuidanceConfig:
     """src/rf/params.rs:9-35 (defaults :23-34)."""
 

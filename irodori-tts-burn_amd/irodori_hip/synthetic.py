@@ -83,6 +83,39 @@ class DitWeights:
 
 
 @dataclass
+class EncoderWeights:
+    """Weights of a condition encoder (EncoderConfig), Burn [d_in, d_out] layouts:
+    io: embedding [vocab, E] (token input) or in_w [in_dim, E] + in_b [E] (latent input),
+    out_norm [E] (the conditioner norm); blocks: per TextBlock attn_norm, wq / wk / wv
+    [E, E], wo [E, E], w_gate [E, E], q_norm / k_norm [H, Dh], mlp_norm, w13 [E, 2F] =
+    [W1 | W3], w2 [F, E]."""
+
+    io: dict
+    blocks: list
+
+    @staticmethod
+    def random(cfg, seed: int = 0, std: float = 0.02, norm_jitter: float = 0.0) -> "EncoderWeights":
+        d = _Draw(seed, std, norm_jitter)
+        E, F, H, Dh = cfg.dim, cfg.mlp_hidden, cfg.num_heads, cfg.head_dim
+        io = {}
+        if cfg.vocab_size:
+            io["embedding"] = d.rng.standard_normal((cfg.vocab_size, E), dtype=np.float32)
+        if cfg.in_dim:
+            io["in_w"] = d.lin(cfg.in_dim, E)
+            io["in_b"] = d.lin(E)
+        io["out_norm"] = d.norm(E)
+        blocks = []
+        for _ in range(cfg.num_layers):
+            blocks.append({
+                "attn_norm": d.norm(E), "wq": d.lin(E, E), "wk": d.lin(E, E), "wv": d.lin(E, E),
+                "wo": d.lin(E, E), "w_gate": d.lin(E, E), "q_norm": d.norm(H, Dh),
+                "k_norm": d.norm(H, Dh), "mlp_norm": d.norm(E), "w13": d.lin(E, 2 * F),
+                "w2": d.lin(F, E),
+            })
+        return EncoderWeights(io, blocks)
+
+
+@dataclass
 class CtxProjWeights:
     """Per-layer context projections of JointAttention (attention.rs:142-147): wk_text /
     wv_text [text_dim, H*Dh] and, when aux_dim > 0, wk_aux / wv_aux [aux_dim, H*Dh] (the

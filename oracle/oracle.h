@@ -90,6 +90,32 @@ typedef struct orc_sampler {
     int32_t ctx_aux_start;  /* first aux (speaker) key of the context sequence */
 } orc_sampler;
 
+/* Condition encoders (text_encoder.rs:17-148, speaker_encoder.rs:85-162): a stack of
+ * TextBlocks of width E = dim, H heads of Dh = E / H, SwiGLU hidden F. */
+typedef struct orc_enc_cfg {
+    int32_t dim;          /* E */
+    int32_t num_layers;
+    int32_t num_heads;    /* H */
+    int32_t mlp_hidden;   /* F */
+    float norm_eps;
+} orc_enc_cfg;
+
+/* One TextBlock (text_encoder.rs:17-60) with its SelfAttention (attention.rs:52-127),
+ * Burn [d_in, d_out] layouts. */
+typedef struct orc_enc_block {
+    const float* attn_norm;  /* [E] attention_norm.weight */
+    const float* wq;         /* [E, H*Dh] */
+    const float* wk;
+    const float* wv;
+    const float* wo;         /* [H*Dh, E] */
+    const float* w_gate;     /* [E, E] */
+    const float* q_norm;     /* [H, Dh] */
+    const float* k_norm;
+    const float* mlp_norm;   /* [E] mlp_norm.weight */
+    const float* w13;        /* [E, 2F] = [W1 | W3] */
+    const float* w2;         /* [F, E] */
+} orc_enc_block;
+
 /* fp8 (e4m3fn) GEMM operands (oracle.c). */
 uint8_t orc_e4m3_encode(float x);
 float orc_e4m3_decode(uint8_t b);
@@ -124,6 +150,14 @@ int orc_get_threads(void);
                           const float* cond, int B, float* shift, float* scale,            \
                           float* gate);                                                     \
     void P##gemm_fp8(const float* x, const float* w, int M, int K, int N, float* y);      \
+    void P##text_block(const orc_enc_cfg* c, const orc_enc_block* blk, float* x,           \
+                       const uint8_t* mask, int B, int S, const float* cos_t,              \
+                       const float* sin_t);                                                 \
+    void P##encoder_forward(const orc_enc_cfg* c, const orc_enc_block* blocks,             \
+                            const float* embedding, const float* in_w, const float* in_b,  \
+                            int in_dim, const float* out_norm, int mean_token, int B,       \
+                            int S, const int32_t* ids, const float* latent,                \
+                            const uint8_t* mask, float* out, uint8_t* mask_out);           \
     void P##swiglu(const float* h, const float* w13, const float* w2, int M, int D, int F, \
                    float* out);                                                             \
     void P##joint_attention(const orc_cfg* c, const orc_block* blk, const float* h, int B, \

@@ -46,6 +46,16 @@ class OrcIo(C.Structure):
     ]
 
 
+class OrcEncCfg(C.Structure):
+    _fields_ = [("dim", C.c_int32), ("num_layers", C.c_int32), ("num_heads", C.c_int32),
+                ("mlp_hidden", C.c_int32), ("norm_eps", C.c_float)]
+
+
+class OrcEncBlock(C.Structure):
+    _fields_ = [(n, _f32p) for n in ("attn_norm", "wq", "wk", "wv", "wo", "w_gate", "q_norm",
+                                     "k_norm", "mlp_norm", "w13", "w2")]
+
+
 class OrcSampler(C.Structure):
     """orc_sampler (oracle.h): the sampler parameters and request facts."""
     _fields_ = [
@@ -303,6 +313,42 @@ class Oracle:
         y = np.empty((M, N), np.float32)
         self._fn("gemm_fp8")(_f(x), _f(w), M, K, N, _f(y))
         return y
+
+    # ---- condition encoders --------------------------------------------------------
+    @staticmethod
+    def enc_cfg_struct(ecfg) -> OrcEncCfg:
+        return OrcEncCfg(ecfg.dim, ecfg.num_layers, ecfg.num_heads, ecfg.mlp_hidden, ecfg.norm_eps)
+
+    @staticmethod
+    def enc_block_struct(b) -> OrcEncBlock:
+        return OrcEncBlock(*[_f(b[k]) for k in ("attn_norm", "wq", "wk", "wv", "wo", "w_gate",
+                                                 "q_norm", "k_norm", "mlp_norm", "w13", "w2")])
+
+    def encoder_forward(self, ecfg, ew, mask, ids=None, latent=None):
+        """Condition encoder + conditioner norm (+ the speaker mean token): ids [B, S] int32
+        or latent [B, S, in_dim]; mask [B, S] -> (state [B, S + mean_token, E],
+        mask_out [B, S + mean_token])."""
+        mask = np.ascontiguousarray(mask, np.uint8)
+        B, S = mask.shape
+        Tn = S + (1 if ecfg.mean_token else 0)
+        out = np.empty((B, Tn, ecfg.dim), np.float32)
+        mo = np.empty((B, Tn), np.uint8)
+        blocks = (OrcEncBlock * ecfg.num_layers)(*[self.enc_block_struct(b) for b in ew.blocks])
+        keep = [ew.blocks, ew.io]
+        idp = None
+        if ids is not None:
+            ids = np.ascontiguousarray(ids, np.int32)
+            idp = ids.ctypes.data_as(C.POINTER(C.c_int32))
+        lat = _c32(latent) if latent is not None else None
+        self._fn("encoder_forward")(
+            C.byref(self.enc_cfg_struct(ecfg)), blocks,
+            _f(ew.io["embedding"]) if ids is not None else None,
+            _f(ew.io["in_w"]) if lat is not None else None,
+            _f(ew.io["in_b"]) if lat is not None else None, ecfg.in_dim,
+            _f(ew.io["out_norm"]), int(ecfg.mean_token), B, S, idp,
+            _f(lat) if lat is not None else None, _u8(mask), _f(out), _u8(mo))
+        del keep
+        return out, mo
 
     def swiglu(self, h, w13, w2):
         h = _c32(h)

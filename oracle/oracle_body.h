@@ -685,3 +685,119 @@ int P(sample_rf)(const orc_cfg* c, const orc_io* io, const orc_block* blocks, in
     free(ts); free(v1); free(v2); free(xp); free(vtmp); free(hist); free(tt);
     return run;
 }
+
+/* TextBlock::forward (text_encoder.rs:46-60), dropout = identity:
+ *   a = SelfAttention(attention_norm(x)); x += a;  x += SwiGlu(mlp_norm(x)).
+ * SelfAttention (attention.rs:96-121): q, k, v = h @ Wq, Wk, Wv -> [B, S, H, Dh];
+ * q, k head-RMSNormed (q_norm / k_norm), full RoPE on every head (rope.rs:82-113);
+ * o = SDPA(q, k, v, key mask, Dh^-0.5); out = (o * sigmoid(h @ W_gate)) @ Wo.
+ * x [B, S, E] in place; mask [B, S] (nonzero = valid key). */
+void P(text_block)(const orc_enc_cfg* c, const orc_enc_block* blk, float* x, const uint8_t* mask, int B,
+                   int S, const float* cos_t, const float* sin_t) {
+    const int E = c->dim, H = c->num_heads, Dh = E / H, HD = H * Dh, F = c->mlp_hidden, M = B * S;
+    const size_t n = (size_t)M * E, nq = (size_t)M * HD;
+    float* h = (float*)malloc(sizeof(float) * n);
+    float* q = (float*)malloc(sizeof(float) * nq);
+    float* k = (float*)malloc(sizeof(float) * nq);
+    float* v = (float*)malloc(sizeof(float) * nq);
+    float* t = (float*)malloc(sizeof(float) * nq);
+    float* qh = (float*)malloc(sizeof(float) * nq);
+    float* kh = (float*)malloc(sizeof(float) * nq);
+    float* vh = (float*)malloc(sizeof(float) * nq);
+    float* oh = (float*)malloc(sizeof(float) * nq);
+    float* g = (float*)malloc(sizeof(float) * n);
+    float* mk = (float*)malloc(sizeof(float) * (size_t)B * S);
+    float* y = (float*)malloc(sizeof(float) * n);
+    P(rms_norm)(x, blk->attn_norm, M, E, c->norm_eps, h);
+    P(linear)(h, blk->wq, NULL, M, E, HD, q);
+    P(linear)(h, blk->wk, NULL, M, E, HD, k);
+    P(linear)(h, blk->wv, NULL, M, E, HD, v);
+    P(head_rms_norm)(q, blk->q_norm, M, H, Dh, c->norm_eps, t);
+    P(rope_full)(t, cos_t, sin_t, B, S, H, Dh, q);
+    P(head_rms_norm)(k, blk->k_norm, M, H, Dh, c->norm_eps, t);
+    P(rope_full)(t, cos_t, sin_t, B, S, H, Dh, k);
+    for (int b = 0; b < B; b++)
+        for (int hh = 0; hh < H; hh++)
+            for (int s = 0; s < S; s++)
+                for (int d = 0; d < Dh; d++) {
+                    const size_t src = (((size_t)b * S + s) * H + hh) * Dh + d;
+                    const size_t dst = (((size_t)b * H + hh) * S + s) * Dh + d;
+                    qh[dst] = q[src];
+                    kh[dst] = k[src];
+                    vh[dst] = v[src];
+                }
+    for (int i = 0; i < B * S; i++) mk[i] = mask[i] ? 1.f : 0.f;
+    P(sdpa)(qh, kh, vh, mk, B, H, S, S, Dh, (float)(R_C(1.0) / SQRT((R)Dh)), oh);
+    P(linear)(h, blk->w_gate, NULL, M, E, E, g);
+    for (int b = 0; b < B; b++)
+        for (int s = 0; s < S; s++)
+            for (int hh = 0; hh < H; hh++)
+                for (int d = 0; d < Dh; d++) {
+                    const size_t dst = (((size_t)b * S + s) * H + hh) * Dh + d;
+                    t[dst] = (float)((R)oh[(((size_t)b * H + hh) * S + s) * Dh + d] * P(sigmoid)((R)g[dst]));
+                }
+    P(linear)(t, blk->wo, NULL, M, HD, E, y);
+    for (size_t i = 0; i < n; i++) x[i] = (float)((R)x[i] + (R)y[i]);
+    P(rms_norm)(x, blk->mlp_norm, M, E, c->norm_eps, h);
+    P(swiglu)(h, blk->w13, blk->w2, M, E, F, y);
+    for (size_t i = 0; i < n; i++) x[i] = (float)((R)x[i] + (R)y[i]);
+    free(h); free(q); free(k); free(v); free(t); free(qh); free(kh); free(vh); free(oh); free(g);
+    free(mk); free(y);
+}
+
+/* A condition encoder and its conditioner norm:
+ *   text / caption (TextEncoder::forward, text_encoder.rs:117-147): x = embedding[ids];
+ *   speaker (ReferenceLatentEncoder::forward, speaker_encoder.rs:135-162):
+ *     x = (latent @ in_w + in_b) / 6;
+ *   then x *= mask; per block x = TextBlock(x), x *= mask; x *= mask;
+ *   state = RmsNorm(out_norm)(x) (text_norm, dit/model.rs:189-190, or the speaker /
+ *   caption conditioner's norm, aux_conditioner.rs:60-85);
+ *   mean_token (speaker, prepend_masked_mean_token, aux_conditioner.rs:150-185): out =
+ *   [sum_s mask * state / max(count, 1) | state], mask_out = [count > 0 | mask].
+ * ids [B, S] (embedding != NULL) or latent [B, S, in_dim]; out [B, S + mean_token, E]. */
+void P(encoder_forward)(const orc_enc_cfg* c, const orc_enc_block* blocks, const float* embedding,
+                        const float* in_w, const float* in_b, int in_dim, const float* out_norm, int mean_token,
+                        int B, int S, const int32_t* ids, const float* latent, const uint8_t* mask, float* out,
+                        uint8_t* mask_out) {
+    const int E = c->dim, Dh = E / c->num_heads, M = B * S;
+    const size_t n = (size_t)M * E;
+    float* x = (float*)malloc(sizeof(float) * n);
+    float* st = (float*)malloc(sizeof(float) * n);
+    float* cs = (float*)malloc(sizeof(float) * (size_t)S * (Dh / 2));
+    float* sn = (float*)malloc(sizeof(float) * (size_t)S * (Dh / 2));
+    if (embedding) {
+        for (int i = 0; i < M; i++) memcpy(x + (size_t)i * E, embedding + (size_t)ids[i] * E, sizeof(float) * E);
+    } else {
+        P(linear)(latent, in_w, in_b, M, in_dim, E, x);
+        for (size_t i = 0; i < n; i++) x[i] = (float)((R)x[i] / R_C(6.0));
+    }
+    for (int i = 0; i < M; i++)
+        if (!mask[i]) memset(x + (size_t)i * E, 0, sizeof(float) * E);
+    P(rope_tables)(S, Dh, 10000.f, cs, sn);
+    for (int l = 0; l < c->num_layers; l++) {
+        P(text_block)(c, &blocks[l], x, mask, B, S, cs, sn);
+        for (int i = 0; i < M; i++)
+            if (!mask[i]) memset(x + (size_t)i * E, 0, sizeof(float) * E);
+    }
+    P(rms_norm)(x, out_norm, M, E, c->norm_eps, st);
+    const int T = S + (mean_token ? 1 : 0);
+    for (int b = 0; b < B; b++) {
+        float* ob = out + (size_t)b * T * E;
+        if (mean_token) {
+            int cnt = 0;
+            for (int s = 0; s < S; s++) cnt += mask[(size_t)b * S + s] ? 1 : 0;
+            const R den = cnt > 0 ? (R)cnt : R_C(1.0);
+            for (int d = 0; d < E; d++) {
+                R acc = 0;
+                for (int s = 0; s < S; s++)
+                    if (mask[(size_t)b * S + s]) acc += (R)st[((size_t)b * S + s) * E + d];
+                ob[d] = (float)(acc / den);
+            }
+            if (mask_out) mask_out[(size_t)b * T] = cnt > 0;
+        }
+        memcpy(ob + (size_t)(T - S) * E, st + (size_t)b * S * E, sizeof(float) * (size_t)S * E);
+        if (mask_out)
+            for (int s = 0; s < S; s++) mask_out[(size_t)b * T + (T - S) + s] = mask[(size_t)b * S + s] ? 1 : 0;
+    }
+    free(x); free(st); free(cs); free(sn);
+}

@@ -117,3 +117,45 @@ def forward(cfg, weights, x_t, t, ctx_k, ctx_v, ctx_mask, debug=False, latent_ma
     if debug:
         return v.numpy(), torch.stack(outs).numpy()
     return v.numpy()
+
+
+# ---- condition encoders (text_encoder.rs:17-148, speaker_encoder.rs:85-162,
+# attention.rs:52-127, aux_conditioner.rs:150-185) ------------------------------------------
+def text_block(x, blk, mask, cos, sin, H, eps):
+    B, S, E = x.shape
+    Dh = E // H
+    h = x / rms(x, eps) * T(blk["attn_norm"])
+    q = lin(h, blk["wq"]).reshape(B, S, H, Dh)
+    k = lin(h, blk["wk"]).reshape(B, S, H, Dh)
+    v = lin(h, blk["wv"]).reshape(B, S, H, Dh)
+    q = rope(q / rms(q, eps) * T(blk["q_norm"]), cos, sin)
+    k = rope(k / rms(k, eps) * T(blk["k_norm"]), cos, sin)
+    valid = T(mask) > 0
+    o = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),
+                                       attn_mask=valid[:, None, None, :])
+    o = torch.nan_to_num(o)  # a row with no valid key: 0 (attention.rs:686-716)
+    o = o.transpose(1, 2).reshape(B, S, E)
+    x = x + lin(torch.sigmoid(lin(h, blk["w_gate"])) * o, blk["wo"])
+    h2 = x / rms(x, eps) * T(blk["mlp_norm"])
+    return x + swiglu(h2, blk["w13"], blk["w2"])
+
+
+def encoder_forward(ecfg, ew, mask, ids=None, latent=None):
+    m = T(mask)[..., None]
+    if ids is not None:
+        x = T(ew.io["embedding"])[torch.as_tensor(np.asarray(ids), dtype=torch.long)]
+    else:
+        x = lin(T(latent), ew.io["in_w"], ew.io["in_b"]) / 6.0
+    x = x * m
+    S = x.shape[1]
+    cos, sin = rope_tables(S, ecfg.dim // ecfg.num_heads)
+    for blk in ew.blocks:
+        x = text_block(x, blk, mask, cos, sin, ecfg.num_heads, ecfg.norm_eps) * m
+    st = x / rms(x, ecfg.norm_eps) * T(ew.io["out_norm"])
+    mo = torch.as_tensor(np.asarray(mask, np.uint8))
+    if ecfg.mean_token:
+        cnt = m.sum(1, keepdim=True)
+        mean = (st * m).sum(1, keepdim=True) / cnt.clamp(min=1.0)
+        st = torch.cat([mean, st], 1)
+        mo = torch.cat([(cnt[:, 0, 0] > 0).to(torch.uint8)[:, None], mo], 1)
+    return st.numpy(), mo.numpy()
