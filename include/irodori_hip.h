@@ -256,6 +256,66 @@ typedef struct irodori_kernel_times {
 int irodori_profile_layer(irodori_ctx* ctx, int batch, int seq, int iters,
                           irodori_kernel_times* out);
 
+/* ---- condition encoders ---------------------------------------------------------------
+ * TextEncoder (text / caption, text_encoder.rs:64-148) and ReferenceLatentEncoder (speaker,
+ * speaker_encoder.rs:85-162) with their conditioner norm (text_norm, dit/model.rs:189-190;
+ * aux_conditioner.rs:60-85) and, for the speaker, the masked-mean token
+ * (aux_conditioner.rs:150-185): EncodedCondition's text_state / aux state on the device.
+ * The reference runs these once per request on the CPU backend; here they run on the GPU
+ * (compute_dtype BF16: bf16 GEMM / attention operands, f32 residual; F32: f32 throughout). */
+typedef struct irodori_encoder irodori_encoder;
+
+typedef struct irodori_encoder_config {
+    int32_t dim;           /* text_dim / speaker_dim / caption_dim */
+    int32_t num_layers;
+    int32_t num_heads;     /* head_dim = dim / num_heads: 64 or 128 */
+    int32_t mlp_hidden;    /* floor(dim * mlp_ratio) (text_encoder.rs:36), multiple of 16 */
+    int32_t vocab_size;    /* > 0: token ids in (TextEncoder), embedding [vocab, dim] */
+    int32_t in_dim;        /* > 0: latent frames in (ReferenceLatentEncoder), in_proj [in_dim, dim] */
+    int32_t mean_token;    /* 1: prepend the speaker conditioner's masked-mean token */
+    float norm_eps;
+    int32_t compute_dtype; /* IRODORI_DTYPE_BF16 or IRODORI_DTYPE_F32 */
+    int32_t max_rows;      /* max batch rows */
+    int32_t max_seq;       /* max tokens / frames per row */
+} irodori_encoder_config;
+
+/* Front end and conditioner norm, Burn layouts, host f32; unused pointers may be NULL. */
+typedef struct irodori_encoder_io_weights {
+    const float* embedding; /* [vocab, dim] text_embedding.weight */
+    const float* in_w;      /* [in_dim, dim] in_proj.weight */
+    const float* in_b;      /* [dim] in_proj.bias */
+    const float* out_norm;  /* [dim] text_norm / speaker or caption conditioner norm weight */
+} irodori_encoder_io_weights;
+
+/* One TextBlock (text_encoder.rs:17-60): attention_norm, SelfAttention (wq, wk, wv, wo,
+ * gate, q_norm, k_norm; attention.rs:52-127), mlp_norm, SwiGlu (w13 = [W1 | W3], w2). */
+typedef struct irodori_encoder_block_weights {
+    const float* attn_norm; /* [dim] */
+    const float* wq;        /* [dim, dim] */
+    const float* wk;
+    const float* wv;
+    const float* wo;        /* [dim, dim] */
+    const float* w_gate;    /* [dim, dim] */
+    const float* q_norm;    /* [heads, head_dim] */
+    const float* k_norm;
+    const float* mlp_norm;  /* [dim] */
+    const float* w13;       /* [dim, 2 * mlp_hidden] */
+    const float* w2;        /* [mlp_hidden, dim] */
+} irodori_encoder_block_weights;
+
+int irodori_encoder_create(int device, const irodori_encoder_config* cfg, irodori_encoder** out);
+int irodori_encoder_destroy(irodori_encoder* enc);
+int irodori_encoder_load_io_weights(irodori_encoder* enc, const irodori_encoder_io_weights* w);
+int irodori_encoder_load_block_weights(irodori_encoder* enc, int layer,
+                                       const irodori_encoder_block_weights* w);
+/* Encode `batch` rows of `seq` tokens (ids [batch, seq], vocab_size > 0) or latent frames
+ * (latent [batch, seq, in_dim], in_dim > 0); mask [batch, seq] (nonzero = valid).
+ * state_out [batch, seq + mean_token, dim] f32; mask_out (nullable) [batch, seq +
+ * mean_token].  Host pointers; synchronous. */
+int irodori_encoder_forward(irodori_encoder* enc, int batch, int seq, const int32_t* ids,
+                            const float* latent, const uint8_t* mask, float* state_out,
+                            uint8_t* mask_out);
+
 /* ---- operator entry points (device pointers; stream may be NULL) ------------------- */
 /* rms_norm_wgsl (rms_norm.rs:70-142): y = x / sqrt(mean(x^2)+eps) * w, x [rows, dim]. */
 int irodori_op_rms_norm(const float* x, const float* w, int rows, int dim, float eps,

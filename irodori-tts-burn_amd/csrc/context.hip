@@ -25,49 +25,13 @@
 #include "../../include/irodori_hip.h"
 #include "common.hpp"
 #include "kernels.hpp"
+#include "host.hpp"
 
 namespace irodori {
 
 static thread_local std::string g_last_error;
 void set_last_error(const std::string& msg) { g_last_error = msg; }
 
-namespace {
-
-// ---------------------------------------------------------------------------------------
-// Weight ingest kernels: Burn [K, N] f32 -> K-major [N, K] compute dtype.
-// mode 0: dst row n = source column n.
-// mode 1: SwiGLU interleave — dst rows 64g..64g+31 = W1 columns 32g.., rows 64g+32..64g+63 =
-//         W3 columns 32g.. (W3 starts at source column N/2).
-// ---------------------------------------------------------------------------------------
-template <typename T>
-__global__ void transpose_kmajor_kernel(const float* __restrict__ src, int K, int N, int mode,
-                                        T* __restrict__ dst) {
-    __shared__ float tile[32][33];
-    int k0 = blockIdx.x * 32, n0 = blockIdx.y * 32;
-    int tx = threadIdx.x, ty = threadIdx.y;  // 32 x 8
-    for (int r = ty; r < 32; r += 8) {
-        int k = k0 + r, n = n0 + tx;
-        int sc = n;
-        if (mode == 1 && n < N) {
-            int half = N / 2, g = n / 64, w = n % 64;
-            sc = w < 32 ? 32 * g + w : half + 32 * g + (w - 32);
-        }
-        tile[r][tx] = (k < K && n < N) ? src[(size_t)k * N + sc] : 0.f;
-    }
-    __syncthreads();
-    for (int r = ty; r < 32; r += 8) {
-        int n = n0 + r, k = k0 + tx;
-        if (n < N && k < K) dst[(size_t)n * K + k] = from_f32<T>(tile[tx][r]);
-    }
-}
-
-template <typename T>
-void launch_transpose(const float* src, int K, int N, int mode, T* dst, hipStream_t st) {
-    dim3 grid((K + 31) / 32, (N + 31) / 32), block(32, 8);
-    transpose_kmajor_kernel<T><<<grid, block, 0, st>>>(src, K, N, mode, dst);
-}
-
-}  // namespace
 }  // namespace irodori
 
 using namespace irodori;
@@ -216,34 +180,8 @@ int dalloc(irodori_ctx* c, P** p, size_t bytes) {
     return dev_alloc(c, reinterpret_cast<void**>(p), bytes);
 }
 
-#define IRO_TRY(expr)                   \
-    do {                                \
-        int _rc = (expr);               \
-        if (_rc != IRODORI_OK) return _rc; \
-    } while (0)
 
-int check_launch(const char* what) {
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) {
-        set_last_error(std::string(what) + ": " + hipGetErrorString(e));
-        return IRODORI_ERR_HIP;
-    }
-    return IRODORI_OK;
-}
 
-// rope.rs:24-63 in f32: freq_i = 1 / theta^(2i/Dh), angle = pos * freq_i.
-void host_rope_tables(int S, int Dh, float theta, std::vector<float>& cs, std::vector<float>& sn) {
-    int half = Dh / 2;
-    cs.resize((size_t)S * half);
-    sn.resize((size_t)S * half);
-    for (int s = 0; s < S; s++)
-        for (int i = 0; i < half; i++) {
-            float freq = 1.0f / powf(theta, 2.0f * (float)i / (float)Dh);
-            float a = (float)s * freq;
-            cs[(size_t)s * half + i] = cosf(a);
-            sn[(size_t)s * half + i] = sinf(a);
-        }
-}
 
 int upload(irodori_ctx* c, void* dst, const void* src, size_t bytes) {
     IRO_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream));
@@ -744,17 +682,6 @@ int cfg_roles(const irodori_sampler_params* p, int n) {
 
 }  // namespace
 
-#define IRO_GUARD_BEGIN try {
-#define IRO_GUARD_END                                             \
-    }                                                             \
-    catch (const std::bad_alloc&) {                               \
-        set_last_error("host allocation failed");                 \
-        return IRODORI_ERR_OOM;                                   \
-    }                                                             \
-    catch (...) {                                                 \
-        set_last_error("unexpected C++ exception");               \
-        return IRODORI_ERR_HIP;                                   \
-    }
 
 extern "C" {
 

@@ -164,7 +164,7 @@ void launch_timestep_embedding(const float* t, int nvec, int t_dim, float* out, 
 void launch_vec_linear(const VecLinJob* d_jobs, int njobs, int nvec, int max_n, hipStream_t st);
 
 // ---- kernels_gemm.hip ------------------------------------------------------------------
-enum GemmEpi { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_QKVG = 3, EPI_CTXKV = 4 };
+enum GemmEpi { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_QKVG = 3, EPI_CTXKV = 4, EPI_ADD = 5 };
 template <typename T>
 struct GemmArgs {
     const T* A;   // [M, K] row-major
@@ -198,6 +198,9 @@ struct GemmArgs {
     T* Ck;
     T* Cv;
     int key_off, ctx_stride, ctx_vstride;
+    // EPI_ADD: x[m, n] = (x[m, n] + acc) * rmask[m] (rmask nullable: 1), the encoder's
+    // plain residual with its per-block re-masking (text_encoder.rs:131-145).
+    const float* rmask;
     // fp8 operands (launch_gemm_fp8): A8 [M, K] e4m3 with As [M, K/32] E8M0 block scales
     // (power-of-two scale of row m, k block kb = 2^(As - 127)); W8 [N, K] e4m3 with f32
     // per-output-channel scales ws [N].  C = (A8 * 2^As) @ W8^T * ws.
@@ -214,6 +217,21 @@ template <typename T>
 int launch_gemm(int epi, const GemmArgs<T>& a, hipStream_t st);
 // The same epilogues over fp8 operands (K % 128 == 0); outputs in bf16 / f32 as above.
 int launch_gemm_fp8(int epi, const GemmArgs<bf16>& a, hipStream_t st);
+
+// ---- kernels_enc.hip -------------------------------------------------------------------
+// Host f32 [K, N] (Burn layout, on the device) -> K-major [N, K]; mode 1 interleaves the
+// W1 / W3 halves per 32 rows (the SwiGLU GEMM's layout).
+template <typename T>
+void launch_transpose(const float* src, int K, int N, int mode, T* dst, hipStream_t st);
+void launch_enc_embed(const int* ids, const float* emb, const float* mask, float* x, int M, int E, hipStream_t st);
+void launch_enc_inproj(const float* lat, const float* w, const float* b, const float* mask, float* x, int M, int K,
+                       int E, hipStream_t st);
+template <typename TO>
+void launch_rmsnorm_w(const float* x, const float* w, int M, int E, float eps, TO* y, int ystride, hipStream_t st);
+template <typename T>
+void launch_enc_head_prep(const float* qkvg, const float* q_norm, const float* k_norm, const float* cs, const float* sn,
+                          int M, int S, int H, int Dh, float eps, T* q, T* k, T* v, T* gate, hipStream_t st);
+void launch_enc_mean_token(float* out, const float* mask, uint8_t* mask_out, int B, int S, int E, hipStream_t st);
 
 // ---- kernels_fp8.hip -------------------------------------------------------------------
 // Weights w [N, K] f32 (K-major, K % 4 == 0) -> e4m3 codes q [N, K], channel scales s [N].

@@ -18,6 +18,7 @@
 //   EPI_STORE  C f32
 //   EPI_RESID  x += gate * C            (gated residual, diffusion.rs:98 / :104)
 //   EPI_SWIGLU U = silu(C1) * C3        (feed_forward.rs:80-84; W rows interleaved per 32)
+//   EPI_ADD    x = (x + C) * rmask[row]  (encoder residual + re-mask)
 //   EPI_QKVG   q,k: head RMSNorm (norm.rs:60-74) + half RoPE (rope.rs:82-135);
 //              q pre-scaled by Dh^-1/2 log2(e) for the attention softmax;
 //              v: scatter to V^T [B,H,Dh,S'] (key-permuted); gate: sigmoid (attention.rs:423)
@@ -366,6 +367,21 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
                 if (row >= a.M) continue;
 #pragma unroll
                 for (int j = 0; j < FN; j++) C[(size_t)row * a.N + n0 + wn0 + 32 * j + cl] = acc[i][j][e];
+            }
+    } else if constexpr (EPI == EPI_ADD) {
+        float* __restrict__ xg = a.x;
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const int row = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
+                if (row >= a.M) continue;
+                const float rm = a.rmask ? a.rmask[row] : 1.f;
+#pragma unroll
+                for (int j = 0; j < FN; j++) {
+                    float* px = xg + (size_t)row * a.N + n0 + wn0 + 32 * j + cl;
+                    *px = (*px + acc[i][j][e]) * rm;
+                }
             }
     } else if constexpr (EPI == EPI_RESID) {
         // x[row, col] += gate[b(row), col] * C, from the values loaded before the main loop.
@@ -724,6 +740,9 @@ int launch_gemm(int epi, const GemmArgs<T>& a, hipStream_t st) {
         case EPI_RESID:
             if (wide_enough(a)) return launch_cfg<T, 128, 128, 2, 2, 2, EPI_RESID>(a, st);
             return launch_cfg<T, 64, 64, 2, 2, 4, EPI_RESID>(a, st);
+        case EPI_ADD:
+            if (wide_enough(a)) return launch_cfg<T, 128, 128, 2, 2, 2, EPI_ADD>(a, st);
+            return launch_cfg<T, 64, 64, 2, 2, 4, EPI_ADD>(a, st);
         case EPI_SWIGLU: return launch_cfg<T, 128, 128, 2, 2, 2, EPI_SWIGLU>(a, st);
         case EPI_QKVG: return launch_cfg<T, 128, 128, 2, 2, 2, EPI_QKVG>(a, st);
         case EPI_CTXKV:

@@ -8,7 +8,7 @@ from .config import (CfgGuidanceMode, DitConfig, EncoderConfig, GuidanceConfig,
                      InferenceBackendKind, IrodoriError, SamplerMethod, SamplerParams,
                      cfg_cpu_plumbing, cfg_full_rf, cfg_tiny, enc_speaker_default,
                      enc_speaker_tiny, enc_text_default, enc_text_tiny)
-from .engine import HipInferenceEngine, ops
+from .engine import HipEncoder, HipInferenceEngine, ops
 from .synthetic import (ROLE_COND, ROLE_NO_AUX, ROLE_NO_TEXT, ROLE_UNCOND, ContextKV,
                         CtxProjWeights, DitWeights, EncoderWeights, make_context_kv, make_noise,
                         make_role_context)
@@ -16,7 +16,7 @@ from .synthetic import (ROLE_COND, ROLE_NO_AUX, ROLE_NO_TEXT, ROLE_UNCOND, Conte
 __all__ = [
     "CfgGuidanceMode", "DitConfig", "GuidanceConfig", "InferenceBackendKind", "IrodoriError",
     "SamplerMethod", "SamplerParams", "cfg_cpu_plumbing", "cfg_full_rf", "cfg_tiny",
-    "HipInferenceEngine", "ops", "ContextKV", "CtxProjWeights", "DitWeights", "make_context_kv", "make_noise",
+    "HipInferenceEngine", "HipEncoder", "ops", "ContextKV", "CtxProjWeights", "DitWeights", "make_context_kv", "make_noise",
     "make_role_context", "ROLE_COND", "ROLE_UNCOND", "ROLE_NO_TEXT", "ROLE_NO_AUX",
     "EncoderConfig", "EncoderWeights", "enc_text_default", "enc_speaker_default", "enc_text_tiny",
     "enc_speaker_tiny",

@@ -76,6 +76,25 @@ class CtxProjWeightsC(C.Structure):
     _fields_ = [("wk_text", _f32p), ("wv_text", _f32p), ("wk_aux", _f32p), ("wv_aux", _f32p)]
 
 
+class EncoderConfigC(C.Structure):
+    _fields_ = [("dim", C.c_int32), ("num_layers", C.c_int32), ("num_heads", C.c_int32),
+                ("mlp_hidden", C.c_int32), ("vocab_size", C.c_int32), ("in_dim", C.c_int32),
+                ("mean_token", C.c_int32), ("norm_eps", C.c_float), ("compute_dtype", C.c_int32),
+                ("max_rows", C.c_int32), ("max_seq", C.c_int32)]
+
+
+class EncoderIoWeightsC(C.Structure):
+    _fields_ = [("embedding", _f32p), ("in_w", _f32p), ("in_b", _f32p), ("out_norm", _f32p)]
+
+
+ENC_BLOCK_FIELDS = ("attn_norm", "wq", "wk", "wv", "wo", "w_gate", "q_norm", "k_norm", "mlp_norm",
+                    "w13", "w2")
+
+
+class EncoderBlockWeightsC(C.Structure):
+    _fields_ = [(n, _f32p) for n in ENC_BLOCK_FIELDS]
+
+
 class KernelTimesC(C.Structure):
     _fields_ = [(n, C.c_float) for n in ("norm_mod_us", "qkvg_gemm_us", "attention_us",
                                           "wo_gemm_us", "w13_gemm_us", "w2_gemm_us", "final_us")]
@@ -113,6 +132,12 @@ SIGNATURES = {
     "irodori_sample_device_masked": (C.c_int, [_vp, C.POINTER(SamplerParamsC), C.c_int, C.c_int,
                                                C.POINTER(C.c_int32), _vp, _vp]),
     "irodori_profile_layer": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.POINTER(KernelTimesC)]),
+    "irodori_encoder_create": (C.c_int, [C.c_int, C.POINTER(EncoderConfigC), C.POINTER(_vp)]),
+    "irodori_encoder_destroy": (C.c_int, [_vp]),
+    "irodori_encoder_load_io_weights": (C.c_int, [_vp, C.POINTER(EncoderIoWeightsC)]),
+    "irodori_encoder_load_block_weights": (C.c_int, [_vp, C.c_int, C.POINTER(EncoderBlockWeightsC)]),
+    "irodori_encoder_forward": (C.c_int, [_vp, C.c_int, C.c_int, C.POINTER(C.c_int32), _f32p,
+                                          C.POINTER(C.c_uint8), _f32p, C.POINTER(C.c_uint8)]),
     "irodori_op_rms_norm": (C.c_int, [_vp, _vp, C.c_int, C.c_int, C.c_float, _vp, _vp]),
     "irodori_op_fused_adaln": (C.c_int, [_vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_float,
                                          _vp, _vp]),

@@ -16,9 +16,9 @@ import ctypes as C
 import numpy as np
 
 from . import _lib as L
-from .config import (CfgGuidanceMode, DitConfig, InferenceBackendKind, IrodoriError,
+from .config import (CfgGuidanceMode, DitConfig, EncoderConfig, InferenceBackendKind, IrodoriError,
                      SamplerMethod, SamplerParams)
-from .synthetic import ContextKV, CtxProjWeights, DitWeights
+from .synthetic import ContextKV, CtxProjWeights, DitWeights, EncoderWeights
 
 _f32p = C.POINTER(C.c_float)
 
@@ -245,6 +245,70 @@ class HipInferenceEngine:
         kt = L.KernelTimesC()
         _check(self.lib.irodori_profile_layer(self.ctx, batch, seq, iters, C.byref(kt)))
         return {n: float(getattr(kt, n)) for n, _ in L.KernelTimesC._fields_}
+
+
+class HipEncoder:
+    """A condition encoder on the GPU (irodori_encoder_*): TextEncoder / ReferenceLatentEncoder
+    + the conditioner norm (+ the speaker mean token), i.e. EncodedCondition's text_state or
+    aux state (dit/model.rs:182-205)."""
+
+    def __init__(self, cfg: EncoderConfig, backend: InferenceBackendKind = InferenceBackendKind.HIP_BF16,
+                 max_rows: int = 2, max_seq: int = 512, device: int = 0):
+        if backend not in (InferenceBackendKind.HIP_BF16, InferenceBackendKind.HIP_F32):
+            raise IrodoriError("Dtype", "the encoders run in bf16 or f32")
+        self.cfg = cfg
+        self.lib = L.load()
+        c = L.EncoderConfigC(cfg.dim, cfg.num_layers, cfg.num_heads, cfg.mlp_hidden, cfg.vocab_size,
+                             cfg.in_dim, int(cfg.mean_token), cfg.norm_eps,
+                             L.DTYPE_BF16 if backend is InferenceBackendKind.HIP_BF16 else L.DTYPE_F32,
+                             max_rows, max_seq)
+        h = C.c_void_p()
+        _check(self.lib.irodori_encoder_create(device, C.byref(c), C.byref(h)))
+        self.enc = h
+
+    def close(self) -> None:
+        if getattr(self, "enc", None):
+            self.lib.irodori_encoder_destroy(self.enc)
+            self.enc = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def load_weights(self, w: EncoderWeights) -> None:
+        io = L.EncoderIoWeightsC(*[_fp(w.io[k]) if k in w.io else None
+                                   for k in ("embedding", "in_w", "in_b", "out_norm")])
+        _check(self.lib.irodori_encoder_load_io_weights(self.enc, C.byref(io)))
+        for l, b in enumerate(w.blocks):
+            s = L.EncoderBlockWeightsC(*[_fp(_c32(b[k])) for k in L.ENC_BLOCK_FIELDS])
+            _check(self.lib.irodori_encoder_load_block_weights(self.enc, l, C.byref(s)))
+
+    def forward(self, mask: np.ndarray, ids: np.ndarray = None, latent: np.ndarray = None):
+        """mask [B, S]; ids [B, S] (token encoder) or latent [B, S, in_dim] ->
+        (state [B, S + mean_token, dim], mask_out [B, S + mean_token])."""
+        mask = np.ascontiguousarray(mask, np.uint8)
+        B, S = mask.shape
+        Tn = S + int(self.cfg.mean_token)
+        out = np.empty((B, Tn, self.cfg.dim), np.float32)
+        mo = np.empty((B, Tn), np.uint8)
+        u8 = C.POINTER(C.c_uint8)
+        idp = lat = None
+        if ids is not None:
+            ids = np.ascontiguousarray(ids, np.int32)
+            idp = ids.ctypes.data_as(C.POINTER(C.c_int32))
+        if latent is not None:
+            lat = _c32(latent)
+        _check(self.lib.irodori_encoder_forward(self.enc, B, S, idp, _fp(lat) if lat is not None else None,
+                                                mask.ctypes.data_as(u8), _fp(out), mo.ctypes.data_as(u8)))
+        return out, mo
 
 
 class ops:
