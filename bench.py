@@ -99,7 +99,7 @@ def main():
     ap.add_argument("--profile-iters", type=int, default=50)
     ap.add_argument("--cfg5-dtype", choices=["fp8", "bf16"], default="fp8",
                     help="compute mode of --workload cfg5 (config 5 names fp8 weights)")
-    ap.add_argument("--workload", choices=["cfg4", "cfg5"], default="cfg4",
+    ap.add_argument("--workload", choices=["cfg4", "cfg5", "encode"], default="cfg4",
                     help="cfg4 (default): the headline B=2 Joint-CFG RF run; cfg5: batched "
                          "throughput, 16 utterances x 2 CFG rows, lengths U[200,750] padded")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -126,6 +126,9 @@ def main():
 
     if args.workload == "cfg5":
         print(json.dumps(run_cfg5(args, np, torch, ih)), flush=True)
+        return
+    if args.workload == "encode":
+        print(json.dumps(run_encode(args, np, torch, ih)), flush=True)
         return
 
     cfg = ih.cfg_full_rf()
@@ -319,6 +322,91 @@ def run_cfg5(args, np, torch, ih):
                      "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
                      "traffic": None},
         "cpu_baseline": None,
+    }
+
+
+def run_encode(args, np, torch, ih):
+    """Per-request conditioning on the GPU at config 4's sizes: the reference-width text
+    encoder over 256 tokens, the speaker encoder over 375 reference frames (plus its mean
+    token), and the context-KV build of the 12-layer d1024 DiT from both states (one CFG row;
+    the unconditioned row is zeros).  value = ms per request (encoders + context build)."""
+    cfg = ih.cfg_full_rf()
+    te, se = ih.enc_text_default(), ih.enc_speaker_default(cfg.latent_dim)
+    te.vocab_size = 4096  # the embedding table's size does not change the work per token
+    log("encode: generating weights (text and speaker encoders, 14 x 1280 each; DiT)")
+    tw, sw = ih.EncoderWeights.random(te, 1), ih.EncoderWeights.random(se, 2)
+    w = ih.DitWeights.random(cfg, 0)
+    proj = ih.CtxProjWeights.random(cfg, te.dim, se.dim, seed=3)
+    rng = np.random.default_rng(4)
+    Tt, Ts = 256, 375
+    ids = rng.integers(0, te.vocab_size, (1, Tt)).astype(np.int32)
+    lat = rng.standard_normal((1, Ts, se.in_dim)).astype(np.float32)
+    tm, sm = np.ones((1, Tt), np.uint8), np.ones((1, Ts), np.uint8)
+    tenc = ih.HipEncoder(te, ih.InferenceBackendKind.HIP_BF16, max_rows=1, max_seq=Tt)
+    senc = ih.HipEncoder(se, ih.InferenceBackendKind.HIP_BF16, max_rows=1, max_seq=Ts)
+    tenc.load_weights(tw)
+    senc.load_weights(sw)
+    eng = ih.HipInferenceEngine(cfg, ih.InferenceBackendKind.HIP_BF16, max_rows=2, max_seq=750,
+                                max_ctx=Tt + Ts + 1)
+    eng.load_weights(w)
+    eng.load_ctx_proj_weights(proj)
+
+    def request():
+        t0 = time.perf_counter()
+        ts, tmo = tenc.forward(tm, ids=ids)
+        t1 = time.perf_counter()
+        ss, smo = senc.forward(sm, latent=lat)
+        t2 = time.perf_counter()
+        eng.build_context_kv(0, ts[0], tmo[0], ss[0], smo[0])
+        t3 = time.perf_counter()
+        return (t1 - t0) * 1e3, (t2 - t1) * 1e3, (t3 - t2) * 1e3
+
+    for _ in range(args.warmup):
+        request()
+    parts = np.array([request() for _ in range(args.steps)])
+    ms = float(parts.sum(1).mean())
+    te_ms, se_ms, kv_ms = (float(v) for v in parts.mean(0))
+    log("encode: text %.2f ms, speaker %.2f ms, context build %.2f ms" % (te_ms, se_ms, kv_ms))
+    # GEMM + attention FLOPs of an encoder over n tokens (TextBlock: [Wq|Wk|Wv|Wg], Wo, W1|W3, W2;
+    # attention 4 n^2 E).
+    def enc_flops(ec, n):
+        E, F = ec.dim, ec.mlp_hidden
+        return ec.num_layers * (2.0 * n * E * (4 * E + E + 2 * F) + 2.0 * n * F * E + 4.0 * n * n * E)
+    kv_flops = cfg.num_layers * 2.0 * (Tt + Ts + 1) * 1280 * 2 * cfg.model_dim
+    flops = enc_flops(te, Tt) + enc_flops(se, Ts) + kv_flops
+    tenc.close()
+    senc.close()
+    eng.close()
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle.oracle import Oracle, get_threads, set_threads
+        if args.cpu_threads:
+            set_threads(args.cpu_threads)
+        te1 = ih.EncoderConfig(dim=te.dim, num_layers=1, num_heads=te.num_heads, mlp_hidden=te.mlp_hidden,
+                               vocab_size=te.vocab_size)
+        tw1 = ih.EncoderWeights(tw.io, tw.blocks[:1])
+        t0 = time.perf_counter()
+        Oracle("f32").encoder_forward(te1, tw1, tm, ids=ids)
+        layer_s = time.perf_counter() - t0
+        cpu = {"value": round(layer_s * te.num_layers * 1e3, 1), "unit": "ms (text encoder, extrapolated)",
+               "cores": get_threads(), "kind": "port",
+               "sample": "1 of 14 text-encoder blocks over 256 tokens (f32 C oracle, OpenMP), measured "
+                         "%.2f s, x14; the speaker encoder and context build not included" % layer_s}
+    return {
+        "metric": "per-request conditioning ms (text + speaker encoders + context-KV build, config 4 sizes)",
+        "value": round(ms, 3), "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 3), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: random-init encoders (1280 wide, 14 blocks, 10 heads, SwiGLU 3328) and DiT, "
+                "random token ids / N(0,1) reference latents",
+        "config": {"workload": "text encoder 256 tokens + speaker encoder 375 frames (+ mean token) + "
+                               "12-layer context-KV build, one CFG row; host pointers in and out",
+                   "global_batch": 1, "seq_len": Tt + Ts, "parallelism": "none"},
+        "parts_ms": {"text_encoder": round(te_ms, 3), "speaker_encoder": round(se_ms, 3),
+                     "context_build": round(kv_ms, 3)},
+        "achieved_tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+        "roofline": None,
+        "cpu_baseline": cpu,
     }
 
 
