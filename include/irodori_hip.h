@@ -316,6 +316,69 @@ int irodori_encoder_forward(irodori_encoder* enc, int batch, int seq, const int3
                             const float* latent, const uint8_t* mask, float* state_out,
                             uint8_t* mask_out);
 
+/* ---- DACVAE decoder -------------------------------------------------------------------
+ * DacVaeCodec::decode (codec/model.rs:60-65): latent [B, T, latent_dim] -> waveform
+ * [B, 1, T * hop], hop = prod(rates): quantizer.out_proj (bottleneck.rs:21-23), the decoder
+ * stem, DecoderBlocks (Snake, ConvTranspose1d(kernel 2r, stride r, padding ceil(r/2),
+ * output padding r % 2), ResidualUnits of dilation 1, 3, 9) and the watermark head (Snake,
+ * Conv1d(-> 1, kernel 7), tanh) of codec/decoder.rs, as built by codec/weights.rs:225-292
+ * (load_codec).  The reference decodes on its CPU/WGPU backend; here the convolutions run
+ * on the matrix cores (BF16: bf16 operands, f32 accumulation and residual stream; F32: f32
+ * throughout). */
+#define IRODORI_CODEC_MAX_BLOCKS 8
+
+typedef struct irodori_codec irodori_codec;
+
+typedef struct irodori_codec_config {
+    int32_t latent_dim;    /* 32: codebook_dim (bottleneck.rs) */
+    int32_t proj_dim;      /* 1024: quantizer.out_proj output channels, multiple of 8 */
+    int32_t decoder_dim;   /* 1536: stem output; block i maps dim >> i to dim >> (i + 1) */
+    int32_t num_blocks;    /* 4, at most IRODORI_CODEC_MAX_BLOCKS */
+    int32_t rates[IRODORI_CODEC_MAX_BLOCKS]; /* 12, 10, 8, 2; each in [2, 64] */
+    int32_t compute_dtype; /* IRODORI_DTYPE_BF16 or IRODORI_DTYPE_F32 */
+    int32_t max_frames;    /* max latent frames per row */
+} irodori_codec_config;
+
+/* One DecoderBlock (decoder.model.{1..}: block.0 Snake, block.1 ConvTranspose1d, block.4 /
+ * .5 / .8 ResidualUnits with block.0 Snake, block.1 Conv1d k 7, block.2 Snake, block.3
+ * Conv1d k 1).  Burn layouts, host f32; biases may be NULL. */
+typedef struct irodori_codec_block_weights {
+    const float* alpha;          /* [in] */
+    const float* convt_w;        /* [in, out, 2 rate] */
+    const float* convt_b;        /* [out] */
+    const float* res_alpha0[3];  /* [out] */
+    const float* res_conv_w[3];  /* [out, out, 7], dilation 1, 3, 9 */
+    const float* res_conv_b[3];  /* [out] */
+    const float* res_alpha1[3];  /* [out] */
+    const float* res_pw_w[3];    /* [out, out, 1] */
+    const float* res_pw_b[3];    /* [out] */
+} irodori_codec_block_weights;
+
+typedef struct irodori_codec_weights {
+    const float* out_proj_w;  /* [proj_dim, latent_dim, 1] quantizer.out_proj */
+    const float* out_proj_b;  /* [proj_dim] */
+    const float* stem_w;      /* [decoder_dim, proj_dim, 7] decoder.model.0 */
+    const float* stem_b;      /* [decoder_dim] */
+    const irodori_codec_block_weights* blocks; /* [num_blocks] */
+    const float* head_alpha;  /* [decoder_dim >> num_blocks] wm_model.encoder_block.pre.0 */
+    const float* head_w;      /* [1, decoder_dim >> num_blocks, 7] pre.1 */
+    const float* head_b;      /* [1] */
+} irodori_codec_weights;
+
+int irodori_codec_create(int device, const irodori_codec_config* cfg, irodori_codec** out);
+int irodori_codec_destroy(irodori_codec* codec);
+int irodori_codec_load_weights(irodori_codec* codec, const irodori_codec_weights* w);
+/* hop_length (codec/model.rs): waveform samples per latent frame, prod(rates). */
+int irodori_codec_hop_length(const irodori_codec* codec);
+/* latent [batch, frames, latent_dim] -> wav [batch, frames * hop] f32; host pointers,
+ * synchronous. */
+int irodori_codec_decode(irodori_codec* codec, int batch, int frames, const float* latent,
+                         float* wav);
+/* The same on device pointers, enqueued on `stream` (NULL: the codec's own stream) without
+ * waiting.  Rows run one after another on the codec's work buffers. */
+int irodori_codec_decode_device(irodori_codec* codec, int batch, int frames,
+                                const float* latent, float* wav, void* stream);
+
 /* ---- operator entry points (device pointers; stream may be NULL) ------------------- */
 /* rms_norm_wgsl (rms_norm.rs:70-142): y = x / sqrt(mean(x^2)+eps) * w, x [rows, dim]. */
 int irodori_op_rms_norm(const float* x, const float* w, int rows, int dim, float eps,

@@ -164,7 +164,7 @@ void launch_timestep_embedding(const float* t, int nvec, int t_dim, float* out, 
 void launch_vec_linear(const VecLinJob* d_jobs, int njobs, int nvec, int max_n, hipStream_t st);
 
 // ---- kernels_gemm.hip ------------------------------------------------------------------
-enum GemmEpi { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_QKVG = 3, EPI_CTXKV = 4, EPI_ADD = 5 };
+enum GemmEpi { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_QKVG = 3, EPI_CTXKV = 4, EPI_ADD = 5, EPI_SNAKE = 6 };
 template <typename T>
 struct GemmArgs {
     const T* A;   // [M, K] row-major
@@ -212,11 +212,24 @@ struct GemmArgs {
     // E8M0 scales U8s [M, N/64]) for the next projection, instead of U.
     uint8_t* U8;
     uint8_t* U8s;
+    // Convolution epilogues (the codec decoder): EPI_STORE and EPI_ADD add bias[n] when it
+    // is set; EPI_SNAKE writes U [M, N] = Snake(acc + bias[n], alpha[n]) in the operand
+    // dtype, Snake(v, a) = v + sin(a v)^2 / (a + 1e-9) (codec/layers.rs:24-31).
+    const float* bias;
+    const float* alpha;
+    // launch_gemm_conv: A is an implicit im2col.  Row m of the GEMM, k = j * conv_cp + c
+    // reads A[(m + j * conv_dil) * conv_cp + c] (A points at the source row the first tap
+    // of output row 0 reads); source rows at or past conv_rows read as zero.
+    int conv_cp, conv_dil, conv_rows;
 };
 template <typename T>
 int launch_gemm(int epi, const GemmArgs<T>& a, hipStream_t st);
 // The same epilogues over fp8 operands (K % 128 == 0); outputs in bf16 / f32 as above.
 int launch_gemm_fp8(int epi, const GemmArgs<bf16>& a, hipStream_t st);
+// Convolution as a GEMM over an implicit im2col (conv_* fields): K = taps * conv_cp with
+// conv_cp a multiple of one 128-byte slice; EPI_STORE, EPI_ADD or EPI_SNAKE.
+template <typename T>
+int launch_gemm_conv(int epi, const GemmArgs<T>& a, hipStream_t st);
 
 // ---- kernels_enc.hip -------------------------------------------------------------------
 // Host f32 [K, N] (Burn layout, on the device) -> K-major [N, K]; mode 1 interleaves the
@@ -232,6 +245,20 @@ template <typename T>
 void launch_enc_head_prep(const float* qkvg, const float* q_norm, const float* k_norm, const float* cs, const float* sn,
                           int M, int S, int H, int Dh, float eps, T* q, T* k, T* v, T* gate, hipStream_t st);
 void launch_enc_mean_token(float* out, const float* mask, uint8_t* mask_out, int B, int S, int E, hipStream_t st);
+
+// ---- kernels_codec.hip -----------------------------------------------------------------
+// DACVAE decoder operands: channels-last [frames, Cp] (Cp % 8 == 0), convolution operands
+// with `halo` zero rows on both sides of the L frames ([L + 2 halo, Cp]).
+template <typename T>
+void launch_codec_snake(const float* x, const float* alpha, int L, int Cp, int halo, T* s, hipStream_t st);
+template <typename T>
+void launch_codec_in(const float* lat, int frames, int Cl, const float* w, const float* b, int Pp, int halo, T* s,
+                     hipStream_t st);
+template <typename T>
+void launch_codec_head(const T* s, int L, int Cp, int halo, const float* w, const float* b, float* wav,
+                       hipStream_t st);
+template <typename T>
+void launch_cvt_f32(const float* src, long n, T* dst, hipStream_t st);
 
 // ---- kernels_fp8.hip -------------------------------------------------------------------
 // Weights w [N, K] f32 (K-major, K % 4 == 0) -> e4m3 codes q [N, K], channel scales s [N].

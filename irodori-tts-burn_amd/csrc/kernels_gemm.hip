@@ -19,6 +19,11 @@
 //   EPI_RESID  x += gate * C            (gated residual, diffusion.rs:98 / :104)
 //   EPI_SWIGLU U = silu(C1) * C3        (feed_forward.rs:80-84; W rows interleaved per 32)
 //   EPI_ADD    x = (x + C) * rmask[row]  (encoder residual + re-mask)
+//   EPI_SNAKE  U = Snake(C + bias)       (codec ResidualUnit's dilated conv + act1)
+// The STORE / ADD epilogues add an optional bias[col].  With CONV set (launch_gemm_conv)
+// the A tile of slice kt is the implicit im2col of a convolution: the slice lies in one
+// tap j = kt * BK / conv_cp, whose source rows sit j * conv_dil rows further down, so only
+// the buffer offset of the A loads changes; the LDS layout and the MFMA loop are the same.
 //   EPI_QKVG   q,k: head RMSNorm (norm.rs:60-74) + half RoPE (rope.rs:82-135);
 //              q pre-scaled by Dh^-1/2 log2(e) for the attention softmax;
 //              v: scatter to V^T [B,H,Dh,S'] (key-permuted); gate: sigmoid (attention.rs:423)
@@ -143,7 +148,8 @@ __device__ __forceinline__ const float* gate_vec(const ModTable& mt, int b, int 
     return mt.tab + ((size_t)vec * mt.layers * 6 + (size_t)layer * 6 + kind * 3 + 2) * D;
 }
 
-template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int EPI, bool F8 = false>
+template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int EPI, bool F8 = false,
+          bool CONV = false>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T> a) {
     constexpr int NW = WAVES_M * WAVES_N;
     constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
@@ -160,6 +166,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
     static_assert(BM % 8 == 0, "a load instruction covers A rows or W rows, not both");
     static_assert((EPI != EPI_QKVG && EPI != EPI_CTXKV) || WN == 64, "QKVG / CTXKV epilogues need one head per wave");
     static_assert(EPI != EPI_SWIGLU || FN % 2 == 0, "SWIGLU epilogue needs column pairs");
+    static_assert(!(F8 && CONV), "convolutions take bf16 / f32 operands");
 
     extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
     const int lane = threadIdx.x & 63;
@@ -183,18 +190,26 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
     // r = 8 (wave*LPW + i) + lane / 8, physical chunk lane % 8 <- logical chunk
     // swz(r, lane % 8).  One SGPR resource per operand tile; A rows past M fall outside
     // the A resource and read as zero.  The slice offset kt * 128 bytes rides in soffset.
-    const int mrows = a.M - m0 < BM ? a.M - m0 : BM;
+    // CONV: A rows are conv_cp elements apart and the resource spans every source row from
+    // m0 on (the taps reach past the tile); rows past conv_rows read as zero.
+    const int lda = CONV ? a.conv_cp : K;
+    int arows = a.M - m0 < BM ? a.M - m0 : BM;
+    if constexpr (CONV) arows = a.conv_rows - m0 > 0 ? a.conv_rows - m0 : 0;
     const unsigned char* Ab = F8 ? a.A8 : reinterpret_cast<const unsigned char*>(a.A);
     const unsigned char* Wb = F8 ? a.W8 : reinterpret_cast<const unsigned char*>(a.W);
-    const __amdgpu_buffer_rsrc_t rA = make_rsrc(Ab + (size_t)m0 * K * ES, (unsigned)(mrows * K * ES));
+    const __amdgpu_buffer_rsrc_t rA = make_rsrc(Ab + (size_t)m0 * lda * ES, (unsigned)((size_t)arows * lda * ES));
     const __amdgpu_buffer_rsrc_t rW = make_rsrc(Wb + (size_t)n0 * K * ES, (unsigned)(BN * K * ES));
     unsigned voff[LPW];
 #pragma unroll
     for (int i = 0; i < LPW; i++) {
         const int r = (wave * LPW + i) * 8 + lane / 8;
         const int rr = r < BM ? r : r - BM;
-        voff[i] = (unsigned)rr * (unsigned)(K * ES) + (unsigned)swz(r, lane % 8) * 16u;
+        voff[i] = (unsigned)rr * (unsigned)((r < BM ? lda : K) * ES) + (unsigned)swz(r, lane % 8) * 16u;
     }
+    // CONV: byte offset of slice kt in the A source = kt * 128 within the row span of its
+    // tap, plus the tap's extra (conv_dil - 1) rows per earlier tap.
+    [[maybe_unused]] const int conv_spt = CONV ? a.conv_cp / BK : 1;
+    [[maybe_unused]] const unsigned conv_dstep = CONV ? (unsigned)((a.conv_dil - 1) * a.conv_cp * ES) : 0u;
     // fp8: the tile's E8M0 block scales (BM rows x K/32 bytes) are staged in LDS past the
     // operand stages before the main loop, slice-major: the word of row r for slice kt (its
     // four k blocks) at (kt * BM + r) * 4, so a wave's 32 rows read 32 consecutive words.
@@ -214,9 +229,11 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
 #define GEMM_ISSUE(kt_, stage_)                                                            \
     do {                                                                                   \
         unsigned char* dst_ = smem + (stage_) * STAGE_BYTES + wave * LPW * 1024;           \
+        const unsigned ws_ = (unsigned)(kt_) * 128u;                                       \
+        const unsigned as_ = CONV ? ws_ + (unsigned)((kt_) / conv_spt) * conv_dstep : ws_; \
         _Pragma("unroll") for (int i_ = 0; i_ < LPW; i_++) {                               \
             const bool isA = (wave * LPW + i_) * 8 < BM;                                   \
-            buf_load_lds16(isA ? rA : rW, voff[i_], (unsigned)(kt_) * 128u, dst_ + i_ * 1024); \
+            buf_load_lds16(isA ? rA : rW, voff[i_], isA ? as_ : ws_, dst_ + i_ * 1024);    \
         }                                                                                  \
     } while (0)
 
@@ -357,6 +374,11 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
     }
 
     // ---- epilogues (acc layout: see rbase / cl above).
+    [[maybe_unused]] float bcol[FN];
+    if constexpr (EPI == EPI_STORE || EPI == EPI_ADD || EPI == EPI_SNAKE) {
+#pragma unroll
+        for (int j = 0; j < FN; j++) bcol[j] = a.bias ? a.bias[n0 + wn0 + 32 * j + cl] : 0.f;
+    }
     if constexpr (EPI == EPI_STORE) {
         float* __restrict__ C = a.C;
 #pragma unroll
@@ -366,7 +388,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
                 int row = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
                 if (row >= a.M) continue;
 #pragma unroll
-                for (int j = 0; j < FN; j++) C[(size_t)row * a.N + n0 + wn0 + 32 * j + cl] = acc[i][j][e];
+                for (int j = 0; j < FN; j++) C[(size_t)row * a.N + n0 + wn0 + 32 * j + cl] = acc[i][j][e] + bcol[j];
             }
     } else if constexpr (EPI == EPI_ADD) {
         float* __restrict__ xg = a.x;
@@ -380,7 +402,28 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
 #pragma unroll
                 for (int j = 0; j < FN; j++) {
                     float* px = xg + (size_t)row * a.N + n0 + wn0 + 32 * j + cl;
-                    *px = (*px + acc[i][j][e]) * rm;
+                    *px = (*px + (acc[i][j][e] + bcol[j])) * rm;
+                }
+            }
+    } else if constexpr (EPI == EPI_SNAKE) {
+        T* __restrict__ U = a.U;
+        float acol[FN], dcol[FN];
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+            acol[j] = a.alpha[n0 + wn0 + 32 * j + cl];
+            dcol[j] = acol[j] + 1e-9f;
+        }
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const int row = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
+                if (row >= a.M) continue;
+#pragma unroll
+                for (int j = 0; j < FN; j++) {
+                    const float v = acc[i][j][e] + bcol[j];
+                    const float sv = sinf(acol[j] * v);
+                    U[(size_t)row * a.N + n0 + wn0 + 32 * j + cl] = from_f32<T>(v + sv * sv / dcol[j]);
                 }
             }
     } else if constexpr (EPI == EPI_RESID) {
@@ -693,24 +736,33 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
     }
 }
 
-template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int EPI, bool F8 = false>
+template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int EPI, bool F8 = false,
+          bool CONV = false>
 int launch_cfg(const GemmArgs<T>& a, hipStream_t st) {
     constexpr int ES = F8 ? 1 : (int)sizeof(T);
     constexpr int BK = 128 / ES;
     constexpr int kMaxK8 = 8192;  // fp8: the staged block scales take BM * K / 32 bytes of LDS
     if (a.M <= 0 || a.N % BN != 0 || a.K % BK != 0 || a.K <= 0 || (F8 && a.K > kMaxK8)) return -1;
     if ((size_t)BN * a.K * ES > 0xffffffffull || (size_t)BM * a.K * ES > 0xffffffffull) return -1;
+    if (CONV) {
+        if (a.conv_cp <= 0 || a.conv_cp % BK != 0 || a.K % a.conv_cp != 0 || a.conv_dil <= 0 || a.conv_rows < 0)
+            return -1;
+        const size_t taps = (size_t)(a.K / a.conv_cp);
+        if ((size_t)a.conv_rows * a.conv_cp * ES > 0xffffffffull ||
+            ((size_t)BM + (taps - 1) * a.conv_dil) * a.conv_cp * ES > 0xffffffffull)
+            return -1;
+    }
     int tiles = ((a.M + BM - 1) / BM) * (a.N / BN);
     const size_t lds = (size_t)STAGES * (BM + BN) * 128 + (F8 ? (size_t)BM * (a.K / 32) : 0);
     static bool attr_set = false;  // per instantiation; the attribute is process-wide
     if (!attr_set) {
         const int lds_max = STAGES * (BM + BN) * 128 + (F8 ? BM * (kMaxK8 / 32) : 0);
-        if (hipFuncSetAttribute((const void*)gemm_kernel<T, BM, BN, WAVES_M, WAVES_N, STAGES, EPI, F8>,
+        if (hipFuncSetAttribute((const void*)gemm_kernel<T, BM, BN, WAVES_M, WAVES_N, STAGES, EPI, F8, CONV>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, lds_max) != hipSuccess)
             return -2;
         attr_set = true;
     }
-    gemm_kernel<T, BM, BN, WAVES_M, WAVES_N, STAGES, EPI, F8><<<tiles, 64 * WAVES_M * WAVES_N, lds, st>>>(a);
+    gemm_kernel<T, BM, BN, WAVES_M, WAVES_N, STAGES, EPI, F8, CONV><<<tiles, 64 * WAVES_M * WAVES_N, lds, st>>>(a);
     return 0;
 }
 
@@ -768,6 +820,28 @@ int launch_gemm_fp8(int epi, const GemmArgs<bf16>& a, hipStream_t st) {
     return -1;
 }
 
+// Convolutions: the residual streams of the codec decoder are 96 .. 1536 channels (padded
+// to 64 / 128) over up to ~10^6 frames, so 128x128 tiles whenever the columns allow.
+template <typename T>
+int launch_gemm_conv(int epi, const GemmArgs<T>& a, hipStream_t st) {
+    const bool wide = a.N % 128 == 0;
+    switch (epi) {
+        case EPI_STORE:
+            if (wide) return launch_cfg<T, 128, 128, 2, 2, 2, EPI_STORE, false, true>(a, st);
+            return launch_cfg<T, 64, 64, 2, 2, 4, EPI_STORE, false, true>(a, st);
+        case EPI_SNAKE:
+            if (!a.U || !a.alpha) return -1;
+            if (wide) return launch_cfg<T, 128, 128, 2, 2, 2, EPI_SNAKE, false, true>(a, st);
+            return launch_cfg<T, 64, 64, 2, 2, 4, EPI_SNAKE, false, true>(a, st);
+        case EPI_ADD:
+            if (wide) return launch_cfg<T, 128, 128, 2, 2, 2, EPI_ADD, false, true>(a, st);
+            return launch_cfg<T, 64, 64, 2, 2, 4, EPI_ADD, false, true>(a, st);
+    }
+    return -1;
+}
+
+template int launch_gemm_conv<bf16>(int, const GemmArgs<bf16>&, hipStream_t);
+template int launch_gemm_conv<float>(int, const GemmArgs<float>&, hipStream_t);
 template int launch_gemm<bf16>(int, const GemmArgs<bf16>&, hipStream_t);
 template int launch_gemm<float>(int, const GemmArgs<float>&, hipStream_t);
 

@@ -4,12 +4,12 @@ Host-side mirror of the reference's inference API for the HIP backend:
 `InferenceBackendKind.HIP_BF16 / HIP_F32`, `SamplerParams`, `GuidanceConfig`, and
 `HipInferenceEngine` (forward_with_cond_cached / sample over libirodori_hip.so).
 """
-from .config import (CfgGuidanceMode, DitConfig, EncoderConfig, GuidanceConfig,
+from .config import (CfgGuidanceMode, CodecConfig, DitConfig, EncoderConfig, GuidanceConfig,
                      InferenceBackendKind, IrodoriError, SamplerMethod, SamplerParams,
-                     cfg_cpu_plumbing, cfg_full_rf, cfg_tiny, enc_speaker_default,
-                     enc_speaker_tiny, enc_text_default, enc_text_tiny)
-from .engine import HipEncoder, HipInferenceEngine, ops
-from .synthetic import (ROLE_COND, ROLE_NO_AUX, ROLE_NO_TEXT, ROLE_UNCOND, ContextKV,
+                     cfg_cpu_plumbing, cfg_full_rf, cfg_tiny, codec_default, codec_tiny,
+                     enc_speaker_default, enc_speaker_tiny, enc_text_default, enc_text_tiny)
+from .engine import HipDacVaeCodec, HipEncoder, HipInferenceEngine, ops
+from .synthetic import (ROLE_COND, ROLE_NO_AUX, ROLE_NO_TEXT, ROLE_UNCOND, CodecWeights, ContextKV,
                         CtxProjWeights, DitWeights, EncoderWeights, make_context_kv, make_noise,
                         make_role_context)
 
@@ -19,5 +19,6 @@ __all__ = [
     "HipInferenceEngine", "HipEncoder", "ops", "ContextKV", "CtxProjWeights", "DitWeights", "make_context_kv", "make_noise",
     "make_role_context", "ROLE_COND", "ROLE_UNCOND", "ROLE_NO_TEXT", "ROLE_NO_AUX",
     "EncoderConfig", "EncoderWeights", "enc_text_default", "enc_speaker_default", "enc_text_tiny",
-    "enc_speaker_tiny",
+    "enc_speaker_tiny", "CodecConfig", "CodecWeights", "HipDacVaeCodec", "codec_default",
+    "codec_tiny",
 ]

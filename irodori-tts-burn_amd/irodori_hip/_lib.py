@@ -95,6 +95,27 @@ class EncoderBlockWeightsC(C.Structure):
     _fields_ = [(n, _f32p) for n in ENC_BLOCK_FIELDS]
 
 
+CODEC_MAX_BLOCKS = 8
+
+
+class CodecConfigC(C.Structure):
+    _fields_ = [("latent_dim", C.c_int32), ("proj_dim", C.c_int32), ("decoder_dim", C.c_int32),
+                ("num_blocks", C.c_int32), ("rates", C.c_int32 * CODEC_MAX_BLOCKS),
+                ("compute_dtype", C.c_int32), ("max_frames", C.c_int32)]
+
+
+class CodecBlockWeightsC(C.Structure):
+    _fields_ = [("alpha", _f32p), ("convt_w", _f32p), ("convt_b", _f32p),
+                ("res_alpha0", _f32p * 3), ("res_conv_w", _f32p * 3), ("res_conv_b", _f32p * 3),
+                ("res_alpha1", _f32p * 3), ("res_pw_w", _f32p * 3), ("res_pw_b", _f32p * 3)]
+
+
+class CodecWeightsC(C.Structure):
+    _fields_ = [("out_proj_w", _f32p), ("out_proj_b", _f32p), ("stem_w", _f32p), ("stem_b", _f32p),
+                ("blocks", C.POINTER(CodecBlockWeightsC)), ("head_alpha", _f32p), ("head_w", _f32p),
+                ("head_b", _f32p)]
+
+
 class KernelTimesC(C.Structure):
     _fields_ = [(n, C.c_float) for n in ("norm_mod_us", "qkvg_gemm_us", "attention_us",
                                           "wo_gemm_us", "w13_gemm_us", "w2_gemm_us", "final_us")]
@@ -138,6 +159,12 @@ SIGNATURES = {
     "irodori_encoder_load_block_weights": (C.c_int, [_vp, C.c_int, C.POINTER(EncoderBlockWeightsC)]),
     "irodori_encoder_forward": (C.c_int, [_vp, C.c_int, C.c_int, C.POINTER(C.c_int32), _f32p,
                                           C.POINTER(C.c_uint8), _f32p, C.POINTER(C.c_uint8)]),
+    "irodori_codec_create": (C.c_int, [C.c_int, C.POINTER(CodecConfigC), C.POINTER(_vp)]),
+    "irodori_codec_destroy": (C.c_int, [_vp]),
+    "irodori_codec_load_weights": (C.c_int, [_vp, C.POINTER(CodecWeightsC)]),
+    "irodori_codec_hop_length": (C.c_int, [_vp]),
+    "irodori_codec_decode": (C.c_int, [_vp, C.c_int, C.c_int, _f32p, _f32p]),
+    "irodori_codec_decode_device": (C.c_int, [_vp, C.c_int, C.c_int, _vp, _vp, _vp]),
     "irodori_op_rms_norm": (C.c_int, [_vp, _vp, C.c_int, C.c_int, C.c_float, _vp, _vp]),
     "irodori_op_fused_adaln": (C.c_int, [_vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_float,
                                          _vp, _vp]),

@@ -146,6 +146,47 @@ def enc_speaker_tiny() -> EncoderConfig:
 
 
 @dataclass
+class CodecConfig:
+    """The DACVAE decoder (codec/weights.rs:225-292): quantizer.out_proj latent_dim ->
+    proj_dim (k 1), the stem proj_dim -> decoder_dim (k 7), one DecoderBlock per rate (the
+    channels halve, ConvTranspose1d kernel 2 * rate), the watermark head to one channel.
+    hop_length = prod(rates) waveform samples per latent frame (codec/model.rs)."""
+
+    latent_dim: int = 32
+    proj_dim: int = 1024
+    decoder_dim: int = 1536
+    rates: tuple = (12, 10, 8, 2)
+    sample_rate: int = 48000
+
+    @property
+    def num_blocks(self) -> int:
+        return len(self.rates)
+
+    @property
+    def hop_length(self) -> int:
+        return int(math.prod(self.rates))
+
+    def block_dims(self, i: int):
+        """(in, out) channels of DecoderBlock i."""
+        return self.decoder_dim >> i, self.decoder_dim >> (i + 1)
+
+    @property
+    def head_dim(self) -> int:
+        return self.decoder_dim >> self.num_blocks
+
+
+def codec_default() -> CodecConfig:
+    """DACVAE as loaded by load_codec (weights.rs:268-292): 1536 -> 96 over rates 12/10/8/2."""
+    return CodecConfig()
+
+
+def codec_tiny() -> CodecConfig:
+    """Small decoder for parity tests: an odd and an even rate, channels 192 -> 96 -> 48
+    (both padded to a multiple of 64 on the GPU)."""
+    return CodecConfig(latent_dim=8, proj_dim=64, decoder_dim=192, rates=(3, 4))
+
+
+@dataclass
 class GuidanceConfig:
     """src/rf/params.rs:9-35 (defaults :23-34)."""
 

@@ -16,9 +16,9 @@ import ctypes as C
 import numpy as np
 
 from . import _lib as L
-from .config import (CfgGuidanceMode, DitConfig, EncoderConfig, InferenceBackendKind, IrodoriError,
-                     SamplerMethod, SamplerParams)
-from .synthetic import ContextKV, CtxProjWeights, DitWeights, EncoderWeights
+from .config import (CfgGuidanceMode, CodecConfig, DitConfig, EncoderConfig, InferenceBackendKind,
+                     IrodoriError, SamplerMethod, SamplerParams)
+from .synthetic import CodecWeights, ContextKV, CtxProjWeights, DitWeights, EncoderWeights
 
 _f32p = C.POINTER(C.c_float)
 
@@ -309,6 +309,83 @@ class HipEncoder:
         _check(self.lib.irodori_encoder_forward(self.enc, B, S, idp, _fp(lat) if lat is not None else None,
                                                 mask.ctypes.data_as(u8), _fp(out), mo.ctypes.data_as(u8)))
         return out, mo
+
+
+class HipDacVaeCodec:
+    """The DACVAE decoder on the GPU (irodori_codec_*): DacVaeCodec::decode
+    (codec/model.rs:60-65) for latents [B, T, latent_dim] -> waveforms [B, 1, T * hop]."""
+
+    def __init__(self, cfg: CodecConfig, backend: InferenceBackendKind = InferenceBackendKind.HIP_BF16,
+                 max_frames: int = 750, device: int = 0):
+        if backend not in (InferenceBackendKind.HIP_BF16, InferenceBackendKind.HIP_F32):
+            raise IrodoriError("Dtype", "the codec runs in bf16 or f32")
+        if cfg.num_blocks > L.CODEC_MAX_BLOCKS:
+            raise IrodoriError("Config", "at most %d decoder blocks" % L.CODEC_MAX_BLOCKS)
+        self.cfg = cfg
+        self.lib = L.load()
+        rates = (C.c_int32 * L.CODEC_MAX_BLOCKS)(*cfg.rates)
+        c = L.CodecConfigC(cfg.latent_dim, cfg.proj_dim, cfg.decoder_dim, cfg.num_blocks, rates,
+                           L.DTYPE_BF16 if backend is InferenceBackendKind.HIP_BF16 else L.DTYPE_F32,
+                           max_frames)
+        h = C.c_void_p()
+        _check(self.lib.irodori_codec_create(device, C.byref(c), C.byref(h)))
+        self.codec = h
+
+    def close(self) -> None:
+        if getattr(self, "codec", None):
+            self.lib.irodori_codec_destroy(self.codec)
+            self.codec = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def sample_rate(self) -> int:
+        return self.cfg.sample_rate
+
+    def hop_length(self) -> int:
+        return int(self.lib.irodori_codec_hop_length(self.codec))
+
+    def load_weights(self, w: CodecWeights) -> None:
+        def p(a):
+            return _fp(_c32(a)) if a is not None else None
+
+        keep = []
+        blocks = (L.CodecBlockWeightsC * self.cfg.num_blocks)()
+        for i, b in enumerate(w.blocks):
+            s = blocks[i]
+            s.alpha, s.convt_w, s.convt_b = p(b["alpha"]), p(b["convt_w"]), p(b["convt_b"])
+            for k in ("res_alpha0", "res_conv_w", "res_conv_b", "res_alpha1", "res_pw_w", "res_pw_b"):
+                arr = getattr(s, k)
+                for u in range(3):
+                    arr[u] = p(b[k][u])
+            keep.append(b)
+        io = w.io
+        cw = L.CodecWeightsC(p(io["out_proj_w"]), p(io["out_proj_b"]), p(io["stem_w"]), p(io["stem_b"]),
+                             blocks, p(io["head_alpha"]), p(io["head_w"]), p(io["head_b"]))
+        _check(self.lib.irodori_codec_load_weights(self.codec, C.byref(cw)))
+        del keep
+
+    def decode(self, latent: np.ndarray) -> np.ndarray:
+        """latent [B, T, latent_dim] -> wav [B, 1, T * hop_length] (host arrays)."""
+        lat = _c32(latent)
+        B, T, _ = lat.shape
+        wav = np.empty((B, 1, T * self.cfg.hop_length), np.float32)
+        _check(self.lib.irodori_codec_decode(self.codec, B, T, _fp(lat), _fp(wav)))
+        return wav
+
+    def decode_device(self, d_latent: int, batch: int, frames: int, d_wav: int, stream: int = 0) -> None:
+        """Device pointers: latent [batch, frames, latent_dim] -> wav [batch, frames * hop]."""
+        _check(self.lib.irodori_codec_decode_device(self.codec, batch, frames, d_latent, d_wav,
+                                                    stream or None))
 
 
 class ops:

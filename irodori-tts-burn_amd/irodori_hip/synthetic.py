@@ -219,3 +219,53 @@ def make_noise(utterances: int, seq: int, latent_dim: int, seed: int = 2) -> np.
     """Initial RF noise x_0 ~ N(0, 1), [U, S, P] (euler_sampler.rs:146-152)."""
     rng = np.random.default_rng(seed)
     return rng.standard_normal((utterances, seq, latent_dim), dtype=np.float32)
+
+
+@dataclass
+class CodecWeights:
+    """DACVAE decoder weights (CodecConfig), Burn layouts (codec/weights.rs): out_proj_w
+    [proj, latent, 1], stem_w [dim, proj, 7], per block alpha [in], convt_w [in, out, 2r],
+    convt_b [out], res_alpha0 / res_conv_w [out, out, 7] / res_conv_b / res_alpha1 /
+    res_pw_w [out, out, 1] / res_pw_b (lists of three), head_alpha [C], head_w [1, C, 7],
+    head_b [1].  Random draws keep the activations of order one: conv weights
+    N(0, gain^2 / fan_in) (residual units 0.5 gain, the head 0.3 gain, so tanh mostly stays
+    off saturation), Snake alphas U(0.5, 2), biases N(0, 0.05^2)."""
+
+    io: dict
+    blocks: list
+
+    @staticmethod
+    def random(cfg, seed: int = 0, gain: float = 1.0, bias: bool = True) -> "CodecWeights":
+        rng = np.random.default_rng(seed)
+
+        def conv(o, i, k, g=gain):
+            return (rng.standard_normal((o, i, k), dtype=np.float32) * np.float32(g / np.sqrt(i * k))).astype(np.float32)
+
+        def vec(n):
+            return (rng.standard_normal(n, dtype=np.float32) * np.float32(0.05)).astype(np.float32) if bias else None
+
+        def alpha(n):
+            return rng.uniform(0.5, 2.0, n).astype(np.float32)
+
+        io = {"out_proj_w": conv(cfg.proj_dim, cfg.latent_dim, 1), "out_proj_b": vec(cfg.proj_dim),
+              "stem_w": conv(cfg.decoder_dim, cfg.proj_dim, 7), "stem_b": vec(cfg.decoder_dim),
+              "head_alpha": alpha(cfg.head_dim), "head_w": conv(1, cfg.head_dim, 7, 0.3 * gain),
+              "head_b": vec(1)}
+        blocks = []
+        for i, r in enumerate(cfg.rates):
+            cin, cout = cfg.block_dims(i)
+            blk = {"alpha": alpha(cin),
+                   "convt_w": (rng.standard_normal((cin, cout, 2 * r), dtype=np.float32)
+                               * np.float32(gain / np.sqrt(2 * cin))).astype(np.float32),
+                   "convt_b": vec(cout)}
+            for k in ("res_alpha0", "res_conv_w", "res_conv_b", "res_alpha1", "res_pw_w", "res_pw_b"):
+                blk[k] = []
+            for _ in range(3):
+                blk["res_alpha0"].append(alpha(cout))
+                blk["res_conv_w"].append(conv(cout, cout, 7, 0.5 * gain))
+                blk["res_conv_b"].append(vec(cout))
+                blk["res_alpha1"].append(alpha(cout))
+                blk["res_pw_w"].append(conv(cout, cout, 1, 0.5 * gain))
+                blk["res_pw_b"].append(vec(cout))
+            blocks.append(blk)
+        return CodecWeights(io, blocks)

@@ -116,6 +116,36 @@ typedef struct orc_enc_block {
     const float* w2;         /* [F, E] */
 } orc_enc_block;
 
+/* DACVAE decoder (src/codec/decoder.rs, layers.rs, bottleneck.rs; built in weights.rs:
+ * 225-292): out_proj Conv1d(latent -> proj, k 1), stem Conv1d(proj -> dim, k 7), blocks i
+ * (Snake, ConvTranspose1d(dim_i -> dim_i / 2, k 2 r_i, stride r_i), ResidualUnits with
+ * dilations 1, 3, 9), head (Snake, Conv1d(-> 1, k 7), tanh).  Burn layouts: Conv1d weight
+ * [out, in, k], ConvTranspose1d weight [in, out, k]; Snake alpha [C]. */
+typedef struct orc_codec_block {
+    const float* alpha;        /* [in] */
+    const float* convt_w;      /* [in, out, 2 r] */
+    const float* convt_b;      /* [out] */
+    const float* res_alpha0[3];
+    const float* res_conv_w[3];  /* [out, out, 7] */
+    const float* res_conv_b[3];
+    const float* res_alpha1[3];
+    const float* res_pw_w[3];    /* [out, out, 1] */
+    const float* res_pw_b[3];
+} orc_codec_block;
+
+typedef struct orc_codec {
+    int32_t latent_dim, proj_dim, decoder_dim, num_blocks;
+    int32_t rates[8];
+    const float* out_proj_w;  /* [proj, latent, 1] */
+    const float* out_proj_b;
+    const float* stem_w;      /* [dim, proj, 7] */
+    const float* stem_b;
+    const orc_codec_block* blocks;
+    const float* head_alpha;  /* [dim >> num_blocks] */
+    const float* head_w;      /* [1, dim >> num_blocks, 7] */
+    const float* head_b;      /* [1] */
+} orc_codec;
+
 /* fp8 (e4m3fn) GEMM operands (oracle.c). */
 uint8_t orc_e4m3_encode(float x);
 float orc_e4m3_decode(uint8_t b);
@@ -150,6 +180,12 @@ int orc_get_threads(void);
                           const float* cond, int B, float* shift, float* scale,            \
                           float* gate);                                                     \
     void P##gemm_fp8(const float* x, const float* w, int M, int K, int N, float* y);      \
+    void P##conv1d(const float* x, int C, int L, const float* w, const float* b, int O,    \
+                   int k, int dil, int pad, float* y);                                      \
+    void P##conv_transpose1d(const float* x, int C, int L, const float* w, const float* b, \
+                             int O, int k, int stride, int pad, int pad_out, float* y);     \
+    void P##snake(const float* x, const float* alpha, int C, int L, float* y);             \
+    void P##codec_decode(const orc_codec* cd, int B, int T, const float* latent, float* wav); \
     void P##text_block(const orc_enc_cfg* c, const orc_enc_block* blk, float* x,           \
                        const uint8_t* mask, int B, int S, const float* cos_t,              \
                        const float* sin_t);                                                 \

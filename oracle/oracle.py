@@ -56,6 +56,20 @@ class OrcEncBlock(C.Structure):
                                      "k_norm", "mlp_norm", "w13", "w2")]
 
 
+class OrcCodecBlock(C.Structure):
+    _fields_ = [("alpha", _f32p), ("convt_w", _f32p), ("convt_b", _f32p),
+                ("res_alpha0", _f32p * 3), ("res_conv_w", _f32p * 3), ("res_conv_b", _f32p * 3),
+                ("res_alpha1", _f32p * 3), ("res_pw_w", _f32p * 3), ("res_pw_b", _f32p * 3)]
+
+
+class OrcCodec(C.Structure):
+    _fields_ = [("latent_dim", C.c_int32), ("proj_dim", C.c_int32), ("decoder_dim", C.c_int32),
+                ("num_blocks", C.c_int32), ("rates", C.c_int32 * 8), ("out_proj_w", _f32p),
+                ("out_proj_b", _f32p), ("stem_w", _f32p), ("stem_b", _f32p),
+                ("blocks", C.POINTER(OrcCodecBlock)), ("head_alpha", _f32p), ("head_w", _f32p),
+                ("head_b", _f32p)]
+
+
 class OrcSampler(C.Structure):
     """orc_sampler (oracle.h): the sampler parameters and request facts."""
     _fields_ = [
@@ -349,6 +363,73 @@ class Oracle:
             _f(lat) if lat is not None else None, _u8(mask), _f(out), _u8(mo))
         del keep
         return out, mo
+
+    # ---- DACVAE decoder -------------------------------------------------------------
+    def conv1d(self, x, w, b=None, dilation=1, padding=0):
+        """Conv1d, stride 1: x [C, L], w [O, C, k] (Burn layout), b [O] -> [O, L_out]."""
+        x, w = _c32(x), _c32(w)
+        Cc, L = x.shape
+        O, _, k = w.shape
+        Lo = L + 2 * padding - dilation * (k - 1)
+        y = np.empty((O, Lo), np.float32)
+        bb = _c32(b) if b is not None else None
+        self._fn("conv1d")(_f(x), Cc, L, _f(w), _f(bb) if bb is not None else None, O, k, dilation,
+                           padding, _f(y))
+        return y
+
+    def conv_transpose1d(self, x, w, b=None, stride=1, padding=0, output_padding=0):
+        """ConvTranspose1d: x [C, L], w [C, O, k] (Burn layout), b [O] -> [O, L_out]."""
+        x, w = _c32(x), _c32(w)
+        Cc, L = x.shape
+        _, O, k = w.shape
+        Lo = (L - 1) * stride - 2 * padding + k + output_padding
+        y = np.empty((O, Lo), np.float32)
+        bb = _c32(b) if b is not None else None
+        self._fn("conv_transpose1d")(_f(x), Cc, L, _f(w), _f(bb) if bb is not None else None, O, k,
+                                     stride, padding, output_padding, _f(y))
+        return y
+
+    def snake(self, x, alpha):
+        """Snake1d: x [C, L], alpha [C]."""
+        x, alpha = _c32(x), _c32(alpha)
+        y = np.empty_like(x)
+        self._fn("snake")(_f(x), _f(alpha), x.shape[0], x.shape[1], _f(y))
+        return y
+
+    def codec_decode(self, ccfg, cw, latent):
+        """DacVaeCodec::decode: latent [B, T, latent_dim] -> wav [B, 1, T * hop]."""
+        lat = _c32(latent)
+        B, T, _ = lat.shape
+
+        def p(a):
+            return _f(_c32(a)) if a is not None else None
+
+        keep = []
+
+        def q(a):
+            if a is None:
+                return None
+            a = _c32(a)
+            keep.append(a)
+            return _f(a)
+
+        blocks = (OrcCodecBlock * ccfg.num_blocks)()
+        for i, b in enumerate(cw.blocks):
+            s = blocks[i]
+            s.alpha, s.convt_w, s.convt_b = q(b["alpha"]), q(b["convt_w"]), q(b["convt_b"])
+            for k in ("res_alpha0", "res_conv_w", "res_conv_b", "res_alpha1", "res_pw_w", "res_pw_b"):
+                arr = getattr(s, k)
+                for u in range(3):
+                    arr[u] = q(b[k][u])
+        io = cw.io
+        cd = OrcCodec(ccfg.latent_dim, ccfg.proj_dim, ccfg.decoder_dim, ccfg.num_blocks,
+                      (C.c_int32 * 8)(*ccfg.rates), q(io["out_proj_w"]), q(io["out_proj_b"]),
+                      q(io["stem_w"]), q(io["stem_b"]), blocks, q(io["head_alpha"]), q(io["head_w"]),
+                      q(io["head_b"]))
+        wav = np.empty((B, 1, T * ccfg.hop_length), np.float32)
+        self._fn("codec_decode")(C.byref(cd), B, T, _f(lat), _f(wav))
+        del keep, p
+        return wav
 
     def swiglu(self, h, w13, w2):
         h = _c32(h)

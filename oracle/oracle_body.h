@@ -801,3 +801,105 @@ void P(encoder_forward)(const orc_enc_cfg* c, const orc_enc_block* blocks, const
     }
     free(x); free(st); free(cs); free(sn);
 }
+
+/* Conv1d (stride 1) on channels-first x [C, L]: y[o, t] = b[o] + sum_{c, j} w[o, c, j]
+ * x[c, t + j dil - pad], zero outside [0, L); y [O, L_out], L_out = L + 2 pad - dil (k - 1)
+ * (burn Conv1d with PaddingConfig1d::Explicit(pad, pad), layers.rs:70-93). */
+void P(conv1d)(const float* x, int C, int L, const float* w, const float* b, int O, int k, int dil, int pad,
+               float* y) {
+    const int Lo = L + 2 * pad - dil * (k - 1);
+    #pragma omp parallel for schedule(static)
+    for (int o = 0; o < O; o++)
+        for (int t = 0; t < Lo; t++) {
+            R acc = b ? (R)b[o] : R_C(0.0);
+            for (int c = 0; c < C; c++)
+                for (int j = 0; j < k; j++) {
+                    const int src = t + j * dil - pad;
+                    if (src >= 0 && src < L) acc += (R)w[((size_t)o * C + c) * k + j] * (R)x[(size_t)c * L + src];
+                }
+            y[(size_t)o * Lo + t] = (float)acc;
+        }
+}
+
+/* ConvTranspose1d on x [C, L]: y[o, t] = b[o] + sum over (i, j) with i stride - pad + j = t
+ * of w[c, o, j] x[c, i]; y [O, L_out], L_out = (L - 1) stride - 2 pad + k + pad_out
+ * (weights.rs:80-103 with conv_transpose_pad, layers.rs:62-65). */
+void P(conv_transpose1d)(const float* x, int C, int L, const float* w, const float* b, int O, int k, int stride,
+                         int pad, int pad_out, float* y) {
+    const int Lo = (L - 1) * stride - 2 * pad + k + pad_out;
+    #pragma omp parallel for schedule(static)
+    for (int o = 0; o < O; o++)
+        for (int t = 0; t < Lo; t++) {
+            R acc = b ? (R)b[o] : R_C(0.0);
+            for (int j = 0; j < k; j++) {
+                const int num = t + pad - j;
+                if (num < 0 || num % stride) continue;
+                const int i = num / stride;
+                if (i >= L) continue;
+                for (int c = 0; c < C; c++) acc += (R)w[((size_t)c * O + o) * k + j] * (R)x[(size_t)c * L + i];
+            }
+            y[(size_t)o * Lo + t] = (float)acc;
+        }
+}
+
+/* Snake1d (layers.rs:24-31): y = x + sin(alpha x)^2 / (alpha + 1e-9), alpha per channel. */
+void P(snake)(const float* x, const float* alpha, int C, int L, float* y) {
+    for (int c = 0; c < C; c++) {
+        const R a = (R)alpha[c];
+        for (int t = 0; t < L; t++) {
+            const R v = (R)x[(size_t)c * L + t];
+            const R sv = SIN(a * v);
+            y[(size_t)c * L + t] = (float)(v + sv * sv / (a + (R)1e-9f));
+        }
+    }
+}
+
+/* DacVaeCodec::decode (model.rs:33-38): latent [B, T, latent_dim] -> wav [B, T * hop],
+ * hop = prod(rates); per row channels-first, as the reference. */
+void P(codec_decode)(const orc_codec* cd, int B, int T, const float* latent, float* wav) {
+    int hop = 1;
+    for (int i = 0; i < cd->num_blocks; i++) hop *= cd->rates[i];
+    size_t cap = (size_t)cd->decoder_dim * T;
+    {
+        int L = T, C = cd->decoder_dim;
+        for (int i = 0; i < cd->num_blocks; i++) {
+            L *= cd->rates[i];
+            C /= 2;
+            if ((size_t)C * L > cap) cap = (size_t)C * L;
+        }
+        if ((size_t)cd->proj_dim * T > cap) cap = (size_t)cd->proj_dim * T;
+    }
+    float* a = (float*)malloc(sizeof(float) * cap);
+    float* b2 = (float*)malloc(sizeof(float) * cap);
+    float* c2 = (float*)malloc(sizeof(float) * cap);
+    for (int bb = 0; bb < B; bb++) {
+        int L = T, C = cd->latent_dim;
+        for (int ch = 0; ch < C; ch++)
+            for (int t = 0; t < L; t++) a[(size_t)ch * L + t] = latent[((size_t)bb * T + t) * C + ch];
+        P(conv1d)(a, C, L, cd->out_proj_w, cd->out_proj_b, cd->proj_dim, 1, 1, 0, b2);
+        C = cd->proj_dim;
+        P(conv1d)(b2, C, L, cd->stem_w, cd->stem_b, cd->decoder_dim, 7, 1, 3, a);
+        C = cd->decoder_dim;
+        for (int i = 0; i < cd->num_blocks; i++) {
+            const orc_codec_block* bl = &cd->blocks[i];
+            const int r = cd->rates[i], O = C / 2;
+            P(snake)(a, bl->alpha, C, L, b2);
+            P(conv_transpose1d)(b2, C, L, bl->convt_w, bl->convt_b, O, 2 * r, r, (r + 1) / 2, r % 2, a);
+            L *= r;
+            C = O;
+            static const int dils[3] = {1, 3, 9};
+            for (int u = 0; u < 3; u++) {
+                P(snake)(a, bl->res_alpha0[u], C, L, b2);
+                P(conv1d)(b2, C, L, bl->res_conv_w[u], bl->res_conv_b[u], C, 7, dils[u], 3 * dils[u], c2);
+                P(snake)(c2, bl->res_alpha1[u], C, L, b2);
+                P(conv1d)(b2, C, L, bl->res_pw_w[u], bl->res_pw_b[u], C, 1, 1, 0, c2);
+                for (size_t e = 0; e < (size_t)C * L; e++) a[e] = (float)((R)a[e] + (R)c2[e]);
+            }
+        }
+        P(snake)(a, cd->head_alpha, C, L, b2);
+        P(conv1d)(b2, C, L, cd->head_w, cd->head_b, 1, 7, 1, 3, c2);
+        for (int t = 0; t < L; t++) wav[(size_t)bb * L + t] = (float)TANH((R)c2[t]);
+        (void)hop;
+    }
+    free(a); free(b2); free(c2);
+}

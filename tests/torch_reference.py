@@ -159,3 +159,34 @@ def encoder_forward(ecfg, ew, mask, ids=None, latent=None):
         st = torch.cat([mean, st], 1)
         mo = torch.cat([(cnt[:, 0, 0] > 0).to(torch.uint8)[:, None], mo], 1)
     return st.numpy(), mo.numpy()
+
+
+# ---- DACVAE decoder (codec/model.rs:60-65, decoder.rs, layers.rs, bottleneck.rs) ----------
+def snake(x, alpha):
+    a = T(alpha)[None, :, None]
+    return x + torch.sin(a * x).pow(2) / (a + 1e-9)
+
+
+def _b(v):
+    return None if v is None else T(v)
+
+
+def codec_decode(ccfg, cw, latent):
+    """latent [B, T, latent_dim] -> wav [B, 1, T * hop] with F.conv1d / F.conv_transpose1d
+    (PyTorch's ConvTranspose1d padding rule of layers.rs:62-65)."""
+    x = T(latent).transpose(1, 2)
+    io = cw.io
+    x = F.conv1d(x, T(io["out_proj_w"]), _b(io["out_proj_b"]))
+    x = F.conv1d(x, T(io["stem_w"]), _b(io["stem_b"]), padding=3)
+    for blk, r in zip(cw.blocks, ccfg.rates):
+        x = snake(x, blk["alpha"])
+        x = F.conv_transpose1d(x, T(blk["convt_w"]), _b(blk["convt_b"]), stride=r, padding=(r + 1) // 2,
+                               output_padding=r % 2)
+        for u, d in enumerate((1, 3, 9)):
+            y = snake(x, blk["res_alpha0"][u])
+            y = F.conv1d(y, T(blk["res_conv_w"][u]), _b(blk["res_conv_b"][u]), padding=3 * d, dilation=d)
+            y = snake(y, blk["res_alpha1"][u])
+            y = F.conv1d(y, T(blk["res_pw_w"][u]), _b(blk["res_pw_b"][u]))
+            x = x + y
+    x = snake(x, io["head_alpha"])
+    return torch.tanh(F.conv1d(x, T(io["head_w"]), _b(io["head_b"]), padding=3)).numpy()
