@@ -99,9 +99,13 @@ def main():
     ap.add_argument("--profile-iters", type=int, default=50)
     ap.add_argument("--cfg5-dtype", choices=["fp8", "bf16"], default="fp8",
                     help="compute mode of --workload cfg5 (config 5 names fp8 weights)")
-    ap.add_argument("--workload", choices=["cfg4", "cfg5", "encode"], default="cfg4",
+    ap.add_argument("--workload", choices=["cfg4", "cfg5", "encode", "codec"], default="cfg4",
                     help="cfg4 (default): the headline B=2 Joint-CFG RF run; cfg5: batched "
-                         "throughput, 16 utterances x 2 CFG rows, lengths U[200,750] padded")
+                         "throughput, 16 utterances x 2 CFG rows, lengths U[200,750] padded; "
+                         "encode: per-request conditioning; codec: DACVAE decode of config 4's "
+                         "two 750-frame latents")
+    ap.add_argument("--codec-dtype", choices=["bf16", "f32"], default="bf16",
+                    help="compute mode of --workload codec")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run one 1 GiB device-to-device copy (the known-size kernel that "
                          "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings; 32x the L2, so "
@@ -129,6 +133,9 @@ def main():
         return
     if args.workload == "encode":
         print(json.dumps(run_encode(args, np, torch, ih)), flush=True)
+        return
+    if args.workload == "codec":
+        print(json.dumps(run_codec(args, np, torch, ih)), flush=True)
         return
 
     cfg = ih.cfg_full_rf()
@@ -406,6 +413,94 @@ def run_encode(args, np, torch, ih):
                      "context_build": round(kv_ms, 3)},
         "achieved_tflops": round(flops / (ms * 1e-3) / 1e12, 1),
         "roofline": None,
+        "cpu_baseline": cpu,
+    }
+
+
+def codec_flops(ccfg, T):
+    """Algorithmic FLOPs of DacVaeCodec::decode over T latent frames (unpadded channels):
+    out_proj, stem (k 7), per block the transposed convolution (two taps of C inputs per
+    output frame) and three ResidualUnits (k 7 + k 1), the head (k 7 to one channel)."""
+    f = 2.0 * T * ccfg.latent_dim * ccfg.proj_dim + 2.0 * T * ccfg.proj_dim * ccfg.decoder_dim * 7
+    L = T
+    for i, r in enumerate(ccfg.rates):
+        C, O = ccfg.block_dims(i)
+        L *= r
+        f += 2.0 * L * O * 2 * C + 3 * (2.0 * L * O * O * 7 + 2.0 * L * O * O)
+    return f + 2.0 * L * ccfg.head_dim * 7
+
+
+def run_codec(args, np, torch, ih):
+    """The DACVAE decode of config 4's output (codec/model.rs:60-65): two 750-frame latents
+    -> two 1.44 M-sample waveforms (2 x 30 s at 48 kHz), latents already in HBM
+    (irodori_codec_decode_device), timed with events on the codec's stream.
+    value = ms per decode of both rows."""
+    ccfg = ih.codec_default()
+    backend = ih.InferenceBackendKind.HIP_BF16 if args.codec_dtype == "bf16" else ih.InferenceBackendKind.HIP_F32
+    B, T = 2, 750
+    log("codec: generating weights (DACVAE decoder, 1536 -> 96 over rates 12/10/8/2)")
+    cw = ih.CodecWeights.random(ccfg, 1)
+    codec = ih.HipDacVaeCodec(ccfg, backend, max_frames=T)
+    codec.load_weights(cw)
+    lat = np.random.default_rng(2).standard_normal((B, T, ccfg.latent_dim)).astype(np.float32)
+    d_lat = torch.from_numpy(lat).cuda()
+    d_wav = torch.empty((B, T * ccfg.hop_length), dtype=torch.float32, device="cuda")
+    # A stream of its own (default priority): the events below must sit on the stream the
+    # decode is enqueued on (handle 0, torch's default stream, would mean the codec's own).
+    st = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        codec.decode_device(d_lat.data_ptr(), B, T, d_wav.data_ptr(), st.cuda_stream)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(st)
+    for _ in range(args.steps):
+        codec.decode_device(d_lat.data_ptr(), B, T, d_wav.data_ptr(), st.cuda_stream)
+    e1.record(st)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / args.steps
+    ms = e0.elapsed_time(e1) / args.steps
+    flops = B * codec_flops(ccfg, T)
+    samples = B * T * ccfg.hop_length
+    log("codec: %.3f ms per decode (wall %.3f ms), %.1f TFLOP/s algorithmic, %.0fx real time"
+        % (ms, wall, flops / (ms * 1e-3) / 1e12, samples / ccfg.sample_rate / (ms * 1e-3)))
+    wav = d_wav.cpu().numpy()
+    if not np.isfinite(wav).all():
+        raise RuntimeError("codec produced non-finite samples")
+    codec.close()
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle.oracle import Oracle, get_threads, set_threads
+        if args.cpu_threads:
+            set_threads(args.cpu_threads)
+        n = 6
+        t0 = time.perf_counter()
+        Oracle("f32").codec_decode(ccfg, cw, lat[:1, :n])
+        sec = time.perf_counter() - t0
+        cpu = {"value": round(sec / n * T * B * 1e3, 1), "unit": "ms (extrapolated)",
+               "cores": get_threads(), "kind": "port",
+               "sample": "%d latent frames of one row (f32 C oracle, OpenMP), measured %.2f s, "
+                         "scaled linearly to 2 x 750 frames" % (n, sec)}
+    achieved = flops / (ms * 1e-3) / 1e12
+    return {
+        "metric": "DACVAE decode ms (2 x 750 latent frames -> 2 x 1.44 M samples at 48 kHz)",
+        "value": round(ms, 3), "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 3), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": args.codec_dtype,
+        "data": "synthetic: random-init DACVAE decoder (Snake alphas U(0.5, 2)), N(0,1) latents",
+        "config": {"workload": "DACVAE decoder (out_proj 32->1024, stem 1024->1536 k7, 4 DecoderBlocks "
+                               "rates 12/10/8/2 with 3 ResidualUnits each, watermark head), config 4's "
+                               "two 750-frame rows; latents resident in HBM",
+                   "global_batch": B, "seq_len": T, "parallelism": "none"},
+        "realtime_factor": round(samples / ccfg.sample_rate / (ms * 1e-3), 1),
+        "achieved_tflops": round(achieved, 1),
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS
+                     if args.codec_dtype == "bf16" else 157.3, "unit": "TFLOP/s",
+                     "frac": round(achieved / (PEAK_BF16_TFLOPS if args.codec_dtype == "bf16" else 157.3), 4),
+                     "traffic": None,
+                     "scope": "whole decode: algorithmic convolution FLOPs (unpadded channels) over the "
+                              "event-timed decode, element-wise passes included"},
         "cpu_baseline": cpu,
     }
 

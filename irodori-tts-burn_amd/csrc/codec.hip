@@ -10,13 +10,13 @@
 //   s = out_proj(latent)                     codec_in_kernel        -> S  [T + 2h, Pp]
 //   x = stem(s)     (k 7, pad 3)             conv GEMM EPI_STORE    -> X  [T, Dp]
 //   per DecoderBlock (rate r, C -> O = C / 2):
-//     s = Snake(x)                           snake_rows_kernel      -> S
-//     x = ConvTranspose1d(s) (k 2r)          conv GEMM EPI_STORE    -> X  (see below)
+//     x = ConvTranspose1d(Snake(x)) (k 2r)   conv GEMM EPI_STORE    -> X  (see below)
 //     per ResidualUnit (dilation 1, 3, 9):
-//       s  = Snake(x)                        snake_rows_kernel      -> S
-//       s2 = Snake(conv_k7(s) + b)           conv GEMM EPI_SNAKE    -> S2 [L, Op]
+//       s2 = Snake(conv_k7(Snake(x)) + b)    conv GEMM EPI_SNAKE    -> S2 [L, Op]
 //       x += conv_1x1(s2) + b                GEMM EPI_ADD
-//   wav = tanh(head_conv_k7(Snake(x)))       snake_rows + codec_head_kernel
+//   wav = tanh(head_conv_k7(Snake(x)))       codec_head_kernel
+// A Snake of x that feeds a convolution is written by the epilogue producing x (the stem,
+// the transposed convolution, the 1x1 residual add) into the haloed operand S / S3.
 //
 // ConvTranspose1d(stride r, kernel 2r, padding ceil(r/2), output padding r % 2) as one
 // GEMM: output frame t with t + pad = i r + q (0 <= q < r) sums input frame i through tap
@@ -45,10 +45,10 @@ inline int round64(int c) { return (c + 63) / 64 * 64; }
 
 struct CodecBlock {
     int cin = 0, cout = 0, cin_p = 0, cout_p = 0, rate = 0;
-    float* alpha = nullptr;  // [cin_p]
+    float* alpha = nullptr;  // Snake constants [3, cin_p] (snake_consts)
     void* wt = nullptr;      // [rate * cout_p, 2 * cin_p]: row (q, o), k (tap window, c)
     float* bt = nullptr;     // [rate * cout_p] bias per (q, o)
-    float* ra0[3] = {};      // [cout_p]
+    float* ra0[3] = {};      // [3, cout_p]
     void* rw[3] = {};        // [cout_p, 7 * cout_p]
     float* rb[3] = {};       // [cout_p] or null
     float* ra1[3] = {};
@@ -70,11 +70,12 @@ struct irodori_codec {
     void* stem_w = nullptr;                  // [dim_p, 7 * proj_p]
     float* stem_b = nullptr;                 // [dim_p] or null
     std::vector<CodecBlock> blocks;
-    float *head_alpha = nullptr, *head_w = nullptr, *head_b = nullptr;  // [last_p], [7, last_p], [1]
+    float *head_alpha = nullptr, *head_w = nullptr, *head_b = nullptr;  // [3, last_p], [7, last_p], [1]
     bool loaded = false;
     size_t x_elems = 0, s_elems = 0, s2_elems = 0;
     float* X = nullptr;  // residual stream (and the transposed convolutions' output)
     void* S = nullptr;   // haloed convolution operand
+    void* S3 = nullptr;  // the other haloed operand (S and S3 alternate)
     void* S2 = nullptr;  // the 1x1 convolutions' operand
     float* lat = nullptr;  // [max_frames, latent_dim] staging of the host entry point
     float* wav = nullptr;  // [max_frames * hop]
@@ -149,6 +150,18 @@ std::vector<float> convt_rows(const float* w, int C, int O, int r, int Cp, int O
     return out;
 }
 
+// Snake constants of a channel vector a [n], padded to np: the block [3, np] = (a, a / pi,
+// 0.5 / (a + 1e-9)) in f32, all zero past n (a padded channel carries exact zeros).
+std::vector<float> snake_consts(const float* a, int n, int np) {
+    std::vector<float> out((size_t)3 * np, 0.f);
+    for (int i = 0; i < n; i++) {
+        out[i] = a[i];
+        out[np + i] = a[i] / 3.14159265358979f;
+        out[2 * np + i] = 0.5f / (a[i] + 1e-9f);
+    }
+    return out;
+}
+
 // A per-channel vector padded with zeros to np entries, repeated `rep` times.
 std::vector<float> padded(const float* v, int n, int np, int rep = 1) {
     std::vector<float> out((size_t)np * rep, 0.f);
@@ -158,63 +171,151 @@ std::vector<float> padded(const float* v, int n, int np, int rep = 1) {
     return out;
 }
 
+// One convolution GEMM.  `cp` > 0: implicit im2col over taps = K / cp source rows spaced
+// `dil` (launch_gemm_conv); 0: a plain GEMM (the 1x1 convolutions).  `U` (with its Snake
+// constants `alpha` of alpha_n channels and the window [u_lo, u_hi) of linear output
+// indices) receives Snake(output) for the next convolution.
 template <typename T>
-int codec_conv(irodori_codec* c, int epi, const T* A, int cp, int dil, int rows, int M, int N, int K, const void* W,
-               const float* bias, const float* alpha, float* C, T* U, hipStream_t st) {
+struct ConvCall {
+    int epi = EPI_STORE;
+    const T* A = nullptr;
+    int cp = 0, dil = 1, rows = 0, M = 0, N = 0, K = 0;
+    const void* W = nullptr;
+    const float* bias = nullptr;
+    const float* alpha = nullptr;
+    int alpha_n = 0;
+    float* C = nullptr;
+    T* U = nullptr;
+    long u_lo = 0, u_hi = 0;
+};
+
+template <typename T>
+int codec_conv(const ConvCall<T>& k, hipStream_t st) {
     GemmArgs<T> ga{};
-    ga.A = A;
-    ga.W = static_cast<const T*>(W);
-    ga.M = M;
-    ga.N = N;
-    ga.K = K;
-    ga.S = M;
-    ga.C = C;
-    ga.x = C;
-    ga.U = U;
-    ga.bias = bias;
-    ga.alpha = alpha;
-    ga.conv_cp = cp;
-    ga.conv_dil = dil;
-    ga.conv_rows = rows;
-    const int rc = cp > 0 ? launch_gemm_conv<T>(epi, ga, st) : launch_gemm<T>(epi, ga, st);
+    ga.A = k.A;
+    ga.W = static_cast<const T*>(k.W);
+    ga.M = k.M;
+    ga.N = k.N;
+    ga.K = k.K;
+    ga.S = k.M;
+    ga.C = k.C;
+    ga.x = k.C;
+    ga.U = k.U;
+    ga.bias = k.bias;
+    ga.alpha = k.alpha;
+    ga.alpha_n = k.alpha_n;
+    ga.u_lo = k.u_lo;
+    ga.u_hi = k.u_hi;
+    ga.conv_cp = k.cp;
+    ga.conv_dil = k.dil;
+    ga.conv_rows = k.rows;
+    const int rc = k.cp > 0 ? launch_gemm_conv<T>(k.epi, ga, st) : launch_gemm<T>(k.epi, ga, st);
     if (rc) {
-        set_last_error("codec convolution GEMM rejected the shape (M " + std::to_string(M) + ", N " +
-                       std::to_string(N) + ", K " + std::to_string(K) + ")");
+        set_last_error("codec convolution GEMM rejected the shape (M " + std::to_string(k.M) + ", N " +
+                       std::to_string(k.N) + ", K " + std::to_string(k.K) + ")");
         return IRODORI_ERR_SHAPE;
     }
     return IRODORI_OK;
 }
 
 // One utterance row: lat [frames, latent_dim] -> wav [frames * hop], device pointers.
+// Every Snake except the head's is applied in the epilogue of the GEMM that produces its
+// input (stem, transposed convolution, 1x1 residual add), which writes the next
+// convolution's haloed operand: two operand buffers alternate (a convolution never writes
+// the buffer it reads), and each new operand layout gets its halo rows zeroed.
 template <typename T>
 int codec_row(irodori_codec* c, const float* lat, int frames, float* wav, hipStream_t st) {
     const auto& g = c->cfg;
     const int H = kHalo;
-    T* S = static_cast<T*>(c->S);
+    T* cur = static_cast<T*>(c->S);
+    T* nxt = static_cast<T*>(c->S3);
     T* S2 = static_cast<T*>(c->S2);
-    launch_codec_in<T>(lat, frames, g.latent_dim, c->in_w, c->in_b, c->proj_p, H, S, st);
+    launch_codec_in<T>(lat, frames, g.latent_dim, c->in_w, c->in_b, c->proj_p, H, cur, st);
     int L = frames;
-    IRO_TRY(codec_conv<T>(c, EPI_STORE, S + (size_t)(H - 3) * c->proj_p, c->proj_p, 1, L + H + 3, L, c->dim_p,
-                          7 * c->proj_p, c->stem_w, c->stem_b, nullptr, c->X, nullptr, st));
+    {  // stem; its epilogue writes Snake(x) of block 0's entry into nxt
+        const CodecBlock& b0 = c->blocks[0];
+        launch_codec_zero_halo<T>(nxt, L, c->dim_p, H, st);
+        ConvCall<T> k;
+        k.A = cur + (size_t)(H - 3) * c->proj_p;
+        k.cp = c->proj_p;
+        k.rows = L + H + 3;
+        k.M = L;
+        k.N = c->dim_p;
+        k.K = 7 * c->proj_p;
+        k.W = c->stem_w;
+        k.bias = c->stem_b;
+        k.C = c->X;
+        k.U = nxt + (size_t)H * c->dim_p;
+        k.alpha = b0.alpha;
+        k.alpha_n = b0.cin_p;
+        k.u_hi = (long)L * c->dim_p;
+        IRO_TRY(codec_conv<T>(k, st));
+        std::swap(cur, nxt);
+    }
     float* x = c->X;
-    for (const CodecBlock& b : c->blocks) {
-        launch_codec_snake<T>(x, b.alpha, L, b.cin_p, H, S, st);
-        const int pad = (b.rate + 1) / 2;
-        IRO_TRY(codec_conv<T>(c, EPI_STORE, S + (size_t)(H - 1) * b.cin_p, b.cin_p, 1, L + H + 1, L + 1,
-                              b.rate * b.cout_p, 2 * b.cin_p, b.wt, b.bt, nullptr, c->X, nullptr, st));
-        x = c->X + (size_t)pad * b.cout_p;
-        L *= b.rate;
-        const int Op = b.cout_p;
+    for (size_t bi = 0; bi < c->blocks.size(); bi++) {
+        const CodecBlock& b = c->blocks[bi];
+        const int pad = (b.rate + 1) / 2, Op = b.cout_p, Lo = L * b.rate;
+        {  // transposed convolution; the epilogue writes Snake(x) of unit 0 into nxt
+            launch_codec_zero_halo<T>(nxt, Lo, Op, H, st);
+            ConvCall<T> k;
+            k.A = cur + (size_t)(H - 1) * b.cin_p;
+            k.cp = b.cin_p;
+            k.rows = L + H + 1;
+            k.M = L + 1;
+            k.N = b.rate * Op;
+            k.K = 2 * b.cin_p;
+            k.W = b.wt;
+            k.bias = b.bt;
+            k.C = c->X;
+            // Row i, column (q, o) is frame i r + q - pad: the operand row frame + H.
+            k.U = nxt + (size_t)(H - pad) * Op;
+            k.alpha = b.ra0[0];
+            k.alpha_n = Op;
+            k.u_lo = (long)pad * Op;
+            k.u_hi = (long)(pad + Lo) * Op;
+            IRO_TRY(codec_conv<T>(k, st));
+            std::swap(cur, nxt);
+        }
+        x = c->X + (size_t)pad * Op;
+        L = Lo;
         for (int u = 0; u < 3; u++) {
             const int d = kDil[u];
-            launch_codec_snake<T>(x, b.ra0[u], L, Op, H, S, st);
-            IRO_TRY(codec_conv<T>(c, EPI_SNAKE, S + (size_t)(H - 3 * d) * Op, Op, d, L + H + 3 * d, L, Op, 7 * Op,
-                                  b.rw[u], b.rb[u], b.ra1[u], nullptr, S2, st));
-            IRO_TRY(codec_conv<T>(c, EPI_ADD, S2, 0, 1, 0, L, Op, Op, b.pw[u], b.pb[u], nullptr, x, nullptr, st));
+            ConvCall<T> k7;
+            k7.epi = EPI_SNAKE;
+            k7.A = cur + (size_t)(H - 3 * d) * Op;
+            k7.cp = Op;
+            k7.dil = d;
+            k7.rows = L + H + 3 * d;
+            k7.M = L;
+            k7.N = Op;
+            k7.K = 7 * Op;
+            k7.W = b.rw[u];
+            k7.bias = b.rb[u];
+            k7.alpha = b.ra1[u];
+            k7.alpha_n = Op;
+            k7.U = S2;
+            IRO_TRY(codec_conv<T>(k7, st));
+            ConvCall<T> k1;  // x += conv_1x1(s2) + b, and the next Snake of x into cur
+            k1.epi = EPI_ADD;
+            k1.A = S2;
+            k1.M = L;
+            k1.N = Op;
+            k1.K = Op;
+            k1.W = b.pw[u];
+            k1.bias = b.pb[u];
+            k1.C = x;
+            const float* next_alpha = u < 2 ? b.ra0[u + 1] : bi + 1 < c->blocks.size() ? c->blocks[bi + 1].alpha : nullptr;
+            if (next_alpha) {
+                k1.U = cur + (size_t)H * Op;
+                k1.alpha = next_alpha;
+                k1.alpha_n = Op;
+                k1.u_hi = (long)L * Op;
+            }
+            IRO_TRY(codec_conv<T>(k1, st));
         }
     }
-    launch_codec_snake<T>(x, c->head_alpha, L, c->last_p, H, S, st);
-    launch_codec_head<T>(S, L, c->last_p, H, c->head_w, c->head_b, wav, st);
+    launch_codec_head<T>(x, L, c->last_p, c->head_alpha, c->head_w, c->head_b, wav, st);
     return check_launch("codec decode");
 }
 
@@ -292,28 +393,30 @@ int irodori_codec_create(int device, const irodori_codec_config* cfg, irodori_co
         se = std::max(se, (L + 2 * H) * b.cout_p);
         s2e = std::max(s2e, L * b.cout_p);
         C = b.cout;
-        IRO_TRY(codec_alloc_t(c.get(), &b.alpha, sizeof(float) * b.cin_p));
+        IRO_TRY(codec_alloc_t(c.get(), &b.alpha, sizeof(float) * 3 * b.cin_p));
         IRO_TRY(codec_alloc(c.get(), &b.wt, es * b.rate * b.cout_p * 2 * b.cin_p));
         IRO_TRY(codec_alloc_t(c.get(), &b.bt, sizeof(float) * b.rate * b.cout_p));
         for (int u = 0; u < 3; u++) {
-            IRO_TRY(codec_alloc_t(c.get(), &b.ra0[u], sizeof(float) * b.cout_p));
-            IRO_TRY(codec_alloc_t(c.get(), &b.ra1[u], sizeof(float) * b.cout_p));
+            IRO_TRY(codec_alloc_t(c.get(), &b.ra0[u], sizeof(float) * 3 * b.cout_p));
+            IRO_TRY(codec_alloc_t(c.get(), &b.ra1[u], sizeof(float) * 3 * b.cout_p));
             IRO_TRY(codec_alloc(c.get(), &b.rw[u], es * b.cout_p * 7 * b.cout_p));
             IRO_TRY(codec_alloc(c.get(), &b.pw[u], es * b.cout_p * b.cout_p));
         }
     }
     c->last_p = round64(C);
+    IRO_REQUIRE(c->last_p <= 256, IRODORI_ERR_SHAPE, "codec head width (decoder_dim >> num_blocks) must be at most 256");
     c->x_elems = xe;
     c->s_elems = se;
     c->s2_elems = s2e;
     IRO_TRY(codec_alloc_t(c.get(), &c->in_w, sizeof(float) * c->proj_p * g.latent_dim));
     IRO_TRY(codec_alloc_t(c.get(), &c->in_b, sizeof(float) * c->proj_p));
     IRO_TRY(codec_alloc(c.get(), &c->stem_w, es * c->dim_p * 7 * c->proj_p));
-    IRO_TRY(codec_alloc_t(c.get(), &c->head_alpha, sizeof(float) * c->last_p));
+    IRO_TRY(codec_alloc_t(c.get(), &c->head_alpha, sizeof(float) * 3 * c->last_p));
     IRO_TRY(codec_alloc_t(c.get(), &c->head_w, sizeof(float) * 7 * c->last_p));
     IRO_TRY(codec_alloc_t(c.get(), &c->head_b, sizeof(float)));
     IRO_TRY(codec_alloc_t(c.get(), &c->X, sizeof(float) * xe));
     IRO_TRY(codec_alloc(c.get(), &c->S, es * se));
+    IRO_TRY(codec_alloc(c.get(), &c->S3, es * se));
     IRO_TRY(codec_alloc(c.get(), &c->S2, es * s2e));
     IRO_TRY(codec_alloc_t(c.get(), &c->lat, sizeof(float) * (size_t)g.max_frames * g.latent_dim));
     IRO_TRY(codec_alloc_t(c.get(), &c->wav, sizeof(float) * (size_t)g.max_frames * hop));
@@ -352,12 +455,12 @@ int irodori_codec_load_weights(irodori_codec* c, const irodori_codec_weights* w)
     for (int i = 0; i < g.num_blocks; i++) {
         CodecBlock& b = c->blocks[i];
         const irodori_codec_block_weights& bw = w->blocks[i];
-        IRO_TRY(put_f32(c, b.alpha, padded(bw.alpha, b.cin, b.cin_p)));
+        IRO_TRY(put_f32(c, b.alpha, snake_consts(bw.alpha, b.cin, b.cin_p)));
         IRO_TRY(put_operand(c, b.wt, convt_rows(bw.convt_w, b.cin, b.cout, b.rate, b.cin_p, b.cout_p)));
         IRO_TRY(put_f32(c, b.bt, padded(bw.convt_b, b.cout, b.cout_p, b.rate)));
         for (int u = 0; u < 3; u++) {
-            IRO_TRY(put_f32(c, b.ra0[u], padded(bw.res_alpha0[u], b.cout, b.cout_p)));
-            IRO_TRY(put_f32(c, b.ra1[u], padded(bw.res_alpha1[u], b.cout, b.cout_p)));
+            IRO_TRY(put_f32(c, b.ra0[u], snake_consts(bw.res_alpha0[u], b.cout, b.cout_p)));
+            IRO_TRY(put_f32(c, b.ra1[u], snake_consts(bw.res_alpha1[u], b.cout, b.cout_p)));
             IRO_TRY(put_operand(c, b.rw[u], conv_rows(bw.res_conv_w[u], b.cout, b.cout, 7, b.cout_p, b.cout_p)));
             IRO_TRY(put_operand(c, b.pw[u], conv_rows(bw.res_pw_w[u], b.cout, b.cout, 1, b.cout_p, b.cout_p)));
             if (bw.res_conv_b[u]) {
@@ -375,7 +478,7 @@ int irodori_codec_load_weights(irodori_codec* c, const irodori_codec_weights* w)
         }
     }
     const int Cl = g.decoder_dim >> g.num_blocks;
-    IRO_TRY(put_f32(c, c->head_alpha, padded(w->head_alpha, Cl, c->last_p)));
+    IRO_TRY(put_f32(c, c->head_alpha, snake_consts(w->head_alpha, Cl, c->last_p)));
     std::vector<float> hw((size_t)7 * c->last_p, 0.f);
     for (int ch = 0; ch < Cl; ch++)
         for (int j = 0; j < 7; j++) hw[(size_t)j * c->last_p + ch] = w->head_w[(size_t)ch * 7 + j];

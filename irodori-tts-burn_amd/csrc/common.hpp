@@ -28,6 +28,24 @@ __device__ __forceinline__ float from_f32<float>(float v) { return v; }
 template <>
 __device__ __forceinline__ bf16 from_f32<bf16>(float v) { return static_cast<bf16>(v); }
 
+// Snake1d (codec/layers.rs:24-31): v + sin(a v)^2 / (a + 1e-9), from the channel's
+// constants (a, ar = a / pi, hc = 0.5 / (a + 1e-9)).  For bf16 results (rounded to 8 bits)
+// sin^2 y = (1 - cos 2y) / 2 with the hardware cosine, which takes revolutions:
+// cos(2 a v) = cos_rev(ar v), reduced to [-1/2, 1/2] first; f32 results use sinf.
+template <typename T>
+__device__ __forceinline__ float snake_eval(float v, float a, float ar, float hc) {
+    if constexpr (sizeof(T) == 2) {
+        float r = ar * v;
+        r -= rintf(r);
+        return fmaf(hc, 1.f - __builtin_amdgcn_cosf(r), v);
+    } else {
+        (void)ar;
+        (void)hc;
+        const float s = sinf(a * v);
+        return v + s * s / (a + 1e-9f);
+    }
+}
+
 // ---------------------------------------------------------------------------------
 // fp8 (e4m3fn) GEMM operands: a 32-wide block of a row is stored as e4m3 codes of
 // x * 2^-e with e the smallest integer such that max |x| <= 448 * 2^e, and the E8M0 byte

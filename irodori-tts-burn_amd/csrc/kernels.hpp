@@ -213,10 +213,16 @@ struct GemmArgs {
     uint8_t* U8;
     uint8_t* U8s;
     // Convolution epilogues (the codec decoder): EPI_STORE and EPI_ADD add bias[n] when it
-    // is set; EPI_SNAKE writes U [M, N] = Snake(acc + bias[n], alpha[n]) in the operand
-    // dtype, Snake(v, a) = v + sin(a v)^2 / (a + 1e-9) (codec/layers.rs:24-31).
+    // is set; EPI_SNAKE writes U [M, N] = Snake(acc + bias[n]) in the operand dtype,
+    // Snake(v, a) = v + sin(a v)^2 / (a + 1e-9) (codec/layers.rs:24-31), alpha the block
+    // [3, alpha_n] = (a, a / pi, 0.5 / (a + 1e-9)) of channel n % alpha_n (bf16: hardware
+    // cosine, f32: sinf).  EPI_STORE / EPI_ADD with U set also write U[i] = Snake(out[i])
+    // for the linear indices i = row * N + n in [u_lo, u_hi): the next convolution's
+    // operand, produced without another pass over the result.
     const float* bias;
     const float* alpha;
+    int alpha_n;
+    long u_lo, u_hi;
     // launch_gemm_conv: A is an implicit im2col.  Row m of the GEMM, k = j * conv_cp + c
     // reads A[(m + j * conv_dil) * conv_cp + c] (A points at the source row the first tap
     // of output row 0 reads); source rows at or past conv_rows read as zero.
@@ -248,17 +254,20 @@ void launch_enc_mean_token(float* out, const float* mask, uint8_t* mask_out, int
 
 // ---- kernels_codec.hip -----------------------------------------------------------------
 // DACVAE decoder operands: channels-last [frames, Cp] (Cp % 8 == 0), convolution operands
-// with `halo` zero rows on both sides of the L frames ([L + 2 halo, Cp]).
-template <typename T>
-void launch_codec_snake(const float* x, const float* alpha, int L, int Cp, int halo, T* s, hipStream_t st);
+// with `halo` zero rows on both sides of the L frames ([L + 2 halo, Cp]).  A Snake's
+// `alpha` is the block [3, Cp] = (a, a / pi, 0.5 / (a + 1e-9)); T = bf16 evaluates it with
+// the hardware cosine, T = float with sinf.
 template <typename T>
 void launch_codec_in(const float* lat, int frames, int Cl, const float* w, const float* b, int Pp, int halo, T* s,
                      hipStream_t st);
+// WmHead with its Snake over x [L, Cp] f32 (Cp a multiple of 64, at most 256).
 template <typename T>
-void launch_codec_head(const T* s, int L, int Cp, int halo, const float* w, const float* b, float* wav,
+void launch_codec_head(const float* x, int L, int Cp, const float* alpha, const float* w, const float* b, float* wav,
                        hipStream_t st);
 template <typename T>
 void launch_cvt_f32(const float* src, long n, T* dst, hipStream_t st);
+template <typename T>
+void launch_codec_zero_halo(T* s, int L, int Cp, int halo, hipStream_t st);
 
 // ---- kernels_fp8.hip -------------------------------------------------------------------
 // Weights w [N, K] f32 (K-major, K % 4 == 0) -> e4m3 codes q [N, K], channel scales s [N].

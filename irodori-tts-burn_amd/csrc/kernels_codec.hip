@@ -13,10 +13,9 @@ namespace irodori {
 
 namespace {
 
-// Snake1d (layers.rs:24-31) in f32: x + sin(a x)^2 / (a + 1e-9).
-__device__ __forceinline__ float snake(float v, float a) {
-    const float s = sinf(a * v);
-    return v + s * s / (a + 1e-9f);
+template <typename T>
+__device__ __forceinline__ float snake_c(float v, float a, float ar, float hc) {
+    return snake_eval<T>(v, a, ar, hc);
 }
 
 template <typename T>
@@ -43,31 +42,6 @@ __device__ __forceinline__ void load8(const T* p, float (&v)[8]) {
         v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
         v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
     }
-}
-
-// One thread per 8 channels of an operand row r in [0, L + 2 halo): Snake of frame
-// r - halo of x [L, Cp] (alpha [Cp], zero past the real channels), zeros in the halos.
-template <typename T>
-__global__ __launch_bounds__(256) void snake_rows_kernel(const float* __restrict__ x, const float* __restrict__ alpha,
-                                                         int L, int Cp, int halo, T* __restrict__ s) {
-    const int c8 = Cp / 8;
-    const long idx = (long)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= (long)(L + 2 * halo) * c8) return;
-    const int r = (int)(idx / c8), c = (int)(idx % c8) * 8;
-    float v[8];
-    const int t = r - halo;
-    if (t >= 0 && t < L) {
-        const float4* px = reinterpret_cast<const float4*>(x + (size_t)t * Cp + c);
-        const float4 a0 = px[0], a1 = px[1];
-        const float4* pa = reinterpret_cast<const float4*>(alpha + c);
-        const float4 b0 = pa[0], b1 = pa[1];
-        v[0] = snake(a0.x, b0.x); v[1] = snake(a0.y, b0.y); v[2] = snake(a0.z, b0.z); v[3] = snake(a0.w, b0.w);
-        v[4] = snake(a1.x, b1.x); v[5] = snake(a1.y, b1.y); v[6] = snake(a1.z, b1.z); v[7] = snake(a1.w, b1.w);
-    } else {
-#pragma unroll
-        for (int i = 0; i < 8; i++) v[i] = 0.f;
-    }
-    store8<T>(s + (size_t)r * Cp + c, v);
 }
 
 // quantizer.out_proj (bottleneck.rs:21-23, a k 1 Conv1d): one thread per 8 output
@@ -98,27 +72,85 @@ __global__ __launch_bounds__(256) void codec_in_kernel(const float* __restrict__
     store8<T>(s + (size_t)r * Pp + o, v);
 }
 
-// WmHead (decoder.rs WmHead::forward): Conv1d(Cp -> 1, k 7, pad 3) over the Snake'd
-// operand s [L + 2 halo, Cp] (halo >= 3), then tanh.  One thread per frame; the taps
-// w [7, Cp] f32 (w[j Cp + c] = weight[0, c, j], zero past the real channels).
+// WmHead (decoder.rs WmHead::forward) fused with its Snake: wav[t] = tanh(b + sum_j sum_c
+// w[j, c] Snake(x[t + j - 3, c])) over x [L, Cp] f32 (zero padding outside [0, L)), taps
+// w [7, Cp] f32 (w[j Cp + c] = weight[0, c, j], zero past the real channels).  A workgroup
+// owns 256 frames: its waves reduce the 262 rows the frames read to per-tap dot products
+// p[row][j] in LDS (16 lanes per row, float4 loads: coalesced), then thread t sums its
+// seven taps.  Cp <= 256.
 template <typename T>
-__global__ __launch_bounds__(256) void codec_head_kernel(const T* __restrict__ s, int L, int Cp, int halo,
-                                                         const float* __restrict__ w, const float* __restrict__ b,
-                                                         float* __restrict__ wav) {
-    const int t = blockIdx.x * 256 + threadIdx.x;
-    if (t >= L) return;
-    float acc = 0.f;
-    for (int j = 0; j < 7; j++) {
-        const T* row = s + (size_t)(t + j - 3 + halo) * Cp;
-        const float* wj = w + j * Cp;
-        for (int c = 0; c < Cp; c += 8) {
-            float v[8];
-            load8<T>(row + c, v);
+__global__ __launch_bounds__(256) void codec_head_kernel(const float* __restrict__ x, int L, int Cp,
+                                                         const float* __restrict__ alpha, const float* __restrict__ w,
+                                                         const float* __restrict__ b, float* __restrict__ wav) {
+    constexpr int FR = 256, ROWS = FR + 6;
+    __shared__ float p[ROWS][8];
+    const int t0 = blockIdx.x * FR, tid = threadIdx.x, lane16 = tid & 15, grp = tid >> 4;  // 16 row groups
+    const int nch = Cp / 64;  // float4 chunks per lane: channels 4 lane16 + 64 k
+    float wr[4][7][4], av[4][4], ar[4][4], hc[4][4];
 #pragma unroll
-            for (int i = 0; i < 8; i++) acc = fmaf(wj[c + i], v[i], acc);
+    for (int k = 0; k < 4; k++) {
+        if (k >= nch) break;
+        const int c = 4 * lane16 + 64 * k;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            av[k][i] = alpha[c + i];
+            ar[k][i] = alpha[Cp + c + i];
+            hc[k][i] = alpha[2 * Cp + c + i];
+#pragma unroll
+            for (int j = 0; j < 7; j++) wr[k][j][i] = w[j * Cp + c + i];
         }
     }
-    wav[t] = tanhf(acc + (b ? b[0] : 0.f));
+    for (int rr = grp; rr < ROWS; rr += 16) {
+        const int f = t0 - 3 + rr;  // frame of this row
+        float acc[7];
+#pragma unroll
+        for (int j = 0; j < 7; j++) acc[j] = 0.f;
+        if (f >= 0 && f < L) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                if (k >= nch) break;
+                const float4 xv = *reinterpret_cast<const float4*>(x + (size_t)f * Cp + 4 * lane16 + 64 * k);
+                const float sv[4] = {snake_c<T>(xv.x, av[k][0], ar[k][0], hc[k][0]),
+                                     snake_c<T>(xv.y, av[k][1], ar[k][1], hc[k][1]),
+                                     snake_c<T>(xv.z, av[k][2], ar[k][2], hc[k][2]),
+                                     snake_c<T>(xv.w, av[k][3], ar[k][3], hc[k][3])};
+#pragma unroll
+                for (int j = 0; j < 7; j++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) acc[j] = fmaf(wr[k][j][i], sv[i], acc[j]);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 7; j++)
+#pragma unroll
+            for (int off = 8; off > 0; off >>= 1) acc[j] += __shfl_xor(acc[j], off, 16);
+        if (lane16 < 7) {
+            float mine = acc[0];
+#pragma unroll
+            for (int j = 1; j < 7; j++)
+                if (lane16 == j) mine = acc[j];
+            p[rr][lane16] = mine;
+        }
+    }
+    __syncthreads();
+    const int t = t0 + tid;
+    if (t >= L) return;
+    float y = b ? b[0] : 0.f;
+#pragma unroll
+    for (int j = 0; j < 7; j++) y += p[tid + j][j];
+    wav[t] = tanhf(y);
+}
+
+// Zero the halo rows [0, halo) and [halo + L, L + 2 halo) of an operand [L + 2 halo, Cp].
+template <typename T>
+__global__ __launch_bounds__(256) void zero_halo_kernel(T* __restrict__ s, int L, int Cp, int halo) {
+    const int c8 = Cp / 8;
+    const int idx = blockIdx.x * 256 + threadIdx.x;
+    if (idx >= 2 * halo * c8) return;
+    int r = idx / c8;
+    if (r >= halo) r += L;
+    float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    store8<T>(s + (size_t)r * Cp + (idx % c8) * 8, z);
 }
 
 template <typename T>
@@ -132,12 +164,6 @@ inline unsigned blocks_for(long n) { return (unsigned)((n + 255) / 256); }
 }  // namespace
 
 template <typename T>
-void launch_codec_snake(const float* x, const float* alpha, int L, int Cp, int halo, T* s, hipStream_t st) {
-    const long n = (long)(L + 2 * halo) * (Cp / 8);
-    if (n > 0) snake_rows_kernel<T><<<blocks_for(n), 256, 0, st>>>(x, alpha, L, Cp, halo, s);
-}
-
-template <typename T>
 void launch_codec_in(const float* lat, int frames, int Cl, const float* w, const float* b, int Pp, int halo, T* s,
                      hipStream_t st) {
     const long n = (long)(frames + 2 * halo) * (Pp / 8);
@@ -145,9 +171,15 @@ void launch_codec_in(const float* lat, int frames, int Cl, const float* w, const
 }
 
 template <typename T>
-void launch_codec_head(const T* s, int L, int Cp, int halo, const float* w, const float* b, float* wav,
+void launch_codec_head(const float* x, int L, int Cp, const float* alpha, const float* w, const float* b, float* wav,
                        hipStream_t st) {
-    if (L > 0) codec_head_kernel<T><<<blocks_for(L), 256, 0, st>>>(s, L, Cp, halo, w, b, wav);
+    if (L > 0) codec_head_kernel<T><<<blocks_for(L), 256, 0, st>>>(x, L, Cp, alpha, w, b, wav);
+}
+
+template <typename T>
+void launch_codec_zero_halo(T* s, int L, int Cp, int halo, hipStream_t st) {
+    const long n = 2L * halo * (Cp / 8);
+    if (n > 0) zero_halo_kernel<T><<<blocks_for(n), 256, 0, st>>>(s, L, Cp, halo);
 }
 
 template <typename T>
@@ -156,11 +188,12 @@ void launch_cvt_f32(const float* src, long n, T* dst, hipStream_t st) {
 }
 
 #define IRO_CODEC_INST(T)                                                                                   \
-    template void launch_codec_snake<T>(const float*, const float*, int, int, int, T*, hipStream_t);          \
     template void launch_codec_in<T>(const float*, int, int, const float*, const float*, int, int, T*,       \
                                      hipStream_t);                                                          \
-    template void launch_codec_head<T>(const T*, int, int, int, const float*, const float*, float*, hipStream_t); \
-    template void launch_cvt_f32<T>(const float*, long, T*, hipStream_t);
+    template void launch_codec_head<T>(const float*, int, int, const float*, const float*, const float*, float*, \
+                                       hipStream_t);                                                          \
+    template void launch_cvt_f32<T>(const float*, long, T*, hipStream_t);                                    \
+    template void launch_codec_zero_halo<T>(T*, int, int, int, hipStream_t);
 IRO_CODEC_INST(bf16)
 IRO_CODEC_INST(float)
 #undef IRO_CODEC_INST

@@ -374,13 +374,26 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
     }
 
     // ---- epilogues (acc layout: see rbase / cl above).
-    [[maybe_unused]] float bcol[FN];
+    // Convolution epilogues: per-column bias and, when a Snake output is written, the
+    // column's Snake constants (channel col % alpha_n of the alpha block).
+    [[maybe_unused]] float bcol[FN], acol[FN], arcol[FN], hcol[FN];
+    [[maybe_unused]] const bool snake_out = (EPI == EPI_SNAKE) || a.U != nullptr;
     if constexpr (EPI == EPI_STORE || EPI == EPI_ADD || EPI == EPI_SNAKE) {
 #pragma unroll
-        for (int j = 0; j < FN; j++) bcol[j] = a.bias ? a.bias[n0 + wn0 + 32 * j + cl] : 0.f;
+        for (int j = 0; j < FN; j++) {
+            const int col = n0 + wn0 + 32 * j + cl;
+            bcol[j] = a.bias ? a.bias[col] : 0.f;
+            if (snake_out) {
+                const int ch = col % a.alpha_n;
+                acol[j] = a.alpha[ch];
+                arcol[j] = a.alpha[a.alpha_n + ch];
+                hcol[j] = a.alpha[2 * a.alpha_n + ch];
+            }
+        }
     }
     if constexpr (EPI == EPI_STORE) {
         float* __restrict__ C = a.C;
+        T* __restrict__ U = a.U;
 #pragma unroll
         for (int i = 0; i < FM; i++)
 #pragma unroll
@@ -388,31 +401,46 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
                 int row = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
                 if (row >= a.M) continue;
 #pragma unroll
-                for (int j = 0; j < FN; j++) C[(size_t)row * a.N + n0 + wn0 + 32 * j + cl] = acc[i][j][e] + bcol[j];
+                for (int j = 0; j < FN; j++) {
+                    const long lin = (long)row * a.N + n0 + wn0 + 32 * j + cl;
+                    const float v = acc[i][j][e] + bcol[j];
+                    C[lin] = v;
+                    if (snake_out && lin >= a.u_lo && lin < a.u_hi)
+                        U[lin] = from_f32<T>(snake_eval<T>(v, acol[j], arcol[j], hcol[j]));
+                }
             }
     } else if constexpr (EPI == EPI_ADD) {
+        // The residual elements of each 32-row block are loaded together before any store:
+        // interleaved with the stores to the same array, every load would wait out the
+        // memory latency on its own.
         float* __restrict__ xg = a.x;
+        T* __restrict__ U = a.U;
 #pragma unroll
-        for (int i = 0; i < FM; i++)
+        for (int i = 0; i < FM; i++) {
+            float xv[16][FN], rmv[16];
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const int row = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
+                const bool ok = row < a.M;
+                rmv[e] = ok && a.rmask ? a.rmask[row] : 1.f;
+#pragma unroll
+                for (int j = 0; j < FN; j++) xv[e][j] = ok ? xg[(long)row * a.N + n0 + wn0 + 32 * j + cl] : 0.f;
+            }
 #pragma unroll
             for (int e = 0; e < 16; e++) {
                 const int row = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
                 if (row >= a.M) continue;
-                const float rm = a.rmask ? a.rmask[row] : 1.f;
 #pragma unroll
                 for (int j = 0; j < FN; j++) {
-                    float* px = xg + (size_t)row * a.N + n0 + wn0 + 32 * j + cl;
-                    *px = (*px + (acc[i][j][e] + bcol[j])) * rm;
+                    const long lin = (long)row * a.N + n0 + wn0 + 32 * j + cl;
+                    const float v = (xv[e][j] + (acc[i][j][e] + bcol[j])) * rmv[e];
+                    xg[lin] = v;
+                    if (snake_out) U[lin] = from_f32<T>(snake_eval<T>(v, acol[j], arcol[j], hcol[j]));
                 }
             }
+        }
     } else if constexpr (EPI == EPI_SNAKE) {
         T* __restrict__ U = a.U;
-        float acol[FN], dcol[FN];
-#pragma unroll
-        for (int j = 0; j < FN; j++) {
-            acol[j] = a.alpha[n0 + wn0 + 32 * j + cl];
-            dcol[j] = acol[j] + 1e-9f;
-        }
 #pragma unroll
         for (int i = 0; i < FM; i++)
 #pragma unroll
@@ -420,11 +448,9 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
                 const int row = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
                 if (row >= a.M) continue;
 #pragma unroll
-                for (int j = 0; j < FN; j++) {
-                    const float v = acc[i][j][e] + bcol[j];
-                    const float sv = sinf(acol[j] * v);
-                    U[(size_t)row * a.N + n0 + wn0 + 32 * j + cl] = from_f32<T>(v + sv * sv / dcol[j]);
-                }
+                for (int j = 0; j < FN; j++)
+                    U[(size_t)row * a.N + n0 + wn0 + 32 * j + cl] =
+                        from_f32<T>(snake_eval<T>(acc[i][j][e] + bcol[j], acol[j], arcol[j], hcol[j]));
             }
     } else if constexpr (EPI == EPI_RESID) {
         // x[row, col] += gate[b(row), col] * C, from the values loaded before the main loop.
@@ -785,6 +811,7 @@ static bool wide_enough(const GemmArgs<T>& a) {
 
 template <typename T>
 int launch_gemm(int epi, const GemmArgs<T>& a, hipStream_t st) {
+    if ((epi == EPI_STORE || epi == EPI_ADD) && a.U && (!a.alpha || a.alpha_n <= 0)) return -1;
     switch (epi) {
         case EPI_STORE:
             if (wide_enough(a)) return launch_cfg<T, 128, 128, 2, 2, 2, EPI_STORE>(a, st);
@@ -794,6 +821,8 @@ int launch_gemm(int epi, const GemmArgs<T>& a, hipStream_t st) {
             return launch_cfg<T, 64, 64, 2, 2, 4, EPI_RESID>(a, st);
         case EPI_ADD:
             if (wide_enough(a)) return launch_cfg<T, 128, 128, 2, 2, 2, EPI_ADD>(a, st);
+            if (a.N % 128 != 0 && a.N % 192 == 0 && (long)((a.M + 127) / 128) * (a.N / 192) >= 512)
+                return launch_cfg<T, 128, 192, 2, 2, 2, EPI_ADD>(a, st);
             return launch_cfg<T, 64, 64, 2, 2, 4, EPI_ADD>(a, st);
         case EPI_SWIGLU: return launch_cfg<T, 128, 128, 2, 2, 2, EPI_SWIGLU>(a, st);
         case EPI_QKVG: return launch_cfg<T, 128, 128, 2, 2, 2, EPI_QKVG>(a, st);
@@ -822,19 +851,25 @@ int launch_gemm_fp8(int epi, const GemmArgs<bf16>& a, hipStream_t st) {
 
 // Convolutions: the residual streams of the codec decoder are 96 .. 1536 channels (padded
 // to 64 / 128) over up to ~10^6 frames, so 128x128 tiles whenever the columns allow.
+// Columns that split into 192-wide tiles but not 128-wide ones (a 192-channel stream) use
+// 128x192 tiles: 2x2 waves of 64x96, five fragment reads per six MFMAs.
 template <typename T>
 int launch_gemm_conv(int epi, const GemmArgs<T>& a, hipStream_t st) {
-    const bool wide = a.N % 128 == 0;
+    const bool wide = a.N % 128 == 0, w192 = a.N % 192 == 0;
+    if ((epi == EPI_SNAKE || a.U) && (!a.alpha || a.alpha_n <= 0)) return -1;
     switch (epi) {
         case EPI_STORE:
             if (wide) return launch_cfg<T, 128, 128, 2, 2, 2, EPI_STORE, false, true>(a, st);
+            if (w192) return launch_cfg<T, 128, 192, 2, 2, 2, EPI_STORE, false, true>(a, st);
             return launch_cfg<T, 64, 64, 2, 2, 4, EPI_STORE, false, true>(a, st);
         case EPI_SNAKE:
-            if (!a.U || !a.alpha) return -1;
+            if (!a.U) return -1;
             if (wide) return launch_cfg<T, 128, 128, 2, 2, 2, EPI_SNAKE, false, true>(a, st);
+            if (w192) return launch_cfg<T, 128, 192, 2, 2, 2, EPI_SNAKE, false, true>(a, st);
             return launch_cfg<T, 64, 64, 2, 2, 4, EPI_SNAKE, false, true>(a, st);
         case EPI_ADD:
             if (wide) return launch_cfg<T, 128, 128, 2, 2, 2, EPI_ADD, false, true>(a, st);
+            if (w192) return launch_cfg<T, 128, 192, 2, 2, 2, EPI_ADD, false, true>(a, st);
             return launch_cfg<T, 64, 64, 2, 2, 4, EPI_ADD, false, true>(a, st);
     }
     return -1;
