@@ -75,61 +75,47 @@ __global__ __launch_bounds__(256) void codec_in_kernel(const float* __restrict__
 // WmHead (decoder.rs WmHead::forward) fused with its Snake: wav[t] = tanh(b + sum_j sum_c
 // w[j, c] Snake(x[t + j - 3, c])) over x [L, Cp] f32 (zero padding outside [0, L)), taps
 // w [7, Cp] f32 (w[j Cp + c] = weight[0, c, j], zero past the real channels).  A workgroup
-// owns 256 frames: its waves reduce the 262 rows the frames read to per-tap dot products
-// p[row][j] in LDS (16 lanes per row, float4 loads: coalesced), then thread t sums its
-// seven taps.  Cp <= 256.
+// owns 256 frames: its waves reduce the 262 rows those frames read to per-tap dot products
+// p[row][j] in LDS (4 lanes per row, each lane Cp / 4 channels in float4 loads), then
+// thread t sums its seven taps.  The taps and Snake constants sit in LDS.  Cp <= 256.
 template <typename T>
 __global__ __launch_bounds__(256) void codec_head_kernel(const float* __restrict__ x, int L, int Cp,
                                                          const float* __restrict__ alpha, const float* __restrict__ w,
                                                          const float* __restrict__ b, float* __restrict__ wav) {
     constexpr int FR = 256, ROWS = FR + 6;
     __shared__ float p[ROWS][8];
-    const int t0 = blockIdx.x * FR, tid = threadIdx.x, lane16 = tid & 15, grp = tid >> 4;  // 16 row groups
-    const int nch = Cp / 64;  // float4 chunks per lane: channels 4 lane16 + 64 k
-    float wr[4][7][4], av[4][4], ar[4][4], hc[4][4];
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        if (k >= nch) break;
-        const int c = 4 * lane16 + 64 * k;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            av[k][i] = alpha[c + i];
-            ar[k][i] = alpha[Cp + c + i];
-            hc[k][i] = alpha[2 * Cp + c + i];
-#pragma unroll
-            for (int j = 0; j < 7; j++) wr[k][j][i] = w[j * Cp + c + i];
-        }
-    }
-    for (int rr = grp; rr < ROWS; rr += 16) {
-        const int f = t0 - 3 + rr;  // frame of this row
-        float acc[7];
-#pragma unroll
-        for (int j = 0; j < 7; j++) acc[j] = 0.f;
+    __shared__ float4 wl[7][64], al[3][64];
+    const int t0 = blockIdx.x * FR, tid = threadIdx.x, q = tid & 3, grp = tid >> 2;  // 64 row groups
+    const int c4n = Cp / 4;  // float4 columns
+    for (int i = tid; i < 7 * c4n; i += 256) wl[i / c4n][i % c4n] = reinterpret_cast<const float4*>(w)[i];
+    for (int i = tid; i < 3 * c4n; i += 256) al[i / c4n][i % c4n] = reinterpret_cast<const float4*>(alpha)[i];
+    __syncthreads();
+    const int per = c4n / 4;  // float4 columns per lane: q, q + 4, ...
+    for (int rr = grp; rr < ROWS; rr += 64) {
+        const int f = t0 - 3 + rr;
+        float acc[7] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
         if (f >= 0 && f < L) {
+            const float4* xr = reinterpret_cast<const float4*>(x + (size_t)f * Cp);
+            for (int k = 0; k < per; k++) {
+                const int c4 = q + 4 * k;
+                const float4 xv = xr[c4], av = al[0][c4], ar = al[1][c4], hc = al[2][c4];
+                const float s0 = snake_c<T>(xv.x, av.x, ar.x, hc.x), s1 = snake_c<T>(xv.y, av.y, ar.y, hc.y);
+                const float s2 = snake_c<T>(xv.z, av.z, ar.z, hc.z), s3 = snake_c<T>(xv.w, av.w, ar.w, hc.w);
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-                if (k >= nch) break;
-                const float4 xv = *reinterpret_cast<const float4*>(x + (size_t)f * Cp + 4 * lane16 + 64 * k);
-                const float sv[4] = {snake_c<T>(xv.x, av[k][0], ar[k][0], hc[k][0]),
-                                     snake_c<T>(xv.y, av[k][1], ar[k][1], hc[k][1]),
-                                     snake_c<T>(xv.z, av[k][2], ar[k][2], hc[k][2]),
-                                     snake_c<T>(xv.w, av[k][3], ar[k][3], hc[k][3])};
-#pragma unroll
-                for (int j = 0; j < 7; j++)
-#pragma unroll
-                    for (int i = 0; i < 4; i++) acc[j] = fmaf(wr[k][j][i], sv[i], acc[j]);
+                for (int j = 0; j < 7; j++) {
+                    const float4 wv = wl[j][c4];
+                    acc[j] = fmaf(wv.x, s0, fmaf(wv.y, s1, fmaf(wv.z, s2, fmaf(wv.w, s3, acc[j]))));
+                }
             }
         }
 #pragma unroll
-        for (int j = 0; j < 7; j++)
+        for (int j = 0; j < 7; j++) {
+            acc[j] += __shfl_xor(acc[j], 1, 4);
+            acc[j] += __shfl_xor(acc[j], 2, 4);
+        }
+        if (q == 0) {
 #pragma unroll
-            for (int off = 8; off > 0; off >>= 1) acc[j] += __shfl_xor(acc[j], off, 16);
-        if (lane16 < 7) {
-            float mine = acc[0];
-#pragma unroll
-            for (int j = 1; j < 7; j++)
-                if (lane16 == j) mine = acc[j];
-            p[rr][lane16] = mine;
+            for (int j = 0; j < 7; j++) p[rr][j] = acc[j];
         }
     }
     __syncthreads();

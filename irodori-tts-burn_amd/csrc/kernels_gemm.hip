@@ -412,7 +412,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
     } else if constexpr (EPI == EPI_ADD) {
         // The residual elements of each 32-row block are loaded together before any store:
         // interleaved with the stores to the same array, every load would wait out the
-        // memory latency on its own.
+        // memory latency on its own.  (Loading them before the main loop measured slower:
+        // the registers and the extra loads compete with the operand stream.)
         float* __restrict__ xg = a.x;
         T* __restrict__ U = a.U;
 #pragma unroll
@@ -864,6 +865,11 @@ int launch_gemm_conv(int epi, const GemmArgs<T>& a, hipStream_t st) {
             return launch_cfg<T, 64, 64, 2, 2, 4, EPI_STORE, false, true>(a, st);
         case EPI_SNAKE:
             if (!a.U) return -1;
+            // The largest convolutions (a million frames and more): 256x128 tiles over 8
+            // waves halve the weight-tile traffic per output (measured 3-4 % faster there,
+            // slower at 90 k frames).
+            if (wide && (long)((a.M + 255) / 256) * (a.N / 128) >= 4096)
+                return launch_cfg<T, 256, 128, 4, 2, 2, EPI_SNAKE, false, true>(a, st);
             if (wide) return launch_cfg<T, 128, 128, 2, 2, 2, EPI_SNAKE, false, true>(a, st);
             if (w192) return launch_cfg<T, 128, 192, 2, 2, 2, EPI_SNAKE, false, true>(a, st);
             return launch_cfg<T, 64, 64, 2, 2, 4, EPI_SNAKE, false, true>(a, st);
