@@ -11,7 +11,9 @@
 //   x = stem(s)     (k 7, pad 3)             conv GEMM EPI_STORE    -> X  [T, Dp]
 //   per DecoderBlock (rate r, C -> O = C / 2):
 //     x = ConvTranspose1d(Snake(x)) (k 2r)   conv GEMM EPI_STORE    -> X  (see below)
-//     per ResidualUnit (dilation 1, 3, 9):
+//     per ResidualUnit (dilation 1, 3, 9), Op = 64 / 128 / 192 channels:
+//       x += conv_1x1(Snake(conv_k7(Snake(x)) + b)) + b   conv GEMM EPI_RESUNIT
+//     wider streams (two kernels):
 //       s2 = Snake(conv_k7(Snake(x)) + b)    conv GEMM EPI_SNAKE    -> S2 [L, Op]
 //       x += conv_1x1(s2) + b                GEMM EPI_ADD
 //   wav = tanh(head_conv_k7(Snake(x)))       codec_head_kernel
@@ -187,6 +189,9 @@ struct ConvCall {
     float* C = nullptr;
     T* U = nullptr;
     long u_lo = 0, u_hi = 0;
+    const void* W2 = nullptr;  // EPI_RESUNIT: the 1x1 conv [N, N], its bias, the next Snake
+    const float* bias2 = nullptr;
+    const float* alpha2 = nullptr;
 };
 
 template <typename T>
@@ -206,6 +211,9 @@ int codec_conv(const ConvCall<T>& k, hipStream_t st) {
     ga.alpha_n = k.alpha_n;
     ga.u_lo = k.u_lo;
     ga.u_hi = k.u_hi;
+    ga.W2 = static_cast<const T*>(k.W2);
+    ga.bias2 = k.bias2;
+    ga.alpha2 = k.alpha2;
     ga.conv_cp = k.cp;
     ga.conv_dil = k.dil;
     ga.conv_rows = k.rows;
@@ -279,8 +287,38 @@ int codec_row(irodori_codec* c, const float* lat, int frames, float* wav, hipStr
         }
         x = c->X + (size_t)pad * Op;
         L = Lo;
+        // Streams of 64 / 128 / 192 channels fit one tile column: each ResidualUnit is one
+        // kernel (EPI_RESUNIT), which writes the next Snake into the other operand buffer.
+        const bool fused = Op == 64 || Op == 128 || Op == 192;
+        if (fused) launch_codec_zero_halo<T>(nxt, L, Op, H, st);
         for (int u = 0; u < 3; u++) {
             const int d = kDil[u];
+            const float* next_alpha = u < 2 ? b.ra0[u + 1] : bi + 1 < c->blocks.size() ? c->blocks[bi + 1].alpha : nullptr;
+            if (fused) {
+                ConvCall<T> k;
+                k.epi = EPI_RESUNIT;
+                k.A = cur + (size_t)(H - 3 * d) * Op;
+                k.cp = Op;
+                k.dil = d;
+                k.rows = L + H + 3 * d;
+                k.M = L;
+                k.N = Op;
+                k.K = 7 * Op;
+                k.W = b.rw[u];
+                k.bias = b.rb[u];
+                k.alpha = b.ra1[u];
+                k.alpha_n = Op;
+                k.C = x;
+                k.W2 = b.pw[u];
+                k.bias2 = b.pb[u];
+                if (next_alpha) {
+                    k.U = nxt + (size_t)H * Op;
+                    k.alpha2 = next_alpha;
+                }
+                IRO_TRY(codec_conv<T>(k, st));
+                if (next_alpha) std::swap(cur, nxt);
+                continue;
+            }
             ConvCall<T> k7;
             k7.epi = EPI_SNAKE;
             k7.A = cur + (size_t)(H - 3 * d) * Op;
@@ -305,7 +343,6 @@ int codec_row(irodori_codec* c, const float* lat, int frames, float* wav, hipStr
             k1.W = b.pw[u];
             k1.bias = b.pb[u];
             k1.C = x;
-            const float* next_alpha = u < 2 ? b.ra0[u + 1] : bi + 1 < c->blocks.size() ? c->blocks[bi + 1].alpha : nullptr;
             if (next_alpha) {
                 k1.U = cur + (size_t)H * Op;
                 k1.alpha = next_alpha;

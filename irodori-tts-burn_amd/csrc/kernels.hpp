@@ -164,7 +164,9 @@ void launch_timestep_embedding(const float* t, int nvec, int t_dim, float* out, 
 void launch_vec_linear(const VecLinJob* d_jobs, int njobs, int nvec, int max_n, hipStream_t st);
 
 // ---- kernels_gemm.hip ------------------------------------------------------------------
-enum GemmEpi { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_QKVG = 3, EPI_CTXKV = 4, EPI_ADD = 5, EPI_SNAKE = 6 };
+enum GemmEpi {
+    EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_QKVG = 3, EPI_CTXKV = 4, EPI_ADD = 5, EPI_SNAKE = 6, EPI_RESUNIT = 7
+};
 template <typename T>
 struct GemmArgs {
     const T* A;   // [M, K] row-major
@@ -223,6 +225,13 @@ struct GemmArgs {
     const float* alpha;
     int alpha_n;
     long u_lo, u_hi;
+    // EPI_RESUNIT (launch_gemm_conv, one tile column: N = 64, 128 or 192): the codec
+    // ResidualUnit's tail after its dilated conv, x[M, N] += Snake(acc + bias) @ W2^T +
+    // bias2 (W2 [N, N], the 1x1 conv; Snake with alpha), then U = Snake(x) with alpha2
+    // when U is set.  The Snake'd tile never leaves LDS.
+    const T* W2;
+    const float* bias2;
+    const float* alpha2;
     // launch_gemm_conv: A is an implicit im2col.  Row m of the GEMM, k = j * conv_cp + c
     // reads A[(m + j * conv_dil) * conv_cp + c] (A points at the source row the first tap
     // of output row 0 reads); source rows at or past conv_rows read as zero.

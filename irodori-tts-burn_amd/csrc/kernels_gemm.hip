@@ -20,6 +20,8 @@
 //   EPI_SWIGLU U = silu(C1) * C3        (feed_forward.rs:80-84; W rows interleaved per 32)
 //   EPI_ADD    x = (x + C) * rmask[row]  (encoder residual + re-mask)
 //   EPI_SNAKE  U = Snake(C + bias)       (codec ResidualUnit's dilated conv + act1)
+//   EPI_RESUNIT x += Snake(C + bias) @ W2^T + bias2 (the whole ResidualUnit tail: the
+//              Snake'd tile goes through LDS into a second MFMA pass over the 1x1 conv)
 // The STORE / ADD epilogues add an optional bias[col].  With CONV set (launch_gemm_conv)
 // the A tile of slice kt is the implicit im2col of a convolution: the slice lies in one
 // tap j = kt * BK / conv_cp, whose source rows sit j * conv_dil rows further down, so only
@@ -377,8 +379,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
     // Convolution epilogues: per-column bias and, when a Snake output is written, the
     // column's Snake constants (channel col % alpha_n of the alpha block).
     [[maybe_unused]] float bcol[FN], acol[FN], arcol[FN], hcol[FN];
-    [[maybe_unused]] const bool snake_out = (EPI == EPI_SNAKE) || a.U != nullptr;
-    if constexpr (EPI == EPI_STORE || EPI == EPI_ADD || EPI == EPI_SNAKE) {
+    [[maybe_unused]] const bool snake_out = (EPI == EPI_SNAKE || EPI == EPI_RESUNIT) || a.U != nullptr;
+    if constexpr (EPI == EPI_STORE || EPI == EPI_ADD || EPI == EPI_SNAKE || EPI == EPI_RESUNIT) {
 #pragma unroll
         for (int j = 0; j < FN; j++) {
             const int col = n0 + wn0 + 32 * j + cl;
@@ -440,6 +442,105 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
                 }
             }
         }
+    } else if constexpr (EPI == EPI_RESUNIT) {
+        // Phase 1: s = Snake(acc + bias) into LDS, slice-major (slice kt2 = columns
+        // kt2 * BK .. + BK - 1, BM rows of 128 bytes, chunks swizzled as in the operand
+        // stages), while the first W2 slice streams into the slot after it.  Phase 2:
+        // acc = s @ W2^T over NK2 slices.  Phase 3: the residual add (+ next Snake).
+        static_assert(BN % (8 * NW) == 0, "W2 slices split over the waves");
+        constexpr int NK2 = BN / BK, LPW2 = BN / 8 / NW, EPC = 16 / ES;
+        unsigned char* tl = smem;
+        unsigned char* w2l = smem + NK2 * BM * 128;
+        __syncthreads();  // every wave is done with the main loop's stages
+        const __amdgpu_buffer_rsrc_t rW2 = make_rsrc(a.W2, (unsigned)(BN * BN * ES));
+        unsigned voff2[LPW2];
+#pragma unroll
+        for (int i = 0; i < LPW2; i++) {
+            const int r = (wave * LPW2 + i) * 8 + lane / 8;
+            voff2[i] = (unsigned)(r * BN * ES) + (unsigned)swz(r, lane % 8) * 16u;
+        }
+#pragma unroll
+        for (int i = 0; i < LPW2; i++) buf_load_lds16(rW2, voff2[i], 0u, w2l + (wave * LPW2 + i) * 1024);
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const int lr = wm0 + 4 * (lane >> 5) + 32 * i + 8 * (e >> 2) + (e & 3);
+#pragma unroll
+                for (int j = 0; j < FN; j++) {
+                    const int col = wn0 + 32 * j + cl, kt2 = col / BK, kk = col % BK;
+                    T* p = reinterpret_cast<T*>(tl + kt2 * BM * 128 + lr * 128 + (swz(lr, kk / EPC) << 4)) + kk % EPC;
+                    *p = from_f32<T>(snake_eval<T>(acc[i][j][e] + bcol[j], acol[j], arcol[j], hcol[j]));
+                    acc[i][j][e] = 0.f;
+                }
+            }
+#pragma unroll
+        for (int kt2 = 0; kt2 < NK2; kt2++) {
+            wait_vmcnt<0>();
+            __syncthreads();  // W2 slice kt2 has landed; the s tile is complete
+            const unsigned char* at = tl + kt2 * BM * 128;
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) {
+                Frag32<T> af[FM], bf[FN];
+#pragma unroll
+                for (int i = 0; i < FM; i++) af[i] = read_frag<T>(at, wm0 + 32 * i + fr, ks, fh);
+#pragma unroll
+                for (int j = 0; j < FN; j++) bf[j] = read_frag<T>(w2l, wn0 + 32 * j + fr, ks, fh);
+#pragma unroll
+                for (int i = 0; i < FM; i++)
+#pragma unroll
+                    for (int j = 0; j < FN; j++) mma32(acc[i][j], af[i], bf[j]);
+            }
+            if (kt2 + 1 < NK2) {
+                __syncthreads();  // every wave is done reading the slot
+#pragma unroll
+                for (int i = 0; i < LPW2; i++)
+                    buf_load_lds16(rW2, voff2[i], (unsigned)(kt2 + 1) * 128u, w2l + (wave * LPW2 + i) * 1024);
+            }
+        }
+        float b2[FN], a2[FN], ar2[FN], hc2[FN];
+        const bool next = a.U != nullptr;
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+            const int col = n0 + wn0 + 32 * j + cl;
+            b2[j] = a.bias2 ? a.bias2[col] : 0.f;
+            if (next) {
+                a2[j] = a.alpha2[col];
+                ar2[j] = a.alpha2[a.N + col];
+                hc2[j] = a.alpha2[2 * a.N + col];
+            }
+        }
+        // The residual in batches of XB rows (loads issued together, then the stores).  Tiles
+        // that fit two workgroups per CU take four rows (few registers); the 8-wave 256-row
+        // tile runs one workgroup per CU anyway and takes all sixteen (more loads in flight).
+        constexpr int XB = BM >= 256 ? 16 : 4;
+        float* __restrict__ xg = a.x;
+        T* __restrict__ U = a.U;
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int e4 = 0; e4 < 16; e4 += XB) {
+                float xv[XB][FN];
+#pragma unroll
+                for (int e = 0; e < XB; e++) {
+                    const int row = rbase + 32 * i + 8 * ((e4 + e) >> 2) + ((e4 + e) & 3);
+#pragma unroll
+                    for (int j = 0; j < FN; j++)
+                        xv[e][j] = row < a.M ? xg[(long)row * a.N + n0 + wn0 + 32 * j + cl] : 0.f;
+                }
+#pragma unroll
+                for (int e = 0; e < XB; e++) {
+                    const int row = rbase + 32 * i + 8 * ((e4 + e) >> 2) + ((e4 + e) & 3);
+                    if (row >= a.M) continue;
+#pragma unroll
+                    for (int j = 0; j < FN; j++) {
+                        const long lin = (long)row * a.N + n0 + wn0 + 32 * j + cl;
+                        const float v = xv[e][j] + (acc[i][j][e4 + e] + b2[j]);
+                        xg[lin] = v;
+                        if (next) U[lin] = from_f32<T>(snake_eval<T>(v, a2[j], ar2[j], hc2[j]));
+                    }
+                }
+            }
     } else if constexpr (EPI == EPI_SNAKE) {
         T* __restrict__ U = a.U;
 #pragma unroll
@@ -780,10 +881,13 @@ int launch_cfg(const GemmArgs<T>& a, hipStream_t st) {
             return -1;
     }
     int tiles = ((a.M + BM - 1) / BM) * (a.N / BN);
-    const size_t lds = (size_t)STAGES * (BM + BN) * 128 + (F8 ? (size_t)BM * (a.K / 32) : 0);
+    // EPI_RESUNIT keeps the Snake'd tile (BN / BK slices of BM rows) and one W2 slice in LDS.
+    constexpr int kResLds = EPI == EPI_RESUNIT ? (BN / BK) * BM * 128 + BN * 128 : 0;
+    constexpr int kStageLds = STAGES * (BM + BN) * 128;
+    const size_t lds = (size_t)(kStageLds > kResLds ? kStageLds : kResLds) + (F8 ? (size_t)BM * (a.K / 32) : 0);
     static bool attr_set = false;  // per instantiation; the attribute is process-wide
     if (!attr_set) {
-        const int lds_max = STAGES * (BM + BN) * 128 + (F8 ? BM * (kMaxK8 / 32) : 0);
+        const int lds_max = (kStageLds > kResLds ? kStageLds : kResLds) + (F8 ? BM * (kMaxK8 / 32) : 0);
         if (hipFuncSetAttribute((const void*)gemm_kernel<T, BM, BN, WAVES_M, WAVES_N, STAGES, EPI, F8, CONV>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, lds_max) != hipSuccess)
             return -2;
@@ -857,7 +961,8 @@ int launch_gemm_fp8(int epi, const GemmArgs<bf16>& a, hipStream_t st) {
 template <typename T>
 int launch_gemm_conv(int epi, const GemmArgs<T>& a, hipStream_t st) {
     const bool wide = a.N % 128 == 0, w192 = a.N % 192 == 0;
-    if ((epi == EPI_SNAKE || a.U) && (!a.alpha || a.alpha_n <= 0)) return -1;
+    if ((epi == EPI_SNAKE || epi == EPI_RESUNIT || (epi != EPI_RESUNIT && a.U)) && (!a.alpha || a.alpha_n <= 0))
+        return -1;
     switch (epi) {
         case EPI_STORE:
             if (wide) return launch_cfg<T, 128, 128, 2, 2, 2, EPI_STORE, false, true>(a, st);
@@ -877,6 +982,14 @@ int launch_gemm_conv(int epi, const GemmArgs<T>& a, hipStream_t st) {
             if (wide) return launch_cfg<T, 128, 128, 2, 2, 2, EPI_ADD, false, true>(a, st);
             if (w192) return launch_cfg<T, 128, 192, 2, 2, 2, EPI_ADD, false, true>(a, st);
             return launch_cfg<T, 64, 64, 2, 2, 4, EPI_ADD, false, true>(a, st);
+        case EPI_RESUNIT:  // one tile column holds every channel
+            if (!a.W2 || !a.x || (a.U && !a.alpha2)) return -1;
+            if (a.N == 128 && (long)((a.M + 255) / 256) >= 4096)  // 694 against 777 us at 1.44 M frames
+                return launch_cfg<T, 256, 128, 4, 2, 2, EPI_RESUNIT, false, true>(a, st);
+            if (a.N == 128) return launch_cfg<T, 128, 128, 2, 2, 2, EPI_RESUNIT, false, true>(a, st);
+            if (a.N == 192) return launch_cfg<T, 128, 192, 2, 2, 2, EPI_RESUNIT, false, true>(a, st);
+            if (a.N == 64) return launch_cfg<T, 64, 64, 2, 2, 4, EPI_RESUNIT, false, true>(a, st);
+            return -1;
     }
     return -1;
 }
