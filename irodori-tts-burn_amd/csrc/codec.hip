@@ -44,6 +44,12 @@ constexpr int kHalo = 32;  // >= the widest padding: 3 * dilation 9 = 27
 constexpr int kDil[3] = {1, 3, 9};
 
 inline int round64(int c) { return (c + 63) / 64 * 64; }
+inline int round_to(int v, int m) { return (v + m - 1) / m * m; }
+// Channels of a stream on the device: 65..96 stay at 96 (one tile column of the 96-wide
+// tiles, K slices straddling taps), everything else rounds up to 64.
+inline int pad_channels(int c) { return c > 64 && c <= 96 ? 96 : round64(c); }
+// Streams whose ResidualUnits run as one kernel (EPI_RESUNIT: every channel in one tile).
+inline bool fused_width(int cp) { return cp == 64 || cp == 96 || cp == 128 || cp == 192; }
 
 struct CodecBlock {
     int cin = 0, cout = 0, cin_p = 0, cout_p = 0, rate = 0;
@@ -127,12 +133,13 @@ int put_operand(irodori_codec* c, void* dst, const std::vector<float>& v) {
     return IRODORI_OK;
 }
 
-// Burn Conv1d weight [O, C, k] -> K-major [Op, k * Cp]: row o, column j * Cp + c.
-std::vector<float> conv_rows(const float* w, int O, int C, int k, int Op, int Cp) {
-    std::vector<float> out((size_t)Op * k * Cp, 0.f);
+// Burn Conv1d weight [O, C, k] -> K-major [Op, Kp]: row o, column j * Cp + c, zero past
+// k * Cp (Kp: the taps' span rounded up to whole GEMM slices).
+std::vector<float> conv_rows(const float* w, int O, int C, int k, int Op, int Cp, int Kp) {
+    std::vector<float> out((size_t)Op * Kp, 0.f);
     for (int o = 0; o < O; o++)
         for (int c = 0; c < C; c++)
-            for (int j = 0; j < k; j++) out[(size_t)o * k * Cp + (size_t)j * Cp + c] = w[((size_t)o * C + c) * k + j];
+            for (int j = 0; j < k; j++) out[(size_t)o * Kp + (size_t)j * Cp + c] = w[((size_t)o * C + c) * k + j];
     return out;
 }
 
@@ -289,7 +296,8 @@ int codec_row(irodori_codec* c, const float* lat, int frames, float* wav, hipStr
         L = Lo;
         // Streams of 64 / 128 / 192 channels fit one tile column: each ResidualUnit is one
         // kernel (EPI_RESUNIT), which writes the next Snake into the other operand buffer.
-        const bool fused = Op == 64 || Op == 128 || Op == 192;
+        const bool fused = fused_width(Op);
+        const int K7 = round_to(7 * Op, 128 / (int)c->esz);
         if (fused) launch_codec_zero_halo<T>(nxt, L, Op, H, st);
         for (int u = 0; u < 3; u++) {
             const int d = kDil[u];
@@ -303,7 +311,7 @@ int codec_row(irodori_codec* c, const float* lat, int frames, float* wav, hipStr
                 k.rows = L + H + 3 * d;
                 k.M = L;
                 k.N = Op;
-                k.K = 7 * Op;
+                k.K = K7;
                 k.W = b.rw[u];
                 k.bias = b.rb[u];
                 k.alpha = b.ra1[u];
@@ -327,7 +335,7 @@ int codec_row(irodori_codec* c, const float* lat, int frames, float* wav, hipStr
             k7.rows = L + H + 3 * d;
             k7.M = L;
             k7.N = Op;
-            k7.K = 7 * Op;
+            k7.K = K7;
             k7.W = b.rw[u];
             k7.bias = b.rb[u];
             k7.alpha = b.ra1[u];
@@ -410,7 +418,7 @@ int irodori_codec_create(int device, const irodori_codec_config* cfg, irodori_co
     c->esz = c->bf16 ? 2 : 4;
     c->hop = (int)hop;
     c->proj_p = round64(g.proj_dim);
-    c->dim_p = round64(g.decoder_dim);
+    c->dim_p = pad_channels(g.decoder_dim);
     IRO_HIP_CHECK(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
     const size_t es = c->esz, H = kHalo;
     size_t L = g.max_frames;
@@ -421,8 +429,10 @@ int irodori_codec_create(int device, const irodori_codec_config* cfg, irodori_co
         CodecBlock& b = c->blocks[i];
         b.cin = C;
         b.cout = C / 2;
-        b.cin_p = round64(b.cin);
-        b.cout_p = round64(b.cout);
+        b.cin_p = pad_channels(b.cin);
+        b.cout_p = pad_channels(b.cout);
+        const int slice = 128 / (int)es;  // GEMM K slice in elements
+        IRO_REQUIRE(b.cout_p % 64 == 0 || fused_width(b.cout_p), IRODORI_ERR_SHAPE, "codec stream width without a kernel");
         b.rate = g.rates[i];
         se = std::max(se, (L + 2 * H) * b.cin_p);
         xe = std::max(xe, (L + 1) * b.rate * b.cout_p);
@@ -436,11 +446,11 @@ int irodori_codec_create(int device, const irodori_codec_config* cfg, irodori_co
         for (int u = 0; u < 3; u++) {
             IRO_TRY(codec_alloc_t(c.get(), &b.ra0[u], sizeof(float) * 3 * b.cout_p));
             IRO_TRY(codec_alloc_t(c.get(), &b.ra1[u], sizeof(float) * 3 * b.cout_p));
-            IRO_TRY(codec_alloc(c.get(), &b.rw[u], es * b.cout_p * 7 * b.cout_p));
-            IRO_TRY(codec_alloc(c.get(), &b.pw[u], es * b.cout_p * b.cout_p));
+            IRO_TRY(codec_alloc(c.get(), &b.rw[u], es * b.cout_p * round_to(7 * b.cout_p, slice)));
+            IRO_TRY(codec_alloc(c.get(), &b.pw[u], es * b.cout_p * round_to(b.cout_p, slice)));
         }
     }
-    c->last_p = round64(C);
+    c->last_p = pad_channels(C);
     IRO_REQUIRE(c->last_p <= 256, IRODORI_ERR_SHAPE, "codec head width (decoder_dim >> num_blocks) must be at most 256");
     c->x_elems = xe;
     c->s_elems = se;
@@ -482,7 +492,9 @@ int irodori_codec_load_weights(irodori_codec* c, const irodori_codec_weights* w)
     std::copy(w->out_proj_w, w->out_proj_w + (size_t)g.proj_dim * g.latent_dim, inw.begin());
     IRO_TRY(put_f32(c, c->in_w, inw));
     IRO_TRY(put_f32(c, c->in_b, padded(w->out_proj_b, g.proj_dim, c->proj_p)));
-    IRO_TRY(put_operand(c, c->stem_w, conv_rows(w->stem_w, g.decoder_dim, g.proj_dim, 7, c->dim_p, c->proj_p)));
+    const int slice = 128 / (int)c->esz;
+    IRO_TRY(put_operand(c, c->stem_w, conv_rows(w->stem_w, g.decoder_dim, g.proj_dim, 7, c->dim_p, c->proj_p,
+                                                round_to(7 * c->proj_p, slice))));
     if (w->stem_b) {
         if (!c->stem_b) IRO_TRY(codec_alloc_t(c, &c->stem_b, sizeof(float) * c->dim_p));
         IRO_TRY(put_f32(c, c->stem_b, padded(w->stem_b, g.decoder_dim, c->dim_p)));
@@ -498,8 +510,10 @@ int irodori_codec_load_weights(irodori_codec* c, const irodori_codec_weights* w)
         for (int u = 0; u < 3; u++) {
             IRO_TRY(put_f32(c, b.ra0[u], snake_consts(bw.res_alpha0[u], b.cout, b.cout_p)));
             IRO_TRY(put_f32(c, b.ra1[u], snake_consts(bw.res_alpha1[u], b.cout, b.cout_p)));
-            IRO_TRY(put_operand(c, b.rw[u], conv_rows(bw.res_conv_w[u], b.cout, b.cout, 7, b.cout_p, b.cout_p)));
-            IRO_TRY(put_operand(c, b.pw[u], conv_rows(bw.res_pw_w[u], b.cout, b.cout, 1, b.cout_p, b.cout_p)));
+            IRO_TRY(put_operand(c, b.rw[u], conv_rows(bw.res_conv_w[u], b.cout, b.cout, 7, b.cout_p, b.cout_p,
+                                                      round_to(7 * b.cout_p, slice))));
+            IRO_TRY(put_operand(c, b.pw[u], conv_rows(bw.res_pw_w[u], b.cout, b.cout, 1, b.cout_p, b.cout_p,
+                                                      round_to(b.cout_p, slice))));
             if (bw.res_conv_b[u]) {
                 if (!b.rb[u]) IRO_TRY(codec_alloc_t(c, &b.rb[u], sizeof(float) * b.cout_p));
                 IRO_TRY(put_f32(c, b.rb[u], padded(bw.res_conv_b[u], b.cout, b.cout_p)));

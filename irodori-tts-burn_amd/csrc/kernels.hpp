@@ -225,24 +225,28 @@ struct GemmArgs {
     const float* alpha;
     int alpha_n;
     long u_lo, u_hi;
-    // EPI_RESUNIT (launch_gemm_conv, one tile column: N = 64, 128 or 192): the codec
+    // EPI_RESUNIT (launch_gemm_conv, one tile column: N = 64, 96, 128 or 192): the codec
     // ResidualUnit's tail after its dilated conv, x[M, N] += Snake(acc + bias) @ W2^T +
-    // bias2 (W2 [N, N], the 1x1 conv; Snake with alpha), then U = Snake(x) with alpha2
-    // when U is set.  The Snake'd tile never leaves LDS.
+    // bias2 (W2 [N, K2] with K2 = N rounded up to 64 / 32 columns for bf16 / f32, zero
+    // past N: the 1x1 conv; Snake with alpha), then U = Snake(x) with alpha2 when U is set.
+    // The Snake'd tile never leaves LDS.
     const T* W2;
     const float* bias2;
     const float* alpha2;
     // launch_gemm_conv: A is an implicit im2col.  Row m of the GEMM, k = j * conv_cp + c
     // reads A[(m + j * conv_dil) * conv_cp + c] (A points at the source row the first tap
-    // of output row 0 reads); source rows at or past conv_rows read as zero.
+    // of output row 0 reads); source rows at or past conv_rows read as zero.  conv_cp is a
+    // multiple of half a 128-byte slice; K spans the taps rounded up to whole slices (the
+    // weights are zero there).
     int conv_cp, conv_dil, conv_rows;
 };
 template <typename T>
 int launch_gemm(int epi, const GemmArgs<T>& a, hipStream_t st);
 // The same epilogues over fp8 operands (K % 128 == 0); outputs in bf16 / f32 as above.
 int launch_gemm_fp8(int epi, const GemmArgs<bf16>& a, hipStream_t st);
-// Convolution as a GEMM over an implicit im2col (conv_* fields): K = taps * conv_cp with
-// conv_cp a multiple of one 128-byte slice; EPI_STORE, EPI_ADD or EPI_SNAKE.
+// Convolution as a GEMM over an implicit im2col (conv_* fields): K = taps * conv_cp rounded
+// up to whole 128-byte slices, conv_cp a multiple of half a slice; EPI_STORE, EPI_ADD,
+// EPI_SNAKE or EPI_RESUNIT.
 template <typename T>
 int launch_gemm_conv(int epi, const GemmArgs<T>& a, hipStream_t st);
 

@@ -208,10 +208,18 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
         const int rr = r < BM ? r : r - BM;
         voff[i] = (unsigned)rr * (unsigned)((r < BM ? lda : K) * ES) + (unsigned)swz(r, lane % 8) * 16u;
     }
-    // CONV: byte offset of slice kt in the A source = kt * 128 within the row span of its
-    // tap, plus the tap's extra (conv_dil - 1) rows per earlier tap.
-    [[maybe_unused]] const int conv_spt = CONV ? a.conv_cp / BK : 1;
+    // CONV: byte offset of slice kt in the A source = kt * 128 (the taps laid end to end),
+    // plus (conv_dil - 1) rows for each tap before the slice's tap j0 = kt BK / conv_cp.
+    // With conv_cp an odd multiple of BK / 2 a slice can straddle two taps, always at its
+    // middle: the lanes loading logical chunks 4..7 then belong to tap j0 + 1 and add one
+    // more step (voff_hi).
     [[maybe_unused]] const unsigned conv_dstep = CONV ? (unsigned)((a.conv_dil - 1) * a.conv_cp * ES) : 0u;
+    [[maybe_unused]] unsigned voff_hi[LPW];
+    if constexpr (CONV) {
+#pragma unroll
+        for (int i = 0; i < LPW; i++)
+            voff_hi[i] = voff[i] + (swz((wave * LPW + i) * 8 + lane / 8, lane % 8) >= 4 ? conv_dstep : 0u);
+    }
     // fp8: the tile's E8M0 block scales (BM rows x K/32 bytes) are staged in LDS past the
     // operand stages before the main loop, slice-major: the word of row r for slice kt (its
     // four k blocks) at (kt * BM + r) * 4, so a wave's 32 rows read 32 consecutive words.
@@ -232,10 +240,17 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
     do {                                                                                   \
         unsigned char* dst_ = smem + (stage_) * STAGE_BYTES + wave * LPW * 1024;           \
         const unsigned ws_ = (unsigned)(kt_) * 128u;                                       \
-        const unsigned as_ = CONV ? ws_ + (unsigned)((kt_) / conv_spt) * conv_dstep : ws_; \
+        unsigned as_ = ws_;                                                                \
+        bool split_ = false;                                                               \
+        if constexpr (CONV) {                                                              \
+            const int k0_ = (kt_) * BK, j0_ = k0_ / a.conv_cp;                             \
+            as_ += (unsigned)j0_ * conv_dstep;                                             \
+            split_ = k0_ - j0_ * a.conv_cp + BK > a.conv_cp;                               \
+        }                                                                                  \
         _Pragma("unroll") for (int i_ = 0; i_ < LPW; i_++) {                               \
             const bool isA = (wave * LPW + i_) * 8 < BM;                                   \
-            buf_load_lds16(isA ? rA : rW, voff[i_], isA ? as_ : ws_, dst_ + i_ * 1024);    \
+            const unsigned vo_ = (CONV && isA && split_) ? voff_hi[i_] : voff[i_];         \
+            buf_load_lds16(isA ? rA : rW, vo_, isA ? as_ : ws_, dst_ + i_ * 1024);         \
         }                                                                                  \
     } while (0)
 
@@ -447,17 +462,27 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
         // kt2 * BK .. + BK - 1, BM rows of 128 bytes, chunks swizzled as in the operand
         // stages), while the first W2 slice streams into the slot after it.  Phase 2:
         // acc = s @ W2^T over NK2 slices.  Phase 3: the residual add (+ next Snake).
+        // W2 is [BN, K2P] with K2P = BN rounded up to whole slices (zero columns); a partial
+        // last slice of the s tile is zero-filled past column BN.
         static_assert(BN % (8 * NW) == 0, "W2 slices split over the waves");
-        constexpr int NK2 = BN / BK, LPW2 = BN / 8 / NW, EPC = 16 / ES;
+        constexpr int NK2 = (BN + BK - 1) / BK, K2P = NK2 * BK, LPW2 = BN / 8 / NW, EPC = 16 / ES;
         unsigned char* tl = smem;
         unsigned char* w2l = smem + NK2 * BM * 128;
         __syncthreads();  // every wave is done with the main loop's stages
-        const __amdgpu_buffer_rsrc_t rW2 = make_rsrc(a.W2, (unsigned)(BN * BN * ES));
+        const __amdgpu_buffer_rsrc_t rW2 = make_rsrc(a.W2, (unsigned)(BN * K2P * ES));
         unsigned voff2[LPW2];
 #pragma unroll
         for (int i = 0; i < LPW2; i++) {
             const int r = (wave * LPW2 + i) * 8 + lane / 8;
-            voff2[i] = (unsigned)(r * BN * ES) + (unsigned)swz(r, lane % 8) * 16u;
+            voff2[i] = (unsigned)(r * K2P * ES) + (unsigned)swz(r, lane % 8) * 16u;
+        }
+        if constexpr (K2P != BN) {
+            constexpr int c0 = (BN % BK) / EPC;  // first empty chunk of the last slice
+            unsigned char* last = tl + (NK2 - 1) * BM * 128;
+            for (int idx = threadIdx.x; idx < BM * (8 - c0); idx += 64 * NW) {
+                const int r = idx / (8 - c0), c = c0 + idx % (8 - c0);
+                *reinterpret_cast<uint4*>(last + r * 128 + (swz(r, c) << 4)) = make_uint4(0u, 0u, 0u, 0u);
+            }
         }
 #pragma unroll
         for (int i = 0; i < LPW2; i++) buf_load_lds16(rW2, voff2[i], 0u, w2l + (wave * LPW2 + i) * 1024);
@@ -873,16 +898,17 @@ int launch_cfg(const GemmArgs<T>& a, hipStream_t st) {
     if (a.M <= 0 || a.N % BN != 0 || a.K % BK != 0 || a.K <= 0 || (F8 && a.K > kMaxK8)) return -1;
     if ((size_t)BN * a.K * ES > 0xffffffffull || (size_t)BM * a.K * ES > 0xffffffffull) return -1;
     if (CONV) {
-        if (a.conv_cp <= 0 || a.conv_cp % BK != 0 || a.K % a.conv_cp != 0 || a.conv_dil <= 0 || a.conv_rows < 0)
-            return -1;
-        const size_t taps = (size_t)(a.K / a.conv_cp);
+        // conv_cp a multiple of half a slice (a slice straddles at most two taps, at its
+        // middle); K = the taps' span rounded up to whole slices.
+        if (a.conv_cp <= 0 || a.conv_cp % (BK / 2) != 0 || a.conv_dil <= 0 || a.conv_rows < 0) return -1;
+        const size_t taps = (size_t)((a.K + a.conv_cp - 1) / a.conv_cp);
         if ((size_t)a.conv_rows * a.conv_cp * ES > 0xffffffffull ||
             ((size_t)BM + (taps - 1) * a.conv_dil) * a.conv_cp * ES > 0xffffffffull)
             return -1;
     }
     int tiles = ((a.M + BM - 1) / BM) * (a.N / BN);
     // EPI_RESUNIT keeps the Snake'd tile (BN / BK slices of BM rows) and one W2 slice in LDS.
-    constexpr int kResLds = EPI == EPI_RESUNIT ? (BN / BK) * BM * 128 + BN * 128 : 0;
+    constexpr int kResLds = EPI == EPI_RESUNIT ? ((BN + BK - 1) / BK) * BM * 128 + BN * 128 : 0;
     constexpr int kStageLds = STAGES * (BM + BN) * 128;
     const size_t lds = (size_t)(kStageLds > kResLds ? kStageLds : kResLds) + (F8 ? (size_t)BM * (a.K / 32) : 0);
     static bool attr_set = false;  // per instantiation; the attribute is process-wide
@@ -960,13 +986,14 @@ int launch_gemm_fp8(int epi, const GemmArgs<bf16>& a, hipStream_t st) {
 // 128x192 tiles: 2x2 waves of 64x96, five fragment reads per six MFMAs.
 template <typename T>
 int launch_gemm_conv(int epi, const GemmArgs<T>& a, hipStream_t st) {
-    const bool wide = a.N % 128 == 0, w192 = a.N % 192 == 0;
+    const bool wide = a.N % 128 == 0, w192 = a.N % 192 == 0, w96 = a.N % 96 == 0;
     if ((epi == EPI_SNAKE || epi == EPI_RESUNIT || (epi != EPI_RESUNIT && a.U)) && (!a.alpha || a.alpha_n <= 0))
         return -1;
     switch (epi) {
         case EPI_STORE:
             if (wide) return launch_cfg<T, 128, 128, 2, 2, 2, EPI_STORE, false, true>(a, st);
             if (w192) return launch_cfg<T, 128, 192, 2, 2, 2, EPI_STORE, false, true>(a, st);
+            if (a.N % 64 != 0 && w96) return launch_cfg<T, 256, 96, 4, 1, 2, EPI_STORE, false, true>(a, st);
             return launch_cfg<T, 64, 64, 2, 2, 4, EPI_STORE, false, true>(a, st);
         case EPI_SNAKE:
             if (!a.U) return -1;
@@ -988,6 +1015,7 @@ int launch_gemm_conv(int epi, const GemmArgs<T>& a, hipStream_t st) {
                 return launch_cfg<T, 256, 128, 4, 2, 2, EPI_RESUNIT, false, true>(a, st);
             if (a.N == 128) return launch_cfg<T, 128, 128, 2, 2, 2, EPI_RESUNIT, false, true>(a, st);
             if (a.N == 192) return launch_cfg<T, 128, 192, 2, 2, 2, EPI_RESUNIT, false, true>(a, st);
+            if (a.N == 96) return launch_cfg<T, 256, 96, 4, 1, 2, EPI_RESUNIT, false, true>(a, st);
             if (a.N == 64) return launch_cfg<T, 64, 64, 2, 2, 4, EPI_RESUNIT, false, true>(a, st);
             return -1;
     }
