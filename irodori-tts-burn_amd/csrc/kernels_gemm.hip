@@ -991,6 +991,10 @@ int launch_gemm_conv(int epi, const GemmArgs<T>& a, hipStream_t st) {
         return -1;
     switch (epi) {
         case EPI_STORE:
+            // Grids of under 256 128x128 tiles (the stem: 750 frames x 1536 channels over a
+            // K of 7168) take 64x64 tiles, four times as many workgroups.
+            if (wide && (long)((a.M + 127) / 128) * (a.N / 128) < 256 && a.N % 64 == 0)
+                return launch_cfg<T, 64, 64, 2, 2, 4, EPI_STORE, false, true>(a, st);
             if (wide) return launch_cfg<T, 128, 128, 2, 2, 2, EPI_STORE, false, true>(a, st);
             if (w192) return launch_cfg<T, 128, 192, 2, 2, 2, EPI_STORE, false, true>(a, st);
             if (a.N % 64 != 0 && w96) return launch_cfg<T, 256, 96, 4, 1, 2, EPI_STORE, false, true>(a, st);

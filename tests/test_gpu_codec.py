@@ -21,7 +21,7 @@ BF16, F32 = ih.InferenceBackendKind.HIP_BF16, ih.InferenceBackendKind.HIP_F32
 TOL = {F32: 1e-4, BF16: 2e-2}
 
 CONFIGS = {
-    "tiny": ih.codec_tiny,  # rates 3 (odd) and 4; channels 192 -> 96 -> 48, padded on the GPU
+    "tiny": ih.codec_tiny,  # rates 3 (odd) and 4; channels 192 -> 96 (K slices straddling taps) -> 48 (padded to 64)
     "even": lambda: ih.CodecConfig(latent_dim=4, proj_dim=32, decoder_dim=64, rates=(2, 4)),
 }
 
@@ -47,6 +47,22 @@ def test_codec_vs_oracle(oracle64, name, backend):
     assert got.shape == ref.shape and err < TOL[backend]
     ref2 = oracle64.codec_decode(cfg, cw, lat[1:, :20])
     assert rel_l2(again, ref2) < TOL[backend]
+
+
+@pytest.mark.parametrize("frames", [1, 2])
+@pytest.mark.parametrize("backend", [F32, BF16], ids=["f32", "bf16"])
+def test_shortest_latents(oracle64, backend, frames):
+    # One and two latent frames: every convolution reads mostly zero padding (the halos),
+    # the transposed convolutions' first and last windows are partial.
+    cfg = ih.codec_tiny()
+    cw = ih.CodecWeights.random(cfg, 11)
+    lat = latent(cfg, 2, frames, 12)
+    with ih.HipDacVaeCodec(cfg, backend, max_frames=4) as codec:
+        codec.load_weights(cw)
+        got = codec.decode(lat)
+    ref = oracle64.codec_decode(cfg, cw, lat)
+    assert got.shape == ref.shape == (2, 1, frames * cfg.hop_length)
+    assert rel_l2(got, ref) < TOL[backend]
 
 
 @pytest.mark.parametrize("backend", [F32, BF16], ids=["f32", "bf16"])
