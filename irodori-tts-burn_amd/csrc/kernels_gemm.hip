@@ -1019,7 +1019,7 @@ int launch_gemm_conv(int epi, const GemmArgs<T>& a, hipStream_t st) {
                 return launch_cfg<T, 256, 128, 4, 2, 2, EPI_RESUNIT, false, true>(a, st);
             if (a.N == 128) return launch_cfg<T, 128, 128, 2, 2, 2, EPI_RESUNIT, false, true>(a, st);
             if (a.N == 192) return launch_cfg<T, 128, 192, 2, 2, 2, EPI_RESUNIT, false, true>(a, st);
-            if (a.N == 96) return launch_cfg<T, 256, 96, 4, 1, 2, EPI_RESUNIT, false, true>(a, st);
+            if (a.N == 96) return launch_cfg<T, 128, 96, 4, 1, 2, EPI_RESUNIT, false, true>(a, st);
             if (a.N == 64) return launch_cfg<T, 64, 64, 2, 2, 4, EPI_RESUNIT, false, true>(a, st);
             return -1;
     }
