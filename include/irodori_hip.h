@@ -375,7 +375,8 @@ int irodori_codec_hop_length(const irodori_codec* codec);
 int irodori_codec_decode(irodori_codec* codec, int batch, int frames, const float* latent,
                          float* wav);
 /* The same on device pointers, enqueued on `stream` (NULL: the codec's own stream) without
- * waiting.  Rows run one after another on the codec's work buffers. */
+ * waiting.  Rows run one after another on the codec's work buffers, so calls that overlap
+ * on one codec (on different streams, or from different threads) race. */
 int irodori_codec_decode_device(irodori_codec* codec, int batch, int frames,
                                 const float* latent, float* wav, void* stream);
 
@@ -388,7 +389,9 @@ int irodori_op_rms_norm(const float* x, const float* w, int rows, int dim, float
 int irodori_op_fused_adaln(const float* x, const float* scale, const float* shift, int batch,
                            int seq, int dim, float eps, float* y, void* stream);
 /* native_fa_sdpa_wgsl / native_fa_sdpa_f16_in (fused_sdpa_native.rs:220-302,
- * fused_sdpa_native_f16.rs:181): out = softmax(q k^T * scale + mask) v.
+ * fused_sdpa_native_f16.rs:181), and fused_sdpa_wgsl / tiled_fa_sdpa_wgsl (fused_sdpa.rs:107,
+ * fused_sdpa_tiled.rs:202), which take the same tensors and differ only in their WGSL tiling
+ * config: out = softmax(q k^T * scale + mask) v.
  * q [B,H,Sq,Dh], k/v [B,H,Skv,Dh] in `dtype` (F32 or BF16), mask [B,Skv] f32 with
  * 1.0 = attend (may be NULL), out [B,H,Sq,Dh] f32.  Dh in {64, 128}.  A fully masked
  * query row yields 0. */
