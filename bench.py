@@ -358,22 +358,37 @@ def run_encode(args, np, torch, ih):
     eng.load_weights(w)
     eng.load_ctx_proj_weights(proj)
 
+    import threading
+
     def request():
+        # The two encoders are independent and own a stream each: the speaker encoder runs
+        # on a second host thread (the C calls release the GIL), so their kernels overlap.
+        out = {}
+
+        def speaker():
+            t = time.perf_counter()
+            out["s"] = senc.forward(sm, latent=lat)
+            out["s_ms"] = (time.perf_counter() - t) * 1e3
+
         t0 = time.perf_counter()
+        th = threading.Thread(target=speaker)
+        th.start()
         ts, tmo = tenc.forward(tm, ids=ids)
+        te = (time.perf_counter() - t0) * 1e3
+        th.join()
         t1 = time.perf_counter()
-        ss, smo = senc.forward(sm, latent=lat)
-        t2 = time.perf_counter()
+        ss, smo = out["s"]
         eng.build_context_kv(0, ts[0], tmo[0], ss[0], smo[0])
-        t3 = time.perf_counter()
-        return (t1 - t0) * 1e3, (t2 - t1) * 1e3, (t3 - t2) * 1e3
+        t2 = time.perf_counter()
+        return (t1 - t0) * 1e3, (t2 - t1) * 1e3, te, out["s_ms"]
 
     for _ in range(args.warmup):
         request()
     parts = np.array([request() for _ in range(args.steps)])
-    ms = float(parts.sum(1).mean())
-    te_ms, se_ms, kv_ms = (float(v) for v in parts.mean(0))
-    log("encode: text %.2f ms, speaker %.2f ms, context build %.2f ms" % (te_ms, se_ms, kv_ms))
+    ms = float(parts[:, :2].sum(1).mean())
+    enc_ms, kv_ms, te_ms, se_ms = (float(v) for v in parts.mean(0))
+    log("encode: encoders %.2f ms (text %.2f, speaker %.2f, overlapped), context build %.2f ms"
+        % (enc_ms, te_ms, se_ms, kv_ms))
     # GEMM + attention FLOPs of an encoder over n tokens (TextBlock: [Wq|Wk|Wv|Wg], Wo, W1|W3, W2;
     # attention 4 n^2 E).
     def enc_flops(ec, n):
@@ -406,11 +421,12 @@ def run_encode(args, np, torch, ih):
         "dtype": "bf16",
         "data": "synthetic: random-init encoders (1280 wide, 14 blocks, 10 heads, SwiGLU 3328) and DiT, "
                 "random token ids / N(0,1) reference latents",
-        "config": {"workload": "text encoder 256 tokens + speaker encoder 375 frames (+ mean token) + "
-                               "12-layer context-KV build, one CFG row; host pointers in and out",
+        "config": {"workload": "text encoder 256 tokens + speaker encoder 375 frames (+ mean token), "
+                               "run concurrently from two host threads, then the 12-layer context-KV "
+                               "build, one CFG row; host pointers in and out",
                    "global_batch": 1, "seq_len": Tt + Ts, "parallelism": "none"},
-        "parts_ms": {"text_encoder": round(te_ms, 3), "speaker_encoder": round(se_ms, 3),
-                     "context_build": round(kv_ms, 3)},
+        "parts_ms": {"encoders_overlapped": round(enc_ms, 3), "text_encoder": round(te_ms, 3),
+                     "speaker_encoder": round(se_ms, 3), "context_build": round(kv_ms, 3)},
         "achieved_tflops": round(flops / (ms * 1e-3) / 1e12, 1),
         "roofline": None,
         "cpu_baseline": cpu,
