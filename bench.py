@@ -1,4 +1,4 @@
-"""Benchmark: 40-step Joint-CFG RF sampling of a 750-frame latent on
+"""Benchmark: 40-step Joint-CFG RF sampling of a 750-frame latent (the headline workload) on
 one MI355X through libirodori_hip, plus the roofline of the dominant kernel and the CPU
 oracle timed on the host's cores.
 
@@ -255,7 +255,7 @@ def main():
 
 
 def run_cfg5(args, np, torch, ih):
-    """16 utterances x Joint CFG = 32 rows of the 12-layer d1024 DiT, latent
+    """Batched throughput: 16 utterances x Joint CFG = 32 rows of the 12-layer d1024 DiT, latent
     lengths U[200,750] padded to 750 with the latent key mask, text valid lengths U[32,256],
     40 Euler steps; fp8 (e4m3 weights with per-output-channel f32 scales, GEMM inputs with
     power-of-two scales per 32 values, bf16 attention) or bf16.  Aggregate latent

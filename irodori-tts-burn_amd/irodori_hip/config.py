@@ -82,13 +82,13 @@ class DitConfig:
 
 
 def cfg_cpu_plumbing() -> DitConfig:
-    """4 layers, d=256, 4x64 heads, SwiGLU 704, latent 32."""
+    """The CPU-plumbing configuration: 4 layers, d=256, 4x64 heads, SwiGLU 704, latent 32."""
     return DitConfig(latent_dim=32, model_dim=256, num_layers=4, num_heads=4, mlp_hidden=704,
                      adaln_rank=64, timestep_embed_dim=256, norm_eps=1e-5)
 
 
 def cfg_full_rf() -> DitConfig:
-    """12 layers, d=1024, 16x64 heads, SwiGLU 2816, latent 32."""
+    """The benchmark configuration: 12 layers, d=1024, 16x64 heads, SwiGLU 2816, latent 32."""
     return DitConfig(latent_dim=32, model_dim=1024, num_layers=12, num_heads=16,
                      mlp_hidden=2816, adaln_rank=256, timestep_embed_dim=512, norm_eps=1e-5)
 

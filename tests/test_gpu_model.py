@@ -1,7 +1,7 @@
 """GPU parity of the whole RF-step DiT path (libirodori_hip through the C ABI) against the
 CPU oracle, on identical seeded inputs and random-init weights.
 
-Bars (BASELINE north star): f32 HIP path within 1e-4 relative L2 per block, bf16 within
+Bars: f32 HIP path within 1e-4 relative L2 per block, bf16 within
 1e-2 per block and 2e-2 on the final sampled latent.
 """
 import dataclasses
@@ -81,7 +81,7 @@ def test_block_forward_matches_oracle(oracle64, backend):
 
 @pytest.mark.parametrize("backend", [F32, BF16], ids=["f32", "bf16"])
 def test_sample_joint_cfg_cfg1(oracle64, backend):
-    # BASELINE config 1 sampled for 4 Euler steps (Joint CFG, scale 3, min_t 0).
+    # The CPU-plumbing configuration sampled for 4 Euler steps (Joint CFG, scale 3, min_t 0).
     cfg = ih.cfg_cpu_plumbing()
     w = ih.DitWeights.random(cfg, 0)
     ctx = ih.make_context_kv(cfg, 1, 16, 32, seed=1)
@@ -165,7 +165,7 @@ def test_forward_errors_are_reported():
     e.close()
 
 
-# ---- BASELINE config 4 (12 layers, d=1024, 750 frames, 631 context keys) ------------------
+# ---- the benchmark configuration (12 layers, d=1024, 750 frames, 631 context keys) ------------------
 def cfg4_inputs():
     cfg = ih.cfg_full_rf()
     w = ih.DitWeights.random(cfg, 0)
