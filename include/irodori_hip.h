@@ -54,7 +54,7 @@ extern "C" {
 /* bf16 activations and attention; the block GEMMs (QKV+gate, W_o, W1|W3, W2) on e4m3fn
  * operands: weights with one f32 scale per output channel, GEMM inputs with one
  * power-of-two scale per 32 values along k (the gfx950 scaled fp8 MFMA).  No counterpart in
- * the reference (BASELINE config 5's fp8 weights); needs model_dim, mlp_hidden % 128 == 0. */
+ * the reference (fp8 weights for batched throughput); needs model_dim, mlp_hidden % 128 == 0. */
 #define IRODORI_DTYPE_FP8 2
 
 #define IRODORI_CFG_INDEPENDENT 0 /* CfgGuidanceMode (src/config/sampling.rs:100-108) */
@@ -228,7 +228,7 @@ int irodori_sample(irodori_ctx* ctx, const irodori_sampler_params* params, int u
                    int seq, const float* x0, float* x_out);
 /* Sampling of a padded variable-length batch: utterance u attends to its first
  * lengths[u] latent frames (in every role), so frames below lengths[u] match an unpadded
- * run of that utterance (BASELINE config 5's padded batches; the reference sampler always
+ * run of that utterance (padded batches of utterances; the reference sampler always
  * passes latent_mask = None, euler_sampler.rs:410-523).  lengths: host int32 [U]. */
 int irodori_sample_masked(irodori_ctx* ctx, const irodori_sampler_params* params, int utterances,
                           int seq, const int32_t* lengths, const float* x0, float* x_out);

@@ -82,7 +82,7 @@ def test_reference_widths_short(oracle64, backend):
 
 
 def test_full_utterance_prefix_vs_oracle(oracle32):
-    # BASELINE's utterance length (750 frames -> 1.44 M samples) in bf16: finite, in [-1, 1],
+    # The benchmark's utterance length (750 frames -> 1.44 M samples) in bf16: finite, in [-1, 1],
     # two rows decoded together equal each decoded alone (bit for bit), and the first 14
     # frames match the oracle's 24-frame decode at the bf16 bar.
     cfg = ih.codec_default()

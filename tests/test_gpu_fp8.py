@@ -1,5 +1,5 @@
 """GPU parity of the fp8 compute mode (IRODORI_DTYPE_FP8: the block GEMMs on e4m3 operands,
-BASELINE config 5) against the oracle's fp8 mode (Oracle(gemm_fp8=True), whose quantized
+the batched-throughput workload) against the oracle's fp8 mode (Oracle(gemm_fp8=True), whose quantized
 arithmetic test_oracle_fp8.py pins), through the C ABI on the same seeded inputs.
 
 The fp8 pieces are pinned on their own first: the device quantizer bit for bit against the

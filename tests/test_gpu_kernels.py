@@ -2,7 +2,7 @@
 
 Mirrors the reference's kernel tests (rms_norm.rs / fused_adaln.rs / fused_sdpa_native.rs
 test modules: their shapes, deterministic sin/cos inputs, masks and the 1e-5 / 1e-4
-tolerances for f32) and adds BASELINE config 2 (isolated joint attention, bf16).
+tolerances for f32) and adds the isolated joint-attention workload (bf16).
 Tolerances: f32 within 1e-5 abs (the reference's own), bf16 within 1e-2 relative L2.
 """
 import numpy as np
@@ -105,7 +105,7 @@ def test_sdpa_all_masked_rows_are_zero():
 
 
 def test_sdpa_config2_joint_shape_bf16(oracle64):
-    # B=2, H=16, Dh=64, 750 queries; keys = 750 latent ++ 256 text ++
+    # Isolated joint attention: B=2, H=16, Dh=64, 750 queries; keys = 750 latent ++ 256 text ++
     # 375 speaker, text valid length uniform in [32, 256], Q/K/V ~ N(0, 1).  (RoPE is part
     # of the model path and is covered by the model tests.)
     B, H, Sq, Dh, Tt, Ts = 2, 16, 750, 64, 256, 375

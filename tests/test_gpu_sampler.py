@@ -2,7 +2,7 @@
 euler_sampler.rs:132-718) against the oracle's sample_rf, whose loop is pinned on the CPU
 (test_oracle_sampler.py), through the C ABI on the same seeded inputs.
 
-Bars: f32 path 1e-4 relative L2 on the final latent, bf16 2e-2 (BASELINE north star).
+Bars: f32 path 1e-4 relative L2 on the final latent, bf16 2e-2.
 """
 import numpy as np
 import pytest

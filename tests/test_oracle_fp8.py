@@ -1,5 +1,5 @@
 """CPU pins of the oracle's fp8 (e4m3fn) GEMM operands, the arithmetic of the HIP path's
-fp8 compute mode (the reference has no fp8 path):
+fp8 compute mode (the batched-throughput workload; the reference has no fp8 path):
 
 * e4m3 encoding / decoding against torch's float8_e4m3fn conversion (a library routine:
   round to nearest, ties to even), over every code and a dense sweep of values;
