@@ -1,4 +1,4 @@
-"""Writes the golden fixture of the full-size RF run with the CPU
+"""Writes the golden fixture of the full-size RF run (the benchmark configuration) with the CPU
 oracle (f32 arithmetic, the NdArray<f32> analogue): 40 Joint-CFG Euler steps (scale 3,
 min_t 0, max_t 1) of the 12-layer d=1024 DiT on seeded synthetic inputs.
 
