@@ -25,6 +25,8 @@ PEAK_HBM_GBS = 8000.0
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "w13_gemm_config4_hbm_traffic.txt")
+CODEC_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "codec_decode_hbm_traffic.txt")
+CODEC_KERNELS = ("gemm_kernel", "codec_in_kernel", "codec_head_kernel", "zero_halo_kernel")
 W13_KERNEL = "gemm_kernelIDF16bLi128ELi128ELi2ELi2ELi2ELi2E"  # bf16 128x128, EPI_SWIGLU
 COPY_BYTES = 1 << 30  # the --copy-calibration copy: reads and writes 1 GiB
 
@@ -78,11 +80,55 @@ def pmc_summary(fetch_csv, write_csv):
     return "\n".join(lines)
 
 
-def read_traffic():
-    """Calibrated HBM bytes per w13 launch from the committed PMC summary, or None."""
+def pmc_codec_summary(fetch_csv, write_csv, rows=2):
+    """Whole-decode HBM traffic from two rocprofv3 --pmc runs of `--workload codec
+    --copy-calibration` (FETCH_SIZE, then WRITE_SIZE): the calibrated bytes of every decode
+    kernel (convolution GEMMs, out_proj, halo clears, head), per decode of `rows` rows."""
+    import csv
+    per = {}
+    for counter, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
+        for r in csv.DictReader(open(path)):
+            if r["Counter_Name"] == counter:
+                per.setdefault(counter, {}).setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+    lines, factor = [], {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        copies = per[counter].get("__amd_rocclr_copyBuffer", [])
+        kib = max(copies) if copies else 0.0
+        if kib < 0.25 * COPY_BYTES / 1024:
+            raise SystemExit("no 1 GiB calibration copy in %s (run with --copy-calibration)" % counter)
+        factor[counter] = COPY_BYTES / (kib * 1024.0)
+        lines.append("%s calibration: the 1 GiB copy counts %.1f KiB -> factor %.4f bytes per counted byte"
+                     % (counter, kib, factor[counter]))
+    heads = [n for n in per["FETCH_SIZE"] if "codec_head_kernel" in n]
+    if not heads:
+        raise SystemExit("no codec_head_kernel dispatch in the counter files")
+    decodes = len(per["FETCH_SIZE"][heads[0]]) / rows
+    lines.append("decodes in the run: %g (%d rows each)" % (decodes, rows))
+    lines.append("")
+    lines.append("%-72s %6s %14s %14s" % ("kernel (decode kernels only)", "calls", "read MB/decode", "write MB/decode"))
+    tot_r = tot_w = 0.0
+    for n in sorted(per["FETCH_SIZE"], key=lambda n: -sum(per["FETCH_SIZE"][n])):
+        if not any(k in n for k in CODEC_KERNELS):
+            continue
+        rd = sum(per["FETCH_SIZE"][n]) * 1024.0 * factor["FETCH_SIZE"] / decodes
+        wr = sum(per["WRITE_SIZE"].get(n, [0.0])) * 1024.0 * factor["WRITE_SIZE"] / decodes
+        tot_r += rd
+        tot_w += wr
+        short = n.replace("_ZN7irodori12_GLOBAL__N_1", "")
+        short = short if len(short) <= 72 else short[:69] + "..."
+        lines.append("%-72s %6d %14.1f %14.1f" % (short, len(per["FETCH_SIZE"][n]), rd / 1e6, wr / 1e6))
+    lines.append("")
+    lines.append("decode_read_bytes: %d" % round(tot_r))
+    lines.append("decode_write_bytes: %d" % round(tot_w))
+    lines.append("traffic_bytes_per_decode: %d" % round(tot_r + tot_w))
+    return "\n".join(lines)
+
+
+def read_traffic(path=TRAFFIC_FILE, key="traffic_bytes_per_launch:"):
+    """Calibrated HBM bytes from a committed PMC summary (per w13 launch by default), or None."""
     try:
-        for line in open(TRAFFIC_FILE):
-            if line.startswith("traffic_bytes_per_launch:"):
+        for line in open(path):
+            if line.startswith(key):
                 return int(line.split(":")[1])
     except OSError:
         pass
@@ -115,7 +161,7 @@ def main():
                          "counter_collection.csv files of this script and exit")
     args = ap.parse_args()
     if args.pmc_summary:
-        print(pmc_summary(*args.pmc_summary))
+        print(pmc_codec_summary(*args.pmc_summary) if args.workload == "codec" else pmc_summary(*args.pmc_summary))
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the RF step of one model instance "
@@ -433,6 +479,28 @@ def run_encode(args, np, torch, ih):
     }
 
 
+def codec_bytes(ccfg, T, es=2):
+    """Compulsory HBM bytes of the decode's kernel sequence over T latent frames (each
+    tensor read or written once per kernel that touches it; es-byte GEMM operands, f32
+    residual stream): out_proj, the stem, per block the transposed convolution and three
+    ResidualUnits (one kernel each: operand in, x in and out, next operand out; two kernels
+    for streams wider than 192 channels: + the 1x1 operand out and in), the head."""
+    b = T * ccfg.latent_dim * 4 + T * ccfg.proj_dim * es                       # out_proj
+    b += T * ccfg.proj_dim * es + T * ccfg.decoder_dim * (4 + es)               # stem
+    L = T
+    for i, r in enumerate(ccfg.rates):
+        C, O = ccfg.block_dims(i)
+        b += L * C * es + L * r * O * (4 + es)                                  # transposed conv
+        L *= r
+        last = i == ccfg.num_blocks - 1
+        for u in range(3):
+            per = es + 8 + (0 if (last and u == 2) else es)
+            if O > 192:
+                per += 2 * es                                                   # the 1x1 operand
+            b += L * O * per
+    return b + L * ccfg.head_dim * 4 + L * 4                                    # head
+
+
 def codec_flops(ccfg, T):
     """Algorithmic FLOPs of DacVaeCodec::decode over T latent frames (unpadded channels):
     out_proj, stem (k 7), per block the transposed convolution (two taps of C inputs per
@@ -465,6 +533,12 @@ def run_codec(args, np, torch, ih):
     # decode is enqueued on (handle 0, torch's default stream, would mean the codec's own).
     st = torch.cuda.Stream()
     torch.cuda.synchronize()
+    if args.copy_calibration:  # the known-size kernel that scales the --pmc readings
+        src = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     for _ in range(args.warmup):
         codec.decode_device(d_lat.data_ptr(), B, T, d_wav.data_ptr(), st.cuda_stream)
     torch.cuda.synchronize()
@@ -514,7 +588,10 @@ def run_codec(args, np, torch, ih):
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS
                      if args.codec_dtype == "bf16" else 157.3, "unit": "TFLOP/s",
                      "frac": round(achieved / (PEAK_BF16_TFLOPS if args.codec_dtype == "bf16" else 157.3), 4),
-                     "traffic": None,
+                     "traffic": read_traffic(CODEC_TRAFFIC_FILE, "traffic_bytes_per_decode:"),
+                     "traffic_unit": "HBM bytes per decode (rocprofv3 FETCH_SIZE + WRITE_SIZE over the decode "
+                                     "kernels, copy-calibrated; profiles/codec_decode_hbm_traffic.txt)",
+                     "algorithmic_bytes": B * codec_bytes(ccfg, T, 2 if args.codec_dtype == "bf16" else 4),
                      "scope": "whole decode: algorithmic convolution FLOPs (unpadded channels) over the "
                               "event-timed decode, element-wise passes included"},
         "cpu_baseline": cpu,
