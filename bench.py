@@ -219,8 +219,9 @@ def main():
     out = d_out.cpu().numpy()
     assert np.all(np.isfinite(out)), "non-finite sampler output"
 
-    # Per-kernel device time (HIP events on the context's stream) for one block.
-    kt = eng.profile_layer(2 * U, S, args.profile_iters)
+    # Per-kernel device time (HIP events on the context's stream) at the RF graph's launch
+    # shape: one CFG row per role chain (M = S), weights cycling through the 12 layers.
+    kt = eng.profile_layer(U, S, args.profile_iters)
     if args.copy_calibration:
         src = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
         dst = torch.empty_like(src)
@@ -229,13 +230,14 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     log("kernel us: " + ", ".join("%s=%.1f" % (k, v) for k, v in kt.items()))
-    M, D, F, H, Dh = 2 * U * S, cfg.model_dim, cfg.mlp_hidden, cfg.num_heads, cfg.head_dim
+    M, D, F, H, Dh = U * S, cfg.model_dim, cfg.mlp_hidden, cfg.num_heads, cfg.head_dim
     flops = {
         "qkvg_gemm": 2.0 * M * D * 4 * D,
         "wo_gemm": 2.0 * M * D * D,
         "w13_gemm": 2.0 * M * D * 2 * F,
         "w2_gemm": 2.0 * M * F * D,
-        "attention": 4.0 * 2 * U * H * S * (S + Tt + Ts) * Dh,
+        # the conditioned row (the profiled chain): every latent and context key
+        "attention": 4.0 * U * H * S * (S + Tt + Ts) * Dh,
     }
     util = {k: flops[k] / (kt[k + "_us"] * 1e-6) / (PEAK_BF16_TFLOPS * 1e12) for k in flops}
     mlp_util = (flops["w13_gemm"] + flops["w2_gemm"]) / (
@@ -288,7 +290,7 @@ def main():
                       "w13_gemm": round(util["w13_gemm"], 4), "w2_gemm": round(util["w2_gemm"], 4)},
         "kernel_us": {k: round(v, 2) for k, v in kt.items()},
         "norm_mod_gbs": round(norm_gbs, 1),
-        "roofline": {"kernel": "w13_gemm (SwiGLU up-projection, 1500x1024x5632)", "bound": "mfma",
+        "roofline": {"kernel": "w13_gemm (SwiGLU up-projection, %dx1024x5632, one CFG row as the RF graph launches it)" % M, "bound": "mfma",
                      "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": read_traffic(),
                      "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, "

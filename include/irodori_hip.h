@@ -56,6 +56,9 @@ extern "C" {
  * power-of-two scale per 32 values along k (the gfx950 scaled fp8 MFMA).  No counterpart in
  * the reference (fp8 weights for batched throughput); needs model_dim, mlp_hidden % 128 == 0. */
 #define IRODORI_DTYPE_FP8 2
+/* IEEE half storage with f32 arithmetic: the Q/K/V dtype of native_fa_sdpa_f16_in
+ * (fused_sdpa_native_f16.rs:181-200); accepted by irodori_op_sdpa only. */
+#define IRODORI_DTYPE_F16 3
 
 #define IRODORI_CFG_INDEPENDENT 0 /* CfgGuidanceMode (src/config/sampling.rs:100-108) */
 #define IRODORI_CFG_JOINT 1
@@ -240,12 +243,17 @@ int irodori_sample_device_masked(irodori_ctx* ctx, const irodori_sampler_params*
                                  int utterances, int seq, const int32_t* lengths,
                                  const float* d_x0, float* d_x_out);
 
-/* Average device time of each kernel of one DiT block at (batch, seq), measured with HIP
- * events on the context's stream over `iters` back-to-back launches per kernel (the
- * reference's NVTX per-call timings, docs/benchmarks/rtx-a6000.md:131-138, as a
- * measurement entry point).  Weights and context KV must be loaded.  Microseconds. */
+/* Average device time of each kernel of one DiT block over `batch` rows of `seq` frames,
+ * launched as one sampler role chain launches them (every row on the same timestep's
+ * modulation vector; batch = 1 is one CFG row of a Joint-CFG step), measured with HIP
+ * events on the context's stream over `iters` back-to-back launches per kernel, launch i
+ * using layer i % num_layers (weights and context K/V cycle through the layers as in an RF
+ * step) -- the reference's NVTX per-call timings (docs/benchmarks/rtx-a6000.md:131-138) as
+ * a measurement entry point.  norm_mod_us times the unfused adaLN kernel, which the
+ * sampler's bf16 chains fold into their GEMMs.  bf16 contexts; weights and context KV
+ * must be loaded.  Microseconds. */
 typedef struct irodori_kernel_times {
-    float norm_mod_us;   /* RMSNorm + adaLN modulation (one of the two per block) */
+    float norm_mod_us;   /* unfused RMSNorm + adaLN modulation kernel (x f32 -> h bf16) */
     float qkvg_gemm_us;  /* QKV + gate projection with head norm / RoPE epilogue */
     float attention_us;  /* joint flash attention + sigmoid gate */
     float wo_gemm_us;    /* output projection + gated residual */
@@ -389,12 +397,16 @@ int irodori_op_rms_norm(const float* x, const float* w, int rows, int dim, float
 int irodori_op_fused_adaln(const float* x, const float* scale, const float* shift, int batch,
                            int seq, int dim, float eps, float* y, void* stream);
 /* native_fa_sdpa_wgsl / native_fa_sdpa_f16_in (fused_sdpa_native.rs:220-302,
- * fused_sdpa_native_f16.rs:181), and fused_sdpa_wgsl / tiled_fa_sdpa_wgsl (fused_sdpa.rs:107,
- * fused_sdpa_tiled.rs:202), which take the same tensors and differ only in their WGSL tiling
- * config: out = softmax(q k^T * scale + mask) v.
- * q [B,H,Sq,Dh], k/v [B,H,Skv,Dh] in `dtype` (F32 or BF16), mask [B,Skv] f32 with
- * 1.0 = attend (may be NULL), out [B,H,Sq,Dh] f32.  Dh in {64, 128}.  A fully masked
- * query row yields 0. */
+ * fused_sdpa_native_f16.rs:181-200), and fused_sdpa_wgsl / tiled_fa_sdpa_wgsl
+ * (fused_sdpa.rs:107, fused_sdpa_tiled.rs:202), which take the same tensors and differ only
+ * in their WGSL tiling config: out = softmax(q k^T * scale + mask) v.
+ * q [B,H,Sq,Dh], k/v [B,H,Skv,Dh] in `dtype` (F32, BF16 or F16: native_fa_sdpa_f16_in's
+ * f16 storage, f32 accumulation), mask [B,Skv] f32 with 1.0 = attend (values < 0.5 mask
+ * the key; may be NULL), out [B,H,Sq,Dh] f32.  Dh in {64, 128}.  A fully masked query row
+ * yields 0.  Enqueued on `stream` without waiting.  With Dh = 64 and a 16-bit dtype the
+ * call stages Q (pre-scaled), V^T and the key bits in a device buffer it allocates and frees
+ * in stream order on `stream` (hipMallocAsync / hipFreeAsync), and runs the model's joint
+ * attention kernel on them; other shapes need no staging. */
 int irodori_op_sdpa(int dtype, const void* q, const void* k, const void* v, const float* mask,
                     int batch, int heads, int seq_q, int seq_kv, int head_dim, float scale,
                     float* out, void* stream);

@@ -452,6 +452,12 @@ int irodori_codec_create(int device, const irodori_codec_config* cfg, irodori_co
     }
     c->last_p = pad_channels(C);
     IRO_REQUIRE(c->last_p <= 256, IRODORI_ERR_SHAPE, "codec head width (decoder_dim >> num_blocks) must be at most 256");
+    // The convolution GEMMs address each haloed operand [frames + 2 halo, channels] through one
+    // 32-bit buffer resource, so the largest of them must stay below 4 GiB; rejected here,
+    // before the work buffers are allocated, rather than at the first decode.
+    IRO_REQUIRE(es * std::max(se, s2e) <= 0xffffffffull, IRODORI_ERR_SHAPE,
+                "codec max_frames too large: the largest convolution operand would take " +
+                    std::to_string(es * std::max(se, s2e)) + " bytes, above the 4 GiB a GEMM operand may span");
     c->x_elems = xe;
     c->s_elems = se;
     c->s2_elems = s2e;

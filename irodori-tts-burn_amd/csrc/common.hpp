@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
 #include <string>
 
 namespace irodori {
@@ -13,6 +14,10 @@ namespace irodori {
 // ---------------------------------------------------------------------------------
 typedef __bf16 bf16;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+// IEEE half: the storage type of the f16-input SDPA operator (f16 operands on the f16
+// matrix-core instructions, f32 accumulation and softmax).
+typedef _Float16 f16;
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x8 __attribute__((ext_vector_type(8)));
 // Raw 16-byte register chunk (native vector type, so arrays of it stay in VGPRs).
@@ -20,6 +25,7 @@ typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float to_f32(float v) { return v; }
 __device__ __forceinline__ float to_f32(bf16 v) { return static_cast<float>(v); }
+__device__ __forceinline__ float to_f32(f16 v) { return static_cast<float>(v); }
 
 template <typename T>
 __device__ __forceinline__ T from_f32(float v);
@@ -27,6 +33,8 @@ template <>
 __device__ __forceinline__ float from_f32<float>(float v) { return v; }
 template <>
 __device__ __forceinline__ bf16 from_f32<bf16>(float v) { return static_cast<bf16>(v); }
+template <>
+__device__ __forceinline__ f16 from_f32<f16>(float v) { return static_cast<f16>(v); }
 
 // Snake1d (codec/layers.rs:24-31): v + sin(a v)^2 / (a + 1e-9), from the channel's
 // constants (a, ar = a / pi, hc = 0.5 / (a + 1e-9)).  For bf16 results (rounded to 8 bits)
@@ -96,9 +104,16 @@ template <>
 struct Frag<float> {
     f32x8 v;
 };
+template <>
+struct Frag<f16> {
+    f16x8 v;
+};
 
 __device__ __forceinline__ void mma16(f32x4& acc, const Frag<bf16>& a, const Frag<bf16>& b) {
     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, acc, 0, 0, 0);
+}
+__device__ __forceinline__ void mma16(f32x4& acc, const Frag<f16>& a, const Frag<f16>& b) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.v, b.v, acc, 0, 0, 0);
 }
 __device__ __forceinline__ void mma16(f32x4& acc, const Frag<float>& a, const Frag<float>& b) {
 #pragma unroll
@@ -128,6 +143,12 @@ template <>
 __device__ __forceinline__ Frag<float> load_frag<float>(const float* p) {
     Frag<float> f;
     f.v = *reinterpret_cast<const f32x8*>(p);
+    return f;
+}
+template <>
+__device__ __forceinline__ Frag<f16> load_frag<f16>(const f16* p) {
+    Frag<f16> f;
+    f.v = *reinterpret_cast<const f16x8*>(p);
     return f;
 }
 
@@ -173,6 +194,15 @@ __device__ __forceinline__ int xcd_remap(int id, int n) {
 // Host-side error plumbing (thread-local last error, status codes of irodori_hip.h).
 // ---------------------------------------------------------------------------------
 void set_last_error(const std::string& msg);
+
+// Raises a kernel's dynamic-LDS limit once per process.  The first launch of a kernel
+// variant may come from several host threads at once (one context, encoder or codec per
+// thread), so the one-time call is guarded by a once_flag owned by the caller (one static
+// per kernel instantiation); every caller sees the call's result.
+inline hipError_t set_lds_limit_once(std::once_flag& once, hipError_t& rc, const void* fn, int bytes) {
+    std::call_once(once, [&] { rc = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes); });
+    return rc;
+}
 
 }  // namespace irodori
 

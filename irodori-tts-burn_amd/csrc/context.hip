@@ -116,6 +116,15 @@ struct irodori_ctx {
     uint8_t *h8 = nullptr, *h8s = nullptr;  // [rows*S, D], [rows*S, D/32]
     uint8_t *o8 = nullptr, *o8s = nullptr;  // [rows*S, D], [rows*S, D/32]
     uint8_t *u8 = nullptr, *u8s = nullptr;  // [rows*S, F], [rows*S, F/32]
+    // Fused adaLN (bf16 compute; GemmArgs): h holds x (1 + scale) of the next norm and rstat
+    // the row sums of x^2 per 32 columns; the QKV+gate and W1|W3 GEMMs apply 1 / rms and add
+    // the shift's product with their weights, biasq / bias13 [L][nvec_cap][N] per modulation
+    // vector (computed with the table from the bf16 shift rows in shift_stage).
+    bool fused = false;
+    float* rstat = nullptr;     // [rows*S, D/32]
+    float* biasq = nullptr;     // [L][nvec_cap][4D]
+    float* bias13 = nullptr;    // [L][nvec_cap][2F], W1/W3 columns interleaved per 32
+    void* shift_stage = nullptr;  // bf16 [2L][nvec_cap][D]
     float* rope_cos = nullptr;
     float* rope_sin = nullptr;
     float* xt = nullptr;    // [rows, S, P] sampler state / forward input
@@ -248,6 +257,11 @@ int ensure_nvec(irodori_ctx* c, int nvec) {
     IRO_TRY(dalloc(c, &c->cond, sizeof(float) * (size_t)cap * 3 * D));
     IRO_TRY(dalloc(c, &c->mid, sizeof(float) * (size_t)L * 6 * cap * r));
     IRO_TRY(dalloc(c, &c->tab, sizeof(float) * (size_t)cap * L * 6 * D));
+    if (c->fused) {
+        IRO_TRY(dalloc(c, &c->biasq, sizeof(float) * (size_t)L * cap * 4 * D));
+        IRO_TRY(dalloc(c, &c->bias13, sizeof(float) * (size_t)L * cap * 2 * g.mlp_hidden));
+        IRO_TRY(dev_alloc(c, &c->shift_stage, sizeof(bf16) * (size_t)2 * L * cap * D));
+    }
     c->nvec_cap = cap;
 
     // Job tables (pointers depend on the buffers above).
@@ -283,10 +297,13 @@ int ensure_nvec(irodori_ctx* c, int nvec) {
 }
 
 // Modulation table for nvec timesteps already in c->tvec (or, when skip_mlp, for cond
-// vectors already in c->cond): tab[v][l][k][ch][:].
-int enqueue_mod_table(irodori_ctx* c, int nvec, bool skip_mlp) {
+// vectors already in c->cond): tab[v][l][k][ch][:].  With the fused adaLN also the shift
+// biases of layers [l0, l1) (whose weights must be loaded; all layers by default):
+// biasq[l][v] = shift_attn(v, l) W_qkvg, bias13[l][v] = shift_mlp(v, l) W13.
+int enqueue_mod_table(irodori_ctx* c, int nvec, bool skip_mlp, int l0 = 0, int l1 = -1) {
     const auto& g = c->cfg;
     int D = g.model_dim, L = g.num_layers, r = g.adaln_rank;
+    if (l1 < 0) l1 = L;
     if (!skip_mlp) {
         launch_timestep_embedding(c->tvec, nvec, g.timestep_embed_dim, c->emb, c->stream);
         for (int j = 0; j < 3; j++)
@@ -294,8 +311,34 @@ int enqueue_mod_table(irodori_ctx* c, int nvec, bool skip_mlp) {
     }
     launch_vec_linear(c->d_jobs_down, L * 6, nvec, r, c->stream);
     launch_vec_linear(c->d_jobs_up, L * 6, nvec, D, c->stream);
+    if (c->fused) {
+        const int cap = c->nvec_cap, F = g.mlp_hidden;
+        bf16* stage = static_cast<bf16*>(c->shift_stage);
+        launch_shift_stage(c->tab, nvec, cap, L, D, stage, c->stream);
+        for (int l = l0; l < l1; l++)
+            for (int k = 0; k < 2; k++) {
+                GemmArgs<bf16> ga{};
+                ga.A = stage + (size_t)(l * 2 + k) * cap * D;
+                ga.W = static_cast<const bf16*>(k == 0 ? c->layers[l].w_qkvg : c->layers[l].w13);
+                ga.M = nvec;
+                ga.N = k == 0 ? 4 * D : 2 * F;
+                ga.K = D;
+                ga.S = nvec;
+                ga.C = (k == 0 ? c->biasq : c->bias13) + (size_t)l * cap * ga.N;
+                if (launch_gemm<bf16>(EPI_STORE, ga, c->stream)) {
+                    set_last_error("shift bias gemm shape");
+                    return IRODORI_ERR_SHAPE;
+                }
+            }
+    }
     return check_launch("modulation table");
 }
+
+// Whether a forward over B rows with modulation table mt runs the fused adaLN: the bf16
+// context supports it and every row maps to one modulation vector (a sampler evaluation,
+// or a single-row forward).  Decided from (mt, B) alone, so in_proj and every block part
+// of the same forward agree.
+bool fused_for(const irodori_ctx* c, const ModTable& mt, int B) { return c->fused && mt.rows_per_vec >= B; }
 
 // The kernels of one DiT block (diffusion.rs:62-105), in launch order.  The block's
 // first adaLN (attention modulation) is launched by the previous block's PART_NORM_NEXT
@@ -334,6 +377,9 @@ int enqueue_part(irodori_ctx* c, int l, int B, int S, const ModTable& mt, int pa
     T* u = static_cast<T*>(c->u) + tok0 * F;
     // fp8 compute: the e4m3 copies of h / o / u with their block scales (same row slice).
     const bool f8 = c->fp8 && std::is_same<T, bf16>::value;
+    // Fused adaLN (bf16): the partial sums of the slice's rows and this layer's shift biases.
+    const bool fz = std::is_same<T, bf16>::value && fused_for(c, mt, B);
+    float* rstat = fz ? c->rstat + tok0 * (D / 32) : nullptr;
     uint8_t* h8 = f8 ? c->h8 + tok0 * D : nullptr;
     uint8_t* h8s = f8 ? c->h8s + tok0 * (D / 32) : nullptr;
     uint8_t* o8 = f8 ? c->o8 + tok0 * D : nullptr;
@@ -382,6 +428,10 @@ int enqueue_part(irodori_ctx* c, int l, int B, int S, const ModTable& mt, int pa
             ga.rope_sin = c->rope_sin;
             ga.vt_stride = vt_stride;
             ga.q_scale = 1.4426950408889634f / sqrtf((float)g.head_dim);
+            if (fz) {
+                ga.rstat = rstat;
+                ga.rbias = c->biasq + (size_t)l * c->nvec_cap * 4 * D;
+            }
             if (gemm(EPI_QKVG, ga, h, h8, h8s, lb.w_qkvg, lb.ws_qkvg)) {
                 set_last_error("qkvg gemm shape");
                 return IRODORI_ERR_SHAPE;
@@ -439,6 +489,12 @@ int enqueue_part(irodori_ctx* c, int l, int B, int S, const ModTable& mt, int pa
             ga.N = D;
             ga.K = D;
             ga.kind = 0;
+            if (fz) {  // and the mlp adaLN operand of this layer
+                ga.Hn = h;
+                ga.rstat_out = rstat;
+                ga.next_layer = l;
+                ga.next_kind = 1;
+            }
             if (gemm(EPI_RESID, ga, o, o8, o8s, lb.w_o, lb.ws_o)) {
                 set_last_error("wo gemm shape");
                 return IRODORI_ERR_SHAPE;
@@ -446,8 +502,8 @@ int enqueue_part(irodori_ctx* c, int l, int B, int S, const ModTable& mt, int pa
             break;
         }
         case PART_NORM_MLP: {
-            // h2 = mlp adaLN(x) (diffusion.rs:101-102).
-            launch_norm_mod<T>(x, f8 ? nullptr : h, M, S, D, g.norm_eps, mt, l, 1, st, h8, h8s);
+            // h2 = mlp adaLN(x) (diffusion.rs:101-102); fused into W_o / W13 with the fused adaLN.
+            if (!fz) launch_norm_mod<T>(x, f8 ? nullptr : h, M, S, D, g.norm_eps, mt, l, 1, st, h8, h8s);
             break;
         }
         case PART_W13: {
@@ -457,6 +513,10 @@ int enqueue_part(irodori_ctx* c, int l, int B, int S, const ModTable& mt, int pa
             ga.U = u;
             ga.U8 = u8;  // fp8: m goes straight to the W2 operand form
             ga.U8s = u8s;
+            if (fz) {
+                ga.rstat = rstat;
+                ga.rbias = c->bias13 + (size_t)l * c->nvec_cap * 2 * F;
+            }
             if (gemm(EPI_SWIGLU, ga, h, h8, h8s, lb.w13, lb.ws_13)) {
                 set_last_error("w13 gemm shape");
                 return IRODORI_ERR_SHAPE;
@@ -468,6 +528,12 @@ int enqueue_part(irodori_ctx* c, int l, int B, int S, const ModTable& mt, int pa
             ga.N = D;
             ga.K = F;
             ga.kind = 1;
+            if (fz && !last) {  // and the next block's attention adaLN operand
+                ga.Hn = h;
+                ga.rstat_out = rstat;
+                ga.next_layer = l + 1;
+                ga.next_kind = 0;
+            }
             if (gemm(EPI_RESID, ga, u, u8, u8s, lb.w2, lb.ws_2)) {
                 set_last_error("w2 gemm shape");
                 return IRODORI_ERR_SHAPE;
@@ -475,8 +541,8 @@ int enqueue_part(irodori_ctx* c, int l, int B, int S, const ModTable& mt, int pa
             break;
         }
         case PART_NORM_NEXT: {
-            // Next block's attention adaLN.
-            if (!last) {
+            // Next block's attention adaLN (fused into W2 / QKVG with the fused adaLN).
+            if (!last && !fz) {
                 launch_norm_mod<T>(x, f8 ? nullptr : h, M, S, D, g.norm_eps, mt, l + 1, 0, st, h8, h8s);
             }
             break;
@@ -517,7 +583,8 @@ int enqueue_inproj(irodori_ctx* c, int B, int S, const float* src, int src_batch
         bf16* h = c->fp8 ? nullptr : static_cast<bf16*>(c->h) + tok0 * g.model_dim;
         launch_inproj_norm<bf16>(src, src_batches, c->in_w, c->in_b, x, h, B * S, S, g.latent_dim, g.model_dim,
                                  g.norm_eps, mt, st, c->fp8 ? c->h8 + tok0 * g.model_dim : nullptr,
-                                 c->fp8 ? c->h8s + tok0 * (g.model_dim / 32) : nullptr);
+                                 c->fp8 ? c->h8s + tok0 * (g.model_dim / 32) : nullptr,
+                                 fused_for(c, mt, B) ? c->rstat + tok0 * (g.model_dim / 32) : nullptr);
     }
     else
         launch_inproj_norm<float>(src, src_batches, c->in_w, c->in_b, x,
@@ -675,6 +742,59 @@ int validate_params(const irodori_sampler_params* p) {
     return IRODORI_OK;
 }
 
+// ---- SDPA operator helpers ----------------------------------------------------------------
+
+int check_sdpa_args(int dtype, const void* q, const void* k, const void* v, int B, int H, int Sq, int Skv, int Dh,
+                    const float* out) {
+    IRO_REQUIRE(q && k && v && out, IRODORI_ERR_INVALID_ARG, "null argument");
+    IRO_REQUIRE(B > 0 && H > 0 && Sq > 0 && Skv > 0, IRODORI_ERR_SHAPE, "SDPA dims must be positive");
+    IRO_REQUIRE(Dh == 64 || Dh == 128, IRODORI_ERR_SHAPE, "head_dim must be 64 or 128");
+    IRO_REQUIRE(dtype == IRODORI_DTYPE_F32 || dtype == IRODORI_DTYPE_BF16 || dtype == IRODORI_DTYPE_F16,
+                IRODORI_ERR_DTYPE, "dtype must be F32, BF16 or F16");
+    return IRODORI_OK;
+}
+
+// 16-bit operands with Dh = 64 run on the model's joint attention kernel after staging
+// (its tile list holds up to 4096 keys); everything else on the generic flash kernel.
+bool sdpa_staged(int dtype, int Dh, int Skv) {
+    return dtype != IRODORI_DTYPE_F32 && Dh == 64 && Skv <= 4096;
+}
+
+template <typename T>
+int sdpa_direct_t(const void* q, const void* k, const void* v, const float* mask, int B, int H, int Sq, int Skv, int Dh,
+                  float scale, float* out, hipStream_t st) {
+    AttnArgs<T> a{};
+    a.Q = static_cast<const T*>(q);
+    a.K0 = static_cast<const T*>(k);
+    a.V0 = static_cast<const T*>(v);
+    a.len0 = Skv; a.stride0 = Skv; a.mask0 = mask;
+    a.B = B; a.H = H; a.Sq = Sq; a.scale = scale; a.out_mode = 1; a.Of = out;
+    const int rc = Dh == 64 ? launch_attention<T, 64>(a, st) : launch_attention<T, 128>(a, st);
+    IRO_REQUIRE(rc == 0, IRODORI_ERR_SHAPE, "sdpa launch rejected the shape");
+    return check_launch("sdpa");
+}
+
+int sdpa_direct(int dtype, const void* q, const void* k, const void* v, const float* mask, int B, int H, int Sq,
+                int Skv, int Dh, float scale, float* out, hipStream_t st) {
+    if (dtype == IRODORI_DTYPE_BF16) return sdpa_direct_t<bf16>(q, k, v, mask, B, H, Sq, Skv, Dh, scale, out, st);
+    if (dtype == IRODORI_DTYPE_F16) return sdpa_direct_t<f16>(q, k, v, mask, B, H, Sq, Skv, Dh, scale, out, st);
+    return sdpa_direct_t<float>(q, k, v, mask, B, H, Sq, Skv, Dh, scale, out, st);
+}
+
+// The staged path on a caller-provided (or stream-ordered) buffer ws of `bytes`.
+int sdpa_run_staged(int dtype, const void* q, const void* k, const void* v, const float* mask, int B, int H, int Sq,
+                    int Skv, float scale, float* out, void* ws, size_t bytes, hipStream_t st) {
+    int rc;
+    if (dtype == IRODORI_DTYPE_BF16)
+        rc = launch_sdpa_staged<bf16>(static_cast<const bf16*>(q), static_cast<const bf16*>(k),
+                                      static_cast<const bf16*>(v), mask, B, H, Sq, Skv, scale, out, ws, bytes, st);
+    else
+        rc = launch_sdpa_staged<f16>(static_cast<const f16*>(q), static_cast<const f16*>(k),
+                                     static_cast<const f16*>(v), mask, B, H, Sq, Skv, scale, out, ws, bytes, st);
+    IRO_REQUIRE(rc == 0, IRODORI_ERR_SHAPE, "staged sdpa rejected the shape");
+    return check_launch("sdpa");
+}
+
 // Number of sampler roles (context bundles) for n active signals (role-major rows).
 int cfg_roles(const irodori_sampler_params* p, int n) {
     return p->cfg_mode == IRODORI_CFG_JOINT ? (n > 0 ? 2 : 1) : 1 + n;
@@ -748,6 +868,8 @@ int irodori_ctx_create(int device, const irodori_dit_config* cfg, irodori_ctx** 
     c->fp8 = g.compute_dtype == IRODORI_DTYPE_FP8;
     c->bf16 = g.compute_dtype == IRODORI_DTYPE_BF16 || c->fp8;
     c->esz = c->bf16 ? 2 : 4;
+    // The fused adaLN's GEMMs take the row partial sums as up to 8 float4 per row.
+    c->fused = c->bf16 && !c->fp8 && g.model_dim % 128 == 0 && g.model_dim <= 1024;
     IRO_HIP_CHECK(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
     IRO_HIP_CHECK(hipEventCreateWithFlags(&c->ev_fork, hipEventDisableTiming));
     for (int i = 0; i < irodori_ctx::kMaxRoles - 1; i++) {
@@ -808,6 +930,7 @@ int irodori_ctx_create(int device, const irodori_dit_config* cfg, irodori_ctx** 
     IRO_TRY(dev_alloc(c.get(), &c->gate, es * M * D));
     IRO_TRY(dev_alloc(c.get(), &c->o, es * M * D));
     IRO_TRY(dev_alloc(c.get(), &c->u, es * M * F));
+    if (c->fused) IRO_TRY(dalloc(c.get(), &c->rstat, sizeof(float) * M * (D / 32)));
     if (c->fp8) {
         IRO_TRY(dalloc(c.get(), &c->h8, M * D));
         IRO_TRY(dalloc(c.get(), &c->h8s, M * D / 32));
@@ -1284,11 +1407,13 @@ int irodori_block_forward(irodori_ctx* c, int layer, int B, int S, float* x, con
     int D = g.model_dim, L = g.num_layers;
     IRO_TRY(ensure_nvec(c, B));
     IRO_TRY(upload(c, c->cond, cond, sizeof(float) * (size_t)B * 3 * D));
-    IRO_TRY(enqueue_mod_table(c, B, true));
+    IRO_TRY(enqueue_mod_table(c, B, true, layer, layer + 1));
     ModTable mt{c->tab, c->zero_step, 0, 1, L};
     size_t n = (size_t)B * S * D;
     IRO_TRY(upload(c, c->x, x, sizeof(float) * n));
-    if (c->bf16) {
+    if (fused_for(c, mt, B)) {
+        launch_mod_stats<bf16>(c->x, static_cast<bf16*>(c->h), B * S, S, D, mt, layer, 0, c->rstat, c->stream);
+    } else if (c->bf16) {
         launch_norm_mod<bf16>(c->x, c->fp8 ? nullptr : static_cast<bf16*>(c->h), B * S, S, D, g.norm_eps, mt, layer,
                               0, c->stream, c->fp8 ? c->h8 : nullptr, c->fp8 ? c->h8s : nullptr);
     } else
@@ -1566,21 +1691,23 @@ int irodori_profile_layer(irodori_ctx* c, int B, int S, int iters, irodori_kerne
     IRO_GUARD_BEGIN
     IRO_REQUIRE(c && out, IRODORI_ERR_INVALID_ARG, "null argument");
     const auto& g = c->cfg;
-    IRO_REQUIRE(B > 0 && B <= g.max_rows && B % 2 == 0 && S > 0 && S <= g.max_seq, IRODORI_ERR_SHAPE,
-                "batch must be even and <= max_rows, seq <= max_seq");
+    IRO_REQUIRE(B > 0 && B <= g.max_rows && S > 0 && S <= g.max_seq, IRODORI_ERR_SHAPE,
+                "batch must be in [1, max_rows], seq in [1, max_seq]");
     IRO_REQUIRE(iters > 0, IRODORI_ERR_INVALID_ARG, "iters must be > 0");
+    IRO_REQUIRE(c->bf16 && !c->fp8, IRODORI_ERR_DTYPE, "irodori_profile_layer times the bf16 path");
     IRO_TRY(check_ready(c, B));
     IRO_HIP_CHECK(hipSetDevice(c->device));
     int L = g.num_layers;
-    // Modulation vectors for t = 0.5 on every row; state from one in_proj of zeros + 1.
-    std::vector<float> t(B, 0.5f), x0((size_t)B * S * g.latent_dim, 1.0f);
-    IRO_TRY(ensure_nvec(c, B));
-    IRO_TRY(upload(c, c->tvec, t.data(), sizeof(float) * B));
+    // One modulation vector (t = 0.5) shared by every row, as in a sampler evaluation; the
+    // state from one in_proj of ones and one pass over the blocks.
+    std::vector<float> t(1, 0.5f), x0((size_t)B * S * g.latent_dim, 1.0f);
+    IRO_TRY(ensure_nvec(c, 1));
+    IRO_TRY(upload(c, c->tvec, t.data(), sizeof(float)));
     IRO_TRY(upload(c, c->xt, x0.data(), sizeof(float) * x0.size()));
-    IRO_TRY(enqueue_mod_table(c, B, false));
-    ModTable mt{c->tab, c->zero_step, 0, 1, L};
+    IRO_TRY(enqueue_mod_table(c, 1, false));
+    ModTable mt{c->tab, c->zero_step, 0, B, L};
     IRO_TRY(enqueue_inproj(c, B, S, c->xt, B, 0, mt, c->stream));
-    IRO_TRY(enqueue_layer_any(c, 0, B, S, mt));  // fills q/k/v/gate/o/u
+    for (int l = 0; l < L; l++) IRO_TRY(enqueue_layer_any(c, l, B, S, mt));  // fills every operand
     IRO_HIP_CHECK(hipStreamSynchronize(c->stream));
 
     hipEvent_t e0, e1;
@@ -1588,24 +1715,23 @@ int irodori_profile_layer(irodori_ctx* c, int B, int S, int iters, irodori_kerne
     IRO_HIP_CHECK(hipEventCreate(&e1));
     float* outs[7] = {&out->norm_mod_us, &out->qkvg_gemm_us, &out->attention_us, &out->wo_gemm_us,
                       &out->w13_gemm_us, &out->w2_gemm_us, &out->final_us};
+    static const int part_of[6] = {-1, PART_QKVG, PART_ATTN, PART_WO, PART_W13, PART_W2};
     int rc = IRODORI_OK;
     for (int kidx = 0; kidx < 7 && rc == IRODORI_OK; kidx++) {
         (void)hipEventRecord(e0, c->stream);
-        for (int it = 0; it < iters; it++) {
+        for (int it = 0; it < iters && rc == IRODORI_OK; it++) {
+            // Launch `it` uses layer it % L: the weights (and context K / V) cycle through all
+            // layers, as the blocks of an RF step read them.
+            const int l = it % L;
             if (kidx == 6) {
                 rc = enqueue_head(c, B, S, 0, c->stream);
-                if (rc != IRODORI_OK) break;
-                continue;
+            } else if (kidx == 0) {
+                // The unfused adaLN kernel (forwards whose rows carry different t, f32, fp8).
+                launch_norm_mod<bf16>(c->x, static_cast<bf16*>(c->h), B * S, S, g.model_dim, g.norm_eps, mt, l, 1,
+                                      c->stream);
+            } else {
+                rc = enqueue_part<bf16>(c, l, B, S, mt, part_of[kidx], 0, c->stream);
             }
-            if (!c->bf16) {
-                rc = IRODORI_ERR_DTYPE;
-                set_last_error("irodori_profile_layer times the bf16 path");
-                break;
-            }
-            // The kernels exactly as a block launches them.
-            static const int part_of[6] = {PART_NORM_MLP, PART_QKVG, PART_ATTN, PART_WO, PART_W13, PART_W2};
-            rc = enqueue_part_any(c, 0, B, S, mt, part_of[kidx]);
-            if (rc != IRODORI_OK) break;
         }
         (void)hipEventRecord(e1, c->stream);
         hipError_t se = hipEventSynchronize(e1);
@@ -1620,6 +1746,8 @@ int irodori_profile_layer(irodori_ctx* c, int B, int S, int iters, irodori_kerne
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
     if (rc != IRODORI_OK) return rc;
+    // The operands the timed launches overwrote are restored by the next forward (in_proj
+    // rewrites the state); nothing else depends on them.
     return check_launch("profile");
     IRO_GUARD_END
 }
@@ -1680,31 +1808,18 @@ int irodori_op_fused_adaln(const float* x, const float* scale, const float* shif
 int irodori_op_sdpa(int dtype, const void* q, const void* k, const void* v, const float* mask, int B, int H, int Sq,
                     int Skv, int Dh, float scale, float* out, void* stream) {
     IRO_GUARD_BEGIN
-    IRO_REQUIRE(q && k && v && out, IRODORI_ERR_INVALID_ARG, "null argument");
-    IRO_REQUIRE(B > 0 && H > 0 && Sq > 0 && Skv > 0, IRODORI_ERR_SHAPE, "SDPA dims must be positive");
-    IRO_REQUIRE(Dh == 64 || Dh == 128, IRODORI_ERR_SHAPE, "head_dim must be 64 or 128");
-    IRO_REQUIRE(dtype == IRODORI_DTYPE_F32 || dtype == IRODORI_DTYPE_BF16, IRODORI_ERR_DTYPE, "dtype must be F32 or BF16");
+    IRO_TRY(check_sdpa_args(dtype, q, k, v, B, H, Sq, Skv, Dh, out));
     hipStream_t st = static_cast<hipStream_t>(stream);
-    int rc;
-    if (dtype == IRODORI_DTYPE_BF16) {
-        AttnArgs<bf16> a{};
-        a.Q = static_cast<const bf16*>(q);
-        a.K0 = static_cast<const bf16*>(k);
-        a.V0 = static_cast<const bf16*>(v);
-        a.len0 = Skv; a.stride0 = Skv; a.mask0 = mask;
-        a.B = B; a.H = H; a.Sq = Sq; a.scale = scale; a.out_mode = 1; a.Of = out;
-        rc = Dh == 64 ? launch_attention<bf16, 64>(a, st) : launch_attention<bf16, 128>(a, st);
-    } else {
-        AttnArgs<float> a{};
-        a.Q = static_cast<const float*>(q);
-        a.K0 = static_cast<const float*>(k);
-        a.V0 = static_cast<const float*>(v);
-        a.len0 = Skv; a.stride0 = Skv; a.mask0 = mask;
-        a.B = B; a.H = H; a.Sq = Sq; a.scale = scale; a.out_mode = 1; a.Of = out;
-        rc = Dh == 64 ? launch_attention<float, 64>(a, st) : launch_attention<float, 128>(a, st);
-    }
-    IRO_REQUIRE(rc == 0, IRODORI_ERR_SHAPE, "sdpa launch rejected the shape");
-    return check_launch("sdpa");
+    if (!sdpa_staged(dtype, Dh, Skv)) return sdpa_direct(dtype, q, k, v, mask, B, H, Sq, Skv, Dh, scale, out, st);
+    // Staging buffer in stream order: overlapping calls on different streams never share it.
+    const size_t bytes = sdpa_stage_bytes(B, H, Sq, Skv);
+    void* ws = nullptr;
+    IRO_HIP_CHECK(hipMallocAsync(&ws, bytes, st));
+    const int rc = sdpa_run_staged(dtype, q, k, v, mask, B, H, Sq, Skv, scale, out, ws, bytes, st);
+    const hipError_t fe = hipFreeAsync(ws, st);
+    if (rc != IRODORI_OK) return rc;
+    IRO_HIP_CHECK(fe);
+    return IRODORI_OK;
     IRO_GUARD_END
 }
 

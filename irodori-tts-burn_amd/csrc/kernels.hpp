@@ -45,11 +45,20 @@ void launch_norm_mod(const float* x, T* h, int M, int S, int D, float eps, ModTa
 // x[b] = x_src[b mod src_batches] @ in_w + in_b (in_proj), then h = norm_mod(x) for
 // (layer 0, attn); b is the batch row.  h is nullable; q8 / q8s (nullable) receive the fp8
 // GEMM-operand form of h (e4m3 codes, E8M0 scales per 32 values; D % 32 == 0).
+// rstat (nullable; the fused adaLN of the bf16 model path, see GemmArgs): h gets
+// x (1 + scale) and rstat [M, D/32] the row sums of x^2 per 32 columns instead.
 template <typename T>
 void launch_inproj_norm(const float* x_src, int src_batches, const float* in_w,
                         const float* in_b, float* x, T* h, int M, int S, int P, int D,
                         float eps, ModTable mt, hipStream_t st, uint8_t* q8 = nullptr,
-                        uint8_t* q8s = nullptr);
+                        uint8_t* q8s = nullptr, float* rstat = nullptr);
+// The fused adaLN operand of (layer, kind) from x: h = x (1 + scale), rstat [M, D/32].
+template <typename T>
+void launch_mod_stats(const float* x, T* h, int M, int S, int D, ModTable mt, int layer, int kind, float* rstat,
+                      hipStream_t st);
+// Shift rows of the modulation table as GEMM operands: stage[(l * 2 + k) * cap + v][D] =
+// shift of (vector v, layer l, kind k) in bf16, for v < nvec.
+void launch_shift_stage(const float* tab, int nvec, int cap, int L, int D, bf16* stage, hipStream_t st);
 
 
 // One model evaluation of the RF sampler, as the update kernel applies it
@@ -239,6 +248,20 @@ struct GemmArgs {
     // multiple of half a 128-byte slice; K spans the taps rounded up to whole slices (the
     // weights are zero there).
     int conv_cp, conv_dil, conv_rows;
+    // Fused adaLN of the model path (bf16 operands, norm.rs:160-169): with r =
+    // rsqrt(mean(x^2) + eps), h = x r (1 + scale) + shift, so h W = r (x (1 + scale)) W + shift W.
+    //   consumer (EPI_QKVG / EPI_SWIGLU with rstat set): A holds x (1 + scale) and rstat
+    //   [M, K/32] the sums of x^2 per 32 columns; each accumulator row is multiplied by r
+    //   and rbias[vec, n] (= shift W of the launch's one modulation vector, [nvec, N]) is
+    //   added before the epilogue.  Every row must map to the same vector (a sampler
+    //   evaluation, where all rows share the step's t).
+    //   producer (EPI_RESID with Hn set): after x += gate * acc, writes Hn [M, N] =
+    //   x (1 + scale of (next_layer, next_kind)) and rstat_out [M, N/32].
+    const float* rstat;
+    const float* rbias;
+    T* Hn;
+    float* rstat_out;
+    int next_layer, next_kind;
 };
 template <typename T>
 int launch_gemm(int epi, const GemmArgs<T>& a, hipStream_t st);
@@ -331,7 +354,16 @@ struct AttnArgs {
 };
 template <typename T, int DH>
 int launch_attention(const AttnArgs<T>& a, hipStream_t st);
-// bf16, Dh = 64, V^T in vt_pos_bf16 order, Q pre-scaled (kernels_attn32.hip).
+// bf16 / f16, Dh = 64, V^T in vt_pos_bf16 order, Q pre-scaled (kernels_attn32.hip).
 int launch_attention32(const AttnArgs<bf16>& a, hipStream_t st);
+int launch_attention32(const AttnArgs<f16>& a, hipStream_t st);
+// The SDPA operator on 16-bit operands with Dh = 64 through attn32_kernel: q, k, v
+// [B, H, S, 64] as given, mask [B, Skv] f32 (>= 0.5 attends; nullable), out [B, H, Sq, 64]
+// f32.  Q (pre-scaled), V^T and the key bits are staged in ws (256-byte aligned, at least
+// sdpa_stage_bytes); Skv <= 4096.  Returns -1 on a shape the kernel does not take.
+size_t sdpa_stage_bytes(int B, int H, int Sq, int Skv);
+template <typename T>
+int launch_sdpa_staged(const T* q, const T* k, const T* v, const float* mask, int B, int H, int Sq, int Skv,
+                       float scale, float* out, void* ws, size_t ws_bytes, hipStream_t st);
 
 }  // namespace irodori

@@ -35,6 +35,12 @@ __device__ __forceinline__ Frag<bf16> lds_frag8<bf16>(const bf16* p) {
     return f;
 }
 template <>
+__device__ __forceinline__ Frag<f16> lds_frag8<f16>(const f16* p) {
+    Frag<f16> f;
+    f.v = *reinterpret_cast<const f16x8*>(p);
+    return f;
+}
+template <>
 __device__ __forceinline__ Frag<float> lds_frag8<float>(const float* p) {
     Frag<float> f;
     float4 lo = *reinterpret_cast<const float4*>(p);
@@ -51,6 +57,12 @@ __device__ __forceinline__ bf16 vec_elem<bf16>(const u32x4& v, int e) {
     unsigned w = v[e >> 1];
     unsigned short u = (e & 1) ? (unsigned short)(w >> 16) : (unsigned short)(w & 0xffff);
     return __builtin_bit_cast(bf16, u);
+}
+template <>
+__device__ __forceinline__ f16 vec_elem<f16>(const u32x4& v, int e) {
+    unsigned w = v[e >> 1];
+    unsigned short u = (e & 1) ? (unsigned short)(w >> 16) : (unsigned short)(w & 0xffff);
+    return __builtin_bit_cast(f16, u);
 }
 template <>
 __device__ __forceinline__ float vec_elem<float>(const u32x4& v, int e) {
@@ -329,6 +341,8 @@ int launch_attention(const AttnArgs<T>& a, hipStream_t st) {
 
 template int launch_attention<bf16, 64>(const AttnArgs<bf16>&, hipStream_t);
 template int launch_attention<bf16, 128>(const AttnArgs<bf16>&, hipStream_t);
+template int launch_attention<f16, 64>(const AttnArgs<f16>&, hipStream_t);
+template int launch_attention<f16, 128>(const AttnArgs<f16>&, hipStream_t);
 template int launch_attention<float, 64>(const AttnArgs<float>&, hipStream_t);
 template int launch_attention<float, 128>(const AttnArgs<float>&, hipStream_t);
 

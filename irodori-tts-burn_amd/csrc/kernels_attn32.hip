@@ -26,6 +26,8 @@
 // into unpadded 128-byte rows whose 16-byte chunks are xor-swizzled by (row >> 1) & 7.
 // K streams one tile ahead of V so that the score MFMAs of the next tile overlap the
 // softmax of the current one.
+#include <type_traits>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -35,6 +37,24 @@ namespace {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+// 8-element operand vector of the 32x32x16 matrix-core step for each element type.
+template <typename T>
+struct Vec8;
+template <>
+struct Vec8<bf16> {
+    typedef bf16x8 type;
+};
+template <>
+struct Vec8<f16> {
+    typedef f16x8 type;
+};
+__device__ __forceinline__ f32x16 mma32x16(bf16x8 a, bf16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mma32x16(f16x8 a, f16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
 
 constexpr int KT = 64;
 constexpr int TILE_BYTES = KT * 128;  // 64 rows x 128 bytes (bf16 Dh = 64)
@@ -49,11 +69,14 @@ __device__ __forceinline__ void buf_load_lds16(__amdgpu_buffer_rsrc_t r, unsigne
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 0);
 }
 __device__ __forceinline__ int swz(int r, int c) { return c ^ ((r >> 1) & 7); }
-__device__ __forceinline__ bf16x8 frag(const unsigned char* tile, int r, int chunk) {
-    return *reinterpret_cast<const bf16x8*>(tile + r * 128 + (swz(r, chunk) << 4));
+template <typename T>
+__device__ __forceinline__ typename Vec8<T>::type frag(const unsigned char* tile, int r, int chunk) {
+    return *reinterpret_cast<const typename Vec8<T>::type*>(tile + r * 128 + (swz(r, chunk) << 4));
 }
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-__device__ __forceinline__ float bf16_round(float x) { return static_cast<float>(static_cast<bf16>(x)); }
+// x rounded to the operand type (the softmax reference must be exactly representable).
+template <typename T>
+__device__ __forceinline__ float round_to(float x) { return static_cast<float>(static_cast<T>(x)); }
 
 // Tile list of one (row, head): entry i < nact of the list is held by lane i as the tile
 // index and its 64-bit key-validity mask.  Latent tiles are valid up to len0 (or carry the
@@ -64,7 +87,8 @@ struct TileList {
     int nact;       // wave-uniform
 };
 
-__device__ __forceinline__ TileList build_tile_list(const AttnArgs<bf16>& a, int b, int lane, int nt0, int nt1) {
+template <typename T>
+__device__ __forceinline__ TileList build_tile_list(const AttnArgs<T>& a, int b, int lane, int nt0, int nt1) {
     unsigned long long bits = 0ull;
     if (lane < nt0) {
         const int rem = a.len0 & (KT - 1);
@@ -86,17 +110,19 @@ __device__ __forceinline__ TileList build_tile_list(const AttnArgs<bf16>& a, int
 }
 
 // S'^T of one 64-key tile (two 32-key blocks): the reference step, then 4 k16 steps.
+template <typename T>
 __device__ __forceinline__ void score_tile(f32x16 (&s)[2], const unsigned char* kt, int fr, int fh,
-                                           const bf16x8 (&qf)[4], bf16x8 ones, bf16x8 qbias) {
+                                           const typename Vec8<T>::type (&qf)[4], typename Vec8<T>::type ones,
+                                           typename Vec8<T>::type qbias) {
 #pragma unroll
     for (int kb = 0; kb < 2; kb++) {
         f32x16 z;
 #pragma unroll
         for (int e = 0; e < 16; e++) z[e] = 0.f;
-        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ones, qbias, z, 0, 0, 0);
+        s[kb] = mma32x16(ones, qbias, z);
 #pragma unroll
         for (int ks = 0; ks < 4; ks++)
-            s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag(kt, 32 * kb + fr, 2 * ks + fh), qf[ks], s[kb], 0, 0, 0);
+            s[kb] = mma32x16(frag<T>(kt, 32 * kb + fr, 2 * ks + fh), qf[ks], s[kb]);
     }
 }
 
@@ -110,8 +136,9 @@ __device__ __forceinline__ void score_tile(f32x16 (&s)[2], const unsigned char* 
 // the K tiles of iteration j + 1 and the V tiles of iteration j have landed, and the
 // loads of K_{j+2} / V_{j+1} are issued into the slots freed by iteration j - 1.  LDS:
 // K ring [2][KVS] tiles + V ring [2][KVS] tiles.
-template <int QB, int KVS>
-__global__ __launch_bounds__(64 * QB * KVS) void attn32_kernel(AttnArgs<bf16> a, int nqb) {
+template <typename T, int QB, int KVS>
+__global__ __launch_bounds__(64 * QB * KVS) void attn32_kernel(AttnArgs<T> a, int nqb) {
+    typedef typename Vec8<T>::type V8;
     constexpr int NW = QB * KVS;
     constexpr int LPK = KVS * 8 / NW;  // load instructions per wave per K (or V) stage
     static_assert(LPK * NW == KVS * 8, "tiles must split over the waves");
@@ -136,10 +163,10 @@ __global__ __launch_bounds__(64 * QB * KVS) void attn32_kernel(AttnArgs<bf16> a,
     const int nact = tl.nact;
     const int niter = (nact + KVS - 1) / KVS;
 
-    const bf16* K0b = a.K0 + bh * a.stride0 * 64;
-    const bf16* K1b = a.K1 ? a.K1 + bh * a.stride1 * 64 : nullptr;
-    const bf16* V0b = a.V0 + bh * 64 * (size_t)a.vstride0;
-    const bf16* V1b = a.V1 ? a.V1 + bh * 64 * (size_t)a.vstride1 : nullptr;
+    const T* K0b = a.K0 + bh * a.stride0 * 64;
+    const T* K1b = a.K1 ? a.K1 + bh * a.stride1 * 64 : nullptr;
+    const T* V0b = a.V0 + bh * 64 * (size_t)a.vstride0;
+    const T* V1b = a.V1 ? a.V1 + bh * 64 * (size_t)a.vstride1 : nullptr;
 
     // Load instruction ii of this wave within a K (or V) stage: gi = wave*LPK + ii ->
     // parity tile gi / 8, rows 8 (gi % 8) .. +7; lane -> row + lane / 8, physical chunk
@@ -180,22 +207,22 @@ __global__ __launch_bounds__(64 * QB * KVS) void attn32_kernel(AttnArgs<bf16> a,
     } while (0)
 
     // Q^T fragments (B operand): query q0 + fr, dims 16 ks + 8 fh .. +8.
-    bf16x8 qf[4];
+    V8 qf[4];
     {
         int q = q0 + fr;
         q = q < a.Sq ? q : a.Sq - 1;
-        const bf16* qp = a.Q + (bh * a.Sq + q) * 64 + 8 * fh;
+        const T* qp = a.Q + (bh * a.Sq + q) * 64 + 8 * fh;
 #pragma unroll
-        for (int ks = 0; ks < 4; ks++) qf[ks] = *reinterpret_cast<const bf16x8*>(qp + 16 * ks);
+        for (int ks = 0; ks < 4; ks++) qf[ks] = *reinterpret_cast<const V8*>(qp + 16 * ks);
     }
     // Reference subtraction fragments: A = 1 at k = 0 for every key row, B = -m at k = 0.
-    bf16x8 ones, qbias;
+    V8 ones, qbias;
 #pragma unroll
     for (int e = 0; e < 8; e++) {
-        ones[e] = static_cast<bf16>(0.f);
-        qbias[e] = static_cast<bf16>(0.f);
+        ones[e] = static_cast<T>(0.f);
+        qbias[e] = static_cast<T>(0.f);
     }
-    if (fh == 0) ones[0] = static_cast<bf16>(1.f);
+    if (fh == 0) ones[0] = static_cast<T>(1.f);
 
     f32x16 o[2];
 #pragma unroll
@@ -205,18 +232,22 @@ __global__ __launch_bounds__(64 * QB * KVS) void attn32_kernel(AttnArgs<bf16> a,
     float m_ref = 0.f, l_run = 0.f;
     bool first = true;  // wave-uniform: no tile processed yet
 
-    // Prologue: K_0, V_0, then K_1 in flight; scores of tile 0.
-    ATT_ISSUE(0, 0, 0);
-    ATT_ISSUE(1, 0, 0);
-    if (niter > 1) {
-        ATT_ISSUE(0, 1, 1);
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LPK) : "memory");
-    } else {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    }
-    raw_barrier();
+    // Prologue: K_0, V_0, then K_1 in flight; scores of tile 0.  A (row, head) with no
+    // valid key at all (nact = 0, the same for every wave of the workgroup) issues no load
+    // (the clamped tile index would be -1) and runs no iteration: its queries store 0.
     f32x16 s[2];
-    if (par < nact) score_tile(s, kring + par * TILE_BYTES, fr, fh, qf, ones, qbias);
+    if (nact > 0) {
+        ATT_ISSUE(0, 0, 0);
+        ATT_ISSUE(1, 0, 0);
+        if (niter > 1) {
+            ATT_ISSUE(0, 1, 1);
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LPK) : "memory");
+        } else {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+        raw_barrier();
+        if (par < nact) score_tile<T>(s, kring + par * TILE_BYTES, fr, fh, qf, ones, qbias);
+    }
 
     for (int j = 0; j < niter; j++) {
         // K_{j+1} and V_j have landed once this wave's loads are done and all waves met.
@@ -250,7 +281,7 @@ __global__ __launch_bounds__(64 * QB * KVS) void attn32_kernel(AttnArgs<bf16> a,
         // Move the reference on the first tile or when a score exceeds it by 2^TAU.
         const bool need = first || mx > TAU;
         if (__ballot(need)) {
-            const float nref = need ? bf16_round(m_ref + mx) : m_ref;
+            const float nref = need ? round_to<T>(m_ref + mx) : m_ref;
             const float delta = nref - m_ref;
             const float corr = first ? 0.f : fast_exp2(-delta);
             m_ref = nref;
@@ -261,7 +292,7 @@ __global__ __launch_bounds__(64 * QB * KVS) void attn32_kernel(AttnArgs<bf16> a,
 #pragma unroll
             for (int db = 0; db < 2; db++) o[db] *= corr;
             l_run *= corr;
-            if (fh == 0) qbias[0] = static_cast<bf16>(-m_ref);
+            if (fh == 0) qbias[0] = static_cast<T>(-m_ref);
         }
         first = false;
 
@@ -269,16 +300,16 @@ __global__ __launch_bounds__(64 * QB * KVS) void attn32_kernel(AttnArgs<bf16> a,
         // (Computed unconditionally to keep one scheduling region; without a next tile the
         // slot holds stale data and the result is dropped.)
         f32x16 sn[2];
-        score_tile(sn, kring + (((j + 1) & 1) * KVS + par) * TILE_BYTES, fr, fh, qf, ones, qbias);
+        score_tile<T>(sn, kring + (((j + 1) & 1) * KVS + par) * TILE_BYTES, fr, fh, qf, ones, qbias);
         float psum = 0.f;
-        bf16x8 pf[4];
+        V8 pf[4];
 #pragma unroll
         for (int kb = 0; kb < 2; kb++)
 #pragma unroll
             for (int e = 0; e < 16; e++) {
                 const float p = fast_exp2(s[kb][e]);
                 psum += p;
-                pf[2 * kb + (e >> 3)][e & 7] = static_cast<bf16>(p);
+                pf[2 * kb + (e >> 3)][e & 7] = static_cast<T>(p);
             }
         l_run += psum;
         // 8 K-fragment reads, then each score MFMA followed by a slice of the softmax.
@@ -294,7 +325,7 @@ __global__ __launch_bounds__(64 * QB * KVS) void attn32_kernel(AttnArgs<bf16> a,
         for (int db = 0; db < 2; db++)
 #pragma unroll
             for (int g = 0; g < 4; g++)
-                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag(vt, 32 * db + fr, 2 * g + fh), pf[g], o[db], 0, 0, 0);
+                o[db] = mma32x16(frag<T>(vt, 32 * db + fr, 2 * g + fh), pf[g], o[db]);
         s[0] = sn[0];
         s[1] = sn[1];
     }
@@ -339,7 +370,7 @@ __global__ __launch_bounds__(64 * QB * KVS) void attn32_kernel(AttnArgs<bf16> a,
     const int q = q0 + fr;
     if (q >= a.Sq) return;
     const size_t m = (size_t)b * a.Sq + q;
-    if (a.out_mode == 2) {
+    if constexpr (std::is_same<T, bf16>::value) if (a.out_mode == 2) {
         // fp8 operand form: head dims 32 db .. 32 db + 31 of query q are one scale block,
         // split between this lane and lane ^ 32.
         const size_t ob = m * (a.H * 64) + hh * 64;
@@ -373,11 +404,12 @@ __global__ __launch_bounds__(64 * QB * KVS) void attn32_kernel(AttnArgs<bf16> a,
         for (int g4 = 0; g4 < 4; g4++) {
             const int dim = 32 * db + 8 * g4 + 4 * fh;
             if (a.out_mode == 0) {
-                const bf16x4 gv = *reinterpret_cast<const bf16x4*>(a.G + m * (a.H * 64) + hh * 64 + dim);
-                bf16x4 ov;
+                typedef T T4 __attribute__((ext_vector_type(4)));
+                const T4 gv = *reinterpret_cast<const T4*>(a.G + m * (a.H * 64) + hh * 64 + dim);
+                T4 ov;
 #pragma unroll
-                for (int c = 0; c < 4; c++) ov[c] = static_cast<bf16>(o[db][4 * g4 + c] * inv * static_cast<float>(gv[c]));
-                *reinterpret_cast<bf16x4*>(a.O + m * (a.H * 64) + hh * 64 + dim) = ov;
+                for (int c = 0; c < 4; c++) ov[c] = static_cast<T>(o[db][4 * g4 + c] * inv * static_cast<float>(gv[c]));
+                *reinterpret_cast<T4*>(a.O + m * (a.H * 64) + hh * 64 + dim) = ov;
             } else {
                 float* op = a.Of + ((bh * a.Sq) + q) * 64 + dim;
                 *reinterpret_cast<float4*>(op) = make_float4(o[db][4 * g4] * inv, o[db][4 * g4 + 1] * inv,
@@ -386,27 +418,23 @@ __global__ __launch_bounds__(64 * QB * KVS) void attn32_kernel(AttnArgs<bf16> a,
         }
 }
 
-template <int QB, int KVS>
-int launch_attn32_cfg(const AttnArgs<bf16>& a, hipStream_t st) {
+template <typename T, int QB, int KVS>
+int launch_attn32_cfg(const AttnArgs<T>& a, hipStream_t st) {
     const size_t lds = (size_t)4 * KVS * TILE_BYTES;
-    static bool attr_set = false;
-    if (!attr_set) {
-        if (hipFuncSetAttribute((const void*)attn32_kernel<QB, KVS>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)lds) != hipSuccess)
-            return -2;
-        attr_set = true;
-    }
+    static std::once_flag once;
+    static hipError_t attr_rc = hipSuccess;
+    if (set_lds_limit_once(once, attr_rc, (const void*)attn32_kernel<T, QB, KVS>, (int)lds) != hipSuccess) return -2;
     const int nqb = (a.Sq + 32 * QB - 1) / (32 * QB);
-    attn32_kernel<QB, KVS><<<dim3(nqb * a.H * a.B), 64 * QB * KVS, lds, st>>>(a, nqb);
+    attn32_kernel<T, QB, KVS><<<dim3(nqb * a.H * a.B), 64 * QB * KVS, lds, st>>>(a, nqb);
     return 0;
 }
 
-}  // namespace
-
-int launch_attention32(const AttnArgs<bf16>& a, hipStream_t st) {
+template <typename T>
+int launch_attention32_t(const AttnArgs<T>& a, hipStream_t st) {
     if (a.Sq <= 0 || a.len0 <= 0 || !a.v_transposed || !a.prescaled || (a.mask0 && !a.bits0)) return -1;
     if (a.K1 && !a.bits1) return -1;
     if ((a.vstride0 % KT) || (a.K1 && (a.vstride1 % KT))) return -1;
+    if (!std::is_same<T, bf16>::value && a.out_mode == 2) return -1;
     const int ntiles = (a.len0 + KT - 1) / KT + (a.K1 ? (a.len1 + KT - 1) / KT : 0);
     if (ntiles > 64) return -1;  // the tile list holds one entry per lane (4096 keys)
     // Latency vs throughput: when 2 query blocks x 2 key parities (4 waves, 64 KB LDS)
@@ -414,8 +442,96 @@ int launch_attention32(const AttnArgs<bf16>& a, hipStream_t st) {
     // of 750 frames: 18.2 vs 21.1 us with context keys, 12.3 vs 14.5 us without); larger
     // launches keep 4 x 2.
     const long wg22 = (long)((a.Sq + 63) / 64) * a.H * a.B;
-    if (wg22 <= 256) return launch_attn32_cfg<2, 2>(a, st);
-    return launch_attn32_cfg<4, 2>(a, st);
+    if (wg22 <= 256) return launch_attn32_cfg<T, 2, 2>(a, st);
+    return launch_attn32_cfg<T, 4, 2>(a, st);
 }
+
+// Operator staging (irodori_op_sdpa, Dh = 64 on 16-bit operands): the caller's Q, V and
+// float key mask in the layouts attn32_kernel reads.  One block per (row, head) and
+// 64-key tile: Q rows pre-scaled by scale * log2(e) (rounded once more to T), the tile's
+// V rows transposed through LDS into V^T rows in vt_pos_bf16 key order (keys past seq_kv
+// zero), and the tile's 64-bit key-validity word (key < seq_kv and mask >= 0.5; the
+// mask is per batch row, so only head 0 writes it).
+template <typename T>
+__global__ __launch_bounds__(256) void sdpa_stage_kernel(const T* __restrict__ q, const T* __restrict__ v,
+                                                         const float* __restrict__ mask, int H, int Sq, int Skv,
+                                                         int vstride, float qmul, T* __restrict__ qs,
+                                                         T* __restrict__ vt, unsigned long long* __restrict__ bits) {
+    __shared__ T tile[64][64 + 2];
+    const int t = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;
+    const int ntq = (Sq + 63) / 64, ntk = vstride / 64;
+    const int tid = threadIdx.x;
+    if (t < ntq) {  // 64 query rows of 64 dims
+        const size_t base = ((size_t)bh * Sq + (size_t)t * 64) * 64;
+        const int rows = Sq - t * 64 < 64 ? Sq - t * 64 : 64;
+        for (int i = tid; i < rows * 64; i += 256) qs[base + i] = static_cast<T>(static_cast<float>(q[base + i]) * qmul);
+    }
+    if (t >= ntk) return;
+    const int k0 = t * 64;
+    for (int i = tid; i < 64 * 64; i += 256) {
+        const int kk = i / 64, d = i % 64, key = k0 + kk;
+        tile[kk][d] = key < Skv ? v[((size_t)bh * Skv + key) * 64 + d] : static_cast<T>(0.f);
+    }
+    __syncthreads();
+    for (int i = tid; i < 64 * 64; i += 256) {
+        const int d = i / 64, kk = i % 64;
+        vt[((size_t)bh * 64 + d) * vstride + vt_pos_bf16(k0 + kk)] = tile[kk][d];
+    }
+    if (h == 0 && tid < 64) {
+        const int key = k0 + tid;
+        const bool ok = key < Skv && (mask == nullptr || mask[(size_t)b * Skv + key] >= 0.5f);
+        const unsigned long long w = __ballot(ok);
+        if (tid == 0) bits[(size_t)b * ntk + t] = w;
+    }
+}
+
+}  // namespace
+
+int launch_attention32(const AttnArgs<bf16>& a, hipStream_t st) { return launch_attention32_t<bf16>(a, st); }
+int launch_attention32(const AttnArgs<f16>& a, hipStream_t st) { return launch_attention32_t<f16>(a, st); }
+
+size_t sdpa_stage_bytes(int B, int H, int Sq, int Skv) {
+    const size_t vs = (size_t)(Skv + 63) / 64 * 64;
+    auto al = [](size_t n) { return (n + 255) / 256 * 256; };
+    return al((size_t)B * H * Sq * 64 * 2) + al((size_t)B * H * 64 * vs * 2) + al((size_t)B * (vs / 64) * 8);
+}
+
+template <typename T>
+int launch_sdpa_staged(const T* q, const T* k, const T* v, const float* mask, int B, int H, int Sq, int Skv,
+                       float scale, float* out, void* ws, size_t ws_bytes, hipStream_t st) {
+    const int vs = (Skv + 63) / 64 * 64;
+    if (B <= 0 || H <= 0 || Sq <= 0 || Skv <= 0 || vs / 64 > 64) return -1;
+    if (ws_bytes < sdpa_stage_bytes(B, H, Sq, Skv) || ((uintptr_t)ws & 255)) return -1;
+    auto al = [](size_t n) { return (n + 255) / 256 * 256; };
+    unsigned char* p = static_cast<unsigned char*>(ws);
+    T* qs = reinterpret_cast<T*>(p);
+    T* vt = reinterpret_cast<T*>(p + al((size_t)B * H * Sq * 64 * 2));
+    unsigned long long* bits =
+        reinterpret_cast<unsigned long long*>(p + al((size_t)B * H * Sq * 64 * 2) + al((size_t)B * H * 64 * vs * 2));
+    const int ntq = (Sq + 63) / 64, ntk = vs / 64;
+    sdpa_stage_kernel<T><<<dim3(ntq > ntk ? ntq : ntk, B * H), 256, 0, st>>>(
+        q, v, mask, H, Sq, Skv, vs, scale * 1.4426950408889634f, qs, vt, bits);
+    AttnArgs<T> a{};
+    a.Q = qs;
+    a.K0 = k;
+    a.V0 = vt;
+    a.len0 = Skv;
+    a.stride0 = Skv;
+    a.bits0 = bits;
+    a.B = B;
+    a.H = H;
+    a.Sq = Sq;
+    a.scale = scale;
+    a.v_transposed = true;
+    a.prescaled = true;
+    a.vstride0 = vs;
+    a.out_mode = 1;
+    a.Of = out;
+    return launch_attention32_t<T>(a, st);
+}
+template int launch_sdpa_staged<bf16>(const bf16*, const bf16*, const bf16*, const float*, int, int, int, int, float,
+                                      float*, void*, size_t, hipStream_t);
+template int launch_sdpa_staged<f16>(const f16*, const f16*, const f16*, const float*, int, int, int, int, float,
+                                     float*, void*, size_t, hipStream_t);
 
 }  // namespace irodori

@@ -105,7 +105,21 @@ __global__ __launch_bounds__(256) void vec_linear_kernel(const VecLinJob* __rest
     }
 }
 
+// Shift rows of the modulation table [vec][layer][kind][chunk][D] as bf16 GEMM operands:
+// block (v, l * 2 + k) copies chunk 0 of (v, l, k) to stage row (l * 2 + k) * cap + v.
+__global__ __launch_bounds__(256) void shift_stage_kernel(const float* __restrict__ tab, int cap, int L, int D,
+                                                          bf16* __restrict__ stage) {
+    const int v = blockIdx.x, lk = blockIdx.y;
+    const float* src = tab + ((size_t)v * L * 6 + (size_t)lk * 3) * D;
+    bf16* dst = stage + ((size_t)lk * cap + v) * D;
+    for (int d = threadIdx.x; d < D; d += 256) dst[d] = static_cast<bf16>(src[d]);
+}
+
 }  // namespace
+
+void launch_shift_stage(const float* tab, int nvec, int cap, int L, int D, bf16* stage, hipStream_t st) {
+    shift_stage_kernel<<<dim3(nvec, 2 * L), 256, 0, st>>>(tab, cap, L, D, stage);
+}
 
 void launch_timestep_embedding(const float* t, int nvec, int t_dim, float* out, hipStream_t st) {
     dim3 grid((t_dim / 2 + 255) / 256, nvec);

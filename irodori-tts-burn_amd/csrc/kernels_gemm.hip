@@ -135,6 +135,31 @@ __device__ __forceinline__ float half_wave_sum(float v) {
     return __builtin_bit_cast(float, (unsigned)sw[0]) + __builtin_bit_cast(float, (unsigned)sw[1]);
 }
 
+// Sums of 16 values per lane over the 32 lanes of each half-wave, one value per row: a
+// halving butterfly over lane bits 4, 3, 2, 1 (at each step a lane keeps the lower or upper
+// half of its values, by its lane bit, and adds the partner's copy of those), then bit 0.
+// v[0] ends as the sum of value e over the half-wave at every lane l with
+// e = 8 b4 + 4 b3 + 2 b2 + b1 (the bits of l % 32); returns e.  The order of additions is
+// fixed, so the sums are deterministic.
+__device__ __forceinline__ int half_wave_row_sums(float (&v)[16], int l) {
+#pragma unroll
+    for (int n = 16, m = 16; n > 1; n >>= 1, m >>= 1) {
+        const bool hi = (l & m) != 0;
+#pragma unroll
+        for (int k = 0; k < n / 2; k++) {
+            // Both values in registers before the selects (else the select of two array
+            // elements is folded into a lane-variable register index: a 16-way select chain).
+            float lo = v[k], up = v[k + n / 2];
+            asm volatile("" : "+v"(lo), "+v"(up));
+            const float send = hi ? lo : up;
+            const float keep = hi ? up : lo;
+            v[k] = keep + __shfl_xor(send, m, 64);
+        }
+    }
+    v[0] += __shfl_xor(v[0], 1, 64);
+    return 8 * ((l >> 4) & 1) + 4 * ((l >> 3) & 1) + 2 * ((l >> 2) & 1) + ((l >> 1) & 1);
+}
+
 // Staged bf16 wave tile of the QKVG epilogue: row r (< 64) of 64 columns lives at
 // slot + 256 r, its 16-byte chunk c at chunk position c ^ (4 * ((r >> 2 ^ r) & 1)).  The
 // column writes of an accumulator step touch rows r and r + 4 together and the 16-byte row
@@ -271,8 +296,10 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
     // EPI_RESID (S >= 32): the residual elements this lane updates and the gate rows of
     // the (at most two) batch rows each 32-row block touches are loaded before the main
     // loop, so their latency hides behind it (each element belongs to one lane only).
+    // With Hn set (fused adaLN producer) the next norm's scale columns are loaded likewise.
     [[maybe_unused]] float xpre[FM][16][FN];
     [[maybe_unused]] float gpre[FM][2][FN];
+    [[maybe_unused]] float spre[FM][2][FN];
     [[maybe_unused]] int hi_row[FM];  // first row of the upper batch row of block i
     if constexpr (EPI == EPI_RESID) {
         if (a.S >= 32) {
@@ -292,6 +319,12 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
                                                  (size_t)a.layer * 6 + a.kind * 3 + 2) * a.N;
 #pragma unroll
                     for (int j = 0; j < FN; j++) gpre[i][u][j] = (!u || need_hi) ? g[n0 + wn0 + 32 * j + cl] : 0.f;
+                    if (!F8 && a.Hn) {
+                        const float* sc = a.mt.tab + ((size_t)mod_vec_index(a.mt, step, bb) * a.mt.layers * 6 +
+                                                      (size_t)a.next_layer * 6 + a.next_kind * 3 + 1) * a.N;
+#pragma unroll
+                        for (int j = 0; j < FN; j++) spre[i][u][j] = (!u || need_hi) ? sc[n0 + wn0 + 32 * j + cl] : 0.f;
+                    }
                 }
 #pragma unroll
                 for (int e = 0; e < 16; e++) {
@@ -300,6 +333,32 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
                     for (int j = 0; j < FN; j++)
                         xpre[i][e][j] = row < a.M ? a.x[(size_t)row * a.N + n0 + wn0 + 32 * j + cl] : 0.f;
                 }
+            }
+        }
+    }
+
+    // Fused adaLN consumer: lane l of a wave loads the K/32 partial sums of row m0 + wm0 + l
+    // and this wave's shift-bias columns before the operand stream starts, so their latency
+    // hides behind it; iteration 0 of the main loop turns the sums into r = rsqrt(mean x^2 +
+    // eps) in the wave's own LDS slot (rows of the wave only: no workgroup barrier).
+    constexpr bool FUSE_IN = !F8 && (EPI == EPI_QKVG || EPI == EPI_SWIGLU);
+    [[maybe_unused]] float* rs_lds = reinterpret_cast<float*>(smem + STAGES * STAGE_BYTES) + wave * WM;
+    [[maybe_unused]] float4 rsv[8];
+    [[maybe_unused]] float bc[FN];
+    if constexpr (FUSE_IN) {
+        static_assert(WM <= 64, "one row per lane");
+        if (a.rstat) {
+            const int vec = mod_vec_index(a.mt, a.mt.step ? *a.mt.step : 0, 0);
+#pragma unroll
+            for (int j = 0; j < FN; j++) bc[j] = a.rbias[(size_t)vec * a.N + n0 + wn0 + 32 * j + lane % 32];
+            const int row = m0 + wm0 + lane, nq = K / 128;
+#pragma unroll
+            for (int q = 0; q < 8; q++) rsv[q] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (lane < WM && row < a.M) {
+                const float4* p = reinterpret_cast<const float4*>(a.rstat + (size_t)row * (K / 32));
+#pragma unroll
+                for (int q = 0; q < 8; q++)
+                    if (q < nq) rsv[q] = p[q];
             }
         }
     }
@@ -316,6 +375,19 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
         else wait_vmcnt<0>();
         raw_barrier();
         if (kt + STAGES - 1 < nk) GEMM_ISSUE(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
+        if constexpr (FUSE_IN) {
+            if (a.rstat && kt == 0) {
+                float ss = 0.f;
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    ss += rsv[q].x;
+                    ss += rsv[q].y;
+                    ss += rsv[q].z;
+                    ss += rsv[q].w;
+                }
+                if (lane < WM) rs_lds[lane] = m0 + wm0 + lane < a.M ? 1.f / sqrtf(ss / (float)K + a.eps) : 1.f;
+            }
+        }
         const unsigned char* st = smem + (kt % STAGES) * STAGE_BYTES;
         if constexpr (F8) {
             // Scale bytes of this lane's rows for the slice's four k blocks.
@@ -387,6 +459,26 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
             for (int i = 0; i < FM; i++)
 #pragma unroll
                 for (int e = 0; e < 16; e++) acc[i][j][e] *= wsv;
+        }
+    }
+
+    if constexpr (FUSE_IN) {
+        if (a.rstat) {
+            // acc = r * acc + (shift W)[vec, col]; every row of the launch has the same
+            // modulation vector (checked at launch).
+            // Row scales of this lane (its wave's slot): rows 4 (lane / 32) + 32 i + 8 q + 0..3.
+            float4 rr[FM][4];
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    rr[i][q] = *reinterpret_cast<const float4*>(rs_lds + 4 * (lane >> 5) + 32 * i + 8 * q);
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int e = 0; e < 16; e++)
+#pragma unroll
+                    for (int j = 0; j < FN; j++) acc[i][j][e] = acc[i][j][e] * rr[i][e >> 2][e & 3] + bc[j];
         }
     }
 
@@ -581,32 +673,61 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
             }
     } else if constexpr (EPI == EPI_RESID) {
         // x[row, col] += gate[b(row), col] * C, from the values loaded before the main loop.
+        // Fused adaLN producer (Hn set): also Hn = x (1 + scale_next) and the sums of x^2 of
+        // each row over the lane group's 32 columns (one half-wave holds one row's 32 columns
+        // of a block, so every lane takes part in the reduction; rows past M add zero).
         float* __restrict__ xg = a.x;
+        const bool fuse_out = !F8 && a.Hn != nullptr;
+        const int np = a.N / 32;
         if (a.S < 32) {  // a 32-row block may span more than two batch rows
+            const int step = a.mt.step ? *a.mt.step : 0;
 #pragma unroll
             for (int i = 0; i < FM; i++)
 #pragma unroll
                 for (int e = 0; e < 16; e++) {
                     const int row = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
-                    if (row >= a.M) continue;
-                    const float* g = gate_vec(a.mt, row / a.S, a.layer, a.kind, a.N);
+                    const bool ok = row < a.M;
+                    const int b = (ok ? row : a.M - 1) / a.S;
+                    const float* g = gate_vec(a.mt, b, a.layer, a.kind, a.N);
+                    const float* sc = a.mt.tab + ((size_t)mod_vec_index(a.mt, step, b) * a.mt.layers * 6 +
+                                                  (size_t)a.next_layer * 6 + a.next_kind * 3 + 1) * a.N;
 #pragma unroll
                     for (int j = 0; j < FN; j++) {
                         const int col = n0 + wn0 + 32 * j + cl;
-                        xg[(size_t)row * a.N + col] += g[col] * acc[i][j][e];
+                        const float xn = ok ? xg[(size_t)row * a.N + col] + g[col] * acc[i][j][e] : 0.f;
+                        if (ok) xg[(size_t)row * a.N + col] = xn;
+                        if (fuse_out) {
+                            if (ok) a.Hn[(size_t)row * a.N + col] = from_f32<T>(xn * (1.f + sc[col]));
+                            const float ss = half_wave_sum(xn * xn);
+                            if (ok && cl == 0) a.rstat_out[(size_t)row * np + (n0 + wn0) / 32 + j] = ss;
+                        }
                     }
                 }
         } else
 #pragma unroll
         for (int i = 0; i < FM; i++) {
 #pragma unroll
-            for (int e = 0; e < 16; e++) {
-                const int row = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
-                if (row >= a.M) continue;
-                const int u = row >= hi_row[i] ? 1 : 0;
+            for (int j = 0; j < FN; j++) {
+                float sq[16];
 #pragma unroll
-                for (int j = 0; j < FN; j++)
-                    xg[(size_t)row * a.N + n0 + wn0 + 32 * j + cl] = xpre[i][e][j] + gpre[i][u][j] * acc[i][j][e];
+                for (int e = 0; e < 16; e++) {
+                    const int row = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
+                    const bool ok = row < a.M;
+                    const int u = row >= hi_row[i] ? 1 : 0;
+                    const float xn = xpre[i][e][j] + gpre[i][u][j] * acc[i][j][e];
+                    sq[e] = ok ? xn * xn : 0.f;
+                    if (ok) xg[(size_t)row * a.N + n0 + wn0 + 32 * j + cl] = xn;
+                    if (fuse_out && ok)
+                        a.Hn[(size_t)row * a.N + n0 + wn0 + 32 * j + cl] = from_f32<T>(xn * (1.f + spre[i][u][j]));
+                }
+                if (fuse_out) {
+                    // Row sums over the half-wave's 32 columns: a halving butterfly over lane
+                    // bits 4..1 (each step keeps half the rows and adds the partner's values of
+                    // them), then bit 0; lane l ends with row e = 8 b4 + 4 b3 + 2 b2 + b1 of l.
+                    const int e = half_wave_row_sums(sq, cl);
+                    const int row = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
+                    if (row < a.M && (cl & 1) == 0) a.rstat_out[(size_t)row * np + (n0 + wn0) / 32 + j] = sq[0];
+                }
             }
         }
     } else if constexpr (EPI == EPI_SWIGLU) {
@@ -896,6 +1017,35 @@ int launch_cfg(const GemmArgs<T>& a, hipStream_t st) {
     constexpr int BK = 128 / ES;
     constexpr int kMaxK8 = 8192;  // fp8: the staged block scales take BM * K / 32 bytes of LDS
     if (a.M <= 0 || a.N % BN != 0 || a.K % BK != 0 || a.K <= 0 || (F8 && a.K > kMaxK8)) return -1;
+    // Every pointer the instantiation's main loop and epilogue dereference must be set (the
+    // guard sits here, under every launcher, so no caller can skip it).
+    if (F8 ? (!a.A8 || !a.As || !a.W8 || !a.ws) : (!a.A || !a.W)) return -1;
+    const bool snake_out = EPI == EPI_SNAKE || EPI == EPI_RESUNIT || ((EPI == EPI_STORE || EPI == EPI_ADD) && a.U);
+    if (snake_out && (!a.alpha || a.alpha_n <= 0)) return -1;
+    switch (EPI) {
+        case EPI_STORE: if (!a.C) return -1; break;
+        case EPI_RESID: if (!a.x || !a.mt.tab) return -1; break;
+        case EPI_ADD: if (!a.x) return -1; break;
+        case EPI_SWIGLU: if (F8 ? (!a.U8 || !a.U8s) : !a.U) return -1; break;
+        case EPI_SNAKE: if (!a.U) return -1; break;
+        case EPI_RESUNIT: if (!a.W2 || !a.x || (a.U && !a.alpha2)) return -1; break;
+        case EPI_QKVG:
+            if (!a.Q || !a.Kd || !a.Vd || !a.G || !a.q_norm || !a.k_norm || !a.rope_cos || !a.rope_sin || a.H <= 0 ||
+                a.D != a.H * 64 || a.N != 4 * a.D || a.vt_stride < a.S || a.S <= 0)
+                return -1;
+            break;
+        case EPI_CTXKV: if (!a.Ck || !a.Cv || !a.k_norm || a.H <= 0) return -1; break;
+    }
+    // Fused adaLN: a consumer takes bf16 / f32 operands of the QKVG or SwiGLU projections
+    // (K a multiple of 32), a producer writes the next operand after a residual update.
+    // The consumer loads each row's K / 32 partials as at most 8 float4 (K % 128 == 0, K <= 1024),
+    // and every row of the launch shares one modulation vector (the batch rows all map to it).
+    if (a.rstat && (F8 || (EPI != EPI_QKVG && EPI != EPI_SWIGLU) || !a.rbias || a.K % 128 || a.K > 1024 ||
+                    a.S <= 0 || !a.mt.tab || a.mt.rows_per_vec < (a.M + a.S - 1) / a.S))
+        return -1;
+    if (a.Hn && (F8 || EPI != EPI_RESID || !a.rstat_out || a.N % 32 || a.next_layer < 0 ||
+                 a.next_layer >= a.mt.layers || a.next_kind < 0 || a.next_kind > 1))
+        return -1;
     if ((size_t)BN * a.K * ES > 0xffffffffull || (size_t)BM * a.K * ES > 0xffffffffull) return -1;
     if (CONV) {
         // conv_cp a multiple of half a slice (a slice straddles at most two taps, at its
@@ -910,15 +1060,17 @@ int launch_cfg(const GemmArgs<T>& a, hipStream_t st) {
     // EPI_RESUNIT keeps the Snake'd tile (BN / BK slices of BM rows) and one W2 slice in LDS.
     constexpr int kResLds = EPI == EPI_RESUNIT ? ((BN + BK - 1) / BK) * BM * 128 + BN * 128 : 0;
     constexpr int kStageLds = STAGES * (BM + BN) * 128;
-    const size_t lds = (size_t)(kStageLds > kResLds ? kStageLds : kResLds) + (F8 ? (size_t)BM * (a.K / 32) : 0);
-    static bool attr_set = false;  // per instantiation; the attribute is process-wide
-    if (!attr_set) {
-        const int lds_max = (kStageLds > kResLds ? kStageLds : kResLds) + (F8 ? BM * (kMaxK8 / 32) : 0);
-        if (hipFuncSetAttribute((const void*)gemm_kernel<T, BM, BN, WAVES_M, WAVES_N, STAGES, EPI, F8, CONV>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, lds_max) != hipSuccess)
-            return -2;
-        attr_set = true;
-    }
+    // The fused-adaLN consumer keeps the row scales of each wave's rows past the stages.
+    constexpr int kRowLds = (!F8 && (EPI == EPI_QKVG || EPI == EPI_SWIGLU)) ? WAVES_M * WAVES_N * (BM / WAVES_M) * 4 : 0;
+    const size_t lds = (size_t)(kStageLds > kResLds ? kStageLds : kResLds) + (F8 ? (size_t)BM * (a.K / 32) : 0) +
+                       (a.rstat ? kRowLds : 0);
+    // Per instantiation; the attribute is process-wide.
+    static std::once_flag once;
+    static hipError_t attr_rc = hipSuccess;
+    constexpr int lds_max = (kStageLds > kResLds ? kStageLds : kResLds) + (F8 ? BM * (kMaxK8 / 32) : 0) + kRowLds;
+    if (set_lds_limit_once(once, attr_rc, (const void*)gemm_kernel<T, BM, BN, WAVES_M, WAVES_N, STAGES, EPI, F8, CONV>,
+                           lds_max) != hipSuccess)
+        return -2;
     gemm_kernel<T, BM, BN, WAVES_M, WAVES_N, STAGES, EPI, F8, CONV><<<tiles, 64 * WAVES_M * WAVES_N, lds, st>>>(a);
     return 0;
 }

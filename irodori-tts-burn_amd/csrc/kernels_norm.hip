@@ -104,6 +104,34 @@ __global__ __launch_bounds__(256) void norm_mod_kernel(const float* __restrict__
     }
 }
 
+// The fused adaLN's operand of one (layer, kind) from the residual x: h = x (1 + scale)
+// in the compute dtype and rstat [M, D/32] the sums of x^2 per 32 columns (the GEMM that
+// reads h applies 1 / rms and the shift).  Lane chunks as in norm_mod_kernel: a 32-column
+// block is the quads of 8 neighbouring lanes.
+template <typename T, int NCH>
+__global__ __launch_bounds__(256) void mod_stats_kernel(const float* __restrict__ x, T* __restrict__ h, int M,
+                                                        int S, int D, ModTable mt, int layer, int kind,
+                                                        float* __restrict__ rstat) {
+    int row = blockIdx.x * kRowsPerBlock + threadIdx.x / 64, lane = threadIdx.x % 64;
+    if (row >= M) return;
+    const float* xr = x + (size_t)row * D;
+    const float* scale = mod_base(mt, row / S, layer, kind, D) + D;
+#pragma unroll
+    for (int j = 0; j < NCH; j++) {
+        int d = lane * 4 + 256 * j;
+        if (d >= D) break;
+        const float4 v = *reinterpret_cast<const float4*>(xr + d);
+        const float4 sc = *reinterpret_cast<const float4*>(scale + d);
+        store4<T>(h + (size_t)row * D + d, v.x * (1.f + sc.x), v.y * (1.f + sc.y), v.z * (1.f + sc.z),
+                  v.w * (1.f + sc.w));
+        float q = v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        q += __shfl_xor(q, 1, 64);
+        q += __shfl_xor(q, 2, 64);
+        q += __shfl_xor(q, 4, 64);
+        if ((lane & 7) == 0) rstat[(size_t)row * (D / 32) + d / 32] = q;
+    }
+}
+
 // in_proj (x = x_src @ W_in + b_in, dit/model.rs:370) fused with the first adaLN.  A
 // 256-thread block owns ROWS rows (8, or 2 when that leaves too few blocks to fill the chip); thread t owns the column quads 4 t + 1024 j (j <
 // NCH) of every row, so each W_in quad is loaded once per block and applied to all its
@@ -111,11 +139,14 @@ __global__ __launch_bounds__(256) void norm_mod_kernel(const float* __restrict__
 // in LDS 64 latent channels at a time; the row RMS reduces over lanes, then over the 4
 // wavefronts through LDS.
 
+// With rstat set (the fused adaLN of the bf16 model path) h gets x (1 + scale) instead, and
+// rstat [M, D/32] the sums of x^2 per 32 columns (8 neighbouring lanes hold one block).
 template <typename T, int NCH, int ROWS>
 __global__ __launch_bounds__(256) void inproj_norm_kernel(
     const float* __restrict__ x_src, int src_batches, const float* __restrict__ in_w,
     const float* __restrict__ in_b, float* __restrict__ x, T* __restrict__ h, int M, int S, int P,
-    int D, float eps, ModTable mt, uint8_t* __restrict__ q8, uint8_t* __restrict__ q8s) {
+    int D, float eps, ModTable mt, uint8_t* __restrict__ q8, uint8_t* __restrict__ q8s,
+    float* __restrict__ rstat) {
     __shared__ float xs[ROWS][64];
     __shared__ float red[ROWS][4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -177,12 +208,38 @@ __global__ __launch_bounds__(256) void inproj_norm_kernel(
             if (d >= D) break;
             const float4 v = acc[r][j];
             if (row < M) *reinterpret_cast<float4*>(x + (size_t)row * D + d) = v;
-            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+            float q = v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+            ss += q;
+            if (rstat) {
+                // Columns 32 c .. 32 c + 31 are the quads of lanes 8 c' .. 8 c' + 7.
+                q += __shfl_xor(q, 1, 64);
+                q += __shfl_xor(q, 2, 64);
+                q += __shfl_xor(q, 4, 64);
+                if (row < M && (tid & 7) == 0) rstat[(size_t)row * (D / 32) + d / 32] = q;
+            }
         }
         ss = wave_sum(ss);
         if (lane == 0) red[r][wave] = ss;
     }
     __syncthreads();
+    if (rstat) {  // fused adaLN: the GEMMs apply 1 / rms and the shift themselves
+#pragma unroll
+        for (int r = 0; r < ROWS; r++) {
+            const int row = row0 + r;
+            if (row >= M) break;
+            const float* scale = mod_base(mt, row / S, 0, 0, D) + D;
+#pragma unroll
+            for (int j = 0; j < NCH; j++) {
+                const int d = 4 * tid + 1024 * j;
+                if (d >= D) break;
+                const float4 sc = *reinterpret_cast<const float4*>(scale + d);
+                const float4 v = acc[r][j];
+                store4<T>(h + (size_t)row * D + d, v.x * (1.f + sc.x), v.y * (1.f + sc.y), v.z * (1.f + sc.z),
+                          v.w * (1.f + sc.w));
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int r = 0; r < ROWS; r++) {
         const int row = row0 + r;
@@ -359,15 +416,27 @@ void launch_norm_mod(const float* x, T* h, int M, int S, int D, float eps, ModTa
 }
 
 template <typename T>
+void launch_mod_stats(const float* x, T* h, int M, int S, int D, ModTable mt, int layer, int kind, float* rstat,
+                      hipStream_t st) {
+    int grid = (M + kRowsPerBlock - 1) / kRowsPerBlock;
+    int nch = (D + 255) / 256;
+    if (nch <= 1) mod_stats_kernel<T, 1><<<grid, 256, 0, st>>>(x, h, M, S, D, mt, layer, kind, rstat);
+    else if (nch <= 2) mod_stats_kernel<T, 2><<<grid, 256, 0, st>>>(x, h, M, S, D, mt, layer, kind, rstat);
+    else if (nch <= 4) mod_stats_kernel<T, 4><<<grid, 256, 0, st>>>(x, h, M, S, D, mt, layer, kind, rstat);
+    else mod_stats_kernel<T, 8><<<grid, 256, 0, st>>>(x, h, M, S, D, mt, layer, kind, rstat);
+}
+template void launch_mod_stats<bf16>(const float*, bf16*, int, int, int, ModTable, int, int, float*, hipStream_t);
+
+template <typename T>
 void launch_inproj_norm(const float* x_src, int src_batches, const float* in_w,
                         const float* in_b, float* x, T* h, int M, int S, int P, int D, float eps,
-                        ModTable mt, hipStream_t st, uint8_t* q8, uint8_t* q8s) {
+                        ModTable mt, hipStream_t st, uint8_t* q8, uint8_t* q8s, float* rstat) {
     const int nch = (D + 1023) / 1024;
     const bool fine = (M + 7) / 8 < 512;  // fewer than two blocks per CU at 8 rows
     const int rows = fine ? 2 : 8, grid = (M + rows - 1) / rows;
 #define IRO_INPROJ(N, R)                                                                      \
     inproj_norm_kernel<T, N, R><<<grid, 256, 0, st>>>(x_src, src_batches, in_w, in_b, x, h, M, \
-                                                      S, P, D, eps, mt, q8, q8s)
+                                                      S, P, D, eps, mt, q8, q8s, rstat)
     if (fine) {
         if (nch <= 1) IRO_INPROJ(1, 2);
         else if (nch <= 2) IRO_INPROJ(2, 2);
@@ -386,22 +455,20 @@ template void launch_norm_mod<bf16>(const float*, bf16*, int, int, int, float, M
                                     int, hipStream_t, uint8_t*, uint8_t*);
 template void launch_inproj_norm<float>(const float*, int, const float*, const float*, float*,
                                         float*, int, int, int, int, float, ModTable,
-                                        hipStream_t, uint8_t*, uint8_t*);
+                                        hipStream_t, uint8_t*, uint8_t*, float*);
 template void launch_inproj_norm<bf16>(const float*, int, const float*, const float*, float*,
                                        bf16*, int, int, int, int, float, ModTable, hipStream_t,
-                                       uint8_t*, uint8_t*);
+                                       uint8_t*, uint8_t*, float*);
 
 template <int PT, int NR, int FR>
 static void launch_final_cfg(const FinalArgs& a, hipStream_t st) {
     constexpr int KS = 256 / PT, R = NR * FR;
     const size_t lds = sizeof(float) * ((size_t)R * a.D + (size_t)KS * R * PT + (size_t)R * PT + R);
-    static bool attr_set = false;
-    if (!attr_set) {
-        // Sized for the largest model width the context accepts (D <= 2048).
-        constexpr int kMax = (int)sizeof(float) * (R * 2048 + KS * R * PT + R * PT + R);
-        (void)hipFuncSetAttribute((const void*)final_kernel<PT, NR, FR>, hipFuncAttributeMaxDynamicSharedMemorySize, kMax);
-        attr_set = true;
-    }
+    // Sized for the largest model width the context accepts (D <= 2048).
+    constexpr int kMax = (int)sizeof(float) * (R * 2048 + KS * R * PT + R * PT + R);
+    static std::once_flag once;
+    static hipError_t attr_rc = hipSuccess;
+    (void)set_lds_limit_once(once, attr_rc, (const void*)final_kernel<PT, NR, FR>, kMax);
     const int ngroups = a.rf.plan ? a.B : (a.B + NR - 1) / NR;
     const dim3 grid((a.S + FR - 1) / FR, ngroups < 65535 ? ngroups : 65535);
     final_kernel<PT, NR, FR><<<grid, 256, lds, st>>>(a);

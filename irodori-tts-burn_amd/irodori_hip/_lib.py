@@ -28,6 +28,7 @@ ERR_NAMES = {ERR_INVALID_ARG: "InvalidArg", ERR_SHAPE: "Shape", ERR_DTYPE: "Dtyp
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 DTYPE_FP8 = 2
+DTYPE_F16 = 3  # irodori_op_sdpa operands only (native_fa_sdpa_f16_in)
 CFG_INDEPENDENT, CFG_JOINT, CFG_ALTERNATING = 0, 1, 2
 METHOD_EULER, METHOD_HEUN, METHOD_PLMS4 = 0, 1, 2
 

@@ -88,6 +88,60 @@ def test_sdpa_op_bf16(oracle64, B, H, Sq, Skv, Dh, mask):
     assert rel_l2(out.cpu().numpy(), want) < 1e-2
 
 
+# The reference's f16-input FA tests (fused_sdpa_native_f16.rs:455-585): shapes, masks and
+# tolerances (1e-3 max abs; 1e-6 for the all-masked case), with the oracle fed the same
+# f16-rounded inputs as the reference's own CPU check (:384-388).  head_dim 128 runs on the
+# generic flash kernel, head_dim 64 on the model's joint attention kernel after staging.
+F16_CASES = [
+    (1, 2, 4, 6, 128, None, 1e-3),
+    (1, 2, 4, 8, 128, [1, 1, 1, 1, 1, 0, 0, 0], 1e-3),
+    (1, 16, 32, 48, 128, None, 1e-3),
+    (1, 1, 17, 9, 128, None, 1e-3),
+    (1, 2, 4, 8, 128, [0] * 8, 1e-6),
+    (2, 4, 16, 24, 128, None, 1e-3),
+    (1, 16, 32, 48, 64, None, 1e-3),
+    # head_dim 64 beyond the reference's cases: a partial last key tile, a random mask and
+    # more than one query block per head.
+    (2, 3, 100, 70, 64, "random", 1e-3),
+    (1, 2, 4, 8, 64, [0] * 8, 1e-6),
+]
+
+
+@pytest.mark.parametrize("B,H,Sq,Skv,Dh,mask,tol", F16_CASES)
+def test_sdpa_op_f16(oracle64, B, H, Sq, Skv, Dh, mask, tol):
+    q, k, v = (a.astype(np.float16) for a in _ref_inputs(B, H, Sq, Skv, Dh))
+    m = _mask_for(mask, B, Skv)
+    dq, dk, dv = (dev(a, torch.float16) for a in (q, k, v))
+    dm = dev(m)
+    out = torch.full(q.shape, 7.0, dtype=torch.float32, device="cuda")
+    ops.sdpa(L.DTYPE_F16, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), dm.data_ptr(), B, H, Sq,
+             Skv, Dh, Dh ** -0.5, out.data_ptr())
+    torch.cuda.synchronize()
+    want = oracle64.sdpa(q.astype(np.float32), k.astype(np.float32), v.astype(np.float32), m, Dh ** -0.5)
+    assert np.abs(out.cpu().numpy() - want).max() < tol
+
+
+def test_sdpa_op_f16_bf16_share_the_joint_kernel(oracle64):
+    # Dh = 64 16-bit operators run the model's joint attention kernel: a context longer than
+    # one key tile per parity and a query count that is not a multiple of the query block.
+    B, H, Sq, Skv, Dh = 1, 4, 75, 300, 64
+    rng = np.random.default_rng(3)
+    q, k, v = (rng.standard_normal((B, H, n, Dh)).astype(np.float32) for n in (Sq, Skv, Skv))
+    m = np.ones((B, Skv), np.float32)
+    m[0, 200:] = 0
+    m[0, 37] = 0
+    for dtype, tdt, npdt in ((L.DTYPE_F16, torch.float16, np.float16), (L.DTYPE_BF16, torch.bfloat16, None)):
+        qq, kk, vv = ((a.astype(npdt).astype(np.float32) if npdt else bf16_round(a)) for a in (q, k, v))
+        dq, dk, dv = (dev(a, tdt) for a in (qq, kk, vv))
+        out = torch.empty(q.shape, dtype=torch.float32, device="cuda")
+        ops.sdpa(dtype, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), dev(m).data_ptr(), B, H, Sq, Skv, Dh,
+                 Dh ** -0.5, out.data_ptr())
+        torch.cuda.synchronize()
+        want = oracle64.sdpa(qq, kk, vv, m, Dh ** -0.5)
+        # f16: 11-bit operands (the probabilities too); bf16: 8-bit.
+        assert rel_l2(out.cpu().numpy(), want) < (2e-3 if npdt else 1e-2)
+
+
 def test_sdpa_all_masked_rows_are_zero():
     # attention.rs:770-787: a query row with no valid key yields exactly 0.
     B, H, Sq, Skv, Dh = 2, 2, 5, 70, 64

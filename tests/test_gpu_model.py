@@ -260,6 +260,28 @@ def test_forward_latent_mask_vs_oracle(oracle64, name, backend):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("backend", [F32, BF16], ids=["f32", "bf16"])
+def test_forward_row_without_any_valid_key(oracle64, backend):
+    # Row 1 is the unconditioned bundle (every context key masked); with its latent keys
+    # masked too, no key of that row attends: its attention output is 0 in every block
+    # (attention.rs:770-787) and the forward still matches the oracle.
+    cfg = ih.cfg_tiny()
+    w = ih.DitWeights.random(cfg, 3, std=0.05, norm_jitter=0.1)
+    ctx = ih.make_context_kv(cfg, 1, 12, 9, seed=4)
+    S = 40
+    x = ih.make_noise(2, S, cfg.latent_dim, 5)
+    t = np.array([0.7, 0.7], np.float32)
+    m = _latent_mask(2, S, [S, 0])
+    with make_engine(cfg, backend, w, ctx, 2, S) as e:
+        v, dbg = e.forward_with_cond_cached(x, t, debug=True, latent_mask=m)
+    v_ref, dbg_ref = oracle64.forward(cfg, w, x, t, ctx.k, ctx.v, ctx.mask, debug=True, latent_mask=m)
+    assert np.all(np.isfinite(v))
+    errs = [rel_l2(dbg[i], dbg_ref[i]) for i in range(dbg.shape[0])]
+    assert max(errs) < TOL_BLOCK[backend], errs
+    assert rel_l2(v, v_ref) < TOL_BLOCK[backend]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("backend", [F32, BF16], ids=["f32", "bf16"])
 def test_sample_padded_batch_matches_unpadded(backend):
     # Two utterances padded to 64 frames, the second only 41 long: its first 41 frames
     # equal an unpadded 41-frame run of that utterance alone.
