@@ -410,6 +410,18 @@ int irodori_op_fused_adaln(const float* x, const float* scale, const float* shif
 int irodori_op_sdpa(int dtype, const void* q, const void* k, const void* v, const float* mask,
                     int batch, int heads, int seq_q, int seq_kv, int head_dim, float scale,
                     float* out, void* stream);
+/* No counterpart in the reference: irodori_op_sdpa for callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops that forbid hipMalloc).  Same
+ * arguments, kernels and results; the staging of the 16-bit head_dim-64 path lives in one
+ * fixed device buffer of IRODORI_SDPA_SCRATCH_BYTES per GPU, held until the process ends,
+ * instead of a per-call allocation.  A shape whose staging (Q + V^T in the operand dtype +
+ * the key bits, each rounded up to 256 bytes) exceeds it returns IRODORI_ERR_SHAPE.  Every
+ * call on a GPU shares that buffer: calls that overlap on one GPU (other streams or
+ * threads) race. */
+#define IRODORI_SDPA_SCRATCH_BYTES (16u << 20)
+int irodori_op_sdpa_noalloc(int dtype, const void* q, const void* k, const void* v, const float* mask,
+                            int batch, int heads, int seq_q, int seq_kv, int head_dim, float scale,
+                            float* out, void* stream);
 /* The fp8 GEMM-operand form of the IRODORI_DTYPE_FP8 mode (no counterpart in the
  * reference): x [rows, dim] f32 (dim % 32 == 0) -> e4m3 codes q [rows, dim] and E8M0 scale
  * bytes s [rows, dim/32]; per 32-wide block, 2^e with e the smallest integer such that

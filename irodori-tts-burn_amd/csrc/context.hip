@@ -567,11 +567,6 @@ int enqueue_layer_any(irodori_ctx* c, int l, int B, int S, const ModTable& mt, i
     return c->bf16 ? enqueue_layer<bf16>(c, l, B, S, mt, r0, st) : enqueue_layer<float>(c, l, B, S, mt, r0, st);
 }
 
-int enqueue_part_any(irodori_ctx* c, int l, int B, int S, const ModTable& mt, int part) {
-    return c->bf16 ? enqueue_part<bf16>(c, l, B, S, mt, part, 0, c->stream)
-                   : enqueue_part<float>(c, l, B, S, mt, part, 0, c->stream);
-}
-
 // in_proj + the first adaLN for batch rows [r0, r0 + B): row r0 + b reads source row
 // b mod src_batches of src [src_batches, S, P].
 int enqueue_inproj(irodori_ctx* c, int B, int S, const float* src, int src_batches, int r0, const ModTable& mt,
@@ -740,59 +735,6 @@ int validate_params(const irodori_sampler_params* p) {
                         ", caption=" + std::to_string(p->scale_caption));
     }
     return IRODORI_OK;
-}
-
-// ---- SDPA operator helpers ----------------------------------------------------------------
-
-int check_sdpa_args(int dtype, const void* q, const void* k, const void* v, int B, int H, int Sq, int Skv, int Dh,
-                    const float* out) {
-    IRO_REQUIRE(q && k && v && out, IRODORI_ERR_INVALID_ARG, "null argument");
-    IRO_REQUIRE(B > 0 && H > 0 && Sq > 0 && Skv > 0, IRODORI_ERR_SHAPE, "SDPA dims must be positive");
-    IRO_REQUIRE(Dh == 64 || Dh == 128, IRODORI_ERR_SHAPE, "head_dim must be 64 or 128");
-    IRO_REQUIRE(dtype == IRODORI_DTYPE_F32 || dtype == IRODORI_DTYPE_BF16 || dtype == IRODORI_DTYPE_F16,
-                IRODORI_ERR_DTYPE, "dtype must be F32, BF16 or F16");
-    return IRODORI_OK;
-}
-
-// 16-bit operands with Dh = 64 run on the model's joint attention kernel after staging
-// (its tile list holds up to 4096 keys); everything else on the generic flash kernel.
-bool sdpa_staged(int dtype, int Dh, int Skv) {
-    return dtype != IRODORI_DTYPE_F32 && Dh == 64 && Skv <= 4096;
-}
-
-template <typename T>
-int sdpa_direct_t(const void* q, const void* k, const void* v, const float* mask, int B, int H, int Sq, int Skv, int Dh,
-                  float scale, float* out, hipStream_t st) {
-    AttnArgs<T> a{};
-    a.Q = static_cast<const T*>(q);
-    a.K0 = static_cast<const T*>(k);
-    a.V0 = static_cast<const T*>(v);
-    a.len0 = Skv; a.stride0 = Skv; a.mask0 = mask;
-    a.B = B; a.H = H; a.Sq = Sq; a.scale = scale; a.out_mode = 1; a.Of = out;
-    const int rc = Dh == 64 ? launch_attention<T, 64>(a, st) : launch_attention<T, 128>(a, st);
-    IRO_REQUIRE(rc == 0, IRODORI_ERR_SHAPE, "sdpa launch rejected the shape");
-    return check_launch("sdpa");
-}
-
-int sdpa_direct(int dtype, const void* q, const void* k, const void* v, const float* mask, int B, int H, int Sq,
-                int Skv, int Dh, float scale, float* out, hipStream_t st) {
-    if (dtype == IRODORI_DTYPE_BF16) return sdpa_direct_t<bf16>(q, k, v, mask, B, H, Sq, Skv, Dh, scale, out, st);
-    if (dtype == IRODORI_DTYPE_F16) return sdpa_direct_t<f16>(q, k, v, mask, B, H, Sq, Skv, Dh, scale, out, st);
-    return sdpa_direct_t<float>(q, k, v, mask, B, H, Sq, Skv, Dh, scale, out, st);
-}
-
-// The staged path on a caller-provided (or stream-ordered) buffer ws of `bytes`.
-int sdpa_run_staged(int dtype, const void* q, const void* k, const void* v, const float* mask, int B, int H, int Sq,
-                    int Skv, float scale, float* out, void* ws, size_t bytes, hipStream_t st) {
-    int rc;
-    if (dtype == IRODORI_DTYPE_BF16)
-        rc = launch_sdpa_staged<bf16>(static_cast<const bf16*>(q), static_cast<const bf16*>(k),
-                                      static_cast<const bf16*>(v), mask, B, H, Sq, Skv, scale, out, ws, bytes, st);
-    else
-        rc = launch_sdpa_staged<f16>(static_cast<const f16*>(q), static_cast<const f16*>(k),
-                                     static_cast<const f16*>(v), mask, B, H, Sq, Skv, scale, out, ws, bytes, st);
-    IRO_REQUIRE(rc == 0, IRODORI_ERR_SHAPE, "staged sdpa rejected the shape");
-    return check_launch("sdpa");
 }
 
 // Number of sampler roles (context bundles) for n active signals (role-major rows).
@@ -1802,24 +1744,6 @@ int irodori_op_fused_adaln(const float* x, const float* scale, const float* shif
     IRO_REQUIRE(batch > 0 && seq > 0 && dim > 0, IRODORI_ERR_SHAPE, "fused AdaLN requires positive dims");
     launch_fused_adaln_op(x, scale, shift, batch, seq, dim, eps, y, static_cast<hipStream_t>(stream));
     return check_launch("fused_adaln");
-    IRO_GUARD_END
-}
-
-int irodori_op_sdpa(int dtype, const void* q, const void* k, const void* v, const float* mask, int B, int H, int Sq,
-                    int Skv, int Dh, float scale, float* out, void* stream) {
-    IRO_GUARD_BEGIN
-    IRO_TRY(check_sdpa_args(dtype, q, k, v, B, H, Sq, Skv, Dh, out));
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    if (!sdpa_staged(dtype, Dh, Skv)) return sdpa_direct(dtype, q, k, v, mask, B, H, Sq, Skv, Dh, scale, out, st);
-    // Staging buffer in stream order: overlapping calls on different streams never share it.
-    const size_t bytes = sdpa_stage_bytes(B, H, Sq, Skv);
-    void* ws = nullptr;
-    IRO_HIP_CHECK(hipMallocAsync(&ws, bytes, st));
-    const int rc = sdpa_run_staged(dtype, q, k, v, mask, B, H, Sq, Skv, scale, out, ws, bytes, st);
-    const hipError_t fe = hipFreeAsync(ws, st);
-    if (rc != IRODORI_OK) return rc;
-    IRO_HIP_CHECK(fe);
-    return IRODORI_OK;
     IRO_GUARD_END
 }
 

@@ -29,6 +29,7 @@ DTYPE_F32 = 0
 DTYPE_BF16 = 1
 DTYPE_FP8 = 2
 DTYPE_F16 = 3  # irodori_op_sdpa operands only (native_fa_sdpa_f16_in)
+SDPA_SCRATCH_BYTES = 16 << 20  # IRODORI_SDPA_SCRATCH_BYTES
 CFG_INDEPENDENT, CFG_JOINT, CFG_ALTERNATING = 0, 1, 2
 METHOD_EULER, METHOD_HEUN, METHOD_PLMS4 = 0, 1, 2
 
@@ -171,6 +172,8 @@ SIGNATURES = {
                                          _vp, _vp]),
     "irodori_op_sdpa": (C.c_int, [C.c_int, _vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int,
                                   C.c_int, C.c_int, C.c_float, _vp, _vp]),
+    "irodori_op_sdpa_noalloc": (C.c_int, [C.c_int, _vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int,
+                                          C.c_int, C.c_int, C.c_float, _vp, _vp]),
     "irodori_op_mx_quantize": (C.c_int, [_vp, C.c_int, C.c_int, _vp, _vp, _vp]),
     "irodori_op_gemm_fp8": (C.c_int, [_vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int, _vp, _vp]),
 }

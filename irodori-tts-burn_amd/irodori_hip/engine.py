@@ -414,3 +414,11 @@ class ops:
              d_out, stream: int = 0) -> None:
         _check(L.load().irodori_op_sdpa(dtype, d_q, d_k, d_v, d_mask or None, batch, heads, seq_q,
                                         seq_kv, head_dim, scale, d_out, stream or None))
+
+    @staticmethod
+    def sdpa_noalloc(dtype: int, d_q, d_k, d_v, d_mask, batch, heads, seq_q, seq_kv, head_dim, scale,
+                     d_out, stream: int = 0) -> None:
+        """sdpa without any device allocation: the staging lives in the library's fixed
+        per-GPU buffer (SDPA_SCRATCH_BYTES); overlapping calls on one GPU race."""
+        _check(L.load().irodori_op_sdpa_noalloc(dtype, d_q, d_k, d_v, d_mask or None, batch, heads, seq_q,
+                                                seq_kv, head_dim, scale, d_out, stream or None))
