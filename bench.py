@@ -145,8 +145,9 @@ def main():
     ap.add_argument("--profile-iters", type=int, default=50)
     ap.add_argument("--cfg5-dtype", choices=["fp8", "bf16"], default="fp8",
                     help="compute mode of --workload cfg5 (config 5 names fp8 weights)")
-    ap.add_argument("--workload", choices=["cfg4", "cfg5", "encode", "codec"], default="cfg4",
-                    help="cfg4 (default): the headline B=2 Joint-CFG RF run; cfg5: batched "
+    ap.add_argument("--workload", choices=["cfg4", "cfg2", "cfg3", "cfg5", "encode", "codec"], default="cfg4",
+                    help="cfg4 (default): the headline B=2 Joint-CFG RF run; cfg2: the isolated joint "
+                         "attention operator; cfg3: the isolated SwiGLU MLP half of a block; cfg5: batched "
                          "throughput, 16 utterances x 2 CFG rows, lengths U[200,750] padded; "
                          "encode: per-request conditioning; codec: DACVAE decode of config 4's "
                          "two 750-frame latents")
@@ -176,6 +177,9 @@ def main():
 
     if args.workload == "cfg5":
         print(json.dumps(run_cfg5(args, np, torch, ih)), flush=True)
+        return
+    if args.workload in ("cfg2", "cfg3"):
+        print(json.dumps(run_isolated(args, np, torch, ih)), flush=True)
         return
     if args.workload == "encode":
         print(json.dumps(run_encode(args, np, torch, ih)), flush=True)
@@ -300,6 +304,90 @@ def main():
     }
     eng.close()
     print(json.dumps(rec), flush=True)
+
+
+def time_on_stream(torch, fn, warmup, steps):
+    """Average ms per call of fn(stream_handle), HIP events on a default-priority torch stream
+    (the one the calls are enqueued on)."""
+    st = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    for _ in range(warmup):
+        fn(st.cuda_stream)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(steps):
+        fn(st.cuda_stream)
+    e1.record(st)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def run_isolated(args, np, torch, ih):
+    """The block's hot kernels alone at the isolated-kernel configurations, on a one-layer
+    d1024 context (bf16): cfg2 = irodori_op_joint_attention (B = 2, 16 x 64 heads, 750 latent
+    queries; keys 750 latent + 256 text (valid U[32, 256]) + 375 speaker; Q/K/V ~ N(0, 1); RoPE
+    on the latent keys; sigmoid gate), cfg3 = irodori_op_swiglu_mlp (1500 tokens = 2 x 750,
+    1024 -> 2816 -> 1024, weights N(0, 0.02), x ~ N(0, 1), shift / scale / gate ~ N(0, 0.1) per
+    row, eps 1e-6).  value = us per operator call, inputs resident in HBM."""
+    import dataclasses
+    cfg2 = args.workload == "cfg2"
+    cfg = dataclasses.replace(ih.cfg_full_rf(), num_layers=1, norm_eps=1e-5 if cfg2 else 1e-6)
+    B, S, H, Dh, D, F = 2, 750, cfg.num_heads, cfg.head_dim, cfg.model_dim, cfg.mlp_hidden
+    w = ih.DitWeights.random(cfg, 7 if cfg2 else 3, norm_jitter=0.1 if cfg2 else 0.0)
+    rng = np.random.default_rng(9 if cfg2 else 4)
+    Tt, Ts = 256, 375
+    eng = ih.HipInferenceEngine(cfg, ih.InferenceBackendKind.HIP_BF16, max_rows=B, max_seq=S,
+                                max_ctx=Tt + Ts if cfg2 else 1)
+    eng.load_weights(w)
+
+    def cuda(a):
+        return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to("cuda")
+
+    if cfg2:
+        ctx = ih.make_role_context(cfg, B, Tt, Ts, ["cond"], seed=8)
+        eng.set_context_kv(ctx)
+        q, k, v = (cuda(rng.standard_normal((B, S, H, Dh)).astype(np.float32)) for _ in range(3))
+        g = cuda(rng.standard_normal((B, S, H * Dh)).astype(np.float32))
+        out = torch.empty((B, S, H * Dh), dtype=torch.float32, device="cuda")
+        fn = lambda st: eng.joint_attention(0, B, S, q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(),
+                                            out.data_ptr(), st)
+        ms = time_on_stream(torch, fn, args.warmup, args.steps)
+        valid = int(ctx.mask.sum())
+        flops = 4.0 * B * H * S * (S + Tt + Ts) * Dh  # every key, as the workload counts them
+        useful = 4.0 * H * S * Dh * (B * S + valid)
+        kernel = "joint attention operator (staging + attn32 + f32 store), B=2 x 16 heads x 750 queries x 1381 keys"
+        metric = "isolated joint attention us per call (B=2, 16x64 heads, 750 q, 750+256+375 keys)"
+        extra = {"valid_context_keys": valid, "useful_tflops": round(useful / (ms * 1e-3) / 1e12, 1)}
+        algo_bytes = 2 * B * H * Dh * 4 * (3 * S) + B * S * H * Dh * 4 * 2  # q,k,v,gate in, out (f32)
+    else:
+        x = cuda(rng.standard_normal((B, S, D)).astype(np.float32))
+        shift, scale, gate = (cuda((0.1 * rng.standard_normal((B, D))).astype(np.float32)) for _ in range(3))
+        fn = lambda st: eng.swiglu_mlp(0, B, S, x.data_ptr(), shift.data_ptr(), scale.data_ptr(), gate.data_ptr(),
+                                       st)
+        ms = time_on_stream(torch, fn, args.warmup, args.steps)
+        flops = 2.0 * B * S * D * 2 * F + 2.0 * B * S * F * D
+        kernel = "SwiGLU MLP half (fused adaLN operand + W1|W3 + W2 gated residual, one launch set per row)"
+        metric = "isolated SwiGLU MLP + adaLN us per call (1500 tokens, 1024 -> 2816 -> 1024)"
+        extra = {}
+        algo_bytes = 2 * (2 * F * D + F * D) + B * S * D * 4 * 2 + B * S * D * 2  # weights, x r/w, h
+    eng.close()
+    achieved = flops / (ms * 1e-3) / 1e12
+    log("%s: %.2f us per call, %.1f TFLOP/s" % (args.workload, ms * 1e3, achieved))
+    rec = {
+        "metric": metric, "value": round(ms * 1e3, 2), "unit": "us", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: seeded N(0,1) activations, N(0,0.02) weights" + (
+            ", N(0,1) context K/V" if cfg2 else ", N(0,0.1) modulation vectors"),
+        "config": {"workload": metric, "global_batch": B, "seq_len": S, "parallelism": "none"},
+        "roofline": {"kernel": kernel, "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "algorithmic_bytes": int(algo_bytes)},
+        "cpu_baseline": None,
+    }
+    rec.update(extra)
+    return rec
 
 
 def run_cfg5(args, np, torch, ih):

@@ -243,6 +243,36 @@ int irodori_sample_device_masked(irodori_ctx* ctx, const irodori_sampler_params*
                                  int utterances, int seq, const int32_t* lengths,
                                  const float* d_x0, float* d_x_out);
 
+/* ---- isolated block operators on a loaded context --------------------------------------
+ * The block's hot kernels alone, on the context's weights of `layer` (loaded in the kernels'
+ * layouts), with device pointers, enqueued on `stream` (NULL: the context's stream) without
+ * waiting.  They use the context's work buffers: calls that overlap with each other or with
+ * a forward / sampling call on the same context race. */
+
+/* attention_after_qkv (attention.rs:328-425) of one block: the latent projections q, k, v
+ * [batch, seq, H, 64] f32 (before the head norms), head-normed with the layer's q_norm /
+ * k_norm, half-RoPE'd at latent positions 0..seq-1 (rope.rs:119-135), joined with the
+ * layer's cached context keys / values / mask of rows 0..batch-1 (irodori_set_ctx_kv or
+ * irodori_build_ctx_kv; the keys are normed, not rotated), SDPA (attention.rs:619-664; a
+ * row with no valid key gives 0), then sigmoid(gate) times the output (gate: logits
+ * [batch, seq, H*64] f32, nullable = 1, attention.rs:423).  out [batch, seq, H*64] f32.
+ * Runs the model's attention kernel on the layouts its QKV+gate epilogue writes.  bf16 or
+ * f32 contexts. */
+int irodori_op_joint_attention(irodori_ctx* ctx, int layer, int batch, int seq, const float* q,
+                               const float* k, const float* v, const float* gate, float* out,
+                               void* stream);
+
+/* The MLP half of DiffusionBlock::forward_fused (diffusion.rs:101-104) of one block:
+ * x += gate * SwiGlu(x / rms(x) * (1 + scale) + shift) (norm.rs:160-169,
+ * feed_forward.rs:76-85), with the caller's modulation vectors shift / scale / gate
+ * [batch, D] f32 (gate as applied, after tanh) and the context's norm_eps; x [batch, seq, D]
+ * f32, updated in place.  bf16 contexts with the fused adaLN run each row as a sampler
+ * chain does (the norm folded into the W1|W3 GEMM); otherwise the adaLN kernel, W1|W3 and W2
+ * over all rows.  Overwrites the context's modulation table rows 0..batch-1 of (layer,
+ * mlp), which the next forward or sampling call rebuilds. */
+int irodori_op_swiglu_mlp(irodori_ctx* ctx, int layer, int batch, int seq, float* x,
+                          const float* shift, const float* scale, const float* gate, void* stream);
+
 /* Average device time of each kernel of one DiT block over `batch` rows of `seq` frames,
  * launched as one sampler role chain launches them (every row on the same timestep's
  * modulation vector; batch = 1 is one CFG row of a Joint-CFG step), measured with HIP

@@ -354,13 +354,21 @@ enum LayerPart {
     PART_COUNT = 7
 };
 
+// Options of one block part: the residual stream in a caller buffer instead of the
+// context's (already offset to the slice's first row), and no next-norm operand from the
+// W2 epilogue (an isolated MLP half).
+struct PartOpts {
+    float* x = nullptr;
+    bool no_next = false;
+};
+
 // One kernel of a DiT block over batch rows [r0, r0 + B) of the context's buffers, on
 // stream st.  Every row-indexed buffer is offset to row r0; mt must map the slice's local
 // row b to the vector of global row r0 + b (rows_per_vec == 1 with the table offset, or
 // all rows sharing one vector).
 template <typename T>
 int enqueue_part(irodori_ctx* c, int l, int B, int S, const ModTable& mt, int part, int r0,
-                 hipStream_t st) {
+                 hipStream_t st, const PartOpts& opt = PartOpts()) {
     const auto& g = c->cfg;
     const int D = g.model_dim, H = g.num_heads, F = g.mlp_hidden, M = B * S, Dh = g.head_dim;
     const bool last = l + 1 == g.num_layers;
@@ -368,7 +376,7 @@ int enqueue_part(irodori_ctx* c, int l, int B, int S, const ModTable& mt, int pa
     const int vt_stride = (S + 63) / 64 * 64;
     const size_t tok0 = (size_t)r0 * S;  // first token row of the slice
     T* h = static_cast<T*>(c->h) + tok0 * D;
-    float* x = c->x + tok0 * D;
+    float* x = opt.x ? opt.x : c->x + tok0 * D;
     T* q = static_cast<T*>(c->q) + (size_t)r0 * H * S * Dh;
     T* ks = static_cast<T*>(c->ks) + (size_t)r0 * H * S * Dh;
     T* vs = static_cast<T*>(c->vs) + (size_t)r0 * H * Dh * vt_stride;
@@ -528,7 +536,7 @@ int enqueue_part(irodori_ctx* c, int l, int B, int S, const ModTable& mt, int pa
             ga.N = D;
             ga.K = F;
             ga.kind = 1;
-            if (fz && !last) {  // and the next block's attention adaLN operand
+            if (fz && !last && !opt.no_next) {  // and the next block's attention adaLN operand
                 ga.Hn = h;
                 ga.rstat_out = rstat;
                 ga.next_layer = l + 1;
@@ -542,7 +550,7 @@ int enqueue_part(irodori_ctx* c, int l, int B, int S, const ModTable& mt, int pa
         }
         case PART_NORM_NEXT: {
             // Next block's attention adaLN (fused into W2 / QKVG with the fused adaLN).
-            if (!last && !fz) {
+            if (!last && !fz && !opt.no_next) {
                 launch_norm_mod<T>(x, f8 ? nullptr : h, M, S, D, g.norm_eps, mt, l + 1, 0, st, h8, h8s);
             }
             break;
@@ -711,6 +719,10 @@ int validate_params(const irodori_sampler_params* p) {
                 "sampler PLMS4 is not compatible with cfg_guidance_mode=Alternating; use Independent or "
                 "Joint instead");
     IRO_REQUIRE(p->method >= 0 && p->method <= 2, IRODORI_ERR_CONFIG, "unknown sampler method");
+    // The condition's auxiliary state is a speaker or a caption, never both
+    // (AuxConditioner, aux_conditioner.rs:43-52).
+    IRO_REQUIRE(!(p->has_speaker && p->has_caption), IRODORI_ERR_CONFIG,
+                "has_speaker and has_caption are exclusive: the auxiliary condition is a speaker or a caption");
     IRO_REQUIRE(p->cfg_mode >= 0 && p->cfg_mode <= 2, IRODORI_ERR_CONFIG, "unknown cfg guidance mode");
     if (p->has_temporal_rescale) {
         IRO_REQUIRE(std::isfinite(p->rescale_k), IRODORI_ERR_CONFIG, "temporal_rescale.k must be finite");
@@ -1626,6 +1638,104 @@ static int sample_host(irodori_ctx* c, const irodori_sampler_params* p, int U, i
     if (rc != IRODORI_OK) return rc;
     IRO_HIP_CHECK(hipMemcpy(x_out, c->xin, sizeof(float) * n, hipMemcpyDeviceToHost));
     return IRODORI_OK;
+    IRO_GUARD_END
+}
+
+// ---- isolated block operators (the model's kernels on a loaded context) -----------------
+
+int irodori_op_joint_attention(irodori_ctx* c, int layer, int B, int S, const float* q, const float* k,
+                               const float* v, const float* gate, float* out, void* stream) {
+    IRO_GUARD_BEGIN
+    IRO_REQUIRE(c && q && k && v && out, IRODORI_ERR_INVALID_ARG, "null argument");
+    const auto& g = c->cfg;
+    IRO_REQUIRE(layer >= 0 && layer < g.num_layers, IRODORI_ERR_INVALID_ARG, "layer index out of range");
+    IRO_REQUIRE(B > 0 && B <= g.max_rows && S > 0 && S <= g.max_seq, IRODORI_ERR_SHAPE,
+                "batch must be in [1, max_rows], seq in [1, max_seq]");
+    IRO_REQUIRE(!c->fp8, IRODORI_ERR_DTYPE, "the joint attention operator runs bf16 or f32 contexts");
+    IRO_REQUIRE(c->layers[layer].loaded, IRODORI_ERR_NOT_LOADED, "block weights of the layer not loaded");
+    if (c->t_ctx > 0)
+        for (int r = 0; r < B; r++)
+            IRO_REQUIRE(c->layers[layer].row_set[r], IRODORI_ERR_NOT_LOADED,
+                        "context KV of row " + std::to_string(r) + " not set");
+    IRO_HIP_CHECK(hipSetDevice(c->device));
+    hipStream_t st = stream ? static_cast<hipStream_t>(stream) : c->stream;
+    const int H = g.num_heads, D = g.model_dim, vt = (S + 63) / 64 * 64;
+    const float q_scale = 1.4426950408889634f / sqrtf((float)g.head_dim);
+    auto& lb = c->layers[layer];
+    ModTable mt{c->tab, c->zero_step, 0, B, g.num_layers};  // not read by the attention
+    if (c->bf16) {
+        launch_attn_op_stage<bf16>(q, k, v, gate, lb.q_norm, lb.k_norm, c->rope_cos, c->rope_sin, B, S, H, g.norm_eps,
+                                   q_scale, vt, static_cast<bf16*>(c->q), static_cast<bf16*>(c->ks),
+                                   static_cast<bf16*>(c->vs), static_cast<bf16*>(c->gate), st);
+        IRO_TRY(enqueue_part<bf16>(c, layer, B, S, mt, PART_ATTN, 0, st));
+        launch_to_f32<bf16>(static_cast<const bf16*>(c->o), (long)B * S * D, out, st);
+    } else {
+        launch_attn_op_stage<float>(q, k, v, gate, lb.q_norm, lb.k_norm, c->rope_cos, c->rope_sin, B, S, H,
+                                    g.norm_eps, q_scale, vt, static_cast<float*>(c->q), static_cast<float*>(c->ks),
+                                    static_cast<float*>(c->vs), static_cast<float*>(c->gate), st);
+        IRO_TRY(enqueue_part<float>(c, layer, B, S, mt, PART_ATTN, 0, st));
+        launch_to_f32<float>(static_cast<const float*>(c->o), (long)B * S * D, out, st);
+    }
+    return check_launch("joint attention operator");
+    IRO_GUARD_END
+}
+
+int irodori_op_swiglu_mlp(irodori_ctx* c, int layer, int B, int S, float* x, const float* shift, const float* scale,
+                          const float* gate, void* stream) {
+    IRO_GUARD_BEGIN
+    IRO_REQUIRE(c && x && shift && scale && gate, IRODORI_ERR_INVALID_ARG, "null argument");
+    const auto& g = c->cfg;
+    IRO_REQUIRE(layer >= 0 && layer < g.num_layers, IRODORI_ERR_INVALID_ARG, "layer index out of range");
+    IRO_REQUIRE(B > 0 && B <= g.max_rows && S > 0 && S <= g.max_seq, IRODORI_ERR_SHAPE,
+                "batch must be in [1, max_rows], seq in [1, max_seq]");
+    IRO_REQUIRE(c->layers[layer].loaded, IRODORI_ERR_NOT_LOADED, "block weights of the layer not loaded");
+    IRO_HIP_CHECK(hipSetDevice(c->device));
+    const int D = g.model_dim, L = g.num_layers;
+    IRO_TRY(ensure_nvec(c, B));
+    hipStream_t st = stream ? static_cast<hipStream_t>(stream) : c->stream;
+    // The caller's vectors in table rows 0..B-1 of (layer, mlp); the table is rebuilt by
+    // the next forward or sampling call.
+    launch_put_mod_vectors(shift, scale, gate, B, D, L, layer, 1, c->tab, st);
+    PartOpts opt;
+    opt.no_next = true;
+    const ModTable one{c->tab, c->zero_step, 0, 1, L};
+    if (c->bf16 && fused_for(c, one, 1)) {
+        // The sampler chain's form, one batch row per launch (each on its own vector): the
+        // operand x (1 + scale) and the row sums, then W1|W3 with the norm folded in and W2
+        // with the gated residual.
+        const int cap = c->nvec_cap, F = g.mlp_hidden;
+        bf16* stage = static_cast<bf16*>(c->shift_stage);
+        launch_shift_stage(c->tab, B, cap, L, D, stage, st);
+        GemmArgs<bf16> ga{};
+        ga.A = stage + (size_t)(layer * 2 + 1) * cap * D;
+        ga.W = static_cast<const bf16*>(c->layers[layer].w13);
+        ga.M = B;
+        ga.N = 2 * F;
+        ga.K = D;
+        ga.S = B;
+        ga.C = c->bias13 + (size_t)layer * cap * 2 * F;
+        IRO_REQUIRE(launch_gemm<bf16>(EPI_STORE, ga, st) == 0, IRODORI_ERR_SHAPE, "shift bias gemm shape");
+        for (int b = 0; b < B; b++) {
+            ModTable mt{c->tab, c->zero_step, 0, 1, L, 0, b};
+            const size_t tok0 = (size_t)b * S;
+            opt.x = x + tok0 * D;
+            launch_mod_stats<bf16>(opt.x, static_cast<bf16*>(c->h) + tok0 * D, S, S, D, mt, layer, 1,
+                                   c->rstat + tok0 * (D / 32), st);
+            IRO_TRY(enqueue_part<bf16>(c, layer, 1, S, mt, PART_W13, b, st, opt));
+            IRO_TRY(enqueue_part<bf16>(c, layer, 1, S, mt, PART_W2, b, st, opt));
+        }
+    } else {
+        // All rows in one launch set, each row on its own vector (rows_per_vec 1): the adaLN
+        // kernel, W1|W3 with the SwiGLU epilogue, W2 with the gated residual.
+        opt.x = x;
+        for (int part : {PART_NORM_MLP, PART_W13, PART_W2}) {
+            if (c->bf16)
+                IRO_TRY(enqueue_part<bf16>(c, layer, B, S, one, part, 0, st, opt));
+            else
+                IRO_TRY(enqueue_part<float>(c, layer, B, S, one, part, 0, st, opt));
+        }
+    }
+    return check_launch("swiglu mlp operator");
     IRO_GUARD_END
 }
 

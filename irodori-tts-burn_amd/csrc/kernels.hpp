@@ -18,9 +18,10 @@ struct ModTable {
     int rows_per_vec;  // batch rows sharing one vector
     int layers;
     int step_add = 0;  // evaluation offset (1: the Heun corrector at t_{i+1})
+    int vec_base = 0;  // first vector (a launch over one batch row of a multi-row table)
 };
 __host__ __device__ inline int mod_vec_index(const ModTable& mt, int step, int b) {
-    return (step + mt.step_add) * mt.step_stride + b / mt.rows_per_vec;
+    return (step + mt.step_add) * mt.step_stride + b / mt.rows_per_vec + mt.vec_base;
 }
 
 // Position of latent/context key s inside a V^T row.  bf16 path (32x32x16 attention):
@@ -157,6 +158,24 @@ void launch_scale_ctx_aux(const T* src_k, const T* src_v, T* dst_k, T* dst_v, in
                           float factor, hipStream_t st);
 void launch_step_advance(int* step, hipStream_t st);
 void launch_scale_copy(const float* src, float* dst, int n, float s, hipStream_t st);
+
+// ---- kernels_ops.hip -------------------------------------------------------------------
+// The joint-attention operator's staging: latent q, k, v [B, S, H, 64] f32 and gate logits
+// [B, S, H*64] f32 (nullable: gate 1) into the layouts the QKV+gate epilogue writes -- Q
+// [B, H, S, 64] head-normed (q_norm / k_norm [H, 64], nullable: no norm), half-RoPE'd
+// (heads < H/2, tables [S, 32]) and pre-scaled by q_scale; K likewise without the scale;
+// V^T [B, H, 64, vt_stride] at vt_pos_bf16 (T = bf16) / vt_pos_f32 (T = float); G =
+// sigmoid(gate).
+template <typename T>
+void launch_attn_op_stage(const float* q, const float* k, const float* v, const float* gate, const float* q_norm,
+                          const float* k_norm, const float* rope_cos, const float* rope_sin, int B, int S, int H,
+                          float eps, float q_scale, int vt_stride, T* Q, T* K, T* Vt, T* G, hipStream_t st);
+template <typename T>
+void launch_to_f32(const T* src, long n, float* dst, hipStream_t st);
+// Modulation vectors [B, D] (shift, scale, gate as applied) into table rows vec b, (layer,
+// kind) of tab [vec][layer][2][3][D].
+void launch_put_mod_vectors(const float* shift, const float* scale, const float* gate, int B, int D, int layers,
+                            int layer, int kind, float* tab, hipStream_t st);
 
 // ---- kernels_cond.hip ------------------------------------------------------------------
 struct VecLinJob {

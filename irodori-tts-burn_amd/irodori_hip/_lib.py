@@ -174,6 +174,8 @@ SIGNATURES = {
                                   C.c_int, C.c_int, C.c_float, _vp, _vp]),
     "irodori_op_sdpa_noalloc": (C.c_int, [C.c_int, _vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int,
                                           C.c_int, C.c_int, C.c_float, _vp, _vp]),
+    "irodori_op_joint_attention": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "irodori_op_swiglu_mlp": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp, _vp, _vp]),
     "irodori_op_mx_quantize": (C.c_int, [_vp, C.c_int, C.c_int, _vp, _vp, _vp]),
     "irodori_op_gemm_fp8": (C.c_int, [_vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int, _vp, _vp]),
 }

@@ -257,6 +257,10 @@ class SamplerParams:
                 raise IrodoriError("Config", "speaker_kv.scale must be finite and > 0")
             if skv.min_t is not None and not (math.isfinite(skv.min_t) and 0.0 <= skv.min_t <= 1.0):
                 raise IrodoriError("Config", "speaker_kv.min_t must be finite and in [0, 1]")
+        if has_speaker and has_caption:
+            # AuxConditioner is a speaker or a caption conditioner (aux_conditioner.rs:43-52).
+            raise IrodoriError("Config", "has_speaker and has_caption are exclusive: the auxiliary "
+                                         "condition is a speaker or a caption")
         if self.method is SamplerMethod.PLMS4 and g.mode is CfgGuidanceMode.ALTERNATING:
             raise IrodoriError("Config", "sampler PLMS4 is not compatible with "
                                          "cfg_guidance_mode=Alternating; use Independent or Joint instead")

@@ -240,6 +240,21 @@ class HipInferenceEngine:
             C.c_void_p(d_x0), C.c_void_p(d_out)))
 
 
+    def joint_attention(self, layer: int, batch: int, seq: int, d_q: int, d_k: int, d_v: int, d_gate: int,
+                        d_out: int, stream: int = 0) -> None:
+        """irodori_op_joint_attention on device pointers: q, k, v [batch, seq, H, 64] f32, gate
+        logits [batch, seq, H*64] (0: none) -> out [batch, seq, H*64] f32, with this layer's head
+        norms and cached context of rows 0..batch-1."""
+        _check(self.lib.irodori_op_joint_attention(self.ctx, layer, batch, seq, d_q, d_k, d_v, d_gate or None,
+                                                   d_out, stream or None))
+
+    def swiglu_mlp(self, layer: int, batch: int, seq: int, d_x: int, d_shift: int, d_scale: int, d_gate: int,
+                   stream: int = 0) -> None:
+        """irodori_op_swiglu_mlp on device pointers: x [batch, seq, D] f32 += gate * SwiGLU(adaLN(x))
+        with modulation vectors [batch, D] f32."""
+        _check(self.lib.irodori_op_swiglu_mlp(self.ctx, layer, batch, seq, d_x, d_shift, d_scale, d_gate,
+                                              stream or None))
+
     def profile_layer(self, batch: int, seq: int, iters: int = 20) -> dict:
         """Average microseconds per kernel of one block (HIP events on the context stream)."""
         kt = L.KernelTimesC()

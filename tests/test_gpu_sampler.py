@@ -28,7 +28,7 @@ def params(mode, method, steps=4, scale_text=2.0, scale_speaker=3.0, min_t=0.0, 
     return ih.SamplerParams(num_steps=steps, method=method, guidance=g, **kw)
 
 
-def orc_params(p, has_speaker=True, aux_start=TT):
+def orc_params(p, has_speaker=True, aux_start=TT, has_caption=False):
     g = p.guidance
     tr, skv = p.temporal_rescale, p.speaker_kv
     return sampler_struct(
@@ -36,7 +36,7 @@ def orc_params(p, has_speaker=True, aux_start=TT):
         cfg_mode={M.INDEPENDENT: 0, M.JOINT: 1, M.ALTERNATING: 2}[g.mode],
         scale_text=g.scale_text, scale_caption=g.scale_caption, scale_speaker=g.scale_speaker,
         min_t=g.min_t, max_t=g.max_t, has_truncation=int(p.truncation_factor is not None),
-        truncation_factor=p.truncation_factor or 1.0, has_speaker=int(has_speaker), has_caption=0,
+        truncation_factor=p.truncation_factor or 1.0, has_speaker=int(has_speaker), has_caption=int(has_caption),
         has_temporal_rescale=int(tr is not None), rescale_k=tr.k if tr else 1.0,
         rescale_sigma=tr.sigma if tr else 1.0, has_speaker_kv=int(skv is not None),
         speaker_kv_scale=skv.scale if skv else 1.0,
@@ -132,3 +132,32 @@ def test_heun_rescale_reaches_t_zero_as_the_reference(oracle64, model):
     p = params(M.JOINT, SM.HEUN, steps=3, temporal_rescale=ih.config.TemporalRescaleConfig(k=2.0, sigma=0.8))
     got, _, ref = run(oracle64, model, F32, p)
     assert np.isnan(ref).all() and np.isnan(got).all()
+
+
+# ---- caption-conditioned CFG (euler_sampler.rs:186-195, :205, :314-321, :490) -------------
+@pytest.mark.parametrize("backend", [F32, BF16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("mode,method", [(M.INDEPENDENT, SM.EULER), (M.ALTERNATING, SM.HEUN), (M.JOINT, SM.PLMS4)],
+                         ids=["indep-euler", "alt-heun", "joint-plms4"])
+def test_caption_cfg_matches_oracle(oracle64, model, backend, mode, method):
+    # A caption model: the aux segment holds caption keys, has_caption = 1, has_speaker = 0;
+    # the caption signal follows text and takes scale_caption (the speaker scale is ignored).
+    cfg, w = model
+    s_cap = 2.0 if mode is M.JOINT else 3.5
+    g = ih.GuidanceConfig(mode=mode, scale_text=2.0, scale_caption=s_cap, scale_speaker=9.0,
+                          min_t=0.0, max_t=1.0)
+    p = ih.SamplerParams(num_steps=4, method=method, guidance=g)
+    roles = p.cfg_roles(has_speaker=False, has_caption=True)
+    assert roles == (["cond", "uncond"] if mode is M.JOINT else ["cond", "no_text", "no_aux"])
+    ctx = ih.make_role_context(cfg, 1, TT, TA, roles, seed=13)
+    x0 = ih.make_noise(1, S, cfg.latent_dim, 14)
+    with ih.HipInferenceEngine(cfg, backend, max_rows=len(roles), max_seq=S, max_ctx=ctx.t_ctx) as e:
+        e.load_weights(w)
+        e.set_context_kv(ctx)
+        got = e.sample(x0, p, has_speaker=False, has_caption=True, ctx_aux_start=TT)
+        with pytest.raises(ih.IrodoriError, match="exclusive"):
+            e.sample(x0, p, has_speaker=True, has_caption=True, ctx_aux_start=TT)
+    ref, _ = oracle64.sample_rf(cfg, w, x0, (ctx.k, ctx.v, ctx.mask),
+                                orc_params(p, has_speaker=False, has_caption=True))
+    err = rel_l2(got, ref)
+    print(mode, method, backend.value, "caption CFG rel L2 %.2e" % err)
+    assert err < TOL[backend]

@@ -263,3 +263,72 @@ def test_speaker_kv_reverts_below_min_t(orc, model):
         vu = _fwd(orc, cfg, w, x, t[i], c, 1, 1)
         x = x + (vc + (vc - vu) * 2.0) * (t[i + 1] - t[i])
     assert rel(got, x) < 1e-6
+
+
+# ---- caption-conditioned CFG (euler_sampler.rs:186-195, :205, :314-321, :490) ----------------
+# A caption model's aux segment holds the caption keys; its CFG signal comes last in the
+# order (text, speaker, caption), takes scale_caption, and dropping it zeroes the aux
+# segment like dropping a speaker (make_aux_uncond, euler_sampler.rs:59-82).  The speaker
+# scale is ignored there (cfg_scale_speaker = 0 without speaker conditioning, :162-166).
+
+def test_caption_independent_one_step(orc, model):
+    cfg, w = model
+    ctx = _ctx(cfg, ["cond", "no_text", "no_aux"])
+    x0 = ih.make_noise(1, 18, cfg.latent_dim, 17)
+    sp = sampler_struct(num_steps=2, cfg_mode=INDEP, scale_text=3.0, scale_caption=4.0, scale_speaker=9.0,
+                        has_speaker=0, has_caption=1, min_t=0.0, max_t=1.0)
+    got, _ = orc.sample_rf(cfg, w, x0, (ctx.k, ctx.v, ctx.mask), sp, max_steps_run=1)
+    t = _sched(2)
+    vc, v1, v2 = (_fwd(orc, cfg, w, x0, t[0], ctx, r, 1) for r in range(3))
+    v = vc + (vc - v1) * 3.0 + (vc - v2) * 4.0
+    assert rel(got, x0 + v * (t[1] - t[0])) < 1e-6
+
+
+def test_caption_alternating_drops_text_then_caption(orc, model):
+    cfg, w = model
+    ctx = _ctx(cfg, ["cond", "no_text", "no_aux"])
+    x0 = ih.make_noise(1, 18, cfg.latent_dim, 18)
+    sp = sampler_struct(num_steps=2, cfg_mode=ALT, scale_text=3.0, scale_caption=4.0, has_speaker=0,
+                        has_caption=1, min_t=0.0, max_t=1.0)
+    got, _ = orc.sample_rf(cfg, w, x0, (ctx.k, ctx.v, ctx.mask), sp)
+    t = _sched(2)
+    x = x0.astype(np.float64)
+    for i, (role, s) in enumerate([(1, 3.0), (2, 4.0)]):  # step 0 drops text, step 1 the caption
+        vc = _fwd(orc, cfg, w, x, t[i], ctx, 0, 1)
+        va = _fwd(orc, cfg, w, x, t[i], ctx, role, 1)
+        x = x + (vc + (vc - va) * s) * (t[i + 1] - t[i])
+    assert rel(got, x) < 1e-6
+
+
+def test_caption_joint_equals_speaker_joint(orc32, model):
+    # Joint mode with text + caption at one scale runs the same two roles as text + speaker.
+    cfg, w = model
+    ctx = _ctx(cfg, ["cond", "uncond"], 2)
+    x0 = ih.make_noise(2, 16, cfg.latent_dim, 19)
+    kw = dict(num_steps=3, cfg_mode=JOINT, scale_text=2.5, min_t=0.0, max_t=1.0)
+    cap, _ = orc32.sample_rf(cfg, w, x0, (ctx.k, ctx.v, ctx.mask),
+                             sampler_struct(scale_caption=2.5, scale_speaker=7.0, has_caption=1, **kw))
+    spk, _ = orc32.sample_rf(cfg, w, x0, (ctx.k, ctx.v, ctx.mask),
+                             sampler_struct(scale_speaker=2.5, has_speaker=1, **kw))
+    assert np.array_equal(cap, spk)
+
+
+def test_caption_without_valid_token_is_no_signal(orc32, model):
+    # has_caption = 0 (no caption token is valid, euler_sampler.rs:186-195): text guidance
+    # only, whatever scale_caption says.
+    cfg, w = model
+    ctx = ih.make_role_context(cfg, 1, TT, TA, ["cond", "no_text"], seed=20)
+    x0 = ih.make_noise(1, 16, cfg.latent_dim, 21)
+    kw = dict(num_steps=3, cfg_mode=INDEP, scale_text=2.0, min_t=0.0, max_t=1.0, has_speaker=0)
+    a, _ = orc32.sample_rf(cfg, w, x0, (ctx.k, ctx.v, ctx.mask),
+                           sampler_struct(scale_caption=4.0, has_caption=0, **kw))
+    b, _ = orc32.sample_rf(cfg, w, x0, (ctx.k, ctx.v, ctx.mask), sampler_struct(**kw))
+    assert np.array_equal(a, b)
+
+
+def test_speaker_and_caption_flags_are_exclusive():
+    g = ih.GuidanceConfig(mode=ih.CfgGuidanceMode.INDEPENDENT, scale_text=2.0, scale_caption=3.0)
+    p = ih.SamplerParams(num_steps=4, guidance=g)
+    with pytest.raises(ih.IrodoriError, match="exclusive"):
+        p.validate(has_speaker=True, has_caption=True)
+    p.validate(has_speaker=False, has_caption=True)
