@@ -142,15 +142,19 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--cpu-steps", type=int, default=6,
+                    help="Euler steps of the CPU oracle timed after one warm-up step (at least 2)")
     ap.add_argument("--profile-iters", type=int, default=50)
     ap.add_argument("--cfg5-dtype", choices=["fp8", "bf16"], default="fp8",
                     help="compute mode of --workload cfg5 (config 5 names fp8 weights)")
-    ap.add_argument("--workload", choices=["cfg4", "cfg2", "cfg3", "cfg5", "encode", "codec"], default="cfg4",
+    ap.add_argument("--workload", choices=["cfg4", "cfg2", "cfg3", "cfg5", "encode", "codec", "a6000"],
+                    default="cfg4",
                     help="cfg4 (default): the headline B=2 Joint-CFG RF run; cfg2: the isolated joint "
                          "attention operator; cfg3: the isolated SwiGLU MLP half of a block; cfg5: batched "
                          "throughput, 16 utterances x 2 CFG rows, lengths U[200,750] padded; "
                          "encode: per-request conditioning; codec: DACVAE decode of config 4's "
-                         "two 750-frame latents")
+                         "two 750-frame latents; a6000: the published RTX A6000 benchmark's "
+                         "request (500M-v2 shape, Independent CFG, encoders included) as context")
     ap.add_argument("--codec-dtype", choices=["bf16", "f32"], default="bf16",
                     help="compute mode of --workload codec")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -186,6 +190,9 @@ def main():
         return
     if args.workload == "codec":
         print(json.dumps(run_codec(args, np, torch, ih)), flush=True)
+        return
+    if args.workload == "a6000":
+        print(json.dumps(run_a6000(args, np, torch, ih)), flush=True)
         return
 
     cfg = ih.cfg_full_rf()
@@ -258,15 +265,23 @@ def main():
         if args.cpu_threads:
             set_threads(args.cpu_threads)
         c, u = ctx.rows([0]), ctx.rows([1])
-        log("timing the CPU oracle (f32, %d threads): 1 of 40 Euler steps" % get_threads())
+        orc = Oracle("f32")
+        K = max(2, args.cpu_steps)
+        log("timing the CPU oracle (f32, %d threads): 1 warm-up step, then %d of 40 Euler steps"
+            % (get_threads(), K))
+        orc.sample_joint_cfg(cfg, w, x0, (c.k, c.v, c.mask), (u.k, u.v, u.mask), N, SCALE, 0.0,
+                             1.0, max_steps_run=1)
         t0 = time.perf_counter()
-        Oracle("f32").sample_joint_cfg(cfg, w, x0, (c.k, c.v, c.mask), (u.k, u.v, u.mask), N,
-                                       SCALE, 0.0, 1.0, max_steps_run=1)
-        step_s = time.perf_counter() - t0
+        _, ran = orc.sample_joint_cfg(cfg, w, x0, (c.k, c.v, c.mask), (u.k, u.v, u.mask), N,
+                                      SCALE, 0.0, 1.0, max_steps_run=K)
+        total_s = time.perf_counter() - t0
+        assert ran == K, "oracle ran %d steps, expected %d" % (ran, K)
+        step_s = total_s / K
         cpu = {"value": round(step_s * N * 1e3, 1), "unit": "ms (extrapolated 40-step RF run)",
-               "cores": get_threads(), "kind": "port",
-               "sample": "1 of 40 Joint-CFG Euler steps at config 4 (cond + uncond forward, "
-                         "B=1 each, f32 C oracle, OpenMP), measured %.2f s, x40" % step_s}
+               "cores": get_threads(), "kind": "port", "cpu_model": cpu_model(),
+               "sample": "%d of 40 Joint-CFG Euler steps at config 4 (cond + uncond forward, B=1 "
+                         "each, f32 C oracle, OpenMP) after one untimed warm-up step: %.2f s, "
+                         "%.3f s per step, x40" % (K, total_s, step_s)}
         log("CPU oracle: %.2f s per step -> %.0f ms per RF run" % (step_s, step_s * N * 1e3))
 
     rec = {
@@ -304,6 +319,20 @@ def main():
     }
     eng.close()
     print(json.dumps(rec), flush=True)
+
+
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo) and logical CPU count."""
+    name = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    name = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return "%s (%d logical CPUs visible)" % (name, os.cpu_count() or 0)
 
 
 def time_on_stream(torch, fn, warmup, steps):
@@ -464,6 +493,103 @@ def run_cfg5(args, np, torch, ih):
                      "bound": "mfma", "achieved": round(achieved, 2), "peak": peak,
                      "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
                      "traffic": None},
+        "cpu_baseline": None,
+    }
+
+
+A6000_LIBTORCH_BF16_MS = 987.0  # docs/benchmarks/rtx-a6000.md:44 (RTX A6000, Rust/burn LibTorch bf16)
+
+
+def run_a6000(args, np, torch, ih):
+    """The reference's published full-inference benchmark request (bench_realmodel.rs:219-246,
+    docs/benchmarks/rtx-a6000.md:13-36) at the 500M-v2 shape: d 1280, 12 layers, 20 x 64 heads,
+    SwiGLU 3680; text and speaker encoders 1280 wide, 14 layers, 10 heads, SwiGLU 3328.  One
+    request = text encoder over 4 tokens + speaker encoder over 8 reference frames (+ the mean
+    token) + the context-KV build of the three Independent-CFG rows (conditioned, text dropped,
+    speaker dropped: the dropped signal's keys masked out, euler_sampler.rs:41-67) + 40 Euler
+    steps over 750 frames (text scale 3, speaker scale 5, CFG on the steps with t >= 0.5) + the
+    latent read back to the host, as the reference times sample_euler_rf_cfg and into_data.
+    The initial noise is made once and stays resident.  Random-init weights (no checkpoint)."""
+    cfg = ih.cfg_published_500m()
+    te, se = ih.enc_text_default(), ih.enc_speaker_default(cfg.latent_dim)
+    te.vocab_size = 4096  # the embedding table's size does not change the work per token
+    Tt, Tr, S, N = 4, 8, 750, 40
+    log("a6000: generating random-init weights (DiT 12 x d1280; encoders 14 x 1280 each)")
+    w = ih.DitWeights.random(cfg, 0)
+    tw, sw = ih.EncoderWeights.random(te, 1), ih.EncoderWeights.random(se, 2)
+    proj = ih.CtxProjWeights.random(cfg, te.dim, se.dim, seed=3)
+    g = ih.GuidanceConfig(mode=ih.CfgGuidanceMode.INDEPENDENT, scale_text=3.0, scale_speaker=5.0,
+                          min_t=0.5, max_t=1.0)
+    params = ih.SamplerParams(num_steps=N, guidance=g)
+    roles = params.cfg_roles(has_speaker=True)
+    assert roles == ["cond", "no_text", "no_aux"]
+    ids = np.zeros((1, Tt), np.int32)  # the reference's request: token ids 0, reference latent 0
+    lat = np.zeros((1, Tr, se.in_dim), np.float32)
+    tm, rm = np.ones((1, Tt), np.uint8), np.ones((1, Tr), np.uint8)
+    tenc = ih.HipEncoder(te, ih.InferenceBackendKind.HIP_BF16, max_rows=1, max_seq=Tt)
+    senc = ih.HipEncoder(se, ih.InferenceBackendKind.HIP_BF16, max_rows=1, max_seq=Tr)
+    tenc.load_weights(tw)
+    senc.load_weights(sw)
+    eng = ih.HipInferenceEngine(cfg, ih.InferenceBackendKind.HIP_BF16, max_rows=len(roles), max_seq=S,
+                                max_ctx=Tt + Tr + 1)
+    eng.load_weights(w)
+    eng.load_ctx_proj_weights(proj)
+    del w, tw, sw, proj
+    d_x0 = torch.from_numpy(ih.make_noise(1, S, cfg.latent_dim, 2)).to("cuda")
+    d_out = torch.empty_like(d_x0)
+    torch.cuda.synchronize()
+
+    def request():
+        ts, tmo = tenc.forward(tm, ids=ids)
+        ss, smo = senc.forward(rm, latent=lat)
+        none_t, none_s = np.zeros_like(tmo[0]), np.zeros_like(smo[0])
+        eng.build_context_kv(0, ts[0], tmo[0], ss[0], smo[0])       # conditioned
+        eng.build_context_kv(1, ts[0], none_t, ss[0], smo[0])       # text dropped
+        eng.build_context_kv(2, ts[0], tmo[0], ss[0], none_s)       # speaker dropped
+        eng.sample_device(d_x0.data_ptr(), d_out.data_ptr(), 1, S, params, has_speaker=True,
+                          ctx_aux_start=Tt)
+        return d_out.cpu().numpy()
+
+    for _ in range(max(args.warmup, 2)):
+        request()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(args.steps):
+        t0 = time.perf_counter()
+        out = request()
+        times.append((time.perf_counter() - t0) * 1e3)
+    assert np.all(np.isfinite(out)), "non-finite sampler output"
+    ms = float(np.mean(times))
+    log("a6000 request: mean %.2f ms, p50 %.2f ms, min %.2f ms" % (ms, float(np.median(times)), min(times)))
+    kt = eng.profile_layer(1, S, args.profile_iters)
+    log("kernel us (M=750): " + ", ".join("%s=%.1f" % (k, v) for k, v in kt.items()))
+    tenc.close()
+    senc.close()
+    eng.close()
+    M, D, F = S, cfg.model_dim, cfg.mlp_hidden
+    w13_flops = 2.0 * M * D * 2 * F
+    achieved = w13_flops / (kt["w13_gemm_us"] * 1e-6) / 1e12
+    return {
+        "metric": "full-inference request ms at the published 500M-v2 shape (RTX A6000 benchmark "
+                  "configuration; context, not the headline)",
+        "value": round(ms, 3), "unit": "ms", "n_gpus": 1, "steps": args.steps,
+        "warmup": max(args.warmup, 2), "ms_per_step": round(ms, 3), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": round(ms / A6000_LIBTORCH_BF16_MS, 4),
+        "vs_baseline_note": "value / 987 ms, the reference's Rust/burn LibTorch bf16 mean on an RTX "
+                            "A6000 (docs/benchmarks/rtx-a6000.md:44): other hardware, published",
+        "dtype": "bf16",
+        "data": "synthetic: random-init DiT, encoders and context projections (N(0,0.02)); token ids 0, "
+                "reference latent 0 (as the reference's request); N(0,1) initial noise",
+        "config": {"workload": "500M-v2 shape (d1280, 12 layers, 20x64 heads, SwiGLU 3680 padded to 3712, "
+                               "latent 32); text encoder 4 tokens + speaker encoder 8 frames (+mean "
+                               "token); Independent CFG 3 rows (text 3, speaker 5, min_t 0.5); 750 "
+                               "frames; 40 Euler steps; latent read back",
+                   "global_batch": 1, "seq_len": S, "rf_steps": N, "parallelism": "none"},
+        "p50_ms": round(float(np.median(times)), 3), "min_ms": round(min(times), 3),
+        "kernel_us": {k: round(v, 2) for k, v in kt.items()},
+        "roofline": {"kernel": "w13_gemm (SwiGLU up-projection, 750x1280x7424)", "bound": "mfma",
+                     "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None},
         "cpu_baseline": None,
     }
 

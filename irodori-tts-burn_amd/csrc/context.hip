@@ -14,6 +14,7 @@
 #include <math.h>
 #include <string.h>
 
+#include <algorithm>
 #include <map>
 #include <memory>
 #include <new>
@@ -84,6 +85,10 @@ struct GraphKey {
 struct irodori_ctx {
     int device = 0;
     irodori_dit_config cfg{};
+    // SwiGLU hidden width on the device: mlp_hidden rounded up to 128 (whole GEMM tiles and
+    // K slices).  The padding columns of W1 / W3 and rows of W2 are zero, so the padded
+    // products are silu(0) * 0 = 0 and add nothing.
+    int Fp = 0;
     bool bf16 = true;
     bool fp8 = false;  // block GEMMs on e4m3 operands (activations and attention stay bf16)
     size_t esz = 2;    // compute element size
@@ -259,7 +264,7 @@ int ensure_nvec(irodori_ctx* c, int nvec) {
     IRO_TRY(dalloc(c, &c->tab, sizeof(float) * (size_t)cap * L * 6 * D));
     if (c->fused) {
         IRO_TRY(dalloc(c, &c->biasq, sizeof(float) * (size_t)L * cap * 4 * D));
-        IRO_TRY(dalloc(c, &c->bias13, sizeof(float) * (size_t)L * cap * 2 * g.mlp_hidden));
+        IRO_TRY(dalloc(c, &c->bias13, sizeof(float) * (size_t)L * cap * 2 * c->Fp));
         IRO_TRY(dev_alloc(c, &c->shift_stage, sizeof(bf16) * (size_t)2 * L * cap * D));
     }
     c->nvec_cap = cap;
@@ -312,7 +317,7 @@ int enqueue_mod_table(irodori_ctx* c, int nvec, bool skip_mlp, int l0 = 0, int l
     launch_vec_linear(c->d_jobs_down, L * 6, nvec, r, c->stream);
     launch_vec_linear(c->d_jobs_up, L * 6, nvec, D, c->stream);
     if (c->fused) {
-        const int cap = c->nvec_cap, F = g.mlp_hidden;
+        const int cap = c->nvec_cap, F = c->Fp;
         bf16* stage = static_cast<bf16*>(c->shift_stage);
         launch_shift_stage(c->tab, nvec, cap, L, D, stage, c->stream);
         for (int l = l0; l < l1; l++)
@@ -370,7 +375,7 @@ template <typename T>
 int enqueue_part(irodori_ctx* c, int l, int B, int S, const ModTable& mt, int part, int r0,
                  hipStream_t st, const PartOpts& opt = PartOpts()) {
     const auto& g = c->cfg;
-    const int D = g.model_dim, H = g.num_heads, F = g.mlp_hidden, M = B * S, Dh = g.head_dim;
+    const int D = g.model_dim, H = g.num_heads, F = c->Fp, M = B * S, Dh = g.head_dim;
     const bool last = l + 1 == g.num_layers;
     auto& lb = c->layers[l];
     const int vt_stride = (S + 63) / 64 * 64;
@@ -794,15 +799,15 @@ int irodori_ctx_create(int device, const irodori_dit_config* cfg, irodori_ctx** 
     IRO_REQUIRE(g.compute_dtype == IRODORI_DTYPE_BF16 || g.compute_dtype == IRODORI_DTYPE_F32 ||
                     g.compute_dtype == IRODORI_DTYPE_FP8,
                 IRODORI_ERR_DTYPE, "compute_dtype must be IRODORI_DTYPE_BF16, _F32 or _FP8");
-    IRO_REQUIRE(g.compute_dtype != IRODORI_DTYPE_FP8 || (g.model_dim % 128 == 0 && g.mlp_hidden % 128 == 0),
-                IRODORI_ERR_SHAPE, "fp8 compute needs model_dim and mlp_hidden multiples of 128");
+    IRO_REQUIRE(g.compute_dtype != IRODORI_DTYPE_FP8 || g.model_dim % 128 == 0, IRODORI_ERR_SHAPE,
+                "fp8 compute needs a model_dim multiple of 128");
     IRO_REQUIRE(g.num_layers > 0 && g.num_heads > 0 && g.model_dim > 0 && g.latent_dim > 0,
                 IRODORI_ERR_SHAPE, "dimensions must be positive");
     IRO_REQUIRE(g.head_dim == 64, IRODORI_ERR_SHAPE, "head_dim must be 64");
     IRO_REQUIRE(g.num_heads * g.head_dim == g.model_dim, IRODORI_ERR_SHAPE, "num_heads * head_dim must equal model_dim");
     IRO_REQUIRE(g.model_dim % 64 == 0 && g.model_dim <= 2048, IRODORI_ERR_SHAPE,
                 "model_dim must be a multiple of 64 and <= 2048");
-    IRO_REQUIRE(g.mlp_hidden > 0 && g.mlp_hidden % 64 == 0, IRODORI_ERR_SHAPE, "mlp_hidden must be a positive multiple of 64");
+    IRO_REQUIRE(g.mlp_hidden > 0, IRODORI_ERR_SHAPE, "mlp_hidden must be positive");
     IRO_REQUIRE(g.latent_dim <= 64, IRODORI_ERR_SHAPE, "latent_dim must be <= 64");
     IRO_REQUIRE(g.adaln_rank > 0 && g.timestep_embed_dim > 0 && g.timestep_embed_dim % 2 == 0,
                 IRODORI_ERR_SHAPE, "adaln_rank > 0 and even timestep_embed_dim required");
@@ -819,6 +824,7 @@ int irodori_ctx_create(int device, const irodori_dit_config* cfg, irodori_ctx** 
     std::unique_ptr<irodori_ctx, int (*)(irodori_ctx*)> c(new irodori_ctx(), irodori_ctx_destroy);
     c->device = device;
     c->cfg = g;
+    c->Fp = (g.mlp_hidden + 127) / 128 * 128;
     c->fp8 = g.compute_dtype == IRODORI_DTYPE_FP8;
     c->bf16 = g.compute_dtype == IRODORI_DTYPE_BF16 || c->fp8;
     c->esz = c->bf16 ? 2 : 4;
@@ -831,7 +837,7 @@ int irodori_ctx_create(int device, const irodori_dit_config* cfg, irodori_ctx** 
         IRO_HIP_CHECK(hipEventCreateWithFlags(&c->ev_join[i], hipEventDisableTiming));
     }
 
-    int D = g.model_dim, F = g.mlp_hidden, H = g.num_heads, Dh = g.head_dim, L = g.num_layers;
+    int D = g.model_dim, F = c->Fp, H = g.num_heads, Dh = g.head_dim, L = g.num_layers;
     int R = g.max_rows, S = g.max_seq, T = g.max_ctx > 0 ? g.max_ctx : 1, P = g.latent_dim;
     size_t es = c->esz, M = (size_t)R * S;
     c->layers.resize(L);
@@ -960,7 +966,23 @@ int irodori_load_block_weights(irodori_ctx* c, int layer, const irodori_block_we
                         "null adaLN weight pointer");
     IRO_HIP_CHECK(hipSetDevice(c->device));
     const auto& g = c->cfg;
-    int D = g.model_dim, F = g.mlp_hidden, HD = g.num_heads * g.head_dim, r = g.adaln_rank;
+    const int D = g.model_dim, F = g.mlp_hidden, Fp = c->Fp, HD = g.num_heads * g.head_dim, r = g.adaln_rank;
+    // SwiGLU weights padded to Fp on the host: [W1 | 0 | W3 | 0] and W2 with zero rows.
+    std::vector<float> w13p, w2p;
+    const float* w13 = w->w13;
+    const float* w2 = w->w2;
+    if (Fp != F) {
+        w13p.assign((size_t)D * 2 * Fp, 0.f);
+        for (int d = 0; d < D; d++) {
+            std::copy(w->w13 + (size_t)d * 2 * F, w->w13 + (size_t)d * 2 * F + F, w13p.data() + (size_t)d * 2 * Fp);
+            std::copy(w->w13 + (size_t)d * 2 * F + F, w->w13 + (size_t)d * 2 * F + 2 * F,
+                      w13p.data() + (size_t)d * 2 * Fp + Fp);
+        }
+        w2p.assign((size_t)Fp * D, 0.f);
+        std::copy(w->w2, w->w2 + (size_t)F * D, w2p.data());
+        w13 = w13p.data();
+        w2 = w2p.data();
+    }
     auto& lb = c->layers[layer];
     char* qkvg = static_cast<char*>(lb.w_qkvg);
     if (c->fp8) {
@@ -968,14 +990,14 @@ int irodori_load_block_weights(irodori_ctx* c, int layer, const irodori_block_we
         IRO_TRY(ingest_fp8(c, w->w_qkv, D, 3 * HD, 0, q8, lb.ws_qkvg));
         IRO_TRY(ingest_fp8(c, w->w_gate, D, D, 0, q8 + (size_t)3 * HD * D, lb.ws_qkvg + 3 * HD));
         IRO_TRY(ingest_fp8(c, w->w_o, HD, D, 0, static_cast<uint8_t*>(lb.w_o), lb.ws_o));
-        IRO_TRY(ingest_fp8(c, w->w13, D, 2 * F, 1, static_cast<uint8_t*>(lb.w13), lb.ws_13));
-        IRO_TRY(ingest_fp8(c, w->w2, F, D, 0, static_cast<uint8_t*>(lb.w2), lb.ws_2));
+        IRO_TRY(ingest_fp8(c, w13, D, 2 * Fp, 1, static_cast<uint8_t*>(lb.w13), lb.ws_13));
+        IRO_TRY(ingest_fp8(c, w2, Fp, D, 0, static_cast<uint8_t*>(lb.w2), lb.ws_2));
     } else {
         IRO_TRY(ingest_kmajor(c, w->w_qkv, D, 3 * HD, 0, qkvg));
         IRO_TRY(ingest_kmajor(c, w->w_gate, D, D, 0, qkvg + c->esz * (size_t)3 * HD * D));
         IRO_TRY(ingest_kmajor(c, w->w_o, HD, D, 0, lb.w_o));
-        IRO_TRY(ingest_kmajor(c, w->w13, D, 2 * F, 1, lb.w13));
-        IRO_TRY(ingest_kmajor(c, w->w2, F, D, 0, lb.w2));
+        IRO_TRY(ingest_kmajor(c, w13, D, 2 * Fp, 1, lb.w13));
+        IRO_TRY(ingest_kmajor(c, w2, Fp, D, 0, lb.w2));
     }
     IRO_TRY(upload(c, lb.q_norm, w->q_norm, sizeof(float) * HD));
     IRO_TRY(upload(c, lb.k_norm, w->k_norm, sizeof(float) * HD));
@@ -1703,7 +1725,7 @@ int irodori_op_swiglu_mlp(irodori_ctx* c, int layer, int B, int S, float* x, con
         // The sampler chain's form, one batch row per launch (each on its own vector): the
         // operand x (1 + scale) and the row sums, then W1|W3 with the norm folded in and W2
         // with the gated residual.
-        const int cap = c->nvec_cap, F = g.mlp_hidden;
+        const int cap = c->nvec_cap, F = c->Fp;
         bf16* stage = static_cast<bf16*>(c->shift_stage);
         launch_shift_stage(c->tab, B, cap, L, D, stage, st);
         GemmArgs<bf16> ga{};

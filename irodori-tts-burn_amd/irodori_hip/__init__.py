@@ -6,7 +6,7 @@ Host-side mirror of the reference's inference API for the HIP backend:
 """
 from .config import (CfgGuidanceMode, CodecConfig, DitConfig, EncoderConfig, GuidanceConfig,
                      InferenceBackendKind, IrodoriError, SamplerMethod, SamplerParams,
-                     cfg_cpu_plumbing, cfg_full_rf, cfg_tiny, codec_default, codec_tiny,
+                     cfg_cpu_plumbing, cfg_full_rf, cfg_published_500m, cfg_tiny, codec_default, codec_tiny,
                      enc_speaker_default, enc_speaker_tiny, enc_text_default, enc_text_tiny)
 from .engine import HipDacVaeCodec, HipEncoder, HipInferenceEngine, ops
 from .synthetic import (ROLE_COND, ROLE_NO_AUX, ROLE_NO_TEXT, ROLE_UNCOND, CodecWeights, ContextKV,
@@ -15,7 +15,7 @@ from .synthetic import (ROLE_COND, ROLE_NO_AUX, ROLE_NO_TEXT, ROLE_UNCOND, Codec
 
 __all__ = [
     "CfgGuidanceMode", "DitConfig", "GuidanceConfig", "InferenceBackendKind", "IrodoriError",
-    "SamplerMethod", "SamplerParams", "cfg_cpu_plumbing", "cfg_full_rf", "cfg_tiny",
+    "SamplerMethod", "SamplerParams", "cfg_cpu_plumbing", "cfg_full_rf", "cfg_published_500m", "cfg_tiny",
     "HipInferenceEngine", "HipEncoder", "ops", "ContextKV", "CtxProjWeights", "DitWeights", "make_context_kv", "make_noise",
     "make_role_context", "ROLE_COND", "ROLE_UNCOND", "ROLE_NO_TEXT", "ROLE_NO_AUX",
     "EncoderConfig", "EncoderWeights", "enc_text_default", "enc_speaker_default", "enc_text_tiny",

@@ -93,6 +93,15 @@ def cfg_full_rf() -> DitConfig:
                      mlp_hidden=2816, adaln_rank=256, timestep_embed_dim=512, norm_eps=1e-5)
 
 
+def cfg_published_500m() -> DitConfig:
+    """The shape of the published Irodori-TTS-500M-v2 checkpoint (docs/benchmarks/rtx-a6000.md:13-21:
+    d 1280, 12 layers, 20 heads) with ModelConfig's default mlp_ratio 2.875
+    (src/config/model.rs:54): SwiGLU hidden floor(1280 * 2.875) = 3680 (src/model/diffusion.rs:32);
+    latents of the DACVAE codebook width 32 (src/codec/weights.rs:213)."""
+    return DitConfig(latent_dim=32, model_dim=1280, num_layers=12, num_heads=20, mlp_hidden=3680,
+                     adaln_rank=256, timestep_embed_dim=512, norm_eps=1e-5)
+
+
 def cfg_tiny() -> DitConfig:
     """Shape of the reference's tiny_model_config (src/config/model.rs:285-313) with
     head_dim 64: small enough for brute-force checks."""

@@ -98,7 +98,7 @@ def test_op_shape_and_dtype_errors_before_any_device_call():
 
 @pytest.mark.parametrize("field,value,code", [
     ("head_dim", 128, L.ERR_SHAPE),
-    ("mlp_hidden", 100, L.ERR_SHAPE),
+    ("mlp_hidden", 0, L.ERR_SHAPE),
     ("compute_dtype", 9, L.ERR_DTYPE),
     ("norm_eps", 0.0, L.ERR_CONFIG),
     ("latent_dim", 100, L.ERR_SHAPE),

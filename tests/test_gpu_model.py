@@ -43,6 +43,10 @@ SMALL = {
     # a 48-channel latent takes the output head's 64-wide tile path (more staged outputs
     # than threads)
     "tiny_p48": (lambda: dataclasses.replace(ih.cfg_tiny(), latent_dim=48), 40, 20, 13, 0.05, 0.1),
+    # the published 500M-v2 width (d 1280, 20 x 64 heads, SwiGLU 3680 padded to 3712 on the
+    # device, norms unfused) with two of its twelve layers; 4 text + 9 speaker keys as the
+    # A6000 benchmark's request (text_len 4, 8 reference frames + the mean token)
+    "pub500m": (lambda: dataclasses.replace(ih.cfg_published_500m(), num_layers=2), 64, 4, 9, 0.02, 0.05),
 }
 
 

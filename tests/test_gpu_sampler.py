@@ -161,3 +161,28 @@ def test_caption_cfg_matches_oracle(oracle64, model, backend, mode, method):
     err = rel_l2(got, ref)
     print(mode, method, backend.value, "caption CFG rel L2 %.2e" % err)
     assert err < TOL[backend]
+
+
+# ---- the published model's width in the A6000 benchmark's sampler configuration -----------
+@pytest.mark.parametrize("backend", [F32, BF16], ids=["f32", "bf16"])
+def test_published_width_independent_cfg(oracle64, backend):
+    # d 1280, 20 x 64 heads, SwiGLU 3680 (two layers); Independent CFG with three roles, text
+    # scale 3, speaker scale 5, min_t 0.5 (CFG only on the steps with t >= 0.5), 4 text keys,
+    # 9 speaker keys (docs/benchmarks/rtx-a6000.md:24-36); 6 Euler steps over 48 frames.
+    import dataclasses
+    cfg = dataclasses.replace(ih.cfg_published_500m(), num_layers=2)
+    w = ih.DitWeights.random(cfg, 31, norm_jitter=0.05)
+    p = params(M.INDEPENDENT, SM.EULER, steps=6, scale_text=3.0, scale_speaker=5.0, min_t=0.5)
+    roles = p.cfg_roles(has_speaker=True)
+    assert roles == ["cond", "no_text", "no_aux"]
+    tt, ta, s = 4, 9, 48
+    ctx = ih.make_role_context(cfg, 1, tt, ta, roles, seed=32)
+    x0 = ih.make_noise(1, s, cfg.latent_dim, 33)
+    with ih.HipInferenceEngine(cfg, backend, max_rows=3, max_seq=s, max_ctx=ctx.t_ctx) as e:
+        e.load_weights(w)
+        e.set_context_kv(ctx)
+        got = e.sample(x0, p, ctx_aux_start=tt)
+    ref, _ = oracle64.sample_rf(cfg, w, x0, (ctx.k, ctx.v, ctx.mask), orc_params(p, aux_start=tt))
+    err = rel_l2(got, ref)
+    print(backend.value, "published width Independent CFG rel L2 %.2e" % err)
+    assert err < TOL[backend]
