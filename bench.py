@@ -27,8 +27,120 @@ PEAK_HBM_GBS = 8000.0
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "w13_gemm_config4_hbm_traffic.txt")
 CODEC_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "codec_decode_hbm_traffic.txt")
 CODEC_KERNELS = ("gemm_kernel", "codec_in_kernel", "codec_head_kernel", "zero_halo_kernel")
-W13_KERNEL = "gemm_kernelIDF16bLi128ELi128ELi2ELi2ELi2ELi2E"  # bf16 128x128, EPI_SWIGLU
+TRACE_FILE = os.path.join(ROOT, "profiles", "rf_config4_kernel_trace.md")
+MFMA_FILE = os.path.join(ROOT, "profiles", "rf_config4_mfma_busy.txt")
 COPY_BYTES = 1 << 30  # the --copy-calibration copy: reads and writes 1 GiB
+SIMDS, SHADER_ENGINES, CLOCK_GHZ = 1024, 32, 2.4  # MI355X: 256 CUs x 4 SIMDs, 8 XCDs x 4 SEs, peak clock
+EPI_NAMES = {0: "STORE", 1: "RESID", 2: "SWIGLU", 3: "QKVG", 4: "CTXKV", 5: "ADD", 6: "SNAKE", 7: "RESUNIT"}
+# The block's hot kernels, keyed as the bench line's kernel_us / mfma_util: GEMMs by epilogue.
+EPI_KEYS = {2: "w13_gemm", 3: "qkvg_gemm", 1: "resid_gemm"}
+
+
+def kernel_info(name):
+    """(key, label) of a kernel name from a rocprofv3 CSV: key is one of w13_gemm, qkvg_gemm,
+    resid_gemm (W_o and W2 share the EPI_RESID instantiation), attention, or None."""
+    import re
+    m = re.search(r"gemm_kernelI(DF16b|DF16_|f)Li(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELb(\d)ELb(\d)E", name)
+    if m:
+        t = {"DF16b": "bf16", "DF16_": "f16", "f": "f32"}[m.group(1)]
+        bm, bn, wm, wn, st, epi, f8, conv = (int(g) for g in m.groups()[1:])
+        label = "gemm_kernel<%s%s, %dx%d, %dx%d waves, %d stages, EPI_%s%s>" % (
+            t, " fp8" if f8 else "", bm, bn, wm, wn, st, EPI_NAMES.get(epi, str(epi)), ", conv" if conv else "")
+        return (EPI_KEYS.get(epi) if t == "bf16" and not f8 and not conv else None), label
+    m = re.search(r"attn32_kernelI(DF16b|DF16_)Li(\d+)ELi(\d+)E", name)
+    if m:
+        return ("attention" if m.group(1) == "DF16b" else None), "attn32_kernel<%s, %s,%s>" % (
+            "bf16" if m.group(1) == "DF16b" else "f16", m.group(2), m.group(3))
+    short = name.replace("_ZN7irodori12_GLOBAL__N_1", "").replace("irodori::(anonymous namespace)::", "")
+    return None, (short if len(short) <= 90 else short[:87] + "...")
+
+
+def trace_summary(trace_csv, M=750, D=1024, F=2816):
+    """Markdown summary of a rocprofv3 --kernel-trace CSV of this script: per kernel and grid,
+    calls / total / avg / min / max; then the hot kernels' average durations, the per-dispatch
+    floor (the trivial step_advance_kernel's average in the same trace) and the SwiGLU
+    up-projection's fraction of the bf16 peak at M rows, raw and floor-corrected."""
+    import csv
+    agg, names = {}, {}
+    for r in csv.DictReader(open(trace_csv)):
+        d = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0
+        key = (r["Kernel_Name"], r["Grid_Size_X"], r["Workgroup_Size_X"])
+        agg.setdefault(key, []).append(d)
+    total = sum(sum(v) for v in agg.values())
+    lines = ["| kernel | grid x | wg | calls | total ms | avg us | min us | max us | % |",
+             "|---|---|---|---|---|---|---|---|---|"]
+    per_key = {}
+    for (n, g, wg), v in sorted(agg.items(), key=lambda kv: -sum(kv[1])):
+        key, label = kernel_info(n)
+        if key:
+            per_key.setdefault(key, []).extend(v)
+        if sum(v) >= 0.001 * total:
+            lines.append("| %s | %s | %s | %d | %.2f | %.2f | %.2f | %.2f | %.2f |" % (
+                label, g, wg, len(v), sum(v) / 1e3, sum(v) / len(v), min(v), max(v), 100 * sum(v) / total))
+    floor = [d for (n, g, wg), v in agg.items() if "step_advance_kernel" in n for d in v]
+    lines.append("")
+    for key in ("w13_gemm", "qkvg_gemm", "resid_gemm", "attention"):
+        v = per_key.get(key, [])
+        if v:
+            lines.append("avg_us.%s: %.3f  (%d dispatches)" % (key, sum(v) / len(v), len(v)))
+    fl = sum(floor) / len(floor) if floor else 0.0
+    lines.append("floor_us.step_advance_kernel: %.3f" % fl)
+    if per_key.get("w13_gemm"):
+        v = per_key["w13_gemm"]
+        avg = sum(v) / len(v)
+        fl_ = 2.0 * M * D * 2 * F / 1e12 / PEAK_BF16_TFLOPS
+        lines.append("w13_frac_at_M%d: %.4f" % (M, fl_ / (avg * 1e-6)))
+        lines.append("w13_frac_at_M%d_floor_corrected: %.4f" % (M, fl_ / ((avg - fl) * 1e-6)))
+    return "\n".join(lines)
+
+
+def mfma_summary(pmc_csv, M=750, D=1024, F=2816, H=16, Dh=64, T=1381):
+    """MFMA busy figures from a rocprofv3 --pmc run of this script collecting
+    SQ_VALU_MFMA_BUSY_CYCLES (per SIMD, summed), SQ_BUSY_CYCLES (per shader engine, summed),
+    SQ_INSTS_VALU_MFMA_MOPS_BF16 (bf16 MFMA FLOPs / 512) and GRBM_GUI_ACTIVE: per hot kernel,
+    busy = MFMA busy SIMD-cycles / (SIMDs x the shader engines' mean active cycles), i.e. the
+    fraction of the time with waves resident that the matrix cores are busy; and the counted
+    MFMA FLOPs per dispatch beside the algorithmic ones at M rows."""
+    import csv
+    per = {}
+    for r in csv.DictReader(open(pmc_csv)):
+        key, _ = kernel_info(r["Kernel_Name"])
+        if not key:
+            continue
+        d = per.setdefault(key, {}).setdefault(r["Dispatch_Id"], {})
+        d[r["Counter_Name"]] = float(r["Counter_Value"])
+        d["ns"] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+    algo = {"w13_gemm": 2.0 * M * D * 2 * F, "qkvg_gemm": 2.0 * M * D * 4 * D,
+            "resid_gemm": None, "attention": 4.0 * H * M * T * Dh}
+    lines = ["%-11s %6s %16s %14s %14s %8s %14s %14s" % (
+        "kernel", "disp", "MFMA busy/disp", "SE active cyc", "GUI active cyc", "busy", "MFMA GFLOP", "algo GFLOP")]
+    out = []
+    for key in ("w13_gemm", "qkvg_gemm", "resid_gemm", "attention"):
+        ds = [d for d in per.get(key, {}).values() if "SQ_VALU_MFMA_BUSY_CYCLES" in d and "SQ_BUSY_CYCLES" in d]
+        if not ds:
+            continue
+        n = len(ds)
+        busy = sum(d["SQ_VALU_MFMA_BUSY_CYCLES"] for d in ds) / n
+        se = sum(d["SQ_BUSY_CYCLES"] for d in ds) / n / SHADER_ENGINES
+        gui = sum(d.get("GRBM_GUI_ACTIVE", 0.0) for d in ds) / n
+        mops = sum(d.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", 0.0) for d in ds) / n * 512
+        ratio = busy / (SIMDS * se) if se else 0.0
+        a = algo[key]
+        lines.append("%-11s %6d %16.0f %14.0f %14.0f %8.4f %14.3f %14s" % (
+            key, n, busy, se, gui, ratio, mops / 1e9, "%.3f" % (a / 1e9) if a else "W_o|W2"))
+        out.append("mfma_busy.%s: %.4f" % (key, ratio))
+    return "\n".join(lines + [""] + out)
+
+
+def read_profile_value(path, key):
+    """The number after `key:` in a committed profile summary, or None."""
+    try:
+        for line in open(path):
+            if line.startswith(key + ":"):
+                return float(line.split(":", 1)[1].split()[0])
+    except OSError:
+        pass
+    return None
 
 
 def log(msg):
@@ -69,10 +181,10 @@ def pmc_summary(fetch_csv, write_csv):
         short = n.replace("_ZN7irodori12_GLOBAL__N_1", "").replace("irodori::(anonymous namespace)::", "")
         short = short if len(short) <= 72 else short[:69] + "..."
         lines.append("%-72s %6d %14.1f %14.1f %12.2f" % (short, len(f), fa, wa, cal / 1e6))
-        if W13_KERNEL in n:
+        if kernel_info(n)[0] == "w13_gemm":
             w13 = (fa * factor["FETCH_SIZE"] * 1024.0, wa * factor["WRITE_SIZE"] * 1024.0)
     if w13 is None:
-        raise SystemExit("SwiGLU GEMM kernel %s not found in the counter files" % W13_KERNEL)
+        raise SystemExit("no bf16 EPI_SWIGLU GEMM kernel in the counter files")
     lines.append("")
     lines.append("w13_fetch_bytes_per_launch: %d" % round(w13[0]))
     lines.append("w13_write_bytes_per_launch: %d" % round(w13[1]))
@@ -164,9 +276,21 @@ def main():
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="print the calibrated traffic summary of two rocprofv3 --pmc "
                          "counter_collection.csv files of this script and exit")
+    ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
+                    help="print the summary of a rocprofv3 --kernel-trace CSV of this script and exit")
+    ap.add_argument("--mfma-summary", metavar="COUNTER_CSV",
+                    help="print the MFMA-busy summary of a rocprofv3 --pmc CSV of this script "
+                         "(SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CYCLES SQ_INSTS_VALU_MFMA_MOPS_BF16 "
+                         "GRBM_GUI_ACTIVE) and exit")
     args = ap.parse_args()
     if args.pmc_summary:
         print(pmc_codec_summary(*args.pmc_summary) if args.workload == "codec" else pmc_summary(*args.pmc_summary))
+        return
+    if args.trace_summary:
+        print(trace_summary(args.trace_summary))
+        return
+    if args.mfma_summary:
+        print(mfma_summary(args.mfma_summary))
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the RF step of one model instance "
@@ -308,13 +432,27 @@ def main():
                       "qkvg_gemm": round(util["qkvg_gemm"], 4), "wo_gemm": round(util["wo_gemm"], 4),
                       "w13_gemm": round(util["w13_gemm"], 4), "w2_gemm": round(util["w2_gemm"], 4)},
         "kernel_us": {k: round(v, 2) for k, v in kt.items()},
-        "norm_mod_gbs": round(norm_gbs, 1),
+        "mfma_busy": {k: read_profile_value(MFMA_FILE, "mfma_busy." + k)
+                      for k in ("attention", "qkvg_gemm", "resid_gemm", "w13_gemm")},
+        "mfma_busy_note": "SQ_VALU_MFMA_BUSY_CYCLES / (1024 SIMDs x mean shader-engine active cycles) per "
+                          "dispatch, from the committed rocprofv3 --pmc summary; resid_gemm = W_o and W2",
+        "norm_mod_hbm_gbs": round(norm_gbs, 1),
+        "norm_mod_note": "unfused adaLN kernel (the bf16 RF chains fold it into their GEMMs), x f32 read + "
+                         "h bf16 write, each launch on its own buffers from a >= 640 MB pool (cold HBM)",
         "roofline": {"kernel": "w13_gemm (SwiGLU up-projection, %dx1024x5632, one CFG row as the RF graph launches it)" % M, "bound": "mfma",
                      "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": read_traffic(),
                      "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, "
                                      "copy-calibrated; profiles/w13_gemm_config4_hbm_traffic.txt)",
-                     "algorithmic_bytes": w13_bytes},
+                     "algorithmic_bytes": w13_bytes,
+                     "rocprof": {"avg_us": read_profile_value(TRACE_FILE, "avg_us.w13_gemm"),
+                                 "dispatch_floor_us": read_profile_value(TRACE_FILE, "floor_us.step_advance_kernel"),
+                                 "frac": read_profile_value(TRACE_FILE, "w13_frac_at_M750"),
+                                 "frac_floor_corrected": read_profile_value(
+                                     TRACE_FILE, "w13_frac_at_M750_floor_corrected"),
+                                 "source": "profiles/rf_config4_kernel_trace.md (rocprofv3 kernel trace of "
+                                           "this script; floor = the trivial step_advance_kernel's average "
+                                           "duration in the same trace)"}},
         "cpu_baseline": cpu,
     }
     eng.close()

@@ -283,7 +283,8 @@ int irodori_op_swiglu_mlp(irodori_ctx* ctx, int layer, int batch, int seq, float
  * sampler's bf16 chains fold into their GEMMs.  bf16 contexts; weights and context KV
  * must be loaded.  Microseconds. */
 typedef struct irodori_kernel_times {
-    float norm_mod_us;   /* unfused RMSNorm + adaLN modulation kernel (x f32 -> h bf16) */
+    float norm_mod_us;   /* unfused RMSNorm + adaLN modulation kernel (x f32 -> h bf16), each
+                            launch on its own buffers from a >= 640 MB pool (cold HBM) */
     float qkvg_gemm_us;  /* QKV + gate projection with head norm / RoPE epilogue */
     float attention_us;  /* joint flash attention + sigmoid gate */
     float wo_gemm_us;    /* output projection + gated residual */

@@ -1784,6 +1784,26 @@ int irodori_profile_layer(irodori_ctx* c, int B, int S, int iters, irodori_kerne
     for (int l = 0; l < L; l++) IRO_TRY(enqueue_layer_any(c, l, B, S, mt));  // fills every operand
     IRO_HIP_CHECK(hipStreamSynchronize(c->stream));
 
+    // The adaLN kernel is HBM-bound: time it on a pool of distinct (x, h) buffer pairs larger
+    // than the L2 and the MALL together (>= 640 MB), one pair per launch, so that every launch
+    // reads x from and writes h to HBM rather than to a warm cache.
+    const size_t xb = (size_t)B * S * g.model_dim * sizeof(float), hb = (size_t)B * S * g.model_dim * sizeof(bf16);
+    const size_t kPoolBytes = (size_t)640 << 20;
+    const int npair = (int)std::max<size_t>(1, (kPoolBytes + xb + hb - 1) / (xb + hb));
+    struct PoolGuard {
+        char* p = nullptr;
+        hipStream_t st;
+        ~PoolGuard() {
+            if (p) {
+                (void)hipStreamSynchronize(st);
+                (void)hipFree(p);
+            }
+        }
+    } pg{nullptr, c->stream};
+    IRO_HIP_CHECK(hipMalloc(&pg.p, (xb + hb) * (size_t)npair));
+    char* const pool = pg.p;
+    IRO_HIP_CHECK(hipMemsetAsync(pool, 0x3c, (xb + hb) * (size_t)npair, c->stream));
+    IRO_HIP_CHECK(hipStreamSynchronize(c->stream));
     hipEvent_t e0, e1;
     IRO_HIP_CHECK(hipEventCreate(&e0));
     IRO_HIP_CHECK(hipEventCreate(&e1));
@@ -1801,8 +1821,9 @@ int irodori_profile_layer(irodori_ctx* c, int B, int S, int iters, irodori_kerne
                 rc = enqueue_head(c, B, S, 0, c->stream);
             } else if (kidx == 0) {
                 // The unfused adaLN kernel (forwards whose rows carry different t, f32, fp8).
-                launch_norm_mod<bf16>(c->x, static_cast<bf16*>(c->h), B * S, S, g.model_dim, g.norm_eps, mt, l, 1,
-                                      c->stream);
+                char* pair = pool + (xb + hb) * (size_t)(it % npair);
+                launch_norm_mod<bf16>(reinterpret_cast<const float*>(pair), reinterpret_cast<bf16*>(pair + xb),
+                                      B * S, S, g.model_dim, g.norm_eps, mt, l, 1, c->stream);
             } else {
                 rc = enqueue_part<bf16>(c, l, B, S, mt, part_of[kidx], 0, c->stream);
             }
