@@ -120,10 +120,116 @@ __device__ __forceinline__ void score_tile(f32x16 (&s)[2], const unsigned char* 
 #pragma unroll
         for (int e = 0; e < 16; e++) z[e] = 0.f;
         s[kb] = mma32x16(ones, qbias, z);
-#pragma unroll
-        for (int ks = 0; ks < 4; ks++)
-            s[kb] = mma32x16(frag<T>(kt, 32 * kb + fr, 2 * ks + fh), qf[ks], s[kb]);
     }
+    typename Vec8<T>::type kf[2][4];
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) kf[kb][ks] = frag<T>(kt, 32 * kb + fr, 2 * ks + fh);
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) s[kb] = mma32x16(kf[kb][ks], qf[ks], s[kb]);
+}
+
+// Merge of the KVS key parities' partial (m, l, O) through LDS (the stage buffers, free
+// once the caller has synchronised the workgroup): [parity - 1][QB][NB][34][64 lanes].
+// Parity p > 0 waves deposit their NB blocks and return false; parity 0 folds them in, in
+// parity order, and returns true.  Every wave of the workgroup must call it.
+template <int QB, int KVS, int NB>
+__device__ __forceinline__ bool merge_parities(unsigned char* smem, int par, int qb, int lane, f32x16 (*o)[2],
+                                               float* m_run, float* l_run) {
+    float* comb = reinterpret_cast<float*>(smem);
+    if (par > 0) {
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++) {
+            float* c = comb + (((size_t)(par - 1) * QB + qb) * NB + nb) * 34 * 64 + lane;
+#pragma unroll
+            for (int db = 0; db < 2; db++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) c[(16 * db + e) * 64] = o[nb][db][e];
+            c[32 * 64] = m_run[nb];
+            c[33 * 64] = l_run[nb];
+        }
+    }
+    __syncthreads();
+    if (par > 0) return false;
+#pragma unroll
+    for (int pp = 1; pp < KVS; pp++)
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++) {
+            const float* c = comb + (((size_t)(pp - 1) * QB + qb) * NB + nb) * 34 * 64 + lane;
+            const float m1 = c[32 * 64], l1 = c[33 * 64];
+            const float mt = fmaxf(m_run[nb], m1);
+            const float mu = mt == -INFINITY ? 0.f : mt;
+            const float c0 = fast_exp2(m_run[nb] - mu), c1 = fast_exp2(m1 - mu);
+#pragma unroll
+            for (int db = 0; db < 2; db++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) o[nb][db][e] = o[nb][db][e] * c0 + c[(16 * db + e) * 64] * c1;
+            l_run[nb] = l_run[nb] * c0 + l1 * c1;
+            m_run[nb] = mt;
+        }
+    return true;
+}
+
+// Normalise, gate and store one 32-query block: o[db][e] = O[q][32 db + 8 (e / 4) + 4 fh +
+// e % 4] for this lane's query q (lanes l and l ^ 32 hold the two halves of its dims).
+template <typename T>
+__device__ __forceinline__ void store_block(const AttnArgs<T>& a, const f32x16 (&o)[2], float l_run, int b, int hh,
+                                            size_t bh, int q, int fh) {
+    const float l = l_run + __shfl_xor(l_run, 32, 64);
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    if (q >= a.Sq) return;
+    const size_t m = (size_t)b * a.Sq + q;
+    if constexpr (std::is_same<T, bf16>::value) {
+        if (a.out_mode == 2) {
+            // fp8 operand form: head dims 32 db .. 32 db + 31 of query q are one scale block,
+            // split between this lane and lane ^ 32.
+            const size_t ob = m * (a.H * 64) + hh * 64;
+#pragma unroll
+            for (int db = 0; db < 2; db++) {
+                float gv[16];
+                float amax = 0.f;
+#pragma unroll
+                for (int g4 = 0; g4 < 4; g4++) {
+                    const bf16x4 gt = *reinterpret_cast<const bf16x4*>(a.G + ob + 32 * db + 8 * g4 + 4 * fh);
+#pragma unroll
+                    for (int c = 0; c < 4; c++) {
+                        gv[4 * g4 + c] = o[db][4 * g4 + c] * inv * static_cast<float>(gt[c]);
+                        amax = fmaxf(amax, fabsf(gv[4 * g4 + c]));
+                    }
+                }
+                amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+                const int ex = mx_exp(amax);
+#pragma unroll
+                for (int g4 = 0; g4 < 4; g4++)
+                    *reinterpret_cast<unsigned*>(a.O8 + ob + 32 * db + 8 * g4 + 4 * fh) =
+                        pack_e4m3(ldexpf(gv[4 * g4], -ex), ldexpf(gv[4 * g4 + 1], -ex), ldexpf(gv[4 * g4 + 2], -ex),
+                                  ldexpf(gv[4 * g4 + 3], -ex));
+                if (fh == 0) a.O8s[m * (a.H * 2) + hh * 2 + db] = (uint8_t)(127 + ex);
+            }
+            return;
+        }
+    }
+#pragma unroll
+    for (int db = 0; db < 2; db++)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; g4++) {
+            const int dim = 32 * db + 8 * g4 + 4 * fh;
+            if (a.out_mode == 0) {
+                typedef T T4 __attribute__((ext_vector_type(4)));
+                const T4 gv = *reinterpret_cast<const T4*>(a.G + m * (a.H * 64) + hh * 64 + dim);
+                T4 ov;
+#pragma unroll
+                for (int c = 0; c < 4; c++) ov[c] = static_cast<T>(o[db][4 * g4 + c] * inv * static_cast<float>(gv[c]));
+                *reinterpret_cast<T4*>(a.O + m * (a.H * 64) + hh * 64 + dim) = ov;
+            } else {
+                float* op = a.Of + ((bh * a.Sq) + q) * 64 + dim;
+                *reinterpret_cast<float4*>(op) = make_float4(o[db][4 * g4] * inv, o[db][4 * g4 + 1] * inv,
+                                                             o[db][4 * g4 + 2] * inv, o[db][4 * g4 + 3] * inv);
+            }
+        }
 }
 
 // QB query blocks of 32 x KVS key parities = QB*KVS wavefronts per workgroup.
@@ -137,7 +243,10 @@ __device__ __forceinline__ void score_tile(f32x16 (&s)[2], const unsigned char* 
 // loads of K_{j+2} / V_{j+1} are issued into the slots freed by iteration j - 1.  LDS:
 // K ring [2][KVS] tiles + V ring [2][KVS] tiles.
 template <typename T, int QB, int KVS>
-__global__ __launch_bounds__(64 * QB * KVS) void attn32_kernel(AttnArgs<T> a, int nqb) {
+// At most two wavefronts per SIMD (the 64 KB of LDS allows no more): the register budget
+// that buys lets every fragment read of a tile go out before the MFMAs that consume it.
+__global__ __launch_bounds__(64 * QB * KVS) __attribute__((amdgpu_waves_per_eu(1, 2))) void attn32_kernel(
+    AttnArgs<T> a, int nqb) {
     typedef typename Vec8<T>::type V8;
     constexpr int NW = QB * KVS;
     constexpr int LPK = KVS * 8 / NW;  // load instructions per wave per K (or V) stage
@@ -257,6 +366,13 @@ __global__ __launch_bounds__(64 * QB * KVS) void attn32_kernel(AttnArgs<T> a, in
         if (j + 2 < niter) ATT_ISSUE(0, j + 2, j & 1);
         const int li = j * KVS + par;
         if (li >= nact) continue;  // this parity has no tile in the last iteration
+        // V^T fragments of tile j, read now so that their latency hides behind the softmax.
+        const unsigned char* vt = vring + ((j & 1) * KVS + par) * TILE_BYTES;
+        V8 vf[2][4];
+#pragma unroll
+        for (int db = 0; db < 2; db++)
+#pragma unroll
+            for (int g = 0; g < 4; g++) vf[db][g] = frag<T>(vt, 32 * db + fr, 2 * g + fh);
 
         // Mask (partial tiles only): keys 32 kb + 8 g4 + 4 fh + c of this lane.
         const unsigned vlo = (unsigned)__builtin_amdgcn_readlane(tl.lo, li);
@@ -320,12 +436,10 @@ __global__ __launch_bounds__(64 * QB * KVS) void attn32_kernel(AttnArgs<T> a, in
             __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);
         }
         // O^T += V^T P^T over the 4 16-key groups of the tile.
-        const unsigned char* vt = vring + ((j & 1) * KVS + par) * TILE_BYTES;
 #pragma unroll
         for (int db = 0; db < 2; db++)
 #pragma unroll
-            for (int g = 0; g < 4; g++)
-                o[db] = mma32x16(frag<T>(vt, 32 * db + fr, 2 * g + fh), pf[g], o[db]);
+            for (int g = 0; g < 4; g++) o[db] = mma32x16(vf[db][g], pf[g], o[db]);
         s[0] = sn[0];
         s[1] = sn[1];
     }
@@ -333,89 +447,245 @@ __global__ __launch_bounds__(64 * QB * KVS) void attn32_kernel(AttnArgs<T> a, in
     float m_run = first ? -INFINITY : m_ref;
 
     // Merge the KVS parities through LDS (reusing the stage buffers; every load has
-    // landed since the last iteration waits for all of them): [parity-1][QB][34][64 lanes].
+    // landed since the last iteration waits for all of them), then normalise, gate, store.
     if constexpr (KVS > 1) {
         __syncthreads();
-        float* comb = reinterpret_cast<float*>(smem);
-        if (par > 0) {
-            float* c = comb + ((size_t)(par - 1) * QB + qb) * 34 * 64 + lane;
-#pragma unroll
-            for (int db = 0; db < 2; db++)
-#pragma unroll
-                for (int e = 0; e < 16; e++) c[(16 * db + e) * 64] = o[db][e];
-            c[32 * 64] = m_run;
-            c[33 * 64] = l_run;
-        }
-        __syncthreads();
-        if (par > 0) return;
-#pragma unroll
-        for (int pp = 1; pp < KVS; pp++) {
-            const float* c = comb + ((size_t)(pp - 1) * QB + qb) * 34 * 64 + lane;
-            const float m1 = c[32 * 64], l1 = c[33 * 64];
-            const float mt = fmaxf(m_run, m1);
-            const float mu = mt == -INFINITY ? 0.f : mt;
-            const float c0 = fast_exp2(m_run - mu), c1 = fast_exp2(m1 - mu);
-#pragma unroll
-            for (int db = 0; db < 2; db++)
-#pragma unroll
-                for (int e = 0; e < 16; e++) o[db][e] = o[db][e] * c0 + c[(16 * db + e) * 64] * c1;
-            l_run = l_run * c0 + l1 * c1;
-            m_run = mt;
-        }
+        if (!merge_parities<QB, KVS, 1>(smem, par, qb, lane, &o, &m_run, &l_run)) return;
     }
+    store_block<T>(a, o, l_run, b, hh, bh, q0 + fr, fh);
+}
 
-    // Normalise, gate, store.  o[db][e] = O[q0 + fr][32 db + 8 (e / 4) + 4 fh + e % 4].
-    float l = l_run + __shfl_xor(l_run, 32, 64);
-    const float inv = l > 0.f ? 1.f / l : 0.f;
-    const int q = q0 + fr;
-    if (q >= a.Sq) return;
-    const size_t m = (size_t)b * a.Sq + q;
-    if constexpr (std::is_same<T, bf16>::value) if (a.out_mode == 2) {
-        // fp8 operand form: head dims 32 db .. 32 db + 31 of query q are one scale block,
-        // split between this lane and lane ^ 32.
-        const size_t ob = m * (a.H * 64) + hh * 64;
+// Two 32-query blocks per wavefront over the same key tiles (QW wavefronts along the
+// queries x KVS key parities per workgroup).  The blocks' dependency chains are
+// independent, so the in-order issue of one wavefront keeps the matrix core and the VALU
+// busy together: block 1's score MFMAs run while block 0's softmax is on the VALU, block
+// 0's P V MFMAs while block 1's softmax runs.  The K and V^T fragments of a tile are read
+// from LDS once for both blocks.  K and V^T tiles move one tile ahead in a two-slot ring.
+// Per query the arithmetic is attn32_kernel's (same MFMA sequences, lazy reference, parity
+// split and merge order), so the two kernels give identical bits.
+template <typename T, int QW, int KVS>
+__global__ __launch_bounds__(64 * QW * KVS) void attn64_kernel(AttnArgs<T> a, int nqg) {
+    typedef typename Vec8<T>::type V8;
+    constexpr int NW = QW * KVS, NB = 2;
+    constexpr int LPK = KVS * 8 / NW;  // load instructions per wave per K (or V) tile set
+    static_assert(LPK * NW == KVS * 8, "tiles must split over the waves");
+    static_assert((KVS - 1) * QW * NB * 34 * 64 * 4 <= 4 * KVS * TILE_BYTES, "merge buffer must fit the rings");
+    extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
+    unsigned char* kring = smem;                         // [2][KVS][TILE_BYTES]
+    unsigned char* vring = smem + 2 * KVS * TILE_BYTES;  // [2][KVS][TILE_BYTES]
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int qw = wave % QW, par = wave / QW;
+    const int pid = xcd_remap(blockIdx.x, gridDim.x);
+    const int qg = pid % nqg, bhid = pid / nqg;
+    const int hh = bhid % a.H, b = bhid / a.H;
+    const int q0 = qg * (64 * QW) + 64 * qw;
+    const int fr = lane & 31, fh = lane >> 5;
+    const size_t bh = (size_t)b * a.H + hh;
+
+    const int nt0 = (a.len0 + KT - 1) / KT;
+    const int nt1 = a.K1 ? (a.len1 + KT - 1) / KT : 0;
+    const TileList tl = build_tile_list(a, b, lane, nt0, nt1);
+    const int nact = tl.nact;
+    const int niter = (nact + KVS - 1) / KVS;
+
+    const T* K0b = a.K0 + bh * a.stride0 * 64;
+    const T* K1b = a.K1 ? a.K1 + bh * a.stride1 * 64 : nullptr;
+    const T* V0b = a.V0 + bh * 64 * (size_t)a.vstride0;
+    const T* V1b = a.V1 ? a.V1 + bh * 64 * (size_t)a.vstride1 : nullptr;
+
+    unsigned voK[LPK], voV0[LPK], voV1[LPK];
 #pragma unroll
-        for (int db = 0; db < 2; db++) {
-            float gv[16];
-            float amax = 0.f;
+    for (int ii = 0; ii < LPK; ii++) {
+        const int gi = wave * LPK + ii;
+        const int r = (gi % 8) * 8 + lane / 8;
+        const unsigned cb = (unsigned)swz(r, lane % 8) * 16u;
+        voK[ii] = (unsigned)r * 128u + cb;
+        voV0[ii] = (unsigned)r * (unsigned)a.vstride0 * 2u + cb;
+        voV1[ii] = (unsigned)r * (unsigned)a.vstride1 * 2u + cb;
+    }
+    // K (kind 0) or V^T (kind 1) tiles of iteration j into ring slot sl: tile list entries
+    // j*KVS + p, clamped to the last entry so every wave issues LPK loads.
+#define ATT64_ISSUE(kind_, j_, sl_)                                                           \
+    do {                                                                                      \
+        _Pragma("unroll") for (int ii = 0; ii < LPK; ii++) {                                  \
+            const int gi = wave * LPK + ii;                                                   \
+            int li = (j_) * KVS + gi / 8;                                                     \
+            li = li < nact ? li : nact - 1;                                                   \
+            const int t = __builtin_amdgcn_readlane(tl.t, li);                                \
+            const bool s0 = t < nt0;                                                          \
+            const int key0 = s0 ? t * KT : (t - nt0) * KT;                                    \
+            unsigned char* dst = ((kind_) ? vring : kring) + ((sl_) * KVS + gi / 8) * TILE_BYTES + (gi % 8) * 1024; \
+            if ((kind_) == 0) {                                                               \
+                const int len = s0 ? a.len0 : a.len1;                                         \
+                buf_load_lds16(make_rsrc((s0 ? K0b : K1b) + (size_t)key0 * 64, (unsigned)(len - key0) * 128u), \
+                               voK[ii], dst);                                                 \
+            } else {                                                                          \
+                const int vs = s0 ? a.vstride0 : a.vstride1;                                  \
+                buf_load_lds16(make_rsrc((s0 ? V0b : V1b) + key0, (unsigned)(64 * vs - key0) * 2u), \
+                               s0 ? voV0[ii] : voV1[ii], dst);                                \
+            }                                                                                 \
+        }                                                                                     \
+    } while (0)
+
+    // Q^T fragments (B operand) of block nb: query q0 + 32 nb + fr, dims 16 ks + 8 fh .. +8.
+    V8 qf[NB][4];
 #pragma unroll
-            for (int g4 = 0; g4 < 4; g4++) {
-                const bf16x4 gt = *reinterpret_cast<const bf16x4*>(a.G + ob + 32 * db + 8 * g4 + 4 * fh);
+    for (int nb = 0; nb < NB; nb++) {
+        int q = q0 + 32 * nb + fr;
+        q = q < a.Sq ? q : a.Sq - 1;
+        const T* qp = a.Q + (bh * a.Sq + q) * 64 + 8 * fh;
 #pragma unroll
-                for (int c = 0; c < 4; c++) {
-                    gv[4 * g4 + c] = o[db][4 * g4 + c] * inv * static_cast<float>(gt[c]);
-                    amax = fmaxf(amax, fabsf(gv[4 * g4 + c]));
+        for (int ks = 0; ks < 4; ks++) qf[nb][ks] = *reinterpret_cast<const V8*>(qp + 16 * ks);
+    }
+    V8 ones, qbias[NB];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        ones[e] = static_cast<T>(0.f);
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++) qbias[nb][e] = static_cast<T>(0.f);
+    }
+    if (fh == 0) ones[0] = static_cast<T>(1.f);
+
+    f32x16 o[NB][2];
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++)
+#pragma unroll
+        for (int db = 0; db < 2; db++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) o[nb][db][e] = 0.f;
+    float m_ref[NB], l_run[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) m_ref[nb] = l_run[nb] = 0.f;
+    bool first = true;  // wave-uniform: no tile processed yet
+
+    // A (row, head) with no valid key (nact = 0) issues no load and runs no iteration.
+    if (nact > 0) {
+        ATT64_ISSUE(0, 0, 0);
+        ATT64_ISSUE(1, 0, 0);
+    }
+    for (int j = 0; j < niter; j++) {
+        // Tile j has landed once this wave's loads are done and all waves met; every wave
+        // is then past tile j - 1, whose slot takes tile j + 1.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        raw_barrier();
+        if (j + 1 < niter) {
+            ATT64_ISSUE(0, j + 1, (j + 1) & 1);
+            ATT64_ISSUE(1, j + 1, (j + 1) & 1);
+        }
+        const int li = j * KVS + par;
+        if (li >= nact) continue;  // this parity has no tile in the last iteration
+        const unsigned char* kt = kring + ((j & 1) * KVS + par) * TILE_BYTES;
+        const unsigned char* vt = vring + ((j & 1) * KVS + par) * TILE_BYTES;
+        const unsigned vlo = (unsigned)__builtin_amdgcn_readlane(tl.lo, li);
+        const unsigned vhi = (unsigned)__builtin_amdgcn_readlane(tl.hi, li);
+        const bool partial = (vlo & vhi) != 0xffffffffu;
+
+        // S'^T of both blocks: the reference step, then 4 k16 steps per 32-key half; the
+        // K fragments are read once.
+        f32x16 s[NB][2];
+        {
+            V8 kf[2][4];
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++)
+#pragma unroll
+                for (int kb = 0; kb < 2; kb++) kf[kb][ks] = frag<T>(kt, 32 * kb + fr, 2 * ks + fh);
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++) {
+#pragma unroll
+                for (int kb = 0; kb < 2; kb++) {
+                    f32x16 z;
+#pragma unroll
+                    for (int e = 0; e < 16; e++) z[e] = 0.f;
+                    s[nb][kb] = mma32x16(ones, qbias[nb], z);
+                }
+#pragma unroll
+                for (int ks = 0; ks < 4; ks++)
+#pragma unroll
+                    for (int kb = 0; kb < 2; kb++) s[nb][kb] = mma32x16(kf[kb][ks], qf[nb][ks], s[nb][kb]);
+            }
+        }
+        V8 vf[2][4];
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+#pragma unroll
+            for (int db = 0; db < 2; db++) vf[db][g] = frag<T>(vt, 32 * db + fr, 2 * g + fh);
+
+        // Online softmax of each block (log2 domain, lazy reference), then O^T += V^T P^T.
+        V8 pf[NB][4];
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++) {
+            if (partial) {
+#pragma unroll
+                for (int kb = 0; kb < 2; kb++) {
+                    const unsigned w = (kb ? vhi : vlo) >> (4 * fh);
+#pragma unroll
+                    for (int g4 = 0; g4 < 4; g4++)
+#pragma unroll
+                        for (int c = 0; c < 4; c++)
+                            if (!((w >> (8 * g4 + c)) & 1u)) s[nb][kb][4 * g4 + c] = -INFINITY;
                 }
             }
-            amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
-            const int ex = mx_exp(amax);
+            float mx = -INFINITY;
 #pragma unroll
-            for (int g4 = 0; g4 < 4; g4++)
-                *reinterpret_cast<unsigned*>(a.O8 + ob + 32 * db + 8 * g4 + 4 * fh) =
-                    pack_e4m3(ldexpf(gv[4 * g4], -ex), ldexpf(gv[4 * g4 + 1], -ex), ldexpf(gv[4 * g4 + 2], -ex),
-                              ldexpf(gv[4 * g4 + 3], -ex));
-            if (fh == 0) a.O8s[m * (a.H * 2) + hh * 2 + db] = (uint8_t)(127 + ex);
+            for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) mx = fmaxf(mx, s[nb][kb][e]);
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const bool need = first || mx > TAU;
+            if (__ballot(need)) {
+                const float nref = need ? round_to<T>(m_ref[nb] + mx) : m_ref[nb];
+                const float delta = nref - m_ref[nb];
+                const float corr = first ? 0.f : fast_exp2(-delta);
+                m_ref[nb] = nref;
+#pragma unroll
+                for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+                    for (int e = 0; e < 16; e++) s[nb][kb][e] -= delta;
+#pragma unroll
+                for (int db = 0; db < 2; db++) o[nb][db] *= corr;
+                l_run[nb] *= corr;
+                if (fh == 0) qbias[nb][0] = static_cast<T>(-m_ref[nb]);
+            }
+            float psum = 0.f;
+#pragma unroll
+            for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const float p = fast_exp2(s[nb][kb][e]);
+                    psum += p;
+                    pf[nb][2 * kb + (e >> 3)][e & 7] = static_cast<T>(p);
+                }
+            l_run[nb] += psum;
+#pragma unroll
+            for (int db = 0; db < 2; db++)
+#pragma unroll
+                for (int g = 0; g < 4; g++) o[nb][db] = mma32x16(vf[db][g], pf[nb][g], o[nb][db]);
         }
-        return;
+        first = false;
+    }
+#undef ATT64_ISSUE
+    float m_run[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) m_run[nb] = first ? -INFINITY : m_ref[nb];
+    if constexpr (KVS > 1) {
+        __syncthreads();
+        if (!merge_parities<QW, KVS, NB>(smem, par, qw, lane, o, m_run, l_run)) return;
     }
 #pragma unroll
-    for (int db = 0; db < 2; db++)
-#pragma unroll
-        for (int g4 = 0; g4 < 4; g4++) {
-            const int dim = 32 * db + 8 * g4 + 4 * fh;
-            if (a.out_mode == 0) {
-                typedef T T4 __attribute__((ext_vector_type(4)));
-                const T4 gv = *reinterpret_cast<const T4*>(a.G + m * (a.H * 64) + hh * 64 + dim);
-                T4 ov;
-#pragma unroll
-                for (int c = 0; c < 4; c++) ov[c] = static_cast<T>(o[db][4 * g4 + c] * inv * static_cast<float>(gv[c]));
-                *reinterpret_cast<T4*>(a.O + m * (a.H * 64) + hh * 64 + dim) = ov;
-            } else {
-                float* op = a.Of + ((bh * a.Sq) + q) * 64 + dim;
-                *reinterpret_cast<float4*>(op) = make_float4(o[db][4 * g4] * inv, o[db][4 * g4 + 1] * inv,
-                                                             o[db][4 * g4 + 2] * inv, o[db][4 * g4 + 3] * inv);
-            }
-        }
+    for (int nb = 0; nb < NB; nb++) store_block<T>(a, o[nb], l_run[nb], b, hh, bh, q0 + 32 * nb + fr, fh);
+}
+
+template <typename T, int QW, int KVS>
+int launch_attn64_cfg(const AttnArgs<T>& a, hipStream_t st) {
+    const size_t lds = (size_t)4 * KVS * TILE_BYTES;
+    static std::once_flag once;
+    static hipError_t attr_rc = hipSuccess;
+    if (set_lds_limit_once(once, attr_rc, (const void*)attn64_kernel<T, QW, KVS>, (int)lds) != hipSuccess) return -2;
+    const int nqg = (a.Sq + 64 * QW - 1) / (64 * QW);
+    attn64_kernel<T, QW, KVS><<<dim3(nqg * a.H * a.B), 64 * QW * KVS, lds, st>>>(a, nqg);
+    return 0;
 }
 
 template <typename T, int QB, int KVS>

@@ -42,6 +42,17 @@ template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
+// Wait until at most `ahead` (<= MAXA) slices of LPW loads each are still in flight.
+template <int MAXA, int LPW>
+__device__ __forceinline__ void wait_slices(int ahead) {
+    if constexpr (MAXA <= 0) {
+        wait_vmcnt<0>();
+    } else {
+        static_assert(MAXA * LPW <= 63, "vmcnt holds 6 bits");
+        if (ahead >= MAXA) wait_vmcnt<MAXA * LPW>();
+        else wait_slices<MAXA - 1, LPW>(ahead);
+    }
+}
 // Workgroup barrier without the implied memory fence (which would drain every in-flight
 // load, including the prefetched slices).
 __device__ __forceinline__ void raw_barrier() { asm volatile("s_barrier" ::: "memory"); }
@@ -337,28 +348,34 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
         }
     }
 
-    // Fused adaLN consumer: lane l of a wave loads the K/32 partial sums of row m0 + wm0 + l
-    // and this wave's shift-bias columns before the operand stream starts, so their latency
-    // hides behind it; iteration 0 of the main loop turns the sums into r = rsqrt(mean x^2 +
-    // eps) in the wave's own LDS slot (rows of the wave only: no workgroup barrier).
+    // Fused adaLN consumer: lane l of a wave loads the K/32 partial sums of rows m0 + wm0 + l
+    // (+ 64) and this wave's shift-bias columns before the operand stream starts, so their
+    // latency hides behind it; iteration 0 of the main loop turns the sums into r = rsqrt(mean
+    // x^2 + eps), kept in registers until the stage buffers are free after the main loop.
     constexpr bool FUSE_IN = !F8 && (EPI == EPI_QKVG || EPI == EPI_SWIGLU);
-    [[maybe_unused]] float* rs_lds = reinterpret_cast<float*>(smem + STAGES * STAGE_BYTES) + wave * WM;
-    [[maybe_unused]] float4 rsv[8];
+    constexpr int RPL = (WM + 63) / 64;  // rows of the wave per lane
+    [[maybe_unused]] float4 rsv[RPL][8];
+    [[maybe_unused]] float rown[RPL];
     [[maybe_unused]] float bc[FN];
     if constexpr (FUSE_IN) {
-        static_assert(WM <= 64, "one row per lane");
+        static_assert(RPL <= 2, "at most two rows per lane");
+        static_assert(STAGES * STAGE_BYTES >= NW * WM * 4, "row scales are staged in the operand buffers");
         if (a.rstat) {
             const int vec = mod_vec_index(a.mt, a.mt.step ? *a.mt.step : 0, 0);
 #pragma unroll
             for (int j = 0; j < FN; j++) bc[j] = a.rbias[(size_t)vec * a.N + n0 + wn0 + 32 * j + lane % 32];
-            const int row = m0 + wm0 + lane, nq = K / 128;
+            const int nq = K / 128;
 #pragma unroll
-            for (int q = 0; q < 8; q++) rsv[q] = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (lane < WM && row < a.M) {
-                const float4* p = reinterpret_cast<const float4*>(a.rstat + (size_t)row * (K / 32));
+            for (int p = 0; p < RPL; p++) {
+                const int rl = 64 * p + lane, row = m0 + wm0 + rl;
 #pragma unroll
-                for (int q = 0; q < 8; q++)
-                    if (q < nq) rsv[q] = p[q];
+                for (int q = 0; q < 8; q++) rsv[p][q] = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (rl < WM && row < a.M) {
+                    const float4* pp = reinterpret_cast<const float4*>(a.rstat + (size_t)row * (K / 32));
+#pragma unroll
+                    for (int q = 0; q < 8; q++)
+                        if (q < nq) rsv[p][q] = pp[q];
+                }
             }
         }
     }
@@ -369,23 +386,25 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
         if (s < nk) GEMM_ISSUE(s, s);
     const int fr = lane & 31, fh = lane >> 5;
     for (int kt = 0; kt < nk; kt++) {
-        // Slice kt has landed (later slices may still be in flight); make it visible.
-        if (STAGES >= 4 && kt + 2 < nk) wait_vmcnt<2 * LPW>();
-        else if (STAGES >= 3 && kt + 1 < nk) wait_vmcnt<LPW>();
-        else wait_vmcnt<0>();
+        // Slice kt has landed (the min(STAGES - 2, nk - 1 - kt) slices issued after it may
+        // still be in flight); make it visible.
+        wait_slices<STAGES - 2, LPW>(nk - 1 - kt);
         raw_barrier();
         if (kt + STAGES - 1 < nk) GEMM_ISSUE(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
         if constexpr (FUSE_IN) {
             if (a.rstat && kt == 0) {
-                float ss = 0.f;
 #pragma unroll
-                for (int q = 0; q < 8; q++) {
-                    ss += rsv[q].x;
-                    ss += rsv[q].y;
-                    ss += rsv[q].z;
-                    ss += rsv[q].w;
+                for (int p = 0; p < RPL; p++) {
+                    float ss = 0.f;
+#pragma unroll
+                    for (int q = 0; q < 8; q++) {
+                        ss += rsv[p][q].x;
+                        ss += rsv[p][q].y;
+                        ss += rsv[p][q].z;
+                        ss += rsv[p][q].w;
+                    }
+                    rown[p] = m0 + wm0 + 64 * p + lane < a.M ? 1.f / sqrtf(ss / (float)K + a.eps) : 1.f;
                 }
-                if (lane < WM) rs_lds[lane] = m0 + wm0 + lane < a.M ? 1.f / sqrtf(ss / (float)K + a.eps) : 1.f;
             }
         }
         const unsigned char* st = smem + (kt % STAGES) * STAGE_BYTES;
@@ -466,7 +485,15 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
         if (a.rstat) {
             // acc = r * acc + (shift W)[vec, col]; every row of the launch has the same
             // modulation vector (checked at launch).
-            // Row scales of this lane (its wave's slot): rows 4 (lane / 32) + 32 i + 8 q + 0..3.
+            // The wave's row scales go through its own slot of the (now free) stage buffers;
+            // this lane then needs rows 4 (lane / 32) + 32 i + 8 q + 0..3.
+            __syncthreads();  // every wave is past its last read of the operand stages
+            float* rs_lds = reinterpret_cast<float*>(smem) + wave * WM;
+#pragma unroll
+            for (int p = 0; p < RPL; p++)
+                if (64 * p + lane < WM) rs_lds[64 * p + lane] = rown[p];
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's slot writes landed
+            __builtin_amdgcn_wave_barrier();
             float4 rr[FM][4];
 #pragma unroll
             for (int i = 0; i < FM; i++)
@@ -1060,14 +1087,11 @@ int launch_cfg(const GemmArgs<T>& a, hipStream_t st) {
     // EPI_RESUNIT keeps the Snake'd tile (BN / BK slices of BM rows) and one W2 slice in LDS.
     constexpr int kResLds = EPI == EPI_RESUNIT ? ((BN + BK - 1) / BK) * BM * 128 + BN * 128 : 0;
     constexpr int kStageLds = STAGES * (BM + BN) * 128;
-    // The fused-adaLN consumer keeps the row scales of each wave's rows past the stages.
-    constexpr int kRowLds = (!F8 && (EPI == EPI_QKVG || EPI == EPI_SWIGLU)) ? WAVES_M * WAVES_N * (BM / WAVES_M) * 4 : 0;
-    const size_t lds = (size_t)(kStageLds > kResLds ? kStageLds : kResLds) + (F8 ? (size_t)BM * (a.K / 32) : 0) +
-                       (a.rstat ? kRowLds : 0);
+    const size_t lds = (size_t)(kStageLds > kResLds ? kStageLds : kResLds) + (F8 ? (size_t)BM * (a.K / 32) : 0);
     // Per instantiation; the attribute is process-wide.
     static std::once_flag once;
     static hipError_t attr_rc = hipSuccess;
-    constexpr int lds_max = (kStageLds > kResLds ? kStageLds : kResLds) + (F8 ? BM * (kMaxK8 / 32) : 0) + kRowLds;
+    constexpr int lds_max = (kStageLds > kResLds ? kStageLds : kResLds) + (F8 ? BM * (kMaxK8 / 32) : 0);
     if (set_lds_limit_once(once, attr_rc, (const void*)gemm_kernel<T, BM, BN, WAVES_M, WAVES_N, STAGES, EPI, F8, CONV>,
                            lds_max) != hipSuccess)
         return -2;
