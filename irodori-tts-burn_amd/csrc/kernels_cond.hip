@@ -22,10 +22,7 @@ __global__ void timestep_embedding_kernel(const float* __restrict__ t, int nvec,
     out[(size_t)v * t_dim + half + i] = sinf(a);
 }
 
-constexpr int kVecChunk = 32;  // vectors per workgroup (blockIdx.z chunks the rest)
-constexpr int kCols = 64;      // output columns per workgroup
-constexpr int kKGroups = 4;    // k-slices per workgroup, reduced through LDS
-constexpr int kKTile = 256;    // staged X columns per pass
+constexpr int kKTile = 64;  // staged X columns per pass
 
 __device__ __forceinline__ float apply_act(float v, int act) {
     if (act == 1) return silu_f(v);
@@ -34,75 +31,96 @@ __device__ __forceinline__ float apply_act(float v, int act) {
 }
 
 // Y[v, n] = act_out(act_in(X[v, :]) @ W[:, n] + bias[n] + R[v, n]) for every job
-// (blockIdx.y), 64-column block (blockIdx.x) and 32-vector chunk (blockIdx.z).  Thread
-// (kg, c) owns column n = 64 blockIdx.x + c and the k-slice k = kg (mod 4), accumulating
-// all vectors of the chunk in registers; a wavefront reads one 256-byte row segment of
-// W per k, so W is streamed once per vector chunk.  The X tile (activation applied) is
-// staged in LDS and the 4 k-slices are summed through LDS at the end.
-__global__ __launch_bounds__(256) void vec_linear_kernel(const VecLinJob* __restrict__ jobs,
-                                                         int nvec) {
-    __shared__ __attribute__((aligned(16))) float xs[kKTile][kVecChunk];  // transposed: one k = 32 vectors
-    __shared__ float red[kKGroups - 1][kVecChunk][kCols];
+// (blockIdx.y), COLS-column block (blockIdx.x) and VC-vector chunk (blockIdx.z).  The 256
+// threads are COLS columns x KG = 256 / COLS k-groups: thread (kg, c) owns column
+// n = COLS blockIdx.x + c and the k values k = kg (mod KG), accumulating all VC vectors of
+// the chunk in registers, so W is streamed once per vector chunk (a wavefront reads 64 / COLS
+// row segments of COLS consecutive columns per k).  K advances in tiles of 64: the X tile
+// (activation applied) is staged transposed in LDS (one k = VC vectors, broadcast 16-byte
+// reads), and the W and X values of tile t + 1 are loaded into registers while tile t is
+// computed.  The k-groups are summed through LDS at the end, in k-group order.
+template <int VC, int COLS>
+__global__ __launch_bounds__(256) void vec_linear_kernel(const VecLinJob* __restrict__ jobs, int nvec) {
+    constexpr int KG = 256 / COLS, NK = kKTile / KG, NX = VC * kKTile / 256;
+    static_assert(VC % 4 == 0 && KG * COLS == 256 && NX * 256 == VC * kKTile, "tile shapes");
+    __shared__ __attribute__((aligned(16))) float xs[kKTile][VC];
+    __shared__ float red[KG - 1][VC][COLS];
     const VecLinJob jb = jobs[blockIdx.y];
-    if (blockIdx.x * kCols >= jb.N) return;  // uniform: this job has fewer columns
-    const int c = threadIdx.x % kCols, kg = threadIdx.x / kCols;
-    const int n = blockIdx.x * kCols + c;
+    if (blockIdx.x * COLS >= jb.N) return;  // uniform: this job has fewer columns
+    const int c = threadIdx.x % COLS, kg = threadIdx.x / COLS;
+    const int n = blockIdx.x * COLS + c;
     const bool active = n < jb.N;
-    const int v0 = blockIdx.z * kVecChunk;
-    const int nv = nvec - v0 < kVecChunk ? nvec - v0 : kVecChunk;
-    float acc[kVecChunk];
+    const int v0 = blockIdx.z * VC;
+    const int nv = nvec - v0 < VC ? nvec - v0 : VC;
+    float acc[VC];
 #pragma unroll
-    for (int v = 0; v < kVecChunk; v++) acc[v] = 0.f;
-    for (int k0 = 0; k0 < jb.K; k0 += kKTile) {
+    for (int v = 0; v < VC; v++) acc[v] = 0.f;
+    float wv[NK], xv[NX];
+    auto load_tile = [&](int k0) {
         const int kt = jb.K - k0 < kKTile ? jb.K - k0 : kKTile;
-        __syncthreads();
-        for (int e = threadIdx.x; e < kVecChunk * kKTile; e += 256) {
-            const int v = e % kVecChunk, k = e / kVecChunk;  // conflict-free LDS writes
-            float val = 0.f;
-            if (v < nv && k < kt) val = apply_act(jb.X[(size_t)(v0 + v) * jb.ldx + k0 + k], jb.act_in);
-            xs[k][v] = val;
+#pragma unroll
+        for (int i = 0; i < NK; i++) {
+            const int k = kg + KG * i;
+            wv[i] = active && k < kt ? jb.W[(size_t)(k0 + k) * jb.N + n] : 0.f;
         }
+#pragma unroll
+        for (int i = 0; i < NX; i++) {
+            const int e = threadIdx.x + 256 * i, v = e % VC, k = e / VC;  // conflict-free LDS writes
+            xv[i] = v < nv && k < kt ? jb.X[(size_t)(v0 + v) * jb.ldx + k0 + k] : 0.f;
+        }
+    };
+    load_tile(0);
+    for (int k0 = 0; k0 < jb.K; k0 += kKTile) {
+        __syncthreads();  // every thread is past the previous tile's X reads
+#pragma unroll
+        for (int i = 0; i < NX; i++) {
+            const int e = threadIdx.x + 256 * i;
+            xs[e / VC][e % VC] = apply_act(xv[i], jb.act_in);
+        }
+        float wc[NK];
+#pragma unroll
+        for (int i = 0; i < NK; i++) wc[i] = wv[i];
         __syncthreads();
+        if (k0 + kKTile < jb.K) load_tile(k0 + kKTile);  // in flight during this tile
         if (active) {
-            // 16 W values (k = kg, kg + 4, ...) are loaded together so their latencies
-            // overlap; each k's 32 vector values are 8 broadcast 16-byte LDS reads.
-            for (int kb = 0; kb < kt; kb += 16 * kKGroups) {
-                float wv[16];
+            const int kt = jb.K - k0 < kKTile ? jb.K - k0 : kKTile;
 #pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    const int k = kb + kg + kKGroups * i;
-                    wv[i] = k < kt ? jb.W[(size_t)(k0 + k) * jb.N + n] : 0.f;
-                }
+            for (int i = 0; i < NK; i++) {
+                const int k = kg + KG * i;
+                if (k >= kt) break;
+                const float4* xr = reinterpret_cast<const float4*>(&xs[k][0]);
 #pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    const int k = kb + kg + kKGroups * i;
-                    if (k >= kt) break;
-                    const float4* xr = reinterpret_cast<const float4*>(&xs[k][0]);
-#pragma unroll
-                    for (int q = 0; q < kVecChunk / 4; q++) {
-                        const float4 xv = xr[q];
-                        acc[4 * q] += xv.x * wv[i];
-                        acc[4 * q + 1] += xv.y * wv[i];
-                        acc[4 * q + 2] += xv.z * wv[i];
-                        acc[4 * q + 3] += xv.w * wv[i];
-                    }
+                for (int q = 0; q < VC / 4; q++) {
+                    const float4 x4 = xr[q];
+                    acc[4 * q] += x4.x * wc[i];
+                    acc[4 * q + 1] += x4.y * wc[i];
+                    acc[4 * q + 2] += x4.z * wc[i];
+                    acc[4 * q + 3] += x4.w * wc[i];
                 }
             }
         }
     }
     if (kg > 0) {
 #pragma unroll
-        for (int v = 0; v < kVecChunk; v++) red[kg - 1][v][c] = acc[v];
+        for (int v = 0; v < VC; v++) red[kg - 1][v][c] = acc[v];
     }
     __syncthreads();
     if (kg == 0 && active) {
         for (int v = 0; v < nv; v++) {
-            float y = acc[v] + red[0][v][c] + red[1][v][c] + red[2][v][c];
+            float y = acc[v];
+#pragma unroll
+            for (int g2 = 0; g2 < KG - 1; g2++) y += red[g2][v][c];
             if (jb.bias) y += jb.bias[n];
             if (jb.R) y += jb.R[(size_t)(v0 + v) * jb.ldr + n];
             jb.Y[(size_t)(v0 + v) * jb.ldy + n] = apply_act(y, jb.act_out);
         }
     }
+}
+
+template <int VC, int COLS>
+void launch_vec_linear_cfg(const VecLinJob* d_jobs, int njobs, int nvec, int max_n, hipStream_t st) {
+    dim3 grid((max_n + COLS - 1) / COLS, njobs, (nvec + VC - 1) / VC);
+    vec_linear_kernel<VC, COLS><<<grid, 256, 0, st>>>(d_jobs, nvec);
 }
 
 // Shift rows of the modulation table [vec][layer][kind][chunk][D] as bf16 GEMM operands:
@@ -126,9 +144,12 @@ void launch_timestep_embedding(const float* t, int nvec, int t_dim, float* out, 
     timestep_embedding_kernel<<<grid, 256, 0, st>>>(t, nvec, t_dim, out);
 }
 
+// Vector chunks of 16 (an RF run's 41 timesteps are three chunks, run side by side).
+// Columns: 64 per block when the jobs x column blocks fill the chip, else 16 per block with
+// 16 k-groups (the cond MLP's single-job launches).
 void launch_vec_linear(const VecLinJob* d_jobs, int njobs, int nvec, int max_n, hipStream_t st) {
-    dim3 grid((max_n + kCols - 1) / kCols, njobs, (nvec + kVecChunk - 1) / kVecChunk);
-    vec_linear_kernel<<<grid, 256, 0, st>>>(d_jobs, nvec);
+    if ((long)((max_n + 63) / 64) * njobs >= 256) launch_vec_linear_cfg<16, 64>(d_jobs, njobs, nvec, max_n, st);
+    else launch_vec_linear_cfg<16, 16>(d_jobs, njobs, nvec, max_n, st);
 }
 
 }  // namespace irodori

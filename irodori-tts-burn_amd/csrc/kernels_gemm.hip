@@ -358,7 +358,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
     [[maybe_unused]] float rown[RPL];
     [[maybe_unused]] float bc[FN];
     if constexpr (FUSE_IN) {
-        static_assert(RPL <= 2, "at most two rows per lane");
+        static_assert(RPL <= 3, "at most three rows per lane");
         static_assert(STAGES * STAGE_BYTES >= NW * WM * 4, "row scales are staged in the operand buffers");
         if (a.rstat) {
             const int vec = mod_vec_index(a.mt, a.mt.step ? *a.mt.step : 0, 0);
