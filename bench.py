@@ -55,7 +55,7 @@ def kernel_info(name):
     return None, (short if len(short) <= 90 else short[:87] + "...")
 
 
-def trace_summary(trace_csv, M=750, D=1024, F=2816):
+def trace_summary(trace_csv, M=750, D=1024, F=2816, w13_frac=True):
     """Markdown summary of a rocprofv3 --kernel-trace CSV of this script: per kernel and grid,
     calls / total / avg / min / max; then the hot kernels' average durations, the per-dispatch
     floor (the trivial step_advance_kernel's average in the same trace) and the SwiGLU
@@ -85,7 +85,7 @@ def trace_summary(trace_csv, M=750, D=1024, F=2816):
             lines.append("avg_us.%s: %.3f  (%d dispatches)" % (key, sum(v) / len(v), len(v)))
     fl = sum(floor) / len(floor) if floor else 0.0
     lines.append("floor_us.step_advance_kernel: %.3f" % fl)
-    if per_key.get("w13_gemm"):
+    if w13_frac and per_key.get("w13_gemm"):
         v = per_key["w13_gemm"]
         avg = sum(v) / len(v)
         fl_ = 2.0 * M * D * 2 * F / 1e12 / PEAK_BF16_TFLOPS
@@ -287,7 +287,8 @@ def main():
         print(pmc_codec_summary(*args.pmc_summary) if args.workload == "codec" else pmc_summary(*args.pmc_summary))
         return
     if args.trace_summary:
-        print(trace_summary(args.trace_summary))
+        # The W13 fraction lines are the headline's (config 4, one CFG row per launch).
+        print(trace_summary(args.trace_summary, w13_frac=args.workload == "cfg4"))
         return
     if args.mfma_summary:
         print(mfma_summary(args.mfma_summary))

@@ -280,8 +280,8 @@ int irodori_op_swiglu_mlp(irodori_ctx* ctx, int layer, int batch, int seq, float
  * using layer i % num_layers (weights and context K/V cycle through the layers as in an RF
  * step) -- the reference's NVTX per-call timings (docs/benchmarks/rtx-a6000.md:131-138) as
  * a measurement entry point.  norm_mod_us times the unfused adaLN kernel, which the
- * sampler's bf16 chains fold into their GEMMs.  bf16 contexts; weights and context KV
- * must be loaded.  Microseconds. */
+ * sampler's bf16 chains fold into their GEMMs.  bf16 contexts (an fp8 context times its
+ * fp8 GEMMs); weights and context KV must be loaded.  Microseconds. */
 typedef struct irodori_kernel_times {
     float norm_mod_us;   /* unfused RMSNorm + adaLN modulation kernel (x f32 -> h bf16), each
                             launch on its own buffers from a >= 640 MB pool (cold HBM) */

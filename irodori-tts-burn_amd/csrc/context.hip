@@ -1768,7 +1768,7 @@ int irodori_profile_layer(irodori_ctx* c, int B, int S, int iters, irodori_kerne
     IRO_REQUIRE(B > 0 && B <= g.max_rows && S > 0 && S <= g.max_seq, IRODORI_ERR_SHAPE,
                 "batch must be in [1, max_rows], seq in [1, max_seq]");
     IRO_REQUIRE(iters > 0, IRODORI_ERR_INVALID_ARG, "iters must be > 0");
-    IRO_REQUIRE(c->bf16 && !c->fp8, IRODORI_ERR_DTYPE, "irodori_profile_layer times the bf16 path");
+    IRO_REQUIRE(c->bf16, IRODORI_ERR_DTYPE, "irodori_profile_layer times the bf16 / fp8 path");
     IRO_TRY(check_ready(c, B));
     IRO_HIP_CHECK(hipSetDevice(c->device));
     int L = g.num_layers;

@@ -353,3 +353,21 @@ def test_sample_padded_batch_matches_unpadded(backend):
     with pytest.raises(ih.IrodoriError):
         with make_engine(cfg, backend, w, ctx, 4, 64) as e:
             e.sample(x0, p, lengths=[64, 65])
+
+
+@pytest.mark.parametrize("backend", [BF16, ih.InferenceBackendKind.HIP_FP8], ids=["bf16", "fp8"])
+def test_profile_layer_reports_every_kernel(backend):
+    # irodori_profile_layer on the configuration-1 model (bf16, and its fp8 GEMM mode): one
+    # positive, finite time per kernel of the block and the output head; an f32 context is
+    # refused with a dtype error.
+    cfg = ih.cfg_cpu_plumbing()
+    w = ih.DitWeights.random(cfg, 0)
+    ctx = ih.make_context_kv(cfg, 1, 16, 32, seed=1)
+    with make_engine(cfg, backend, w, ctx, 2, 64) as e:
+        kt = e.profile_layer(1, 64, 3)
+    assert set(kt) == {"norm_mod_us", "qkvg_gemm_us", "attention_us", "wo_gemm_us", "w13_gemm_us",
+                       "w2_gemm_us", "final_us"}
+    assert all(np.isfinite(v) and v > 0 for v in kt.values()), kt
+    with make_engine(cfg, F32, w, ctx, 2, 64) as e:
+        with pytest.raises(ih.IrodoriError, match="Dtype"):
+            e.profile_layer(1, 64, 3)
