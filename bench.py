@@ -58,7 +58,8 @@ def kernel_info(name):
 def trace_summary(trace_csv, M=750, D=1024, F=2816, w13_frac=True):
     """Markdown summary of a rocprofv3 --kernel-trace CSV of this script: per kernel and grid,
     calls / total / avg / min / max; then the hot kernels' average durations, the per-dispatch
-    floor (the trivial step_advance_kernel's average in the same trace) and the SwiGLU
+    floor (the average of scale_copy_kernel in the same trace: one pass over the 24k-float
+    initial state per RF run, a launch with next to no work) and the SwiGLU
     up-projection's fraction of the bf16 peak at M rows, raw and floor-corrected."""
     import csv
     agg, names = {}, {}
@@ -77,14 +78,14 @@ def trace_summary(trace_csv, M=750, D=1024, F=2816, w13_frac=True):
         if sum(v) >= 0.001 * total:
             lines.append("| %s | %s | %s | %d | %.2f | %.2f | %.2f | %.2f | %.2f |" % (
                 label, g, wg, len(v), sum(v) / 1e3, sum(v) / len(v), min(v), max(v), 100 * sum(v) / total))
-    floor = [d for (n, g, wg), v in agg.items() if "step_advance_kernel" in n for d in v]
+    floor = [d for (n, g, wg), v in agg.items() if "scale_copy_kernel" in n for d in v]
     lines.append("")
     for key in ("w13_gemm", "qkvg_gemm", "resid_gemm", "attention"):
         v = per_key.get(key, [])
         if v:
             lines.append("avg_us.%s: %.3f  (%d dispatches)" % (key, sum(v) / len(v), len(v)))
     fl = sum(floor) / len(floor) if floor else 0.0
-    lines.append("floor_us.step_advance_kernel: %.3f" % fl)
+    lines.append("floor_us.scale_copy_kernel: %.3f" % fl)
     if w13_frac and per_key.get("w13_gemm"):
         v = per_key["w13_gemm"]
         avg = sum(v) / len(v)
@@ -447,12 +448,12 @@ def main():
                                      "copy-calibrated; profiles/w13_gemm_config4_hbm_traffic.txt)",
                      "algorithmic_bytes": w13_bytes,
                      "rocprof": {"avg_us": read_profile_value(TRACE_FILE, "avg_us.w13_gemm"),
-                                 "dispatch_floor_us": read_profile_value(TRACE_FILE, "floor_us.step_advance_kernel"),
+                                 "dispatch_floor_us": read_profile_value(TRACE_FILE, "floor_us.scale_copy_kernel"),
                                  "frac": read_profile_value(TRACE_FILE, "w13_frac_at_M750"),
                                  "frac_floor_corrected": read_profile_value(
                                      TRACE_FILE, "w13_frac_at_M750_floor_corrected"),
                                  "source": "profiles/rf_config4_kernel_trace.md (rocprofv3 kernel trace of "
-                                           "this script; floor = the trivial step_advance_kernel's average "
+                                           "this script; floor = the near-empty scale_copy_kernel's average "
                                            "duration in the same trace)"}},
         "cpu_baseline": cpu,
     }

@@ -104,7 +104,7 @@ struct irodori_ctx {
     std::vector<LayerBufs> layers;
     bool io_loaded = false;
     float *cond_w0 = nullptr, *cond_w1 = nullptr, *cond_w2 = nullptr;
-    float *in_w = nullptr, *in_b = nullptr, *out_norm_w = nullptr, *out_wT = nullptr,
+    float *in_w = nullptr, *in_b = nullptr, *out_norm_w = nullptr, *out_w = nullptr,
           *out_b = nullptr;
     int t_ctx = -1;
 
@@ -150,7 +150,7 @@ struct irodori_ctx {
     std::vector<void*> act_k, act_v;
     bool kvs_on = false;
     int kvs_layers = 0;
-    int* step = nullptr;    // device step counter
+    int* step = nullptr;    // device step counter; step[1]: the output head's finished-workgroup count
     int* zero_step = nullptr;
     // Latent key mask of the current call (build_joint_mask's self part,
     // attention.rs:730-750): per row and 64-key tile a validity word (bf16 attention)
@@ -581,23 +581,27 @@ int enqueue_layer_any(irodori_ctx* c, int l, int B, int S, const ModTable& mt, i
 }
 
 // in_proj + the first adaLN for batch rows [r0, r0 + B): row r0 + b reads source row
-// b mod src_batches of src [src_batches, S, P].
+// b mod src_batches of src [src_batches, S, P].  When every row shares one modulation vector
+// (a sampler evaluation's roles), the src_batches distinct rows are computed once and
+// written B / src_batches times.
 int enqueue_inproj(irodori_ctx* c, int B, int S, const float* src, int src_batches, int r0, const ModTable& mt,
                    hipStream_t st) {
     const auto& g = c->cfg;
     const size_t tok0 = (size_t)r0 * S;
     float* x = c->x + tok0 * g.model_dim;
+    const bool rep = B > src_batches && B % src_batches == 0 && mt.rows_per_vec >= B;
+    const int copies = rep ? B / src_batches : 1, Bc = B / copies;
     if (c->bf16) {
         bf16* h = c->fp8 ? nullptr : static_cast<bf16*>(c->h) + tok0 * g.model_dim;
-        launch_inproj_norm<bf16>(src, src_batches, c->in_w, c->in_b, x, h, B * S, S, g.latent_dim, g.model_dim,
+        launch_inproj_norm<bf16>(src, src_batches, c->in_w, c->in_b, x, h, Bc * S, S, g.latent_dim, g.model_dim,
                                  g.norm_eps, mt, st, c->fp8 ? c->h8 + tok0 * g.model_dim : nullptr,
                                  c->fp8 ? c->h8s + tok0 * (g.model_dim / 32) : nullptr,
-                                 fused_for(c, mt, B) ? c->rstat + tok0 * (g.model_dim / 32) : nullptr);
+                                 fused_for(c, mt, B) ? c->rstat + tok0 * (g.model_dim / 32) : nullptr, copies);
     }
     else
         launch_inproj_norm<float>(src, src_batches, c->in_w, c->in_b, x,
-                                  static_cast<float*>(c->h) + tok0 * g.model_dim, B * S, S, g.latent_dim,
-                                  g.model_dim, g.norm_eps, mt, st);
+                                  static_cast<float*>(c->h) + tok0 * g.model_dim, Bc * S, S, g.latent_dim,
+                                  g.model_dim, g.norm_eps, mt, st, nullptr, nullptr, nullptr, copies);
     return check_launch("in_proj");
 }
 
@@ -607,7 +611,7 @@ int enqueue_head(irodori_ctx* c, int B, int S, int r0, hipStream_t st) {
     FinalArgs fa{};
     fa.x = c->x + (size_t)r0 * S * g.model_dim;
     fa.norm_w = c->out_norm_w;
-    fa.out_wT = c->out_wT;
+    fa.out_w = c->out_w;
     fa.out_b = c->out_b;
     fa.B = B;
     fa.S = S;
@@ -654,7 +658,7 @@ int enqueue_eval(irodori_ctx* c, int U, int S, int roles, int method, int phase,
     FinalArgs fa{};
     fa.x = c->x;
     fa.norm_w = c->out_norm_w;
-    fa.out_wT = c->out_wT;
+    fa.out_w = c->out_w;
     fa.out_b = c->out_b;
     fa.B = U;
     fa.S = S;
@@ -668,11 +672,12 @@ int enqueue_eval(irodori_ctx* c, int U, int S, int roles, int method, int phase,
     fa.rf.hist = c->hist;
     fa.rf.plan = c->plan;
     fa.rf.step = c->step;
+    fa.rf.done = c->step + 1;
+    fa.rf.advance = method != IRODORI_METHOD_HEUN || phase == 1;
     fa.rf.phase = phase;
     fa.rf.method = method;
     fa.rf.n = U * S * g.latent_dim;
     launch_final(fa, c->stream);
-    if (method != IRODORI_METHOD_HEUN || phase == 1) launch_step_advance(c->step, c->stream);
     return check_launch("sampler evaluation");
 }
 
@@ -878,7 +883,7 @@ int irodori_ctx_create(int device, const irodori_dit_config* cfg, irodori_ctx** 
     IRO_TRY(dalloc(c.get(), &c->in_w, sizeof(float) * (size_t)P * D));
     IRO_TRY(dalloc(c.get(), &c->in_b, sizeof(float) * D));
     IRO_TRY(dalloc(c.get(), &c->out_norm_w, sizeof(float) * D));
-    IRO_TRY(dalloc(c.get(), &c->out_wT, sizeof(float) * (size_t)P * D));
+    IRO_TRY(dalloc(c.get(), &c->out_w, sizeof(float) * (size_t)D * (P <= 32 ? 32 : 64)));
     IRO_TRY(dalloc(c.get(), &c->out_b, sizeof(float) * P));
 
     IRO_TRY(dalloc(c.get(), &c->x, sizeof(float) * M * D));
@@ -907,7 +912,7 @@ int irodori_ctx_create(int device, const irodori_dit_config* cfg, irodori_ctx** 
     IRO_TRY(dalloc(c.get(), &c->hist, sizeof(float) * 4 * M * P));
     IRO_TRY(dalloc(c.get(), &c->lat_bits, sizeof(unsigned long long) * (size_t)R * ((S + 63) / 64)));
     IRO_TRY(dalloc(c.get(), &c->lat_mask_f, sizeof(float) * (size_t)R * S));
-    IRO_TRY(dalloc(c.get(), &c->step, sizeof(int)));
+    IRO_TRY(dalloc(c.get(), &c->step, 2 * sizeof(int)));
     IRO_TRY(dalloc(c.get(), &c->zero_step, sizeof(int)));
     IRO_HIP_CHECK(hipMemsetAsync(c->zero_step, 0, sizeof(int), c->stream));
 
@@ -942,11 +947,13 @@ int irodori_load_io_weights(irodori_ctx* c, const irodori_io_weights* w) {
     IRO_TRY(upload(c, c->in_w, w->in_w, sizeof(float) * (size_t)P * D));
     IRO_TRY(upload(c, c->in_b, w->in_b, sizeof(float) * D));
     IRO_TRY(upload(c, c->out_norm_w, w->out_norm_w, sizeof(float) * D));
-    // Output head weight with the out_norm weight folded in, transposed to [P, D].
-    std::vector<float> wt((size_t)P * D);
+    // Output head weight with the out_norm weight folded in, rows padded to PW columns
+    // (zeros past P) for the head's whole-row loads.
+    const int PW = P <= 32 ? 32 : 64;
+    std::vector<float> wt((size_t)D * PW, 0.f);
     for (int d = 0; d < D; d++)
-        for (int p = 0; p < P; p++) wt[(size_t)p * D + d] = w->out_w[(size_t)d * P + p] * w->out_norm_w[d];
-    IRO_TRY(upload(c, c->out_wT, wt.data(), sizeof(float) * wt.size()));
+        for (int p = 0; p < P; p++) wt[(size_t)d * PW + p] = w->out_w[(size_t)d * P + p] * w->out_norm_w[d];
+    IRO_TRY(upload(c, c->out_w, wt.data(), sizeof(float) * wt.size()));
     IRO_TRY(upload(c, c->out_b, w->out_b, sizeof(float) * P));
     IRO_HIP_CHECK(hipStreamSynchronize(c->stream));
     c->io_loaded = true;
@@ -1577,7 +1584,7 @@ static int sample_device_impl(irodori_ctx* c, const irodori_sampler_params* p, i
     }
 
     launch_scale_copy(d_x0, c->xt, U * S * P, p->has_truncation ? p->truncation_factor : 1.0f, c->stream);
-    IRO_HIP_CHECK(hipMemsetAsync(c->step, 0, sizeof(int), c->stream));
+    IRO_HIP_CHECK(hipMemsetAsync(c->step, 0, 2 * sizeof(int), c->stream));
     IRO_TRY(check_launch("sampler setup"));
 
     // One captured graph per distinct evaluation (roles, phase), replayed per step.

@@ -48,11 +48,13 @@ void launch_norm_mod(const float* x, T* h, int M, int S, int D, float eps, ModTa
 // GEMM-operand form of h (e4m3 codes, E8M0 scales per 32 values; D % 32 == 0).
 // rstat (nullable; the fused adaLN of the bf16 model path, see GemmArgs): h gets
 // x (1 + scale) and rstat [M, D/32] the row sums of x^2 per 32 columns instead.
+// copies > 1: M rows computed, every output also written to the copies - 1 following
+// M-row blocks (rows that share their source row and modulation vector).
 template <typename T>
 void launch_inproj_norm(const float* x_src, int src_batches, const float* in_w,
                         const float* in_b, float* x, T* h, int M, int S, int P, int D,
                         float eps, ModTable mt, hipStream_t st, uint8_t* q8 = nullptr,
-                        uint8_t* q8s = nullptr, float* rstat = nullptr);
+                        uint8_t* q8s = nullptr, float* rstat = nullptr, int copies = 1);
 // The fused adaLN operand of (layer, kind) from x: h = x (1 + scale), rstat [M, D/32].
 template <typename T>
 void launch_mod_stats(const float* x, T* h, int M, int S, int D, ModTable mt, int layer, int kind, float* rstat,
@@ -86,18 +88,19 @@ struct RfUpdateArgs {
     float* xin;   // [n] Heun predictor state
     float* hist;  // [4][n]
     const RfEval* plan;  // null: no update (plain output head)
-    const int* step;
+    int* step;
+    int* done;    // advance set: workgroups finished, 0 between launches
+    int advance;  // the last workgroup to finish sets done = 0 and *step += 1
     int phase, method;
     int n;        // U * S * P
 };
 
 // Element j of the state after the guided velocity v of evaluation e (f32, in the
-// reference's operation order).
-__device__ inline void rf_apply(const RfUpdateArgs& a, const RfEval& e, int step, int j, float v) {
+// reference's operation order); x = a.x[j], loaded by the caller.
+__device__ inline void rf_apply(const RfUpdateArgs& a, const RfEval& e, int step, int j, float v, float x) {
     const bool corr = a.method == RF_HEUN && a.phase == 1;
-    const float xs = corr ? a.xin[j] : a.x[j];
+    const float xs = corr ? a.xin[j] : x;
     if (e.rescale) v = (v * e.omt + xs) * e.ratio / e.omt - xs / e.omt;  // math.rs:38-53
-    const float x = a.x[j];
     if (a.method == RF_EULER) {
         a.x[j] = x + v * e.dt;
     } else if (a.method == RF_HEUN) {
@@ -137,7 +140,7 @@ __device__ inline void rf_apply(const RfUpdateArgs& a, const RfEval& e, int step
 struct FinalArgs {
     const float* x;
     const float* norm_w;
-    const float* out_wT;  // [P, D] = (out_norm.weight (.) W_out)^T
+    const float* out_w;   // [D, PT] = out_norm.weight (.) W_out, PT = 32 (P <= 32) or 64, zero past P
     const float* out_b;   // [P]
     int B, S, D, P;
     float eps;
@@ -156,7 +159,6 @@ template <typename T>
 void launch_scale_ctx_aux(const T* src_k, const T* src_v, T* dst_k, T* dst_v, int rows,
                           int rows_scaled, int H, int T1, int vs1, int t_ctx, int aux_start,
                           float factor, hipStream_t st);
-void launch_step_advance(int* step, hipStream_t st);
 void launch_scale_copy(const float* src, float* dst, int n, float s, hipStream_t st);
 
 // ---- kernels_ops.hip -------------------------------------------------------------------

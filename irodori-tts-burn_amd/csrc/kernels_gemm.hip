@@ -861,9 +861,10 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
     } else if constexpr (EPI == EPI_QKVG) {
         // Each wave owns WM rows x one 64-column head of one region (q | k | v | gate).
         // The stage buffers are free once every wave is past the main loop; each wave then
-        // uses its own LDS slot: RoPE table rows (WM x 64 f32) and, for bf16, the staged
-        // q / k / gate tile (stage_off) written out with 16-byte stores; or the V^T transpose
-        // (64 x (WM + 2) elements; an odd word stride keeps both passes conflict-free).
+        // uses its own LDS slot: RoPE table rows (WM x 32 (cos, sin) pairs, f32) and, for
+        // bf16, the staged q / k / gate tile (stage_off) written out with 16-byte stores; or
+        // the V^T transpose (64 x (WM + 2) elements; an odd word stride keeps both passes
+        // conflict-free).
         constexpr int VT_BYTES = sizeof(T) == 2 ? 64 * (WM + 2) * 2 : 0;  // f32 scatters V^T directly
         constexpr int SLOT = WM * 256 > VT_BYTES ? WM * 256 : VT_BYTES;
         static_assert(STAGES * STAGE_BYTES >= NW * SLOT, "QKVG epilogue needs one LDS slot per wave");
@@ -872,27 +873,48 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
         const int region = col0 / D;
         const int h = (col0 % D) / Dh;
         const int half_heads = a.H / 2;
+        const int rw0 = m0 + wm0;  // first row of this wave
+        const bool rope = region <= 1 && h < half_heads;
+        // RoPE rows of the wave's WM tokens: lane task (r, k4) holds cos / sin of pairs
+        // 4 k4 .. 4 k4 + 3 at token r.  Loaded before the barrier (registers only), so their
+        // latency overlaps the wait for the other waves' main loops.
+        constexpr int RT_IT = WM / 8;
+        float4 rc[RT_IT], rs[RT_IT];
+        if (rope) {
+#pragma unroll
+            for (int it = 0; it < RT_IT; it++) {
+                const int idx = it * 64 + lane, r = idx >> 3, k4 = idx & 7;
+                int row = rw0 + r;
+                row = row < a.M ? row : a.M - 1;
+                int bq, sq;
+                row_bs(row, a.S, inv_s, bq, sq);
+                rc[it] = *reinterpret_cast<const float4*>(a.rope_cos + (size_t)sq * (Dh / 2) + k4 * 4);
+                rs[it] = *reinterpret_cast<const float4*>(a.rope_sin + (size_t)sq * (Dh / 2) + k4 * 4);
+            }
+        }
         __syncthreads();
         unsigned char* slot = smem + wave * SLOT;
-        const int rw0 = m0 + wm0;  // first row of this wave
         if (region <= 1) {
+            // Head RMSNorm weight, with the query scale folded in for q.
             const float* nwp = (region == 0 ? a.q_norm : a.k_norm) + h * Dh;
-            const float nw0 = nwp[cl], nw1 = nwp[32 + cl];
+            const float qs = region == 0 ? a.q_scale : 1.f;
+            const float nw0 = nwp[cl] * qs, nw1 = nwp[32 + cl] * qs;
             T* dst = region == 0 ? a.Q : a.Kd;
-            const bool rope = h < half_heads;
-            float* rt = reinterpret_cast<float*>(slot);  // [WM rows][cos 32 | sin 32]
+            float* rt = reinterpret_cast<float*>(slot);  // [WM rows][32 pairs][cos, sin]
             if (rope) {
 #pragma unroll
-                for (int it = 0; it < WM / 4; it++) {
-                    const int idx = it * 64 + lane, r = idx >> 4, q4 = idx & 15;
-                    int row = rw0 + r;
-                    row = row < a.M ? row : a.M - 1;
-                    int bq, sq;
-                    row_bs(row, a.S, inv_s, bq, sq);
-                    const float* tb = (q4 < 8 ? a.rope_cos : a.rope_sin) + (size_t)sq * (Dh / 2) + (q4 & 7) * 4;
-                    *reinterpret_cast<float4*>(rt + r * 64 + q4 * 4) = *reinterpret_cast<const float4*>(tb);
+                for (int it = 0; it < RT_IT; it++) {
+                    const int idx = it * 64 + lane, r = idx >> 3, k4 = idx & 7;
+                    float4* o = reinterpret_cast<float4*>(rt + r * 64 + k4 * 8);
+                    o[0] = make_float4(rc[it].x, rs[it].x, rc[it].y, rs[it].y);
+                    o[1] = make_float4(rc[it].z, rs[it].z, rc[it].w, rs[it].w);
                 }
             }
+            // Interleaved RoPE pairs (2k, 2k+1) sit in neighbouring lanes: the even lane
+            // takes y c - y' s, the odd one y c + y' s (y' the partner's value), so each
+            // lane hands its partner its value with the sign the partner needs.
+            const float sgn = (cl & 1) ? -1.f : 1.f;
+            const int k0 = cl >> 1, k1 = 16 + (cl >> 1);
 #pragma unroll
             for (int i = 0; i < FM; i++)
 #pragma unroll
@@ -904,17 +926,12 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
                     const float inv = __builtin_amdgcn_rsqf(ss * (1.f / (float)Dh) + a.eps);
                     float ya = y0 * inv * nw0, yb = y1 * inv * nw1;
                     if (rope) {
-                        // interleaved pairs (2k, 2k+1) sit in neighbouring lanes
-                        const float pa = IRO_DPP(ya, 0xB1), pb = IRO_DPP(yb, 0xB1);
-                        const int k0 = cl >> 1, k1 = 16 + (cl >> 1);
-                        const float c0 = rt[rl * 64 + k0], s0 = rt[rl * 64 + 32 + k0];
-                        const float c1 = rt[rl * 64 + k1], s1 = rt[rl * 64 + 32 + k1];
-                        ya = (cl & 1) ? (pa * s0 + ya * c0) : (ya * c0 - pa * s0);
-                        yb = (cl & 1) ? (pb * s1 + yb * c1) : (yb * c1 - pb * s1);
-                    }
-                    if (region == 0) {
-                        ya *= a.q_scale;
-                        yb *= a.q_scale;
+                        const float2 cs0 = *reinterpret_cast<const float2*>(rt + rl * 64 + 2 * k0);
+                        const float2 cs1 = *reinterpret_cast<const float2*>(rt + rl * 64 + 2 * k1);
+                        const float pa = IRO_DPP(ya * sgn, 0xB1) * cs0.y;
+                        const float pb = IRO_DPP(yb * sgn, 0xB1) * cs1.y;
+                        ya = fmaf(ya, cs0.x, pa);
+                        yb = fmaf(yb, cs1.x, pb);
                     }
                     if constexpr (sizeof(T) == 2) {
                         // Staged over the first half of row rl's table entries, which this

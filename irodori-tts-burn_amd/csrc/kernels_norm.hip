@@ -141,12 +141,15 @@ __global__ __launch_bounds__(256) void mod_stats_kernel(const float* __restrict_
 
 // With rstat set (the fused adaLN of the bf16 model path) h gets x (1 + scale) instead, and
 // rstat [M, D/32] the sums of x^2 per 32 columns (8 neighbouring lanes hold one block).
+// copies > 1: the M rows are computed once and every output (x, h, rstat, q8, q8s) is also
+// written to the copies - 1 row blocks that follow, M rows apart (batch rows that read the
+// same source row and modulation vector).
 template <typename T, int NCH, int ROWS>
 __global__ __launch_bounds__(256) void inproj_norm_kernel(
     const float* __restrict__ x_src, int src_batches, const float* __restrict__ in_w,
     const float* __restrict__ in_b, float* __restrict__ x, T* __restrict__ h, int M, int S, int P,
     int D, float eps, ModTable mt, uint8_t* __restrict__ q8, uint8_t* __restrict__ q8s,
-    float* __restrict__ rstat) {
+    float* __restrict__ rstat, int copies) {
     __shared__ float xs[ROWS][64];
     __shared__ float red[ROWS][4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -207,7 +210,9 @@ __global__ __launch_bounds__(256) void inproj_norm_kernel(
             const int d = 4 * tid + 1024 * j;
             if (d >= D) break;
             const float4 v = acc[r][j];
-            if (row < M) *reinterpret_cast<float4*>(x + (size_t)row * D + d) = v;
+            if (row < M)
+                for (int cp = 0; cp < copies; cp++)
+                    *reinterpret_cast<float4*>(x + ((size_t)cp * M + row) * D + d) = v;
             float q = v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
             ss += q;
             if (rstat) {
@@ -215,7 +220,9 @@ __global__ __launch_bounds__(256) void inproj_norm_kernel(
                 q += __shfl_xor(q, 1, 64);
                 q += __shfl_xor(q, 2, 64);
                 q += __shfl_xor(q, 4, 64);
-                if (row < M && (tid & 7) == 0) rstat[(size_t)row * (D / 32) + d / 32] = q;
+                if (row < M && (tid & 7) == 0)
+                    for (int cp = 0; cp < copies; cp++)
+                        rstat[((size_t)cp * M + row) * (D / 32) + d / 32] = q;
             }
         }
         ss = wave_sum(ss);
@@ -234,8 +241,9 @@ __global__ __launch_bounds__(256) void inproj_norm_kernel(
                 if (d >= D) break;
                 const float4 sc = *reinterpret_cast<const float4*>(scale + d);
                 const float4 v = acc[r][j];
-                store4<T>(h + (size_t)row * D + d, v.x * (1.f + sc.x), v.y * (1.f + sc.y), v.z * (1.f + sc.z),
-                          v.w * (1.f + sc.w));
+                for (int cp = 0; cp < copies; cp++)
+                    store4<T>(h + ((size_t)cp * M + row) * D + d, v.x * (1.f + sc.x), v.y * (1.f + sc.y),
+                              v.z * (1.f + sc.z), v.w * (1.f + sc.w));
             }
         }
         return;
@@ -257,37 +265,54 @@ __global__ __launch_bounds__(256) void inproj_norm_kernel(
             const float4 v = acc[r][j];
             const float h0 = v.x / rms * (1.f + sc.x) + sh.x, h1 = v.y / rms * (1.f + sc.y) + sh.y;
             const float h2 = v.z / rms * (1.f + sc.z) + sh.z, h3 = v.w / rms * (1.f + sc.w) + sh.w;
-            if (h) store4<T>(h + (size_t)row * D + d, h0, h1, h2, h3);
-            if (q8) mx_store4_group8(h0, h1, h2, h3, q8 + (size_t)row * D + d, q8s + (size_t)row * (D / 32) + d / 32, lane);
+            for (int cp = 0; cp < copies; cp++) {
+                const size_t cr = (size_t)cp * M + row;
+                if (h) store4<T>(h + cr * D + d, h0, h1, h2, h3);
+                if (q8) mx_store4_group8(h0, h1, h2, h3, q8 + cr * D + d, q8s + cr * (D / 32) + d / 32, lane);
+            }
         }
     }
 }
 
 // Output head: one 256-thread block per FR latent frames and row group (NR rows;
-// blockIdx.y strides over the groups).  v[b,s,p] = (sum_d x[b,s,d] * W'[p,d]) /
-// rms(x[b,s,:]) + b_out[p] with W' = out_norm.weight (.) W_out^T folded at ingest — the
-// same product as out_proj(out_norm(x)) (norm.rs:25-39, dit/model.rs:391-392).  The group's
-// rows are staged in LDS; thread (ks, p) computes output p over the k-slice ks for every
-// staged row (reading its own W' row once per block), and the KS slices are summed through
-// LDS.  Plain head: groups are consecutive rows.  Sampler evaluation: group u holds the
-// active roles' rows of utterance u, and the block applies the guided combine and the
-// integrator update to them (euler_sampler.rs:460-467, :497-510, :683-714) — one kernel
-// after the role chains join.
+// blockIdx.y strides over the groups).  v[b,s,p] = (sum_d x[b,s,d] * W'[d,p]) /
+// rms(x[b,s,:]) + b_out[p] with W' = out_norm.weight (.) W_out folded at ingest, stored
+// [D][PT] with the columns past P zero — the same product as out_proj(out_norm(x))
+// (norm.rs:25-39, dit/model.rs:391-392).  The group's rows are staged in LDS; thread
+// (kk, q) accumulates the output quad p = 4 q .. 4 q + 3 of every staged row over its own
+// KPT = D / KL consecutive k, so one wavefront load covers 64 / QN whole W' rows (coalesced;
+// W' is read once per block from L2) and a thread's loads sit at immediate offsets of one
+// base.  Staged rows keep 4 pad floats after every 32 (the 64 / QN distinct k of one LDS
+// read fall in distinct banks).  The first KB W' quads of each thread and the sampler state
+// the update reads are loaded before the rows are staged, so their latency overlaps the
+// staging.  The KL partial sums reduce across lanes, then across the 4 wavefronts through
+// LDS.  Plain head: groups are consecutive rows.  Sampler
+// evaluation: group u holds the active roles' rows of utterance u, and the block applies
+// the guided combine and the integrator update to them (euler_sampler.rs:460-467,
+// :497-510, :683-714) — one kernel after the role chains join.  With rf.advance set the
+// last workgroup to finish also advances the step counter (every workgroup has read it by
+// then).  Role and plan arrays are indexed by unrolled selects only (a runtime index would
+// place them in scratch).
 template <int PT, int NR, int FR>
 __global__ __launch_bounds__(256) void final_kernel(FinalArgs a) {
-    constexpr int KS = 256 / PT;
-    constexpr int R = NR * FR;  // staged row slot f * NR + i
+    constexpr int QN = PT / 4;    // output quads per W' row
+    constexpr int KL = 256 / QN;  // k positions per pass of the block
+    constexpr int R = NR * FR;    // staged row slot f * NR + i
+    // W' quads in flight per thread (offsets below 4 KB; all of them for D = 1024, PT = 32)
+    constexpr int KB = PT == 32 ? 32 : 16;
+    static_assert(FR * PT <= 256, "one update element per thread");
     extern __shared__ __attribute__((aligned(16))) float fsm[];
     const int D = a.D, P = a.P;
-    float* xs = fsm;                  // [R][D]
-    float* red = xs + R * D;          // [KS][R][PT]
-    float* vals = red + KS * R * PT;  // [R][PT]
-    float* rinv = vals + R * PT;      // [R]
+    const int DP = D + D / 8;        // staged row stride (4 pad floats per 32)
+    const int KPT = D / KL;          // D % KL == 0
+    float* xs = fsm;                 // [R][DP]
+    float* red = xs + R * DP;        // [4][R][PT]
+    float* vals = red + 4 * R * PT;  // [R][PT]
+    float* rinv = vals + R * PT;     // [R]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int p = tid % PT, ks = tid / PT;
+    const int q = tid % QN, kk = tid / QN;
     const int s0 = blockIdx.x * FR;
     const int nf = a.S - s0 < FR ? a.S - s0 : FR;
-    const int kper = D / KS;
     const bool rf = a.rf.plan != nullptr;
     int step = 0;
     RfEval ev{};
@@ -300,60 +325,92 @@ __global__ __launch_bounds__(256) void final_kernel(FinalArgs a) {
         // Row of slot i: the group's i-th row (a plain head's short last group repeats its
         // first row); frames past S stage zeros.
         auto row_of = [&](int i) {
-            if (rf) return a.role[i] * a.B + g;
+            if (rf) {
+                int ro = a.role[0];
+#pragma unroll
+                for (int k = 1; k < NR; k++)
+                    if (i == k) ro = a.role[k];
+                return ro * a.B + g;
+            }
             const int b = g * NR + i;
             return b < a.B ? b : g * NR;
         };
+        const int kb0 = kk * KPT;
+        const float* wq = a.out_w + (size_t)kb0 * PT + 4 * q;
+        // Whole batches of KB thread-local k (the first one issued now), then a tail of
+        // single k when KB does not divide KPT.
+        float4 w[KB];
+        if (KPT >= KB) {
+#pragma unroll
+            for (int i = 0; i < KB; i++) w[i] = *reinterpret_cast<const float4*>(wq + (size_t)i * PT);
+        }
+        // Sampler state element of this thread's update (thread e < nf * PT: frame e / PT,
+        // column e % PT).
+        float xst = 0.f;
+        if (rf && tid < nf * PT && tid % PT < P) xst = a.rf.x[(g * a.S + s0 + tid / PT) * P + tid % PT];
         __syncthreads();
         for (int e = tid * 4; e < R * D; e += 1024) {
             const int r = e / D, d = e % D, f = r / NR, i = r % NR;
             float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
             if (f < nf) v = *reinterpret_cast<const float4*>(a.x + ((size_t)row_of(i) * a.S + s0 + f) * D + d);
-            *reinterpret_cast<float4*>(xs + r * D + d) = v;
+            *reinterpret_cast<float4*>(xs + r * DP + d + 4 * (d >> 5)) = v;
         }
         __syncthreads();
         for (int r = wave; r < R; r += 4) {
             float ss = 0.f;
-            for (int d = lane; d < D; d += 64) ss += xs[r * D + d] * xs[r * D + d];
+            for (int d = lane; d < D; d += 64) {
+                const float xv = xs[r * DP + d + 4 * (d >> 5)];
+                ss += xv * xv;
+            }
             ss = wave_sum(ss);
             if (lane == 0) rinv[r] = 1.f / sqrtf(ss / (float)D + a.eps);
         }
-        float acc[R];
+        float4 acc[R];
 #pragma unroll
-        for (int r = 0; r < R; r++) acc[r] = 0.f;
-        if (p < P) {
-            // 16 W' quads are loaded together so their latencies overlap (kper % 8 == 0).
-            const float* wr = a.out_wT + (size_t)p * D;
-            const int kend = (ks + 1) * kper;
-            for (int k0 = ks * kper; k0 < kend; k0 += 64) {
-                float4 w[16];
+        for (int r = 0; r < R; r++) acc[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+        auto fma_k = [&](int k, const float4& wv) {  // k: row of W' and column of the staged rows
+            const int kx = k + 4 * (k >> 5);
 #pragma unroll
-                for (int i = 0; i < 16; i++)
-                    w[i] = k0 + 4 * i < kend ? *reinterpret_cast<const float4*>(wr + k0 + 4 * i)
-                                             : make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    if (k0 + 4 * i >= kend) break;
-#pragma unroll
-                    for (int r = 0; r < R; r++) {
-                        const float4 xv = *reinterpret_cast<const float4*>(xs + r * D + k0 + 4 * i);
-                        acc[r] += xv.x * w[i].x + xv.y * w[i].y + xv.z * w[i].z + xv.w * w[i].w;
-                    }
-                }
+            for (int r = 0; r < R; r++) {
+                const float xv = xs[r * DP + kx];
+                acc[r].x += xv * wv.x;
+                acc[r].y += xv * wv.y;
+                acc[r].z += xv * wv.z;
+                acc[r].w += xv * wv.w;
             }
-        }
+        };
+        int k0 = 0;
+        for (; k0 + KB <= KPT; k0 += KB) {
+            if (k0 > 0) {
 #pragma unroll
-        for (int r = 0; r < R; r++) red[(ks * R + r) * PT + p] = acc[r];
+                for (int i = 0; i < KB; i++) w[i] = *reinterpret_cast<const float4*>(wq + (size_t)(k0 + i) * PT);
+            }
+#pragma unroll
+            for (int i = 0; i < KB; i++) fma_k(kb0 + k0 + i, w[i]);
+        }
+        for (; k0 < KPT; k0++) fma_k(kb0 + k0, *reinterpret_cast<const float4*>(wq + (size_t)k0 * PT));
+        // Lanes q, q + QN, ... of a wavefront hold one quad's partial sums.
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            float4 v = acc[r];
+#pragma unroll
+            for (int m = QN; m < 64; m <<= 1) {
+                v.x += __shfl_xor(v.x, m, 64);
+                v.y += __shfl_xor(v.y, m, 64);
+                v.z += __shfl_xor(v.z, m, 64);
+                v.w += __shfl_xor(v.w, m, 64);
+            }
+            if (lane < QN) *reinterpret_cast<float4*>(red + (wave * R + r) * PT + 4 * q) = v;
+        }
         __syncthreads();
         for (int idx = tid; idx < R * PT; idx += 256) {  // R * PT may exceed the block
             const int r = idx / PT, pp = idx % PT;
-            float v = 0.f;
-#pragma unroll
-            for (int k2 = 0; k2 < KS; k2++) v += red[(k2 * R + r) * PT + pp];
+            const float v = red[r * PT + pp] + red[(R + r) * PT + pp] + red[(2 * R + r) * PT + pp] +
+                            red[(3 * R + r) * PT + pp];
             vals[r * PT + pp] = pp < P ? v * rinv[r] + a.out_b[pp] : 0.f;
         }
         __syncthreads();
-        for (int e = tid; e < nf * PT; e += 256) {
+        for (int e = tid; e < nf * PT; e += 256) {  // nf * PT <= 256: one pass
             const int f = e / PT, pp = e % PT, sq = s0 + f;
             if (pp >= P) continue;
             if (!rf) {
@@ -364,20 +421,28 @@ __global__ __launch_bounds__(256) void final_kernel(FinalArgs a) {
             }
             const float v0 = vals[(f * NR) * PT + pp];
             float v = v0;
-            for (int k = 0; k < ev.nterm; k++) {
+#pragma unroll
+            for (int k = 0; k < 3; k++) {
+                if (k >= ev.nterm) break;
                 int slot = 0;
 #pragma unroll
                 for (int i = 1; i < NR; i++)
                     if (a.role[i] == ev.role[k]) slot = i;
                 v = v + (v0 - vals[(f * NR + slot) * PT + pp]) * ev.scale[k];
             }
-            rf_apply(a.rf, ev, step, (g * a.S + sq) * P + pp, v);
+            rf_apply(a.rf, ev, step, (g * a.S + sq) * P + pp, v, xst);
         }
     }
-}
-
-__global__ void step_advance_kernel(int* step) {
-    if (threadIdx.x == 0) *step = *step + 1;
+    if (rf && a.rf.advance) {
+        __syncthreads();
+        if (tid == 0) {
+            const int total = gridDim.x * gridDim.y;
+            if (atomicAdd(a.rf.done, 1) == total - 1) {
+                *a.rf.done = 0;
+                *a.rf.step = step + 1;
+            }
+        }
+    }
 }
 
 __global__ void scale_copy_kernel(const float* __restrict__ src, float* __restrict__ dst, int n,
@@ -430,13 +495,13 @@ template void launch_mod_stats<bf16>(const float*, bf16*, int, int, int, ModTabl
 template <typename T>
 void launch_inproj_norm(const float* x_src, int src_batches, const float* in_w,
                         const float* in_b, float* x, T* h, int M, int S, int P, int D, float eps,
-                        ModTable mt, hipStream_t st, uint8_t* q8, uint8_t* q8s, float* rstat) {
+                        ModTable mt, hipStream_t st, uint8_t* q8, uint8_t* q8s, float* rstat, int copies) {
     const int nch = (D + 1023) / 1024;
     const bool fine = (M + 7) / 8 < 512;  // fewer than two blocks per CU at 8 rows
     const int rows = fine ? 2 : 8, grid = (M + rows - 1) / rows;
 #define IRO_INPROJ(N, R)                                                                      \
     inproj_norm_kernel<T, N, R><<<grid, 256, 0, st>>>(x_src, src_batches, in_w, in_b, x, h, M, \
-                                                      S, P, D, eps, mt, q8, q8s, rstat)
+                                                      S, P, D, eps, mt, q8, q8s, rstat, copies)
     if (fine) {
         if (nch <= 1) IRO_INPROJ(1, 2);
         else if (nch <= 2) IRO_INPROJ(2, 2);
@@ -455,17 +520,17 @@ template void launch_norm_mod<bf16>(const float*, bf16*, int, int, int, float, M
                                     int, hipStream_t, uint8_t*, uint8_t*);
 template void launch_inproj_norm<float>(const float*, int, const float*, const float*, float*,
                                         float*, int, int, int, int, float, ModTable,
-                                        hipStream_t, uint8_t*, uint8_t*, float*);
+                                        hipStream_t, uint8_t*, uint8_t*, float*, int);
 template void launch_inproj_norm<bf16>(const float*, int, const float*, const float*, float*,
                                        bf16*, int, int, int, int, float, ModTable, hipStream_t,
-                                       uint8_t*, uint8_t*, float*);
+                                       uint8_t*, uint8_t*, float*, int);
 
 template <int PT, int NR, int FR>
 static void launch_final_cfg(const FinalArgs& a, hipStream_t st) {
-    constexpr int KS = 256 / PT, R = NR * FR;
-    const size_t lds = sizeof(float) * ((size_t)R * a.D + (size_t)KS * R * PT + (size_t)R * PT + R);
+    constexpr int R = NR * FR;
+    const size_t lds = sizeof(float) * ((size_t)R * (a.D + a.D / 8) + (size_t)4 * R * PT + (size_t)R * PT + R);
     // Sized for the largest model width the context accepts (D <= 2048).
-    constexpr int kMax = (int)sizeof(float) * (R * 2048 + KS * R * PT + R * PT + R);
+    constexpr int kMax = (int)sizeof(float) * (R * (2048 + 256) + 4 * R * PT + R * PT + R);
     static std::once_flag once;
     static hipError_t attr_rc = hipSuccess;
     (void)set_lds_limit_once(once, attr_rc, (const void*)final_kernel<PT, NR, FR>, kMax);
@@ -474,8 +539,8 @@ static void launch_final_cfg(const FinalArgs& a, hipStream_t st) {
     final_kernel<PT, NR, FR><<<grid, 256, lds, st>>>(a);
 }
 
-// Four frames per block, or one when that leaves too few blocks to fill the chip (each
-// block re-reads W' from L2, so coarser blocks win once there are enough of them).
+// Four, two or one frames per block: the most that still gives 256 blocks (each block reads
+// all of W' from L2, so coarser blocks win once there are enough of them).
 template <int PT, int FR>
 static void launch_final_fr(const FinalArgs& a, hipStream_t st) {
     const int nr = a.rf.plan ? a.nrole : 2;
@@ -487,8 +552,9 @@ template <int PT>
 static void launch_final_pt(const FinalArgs& a, hipStream_t st) {
     const int nr = a.rf.plan ? a.nrole : 2;
     const int ngroups = a.rf.plan ? a.B : (a.B + nr - 1) / nr;
-    if ((long)((a.S + 3) / 4) * ngroups < 512) launch_final_fr<PT, 1>(a, st);
-    else launch_final_fr<PT, 4>(a, st);
+    if ((long)((a.S + 3) / 4) * ngroups >= 256) launch_final_fr<PT, 4>(a, st);
+    else if ((long)((a.S + 1) / 2) * ngroups >= 256) launch_final_fr<PT, 2>(a, st);
+    else launch_final_fr<PT, 1>(a, st);
 }
 
 void launch_final(const FinalArgs& a, hipStream_t st) {
@@ -496,7 +562,6 @@ void launch_final(const FinalArgs& a, hipStream_t st) {
     else launch_final_pt<64>(a, st);
 }
 
-void launch_step_advance(int* step, hipStream_t st) { step_advance_kernel<<<1, 64, 0, st>>>(step); }
 
 void launch_scale_copy(const float* src, float* dst, int n, float s, hipStream_t st) {
     scale_copy_kernel<<<(n + 255) / 256, 256, 0, st>>>(src, dst, n, s);
