@@ -29,6 +29,8 @@
 //   EPI_QKVG   q,k: head RMSNorm (norm.rs:60-74) + half RoPE (rope.rs:82-135);
 //              q pre-scaled by Dh^-1/2 log2(e) for the attention softmax;
 //              v: scatter to V^T [B,H,Dh,S'] (key-permuted); gate: sigmoid (attention.rs:423)
+#include <type_traits>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -186,9 +188,12 @@ __device__ __forceinline__ const float* gate_vec(const ModTable& mt, int b, int 
     return mt.tab + ((size_t)vec * mt.layers * 6 + (size_t)layer * 6 + kind * 3 + 2) * D;
 }
 
+// Four-wave workgroups are sized for two per CU (LDS), so they ask the compiler for two
+// waves per SIMD: at most 256 registers per wave, accumulators included.
 template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int EPI, bool F8 = false,
           bool CONV = false>
-__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T> a) {
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N)
+__attribute__((amdgpu_waves_per_eu(WAVES_M * WAVES_N == 4 ? 2 : 1))) void gemm_kernel(GemmArgs<T> a) {
     constexpr int NW = WAVES_M * WAVES_N;
     constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
     constexpr int FM = WM / 32, FN = WN / 32;
@@ -730,31 +735,54 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
                         }
                     }
                 }
-        } else
+        } else {
+            // One straight-line body per (all rows inside M, fused output) pair, both uniform
+            // per wave: per-element tests would split the stores into separate blocks.
+            auto resid_rows = [&](auto full_c, auto fuse_c) {
+                constexpr bool FULL = decltype(full_c)::value, FUSE = decltype(fuse_c)::value;
 #pragma unroll
-        for (int i = 0; i < FM; i++) {
+                for (int i = 0; i < FM; i++) {
 #pragma unroll
-            for (int j = 0; j < FN; j++) {
-                float sq[16];
+                    for (int j = 0; j < FN; j++) {
+                        float sq[16];
+                        const size_t off0 = (size_t)(rbase + 32 * i) * a.N + n0 + wn0 + 32 * j + cl;
+                        float* xr = xg + off0;
+                        [[maybe_unused]] T* hr = a.Hn + off0;
 #pragma unroll
-                for (int e = 0; e < 16; e++) {
-                    const int row = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
-                    const bool ok = row < a.M;
-                    const int u = row >= hi_row[i] ? 1 : 0;
-                    const float xn = xpre[i][e][j] + gpre[i][u][j] * acc[i][j][e];
-                    sq[e] = ok ? xn * xn : 0.f;
-                    if (ok) xg[(size_t)row * a.N + n0 + wn0 + 32 * j + cl] = xn;
-                    if (fuse_out && ok)
-                        a.Hn[(size_t)row * a.N + n0 + wn0 + 32 * j + cl] = from_f32<T>(xn * (1.f + spre[i][u][j]));
+                        for (int e = 0; e < 16; e++) {
+                            const int ro = 8 * (e >> 2) + (e & 3);  // row offset from rbase + 32 i
+                            const int row = rbase + 32 * i + ro;
+                            const bool ok = FULL || row < a.M;
+                            const int u = row >= hi_row[i] ? 1 : 0;
+                            const float xn = xpre[i][e][j] + gpre[i][u][j] * acc[i][j][e];
+                            sq[e] = ok ? xn * xn : 0.f;
+                            if constexpr (FULL) {
+                                xr[(size_t)ro * a.N] = xn;
+                                if constexpr (FUSE) hr[(size_t)ro * a.N] = from_f32<T>(xn * (1.f + spre[i][u][j]));
+                            } else if (ok) {
+                                xr[(size_t)ro * a.N] = xn;
+                                if constexpr (FUSE) hr[(size_t)ro * a.N] = from_f32<T>(xn * (1.f + spre[i][u][j]));
+                            }
+                        }
+                        if constexpr (FUSE) {
+                            // Row sums over the half-wave's 32 columns: a halving butterfly over
+                            // lane bits 4..1 (each step keeps half the rows and adds the partner's
+                            // values of them), then bit 0; lane l ends with row
+                            // e = 8 b4 + 4 b3 + 2 b2 + b1 of l.
+                            const int e = half_wave_row_sums(sq, cl);
+                            const int row = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
+                            if (row < a.M && (cl & 1) == 0) a.rstat_out[(size_t)row * np + (n0 + wn0) / 32 + j] = sq[0];
+                        }
+                    }
                 }
-                if (fuse_out) {
-                    // Row sums over the half-wave's 32 columns: a halving butterfly over lane
-                    // bits 4..1 (each step keeps half the rows and adds the partner's values of
-                    // them), then bit 0; lane l ends with row e = 8 b4 + 4 b3 + 2 b2 + b1 of l.
-                    const int e = half_wave_row_sums(sq, cl);
-                    const int row = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
-                    if (row < a.M && (cl & 1) == 0) a.rstat_out[(size_t)row * np + (n0 + wn0) / 32 + j] = sq[0];
-                }
+            };
+            const bool full = m0 + wm0 + WM <= a.M;
+            if (full) {
+                if (fuse_out) resid_rows(std::true_type{}, std::true_type{});
+                else resid_rows(std::true_type{}, std::false_type{});
+            } else {
+                if (fuse_out) resid_rows(std::false_type{}, std::true_type{});
+                else resid_rows(std::false_type{}, std::false_type{});
             }
         }
     } else if constexpr (EPI == EPI_SWIGLU) {
@@ -808,19 +836,24 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
                 __builtin_amdgcn_wave_barrier();  // the slot is rewritten by the next pair
             }
         } else {
+            // Straight-line stores when every row of the wave is inside M (uniform).
+            auto swiglu_rows = [&](auto full_c) {
+                constexpr bool FULL = decltype(full_c)::value;
 #pragma unroll
-        for (int i = 0; i < FM; i++)
+                for (int i = 0; i < FM; i++) {
+                    T* ur = a.U + (size_t)(rbase + 32 * i) * half_n + (n0 + wn0) / 2 + cl;
 #pragma unroll
-            for (int e = 0; e < 16; e++) {
-                int row = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
-                if (row >= a.M) continue;
+                    for (int e = 0; e < 16; e++) {
+                        const int ro = 8 * (e >> 2) + (e & 3);
+                        if (!FULL && rbase + 32 * i + ro >= a.M) continue;
 #pragma unroll
-                for (int j = 0; j < FN; j += 2) {
-                    int pair = (n0 + wn0) / 64 + j / 2;
-                    float u1 = acc[i][j][e], u3 = acc[i][j + 1][e];
-                    a.U[(size_t)row * half_n + pair * 32 + cl] = from_f32<T>(silu_f(u1) * u3);
+                        for (int j = 0; j < FN; j += 2)
+                            ur[(size_t)ro * half_n + 16 * j] = from_f32<T>(silu_f(acc[i][j][e]) * acc[i][j + 1][e]);
+                    }
                 }
-            }
+            };
+            if (m0 + wm0 + WM <= a.M) swiglu_rows(std::true_type{});
+            else swiglu_rows(std::false_type{});
         }
     } else if constexpr (EPI == EPI_CTXKV) {
         // One 64-column head per wave: region 0 = K (head RMSNorm, norm.rs:60-74, no RoPE),
@@ -881,15 +914,19 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
         constexpr int RT_IT = WM / 8;
         float4 rc[RT_IT], rs[RT_IT];
         if (rope) {
+            // Lane task it: token row rw0 + 8 it + lane / 8.  With S >= 8 the token index
+            // steps by 8 with one wrap at most (rows past M wrap too and read a valid table
+            // row, unused); otherwise each row is located on its own.
+            const int k4 = lane & 7;
+            int bq, sq;
+            row_bs(min(rw0 + (lane >> 3), a.M - 1), a.S, inv_s, bq, sq);
 #pragma unroll
             for (int it = 0; it < RT_IT; it++) {
-                const int idx = it * 64 + lane, r = idx >> 3, k4 = idx & 7;
-                int row = rw0 + r;
-                row = row < a.M ? row : a.M - 1;
-                int bq, sq;
-                row_bs(row, a.S, inv_s, bq, sq);
+                if (a.S < 8) row_bs(min(rw0 + it * 8 + (lane >> 3), a.M - 1), a.S, inv_s, bq, sq);
                 rc[it] = *reinterpret_cast<const float4*>(a.rope_cos + (size_t)sq * (Dh / 2) + k4 * 4);
                 rs[it] = *reinterpret_cast<const float4*>(a.rope_sin + (size_t)sq * (Dh / 2) + k4 * 4);
+                sq += 8;
+                sq = sq >= a.S ? sq - a.S : sq;
             }
         }
         __syncthreads();
@@ -915,48 +952,88 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
             // lane hands its partner its value with the sign the partner needs.
             const float sgn = (cl & 1) ? -1.f : 1.f;
             const int k0 = cl >> 1, k1 = 16 + (cl >> 1);
+            // One straight-line body per RoPE setting (the flag is uniform per wave): a
+            // runtime test inside the unrolled rows would split them into separate blocks
+            // and serialise each row's reduction and table reads.
+            auto qk_rows = [&](auto rope_c) {
+                constexpr bool ROPE = decltype(rope_c)::value;
 #pragma unroll
-            for (int i = 0; i < FM; i++)
+                for (int i = 0; i < FM; i++)
 #pragma unroll
-                for (int e = 0; e < 16; e++) {
-                    const int rl = 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);  // row within the wave
-                    const int row = rw0 + rl;
-                    const float y0 = acc[i][0][e], y1 = acc[i][1][e];
-                    const float ss = half_wave_sum(y0 * y0 + y1 * y1);
-                    const float inv = __builtin_amdgcn_rsqf(ss * (1.f / (float)Dh) + a.eps);
-                    float ya = y0 * inv * nw0, yb = y1 * inv * nw1;
-                    if (rope) {
-                        const float2 cs0 = *reinterpret_cast<const float2*>(rt + rl * 64 + 2 * k0);
-                        const float2 cs1 = *reinterpret_cast<const float2*>(rt + rl * 64 + 2 * k1);
-                        const float pa = IRO_DPP(ya * sgn, 0xB1) * cs0.y;
-                        const float pb = IRO_DPP(yb * sgn, 0xB1) * cs1.y;
-                        ya = fmaf(ya, cs0.x, pa);
-                        yb = fmaf(yb, cs1.x, pb);
+                    for (int e = 0; e < 16; e++) {
+                        const int rl = 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);  // row within the wave
+                        const int row = rw0 + rl;
+                        const float y0 = acc[i][0][e], y1 = acc[i][1][e];
+                        const float ss = half_wave_sum(y0 * y0 + y1 * y1);
+                        const float inv = __builtin_amdgcn_rsqf(ss * (1.f / (float)Dh) + a.eps);
+                        float ya = y0 * inv * nw0, yb = y1 * inv * nw1;
+                        if constexpr (ROPE) {
+                            const float2 cs0 = *reinterpret_cast<const float2*>(rt + rl * 64 + 2 * k0);
+                            const float2 cs1 = *reinterpret_cast<const float2*>(rt + rl * 64 + 2 * k1);
+                            const float pa = IRO_DPP(ya * sgn, 0xB1) * cs0.y;
+                            const float pb = IRO_DPP(yb * sgn, 0xB1) * cs1.y;
+                            ya = fmaf(ya, cs0.x, pa);
+                            yb = fmaf(yb, cs1.x, pb);
+                        }
+                        if constexpr (sizeof(T) == 2) {
+                            acc[i][0][e] = ya;
+                            acc[i][1][e] = yb;
+                        } else if (row < a.M) {
+                            int b, sq;
+                            row_bs(row, a.S, inv_s, b, sq);
+                            T* o = dst + (((size_t)b * a.H + h) * a.S + sq) * Dh;
+                            o[cl] = from_f32<T>(ya);
+                            o[32 + cl] = from_f32<T>(yb);
+                        }
                     }
-                    if constexpr (sizeof(T) == 2) {
-                        // Staged over the first half of row rl's table entries, which this
-                        // step has already read (each row is handled in exactly one step).
-                        *reinterpret_cast<T*>(slot + stage_off(rl, cl)) = from_f32<T>(ya);
-                        *reinterpret_cast<T*>(slot + stage_off(rl, 32 + cl)) = from_f32<T>(yb);
-                    } else if (row < a.M) {
+            };
+            if (rope)
+                qk_rows(std::true_type{});
+            else
+                qk_rows(std::false_type{});
+            if constexpr (sizeof(T) == 2) {
+                // Staged over the table once every row is computed (the stage overlaps the
+                // table, so staging inside the loop above would order each row's table reads
+                // after the previous row's stage writes).
+#pragma unroll
+                for (int i = 0; i < FM; i++)
+#pragma unroll
+                    for (int e = 0; e < 16; e++) {
+                        const int rl = 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+                        *reinterpret_cast<T*>(slot + stage_off(rl, cl)) = from_f32<T>(acc[i][0][e]);
+                        *reinterpret_cast<T*>(slot + stage_off(rl, 32 + cl)) = from_f32<T>(acc[i][1][e]);
+                    }
+                // 16-byte stores: 8 lanes per 128-byte head row of [B, H, S, Dh]; pass it
+                // writes token row rw0 + 8 it + lane / 8.  All staged reads are issued first.
+                const int c = lane & 7;
+                uint4 sv[WM / 8];
+#pragma unroll
+                for (int it = 0; it < WM / 8; it++)
+                    sv[it] = *reinterpret_cast<const uint4*>(slot + stage_off(it * 8 + (lane >> 3), 8 * c));
+                if (a.S >= 8 && rw0 + WM <= a.M) {
+                    // Every row is inside M: the destination steps by 8 tokens, moving to the
+                    // next batch row (H - 1 head blocks further) when the token index wraps.
+                    int b, sq;
+                    row_bs(rw0 + (lane >> 3), a.S, inv_s, b, sq);
+                    T* o = dst + (((size_t)b * a.H + h) * a.S + sq) * Dh + 8 * c;
+                    const size_t wrap_add = (size_t)(a.H - 1) * a.S * Dh;
+#pragma unroll
+                    for (int it = 0; it < WM / 8; it++) {
+                        *reinterpret_cast<uint4*>(o) = sv[it];
+                        sq += 8;
+                        const bool wrap = sq >= a.S;
+                        sq = wrap ? sq - a.S : sq;
+                        o += 8 * Dh + (wrap ? wrap_add : 0);
+                    }
+                } else {
+#pragma unroll
+                    for (int it = 0; it < WM / 8; it++) {
+                        const int row = rw0 + it * 8 + (lane >> 3);
+                        if (row >= a.M) continue;
                         int b, sq;
                         row_bs(row, a.S, inv_s, b, sq);
-                        T* o = dst + (((size_t)b * a.H + h) * a.S + sq) * Dh;
-                        o[cl] = from_f32<T>(ya);
-                        o[32 + cl] = from_f32<T>(yb);
+                        *reinterpret_cast<uint4*>(dst + (((size_t)b * a.H + h) * a.S + sq) * Dh + 8 * c) = sv[it];
                     }
-                }
-            if constexpr (sizeof(T) == 2) {
-                // 16-byte stores: 8 lanes per 128-byte head row of [B, H, S, Dh].
-#pragma unroll
-                for (int it = 0; it < WM / 8; it++) {
-                    const int r = it * 8 + (lane >> 3), c = lane & 7;
-                    const int row = rw0 + r;
-                    if (row >= a.M) continue;
-                    int b, sq;
-                    row_bs(row, a.S, inv_s, b, sq);
-                    const uint4 v = *reinterpret_cast<const uint4*>(slot + stage_off(r, 8 * c));
-                    *reinterpret_cast<uint4*>(dst + (((size_t)b * a.H + h) * a.S + sq) * Dh + 8 * c) = v;
                 }
             }
         } else if (region == 2) {
@@ -974,29 +1051,36 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
 #pragma unroll
                         for (int j = 0; j < 2; j++) vt[(32 * j + cl) * VS + rl] = from_f32<T>(acc[i][j][e]);
                     }
-#pragma unroll
-                for (int it = 0; it < WM / 2; it++) {
-                    const int t = it * 64 + lane;
-                    const int d = t / (WM / 2), p = t % (WM / 2);  // dim d, token pair p
-                    const int row = rw0 + 2 * p;
-                    if (row >= a.M) continue;
+                // Pass it covers dims d = it * (64 / PP) + lane / PP of token pair p = lane % PP,
+                // the same pair in every pass, so the pair's position and the choice between
+                // one word and two elements are decided once per lane.
+                constexpr int PP = WM / 2;  // token pairs per wave
+                static_assert(64 % PP == 0, "a lane keeps one token pair");
+                const int p = lane % PP, row = rw0 + 2 * p;
+                if (row < a.M) {
                     int b, sq;
                     row_bs(row, a.S, inv_s, b, sq);
                     // One word only for an even token with its successor in the same batch
                     // row: (s, s+1) are then adjacent and 4-byte aligned under the key
                     // permutation.  With odd S, odd batch rows start on an odd token.
                     if (!(sq & 1) && sq + 1 < a.S && row + 1 < a.M) {
-                        T* o = a.Vd + (((size_t)b * a.H + h) * Dh + d) * a.vt_stride;
-                        *reinterpret_cast<unsigned*>(o + vt_pos_bf16(sq)) =
-                            *reinterpret_cast<const unsigned*>(vt + d * VS + 2 * p);
-                    } else {
+                        T* o = a.Vd + ((size_t)b * a.H + h) * Dh * a.vt_stride + vt_pos_bf16(sq);
 #pragma unroll
-                        for (int u = 0; u < 2; u++) {
-                            const int r2 = row + u;
-                            if (r2 >= a.M) break;
-                            int b2, s2;
-                            row_bs(r2, a.S, inv_s, b2, s2);
-                            a.Vd[(((size_t)b2 * a.H + h) * Dh + d) * a.vt_stride + vt_pos_bf16(s2)] = vt[d * VS + 2 * p + u];
+                        for (int it = 0; it < PP; it++) {
+                            const int d = it * (64 / PP) + lane / PP;
+                            *reinterpret_cast<unsigned*>(o + (size_t)d * a.vt_stride) =
+                                *reinterpret_cast<const unsigned*>(vt + d * VS + 2 * p);
+                        }
+                    } else {
+                        const bool has2 = row + 1 < a.M;
+                        int b2 = b, s2 = sq;
+                        if (has2) row_bs(row + 1, a.S, inv_s, b2, s2);
+                        T* o0 = a.Vd + ((size_t)b * a.H + h) * Dh * a.vt_stride + vt_pos_bf16(sq);
+                        T* o1 = a.Vd + ((size_t)b2 * a.H + h) * Dh * a.vt_stride + vt_pos_bf16(s2);
+                        for (int it = 0; it < PP; it++) {
+                            const int d = it * (64 / PP) + lane / PP;
+                            o0[(size_t)d * a.vt_stride] = vt[d * VS + 2 * p];
+                            if (has2) o1[(size_t)d * a.vt_stride] = vt[d * VS + 2 * p + 1];
                         }
                     }
                 }
@@ -1028,14 +1112,19 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_kernel(GemmArgs<T
                     for (int j = 0; j < 2; j++)
                         *reinterpret_cast<T*>(slot + stage_off(rl, 32 * j + cl)) = from_f32<T>(sigmoid_f(acc[i][j][e]));
                 }
-            T* gdst = a.G + (col0 - 3 * D);
+            const int c = lane & 7;
+            T* gdst = a.G + (col0 - 3 * D) + (size_t)(rw0 + (lane >> 3)) * D + 8 * c;
+            uint4 sv[WM / 8];
 #pragma unroll
-            for (int it = 0; it < WM / 8; it++) {
-                const int r = it * 8 + (lane >> 3), c = lane & 7;
-                const int row = rw0 + r;
-                if (row >= a.M) continue;
-                const uint4 v = *reinterpret_cast<const uint4*>(slot + stage_off(r, 8 * c));
-                *reinterpret_cast<uint4*>(gdst + (size_t)row * D + 8 * c) = v;
+            for (int it = 0; it < WM / 8; it++)
+                sv[it] = *reinterpret_cast<const uint4*>(slot + stage_off(it * 8 + (lane >> 3), 8 * c));
+            if (rw0 + WM <= a.M) {
+#pragma unroll
+                for (int it = 0; it < WM / 8; it++) *reinterpret_cast<uint4*>(gdst + (size_t)it * 8 * D) = sv[it];
+            } else {
+#pragma unroll
+                for (int it = 0; it < WM / 8; it++)
+                    if (rw0 + it * 8 + (lane >> 3) < a.M) *reinterpret_cast<uint4*>(gdst + (size_t)it * 8 * D) = sv[it];
             }
         } else {
 #pragma unroll
