@@ -175,9 +175,27 @@ __device__ __forceinline__ bool merge_parities(unsigned char* smem, int par, int
 
 // Normalise, gate and store one 32-query block: o[db][e] = O[q][32 db + 8 (e / 4) + 4 fh +
 // e % 4] for this lane's query q (lanes l and l ^ 32 hold the two halves of its dims).
+// Gate values of one lane's output dims (out_mode 0): dims 32 db + 8 g4 + 4 fh .. + 3.
+template <typename T>
+struct GateQuads {
+    typedef T T4 __attribute__((ext_vector_type(4)));
+    T4 v[2][4];
+};
+template <typename T>
+__device__ __forceinline__ void load_gate(const AttnArgs<T>& a, GateQuads<T>& g, int b, int hh, int q, int fh) {
+    typedef typename GateQuads<T>::T4 T4;
+    q = q < a.Sq ? q : a.Sq - 1;
+    const T* gp = a.G + ((size_t)b * a.Sq + q) * (a.H * 64) + hh * 64 + 4 * fh;
+#pragma unroll
+    for (int db = 0; db < 2; db++)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; g4++) g.v[db][g4] = *reinterpret_cast<const T4*>(gp + 32 * db + 8 * g4);
+}
+
+// gpre: the lane's gate values loaded ahead (out_mode 0), or null to load them here.
 template <typename T>
 __device__ __forceinline__ void store_block(const AttnArgs<T>& a, const f32x16 (&o)[2], float l_run, int b, int hh,
-                                            size_t bh, int q, int fh) {
+                                            size_t bh, int q, int fh, const GateQuads<T>* gpre = nullptr) {
     const float l = l_run + __shfl_xor(l_run, 32, 64);
     const float inv = l > 0.f ? 1.f / l : 0.f;
     if (q >= a.Sq) return;
@@ -212,24 +230,34 @@ __device__ __forceinline__ void store_block(const AttnArgs<T>& a, const f32x16 (
             return;
         }
     }
+    // Dims 32 db + 8 g4 + 4 fh .. + 3 of query q.  The output mode is uniform: one
+    // straight-line body per mode, the gate loads all issued before the first store.
+    if (a.out_mode == 0) {
+        typedef typename GateQuads<T>::T4 T4;
+        const size_t base = m * (a.H * 64) + hh * 64 + 4 * fh;
+        GateQuads<T> gl;
+        if (!gpre) load_gate<T>(a, gl, b, hh, q, fh);
+        const GateQuads<T>& g = gpre ? *gpre : gl;
 #pragma unroll
-    for (int db = 0; db < 2; db++)
+        for (int db = 0; db < 2; db++)
 #pragma unroll
-        for (int g4 = 0; g4 < 4; g4++) {
-            const int dim = 32 * db + 8 * g4 + 4 * fh;
-            if (a.out_mode == 0) {
-                typedef T T4 __attribute__((ext_vector_type(4)));
-                const T4 gv = *reinterpret_cast<const T4*>(a.G + m * (a.H * 64) + hh * 64 + dim);
+            for (int g4 = 0; g4 < 4; g4++) {
                 T4 ov;
 #pragma unroll
-                for (int c = 0; c < 4; c++) ov[c] = static_cast<T>(o[db][4 * g4 + c] * inv * static_cast<float>(gv[c]));
-                *reinterpret_cast<T4*>(a.O + m * (a.H * 64) + hh * 64 + dim) = ov;
-            } else {
-                float* op = a.Of + ((bh * a.Sq) + q) * 64 + dim;
-                *reinterpret_cast<float4*>(op) = make_float4(o[db][4 * g4] * inv, o[db][4 * g4 + 1] * inv,
-                                                             o[db][4 * g4 + 2] * inv, o[db][4 * g4 + 3] * inv);
+                for (int c = 0; c < 4; c++)
+                    ov[c] = static_cast<T>(o[db][4 * g4 + c] * inv * static_cast<float>(g.v[db][g4][c]));
+                *reinterpret_cast<T4*>(a.O + base + 32 * db + 8 * g4) = ov;
             }
-        }
+    } else {
+        float* op = a.Of + ((bh * a.Sq) + q) * 64 + 4 * fh;
+#pragma unroll
+        for (int db = 0; db < 2; db++)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; g4++)
+                *reinterpret_cast<float4*>(op + 32 * db + 8 * g4) =
+                    make_float4(o[db][4 * g4] * inv, o[db][4 * g4 + 1] * inv, o[db][4 * g4 + 2] * inv,
+                                o[db][4 * g4 + 3] * inv);
+    }
 }
 
 // QB query blocks of 32 x KVS key parities = QB*KVS wavefronts per workgroup.
