@@ -132,6 +132,7 @@ struct irodori_ctx {
     void* shift_stage = nullptr;  // bf16 [2L][nvec_cap][D]
     float* rope_cos = nullptr;
     float* rope_sin = nullptr;
+    float* rope_cs = nullptr;  // [S, Dh/2, 2] interleaved (cos, sin), the QKVG epilogue's form
     float* xt = nullptr;    // [rows, S, P] sampler state / forward input
     float* vout = nullptr;  // [rows, S, P] head outputs (role-major in the sampler)
     float* xin = nullptr;   // [rows, S, P] Heun predictor state
@@ -439,6 +440,7 @@ int enqueue_part(irodori_ctx* c, int l, int B, int S, const ModTable& mt, int pa
             ga.k_norm = lb.k_norm;
             ga.rope_cos = c->rope_cos;
             ga.rope_sin = c->rope_sin;
+            ga.rope_cs = c->rope_cs;
             ga.vt_stride = vt_stride;
             ga.q_scale = 1.4426950408889634f / sqrtf((float)g.head_dim);
             if (fz) {
@@ -906,6 +908,7 @@ int irodori_ctx_create(int device, const irodori_dit_config* cfg, irodori_ctx** 
     }
     IRO_TRY(dalloc(c.get(), &c->rope_cos, sizeof(float) * (size_t)S * Dh / 2));
     IRO_TRY(dalloc(c.get(), &c->rope_sin, sizeof(float) * (size_t)S * Dh / 2));
+    IRO_TRY(dalloc(c.get(), &c->rope_cs, sizeof(float) * (size_t)S * Dh));
     IRO_TRY(dalloc(c.get(), &c->xt, sizeof(float) * M * P));
     IRO_TRY(dalloc(c.get(), &c->vout, sizeof(float) * M * P));
     IRO_TRY(dalloc(c.get(), &c->xin, sizeof(float) * M * P));
@@ -920,6 +923,12 @@ int irodori_ctx_create(int device, const irodori_dit_config* cfg, irodori_ctx** 
     host_rope_tables(S, Dh, g.rope_theta, cs, sn);
     IRO_TRY(upload(c.get(), c->rope_cos, cs.data(), sizeof(float) * cs.size()));
     IRO_TRY(upload(c.get(), c->rope_sin, sn.data(), sizeof(float) * sn.size()));
+    std::vector<float> csi(cs.size() * 2);
+    for (size_t i = 0; i < cs.size(); i++) {
+        csi[2 * i] = cs[i];
+        csi[2 * i + 1] = sn[i];
+    }
+    IRO_TRY(upload(c.get(), c->rope_cs, csi.data(), sizeof(float) * csi.size()));
     IRO_HIP_CHECK(hipStreamSynchronize(c->stream));
     *out = c.release();
     return IRODORI_OK;

@@ -222,6 +222,7 @@ struct GemmArgs {
     const float* k_norm;
     const float* rope_cos;  // [S, Dh/2]
     const float* rope_sin;
+    const float* rope_cs;   // [S, Dh/2, 2]: the same (cos, sin) pairs interleaved
     int H, D;
     float eps;
     // EPI_CTXKV (context KV build, attention.rs:431-501): N = 2 H Dh columns [K | V] of the

@@ -181,6 +181,12 @@ __device__ __forceinline__ int stage_off(int r, int col) {
     const int c = col >> 3;
     return r * 256 + ((c ^ (4 * (((r >> 2) ^ r) & 1))) << 4) + (col & 7) * 2;
 }
+// The same tile packed at 128 bytes per row (the q / k staging, which shares no row with
+// a table): the same chunk xor keeps rows r and r + 4 of a column write on different banks.
+__device__ __forceinline__ int stage_off_packed(int r, int col) {
+    const int c = col >> 3;
+    return r * 128 + ((c ^ (4 * (((r >> 2) ^ r) & 1))) << 4) + (col & 7) * 2;
+}
 
 __device__ __forceinline__ const float* gate_vec(const ModTable& mt, int b, int layer, int kind,
                                                 int D) {
@@ -386,6 +392,29 @@ __attribute__((amdgpu_waves_per_eu(WAVES_M * WAVES_N == 4 ? 2 : 1))) void gemm_k
     }
 
     const int nk = K / BK;
+    // QKVG tiles holding a RoPE head (q or k, head < H / 2): the table rows of the tile's BM
+    // tokens, (cos, sin) pairs [S, 32, 2] f32 = 256 bytes per token, go into LDS by the same
+    // buffer-to-LDS loads as the operands, 1 KB (4 tokens) per instruction; token
+    // m0 + 4 j + lane / 16 lands at 256 (4 j) + 16 lane.  With S >= 4 the token index steps
+    // by 4 with one wrap at most (rows past M read a valid table row, unused).
+    [[maybe_unused]] bool rope_wg = false;
+    if constexpr (EPI == EPI_QKVG) rope_wg = n0 / a.D <= 1 && (n0 % a.D) / 64 < a.H / 2;
+    [[maybe_unused]] auto rope_rows_issue = [&](unsigned char* dst) {
+        static_assert(EPI != EPI_QKVG || (BM * 256 <= STAGE_BYTES && (BM * 256 / 1024) % NW == 0),
+                      "RoPE rows fill whole stage instructions");
+        constexpr int RI = BM * 256 / 1024 / NW;  // instructions per wave
+        const __amdgpu_buffer_rsrc_t rT = make_rsrc(a.rope_cs, (unsigned)a.S * 256u);
+        const int r0 = m0 + 4 * wave * RI + lane / 16;
+        int bq, sq;
+        row_bs(min(r0, a.M - 1), a.S, inv_s, bq, sq);
+#pragma unroll
+        for (int j = 0; j < RI; j++) {
+            if (a.S < 4) row_bs(min(r0 + 4 * j, a.M - 1), a.S, inv_s, bq, sq);
+            buf_load_lds16(rT, (unsigned)sq * 256u + (unsigned)(lane % 16) * 16u, 0u, dst + (wave * RI + j) * 1024);
+            sq += 4;
+            sq = sq >= a.S ? sq - a.S : sq;
+        }
+    };
 #pragma unroll
     for (int s = 0; s < STAGES - 1; s++)
         if (s < nk) GEMM_ISSUE(s, s);
@@ -396,6 +425,12 @@ __attribute__((amdgpu_waves_per_eu(WAVES_M * WAVES_N == 4 ? 2 : 1))) void gemm_k
         wait_slices<STAGES - 2, LPW>(nk - 1 - kt);
         raw_barrier();
         if (kt + STAGES - 1 < nk) GEMM_ISSUE(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
+        if constexpr (EPI == EPI_QKVG) {
+            // The stage after the last slice's was last read in iteration nk - 2, which every
+            // wave has finished at this barrier: the RoPE rows of the tile stream into it
+            // while the last slice's MFMAs run.
+            if (rope_wg && kt == nk - 1) rope_rows_issue(smem + (nk % STAGES) * STAGE_BYTES);
+        }
         if constexpr (FUSE_IN) {
             if (a.rstat && kt == 0) {
 #pragma unroll
@@ -493,7 +528,8 @@ __attribute__((amdgpu_waves_per_eu(WAVES_M * WAVES_N == 4 ? 2 : 1))) void gemm_k
             // The wave's row scales go through its own slot of the (now free) stage buffers;
             // this lane then needs rows 4 (lane / 32) + 32 i + 8 q + 0..3.
             __syncthreads();  // every wave is past its last read of the operand stages
-            float* rs_lds = reinterpret_cast<float*>(smem) + wave * WM;
+            // In the last slice's stage: the stage after it may hold the QKVG RoPE rows.
+            float* rs_lds = reinterpret_cast<float*>(smem + ((nk - 1) % STAGES) * STAGE_BYTES) + wave * WM;
 #pragma unroll
             for (int p = 0; p < RPL; p++)
                 if (64 * p + lane < WM) rs_lds[64 * p + lane] = rown[p];
@@ -893,11 +929,12 @@ __attribute__((amdgpu_waves_per_eu(WAVES_M * WAVES_N == 4 ? 2 : 1))) void gemm_k
         }
     } else if constexpr (EPI == EPI_QKVG) {
         // Each wave owns WM rows x one 64-column head of one region (q | k | v | gate).
-        // The stage buffers are free once every wave is past the main loop; each wave then
-        // uses its own LDS slot: RoPE table rows (WM x 32 (cos, sin) pairs, f32) and, for
-        // bf16, the staged q / k / gate tile (stage_off) written out with 16-byte stores; or
-        // the V^T transpose (64 x (WM + 2) elements; an odd word stride keeps both passes
-        // conflict-free).
+        // The stage buffers are free once every wave is past the main loop.  q / k waves read
+        // the tile's RoPE rows from the stage after the last slice's (loaded during the last
+        // slice) and stage their bf16 tile packed in the last slice's stage (WM x 128 bytes
+        // per wave); gate and V waves use a slot of SLOT bytes per wave over both stages: the
+        // staged gate tile (stage_off) written out with 16-byte stores, or the V^T transpose
+        // (64 x (WM + 2) elements; an odd word stride keeps both passes conflict-free).
         constexpr int VT_BYTES = sizeof(T) == 2 ? 64 * (WM + 2) * 2 : 0;  // f32 scatters V^T directly
         constexpr int SLOT = WM * 256 > VT_BYTES ? WM * 256 : VT_BYTES;
         static_assert(STAGES * STAGE_BYTES >= NW * SLOT, "QKVG epilogue needs one LDS slot per wave");
@@ -908,27 +945,8 @@ __attribute__((amdgpu_waves_per_eu(WAVES_M * WAVES_N == 4 ? 2 : 1))) void gemm_k
         const int half_heads = a.H / 2;
         const int rw0 = m0 + wm0;  // first row of this wave
         const bool rope = region <= 1 && h < half_heads;
-        // RoPE rows of the wave's WM tokens: lane task (r, k4) holds cos / sin of pairs
-        // 4 k4 .. 4 k4 + 3 at token r.  Loaded before the barrier (registers only), so their
-        // latency overlaps the wait for the other waves' main loops.
-        constexpr int RT_IT = WM / 8;
-        float4 rc[RT_IT], rs[RT_IT];
-        if (rope) {
-            // Lane task it: token row rw0 + 8 it + lane / 8.  With S >= 8 the token index
-            // steps by 8 with one wrap at most (rows past M wrap too and read a valid table
-            // row, unused); otherwise each row is located on its own.
-            const int k4 = lane & 7;
-            int bq, sq;
-            row_bs(min(rw0 + (lane >> 3), a.M - 1), a.S, inv_s, bq, sq);
-#pragma unroll
-            for (int it = 0; it < RT_IT; it++) {
-                if (a.S < 8) row_bs(min(rw0 + it * 8 + (lane >> 3), a.M - 1), a.S, inv_s, bq, sq);
-                rc[it] = *reinterpret_cast<const float4*>(a.rope_cos + (size_t)sq * (Dh / 2) + k4 * 4);
-                rs[it] = *reinterpret_cast<const float4*>(a.rope_sin + (size_t)sq * (Dh / 2) + k4 * 4);
-                sq += 8;
-                sq = sq >= a.S ? sq - a.S : sq;
-            }
-        }
+        static_assert(NW * WM * 128 <= STAGE_BYTES, "packed q / k staging fits one stage");
+        if (rope_wg) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's RoPE rows landed
         __syncthreads();
         unsigned char* slot = smem + wave * SLOT;
         if (region <= 1) {
@@ -937,16 +955,9 @@ __attribute__((amdgpu_waves_per_eu(WAVES_M * WAVES_N == 4 ? 2 : 1))) void gemm_k
             const float qs = region == 0 ? a.q_scale : 1.f;
             const float nw0 = nwp[cl] * qs, nw1 = nwp[32 + cl] * qs;
             T* dst = region == 0 ? a.Q : a.Kd;
-            float* rt = reinterpret_cast<float*>(slot);  // [WM rows][32 pairs][cos, sin]
-            if (rope) {
-#pragma unroll
-                for (int it = 0; it < RT_IT; it++) {
-                    const int idx = it * 64 + lane, r = idx >> 3, k4 = idx & 7;
-                    float4* o = reinterpret_cast<float4*>(rt + r * 64 + k4 * 8);
-                    o[0] = make_float4(rc[it].x, rs[it].x, rc[it].y, rs[it].y);
-                    o[1] = make_float4(rc[it].z, rs[it].z, rc[it].w, rs[it].w);
-                }
-            }
+            // RoPE rows of this wave's tokens: [WM][32 pairs][cos, sin].
+            const float* rt = reinterpret_cast<const float*>(smem + (nk % STAGES) * STAGE_BYTES) + wm0 * 64;
+            unsigned char* qslot = smem + ((nk - 1) % STAGES) * STAGE_BYTES + wave * (WM * 128);
             // Interleaved RoPE pairs (2k, 2k+1) sit in neighbouring lanes: the even lane
             // takes y c - y' s, the odd one y c + y' s (y' the partner's value), so each
             // lane hands its partner its value with the sign the partner needs.
@@ -992,16 +1003,14 @@ __attribute__((amdgpu_waves_per_eu(WAVES_M * WAVES_N == 4 ? 2 : 1))) void gemm_k
             else
                 qk_rows(std::false_type{});
             if constexpr (sizeof(T) == 2) {
-                // Staged over the table once every row is computed (the stage overlaps the
-                // table, so staging inside the loop above would order each row's table reads
-                // after the previous row's stage writes).
+                // Staged once every row is computed.
 #pragma unroll
                 for (int i = 0; i < FM; i++)
 #pragma unroll
                     for (int e = 0; e < 16; e++) {
                         const int rl = 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-                        *reinterpret_cast<T*>(slot + stage_off(rl, cl)) = from_f32<T>(acc[i][0][e]);
-                        *reinterpret_cast<T*>(slot + stage_off(rl, 32 + cl)) = from_f32<T>(acc[i][1][e]);
+                        *reinterpret_cast<T*>(qslot + stage_off_packed(rl, cl)) = from_f32<T>(acc[i][0][e]);
+                        *reinterpret_cast<T*>(qslot + stage_off_packed(rl, 32 + cl)) = from_f32<T>(acc[i][1][e]);
                     }
                 // 16-byte stores: 8 lanes per 128-byte head row of [B, H, S, Dh]; pass it
                 // writes token row rw0 + 8 it + lane / 8.  All staged reads are issued first.
@@ -1009,7 +1018,7 @@ __attribute__((amdgpu_waves_per_eu(WAVES_M * WAVES_N == 4 ? 2 : 1))) void gemm_k
                 uint4 sv[WM / 8];
 #pragma unroll
                 for (int it = 0; it < WM / 8; it++)
-                    sv[it] = *reinterpret_cast<const uint4*>(slot + stage_off(it * 8 + (lane >> 3), 8 * c));
+                    sv[it] = *reinterpret_cast<const uint4*>(qslot + stage_off_packed(it * 8 + (lane >> 3), 8 * c));
                 if (a.S >= 8 && rw0 + WM <= a.M) {
                     // Every row is inside M: the destination steps by 8 tokens, moving to the
                     // next batch row (H - 1 head blocks further) when the token index wraps.
@@ -1163,7 +1172,7 @@ int launch_cfg(const GemmArgs<T>& a, hipStream_t st) {
         case EPI_SNAKE: if (!a.U) return -1; break;
         case EPI_RESUNIT: if (!a.W2 || !a.x || (a.U && !a.alpha2)) return -1; break;
         case EPI_QKVG:
-            if (!a.Q || !a.Kd || !a.Vd || !a.G || !a.q_norm || !a.k_norm || !a.rope_cos || !a.rope_sin || a.H <= 0 ||
+            if (!a.Q || !a.Kd || !a.Vd || !a.G || !a.q_norm || !a.k_norm || !a.rope_cs || a.H <= 0 ||
                 a.D != a.H * 64 || a.N != 4 * a.D || a.vt_stride < a.S || a.S <= 0)
                 return -1;
             break;
