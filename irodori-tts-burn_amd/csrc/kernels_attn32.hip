@@ -386,14 +386,18 @@ __global__ __launch_bounds__(64 * QB * KVS) __attribute__((amdgpu_waves_per_eu(1
         if (par < nact) score_tile<T>(s, kring + par * TILE_BYTES, fr, fh, qf, ones, qbias);
     }
 
-    for (int j = 0; j < niter; j++) {
+    // Two tiles per iteration with the score buffers swapping roles (no copy of the next
+    // tile's scores into the current ones).  Tile step j consumes sc (tile j's scores) and
+    // leaves tile j + 1's scores in sn.
+    f32x16 sn[2];
+    auto tile_step = [&](const int j, f32x16 (&sc)[2], f32x16 (&sn)[2]) {
         // K_{j+1} and V_j have landed once this wave's loads are done and all waves met.
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         raw_barrier();
         if (j + 1 < niter) ATT_ISSUE(1, j + 1, (j + 1) & 1);
         if (j + 2 < niter) ATT_ISSUE(0, j + 2, j & 1);
         const int li = j * KVS + par;
-        if (li >= nact) continue;  // this parity has no tile in the last iteration
+        if (li >= nact) return;  // this parity has no tile in the last iteration
         // V^T fragments of tile j, read now so that their latency hides behind the softmax.
         const unsigned char* vt = vring + ((j & 1) * KVS + par) * TILE_BYTES;
         V8 vf[2][4];
@@ -413,14 +417,14 @@ __global__ __launch_bounds__(64 * QB * KVS) __attribute__((amdgpu_waves_per_eu(1
                 for (int g4 = 0; g4 < 4; g4++)
 #pragma unroll
                     for (int c = 0; c < 4; c++)
-                        if (!((w >> (8 * g4 + c)) & 1u)) s[kb][4 * g4 + c] = -INFINITY;
+                        if (!((w >> (8 * g4 + c)) & 1u)) sc[kb][4 * g4 + c] = -INFINITY;
             }
         }
         float mx = -INFINITY;
 #pragma unroll
         for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-            for (int e = 0; e < 16; e++) mx = fmaxf(mx, s[kb][e]);
+            for (int e = 0; e < 16; e++) mx = fmaxf(mx, sc[kb][e]);
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
         // Move the reference on the first tile or when a score exceeds it by 2^TAU.
         const bool need = first || mx > TAU;
@@ -432,7 +436,7 @@ __global__ __launch_bounds__(64 * QB * KVS) __attribute__((amdgpu_waves_per_eu(1
 #pragma unroll
             for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-                for (int e = 0; e < 16; e++) s[kb][e] -= delta;
+                for (int e = 0; e < 16; e++) sc[kb][e] -= delta;
 #pragma unroll
             for (int db = 0; db < 2; db++) o[db] *= corr;
             l_run *= corr;
@@ -443,7 +447,6 @@ __global__ __launch_bounds__(64 * QB * KVS) __attribute__((amdgpu_waves_per_eu(1
         // Scores of tile j + 1 on the matrix core, softmax of tile j on the VALU.
         // (Computed unconditionally to keep one scheduling region; without a next tile the
         // slot holds stale data and the result is dropped.)
-        f32x16 sn[2];
         score_tile<T>(sn, kring + (((j + 1) & 1) * KVS + par) * TILE_BYTES, fr, fh, qf, ones, qbias);
         float psum = 0.f;
         V8 pf[4];
@@ -451,7 +454,7 @@ __global__ __launch_bounds__(64 * QB * KVS) __attribute__((amdgpu_waves_per_eu(1
         for (int kb = 0; kb < 2; kb++)
 #pragma unroll
             for (int e = 0; e < 16; e++) {
-                const float p = fast_exp2(s[kb][e]);
+                const float p = fast_exp2(sc[kb][e]);
                 psum += p;
                 pf[2 * kb + (e >> 3)][e & 7] = static_cast<T>(p);
             }
@@ -468,8 +471,10 @@ __global__ __launch_bounds__(64 * QB * KVS) __attribute__((amdgpu_waves_per_eu(1
         for (int db = 0; db < 2; db++)
 #pragma unroll
             for (int g = 0; g < 4; g++) o[db] = mma32x16(vf[db][g], pf[g], o[db]);
-        s[0] = sn[0];
-        s[1] = sn[1];
+    };
+    for (int j = 0; j < niter; j += 2) {
+        tile_step(j, s, sn);
+        if (j + 1 < niter) tile_step(j + 1, sn, s);
     }
 #undef ATT_ISSUE
     float m_run = first ? -INFINITY : m_ref;
