@@ -35,6 +35,20 @@ namespace irodori {
 
 namespace {
 
+// Max of v over lanes l and l ^ 32 (the two halves of a query column) by v_permlane32_swap,
+// a VALU exchange, instead of an LDS-routed shuffle.
+__device__ __forceinline__ float max_halves(float v) {
+    const unsigned u = __builtin_bit_cast(unsigned, v);
+    const auto sw = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return fmaxf(__builtin_bit_cast(float, (unsigned)sw[0]), __builtin_bit_cast(float, (unsigned)sw[1]));
+}
+// Sum of v over lanes l and l ^ 32, the same exchange (the same value in both lanes).
+__device__ __forceinline__ float sum_halves(float v) {
+    const unsigned u = __builtin_bit_cast(unsigned, v);
+    const auto sw = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __builtin_bit_cast(float, (unsigned)sw[0]) + __builtin_bit_cast(float, (unsigned)sw[1]);
+}
+
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 
@@ -196,7 +210,7 @@ __device__ __forceinline__ void load_gate(const AttnArgs<T>& a, GateQuads<T>& g,
 template <typename T>
 __device__ __forceinline__ void store_block(const AttnArgs<T>& a, const f32x16 (&o)[2], float l_run, int b, int hh,
                                             size_t bh, int q, int fh, const GateQuads<T>* gpre = nullptr) {
-    const float l = l_run + __shfl_xor(l_run, 32, 64);
+    const float l = sum_halves(l_run);
     const float inv = l > 0.f ? 1.f / l : 0.f;
     if (q >= a.Sq) return;
     const size_t m = (size_t)b * a.Sq + q;
@@ -420,12 +434,15 @@ __global__ __launch_bounds__(64 * QB * KVS) __attribute__((amdgpu_waves_per_eu(1
                         if (!((w >> (8 * g4 + c)) & 1u)) sc[kb][4 * g4 + c] = -INFINITY;
             }
         }
-        float mx = -INFINITY;
+        // Tile max as a balanced tree (depth 5 instead of a 32-long chain), then the halves.
+        float m16[16];
 #pragma unroll
-        for (int kb = 0; kb < 2; kb++)
+        for (int e = 0; e < 16; e++) m16[e] = fmaxf(sc[0][e], sc[1][e]);
 #pragma unroll
-            for (int e = 0; e < 16; e++) mx = fmaxf(mx, sc[kb][e]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        for (int w = 8; w > 0; w >>= 1)
+#pragma unroll
+            for (int e = 0; e < w; e++) m16[e] = fmaxf(m16[e], m16[e + w]);
+        float mx = max_halves(m16[0]);
         // Move the reference on the first tile or when a score exceeds it by 2^TAU.
         const bool need = first || mx > TAU;
         if (__ballot(need)) {
