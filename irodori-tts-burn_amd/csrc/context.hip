@@ -815,7 +815,7 @@ int irodori_ctx_create(int device, const irodori_dit_config* cfg, irodori_ctx** 
     IRO_REQUIRE(g.model_dim % 64 == 0 && g.model_dim <= 2048, IRODORI_ERR_SHAPE,
                 "model_dim must be a multiple of 64 and <= 2048");
     IRO_REQUIRE(g.mlp_hidden > 0, IRODORI_ERR_SHAPE, "mlp_hidden must be positive");
-    IRO_REQUIRE(g.latent_dim <= 64, IRODORI_ERR_SHAPE, "latent_dim must be <= 64");
+    IRO_REQUIRE(g.latent_dim <= 128, IRODORI_ERR_SHAPE, "latent_dim must be <= 128");
     IRO_REQUIRE(g.adaln_rank > 0 && g.timestep_embed_dim > 0 && g.timestep_embed_dim % 2 == 0,
                 IRODORI_ERR_SHAPE, "adaln_rank > 0 and even timestep_embed_dim required");
     IRO_REQUIRE(g.norm_eps > 0.f && std::isfinite(g.norm_eps), IRODORI_ERR_CONFIG, "norm_eps must be > 0");
@@ -885,7 +885,7 @@ int irodori_ctx_create(int device, const irodori_dit_config* cfg, irodori_ctx** 
     IRO_TRY(dalloc(c.get(), &c->in_w, sizeof(float) * (size_t)P * D));
     IRO_TRY(dalloc(c.get(), &c->in_b, sizeof(float) * D));
     IRO_TRY(dalloc(c.get(), &c->out_norm_w, sizeof(float) * D));
-    IRO_TRY(dalloc(c.get(), &c->out_w, sizeof(float) * (size_t)D * (P <= 32 ? 32 : 64)));
+    IRO_TRY(dalloc(c.get(), &c->out_w, sizeof(float) * (size_t)D * (P <= 32 ? 32 : P <= 64 ? 64 : 128)));
     IRO_TRY(dalloc(c.get(), &c->out_b, sizeof(float) * P));
 
     IRO_TRY(dalloc(c.get(), &c->x, sizeof(float) * M * D));
@@ -958,7 +958,7 @@ int irodori_load_io_weights(irodori_ctx* c, const irodori_io_weights* w) {
     IRO_TRY(upload(c, c->out_norm_w, w->out_norm_w, sizeof(float) * D));
     // Output head weight with the out_norm weight folded in, rows padded to PW columns
     // (zeros past P) for the head's whole-row loads.
-    const int PW = P <= 32 ? 32 : 64;
+    const int PW = P <= 32 ? 32 : P <= 64 ? 64 : 128;
     std::vector<float> wt((size_t)D * PW, 0.f);
     for (int d = 0; d < D; d++)
         for (int p = 0; p < P; p++) wt[(size_t)d * PW + p] = w->out_w[(size_t)d * P + p] * w->out_norm_w[d];

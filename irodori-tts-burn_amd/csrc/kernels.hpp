@@ -140,7 +140,7 @@ __device__ inline void rf_apply(const RfUpdateArgs& a, const RfEval& e, int step
 struct FinalArgs {
     const float* x;
     const float* norm_w;
-    const float* out_w;   // [D, PT] = out_norm.weight (.) W_out, PT = 32 (P <= 32) or 64, zero past P
+    const float* out_w;   // [D, PT] = out_norm.weight (.) W_out, PT = 32, 64 or 128 (the least >= P), zero past P
     const float* out_b;   // [P]
     int B, S, D, P;
     float eps;

@@ -43,6 +43,9 @@ SMALL = {
     # a 48-channel latent takes the output head's 64-wide tile path (more staged outputs
     # than threads)
     "tiny_p48": (lambda: dataclasses.replace(ih.cfg_tiny(), latent_dim=48), 40, 20, 13, 0.05, 0.1),
+    # a 120-channel latent: the output head's 128-wide W' rows (8 zero columns), in_proj over
+    # two 64-channel chunks
+    "tiny_p120": (lambda: dataclasses.replace(ih.cfg_tiny(), latent_dim=120), 40, 20, 13, 0.05, 0.1),
     # the published 500M-v2 width (d 1280, 20 x 64 heads, SwiGLU 3680 padded to 3712 on the
     # device, norms unfused) with two of its twelve layers; 4 text + 9 speaker keys as the
     # A6000 benchmark's request (text_len 4, 8 reference frames + the mean token)
@@ -99,6 +102,23 @@ def test_sample_joint_cfg_cfg1(oracle64, backend):
     print(backend.value, "final rel L2 %.2e" % rel_l2(got, ref))
     assert rel_l2(got, ref) < TOL_FINAL[backend]
     assert np.array_equal(got, again)  # graph replay is deterministic
+
+
+@pytest.mark.parametrize("backend", [F32, BF16], ids=["f32", "bf16"])
+def test_sample_joint_cfg_wide_latent(oracle64, backend):
+    # A 120-channel latent through the sampler: the fused head + update with 128-wide W'
+    # rows and two frames per block, 4 Euler steps of Joint CFG against the oracle.
+    cfg = dataclasses.replace(ih.cfg_tiny(), latent_dim=120)
+    w = ih.DitWeights.random(cfg, 0, std=0.05)
+    ctx = ih.make_context_kv(cfg, 1, 20, 13, seed=1)
+    x0 = ih.make_noise(1, 40, cfg.latent_dim, 2)
+    p = joint_params(4)
+    with make_engine(cfg, backend, w, ctx, 2, 40) as e:
+        got = e.sample(x0, p)
+    c, u = ctx.rows([0]), ctx.rows([1])
+    ref, _ = oracle64.sample_joint_cfg(cfg, w, x0, (c.k, c.v, c.mask), (u.k, u.v, u.mask), 4, 3.0)
+    print(backend.value, "latent 120: final rel L2 %.2e" % rel_l2(got, ref))
+    assert rel_l2(got, ref) < TOL_FINAL[backend]
 
 
 def test_sample_two_utterances_rows_independent(oracle64):
