@@ -73,7 +73,7 @@ typedef struct irodori_ctx irodori_ctx;
 /* Model dimensions: the ModelConfig fields the DiT forward reads
  * (src/config/model.rs:8-44), plus device sizing. */
 typedef struct irodori_dit_config {
-    int32_t latent_dim;         /* patched latent dim P (latent_dim * latent_patch_size) */
+    int32_t latent_dim;         /* patched latent dim P (latent_dim * latent_patch_size), <= 128 */
     int32_t model_dim;          /* D */
     int32_t num_layers;         /* L */
     int32_t num_heads;          /* H (head_dim = D / H must be 64) */
