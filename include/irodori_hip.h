@@ -84,7 +84,7 @@ typedef struct irodori_dit_config {
     float norm_eps;             /* norm_eps (config/model.rs:78) */
     float rope_theta;           /* 10000 (dit/model.rs:216) */
     int32_t compute_dtype;      /* IRODORI_DTYPE_BF16 (MFMA bf16), _F32 or _FP8 */
-    int32_t max_rows;           /* max batch rows in one forward (2 per utterance) */
+    int32_t max_rows;           /* max batch rows in one forward (2 per utterance), <= 65535 */
     int32_t max_seq;            /* max latent frames S */
     int32_t max_ctx;            /* max context keys T = text + speaker */
 } irodori_dit_config;

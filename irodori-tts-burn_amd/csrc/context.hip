@@ -820,6 +820,7 @@ int irodori_ctx_create(int device, const irodori_dit_config* cfg, irodori_ctx** 
                 IRODORI_ERR_SHAPE, "adaln_rank > 0 and even timestep_embed_dim required");
     IRO_REQUIRE(g.norm_eps > 0.f && std::isfinite(g.norm_eps), IRODORI_ERR_CONFIG, "norm_eps must be > 0");
     IRO_REQUIRE(g.max_rows > 0 && g.max_seq > 0 && g.max_ctx >= 0, IRODORI_ERR_SHAPE, "max sizes must be positive");
+    IRO_REQUIRE(g.max_rows <= 65535, IRODORI_ERR_SHAPE, "max_rows must be <= 65535 (one output-head grid row per group)");
 
     int ndev = 0;
     hipError_t e = hipGetDeviceCount(&ndev);

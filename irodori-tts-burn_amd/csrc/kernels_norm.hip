@@ -275,7 +275,7 @@ __global__ __launch_bounds__(256) void inproj_norm_kernel(
 }
 
 // Output head: one 256-thread block per FR latent frames and row group (NR rows;
-// blockIdx.y strides over the groups).  v[b,s,p] = (sum_d x[b,s,d] * W'[d,p]) /
+// blockIdx.y is the group).  v[b,s,p] = (sum_d x[b,s,d] * W'[d,p]) /
 // rms(x[b,s,:]) + b_out[p] with W' = out_norm.weight (.) W_out folded at ingest, stored
 // [D][PT] with the columns past P zero — the same product as out_proj(out_norm(x))
 // (norm.rs:25-39, dit/model.rs:391-392).  The group's rows are staged in LDS; thread
@@ -283,9 +283,9 @@ __global__ __launch_bounds__(256) void inproj_norm_kernel(
 // KPT = D / KL consecutive k, so one wavefront load covers 64 / QN whole W' rows (coalesced;
 // W' is read once per block from L2) and a thread's loads sit at immediate offsets of one
 // base.  Staged rows keep 4 pad floats after every 32 (the 64 / QN distinct k of one LDS
-// read fall in distinct banks).  The first KB W' quads of each thread and the sampler state
-// the update reads are loaded before the rows are staged, so their latency overlaps the
-// staging.  The KL partial sums reduce across lanes, then across the 4 wavefronts through
+// read fall in distinct banks).  The staging loads, the first KB W' quads of each thread and
+// the sampler state the update reads are all issued before the first LDS write, so their
+// latencies overlap.  The KL partial sums reduce across lanes, then across the 4 wavefronts through
 // LDS.  Plain head: groups are consecutive rows.  Sampler
 // evaluation: group u holds the active roles' rows of utterance u, and the block applies
 // the guided combine and the integrator update to them (euler_sampler.rs:460-467,
@@ -320,118 +320,147 @@ __global__ __launch_bounds__(256) void final_kernel(FinalArgs a) {
         step = *a.rf.step;
         ev = a.rf.plan[2 * step + a.rf.phase];
     }
-    const int ngroups = rf ? a.B : (a.B + NR - 1) / NR;
-    for (int g = blockIdx.y; g < ngroups; g += gridDim.y) {
-        // Row of slot i: the group's i-th row (a plain head's short last group repeats its
-        // first row); frames past S stage zeros.
-        auto row_of = [&](int i) {
-            if (rf) {
-                int ro = a.role[0];
+    // One row group per blockIdx.y: the launcher's grid.y is the group count (at most the
+    // context's row limit, 65535).
+    const int g = blockIdx.y;
+    // Row of slot i: the group's i-th row (a plain head's short last group repeats its
+    // first row).
+    auto row_of = [&](int i) {
+        if (rf) {
+            int ro = a.role[0];
 #pragma unroll
-                for (int k = 1; k < NR; k++)
-                    if (i == k) ro = a.role[k];
-                return ro * a.B + g;
-            }
-            const int b = g * NR + i;
-            return b < a.B ? b : g * NR;
-        };
-        const int kb0 = kk * KPT;
-        const float* wq = a.out_w + (size_t)kb0 * PT + 4 * q;
-        // Whole batches of KB thread-local k (the first one issued now), then a tail of
-        // single k when KB does not divide KPT.
-        float4 w[KB];
-        if (KPT >= KB) {
-#pragma unroll
-            for (int i = 0; i < KB; i++) w[i] = *reinterpret_cast<const float4*>(wq + (size_t)i * PT);
+            for (int k = 1; k < NR; k++)
+                if (i == k) ro = a.role[k];
+            return ro * a.B + g;
         }
-        // Sampler state element of this thread's update (thread e < nf * PT: frame e / PT,
-        // column e % PT).
-        float xst = 0.f;
-        if (rf && tid < nf * PT && tid % PT < P) xst = a.rf.x[(g * a.S + s0 + tid / PT) * P + tid % PT];
-        __syncthreads();
-        for (int e = tid * 4; e < R * D; e += 1024) {
-            const int r = e / D, d = e % D, f = r / NR, i = r % NR;
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (f < nf) v = *reinterpret_cast<const float4*>(a.x + ((size_t)row_of(i) * a.S + s0 + f) * D + d);
-            *reinterpret_cast<float4*>(xs + r * DP + d + 4 * (d >> 5)) = v;
+        const int b = g * NR + i;
+        return b < a.B ? b : g * NR;
+    };
+    // Staged rows [R][D]: float4 j of chunk c of this thread is element 4 ((c SC + j) 256 +
+    // tid); frames past S read frame nf - 1 and stage zeros.  One chunk holds every element
+    // for D = 1024; it is issued before the W' quads so that both latencies overlap, and its
+    // loads are all in flight before the first LDS write waits on them.
+    constexpr int SC = R;
+    const int nst = R * D / 4;  // D % 4 == 0
+    float4 sv[SC];
+    auto stage_issue = [&](int c) {
+#pragma unroll
+        for (int j = 0; j < SC; j++) {
+            const int idx = (c * SC + j) * 256 + tid;
+            const int e = (idx < nst ? idx : 0) * 4;
+            const int r = e / D, d = e - r * D, f = r / NR, i = r - f * NR;
+            sv[j] = *reinterpret_cast<const float4*>(
+                a.x + ((size_t)row_of(i) * a.S + s0 + (f < nf ? f : nf - 1)) * D + d);
         }
-        __syncthreads();
-        for (int r = wave; r < R; r += 4) {
-            float ss = 0.f;
-            for (int d = lane; d < D; d += 64) {
-                const float xv = xs[r * DP + d + 4 * (d >> 5)];
-                ss += xv * xv;
+    };
+    auto stage_write = [&](int c) {
+#pragma unroll
+        for (int j = 0; j < SC; j++) {
+            const int idx = (c * SC + j) * 256 + tid;
+            if (idx < nst) {
+                const int e = idx * 4, r = e / D, d = e - r * D;
+                const float4 v = r / NR < nf ? sv[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+                *reinterpret_cast<float4*>(xs + r * DP + d + 4 * (d >> 5)) = v;
             }
-            ss = wave_sum(ss);
-            if (lane == 0) rinv[r] = 1.f / sqrtf(ss / (float)D + a.eps);
         }
-        float4 acc[R];
+    };
+    stage_issue(0);
+    // The first KB W' quads of this thread (rows past D, when KPT < KB, re-read row D - 1
+    // and go unused: the k loop below then loads its rows itself).
+    const int kb0 = kk * KPT;
+    const float* wq = a.out_w + (size_t)kb0 * PT + 4 * q;
+    float4 w[KB];
 #pragma unroll
-        for (int r = 0; r < R; r++) acc[r] = make_float4(0.f, 0.f, 0.f, 0.f);
-        auto fma_k = [&](int k, const float4& wv) {  // k: row of W' and column of the staged rows
-            const int kx = k + 4 * (k >> 5);
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                const float xv = xs[r * DP + kx];
-                acc[r].x += xv * wv.x;
-                acc[r].y += xv * wv.y;
-                acc[r].z += xv * wv.z;
-                acc[r].w += xv * wv.w;
-            }
-        };
-        int k0 = 0;
-        for (; k0 + KB <= KPT; k0 += KB) {
-            if (k0 > 0) {
-#pragma unroll
-                for (int i = 0; i < KB; i++) w[i] = *reinterpret_cast<const float4*>(wq + (size_t)(k0 + i) * PT);
-            }
-#pragma unroll
-            for (int i = 0; i < KB; i++) fma_k(kb0 + k0 + i, w[i]);
+    for (int i = 0; i < KB; i++)
+        w[i] = *reinterpret_cast<const float4*>(wq + (size_t)(kb0 + i < D ? i : D - 1 - kb0) * PT);
+    // Sampler state element of this thread's update (thread e < nf * PT: frame e / PT,
+    // column e % PT; other threads read an element in range and leave it unused).
+    float xst = 0.f;
+    if (rf) {
+        const int fe = tid / PT < nf ? tid / PT : nf - 1, pe = tid % PT < P ? tid % PT : P - 1;
+        xst = a.rf.x[(g * a.S + s0 + fe) * P + pe];
+    }
+    stage_write(0);
+    for (int c = 1; c * SC * 256 < nst; c++) {
+        stage_issue(c);
+        stage_write(c);
+    }
+    __syncthreads();
+    for (int r = wave; r < R; r += 4) {
+        float ss = 0.f;
+        for (int d = lane; d < D; d += 64) {
+            const float xv = xs[r * DP + d + 4 * (d >> 5)];
+            ss += xv * xv;
         }
-        for (; k0 < KPT; k0++) fma_k(kb0 + k0, *reinterpret_cast<const float4*>(wq + (size_t)k0 * PT));
-        // Lanes q, q + QN, ... of a wavefront hold one quad's partial sums.
+        ss = wave_sum(ss);
+        if (lane == 0) rinv[r] = 1.f / sqrtf(ss / (float)D + a.eps);
+    }
+    float4 acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+    auto fma_k = [&](int k, const float4& wv) {  // k: row of W' and column of the staged rows
+        const int kx = k + 4 * (k >> 5);
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            float4 v = acc[r];
-#pragma unroll
-            for (int m = QN; m < 64; m <<= 1) {
-                v.x += __shfl_xor(v.x, m, 64);
-                v.y += __shfl_xor(v.y, m, 64);
-                v.z += __shfl_xor(v.z, m, 64);
-                v.w += __shfl_xor(v.w, m, 64);
-            }
-            if (lane < QN) *reinterpret_cast<float4*>(red + (wave * R + r) * PT + 4 * q) = v;
+            const float xv = xs[r * DP + kx];
+            acc[r].x += xv * wv.x;
+            acc[r].y += xv * wv.y;
+            acc[r].z += xv * wv.z;
+            acc[r].w += xv * wv.w;
         }
-        __syncthreads();
-        for (int idx = tid; idx < R * PT; idx += 256) {  // R * PT may exceed the block
-            const int r = idx / PT, pp = idx % PT;
-            const float v = red[r * PT + pp] + red[(R + r) * PT + pp] + red[(2 * R + r) * PT + pp] +
-                            red[(3 * R + r) * PT + pp];
-            vals[r * PT + pp] = pp < P ? v * rinv[r] + a.out_b[pp] : 0.f;
+    };
+    int k0 = 0;
+    for (; k0 + KB <= KPT; k0 += KB) {
+        if (k0 > 0) {
+#pragma unroll
+            for (int i = 0; i < KB; i++) w[i] = *reinterpret_cast<const float4*>(wq + (size_t)(k0 + i) * PT);
         }
-        __syncthreads();
-        for (int e = tid; e < nf * PT; e += 256) {  // nf * PT <= 256: one pass
-            const int f = e / PT, pp = e % PT, sq = s0 + f;
-            if (pp >= P) continue;
-            if (!rf) {
 #pragma unroll
-                for (int i = 0; i < NR; i++)
-                    if (g * NR + i < a.B) a.v_out[((size_t)(g * NR + i) * a.S + sq) * P + pp] = vals[(f * NR + i) * PT + pp];
-                continue;
-            }
-            const float v0 = vals[(f * NR) * PT + pp];
-            float v = v0;
+        for (int i = 0; i < KB; i++) fma_k(kb0 + k0 + i, w[i]);
+    }
+    for (; k0 < KPT; k0++) fma_k(kb0 + k0, *reinterpret_cast<const float4*>(wq + (size_t)k0 * PT));
+    // Lanes q, q + QN, ... of a wavefront hold one quad's partial sums.
 #pragma unroll
-            for (int k = 0; k < 3; k++) {
-                if (k >= ev.nterm) break;
-                int slot = 0;
+    for (int r = 0; r < R; r++) {
+        float4 v = acc[r];
 #pragma unroll
-                for (int i = 1; i < NR; i++)
-                    if (a.role[i] == ev.role[k]) slot = i;
-                v = v + (v0 - vals[(f * NR + slot) * PT + pp]) * ev.scale[k];
-            }
-            rf_apply(a.rf, ev, step, (g * a.S + sq) * P + pp, v, xst);
+        for (int m = QN; m < 64; m <<= 1) {
+            v.x += __shfl_xor(v.x, m, 64);
+            v.y += __shfl_xor(v.y, m, 64);
+            v.z += __shfl_xor(v.z, m, 64);
+            v.w += __shfl_xor(v.w, m, 64);
         }
+        if (lane < QN) *reinterpret_cast<float4*>(red + (wave * R + r) * PT + 4 * q) = v;
+    }
+    __syncthreads();
+    for (int idx = tid; idx < R * PT; idx += 256) {  // R * PT may exceed the block
+        const int r = idx / PT, pp = idx % PT;
+        const float v = red[r * PT + pp] + red[(R + r) * PT + pp] + red[(2 * R + r) * PT + pp] +
+                        red[(3 * R + r) * PT + pp];
+        vals[r * PT + pp] = pp < P ? v * rinv[r] + a.out_b[pp] : 0.f;
+    }
+    __syncthreads();
+    for (int e = tid; e < nf * PT; e += 256) {  // nf * PT <= 256: one pass
+        const int f = e / PT, pp = e % PT, sq = s0 + f;
+        if (pp >= P) continue;
+        if (!rf) {
+#pragma unroll
+            for (int i = 0; i < NR; i++)
+                if (g * NR + i < a.B) a.v_out[((size_t)(g * NR + i) * a.S + sq) * P + pp] = vals[(f * NR + i) * PT + pp];
+            continue;
+        }
+        const float v0 = vals[(f * NR) * PT + pp];
+        float v = v0;
+#pragma unroll
+        for (int k = 0; k < 3; k++) {
+            if (k >= ev.nterm) break;
+            int slot = 0;
+#pragma unroll
+            for (int i = 1; i < NR; i++)
+                if (a.role[i] == ev.role[k]) slot = i;
+            v = v + (v0 - vals[(f * NR + slot) * PT + pp]) * ev.scale[k];
+        }
+        rf_apply(a.rf, ev, step, (g * a.S + sq) * P + pp, v, xst);
     }
     if (rf && a.rf.advance) {
         __syncthreads();
@@ -534,8 +563,8 @@ static void launch_final_cfg(const FinalArgs& a, hipStream_t st) {
     static std::once_flag once;
     static hipError_t attr_rc = hipSuccess;
     (void)set_lds_limit_once(once, attr_rc, (const void*)final_kernel<PT, NR, FR>, kMax);
-    const int ngroups = a.rf.plan ? a.B : (a.B + NR - 1) / NR;
-    const dim3 grid((a.S + FR - 1) / FR, ngroups < 65535 ? ngroups : 65535);
+    const int ngroups = a.rf.plan ? a.B : (a.B + NR - 1) / NR;  // <= 65535 (row limit)
+    const dim3 grid((a.S + FR - 1) / FR, ngroups);
     final_kernel<PT, NR, FR><<<grid, 256, lds, st>>>(a);
 }
 
