@@ -91,6 +91,9 @@ struct irodori_ctx {
     int Fp = 0;
     bool bf16 = true;
     bool fp8 = false;  // block GEMMs on e4m3 operands (activations and attention stay bf16)
+    // Block GEMM weights stored tile-major (GemmArgs::w_tiled): every row count is a multiple
+    // of 64 and every row a multiple of 128 bytes (fp8 codes: D and H Dh multiples of 128).
+    bool w_tiled = false;
     size_t esz = 2;    // compute element size
     hipStream_t stream = nullptr;
     // Side capture streams and fork/join events: a captured sampler evaluation runs each
@@ -204,20 +207,26 @@ int upload(irodori_ctx* c, void* dst, const void* src, size_t bytes) {
 }
 
 // Host f32 [K, N] -> device compute-dtype [N, K] at dst (row offset applied by caller).
-int ingest_kmajor(irodori_ctx* c, const float* host, int K, int N, int mode, void* dst) {
+// tiled: dst in the tile-major layout of GemmArgs::w_tiled (through a row-major copy).
+int ingest_kmajor(irodori_ctx* c, const float* host, int K, int N, int mode, void* dst, bool tiled = false) {
     float* stage = nullptr;
+    void* rows = nullptr;
     size_t bytes = sizeof(float) * (size_t)K * N;
     IRO_HIP_CHECK(hipMalloc(&stage, bytes));
-    hipError_t e = hipMemcpyAsync(stage, host, bytes, hipMemcpyHostToDevice, c->stream);
+    hipError_t e = tiled ? hipMalloc(&rows, c->esz * (size_t)K * N) : hipSuccess;
+    if (e == hipSuccess) e = hipMemcpyAsync(stage, host, bytes, hipMemcpyHostToDevice, c->stream);
     if (e == hipSuccess) {
+        void* out = tiled ? rows : dst;
         if (c->bf16)
-            launch_transpose<bf16>(stage, K, N, mode, static_cast<bf16*>(dst), c->stream);
+            launch_transpose<bf16>(stage, K, N, mode, static_cast<bf16*>(out), c->stream);
         else
-            launch_transpose<float>(stage, K, N, mode, static_cast<float*>(dst), c->stream);
+            launch_transpose<float>(stage, K, N, mode, static_cast<float*>(out), c->stream);
+        if (tiled) launch_tile_rows(rows, N, (int)(c->esz * K), dst, c->stream);
         e = hipGetLastError();
     }
     hipError_t e2 = hipStreamSynchronize(c->stream);
     (void)hipFree(stage);
+    if (rows) (void)hipFree(rows);
     if (e == hipSuccess) e = e2;
     if (e != hipSuccess) {
         set_last_error(std::string("weight ingest: ") + hipGetErrorString(e));
@@ -228,20 +237,25 @@ int ingest_kmajor(irodori_ctx* c, const float* host, int K, int N, int mode, voi
 
 // Host f32 [K, N] -> device e4m3 codes [N, K] (row n = output channel, transpose mode as
 // ingest_kmajor) at dst_q, and the channel scales at dst_s.
-int ingest_fp8(irodori_ctx* c, const float* host, int K, int N, int mode, uint8_t* dst_q, float* dst_s) {
+int ingest_fp8(irodori_ctx* c, const float* host, int K, int N, int mode, uint8_t* dst_q, float* dst_s,
+               bool tiled = false) {
     float *stage = nullptr, *kmaj = nullptr;
+    uint8_t* rows = nullptr;
     const size_t bytes = sizeof(float) * (size_t)K * N;
     IRO_HIP_CHECK(hipMalloc(&stage, bytes));
     hipError_t e = hipMalloc(&kmaj, bytes);
+    if (e == hipSuccess && tiled) e = hipMalloc(&rows, (size_t)K * N);
     if (e == hipSuccess) e = hipMemcpyAsync(stage, host, bytes, hipMemcpyHostToDevice, c->stream);
     if (e == hipSuccess) {
         launch_transpose<float>(stage, K, N, mode, kmaj, c->stream);
-        launch_quant_weight_rows(kmaj, N, K, dst_q, dst_s, c->stream);
+        launch_quant_weight_rows(kmaj, N, K, tiled ? rows : dst_q, dst_s, c->stream);
+        if (tiled) launch_tile_rows(rows, N, K, dst_q, c->stream);
         e = hipGetLastError();
     }
     hipError_t e2 = hipStreamSynchronize(c->stream);
     (void)hipFree(stage);
     if (kmaj) (void)hipFree(kmaj);
+    if (rows) (void)hipFree(rows);
     if (e == hipSuccess) e = e2;
     if (e != hipSuccess) {
         set_last_error(std::string("fp8 weight ingest: ") + hipGetErrorString(e));
@@ -326,6 +340,7 @@ int enqueue_mod_table(irodori_ctx* c, int nvec, bool skip_mlp, int l0 = 0, int l
                 GemmArgs<bf16> ga{};
                 ga.A = stage + (size_t)(l * 2 + k) * cap * D;
                 ga.W = static_cast<const bf16*>(k == 0 ? c->layers[l].w_qkvg : c->layers[l].w13);
+                ga.w_tiled = c->w_tiled;
                 ga.M = nvec;
                 ga.N = k == 0 ? 4 * D : 2 * F;
                 ga.K = D;
@@ -400,9 +415,11 @@ int enqueue_part(irodori_ctx* c, int l, int B, int S, const ModTable& mt, int pa
     uint8_t* o8s = f8 ? c->o8s + tok0 * (D / 32) : nullptr;
     uint8_t* u8 = f8 ? c->u8 + tok0 * F : nullptr;
     uint8_t* u8s = f8 ? c->u8s + tok0 * (F / 32) : nullptr;
-    // One projection: the bf16 / f32 GEMM on A and W, or the fp8 GEMM on their e4m3 forms.
+    // One projection: the bf16 / f32 GEMM on A and W, or the fp8 GEMM on their e4m3 forms
+    // (block weights, tile-major when the context stores them so).
     auto gemm = [&](int epi, GemmArgs<T>& args, const T* A, const uint8_t* A8, const uint8_t* As,
                     const void* W, const float* ws) -> int {
+        args.w_tiled = c->w_tiled;
         if constexpr (std::is_same<T, bf16>::value) {
             if (f8) {
                 args.A8 = A8;
@@ -836,6 +853,7 @@ int irodori_ctx_create(int device, const irodori_dit_config* cfg, irodori_ctx** 
     c->fp8 = g.compute_dtype == IRODORI_DTYPE_FP8;
     c->bf16 = g.compute_dtype == IRODORI_DTYPE_BF16 || c->fp8;
     c->esz = c->bf16 ? 2 : 4;
+    c->w_tiled = !c->fp8 || (g.model_dim % 128 == 0 && (g.num_heads * g.head_dim) % 128 == 0);
     // The fused adaLN's GEMMs take the row partial sums as up to 8 float4 per row.
     c->fused = c->bf16 && !c->fp8 && g.model_dim % 128 == 0 && g.model_dim <= 1024;
     IRO_HIP_CHECK(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
@@ -1004,17 +1022,20 @@ int irodori_load_block_weights(irodori_ctx* c, int layer, const irodori_block_we
     char* qkvg = static_cast<char*>(lb.w_qkvg);
     if (c->fp8) {
         uint8_t* q8 = reinterpret_cast<uint8_t*>(qkvg);
-        IRO_TRY(ingest_fp8(c, w->w_qkv, D, 3 * HD, 0, q8, lb.ws_qkvg));
-        IRO_TRY(ingest_fp8(c, w->w_gate, D, D, 0, q8 + (size_t)3 * HD * D, lb.ws_qkvg + 3 * HD));
-        IRO_TRY(ingest_fp8(c, w->w_o, HD, D, 0, static_cast<uint8_t*>(lb.w_o), lb.ws_o));
-        IRO_TRY(ingest_fp8(c, w13, D, 2 * Fp, 1, static_cast<uint8_t*>(lb.w13), lb.ws_13));
-        IRO_TRY(ingest_fp8(c, w2, Fp, D, 0, static_cast<uint8_t*>(lb.w2), lb.ws_2));
+        // (The gate rows start a 64-row group: 3 H Dh is a multiple of 64.)
+        const bool t = c->w_tiled;
+        IRO_TRY(ingest_fp8(c, w->w_qkv, D, 3 * HD, 0, q8, lb.ws_qkvg, t));
+        IRO_TRY(ingest_fp8(c, w->w_gate, D, D, 0, q8 + (size_t)3 * HD * D, lb.ws_qkvg + 3 * HD, t));
+        IRO_TRY(ingest_fp8(c, w->w_o, HD, D, 0, static_cast<uint8_t*>(lb.w_o), lb.ws_o, t));
+        IRO_TRY(ingest_fp8(c, w13, D, 2 * Fp, 1, static_cast<uint8_t*>(lb.w13), lb.ws_13, t));
+        IRO_TRY(ingest_fp8(c, w2, Fp, D, 0, static_cast<uint8_t*>(lb.w2), lb.ws_2, t));
     } else {
-        IRO_TRY(ingest_kmajor(c, w->w_qkv, D, 3 * HD, 0, qkvg));
-        IRO_TRY(ingest_kmajor(c, w->w_gate, D, D, 0, qkvg + c->esz * (size_t)3 * HD * D));
-        IRO_TRY(ingest_kmajor(c, w->w_o, HD, D, 0, lb.w_o));
-        IRO_TRY(ingest_kmajor(c, w13, D, 2 * Fp, 1, lb.w13));
-        IRO_TRY(ingest_kmajor(c, w2, Fp, D, 0, lb.w2));
+        const bool t = c->w_tiled;
+        IRO_TRY(ingest_kmajor(c, w->w_qkv, D, 3 * HD, 0, qkvg, t));
+        IRO_TRY(ingest_kmajor(c, w->w_gate, D, D, 0, qkvg + c->esz * (size_t)3 * HD * D, t));
+        IRO_TRY(ingest_kmajor(c, w->w_o, HD, D, 0, lb.w_o, t));
+        IRO_TRY(ingest_kmajor(c, w13, D, 2 * Fp, 1, lb.w13, t));
+        IRO_TRY(ingest_kmajor(c, w2, Fp, D, 0, lb.w2, t));
     }
     IRO_TRY(upload(c, lb.q_norm, w->q_norm, sizeof(float) * HD));
     IRO_TRY(upload(c, lb.k_norm, w->k_norm, sizeof(float) * HD));
@@ -1748,6 +1769,7 @@ int irodori_op_swiglu_mlp(irodori_ctx* c, int layer, int B, int S, float* x, con
         GemmArgs<bf16> ga{};
         ga.A = stage + (size_t)(layer * 2 + 1) * cap * D;
         ga.W = static_cast<const bf16*>(c->layers[layer].w13);
+        ga.w_tiled = c->w_tiled;
         ga.M = B;
         ga.N = 2 * F;
         ga.K = D;

@@ -200,8 +200,13 @@ enum GemmEpi {
 template <typename T>
 struct GemmArgs {
     const T* A;   // [M, K] row-major
-    const T* W;   // [N, K] row-major (K contiguous)
+    const T* W;   // [N, K] row-major (K contiguous), or tile-major with w_tiled
     int M, N, K;
+    // w_tiled: W (and W8) stored tile-major, as launch_tile_rows writes it: each group of 64
+    // rows holds its K * element-size / 128 slices one after the other, a slice being the
+    // group's 64 rows x 128 bytes (8 KB contiguous).  A group spans the same bytes as in the
+    // row-major layout.  Not for convolutions; BN a multiple of 64.
+    int w_tiled;
     // EPI_STORE: C [M, N] f32
     float* C;
     // EPI_RESID: x[m, n] += gate[vec(b), n] * acc, b = m / S
@@ -289,6 +294,11 @@ template <typename T>
 int launch_gemm(int epi, const GemmArgs<T>& a, hipStream_t st);
 // The same epilogues over fp8 operands (K % 128 == 0); outputs in bf16 / f32 as above.
 int launch_gemm_fp8(int epi, const GemmArgs<bf16>& a, hipStream_t st);
+// Row-major [N, row_bytes] -> the tile-major weight layout of GemmArgs::w_tiled (N a
+// multiple of 64, row_bytes of 128).  A weight slice of a 128- or 64-wide tile is then one or
+// two 8 KB runs instead of 64 or 128 rows of 128 bytes a row apart, so a tile's weight
+// loads open far fewer DRAM pages.
+void launch_tile_rows(const void* src, int N, int row_bytes, void* dst, hipStream_t st);
 // Convolution as a GEMM over an implicit im2col (conv_* fields): K = taps * conv_cp rounded
 // up to whole 128-byte slices, conv_cp a multiple of half a slice; EPI_STORE, EPI_ADD,
 // EPI_SNAKE or EPI_RESUNIT.

@@ -248,12 +248,19 @@ __attribute__((amdgpu_waves_per_eu(WAVES_M * WAVES_N == 4 ? 2 : 1))) void gemm_k
     const unsigned char* Wb = F8 ? a.W8 : reinterpret_cast<const unsigned char*>(a.W);
     const __amdgpu_buffer_rsrc_t rA = make_rsrc(Ab + (size_t)m0 * lda * ES, (unsigned)((size_t)arows * lda * ES));
     const __amdgpu_buffer_rsrc_t rW = make_rsrc(Wb + (size_t)n0 * K * ES, (unsigned)(BN * K * ES));
+    // W row rr of the tile: group rr / 64 at 64 K ES bytes in either layout; within the
+    // group rows are K ES bytes apart (row-major) or 128 (tile-major, where consecutive
+    // slices are 8 KB apart instead of 128 bytes).
+    const bool wt = !CONV && a.w_tiled;
+    const unsigned w_row = wt ? 128u : (unsigned)(K * ES), w_slice = wt ? 8192u : 128u;
     unsigned voff[LPW];
 #pragma unroll
     for (int i = 0; i < LPW; i++) {
         const int r = (wave * LPW + i) * 8 + lane / 8;
         const int rr = r < BM ? r : r - BM;
-        voff[i] = (unsigned)rr * (unsigned)((r < BM ? lda : K) * ES) + (unsigned)swz(r, lane % 8) * 16u;
+        voff[i] = (r < BM ? (unsigned)rr * (unsigned)(lda * ES)
+                          : (unsigned)(rr / 64) * (unsigned)(64 * K * ES) + (unsigned)(rr % 64) * w_row) +
+                  (unsigned)swz(r, lane % 8) * 16u;
     }
     // CONV: byte offset of slice kt in the A source = kt * 128 (the taps laid end to end),
     // plus (conv_dil - 1) rows for each tap before the slice's tap j0 = kt BK / conv_cp.
@@ -286,8 +293,8 @@ __attribute__((amdgpu_waves_per_eu(WAVES_M * WAVES_N == 4 ? 2 : 1))) void gemm_k
 #define GEMM_ISSUE(kt_, stage_)                                                            \
     do {                                                                                   \
         unsigned char* dst_ = smem + (stage_) * STAGE_BYTES + wave * LPW * 1024;           \
-        const unsigned ws_ = (unsigned)(kt_) * 128u;                                       \
-        unsigned as_ = ws_;                                                                \
+        const unsigned ws_ = (unsigned)(kt_) * w_slice;                                    \
+        unsigned as_ = (unsigned)(kt_) * 128u;                                             \
         bool split_ = false;                                                               \
         if constexpr (CONV) {                                                              \
             const int k0_ = (kt_) * BK, j0_ = k0_ / a.conv_cp;                             \
@@ -1189,6 +1196,7 @@ int launch_cfg(const GemmArgs<T>& a, hipStream_t st) {
                  a.next_layer >= a.mt.layers || a.next_kind < 0 || a.next_kind > 1))
         return -1;
     if ((size_t)BN * a.K * ES > 0xffffffffull || (size_t)BM * a.K * ES > 0xffffffffull) return -1;
+    if (a.w_tiled && (CONV || BN % 64 != 0)) return -1;
     if (CONV) {
         // conv_cp a multiple of half a slice (a slice straddles at most two taps, at its
         // middle); K = the taps' span rounded up to whole slices.
@@ -1214,7 +1222,26 @@ int launch_cfg(const GemmArgs<T>& a, hipStream_t st) {
     return 0;
 }
 
+__global__ __launch_bounds__(256) void tile_rows_kernel(const uint4* __restrict__ src, int N, int nk,
+                                                        unsigned char* __restrict__ dst) {
+    // One 16-byte chunk per thread, read in row-major order: chunk c of slice kt of row n.
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (long)N * nk * 8) return;
+    const int c = (int)(i % 8);
+    const long rk = i / 8;
+    const int kt = (int)(rk % nk), n = (int)(rk / nk);
+    const size_t off = ((size_t)(n / 64) * nk + kt) * 8192 + (size_t)(n % 64) * 128 + (size_t)c * 16;
+    *reinterpret_cast<uint4*>(dst + off) = src[i];
+}
+
 }  // namespace
+
+void launch_tile_rows(const void* src, int N, int row_bytes, void* dst, hipStream_t st) {
+    const int nk = row_bytes / 128;
+    const long chunks = (long)N * nk * 8;
+    tile_rows_kernel<<<(unsigned)((chunks + 255) / 256), 256, 0, st>>>(static_cast<const uint4*>(src), N, nk,
+                                                                        static_cast<unsigned char*>(dst));
+}
 
 // Tile choice per epilogue.  With 2x2 wavefronts of 32x32 blocks the main loop is bound by
 // LDS bandwidth (fragment reads + the DMA writes): 1.5x the MFMA time for 128x128 tiles,
