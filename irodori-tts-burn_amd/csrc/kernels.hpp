@@ -166,8 +166,8 @@ void launch_scale_copy(const float* src, float* dst, int n, float s, hipStream_t
 // [B, S, H*64] f32 (nullable: gate 1) into the layouts the QKV+gate epilogue writes -- Q
 // [B, H, S, 64] head-normed (q_norm / k_norm [H, 64], nullable: no norm), half-RoPE'd
 // (heads < H/2, tables [S, 32]) and pre-scaled by q_scale; K likewise without the scale;
-// V^T [B, H, 64, vt_stride] at vt_pos_bf16 (T = bf16) / vt_pos_f32 (T = float); G =
-// sigmoid(gate).
+// V^T [B, H, 64, vt_stride] at vt_pos_bf16 (T = bf16) / vt_pos_f32 (T = float), keys S ..
+// vt_stride - 1 zero (vt_stride = S rounded up to 64); G = sigmoid(gate).
 template <typename T>
 void launch_attn_op_stage(const float* q, const float* k, const float* v, const float* gate, const float* q_norm,
                           const float* k_norm, const float* rope_cos, const float* rope_sin, int B, int S, int H,
