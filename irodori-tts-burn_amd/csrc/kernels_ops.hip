@@ -40,15 +40,18 @@ __global__ __launch_bounds__(512) void attn_op_stage_kernel(
     const float qn = q_norm ? q_norm[h * 64 + d] : 1.f, kn = k_norm ? k_norm[h * 64 + d] : 1.f;
     {
         constexpr int i0 = 0;
-        float xq[8], xk[8], xv[8], xg[8];
+        float xq[8], xk[8], xv[8], xg[8], rc[8], rs[8];
+        const bool rope = h < H / 2;
 #pragma unroll
         for (int u = 0; u < 8; u++) {
-            const int s = s0 + wave * 8 + u;
-            const size_t in = (((size_t)b * S + (s < S ? s : S - 1)) * H + h) * 64 + d;
+            const int s = s0 + wave * 8 + u, sc = s < S ? s : S - 1;
+            const size_t in = (((size_t)b * S + sc) * H + h) * 64 + d;
             xq[u] = q[in];
             xk[u] = k[in];
             xv[u] = v[in];
             xg[u] = gate ? gate[in] : 0.f;
+            rc[u] = rope ? rope_cos[(size_t)sc * 32 + (d >> 1)] : 1.f;
+            rs[u] = rope ? rope_sin[(size_t)sc * 32 + (d >> 1)] : 0.f;
         }
 #pragma unroll
         for (int u = 0; u < 8; u++) {
@@ -60,8 +63,8 @@ __global__ __launch_bounds__(512) void attn_op_stage_kernel(
             float yq = xq[u], yk = xk[u];
             if (q_norm) yq *= rsqrtf(wave_sum(yq * yq) * (1.f / 64.f) + eps) * qn;
             if (k_norm) yk *= rsqrtf(wave_sum(yk * yk) * (1.f / 64.f) + eps) * kn;
-            if (h < H / 2) {
-                const float c = rope_cos[(size_t)s * 32 + (d >> 1)], sn = rope_sin[(size_t)s * 32 + (d >> 1)];
+            if (rope) {
+                const float c = rc[u], sn = rs[u];
                 const float pq = __shfl_xor(yq, 1, 64), pk = __shfl_xor(yk, 1, 64);
                 yq = (d & 1) ? pq * sn + yq * c : yq * c - pq * sn;
                 yk = (d & 1) ? pk * sn + yk * c : yk * c - pk * sn;
