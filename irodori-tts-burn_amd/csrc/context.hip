@@ -665,7 +665,11 @@ int enqueue_eval(irodori_ctx* c, int U, int S, int roles, int method, int phase,
     const bool contiguous = active[na - 1] == na - 1;
     if (contiguous) IRO_TRY(enqueue_inproj(c, na * U, S, src, U, 0, mt, c->stream));
     if (na > 1) IRO_HIP_CHECK(hipEventRecord(c->ev_fork, c->stream));
-    for (int k = 0; k < na; k++) {
+    // The chains are captured last role first: the first role (the conditioned one, whose
+    // attention also reads the context) is then captured last, which measured 0.07-0.2 ms
+    // faster per 40-step run at config 4 than the opposite order (never slower in 5 pairs).
+    for (int kk = 0; kk < na; kk++) {
+        const int k = na - 1 - kk;
         hipStream_t st = k == 0 ? c->stream : c->side[k - 1];
         if (k > 0) IRO_HIP_CHECK(hipStreamWaitEvent(st, c->ev_fork, 0));
         const int r0 = active[k] * U;
