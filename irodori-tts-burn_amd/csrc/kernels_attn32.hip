@@ -757,13 +757,15 @@ int launch_attention32_t(const AttnArgs<T>& a, hipStream_t st) {
     if (!std::is_same<T, bf16>::value && a.out_mode == 2) return -1;
     const int ntiles = (a.len0 + KT - 1) / KT + (a.K1 ? (a.len1 + KT - 1) / KT : 0);
     if (ntiles > 64) return -1;  // the tile list holds one entry per lane (4096 keys)
-    // Latency vs throughput: when 2 query blocks x 2 key parities (4 waves, 64 KB LDS)
-    // need at most one workgroup per CU, the smaller workgroups finish sooner (one CFG row
-    // of 750 frames: 18.2 vs 21.1 us with context keys, 12.3 vs 14.5 us without); larger
-    // launches keep 4 x 2.
-    const long wg22 = (long)((a.Sq + 63) / 64) * a.H * a.B;
-    if (wg22 <= 256) return launch_attn32_cfg<T, 2, 2>(a, st);
-    return launch_attn32_cfg<T, 4, 2>(a, st);
+    // 2 query blocks x 2 key parities (4 waves, 64 KB LDS) at every size.  Against 4 x 2:
+    // one CFG row of 750 frames 18.2 vs 21.1 us with context keys, 12.3 vs 14.5 us without;
+    // B = 2 rows 42.0 vs 42.2 us per operator call; BASELINE config 5 (32 rows) 340.5 vs
+    // 344.4 ms per RF run.  Every query block's arithmetic is the same in either shape (its
+    // two parities merged in the same order), so the shape never changes an output bit.
+    // One key parity (4 x 1, 32 KB) ran config 5 faster still (323.8 ms) but slower at
+    // B = 2 (45.2 us), and a size-dependent choice would make a row's result depend on the
+    // batch it is launched with.
+    return launch_attn32_cfg<T, 2, 2>(a, st);
 }
 
 // Operator staging (irodori_op_sdpa, Dh = 64 on 16-bit operands): the caller's Q, V and
