@@ -224,11 +224,13 @@ __attribute__((amdgpu_waves_per_eu(WAVES_M * WAVES_N == 4 ? 2 : 1))) void gemm_k
     // the group's GM row tiles for one column tile, then the next column tile, so the
     // workgroups an XCD runs together share GM A tiles and a few W tiles in its L2.  With
     // at most GM row tiles this is the plain column-by-column order.  Measured on the RF
-    // run (config 4, 750-row launches): GM = 1 / 2 / 3 / 4 / 6 / 8 / 16 gave 47.4 / 46.0 /
-    // 46.0 / 45.85 / 46.2 / 46.4 / 46.8 ms (the 64-row W_o / W2 tiles, 12 row tiles, decide
-    // it); the codec's convolutions keep 8 (4 was 0.4 % slower there).  The raster never
-    // changes a tile's arithmetic.
-    constexpr int GM = CONV ? 8 : 4;
+    // run (config 4, 750-row launches), one GM for every GEMM: GM = 1 / 2 / 3 / 4 / 6 / 8 /
+    // 16 gave 47.4 / 46.0 / 46.0 / 45.85 / 46.2 / 46.4 / 46.8 ms.  The 64-row W_o / W2 tiles
+    // (12 row tiles) decide it; the 128-row tiles run the same at 3, 4 or 8 and keep 8, where
+    // every row tile of a weight column shares the column on one XCD (W13 fetches 30 MB per
+    // launch instead of 37 at GM = 4).  The codec's convolutions keep 8 (4 was 0.4 % slower
+    // there).  The raster never changes a tile's arithmetic.
+    constexpr int GM = (CONV || BM >= 128) ? 8 : 4;
     const int tiles_m = (a.M + BM - 1) / BM, tiles_n = a.N / BN;
     const int pid = xcd_remap(blockIdx.x, gridDim.x);
     const int per_group = GM * tiles_n, group = pid / per_group, first_m = group * GM;
