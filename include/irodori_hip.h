@@ -155,7 +155,9 @@ int irodori_sampler_params_validate(const irodori_sampler_params* params);
 /* ---- context ---------------------------------------------------------------------- */
 /* Creates a context on HIP device `device`; allocates every device buffer up front for
  * cfg->max_rows / max_seq / max_ctx.  Replaces InferenceBuilder::build
- * (src/inference.rs:83-196) for the HIP backend. */
+ * (src/inference.rs:83-196) for the HIP backend.  bf16 / fp8 contexts take at most 16384
+ * keys per attention row: ceil(max_seq / 64) + ceil(max_ctx / 64) <= 256, else
+ * IRODORI_ERR_SHAPE here (never at a later launch). */
 int irodori_ctx_create(int device, const irodori_dit_config* cfg, irodori_ctx** out);
 int irodori_ctx_destroy(irodori_ctx* ctx);
 /* Bytes of device memory the context holds. */
@@ -434,10 +436,16 @@ int irodori_op_fused_adaln(const float* x, const float* scale, const float* shif
  * q [B,H,Sq,Dh], k/v [B,H,Skv,Dh] in `dtype` (F32, BF16 or F16: native_fa_sdpa_f16_in's
  * f16 storage, f32 accumulation), mask [B,Skv] f32 with 1.0 = attend (values < 0.5 mask
  * the key; may be NULL), out [B,H,Sq,Dh] f32.  Dh in {64, 128}.  A fully masked query row
- * yields 0.  Enqueued on `stream` without waiting.  With Dh = 64 and a 16-bit dtype the
- * call stages Q (pre-scaled), V^T and the key bits in a device buffer it allocates and frees
- * in stream order on `stream` (hipMallocAsync / hipFreeAsync), and runs the model's joint
- * attention kernel on them; other shapes need no staging. */
+ * yields 0.  Enqueued on `stream` without waiting.  With Dh = 64, a 16-bit dtype and
+ * seq_kv <= 16384 the call stages Q (pre-scaled), V^T and the key bits in a device buffer it
+ * allocates and frees in stream order on `stream` (hipMallocAsync / hipFreeAsync), and runs
+ * the model's joint attention kernel on them; other shapes need no staging and run the
+ * generic flash kernel, whose softmax is f32 throughout.  Precision of the staged path: the
+ * scores and the softmax state are f32, but q * scale * log2(e) and the probabilities P
+ * (the P V MFMA operand) are rounded to the operand dtype, as the model's bf16 attention
+ * does; the reference's native FA kernels keep both in f32.  Measured against a float64
+ * SDPA of the same rounded inputs at config 2's shape: 2.4e-3 relative L2 in bf16 and
+ * 3.0e-4 in f16 (bars 1e-2 and 2e-3; max abs 1.5e-3 and 2.0e-4). */
 int irodori_op_sdpa(int dtype, const void* q, const void* k, const void* v, const float* mask,
                     int batch, int heads, int seq_q, int seq_kv, int head_dim, float scale,
                     float* out, void* stream);
@@ -448,7 +456,10 @@ int irodori_op_sdpa(int dtype, const void* q, const void* k, const void* v, cons
  * instead of a per-call allocation.  A shape whose staging (Q + V^T in the operand dtype +
  * the key bits, each rounded up to 256 bytes) exceeds it returns IRODORI_ERR_SHAPE.  Every
  * call on a GPU shares that buffer: calls that overlap on one GPU (other streams or
- * threads) race. */
+ * threads) race.  `stream` must belong to the current device (else IRODORI_ERR_INVALID_ARG).
+ * The first call on a device looks up the buffer's address and must not be made under graph
+ * capture (IRODORI_ERR_INVALID_ARG): capturing callers make one call outside the capture
+ * first; later calls may be captured and replayed. */
 #define IRODORI_SDPA_SCRATCH_BYTES (16u << 20)
 int irodori_op_sdpa_noalloc(int dtype, const void* q, const void* k, const void* v, const float* mask,
                             int batch, int heads, int seq_q, int seq_kv, int head_dim, float scale,

@@ -842,6 +842,12 @@ int irodori_ctx_create(int device, const irodori_dit_config* cfg, irodori_ctx** 
     IRO_REQUIRE(g.norm_eps > 0.f && std::isfinite(g.norm_eps), IRODORI_ERR_CONFIG, "norm_eps must be > 0");
     IRO_REQUIRE(g.max_rows > 0 && g.max_seq > 0 && g.max_ctx >= 0, IRODORI_ERR_SHAPE, "max sizes must be positive");
     IRO_REQUIRE(g.max_rows <= 65535, IRODORI_ERR_SHAPE, "max_rows must be <= 65535 (one output-head grid row per group)");
+    // The 16-bit joint attention lists a row's key tiles (latent, then context) in registers.
+    IRO_REQUIRE(g.compute_dtype == IRODORI_DTYPE_F32 ||
+                    (g.max_seq + 63) / 64 + (g.max_ctx + 63) / 64 <= kAttnMaxKeyTiles,
+                IRODORI_ERR_SHAPE,
+                "max_seq and max_ctx rounded up to 64 keys each must total at most " +
+                    std::to_string(64 * kAttnMaxKeyTiles) + " keys (the bf16 / fp8 attention's key-tile list)");
 
     int ndev = 0;
     hipError_t e = hipGetDeviceCount(&ndev);

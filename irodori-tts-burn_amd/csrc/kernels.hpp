@@ -386,13 +386,15 @@ struct AttnArgs {
 };
 template <typename T, int DH>
 int launch_attention(const AttnArgs<T>& a, hipStream_t st);
-// bf16 / f16, Dh = 64, V^T in vt_pos_bf16 order, Q pre-scaled (kernels_attn32.hip).
+// bf16 / f16, Dh = 64, V^T in vt_pos_bf16 order, Q pre-scaled (kernels_attn32.hip).  The
+// latent and context segments together hold at most kAttnMaxKeyTiles 64-key tiles.
+constexpr int kAttnMaxKeyTiles = 256;
 int launch_attention32(const AttnArgs<bf16>& a, hipStream_t st);
 int launch_attention32(const AttnArgs<f16>& a, hipStream_t st);
 // The SDPA operator on 16-bit operands with Dh = 64 through attn32_kernel: q, k, v
 // [B, H, S, 64] as given, mask [B, Skv] f32 (>= 0.5 attends; nullable), out [B, H, Sq, 64]
 // f32.  Q (pre-scaled), V^T and the key bits are staged in ws (256-byte aligned, at least
-// sdpa_stage_bytes); Skv <= 4096.  Returns -1 on a shape the kernel does not take.
+// sdpa_stage_bytes); Skv <= 64 * kAttnMaxKeyTiles.  Returns -1 on a shape the kernel does not take.
 size_t sdpa_stage_bytes(int B, int H, int Sq, int Skv);
 template <typename T>
 int launch_sdpa_staged(const T* q, const T* k, const T* v, const float* mask, int B, int H, int Sq, int Skv,

@@ -92,34 +92,57 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 template <typename T>
 __device__ __forceinline__ float round_to(float x) { return static_cast<float>(static_cast<T>(x)); }
 
-// Tile list of one (row, head): entry i < nact of the list is held by lane i as the tile
-// index and its 64-bit key-validity mask.  Latent tiles are valid up to len0 (or carry the
-// host-computed latent mask bits); context tiles carry the host-computed bits of the row;
-// tiles without a valid key are dropped.
+// Tile list of one (row, head): NT words per lane.  Word w covers the source tiles
+// 64 w .. 64 w + 63 (latent tiles first, then context tiles) and holds its active tiles
+// compacted to lanes 0 .. cnt_w - 1 as the tile index and its 64-bit key-validity mask;
+// list entry i is word w's lane i - base[w] for the last word with base[w] <= i.  Latent
+// tiles are valid up to len0 (or carry the host-computed latent mask bits); context tiles
+// carry the host-computed bits of the row; tiles without a valid key are dropped.  One word
+// (4096 keys) serves every model shape measured here; four words hold 16384 keys.
+template <int NT>
 struct TileList {
-    int t, lo, hi;  // per lane
-    int nact;       // wave-uniform
+    int t[NT], lo[NT], hi[NT];  // per lane
+    int base[NT];               // wave-uniform: list index of word w's first entry
+    int nact;                   // wave-uniform
 };
 
-template <typename T>
-__device__ __forceinline__ TileList build_tile_list(const AttnArgs<T>& a, int b, int lane, int nt0, int nt1) {
-    unsigned long long bits = 0ull;
-    if (lane < nt0) {
-        const int rem = a.len0 & (KT - 1);
-        bits = a.bits0 ? a.bits0[(size_t)b * nt0 + lane] : (lane == nt0 - 1 && rem) ? ((1ull << rem) - 1ull) : ~0ull;
-    } else if (lane < nt0 + nt1) {
-        bits = a.bits1[(size_t)b * ((a.stride1 + KT - 1) / KT) + (lane - nt0)];
+// Entry li (wave-uniform, < nact) of one per-lane field of the list.
+template <int NT>
+__device__ __forceinline__ int tl_read(const int (&v)[NT], const int (&base)[NT], int li) {
+    int r = __builtin_amdgcn_readlane(v[0], li & 63);
+#pragma unroll
+    for (int w = 1; w < NT; w++)
+        if (li >= base[w]) r = __builtin_amdgcn_readlane(v[w], (li - base[w]) & 63);
+    return r;
+}
+
+template <int NT, typename T>
+__device__ __forceinline__ TileList<NT> build_tile_list(const AttnArgs<T>& a, int b, int lane, int nt0, int nt1) {
+    TileList<NT> tl;
+    int total = 0;
+#pragma unroll
+    for (int w = 0; w < NT; w++) {
+        const int g = 64 * w + lane;  // source tile of this lane in word w
+        unsigned long long bits = 0ull;
+        if (g < nt0) {
+            const int rem = a.len0 & (KT - 1);
+            bits = a.bits0 ? a.bits0[(size_t)b * nt0 + g] : (g == nt0 - 1 && rem) ? ((1ull << rem) - 1ull) : ~0ull;
+        } else if (g < nt0 + nt1) {
+            bits = a.bits1[(size_t)b * ((a.stride1 + KT - 1) / KT) + (g - nt0)];
+        }
+        const bool on = bits != 0ull;
+        const unsigned long long act = __ballot(on);
+        const int cnt = __popcll(act);
+        const int below = __popcll(act & ((1ull << lane) - 1ull));
+        // Active lanes go to their rank; the others to distinct slots past the active ones.
+        const int dest = 4 * (on ? below : cnt + (lane - below));
+        tl.t[w] = __builtin_amdgcn_ds_permute(dest, g);
+        tl.lo[w] = __builtin_amdgcn_ds_permute(dest, (int)(unsigned)bits);
+        tl.hi[w] = __builtin_amdgcn_ds_permute(dest, (int)(unsigned)(bits >> 32));
+        tl.base[w] = total;
+        total += cnt;
     }
-    const bool on = bits != 0ull;
-    const unsigned long long act = __ballot(on);
-    TileList tl;
-    tl.nact = __popcll(act);
-    const int below = __popcll(act & ((1ull << lane) - 1ull));
-    // Active lanes go to their rank; the others to distinct slots past the active ones.
-    const int dest = 4 * (on ? below : tl.nact + (lane - below));
-    tl.t = __builtin_amdgcn_ds_permute(dest, lane);
-    tl.lo = __builtin_amdgcn_ds_permute(dest, (int)(unsigned)bits);
-    tl.hi = __builtin_amdgcn_ds_permute(dest, (int)(unsigned)(bits >> 32));
+    tl.nact = total;
     return tl;
 }
 
@@ -284,7 +307,7 @@ __device__ __forceinline__ void store_block(const AttnArgs<T>& a, const f32x16 (
 // the K tiles of iteration j + 1 and the V tiles of iteration j have landed, and the
 // loads of K_{j+2} / V_{j+1} are issued into the slots freed by iteration j - 1.  LDS:
 // K ring [2][KVS] tiles + V ring [2][KVS] tiles.
-template <typename T, int QB, int KVS>
+template <typename T, int QB, int KVS, int NT>
 // At most two wavefronts per SIMD (the 64 KB of LDS allows no more): the register budget
 // that buys lets every fragment read of a tile go out before the MFMAs that consume it.
 __global__ __launch_bounds__(64 * QB * KVS) __attribute__((amdgpu_waves_per_eu(1, 2))) void attn32_kernel(
@@ -310,7 +333,7 @@ __global__ __launch_bounds__(64 * QB * KVS) __attribute__((amdgpu_waves_per_eu(1
 
     const int nt0 = (a.len0 + KT - 1) / KT;
     const int nt1 = a.K1 ? (a.len1 + KT - 1) / KT : 0;
-    const TileList tl = build_tile_list(a, b, lane, nt0, nt1);
+    const TileList<NT> tl = build_tile_list<NT>(a, b, lane, nt0, nt1);
     const int nact = tl.nact;
     const int niter = (nact + KVS - 1) / KVS;
 
@@ -341,7 +364,7 @@ __global__ __launch_bounds__(64 * QB * KVS) __attribute__((amdgpu_waves_per_eu(1
             const int gi = wave * LPK + ii;                                                   \
             int li = (j_) * KVS + gi / 8;                                                     \
             li = li < nact ? li : nact - 1;                                                   \
-            const int t = __builtin_amdgcn_readlane(tl.t, li);                                \
+            const int t = tl_read<NT>(tl.t, tl.base, li);                                     \
             const bool s0 = t < nt0;                                                          \
             const int key0 = s0 ? t * KT : (t - nt0) * KT;                                    \
             unsigned char* dst = ((kind_) ? vring : kring) + ((sl_) * KVS + gi / 8) * TILE_BYTES + (gi % 8) * 1024; \
@@ -421,8 +444,8 @@ __global__ __launch_bounds__(64 * QB * KVS) __attribute__((amdgpu_waves_per_eu(1
             for (int g = 0; g < 4; g++) vf[db][g] = frag<T>(vt, 32 * db + fr, 2 * g + fh);
 
         // Mask (partial tiles only): keys 32 kb + 8 g4 + 4 fh + c of this lane.
-        const unsigned vlo = (unsigned)__builtin_amdgcn_readlane(tl.lo, li);
-        const unsigned vhi = (unsigned)__builtin_amdgcn_readlane(tl.hi, li);
+        const unsigned vlo = (unsigned)tl_read<NT>(tl.lo, tl.base, li);
+        const unsigned vhi = (unsigned)tl_read<NT>(tl.hi, tl.base, li);
         if ((vlo & vhi) != 0xffffffffu) {
 #pragma unroll
             for (int kb = 0; kb < 2; kb++) {
@@ -505,247 +528,15 @@ __global__ __launch_bounds__(64 * QB * KVS) __attribute__((amdgpu_waves_per_eu(1
     store_block<T>(a, o, l_run, b, hh, bh, q0 + fr, fh);
 }
 
-// Two 32-query blocks per wavefront over the same key tiles (QW wavefronts along the
-// queries x KVS key parities per workgroup).  The blocks' dependency chains are
-// independent, so the in-order issue of one wavefront keeps the matrix core and the VALU
-// busy together: block 1's score MFMAs run while block 0's softmax is on the VALU, block
-// 0's P V MFMAs while block 1's softmax runs.  The K and V^T fragments of a tile are read
-// from LDS once for both blocks.  K and V^T tiles move one tile ahead in a two-slot ring.
-// Per query the arithmetic is attn32_kernel's (same MFMA sequences, lazy reference, parity
-// split and merge order), so the two kernels give identical bits.
-template <typename T, int QW, int KVS>
-__global__ __launch_bounds__(64 * QW * KVS) void attn64_kernel(AttnArgs<T> a, int nqg) {
-    typedef typename Vec8<T>::type V8;
-    constexpr int NW = QW * KVS, NB = 2;
-    constexpr int LPK = KVS * 8 / NW;  // load instructions per wave per K (or V) tile set
-    static_assert(LPK * NW == KVS * 8, "tiles must split over the waves");
-    static_assert((KVS - 1) * QW * NB * 34 * 64 * 4 <= 4 * KVS * TILE_BYTES, "merge buffer must fit the rings");
-    extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
-    unsigned char* kring = smem;                         // [2][KVS][TILE_BYTES]
-    unsigned char* vring = smem + 2 * KVS * TILE_BYTES;  // [2][KVS][TILE_BYTES]
-
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int qw = wave % QW, par = wave / QW;
-    const int pid = xcd_remap(blockIdx.x, gridDim.x);
-    const int qg = pid % nqg, bhid = pid / nqg;
-    const int hh = bhid % a.H, b = bhid / a.H;
-    const int q0 = qg * (64 * QW) + 64 * qw;
-    const int fr = lane & 31, fh = lane >> 5;
-    const size_t bh = (size_t)b * a.H + hh;
-
-    const int nt0 = (a.len0 + KT - 1) / KT;
-    const int nt1 = a.K1 ? (a.len1 + KT - 1) / KT : 0;
-    const TileList tl = build_tile_list(a, b, lane, nt0, nt1);
-    const int nact = tl.nact;
-    const int niter = (nact + KVS - 1) / KVS;
-
-    const T* K0b = a.K0 + bh * a.stride0 * 64;
-    const T* K1b = a.K1 ? a.K1 + bh * a.stride1 * 64 : nullptr;
-    const T* V0b = a.V0 + bh * 64 * (size_t)a.vstride0;
-    const T* V1b = a.V1 ? a.V1 + bh * 64 * (size_t)a.vstride1 : nullptr;
-
-    unsigned voK[LPK], voV0[LPK], voV1[LPK];
-#pragma unroll
-    for (int ii = 0; ii < LPK; ii++) {
-        const int gi = wave * LPK + ii;
-        const int r = (gi % 8) * 8 + lane / 8;
-        const unsigned cb = (unsigned)swz(r, lane % 8) * 16u;
-        voK[ii] = (unsigned)r * 128u + cb;
-        voV0[ii] = (unsigned)r * (unsigned)a.vstride0 * 2u + cb;
-        voV1[ii] = (unsigned)r * (unsigned)a.vstride1 * 2u + cb;
-    }
-    // K (kind 0) or V^T (kind 1) tiles of iteration j into ring slot sl: tile list entries
-    // j*KVS + p, clamped to the last entry so every wave issues LPK loads.
-#define ATT64_ISSUE(kind_, j_, sl_)                                                           \
-    do {                                                                                      \
-        _Pragma("unroll") for (int ii = 0; ii < LPK; ii++) {                                  \
-            const int gi = wave * LPK + ii;                                                   \
-            int li = (j_) * KVS + gi / 8;                                                     \
-            li = li < nact ? li : nact - 1;                                                   \
-            const int t = __builtin_amdgcn_readlane(tl.t, li);                                \
-            const bool s0 = t < nt0;                                                          \
-            const int key0 = s0 ? t * KT : (t - nt0) * KT;                                    \
-            unsigned char* dst = ((kind_) ? vring : kring) + ((sl_) * KVS + gi / 8) * TILE_BYTES + (gi % 8) * 1024; \
-            if ((kind_) == 0) {                                                               \
-                const int len = s0 ? a.len0 : a.len1;                                         \
-                buf_load_lds16(make_rsrc((s0 ? K0b : K1b) + (size_t)key0 * 64, (unsigned)(len - key0) * 128u), \
-                               voK[ii], dst);                                                 \
-            } else {                                                                          \
-                const int vs = s0 ? a.vstride0 : a.vstride1;                                  \
-                buf_load_lds16(make_rsrc((s0 ? V0b : V1b) + key0, (unsigned)(64 * vs - key0) * 2u), \
-                               s0 ? voV0[ii] : voV1[ii], dst);                                \
-            }                                                                                 \
-        }                                                                                     \
-    } while (0)
-
-    // Q^T fragments (B operand) of block nb: query q0 + 32 nb + fr, dims 16 ks + 8 fh .. +8.
-    V8 qf[NB][4];
-#pragma unroll
-    for (int nb = 0; nb < NB; nb++) {
-        int q = q0 + 32 * nb + fr;
-        q = q < a.Sq ? q : a.Sq - 1;
-        const T* qp = a.Q + (bh * a.Sq + q) * 64 + 8 * fh;
-#pragma unroll
-        for (int ks = 0; ks < 4; ks++) qf[nb][ks] = *reinterpret_cast<const V8*>(qp + 16 * ks);
-    }
-    V8 ones, qbias[NB];
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-        ones[e] = static_cast<T>(0.f);
-#pragma unroll
-        for (int nb = 0; nb < NB; nb++) qbias[nb][e] = static_cast<T>(0.f);
-    }
-    if (fh == 0) ones[0] = static_cast<T>(1.f);
-
-    f32x16 o[NB][2];
-#pragma unroll
-    for (int nb = 0; nb < NB; nb++)
-#pragma unroll
-        for (int db = 0; db < 2; db++)
-#pragma unroll
-            for (int e = 0; e < 16; e++) o[nb][db][e] = 0.f;
-    float m_ref[NB], l_run[NB];
-#pragma unroll
-    for (int nb = 0; nb < NB; nb++) m_ref[nb] = l_run[nb] = 0.f;
-    bool first = true;  // wave-uniform: no tile processed yet
-
-    // A (row, head) with no valid key (nact = 0) issues no load and runs no iteration.
-    if (nact > 0) {
-        ATT64_ISSUE(0, 0, 0);
-        ATT64_ISSUE(1, 0, 0);
-    }
-    for (int j = 0; j < niter; j++) {
-        // Tile j has landed once this wave's loads are done and all waves met; every wave
-        // is then past tile j - 1, whose slot takes tile j + 1.
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        raw_barrier();
-        if (j + 1 < niter) {
-            ATT64_ISSUE(0, j + 1, (j + 1) & 1);
-            ATT64_ISSUE(1, j + 1, (j + 1) & 1);
-        }
-        const int li = j * KVS + par;
-        if (li >= nact) continue;  // this parity has no tile in the last iteration
-        const unsigned char* kt = kring + ((j & 1) * KVS + par) * TILE_BYTES;
-        const unsigned char* vt = vring + ((j & 1) * KVS + par) * TILE_BYTES;
-        const unsigned vlo = (unsigned)__builtin_amdgcn_readlane(tl.lo, li);
-        const unsigned vhi = (unsigned)__builtin_amdgcn_readlane(tl.hi, li);
-        const bool partial = (vlo & vhi) != 0xffffffffu;
-
-        // S'^T of both blocks: the reference step, then 4 k16 steps per 32-key half; the
-        // K fragments are read once.
-        f32x16 s[NB][2];
-        {
-            V8 kf[2][4];
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++)
-#pragma unroll
-                for (int kb = 0; kb < 2; kb++) kf[kb][ks] = frag<T>(kt, 32 * kb + fr, 2 * ks + fh);
-#pragma unroll
-            for (int nb = 0; nb < NB; nb++) {
-#pragma unroll
-                for (int kb = 0; kb < 2; kb++) {
-                    f32x16 z;
-#pragma unroll
-                    for (int e = 0; e < 16; e++) z[e] = 0.f;
-                    s[nb][kb] = mma32x16(ones, qbias[nb], z);
-                }
-#pragma unroll
-                for (int ks = 0; ks < 4; ks++)
-#pragma unroll
-                    for (int kb = 0; kb < 2; kb++) s[nb][kb] = mma32x16(kf[kb][ks], qf[nb][ks], s[nb][kb]);
-            }
-        }
-        V8 vf[2][4];
-#pragma unroll
-        for (int g = 0; g < 4; g++)
-#pragma unroll
-            for (int db = 0; db < 2; db++) vf[db][g] = frag<T>(vt, 32 * db + fr, 2 * g + fh);
-
-        // Online softmax of each block (log2 domain, lazy reference), then O^T += V^T P^T.
-        V8 pf[NB][4];
-#pragma unroll
-        for (int nb = 0; nb < NB; nb++) {
-            if (partial) {
-#pragma unroll
-                for (int kb = 0; kb < 2; kb++) {
-                    const unsigned w = (kb ? vhi : vlo) >> (4 * fh);
-#pragma unroll
-                    for (int g4 = 0; g4 < 4; g4++)
-#pragma unroll
-                        for (int c = 0; c < 4; c++)
-                            if (!((w >> (8 * g4 + c)) & 1u)) s[nb][kb][4 * g4 + c] = -INFINITY;
-                }
-            }
-            float mx = -INFINITY;
-#pragma unroll
-            for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-                for (int e = 0; e < 16; e++) mx = fmaxf(mx, s[nb][kb][e]);
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            const bool need = first || mx > TAU;
-            if (__ballot(need)) {
-                const float nref = need ? round_to<T>(m_ref[nb] + mx) : m_ref[nb];
-                const float delta = nref - m_ref[nb];
-                const float corr = first ? 0.f : fast_exp2(-delta);
-                m_ref[nb] = nref;
-#pragma unroll
-                for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-                    for (int e = 0; e < 16; e++) s[nb][kb][e] -= delta;
-#pragma unroll
-                for (int db = 0; db < 2; db++) o[nb][db] *= corr;
-                l_run[nb] *= corr;
-                if (fh == 0) qbias[nb][0] = static_cast<T>(-m_ref[nb]);
-            }
-            float psum = 0.f;
-#pragma unroll
-            for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-                for (int e = 0; e < 16; e++) {
-                    const float p = fast_exp2(s[nb][kb][e]);
-                    psum += p;
-                    pf[nb][2 * kb + (e >> 3)][e & 7] = static_cast<T>(p);
-                }
-            l_run[nb] += psum;
-#pragma unroll
-            for (int db = 0; db < 2; db++)
-#pragma unroll
-                for (int g = 0; g < 4; g++) o[nb][db] = mma32x16(vf[db][g], pf[nb][g], o[nb][db]);
-        }
-        first = false;
-    }
-#undef ATT64_ISSUE
-    float m_run[NB];
-#pragma unroll
-    for (int nb = 0; nb < NB; nb++) m_run[nb] = first ? -INFINITY : m_ref[nb];
-    if constexpr (KVS > 1) {
-        __syncthreads();
-        if (!merge_parities<QW, KVS, NB>(smem, par, qw, lane, o, m_run, l_run)) return;
-    }
-#pragma unroll
-    for (int nb = 0; nb < NB; nb++) store_block<T>(a, o[nb], l_run[nb], b, hh, bh, q0 + 32 * nb + fr, fh);
-}
-
-template <typename T, int QW, int KVS>
-int launch_attn64_cfg(const AttnArgs<T>& a, hipStream_t st) {
-    const size_t lds = (size_t)4 * KVS * TILE_BYTES;
-    static std::once_flag once;
-    static hipError_t attr_rc = hipSuccess;
-    if (set_lds_limit_once(once, attr_rc, (const void*)attn64_kernel<T, QW, KVS>, (int)lds) != hipSuccess) return -2;
-    const int nqg = (a.Sq + 64 * QW - 1) / (64 * QW);
-    attn64_kernel<T, QW, KVS><<<dim3(nqg * a.H * a.B), 64 * QW * KVS, lds, st>>>(a, nqg);
-    return 0;
-}
-
-template <typename T, int QB, int KVS>
+template <typename T, int QB, int KVS, int NT>
 int launch_attn32_cfg(const AttnArgs<T>& a, hipStream_t st) {
     const size_t lds = (size_t)4 * KVS * TILE_BYTES;
     static std::once_flag once;
     static hipError_t attr_rc = hipSuccess;
-    if (set_lds_limit_once(once, attr_rc, (const void*)attn32_kernel<T, QB, KVS>, (int)lds) != hipSuccess) return -2;
+    if (set_lds_limit_once(once, attr_rc, (const void*)attn32_kernel<T, QB, KVS, NT>, (int)lds) != hipSuccess)
+        return -2;
     const int nqb = (a.Sq + 32 * QB - 1) / (32 * QB);
-    attn32_kernel<T, QB, KVS><<<dim3(nqb * a.H * a.B), 64 * QB * KVS, lds, st>>>(a, nqb);
+    attn32_kernel<T, QB, KVS, NT><<<dim3(nqb * a.H * a.B), 64 * QB * KVS, lds, st>>>(a, nqb);
     return 0;
 }
 
@@ -756,7 +547,7 @@ int launch_attention32_t(const AttnArgs<T>& a, hipStream_t st) {
     if ((a.vstride0 % KT) || (a.K1 && (a.vstride1 % KT))) return -1;
     if (!std::is_same<T, bf16>::value && a.out_mode == 2) return -1;
     const int ntiles = (a.len0 + KT - 1) / KT + (a.K1 ? (a.len1 + KT - 1) / KT : 0);
-    if (ntiles > 64) return -1;  // the tile list holds one entry per lane (4096 keys)
+    if (ntiles > kAttnMaxKeyTiles) return -1;  // four tile-list words per lane (16384 keys)
     // 2 query blocks x 2 key parities (4 waves, 64 KB LDS) at every size.  Against 4 x 2:
     // one CFG row of 750 frames 18.2 vs 21.1 us with context keys, 12.3 vs 14.5 us without;
     // B = 2 rows 42.0 vs 42.2 us per operator call; BASELINE config 5 (32 rows) 340.5 vs
@@ -765,7 +556,10 @@ int launch_attention32_t(const AttnArgs<T>& a, hipStream_t st) {
     // One key parity (4 x 1, 32 KB) ran config 5 faster still (323.8 ms) but slower at
     // B = 2 (45.2 us), and a size-dependent choice would make a row's result depend on the
     // batch it is launched with.
-    return launch_attn32_cfg<T, 2, 2>(a, st);
+    // The tile list of up to 4096 keys fits one word per lane; longer key ranges take four
+    // (the same arithmetic per tile, in the same order).
+    if (ntiles <= 64) return launch_attn32_cfg<T, 2, 2, 1>(a, st);
+    return launch_attn32_cfg<T, 2, 2, 4>(a, st);
 }
 
 // Operator staging (irodori_op_sdpa, Dh = 64 on 16-bit operands): the caller's Q, V and
@@ -822,7 +616,7 @@ template <typename T>
 int launch_sdpa_staged(const T* q, const T* k, const T* v, const float* mask, int B, int H, int Sq, int Skv,
                        float scale, float* out, void* ws, size_t ws_bytes, hipStream_t st) {
     const int vs = (Skv + 63) / 64 * 64;
-    if (B <= 0 || H <= 0 || Sq <= 0 || Skv <= 0 || vs / 64 > 64) return -1;
+    if (B <= 0 || H <= 0 || Sq <= 0 || Skv <= 0 || vs / 64 > kAttnMaxKeyTiles) return -1;
     if (ws_bytes < sdpa_stage_bytes(B, H, Sq, Skv) || ((uintptr_t)ws & 255)) return -1;
     auto al = [](size_t n) { return (n + 255) / 256 * 256; };
     unsigned char* p = static_cast<unsigned char*>(ws);

@@ -410,8 +410,13 @@ __attribute__((amdgpu_waves_per_eu(WAVES_M * WAVES_N == 4 ? 2 : 1))) void gemm_k
     // buffer-to-LDS loads as the operands, 1 KB (4 tokens) per instruction; token
     // m0 + 4 j + lane / 16 lands at 256 (4 j) + 16 lane.  With S >= 4 the token index steps
     // by 4 with one wrap at most (rows past M read a valid table row, unused).
+    // The tile needs them when any of its 64-column heads does: with D an odd multiple of 64
+    // a tile can start on the last q head (no RoPE) and end on k head 0 (RoPE).
     [[maybe_unused]] bool rope_wg = false;
-    if constexpr (EPI == EPI_QKVG) rope_wg = n0 / a.D <= 1 && (n0 % a.D) / 64 < a.H / 2;
+    if constexpr (EPI == EPI_QKVG) {
+#pragma unroll
+        for (int c = n0; c < n0 + BN; c += 64) rope_wg = rope_wg || (c / a.D <= 1 && (c % a.D) / 64 < a.H / 2);
+    }
     [[maybe_unused]] auto rope_rows_issue = [&](unsigned char* dst) {
         static_assert(EPI != EPI_QKVG || (BM * 256 <= STAGE_BYTES && (BM * 256 / 1024) % NW == 0),
                       "RoPE rows fill whole stage instructions");

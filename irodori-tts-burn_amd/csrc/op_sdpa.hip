@@ -4,6 +4,7 @@
 // staging Q / V^T / key bits) and the generic flash kernel, and the staging buffer --
 // stream-ordered per call (irodori_op_sdpa) or a fixed per-GPU device array
 // (irodori_op_sdpa_noalloc, for callers that cannot allocate).
+#include <atomic>
 #include <mutex>
 
 #include "../../include/irodori_hip.h"
@@ -26,9 +27,9 @@ int check_sdpa_args(int dtype, const void* q, const void* k, const void* v, int 
 }
 
 // 16-bit operands with Dh = 64 run on the model's joint attention kernel after staging
-// (its tile list holds up to 4096 keys); everything else on the generic flash kernel.
+// (its tile list holds up to 16384 keys); everything else on the generic flash kernel.
 bool sdpa_staged(int dtype, int Dh, int Skv) {
-    return dtype != IRODORI_DTYPE_F32 && Dh == 64 && Skv <= 4096;
+    return dtype != IRODORI_DTYPE_F32 && Dh == 64 && Skv <= 64 * kAttnMaxKeyTiles;
 }
 
 template <typename T>
@@ -74,22 +75,43 @@ static __device__ __align__(256) unsigned char scratch[IRODORI_SDPA_SCRATCH_BYTE
 
 constexpr int kMaxDevices = 64;
 std::once_flag g_scratch_once[kMaxDevices];
-void* g_scratch_ptr[kMaxDevices] = {};
+std::atomic<void*> g_scratch_ptr[kMaxDevices] = {};
 hipError_t g_scratch_rc[kMaxDevices] = {};
 
-// The current device's scratch address (device must be current), or a status code.
-int scratch_for_current_device(void** out) {
+// The scratch address on the device of `st`, which must be the current device (the address
+// is looked up with that device current, and the kernels run on the stream's device), or a
+// status code.  The lookup happens on the first call on a device; it is refused while `st`
+// is capturing (a first call inside a graph capture), so capturing callers make one eager
+// call first.
+int scratch_for_stream(hipStream_t st, void** out) {
     int dev = -1;
     IRO_HIP_CHECK(hipGetDevice(&dev));
+    if (st) {
+        int sdev = -1;
+        IRO_HIP_CHECK(hipStreamGetDevice(st, &sdev));
+        IRO_REQUIRE(sdev == dev, IRODORI_ERR_INVALID_ARG,
+                    "irodori_op_sdpa_noalloc: the stream belongs to device " + std::to_string(sdev) +
+                        " but device " + std::to_string(dev) + " is current; make the stream's device current");
+    }
     IRO_REQUIRE(dev >= 0 && dev < kMaxDevices, IRODORI_ERR_INVALID_ARG, "device index beyond the scratch table");
+    if (!g_scratch_ptr[dev].load()) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        IRO_HIP_CHECK(hipStreamIsCapturing(st, &cs));
+        IRO_REQUIRE(cs == hipStreamCaptureStatusNone, IRODORI_ERR_INVALID_ARG,
+                    "irodori_op_sdpa_noalloc: the first call on a device must not be under graph capture "
+                    "(it looks up the fixed buffer's address); make one call outside the capture first");
+    }
     std::call_once(g_scratch_once[dev], [dev] {
-        g_scratch_rc[dev] = hipGetSymbolAddress(&g_scratch_ptr[dev], HIP_SYMBOL(scratch));
+        void* p = nullptr;
+        g_scratch_rc[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        g_scratch_ptr[dev].store(p);
     });
-    if (g_scratch_rc[dev] != hipSuccess || !g_scratch_ptr[dev]) {
+    void* p = g_scratch_ptr[dev].load();
+    if (g_scratch_rc[dev] != hipSuccess || !p) {
         set_last_error(std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(g_scratch_rc[dev]));
         return IRODORI_ERR_HIP;
     }
-    *out = g_scratch_ptr[dev];
+    *out = p;
     return IRODORI_OK;
 }
 
@@ -127,7 +149,7 @@ int irodori_op_sdpa_noalloc(int dtype, const void* q, const void* k, const void*
                     " bytes, above the fixed " + std::to_string((size_t)IRODORI_SDPA_SCRATCH_BYTES) +
                     "-byte buffer; use irodori_op_sdpa");
     void* ws = nullptr;
-    IRO_TRY(scratch_for_current_device(&ws));
+    IRO_TRY(scratch_for_stream(st, &ws));
     // The staging kernel writes every byte the attention kernel reads (Q rows, V^T with zero
     // keys past seq_kv, the key bits), so nothing left by an earlier call is read.
     return sdpa_run_staged(dtype, q, k, v, mask, B, H, Sq, Skv, scale, out, ws, IRODORI_SDPA_SCRATCH_BYTES, st);

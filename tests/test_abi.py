@@ -117,6 +117,35 @@ def test_ctx_create_config_errors(field, value, code):
     assert L.last_error()
 
 
+def _plumbing_cfg_c(dtype, max_seq, max_ctx):
+    cfg = ih.cfg_cpu_plumbing()
+    return L.DitConfigC(cfg.latent_dim, cfg.model_dim, cfg.num_layers, cfg.num_heads, cfg.head_dim,
+                        cfg.mlp_hidden, cfg.adaln_rank, cfg.timestep_embed_dim, cfg.norm_eps,
+                        cfg.rope_theta, dtype, 2, max_seq, max_ctx)
+
+
+@pytest.mark.parametrize("dtype", [L.DTYPE_BF16, L.DTYPE_FP8])
+def test_ctx_create_refuses_more_keys_than_the_attention_lists(dtype):
+    # 16-bit attention: ceil(max_seq / 64) + ceil(max_ctx / 64) <= 256 key tiles, checked
+    # at create (before any device call), so a long request never fails inside a launch.
+    lib = L.load()
+    h = C.c_void_p()
+    c = _plumbing_cfg_c(dtype, 16384 - 64 + 1, 64)  # 256 + 1 tiles
+    assert lib.irodori_ctx_create(0, C.byref(c), C.byref(h)) == L.ERR_SHAPE
+    assert "16384 keys" in L.last_error() and not h.value
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-device error path")
+def test_ctx_create_key_limit_boundary_reaches_the_device_check():
+    # 255 latent tiles + 1 context tile pass the shape checks (the call then fails for want
+    # of a device here); so does an f32 context far past the limit (its attention has none).
+    lib = L.load()
+    h = C.c_void_p()
+    for dtype, S, T in ((L.DTYPE_BF16, 16320, 64), (L.DTYPE_F32, 40000, 3000)):
+        c = _plumbing_cfg_c(dtype, S, T)
+        assert lib.irodori_ctx_create(0, C.byref(c), C.byref(h)) == L.ERR_HIP, L.last_error()
+
+
 @pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-device error path")
 def test_ctx_create_without_device_fails_cleanly():
     with pytest.raises(ih.IrodoriError) as ei:

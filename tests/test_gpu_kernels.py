@@ -158,24 +158,57 @@ def test_sdpa_all_masked_rows_are_zero():
     assert np.abs(o[0]).sum() > 0
 
 
-def test_sdpa_config2_joint_shape_bf16(oracle64):
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_sdpa_config2_joint_shape(oracle64, dtype):
     # Isolated joint attention: B=2, H=16, Dh=64, 750 queries; keys = 750 latent ++ 256 text ++
     # 375 speaker, text valid length uniform in [32, 256], Q/K/V ~ N(0, 1).  (RoPE is part
-    # of the model path and is covered by the model tests.)
+    # of the model path and is covered by the model tests.)  The oracle takes the same
+    # rounded operands; the kernel also rounds q * scale * log2(e) and P to the operand type.
     B, H, Sq, Dh, Tt, Ts = 2, 16, 750, 64, 256, 375
     Skv = Sq + Tt + Ts
     rng = np.random.default_rng(0)
-    q, k, v = (bf16_round(rng.standard_normal((B, H, n, Dh)).astype(np.float32))
-               for n in (Sq, Skv, Skv))
+    q, k, v = (rng.standard_normal((B, H, n, Dh)).astype(np.float32) for n in (Sq, Skv, Skv))
+    if dtype == "bf16":
+        code, tdt, tol = L.DTYPE_BF16, torch.bfloat16, 1e-2
+        q, k, v = (bf16_round(a) for a in (q, k, v))
+    else:
+        code, tdt, tol = L.DTYPE_F16, torch.float16, 2e-3
+        q, k, v = (a.astype(np.float16).astype(np.float32) for a in (q, k, v))
     m = np.ones((B, Skv), np.float32)
     for b in range(B):
         valid = int(rng.integers(32, 257))
         m[b, Sq + valid:Sq + Tt] = 0
-    dq, dk, dv = (dev(a, torch.bfloat16) for a in (q, k, v))
+    dq, dk, dv = (dev(a, tdt) for a in (q, k, v))
     dm = dev(m)
     out = torch.empty(q.shape, dtype=torch.float32, device="cuda")
-    ops.sdpa(L.DTYPE_BF16, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), dm.data_ptr(), B, H, Sq,
+    ops.sdpa(code, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), dm.data_ptr(), B, H, Sq,
              Skv, Dh, Dh ** -0.5, out.data_ptr())
     torch.cuda.synchronize()
     want = oracle64.sdpa(q, k, v, m, Dh ** -0.5)
-    assert rel_l2(out.cpu().numpy(), want) < 1e-2
+    err = rel_l2(out.cpu().numpy(), want)
+    print("config 2 %s: rel L2 %.2e, max abs %.2e" % (dtype, err, np.abs(out.cpu().numpy() - want).max()))
+    assert err < tol
+
+
+@pytest.mark.parametrize("Skv", [4097, 4796, 16384])
+def test_sdpa_key_tiles_beyond_one_list_word(oracle64, Skv):
+    # More than 64 key tiles per row: the joint kernel's tile list spans several words per
+    # lane.  Row 0 drops whole tiles from the first word (and, when present, the second)
+    # so that the entries of later words shift down; row 1 has a partial mask in every tile.
+    B, H, Sq, Dh = 2, 2, 70, 64
+    rng = np.random.default_rng(Skv)
+    q, k, v = (bf16_round(rng.standard_normal((B, H, n, Dh)).astype(np.float32)) for n in (Sq, Skv, Skv))
+    m = np.ones((B, Skv), np.float32)
+    m[0, 640:1600] = 0
+    m[0, 4160:4300] = 0
+    m[0, 9000:9999] = 0
+    m[1, ::7] = 0
+    dq, dk, dv = (dev(a, torch.bfloat16) for a in (q, k, v))
+    out = torch.full(q.shape, 7.0, dtype=torch.float32, device="cuda")
+    ops.sdpa(L.DTYPE_BF16, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), dev(m).data_ptr(), B, H, Sq, Skv, Dh,
+             Dh ** -0.5, out.data_ptr())
+    torch.cuda.synchronize()
+    want = oracle64.sdpa(q, k, v, m, Dh ** -0.5)
+    err = rel_l2(out.cpu().numpy(), want)
+    print("Skv %d: rel L2 %.2e" % (Skv, err))
+    assert err < 1e-2

@@ -50,6 +50,14 @@ SMALL = {
     # device, norms unfused) with two of its twelve layers; 4 text + 9 speaker keys as the
     # A6000 benchmark's request (text_len 4, 8 reference frames + the mean token)
     "pub500m": (lambda: dataclasses.replace(ih.cfg_published_500m(), num_layers=2), 64, 4, 9, 0.02, 0.05),
+    # an odd head count (3 x 64, D = 192): the 128-column QKV+gate tile at column D - 64
+    # holds the last q head (no RoPE) and k head 0 (RoPE), so the tile must load the RoPE
+    # rows although its first head does not rotate
+    "h3": (lambda: dataclasses.replace(ih.cfg_tiny(), model_dim=192, num_heads=3, mlp_hidden=320), 40, 20, 13,
+           0.05, 0.1),
+    # 4000 latent + 250 context keys: 67 key tiles per row, past the 64 one word of the
+    # bf16 attention's tile list holds
+    "long_keys": (ih.cfg_tiny, 4000, 150, 100, 0.05, 0.1),
 }
 
 

@@ -49,9 +49,24 @@ def test_noalloc_matches_allocating_entry_point(oracle64, dtype, tdt):
         assert err < (2e-3 if dtype == L.DTYPE_F16 else 1e-2), (shape, err)
 
 
+def _boundary_shape(sq):
+    # One head of 64 keys: the staging is Q (sq x 128 bytes, rounded up to 256) + V^T
+    # (8192 bytes) + the key bits (one word, rounded up to 256).  sq = 131006 fills the
+    # 16 MiB buffer exactly; 131007 is one 256-byte step past it.
+    return 1, 1, sq, 64
+
+
+def test_noalloc_accepts_the_largest_shape_that_fits():
+    B, H, Sq, Skv = _boundary_shape(131006)
+    assert Sq * 128 + 8192 + 256 == L.SDPA_SCRATCH_BYTES
+    q, k, v, m = _inputs(B, H, Sq, Skv, 4)
+    got, _ = _run(ops.sdpa_noalloc, L.DTYPE_BF16, torch.bfloat16, q, k, v, m)
+    want, _ = _run(ops.sdpa, L.DTYPE_BF16, torch.bfloat16, q, k, v, m)
+    assert np.array_equal(got, want)
+
+
 def test_noalloc_refuses_shapes_beyond_its_buffer():
-    # 4 x 32 heads x 2048 queries: Q alone takes 16 MiB of staging.
-    B, H, Sq, Skv = 4, 32, 2048, 64
+    B, H, Sq, Skv = _boundary_shape(131007)
     q = torch.zeros((B, H, Sq, 64), dtype=torch.bfloat16, device="cuda")
     kv = torch.zeros((B, H, Skv, 64), dtype=torch.bfloat16, device="cuda")
     out = torch.empty((B, H, Sq, 64), dtype=torch.float32, device="cuda")
@@ -59,3 +74,35 @@ def test_noalloc_refuses_shapes_beyond_its_buffer():
         ops.sdpa_noalloc(L.DTYPE_BF16, q.data_ptr(), kv.data_ptr(), kv.data_ptr(), 0, B, H, Sq, Skv, 64, 0.125,
                          out.data_ptr())
     assert ei.value.kind == "Shape" and "noalloc" in str(ei.value)
+
+
+def test_noalloc_under_graph_capture_replays_the_eager_result():
+    # One eager call (it resolves the buffer's address), then the same call captured in a
+    # graph on torch's capture stream and replayed several times, with eager work on the
+    # same buffers between the replays; every replay rewrites the output bit for bit.
+    B, H, Sq, Skv = 2, 4, 200, 300
+    q, k, v, m = _inputs(B, H, Sq, Skv, 5)
+    dq, dk, dv = (torch.from_numpy(a).to("cuda").to(torch.bfloat16).contiguous() for a in (q, k, v))
+    dm = torch.from_numpy(m).to("cuda")
+    out = torch.full((B, H, Sq, 64), 7.0, dtype=torch.float32, device="cuda")
+
+    def call(stream):
+        ops.sdpa_noalloc(L.DTYPE_BF16, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), dm.data_ptr(), B, H, Sq, Skv,
+                         64, 0.125, out.data_ptr(), stream)
+
+    call(torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    eager = out.cpu().numpy()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        call(torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    other_q, other_k, other_v, other_m = _inputs(1, 2, 50, 70, 6)
+    for rep in range(4):
+        out.fill_(7.0)
+        # An eager call of another shape in between leaves other contents in the buffer.
+        _run(ops.sdpa_noalloc, L.DTYPE_BF16, torch.bfloat16, other_q, other_k, other_v, other_m)
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy(), eager), rep
+
