@@ -14,8 +14,9 @@
 //                    group, so a query's max / sum reduce over lanes l and l^32.
 //   online softmax   in the log2 domain (Q is pre-scaled by Dh^-1/2 log2 e), with a lazy
 //                    reference: m (a bf16 value) moves only on the wavefront's first tile
-//                    or when a score exceeds it by more than 2^TAU, so the O / l rescale
-//                    is off the common path and p = exp2(S') <= 2^TAU.
+//                    or when a lane's sum of p = exp2(S') over the tile exceeds 2^TAU, so
+//                    the tile max and the O / l rescale are off the common path and
+//                    p <= 2^TAU.
 //   O^T += V^T P^T   8 MFMAs; P^T is the S'^T accumulator itself, 8 consecutive values per
 //                    k16 step, and V^T is stored with bits 2 and 3 of every key index
 //                    swapped so that the matching 8 keys are one 16-byte LDS read.
@@ -72,7 +73,8 @@ __device__ __forceinline__ f32x16 mma32x16(f16x8 a, f16x8 b, f32x16 c) {
 
 constexpr int KT = 64;
 constexpr int TILE_BYTES = KT * 128;  // 64 rows x 128 bytes (bf16 Dh = 64)
-constexpr float TAU = 8.0f;           // lazy-reference slack, log2 units
+constexpr float TAU = 16.0f;          // lazy-reference slack, log2 units
+constexpr float kSumMax = 65536.0f;   // 2^TAU: a lane's tile sum above it moves the reference
 
 __device__ __forceinline__ void raw_barrier() { asm volatile("s_barrier" ::: "memory"); }
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, unsigned bytes) {
@@ -457,36 +459,15 @@ __global__ __launch_bounds__(64 * QB * KVS) __attribute__((amdgpu_waves_per_eu(1
                         if (!((w >> (8 * g4 + c)) & 1u)) sc[kb][4 * g4 + c] = -INFINITY;
             }
         }
-        // Tile max as a balanced tree (depth 5 instead of a 32-long chain), then the halves.
-        float m16[16];
-#pragma unroll
-        for (int e = 0; e < 16; e++) m16[e] = fmaxf(sc[0][e], sc[1][e]);
-#pragma unroll
-        for (int w = 8; w > 0; w >>= 1)
-#pragma unroll
-            for (int e = 0; e < w; e++) m16[e] = fmaxf(m16[e], m16[e + w]);
-        float mx = max_halves(m16[0]);
-        // Move the reference on the first tile or when a score exceeds it by 2^TAU.
-        const bool need = first || mx > TAU;
-        if (__ballot(need)) {
-            const float nref = need ? round_to<T>(m_ref + mx) : m_ref;
-            const float delta = nref - m_ref;
-            const float corr = first ? 0.f : fast_exp2(-delta);
-            m_ref = nref;
-#pragma unroll
-            for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-                for (int e = 0; e < 16; e++) sc[kb][e] -= delta;
-#pragma unroll
-            for (int db = 0; db < 2; db++) o[db] *= corr;
-            l_run *= corr;
-            if (fh == 0) qbias[0] = static_cast<T>(-m_ref);
-        }
-        first = false;
-
-        // Scores of tile j + 1 on the matrix core, softmax of tile j on the VALU.
-        // (Computed unconditionally to keep one scheduling region; without a next tile the
-        // slot holds stale data and the result is dropped.)
+        // Softmax of tile j against the current reference, on the VALU, while the scores
+        // of tile j + 1 run on the matrix core.  (Those are computed unconditionally to keep
+        // one scheduling region; without a next tile the slot holds stale data and the
+        // result is dropped.)  The reference is corrected afterwards, off the common path:
+        // the tile max is needed only on the wavefront's first tile, or when a lane's sum
+        // shows a probability that may exceed 2^TAU (any p > 2^TAU makes the sum exceed it;
+        // an overflow to +inf does too).
+        // The next tile's scores subtract the reference in use now (qbias is updated below),
+        // so a moved reference also shifts the scores already computed into sn.
         score_tile<T>(sn, kring + (((j + 1) & 1) * KVS + par) * TILE_BYTES, fr, fh, qf, ones, qbias);
         float psum = 0.f;
         V8 pf[4];
@@ -498,14 +479,48 @@ __global__ __launch_bounds__(64 * QB * KVS) __attribute__((amdgpu_waves_per_eu(1
                 psum += p;
                 pf[2 * kb + (e >> 3)][e & 7] = static_cast<T>(p);
             }
-        l_run += psum;
         // 8 K-fragment reads, then each score MFMA followed by a slice of the softmax.
         __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
 #pragma unroll
         for (int i = 0; i < 10; i++) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
         }
+        const unsigned long long over = __ballot(first || !(psum <= kSumMax));
+        if (over) {
+            // Lanes l and l ^ 32 hold one query's two key halves: either one asks for both.
+            const bool need = ((over >> lane) | (over >> (lane ^ 32))) & 1ull;
+            // Tile max as a balanced tree, then the halves.
+            float m16[16];
+#pragma unroll
+            for (int e = 0; e < 16; e++) m16[e] = fmaxf(sc[0][e], sc[1][e]);
+#pragma unroll
+            for (int w = 8; w > 0; w >>= 1)
+#pragma unroll
+                for (int e = 0; e < w; e++) m16[e] = fmaxf(m16[e], m16[e + w]);
+            const float mx = max_halves(m16[0]);
+            const float nref = need ? round_to<T>(m_ref + mx) : m_ref;
+            const float delta = nref - m_ref;
+            const float corr = first ? 0.f : fast_exp2(-delta);
+            m_ref = nref;
+#pragma unroll
+            for (int db = 0; db < 2; db++) o[db] *= corr;
+            l_run *= corr;
+            psum = 0.f;
+#pragma unroll
+            for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    sc[kb][e] -= delta;
+                    sn[kb][e] -= delta;
+                    const float p = fast_exp2(sc[kb][e]);
+                    psum += p;
+                    pf[2 * kb + (e >> 3)][e & 7] = static_cast<T>(p);
+                }
+            if (fh == 0) qbias[0] = static_cast<T>(-m_ref);
+        }
+        first = false;
+        l_run += psum;
         // O^T += V^T P^T over the 4 16-key groups of the tile.
 #pragma unroll
         for (int db = 0; db < 2; db++)
