@@ -73,11 +73,11 @@ typedef struct irodori_ctx irodori_ctx;
 /* Model dimensions: the ModelConfig fields the DiT forward reads
  * (src/config/model.rs:8-44), plus device sizing. */
 typedef struct irodori_dit_config {
-    int32_t latent_dim;         /* patched latent dim P (latent_dim * latent_patch_size), <= 128 */
+    int32_t latent_dim;         /* patched latent dim P (latent_dim * latent_patch_size), <= 256 */
     int32_t model_dim;          /* D */
     int32_t num_layers;         /* L */
-    int32_t num_heads;          /* H (head_dim = D / H must be 64) */
-    int32_t head_dim;           /* Dh */
+    int32_t num_heads;          /* H (head_dim = D / H) */
+    int32_t head_dim;           /* Dh: 64, or 128 for bf16 / f32 (fp8 compute needs 64) */
     int32_t mlp_hidden;         /* F = floor(D * mlp_ratio) (diffusion.rs:32), multiple of 16 */
     int32_t adaln_rank;         /* r (norm.rs:101-104) */
     int32_t timestep_embed_dim; /* t_dim */

@@ -198,6 +198,13 @@ int dalloc(irodori_ctx* c, P** p, size_t bytes) {
     return dev_alloc(c, reinterpret_cast<void**>(p), bytes);
 }
 
+// Key order of the V^T copies (latent and context): the 32x32x16 attention's for bf16 /
+// fp8 contexts with 64-dim heads, the 16x16 attention's otherwise (f32, 128-dim heads).
+bool vt_bf16_order(const irodori_ctx* c) { return c->bf16 && c->cfg.head_dim == 64; }
+
+// Columns of the output head's W' rows for a P-channel latent (zeros past P).
+int head_width(int P) { return P <= 32 ? 32 : P <= 64 ? 64 : P <= 128 ? 128 : 256; }
+
 
 
 
@@ -509,7 +516,9 @@ int enqueue_part(irodori_ctx* c, int l, int B, int S, const ModTable& mt, int pa
             aa.O8 = o8;
             aa.O8s = o8s;
             int arc;
-            if constexpr (std::is_same<T, bf16>::value)
+            if (Dh == 128)
+                arc = launch_attention<T, 128>(aa, st);
+            else if constexpr (std::is_same<T, bf16>::value)
                 arc = launch_attention32(aa, st);
             else
                 arc = launch_attention<T, 64>(aa, st);
@@ -831,12 +840,14 @@ int irodori_ctx_create(int device, const irodori_dit_config* cfg, irodori_ctx** 
                 "fp8 compute needs a model_dim multiple of 128");
     IRO_REQUIRE(g.num_layers > 0 && g.num_heads > 0 && g.model_dim > 0 && g.latent_dim > 0,
                 IRODORI_ERR_SHAPE, "dimensions must be positive");
-    IRO_REQUIRE(g.head_dim == 64, IRODORI_ERR_SHAPE, "head_dim must be 64");
+    IRO_REQUIRE(g.head_dim == 64 || g.head_dim == 128, IRODORI_ERR_SHAPE, "head_dim must be 64 or 128");
+    IRO_REQUIRE(g.compute_dtype != IRODORI_DTYPE_FP8 || g.head_dim == 64, IRODORI_ERR_SHAPE,
+                "fp8 compute needs head_dim 64");
     IRO_REQUIRE(g.num_heads * g.head_dim == g.model_dim, IRODORI_ERR_SHAPE, "num_heads * head_dim must equal model_dim");
     IRO_REQUIRE(g.model_dim % 64 == 0 && g.model_dim <= 2048, IRODORI_ERR_SHAPE,
                 "model_dim must be a multiple of 64 and <= 2048");
     IRO_REQUIRE(g.mlp_hidden > 0, IRODORI_ERR_SHAPE, "mlp_hidden must be positive");
-    IRO_REQUIRE(g.latent_dim <= 128, IRODORI_ERR_SHAPE, "latent_dim must be <= 128");
+    IRO_REQUIRE(g.latent_dim <= 256, IRODORI_ERR_SHAPE, "latent_dim (patched) must be <= 256");
     IRO_REQUIRE(g.adaln_rank > 0 && g.timestep_embed_dim > 0 && g.timestep_embed_dim % 2 == 0,
                 IRODORI_ERR_SHAPE, "adaln_rank > 0 and even timestep_embed_dim required");
     IRO_REQUIRE(g.norm_eps > 0.f && std::isfinite(g.norm_eps), IRODORI_ERR_CONFIG, "norm_eps must be > 0");
@@ -914,7 +925,7 @@ int irodori_ctx_create(int device, const irodori_dit_config* cfg, irodori_ctx** 
     IRO_TRY(dalloc(c.get(), &c->in_w, sizeof(float) * (size_t)P * D));
     IRO_TRY(dalloc(c.get(), &c->in_b, sizeof(float) * D));
     IRO_TRY(dalloc(c.get(), &c->out_norm_w, sizeof(float) * D));
-    IRO_TRY(dalloc(c.get(), &c->out_w, sizeof(float) * (size_t)D * (P <= 32 ? 32 : P <= 64 ? 64 : 128)));
+    IRO_TRY(dalloc(c.get(), &c->out_w, sizeof(float) * (size_t)D * head_width(P)));
     IRO_TRY(dalloc(c.get(), &c->out_b, sizeof(float) * P));
 
     IRO_TRY(dalloc(c.get(), &c->x, sizeof(float) * M * D));
@@ -987,7 +998,7 @@ int irodori_load_io_weights(irodori_ctx* c, const irodori_io_weights* w) {
     IRO_TRY(upload(c, c->out_norm_w, w->out_norm_w, sizeof(float) * D));
     // Output head weight with the out_norm weight folded in, rows padded to PW columns
     // (zeros past P) for the head's whole-row loads.
-    const int PW = P <= 32 ? 32 : P <= 64 ? 64 : 128;
+    const int PW = head_width(P);
     std::vector<float> wt((size_t)D * PW, 0.f);
     for (int d = 0; d < D; d++)
         for (int p = 0; p < P; p++) wt[(size_t)d * PW + p] = w->out_w[(size_t)d * P + p] * w->out_norm_w[d];
@@ -1109,7 +1120,6 @@ int irodori_load_ctx_proj_weights(irodori_ctx* c, int layer, int text_dim, int a
     IRO_REQUIRE(layer >= 0 && layer < g.num_layers, IRODORI_ERR_INVALID_ARG, "layer index out of range");
     IRO_REQUIRE(text_dim > 0 && aux_dim >= 0, IRODORI_ERR_SHAPE, "text_dim must be > 0 and aux_dim >= 0");
     IRO_REQUIRE(aux_dim == 0 || (w->wk_aux && w->wv_aux), IRODORI_ERR_INVALID_ARG, "null aux projection");
-    IRO_REQUIRE(g.head_dim == 64, IRODORI_ERR_CONFIG, "the context KV build needs head_dim 64");
     const int dims[2] = {text_dim, aux_dim};
     for (int sgm = 0; sgm < 2; sgm++)
         IRO_REQUIRE(c->ctx_dim[sgm] == 0 || c->ctx_dim[sgm] == dims[sgm], IRODORI_ERR_SHAPE,
@@ -1269,7 +1279,7 @@ int irodori_set_ctx_kv(irodori_ctx* c, int layer, int row, int t_ctx, const floa
         auto cvt = bf16_bits;
         std::vector<float> kf(nk, 0.f), vf(nv, 0.f);
         for (int j = 0; j < t_ctx; j++) {
-            int pos = c->bf16 ? vt_pos_bf16(j) : vt_pos_f32(j);
+            int pos = vt_bf16_order(c) ? vt_pos_bf16(j) : vt_pos_f32(j);
             for (int hh = 0; hh < H; hh++)
                 for (int d = 0; d < Dh; d++) {
                     size_t src = ((size_t)j * H + hh) * Dh + d;
@@ -1335,7 +1345,7 @@ int irodori_read_ctx_kv(irodori_ctx* c, int layer, int row, float* k, float* v, 
         return f;
     };
     for (int j = 0; j < c->t_ctx; j++) {
-        const int pos = c->bf16 ? vt_pos_bf16(j) : vt_pos_f32(j);
+        const int pos = vt_bf16_order(c) ? vt_pos_bf16(j) : vt_pos_f32(j);
         for (int hh = 0; hh < H; hh++)
             for (int d = 0; d < Dh; d++) {
                 const size_t dst = ((size_t)j * H + hh) * Dh + d;
@@ -1590,20 +1600,19 @@ static int sample_device_impl(irodori_ctx* c, const irodori_sampler_params* p, i
             if (c->bf16)
                 launch_scale_ctx_aux<bf16>(static_cast<const bf16*>(sk), static_cast<const bf16*>(sv),
                                            static_cast<bf16*>(c->act_k[l]), static_cast<bf16*>(c->act_v[l]), B,
-                                           rows_scaled, g.num_heads, T1, vs1, c->t_ctx, p->ctx_aux_start, factor,
-                                           c->stream);
+                                           rows_scaled, g.num_heads, g.head_dim, vt_bf16_order(c), T1, vs1,
+                                           c->t_ctx, p->ctx_aux_start, factor, c->stream);
             else
                 launch_scale_ctx_aux<float>(static_cast<const float*>(sk), static_cast<const float*>(sv),
                                             static_cast<float*>(c->act_k[l]), static_cast<float*>(c->act_v[l]), B,
-                                            rows_scaled, g.num_heads, T1, vs1, c->t_ctx, p->ctx_aux_start, factor,
-                                            c->stream);
+                                            rows_scaled, g.num_heads, g.head_dim, false, T1, vs1, c->t_ctx,
+                                            p->ctx_aux_start, factor, c->stream);
         }
         return check_launch("speaker kv scaling");
     };
     if (kvs) {
         IRO_REQUIRE(p->ctx_aux_start >= 0 && p->ctx_aux_start <= c->t_ctx, IRODORI_ERR_CONFIG,
                     "ctx_aux_start must be in [0, t_ctx]");
-        IRO_REQUIRE(g.head_dim == 64, IRODORI_ERR_CONFIG, "speaker KV scaling needs head_dim 64");
         if ((int)c->act_k.size() < L) {
             IRO_HIP_CHECK(hipStreamSynchronize(c->stream));
             const size_t kb = (size_t)g.max_rows * g.num_heads * T1 * g.head_dim * c->esz;
@@ -1722,6 +1731,7 @@ int irodori_op_joint_attention(irodori_ctx* c, int layer, int B, int S, const fl
     IRO_REQUIRE(B > 0 && B <= g.max_rows && S > 0 && S <= g.max_seq, IRODORI_ERR_SHAPE,
                 "batch must be in [1, max_rows], seq in [1, max_seq]");
     IRO_REQUIRE(!c->fp8, IRODORI_ERR_DTYPE, "the joint attention operator runs bf16 or f32 contexts");
+    IRO_REQUIRE(g.head_dim == 64, IRODORI_ERR_SHAPE, "the joint attention operator takes 64-dim heads");
     IRO_REQUIRE(c->layers[layer].loaded, IRODORI_ERR_NOT_LOADED, "block weights of the layer not loaded");
     if (c->t_ctx > 0)
         for (int r = 0; r < B; r++)

@@ -140,7 +140,7 @@ __device__ inline void rf_apply(const RfUpdateArgs& a, const RfEval& e, int step
 struct FinalArgs {
     const float* x;
     const float* norm_w;
-    const float* out_w;   // [D, PT] = out_norm.weight (.) W_out, PT = 32, 64 or 128 (the least >= P), zero past P
+    const float* out_w;   // [D, PT] = out_norm.weight (.) W_out, PT = 32, 64, 128 or 256 (the least >= P), zero past P
     const float* out_b;   // [P]
     int B, S, D, P;
     float eps;
@@ -153,12 +153,13 @@ void launch_final(const FinalArgs& a, hipStream_t st);
 
 // Speaker-KV scaling of cached context (kv_scaling.rs:10-60) on the device copies the
 // attention reads: for rows < rows_scaled, the keys [aux_start, t_ctx) of K
-// ([R, H, T1, Dh]) and V^T ([R, H, Dh, vs1], key order vt_pos_*) times factor; src == dst
-// scales in place, otherwise every other element is copied unchanged.
+// ([R, H, T1, Dh]) and V^T ([R, H, Dh, vs1], key order vt_pos_bf16 with bf16_order, else
+// vt_pos_f32) times factor; src == dst scales in place, otherwise every other element is
+// copied unchanged.  Dh a multiple of 8.
 template <typename T>
 void launch_scale_ctx_aux(const T* src_k, const T* src_v, T* dst_k, T* dst_v, int rows,
-                          int rows_scaled, int H, int T1, int vs1, int t_ctx, int aux_start,
-                          float factor, hipStream_t st);
+                          int rows_scaled, int H, int Dh, bool bf16_order, int T1, int vs1, int t_ctx,
+                          int aux_start, float factor, hipStream_t st);
 void launch_scale_copy(const float* src, float* dst, int n, float s, hipStream_t st);
 
 // ---- kernels_ops.hip -------------------------------------------------------------------

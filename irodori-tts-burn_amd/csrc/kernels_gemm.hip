@@ -213,7 +213,8 @@ __attribute__((amdgpu_waves_per_eu(WAVES_M * WAVES_N == 4 ? 2 : 1))) void gemm_k
     static_assert(LPW * 8 * NW == ROWS, "rows per slice must split over the waves");
     static_assert(FM * 32 == WM && FN * 32 == WN, "wave tiles are whole 32x32 blocks");
     static_assert(BM % 8 == 0, "a load instruction covers A rows or W rows, not both");
-    static_assert((EPI != EPI_QKVG && EPI != EPI_CTXKV) || WN == 64, "QKVG / CTXKV epilogues need one head per wave");
+    static_assert((EPI != EPI_QKVG && EPI != EPI_CTXKV) || WN == 64 || WN == 128,
+                  "QKVG / CTXKV epilogues need one 64- or 128-column head per wave");
     static_assert(EPI != EPI_SWIGLU || FN % 2 == 0, "SWIGLU epilogue needs column pairs");
     static_assert(!(F8 && CONV), "convolutions take bf16 / f32 operands");
 
@@ -412,8 +413,9 @@ __attribute__((amdgpu_waves_per_eu(WAVES_M * WAVES_N == 4 ? 2 : 1))) void gemm_k
     // by 4 with one wrap at most (rows past M read a valid table row, unused).
     // The tile needs them when any of its 64-column heads does: with D an odd multiple of 64
     // a tile can start on the last q head (no RoPE) and end on k head 0 (RoPE).
+    // (128-dim heads read their table rows from global memory in the epilogue.)
     [[maybe_unused]] bool rope_wg = false;
-    if constexpr (EPI == EPI_QKVG) {
+    if constexpr (EPI == EPI_QKVG && WN == 64) {
 #pragma unroll
         for (int c = n0; c < n0 + BN; c += 64) rope_wg = rope_wg || (c / a.D <= 1 && (c % a.D) / 64 < a.H / 2);
     }
@@ -910,26 +912,33 @@ __attribute__((amdgpu_waves_per_eu(WAVES_M * WAVES_N == 4 ? 2 : 1))) void gemm_k
             else swiglu_rows(std::false_type{});
         }
     } else if constexpr (EPI == EPI_CTXKV) {
-        // One 64-column head per wave: region 0 = K (head RMSNorm, norm.rs:60-74, no RoPE),
-        // region 1 = V (transposed scatter).  A setup-path epilogue: element stores.
-        const int Dh = 64, HD = a.H * Dh;
+        // One head (WN = 64 or 128 columns) per wave: region 0 = K (head RMSNorm,
+        // norm.rs:60-74, no RoPE), region 1 = V (transposed scatter).  A setup-path
+        // epilogue: element stores.  V^T key order: the 32x32x16 attention's (bf16 with
+        // 64-dim heads) or the 16x16 attention's (f32, and 128-dim heads).
+        constexpr int Dh = WN;
+        const int HD = a.H * Dh;
         const int col0 = n0 + wn0;
         const bool is_k = col0 < HD;
         const int h = (is_k ? col0 : col0 - HD) / Dh;
         if (is_k) {
-            const float nw0 = a.k_norm[h * Dh + cl], nw1 = a.k_norm[h * Dh + 32 + cl];
+            float nw[FN];
+#pragma unroll
+            for (int j = 0; j < FN; j++) nw[j] = a.k_norm[h * Dh + 32 * j + cl];
 #pragma unroll
             for (int i = 0; i < FM; i++)
 #pragma unroll
                 for (int e = 0; e < 16; e++) {
                     const int row = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
-                    const float y0 = acc[i][0][e], y1 = acc[i][1][e];
-                    const float ss = half_wave_sum(y0 * y0 + y1 * y1);
+                    float sq = 0.f;
+#pragma unroll
+                    for (int j = 0; j < FN; j++) sq += acc[i][j][e] * acc[i][j][e];
+                    const float ss = half_wave_sum(sq);
                     const float inv = __builtin_amdgcn_rsqf(ss * (1.f / (float)Dh) + a.eps);
                     if (row >= a.M) continue;
                     T* o = a.Ck + ((size_t)h * a.ctx_stride + a.key_off + row) * Dh;
-                    o[cl] = from_f32<T>(y0 * inv * nw0);
-                    o[32 + cl] = from_f32<T>(y1 * inv * nw1);
+#pragma unroll
+                    for (int j = 0; j < FN; j++) o[32 * j + cl] = from_f32<T>(acc[i][j][e] * inv * nw[j]);
                 }
         } else {
 #pragma unroll
@@ -939,10 +948,89 @@ __attribute__((amdgpu_waves_per_eu(WAVES_M * WAVES_N == 4 ? 2 : 1))) void gemm_k
                     const int row = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
                     if (row >= a.M) continue;
                     const int key = a.key_off + row;
-                    const int pos = sizeof(T) == 2 ? vt_pos_bf16(key) : vt_pos_f32(key);
+                    const int pos = (sizeof(T) == 2 && Dh == 64) ? vt_pos_bf16(key) : vt_pos_f32(key);
 #pragma unroll
-                    for (int j = 0; j < 2; j++)
+                    for (int j = 0; j < FN; j++)
                         a.Cv[((size_t)h * Dh + 32 * j + cl) * a.ctx_vstride + pos] = from_f32<T>(acc[i][j][e]);
+                }
+        }
+    } else if constexpr (EPI == EPI_QKVG && WN == 128) {
+        // 128-dim heads (4 x 1 waves: each wave owns 32 rows x one whole head of one region
+        // q | k | v | gate).  q / k: head RMSNorm over the 128 columns (norm.rs:60-74), half
+        // RoPE on the first H / 2 heads (rope.rs:82-135, interleaved pairs in neighbouring
+        // lanes, the (cos, sin) rows read from the table in global memory), q scaled; v:
+        // V^T scatter in the 16x16 attention's key order (vt_pos_f32, either dtype); gate:
+        // sigmoid.  Element stores: a capability path, not the 64-dim headline path.
+        constexpr int Dh = 128;
+        const int D = a.D;
+        const int col0 = n0 + wn0;
+        const int region = col0 / D;
+        const int h = (col0 % D) / Dh;
+        if (region <= 1) {
+            const bool rope = h < a.H / 2;
+            const float* nwp = (region == 0 ? a.q_norm : a.k_norm) + h * Dh;
+            const float qs = region == 0 ? a.q_scale : 1.f;
+            float nw[FN];
+#pragma unroll
+            for (int j = 0; j < FN; j++) nw[j] = nwp[32 * j + cl] * qs;
+            T* dst = region == 0 ? a.Q : a.Kd;
+            const float sgn = (cl & 1) ? -1.f : 1.f;
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const int row = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
+                    float sq = 0.f;
+#pragma unroll
+                    for (int j = 0; j < FN; j++) sq += acc[i][j][e] * acc[i][j][e];
+                    const float ss = half_wave_sum(sq);
+                    const float inv = __builtin_amdgcn_rsqf(ss * (1.f / (float)Dh) + a.eps);
+                    int b, sqi;
+                    row_bs(row < a.M ? row : a.M - 1, a.S, inv_s, b, sqi);
+                    float y[FN];
+#pragma unroll
+                    for (int j = 0; j < FN; j++) y[j] = acc[i][j][e] * inv * nw[j];
+                    if (rope) {
+                        // Pair k = 16 j + cl / 2 of token sqi: (y c - y' s, y c + y' s) for the
+                        // (even, odd) lane, y' the partner lane's value.
+                        const float2* cs = reinterpret_cast<const float2*>(a.rope_cs) + (size_t)sqi * (Dh / 2);
+#pragma unroll
+                        for (int j = 0; j < FN; j++) {
+                            const float2 t = cs[16 * j + (cl >> 1)];
+                            const float pr = IRO_DPP(y[j] * sgn, 0xB1) * t.y;
+                            y[j] = fmaf(y[j], t.x, pr);
+                        }
+                    }
+                    if (row >= a.M) continue;
+                    T* o = dst + (((size_t)b * a.H + h) * a.S + sqi) * Dh;
+#pragma unroll
+                    for (int j = 0; j < FN; j++) o[32 * j + cl] = from_f32<T>(y[j]);
+                }
+        } else if (region == 2) {
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const int row = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
+                    if (row >= a.M) continue;
+                    int b, sqi;
+                    row_bs(row, a.S, inv_s, b, sqi);
+                    const int pos = vt_pos_f32(sqi);
+#pragma unroll
+                    for (int j = 0; j < FN; j++)
+                        a.Vd[(((size_t)b * a.H + h) * Dh + 32 * j + cl) * a.vt_stride + pos] =
+                            from_f32<T>(acc[i][j][e]);
+                }
+        } else {
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const int row = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
+                    if (row >= a.M) continue;
+#pragma unroll
+                    for (int j = 0; j < FN; j++)
+                        a.G[(size_t)row * D + col0 - 3 * D + 32 * j + cl] = from_f32<T>(sigmoid_f(acc[i][j][e]));
                 }
         }
     } else if constexpr (EPI == EPI_QKVG) {
@@ -1191,10 +1279,12 @@ int launch_cfg(const GemmArgs<T>& a, hipStream_t st) {
         case EPI_RESUNIT: if (!a.W2 || !a.x || (a.U && !a.alpha2)) return -1; break;
         case EPI_QKVG:
             if (!a.Q || !a.Kd || !a.Vd || !a.G || !a.q_norm || !a.k_norm || !a.rope_cs || a.H <= 0 ||
-                a.D != a.H * 64 || a.N != 4 * a.D || a.vt_stride < a.S || a.S <= 0)
+                a.D != a.H * (BN / WAVES_N) || a.N != 4 * a.D || a.vt_stride < a.S || a.S <= 0)
                 return -1;
             break;
-        case EPI_CTXKV: if (!a.Ck || !a.Cv || !a.k_norm || a.H <= 0) return -1; break;
+        case EPI_CTXKV:
+            if (!a.Ck || !a.Cv || !a.k_norm || a.H <= 0 || a.N != 2 * a.H * (BN / WAVES_N)) return -1;
+            break;
     }
     // Fused adaLN: a consumer takes bf16 / f32 operands of the QKVG or SwiGLU projections
     // (K a multiple of 32), a producer writes the next operand after a residual update.
@@ -1285,9 +1375,12 @@ int launch_gemm(int epi, const GemmArgs<T>& a, hipStream_t st) {
                 return launch_cfg<T, 128, 192, 2, 2, 2, EPI_ADD>(a, st);
             return launch_cfg<T, 64, 64, 2, 2, 4, EPI_ADD>(a, st);
         case EPI_SWIGLU: return launch_cfg<T, 128, 128, 2, 2, 2, EPI_SWIGLU>(a, st);
-        case EPI_QKVG: return launch_cfg<T, 128, 128, 2, 2, 2, EPI_QKVG>(a, st);
+        // QKVG / CTXKV: one head per wave, 2 x 2 waves of 64 columns or 4 x 1 of 128.
+        case EPI_QKVG:
+            if (a.H > 0 && a.D == a.H * 128) return launch_cfg<T, 128, 128, 4, 1, 2, EPI_QKVG>(a, st);
+            return launch_cfg<T, 128, 128, 2, 2, 2, EPI_QKVG>(a, st);
         case EPI_CTXKV:
-            if (a.N != 2 * a.H * 64) return -1;
+            if (a.H > 0 && a.N == 2 * a.H * 128) return launch_cfg<T, 128, 128, 4, 1, 2, EPI_CTXKV>(a, st);
             return launch_cfg<T, 128, 128, 2, 2, 2, EPI_CTXKV>(a, st);
     }
     return -1;

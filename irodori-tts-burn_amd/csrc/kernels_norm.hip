@@ -299,7 +299,7 @@ __global__ __launch_bounds__(256) void final_kernel(FinalArgs a) {
     constexpr int KL = 256 / QN;  // k positions per pass of the block
     constexpr int R = NR * FR;    // staged row slot f * NR + i
     // W' quads in flight per thread (offsets below 4 KB; all of them for D = 1024, PT = 32)
-    constexpr int KB = PT == 32 ? 32 : (PT == 64 ? 16 : 8);
+    constexpr int KB = PT == 32 ? 32 : (PT == 64 ? 16 : (PT == 128 ? 8 : 4));
     static_assert(FR * PT <= 256, "one update element per thread");
     extern __shared__ __attribute__((aligned(16))) float fsm[];
     const int D = a.D, P = a.P;
@@ -581,21 +581,27 @@ template <int PT>
 static void launch_final_pt(const FinalArgs& a, hipStream_t st) {
     const int nr = a.rf.plan ? a.nrole : 2;
     const int ngroups = a.rf.plan ? a.B : (a.B + nr - 1) / nr;
-    // One update element per thread: PT = 128 takes at most two frames per block.
+    // One update element per thread: PT = 128 takes at most two frames per block, 256 one.
     if constexpr (PT * 4 <= 256) {
         if ((long)((a.S + 3) / 4) * ngroups >= 256) {
             launch_final_fr<PT, 4>(a, st);
             return;
         }
     }
-    if ((long)((a.S + 1) / 2) * ngroups >= 256) launch_final_fr<PT, 2>(a, st);
-    else launch_final_fr<PT, 1>(a, st);
+    if constexpr (PT * 2 <= 256) {
+        if ((long)((a.S + 1) / 2) * ngroups >= 256) {
+            launch_final_fr<PT, 2>(a, st);
+            return;
+        }
+    }
+    launch_final_fr<PT, 1>(a, st);
 }
 
 void launch_final(const FinalArgs& a, hipStream_t st) {
     if (a.P <= 32) launch_final_pt<32>(a, st);
     else if (a.P <= 64) launch_final_pt<64>(a, st);
-    else launch_final_pt<128>(a, st);
+    else if (a.P <= 128) launch_final_pt<128>(a, st);
+    else launch_final_pt<256>(a, st);
 }
 
 

@@ -97,11 +97,11 @@ def test_op_shape_and_dtype_errors_before_any_device_call():
 
 
 @pytest.mark.parametrize("field,value,code", [
-    ("head_dim", 128, L.ERR_SHAPE),
+    ("head_dim", 96, L.ERR_SHAPE),
     ("mlp_hidden", 0, L.ERR_SHAPE),
     ("compute_dtype", 9, L.ERR_DTYPE),
     ("norm_eps", 0.0, L.ERR_CONFIG),
-    ("latent_dim", 129, L.ERR_SHAPE),
+    ("latent_dim", 257, L.ERR_SHAPE),
     ("max_rows", 65536, L.ERR_SHAPE),
 ])
 def test_ctx_create_config_errors(field, value, code):

@@ -46,6 +46,10 @@ SMALL = {
     # a 120-channel latent: the output head's 128-wide W' rows (8 zero columns), in_proj over
     # two 64-channel chunks
     "tiny_p120": (lambda: dataclasses.replace(ih.cfg_tiny(), latent_dim=120), 40, 20, 13, 0.05, 0.1),
+    # patched latents wider than 128 (latent_patch_size > 1: model.rs:231-233): the output
+    # head's 256-wide W' rows, one frame per block; 200 channels leave 56 zero columns
+    "tiny_p200": (lambda: dataclasses.replace(ih.cfg_tiny(), latent_dim=200), 40, 20, 13, 0.05, 0.1),
+    "tiny_p256": (lambda: dataclasses.replace(ih.cfg_tiny(), latent_dim=256), 37, 20, 13, 0.05, 0.1),
     # the published 500M-v2 width (d 1280, 20 x 64 heads, SwiGLU 3680 padded to 3712 on the
     # device, norms unfused) with two of its twelve layers; 4 text + 9 speaker keys as the
     # A6000 benchmark's request (text_len 4, 8 reference frames + the mean token)
@@ -113,10 +117,12 @@ def test_sample_joint_cfg_cfg1(oracle64, backend):
 
 
 @pytest.mark.parametrize("backend", [F32, BF16], ids=["f32", "bf16"])
-def test_sample_joint_cfg_wide_latent(oracle64, backend):
+@pytest.mark.parametrize("P", [120, 256])
+def test_sample_joint_cfg_wide_latent(oracle64, backend, P):
     # A 120-channel latent through the sampler: the fused head + update with 128-wide W'
-    # rows and two frames per block, 4 Euler steps of Joint CFG against the oracle.
-    cfg = dataclasses.replace(ih.cfg_tiny(), latent_dim=120)
+    # rows and two frames per block; a 256-channel one with 256-wide rows and one frame per
+    # block.  4 Euler steps of Joint CFG against the oracle.
+    cfg = dataclasses.replace(ih.cfg_tiny(), latent_dim=P)
     w = ih.DitWeights.random(cfg, 0, std=0.05)
     ctx = ih.make_context_kv(cfg, 1, 20, 13, seed=1)
     x0 = ih.make_noise(1, 40, cfg.latent_dim, 2)
@@ -125,7 +131,7 @@ def test_sample_joint_cfg_wide_latent(oracle64, backend):
         got = e.sample(x0, p)
     c, u = ctx.rows([0]), ctx.rows([1])
     ref, _ = oracle64.sample_joint_cfg(cfg, w, x0, (c.k, c.v, c.mask), (u.k, u.v, u.mask), 4, 3.0)
-    print(backend.value, "latent 120: final rel L2 %.2e" % rel_l2(got, ref))
+    print(backend.value, "latent %d: final rel L2 %.2e" % (P, rel_l2(got, ref)))
     assert rel_l2(got, ref) < TOL_FINAL[backend]
 
 
