@@ -875,8 +875,8 @@ int irodori_ctx_create(int device, const irodori_dit_config* cfg, irodori_ctx** 
     c->bf16 = g.compute_dtype == IRODORI_DTYPE_BF16 || c->fp8;
     c->esz = c->bf16 ? 2 : 4;
     c->w_tiled = !c->fp8 || (g.model_dim % 128 == 0 && (g.num_heads * g.head_dim) % 128 == 0);
-    // The fused adaLN's GEMMs take the row partial sums as up to 8 float4 per row.
-    c->fused = c->bf16 && !c->fp8 && g.model_dim % 128 == 0 && g.model_dim <= 1024;
+    // The fused adaLN's GEMMs take the row partial sums as up to 16 float4 per row.
+    c->fused = c->bf16 && !c->fp8 && g.model_dim % 128 == 0 && g.model_dim <= 2048;
     IRO_HIP_CHECK(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
     IRO_HIP_CHECK(hipEventCreateWithFlags(&c->ev_fork, hipEventDisableTiming));
     for (int i = 0; i < irodori_ctx::kMaxRoles - 1; i++) {

@@ -379,7 +379,7 @@ __attribute__((amdgpu_waves_per_eu(WAVES_M * WAVES_N == 4 ? 2 : 1))) void gemm_k
     // x^2 + eps), kept in registers until the stage buffers are free after the main loop.
     constexpr bool FUSE_IN = !F8 && (EPI == EPI_QKVG || EPI == EPI_SWIGLU);
     constexpr int RPL = (WM + 63) / 64;  // rows of the wave per lane
-    [[maybe_unused]] float4 rsv[RPL][8];
+    [[maybe_unused]] float4 rsv[RPL][16];
     [[maybe_unused]] float rown[RPL];
     [[maybe_unused]] float bc[FN];
     if constexpr (FUSE_IN) {
@@ -394,11 +394,11 @@ __attribute__((amdgpu_waves_per_eu(WAVES_M * WAVES_N == 4 ? 2 : 1))) void gemm_k
             for (int p = 0; p < RPL; p++) {
                 const int rl = 64 * p + lane, row = m0 + wm0 + rl;
 #pragma unroll
-                for (int q = 0; q < 8; q++) rsv[p][q] = make_float4(0.f, 0.f, 0.f, 0.f);
+                for (int q = 0; q < 16; q++) rsv[p][q] = make_float4(0.f, 0.f, 0.f, 0.f);
                 if (rl < WM && row < a.M) {
                     const float4* pp = reinterpret_cast<const float4*>(a.rstat + (size_t)row * (K / 32));
 #pragma unroll
-                    for (int q = 0; q < 8; q++)
+                    for (int q = 0; q < 16; q++)
                         if (q < nq) rsv[p][q] = pp[q];
                 }
             }
@@ -457,7 +457,7 @@ __attribute__((amdgpu_waves_per_eu(WAVES_M * WAVES_N == 4 ? 2 : 1))) void gemm_k
                 for (int p = 0; p < RPL; p++) {
                     float ss = 0.f;
 #pragma unroll
-                    for (int q = 0; q < 8; q++) {
+                    for (int q = 0; q < 16; q++) {
                         ss += rsv[p][q].x;
                         ss += rsv[p][q].y;
                         ss += rsv[p][q].z;
@@ -1288,9 +1288,9 @@ int launch_cfg(const GemmArgs<T>& a, hipStream_t st) {
     }
     // Fused adaLN: a consumer takes bf16 / f32 operands of the QKVG or SwiGLU projections
     // (K a multiple of 32), a producer writes the next operand after a residual update.
-    // The consumer loads each row's K / 32 partials as at most 8 float4 (K % 128 == 0, K <= 1024),
+    // The consumer loads each row's K / 32 partials as at most 16 float4 (K % 128 == 0, K <= 2048),
     // and every row of the launch shares one modulation vector (the batch rows all map to it).
-    if (a.rstat && (F8 || (EPI != EPI_QKVG && EPI != EPI_SWIGLU) || !a.rbias || a.K % 128 || a.K > 1024 ||
+    if (a.rstat && (F8 || (EPI != EPI_QKVG && EPI != EPI_SWIGLU) || !a.rbias || a.K % 128 || a.K > 2048 ||
                     a.S <= 0 || !a.mt.tab || a.mt.rows_per_vec < (a.M + a.S - 1) / a.S))
         return -1;
     if (a.Hn && (F8 || EPI != EPI_RESID || !a.rstat_out || a.N % 32 || a.next_layer < 0 ||
