@@ -297,6 +297,16 @@ typedef struct irodori_kernel_times {
 int irodori_profile_layer(irodori_ctx* ctx, int batch, int seq, int iters,
                           irodori_kernel_times* out);
 
+/* Replaces the reference's NVTX ranges (src/profiling.rs:29-92, compiled in by its `profile`
+ * feature; used at src/model/dit/model.rs:238-392, src/model/diffusion.rs:88-158,
+ * src/rf/euler_sampler.rs:409-580): the library marks the same spans with roctx ranges of the
+ * same names (dit_forward_with_cond_fused, timestep_embed, cond_module, in_proj, dit_block_<i>,
+ * adaln_attn, joint_attention_fused, adaln_mlp, swiglu_mlp_fused, out_proj,
+ * forward_batched_cfg, forward_cond, forward_uncond, heun_corrector) for rocprofv3
+ * --marker-trace when the process runs with IRODORI_ROCTX=1 (read once, at the first range;
+ * the roctx library is then loaded at run time).  Returns 1 when ranges are on, else 0. */
+int irodori_roctx_enabled(void);
+
 /* ---- condition encoders ---------------------------------------------------------------
  * TextEncoder (text / caption, text_encoder.rs:64-148) and ReferenceLatentEncoder (speaker,
  * speaker_encoder.rs:85-162) with their conditioner norm (text_norm, dit/model.rs:189-190;

@@ -26,6 +26,7 @@
 #include "../../include/irodori_hip.h"
 #include "common.hpp"
 #include "kernels.hpp"
+#include "roctx.hpp"
 #include "host.hpp"
 
 namespace irodori {
@@ -332,7 +333,11 @@ int enqueue_mod_table(irodori_ctx* c, int nvec, bool skip_mlp, int l0 = 0, int l
     int D = g.model_dim, L = g.num_layers, r = g.adaln_rank;
     if (l1 < 0) l1 = L;
     if (!skip_mlp) {
-        launch_timestep_embedding(c->tvec, nvec, g.timestep_embed_dim, c->emb, c->stream);
+        RoctxRange r("cond_module");  // timestep embedding + conditioning MLP (dit/model.rs:298-302)
+        {
+            RoctxRange te("timestep_embed");
+            launch_timestep_embedding(c->tvec, nvec, g.timestep_embed_dim, c->emb, c->stream);
+        }
         for (int j = 0; j < 3; j++)
             launch_vec_linear(c->d_jobs_mlp + j, 1, nvec, j == 2 ? 3 * D : D, c->stream);
     }
@@ -598,7 +603,25 @@ int enqueue_part(irodori_ctx* c, int l, int B, int S, const ModTable& mt, int pa
 // One DiT block over batch rows [r0, r0 + B) on stream st (see enqueue_part).
 template <typename T>
 int enqueue_layer(irodori_ctx* c, int l, int B, int S, const ModTable& mt, int r0, hipStream_t st) {
-    for (int p = 0; p < PART_COUNT; p++) IRO_TRY(enqueue_part<T>(c, l, B, S, mt, p, r0, st));
+    char name[32];
+    snprintf(name, sizeof(name), "dit_block_%d", l);
+    RoctxRange block(name);  // the reference's per-block and per-half ranges (diffusion.rs:88-104)
+    {
+        RoctxRange r("joint_attention_fused");
+        for (int p : {PART_QKVG, PART_ATTN, PART_WO}) IRO_TRY(enqueue_part<T>(c, l, B, S, mt, p, r0, st));
+    }
+    {
+        RoctxRange r("adaln_mlp");
+        IRO_TRY(enqueue_part<T>(c, l, B, S, mt, PART_NORM_MLP, r0, st));
+    }
+    {
+        RoctxRange r("swiglu_mlp_fused");
+        for (int p : {PART_W13, PART_W2}) IRO_TRY(enqueue_part<T>(c, l, B, S, mt, p, r0, st));
+    }
+    {
+        RoctxRange r("adaln_attn");  // the next block's attention adaLN, from this block's output
+        IRO_TRY(enqueue_part<T>(c, l, B, S, mt, PART_NORM_NEXT, r0, st));
+    }
     return check_launch("layer");
 }
 
@@ -1409,9 +1432,13 @@ static int forward_impl(irodori_ctx* c, int B, int S, const float* x_t, const fl
     IRO_TRY(ensure_nvec(c, B));
     IRO_TRY(upload(c, c->tvec, t, sizeof(float) * B));
     IRO_TRY(upload(c, c->xt, x_t, sizeof(float) * (size_t)B * S * P));
+    RoctxRange fwd("dit_forward_with_cond_fused");
     IRO_TRY(enqueue_mod_table(c, B, false));
     ModTable mt{c->tab, c->zero_step, 0, 1, L};
-    IRO_TRY(enqueue_inproj(c, B, S, c->xt, B, 0, mt, c->stream));
+    {
+        RoctxRange r("in_proj");
+        IRO_TRY(enqueue_inproj(c, B, S, c->xt, B, 0, mt, c->stream));
+    }
     size_t n = (size_t)B * S * D;
     if (debug) IRO_HIP_CHECK(hipMemcpyAsync(debug, c->x, sizeof(float) * n, hipMemcpyDeviceToHost, c->stream));
     for (int l = 0; l < L; l++) {
@@ -1420,7 +1447,10 @@ static int forward_impl(irodori_ctx* c, int B, int S, const float* x_t, const fl
             IRO_HIP_CHECK(hipMemcpyAsync(debug + (size_t)(l + 1) * n, c->x, sizeof(float) * n, hipMemcpyDeviceToHost,
                                          c->stream));
     }
-    IRO_TRY(enqueue_head(c, B, S, 0, c->stream));
+    {
+        RoctxRange r("out_proj");  // out_norm folded into the head's weights (dit/model.rs:391-392)
+        IRO_TRY(enqueue_head(c, B, S, 0, c->stream));
+    }
     IRO_HIP_CHECK(hipMemcpyAsync(v_out, c->vout, sizeof(float) * (size_t)B * S * P, hipMemcpyDeviceToHost, c->stream));
     IRO_HIP_CHECK(hipStreamSynchronize(c->stream));
     return IRODORI_OK;
@@ -1669,12 +1699,21 @@ static int sample_device_impl(irodori_ctx* c, const irodori_sampler_params* p, i
         *out = exec;
         return IRODORI_OK;
     };
+    // One range per evaluation, named as the reference's (euler_sampler.rs:409-515, :580):
+    // several roles batched, the conditioned role alone, or one dropped-signal role alone.
+    auto eval_name = [](int roles) {
+        return (roles & (roles - 1)) ? "forward_batched_cfg" : roles == 1 ? "forward_cond" : "forward_uncond";
+    };
     for (int i = 0; i < N; i++) {
         hipGraphExec_t ex = nullptr;
-        IRO_TRY(graph_for(roles_of[2 * i], 0, &ex));
-        IRO_HIP_CHECK(hipGraphLaunch(ex, c->stream));
+        {
+            RoctxRange r(eval_name(roles_of[2 * i]));
+            IRO_TRY(graph_for(roles_of[2 * i], 0, &ex));
+            IRO_HIP_CHECK(hipGraphLaunch(ex, c->stream));
+        }
         if (i == revert_step && kvs) IRO_TRY(scale_kv(false, 1.0f / p->speaker_kv_scale));
         if (heun) {
+            RoctxRange r("heun_corrector");
             IRO_TRY(graph_for(roles_of[2 * i + 1], 1, &ex));
             IRO_HIP_CHECK(hipGraphLaunch(ex, c->stream));
         }

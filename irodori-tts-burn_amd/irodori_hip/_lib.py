@@ -128,6 +128,7 @@ _vp = C.c_void_p
 SIGNATURES = {
     "irodori_last_error": (C.c_char_p, []),
     "irodori_version": (C.c_char_p, []),
+    "irodori_roctx_enabled": (C.c_int, []),
     "irodori_sampler_params_validate": (C.c_int, [C.POINTER(SamplerParamsC)]),
     "irodori_ctx_create": (C.c_int, [C.c_int, C.POINTER(DitConfigC), C.POINTER(_vp)]),
     "irodori_ctx_destroy": (C.c_int, [_vp]),

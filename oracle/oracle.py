@@ -112,11 +112,16 @@ _lib = None
 
 
 def _load():
+    """The oracle library; IRODORI_ORACLE_LIB names another build of the same source (the
+    sanitizer build of tests/sanitize/)."""
     global _lib
     if _lib is None:
-        if not os.path.exists(_LIB_PATH):
-            build()
-        _lib = C.CDLL(_LIB_PATH)
+        path = os.environ.get("IRODORI_ORACLE_LIB")
+        if not path:
+            path = _LIB_PATH
+            if not os.path.exists(path):
+                build()
+        _lib = C.CDLL(path)
     return _lib
 
 

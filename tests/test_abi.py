@@ -166,3 +166,21 @@ def test_t_schedule_endpoints_and_uniformity():
     assert len(s) == 41 and abs(s[0] - 0.999) < 1e-7 and s[-1] == 0.0
     d = np.diff(np.asarray(s, np.float64))
     assert np.allclose(d, -0.999 / 40, atol=1e-6)
+
+
+@pytest.mark.parametrize("env,expect", [(None, 0), ("0", 0), ("1", 1)])
+def test_roctx_ranges_are_opt_in(env, expect):
+    # The NVTX-named roctx ranges load the roctx library only with IRODORI_ROCTX=1 (read at
+    # the first range); a fresh process per setting, since the choice is made once.
+    import os
+    import subprocess
+    import sys
+    code = ("import sys; sys.path.insert(0, %r); from irodori_hip import _lib as L; "
+            "print(L.load().irodori_roctx_enabled())" % os.path.join(os.path.dirname(L.__file__), ".."))
+    e = dict(os.environ)
+    e.pop("IRODORI_ROCTX", None)
+    if env is not None:
+        e["IRODORI_ROCTX"] = env
+    out = subprocess.run([sys.executable, "-c", code], env=e, capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0, out.stderr
+    assert out.stdout.strip().splitlines()[-1] == str(expect)

@@ -126,3 +126,36 @@ def test_encoder_errors_are_reported():
         with pytest.raises(ih.IrodoriError) as ei:
             enc.forward(mask, ids=np.full((1, 8), ecfg.vocab_size, np.int32))
         assert ei.value.kind == "InvalidArg"
+
+
+def test_two_threads_match_sequential_runs():
+    # Two host threads, each with its own encoder (the first launches of every kernel
+    # variant, whose one-time LDS limit is guarded by a once flag, race between them), give
+    # the bits of the same encoders run one after the other.
+    import threading
+    jobs = []
+    for i, (make, valid, S) in enumerate([(ih.enc_text_tiny, [20, 13], 20), (ih.enc_speaker_tiny, [37, 30], 37)]):
+        ecfg = make()
+        ew = ih.EncoderWeights.random(ecfg, 10 + i, std=0.05, norm_jitter=0.1)
+        inp, mask = inputs(ecfg, valid, S, 20 + i)
+        jobs.append((ecfg, ew, mask, inp))
+    for backend in (BF16, F32):
+        out = [None, None]
+        errs = []
+
+        def work(k):
+            try:
+                ecfg, ew, mask, inp = jobs[k]
+                out[k] = run(ecfg, ew, backend, mask, **inp)
+            except Exception as exc:  # reported below, on the main thread
+                errs.append(exc)
+
+        ths = [threading.Thread(target=work, args=(k,)) for k in range(2)]
+        for th in ths:
+            th.start()
+        for th in ths:
+            th.join()
+        assert not errs, errs
+        for k, (ecfg, ew, mask, inp) in enumerate(jobs):
+            seq, seq_mask = run(ecfg, ew, backend, mask, **inp)
+            assert np.array_equal(out[k][0], seq) and np.array_equal(out[k][1], seq_mask)
