@@ -286,7 +286,7 @@ def read_traffic(path=TRAFFIC_FILE, key="traffic_bytes_per_launch:"):
     try:
         for line in open(path):
             if line.startswith(key):
-                return int(line.split(":")[1])
+                return int(line.split(":", 1)[1].split()[0])
     except OSError:
         pass
     return None
