@@ -37,6 +37,12 @@ typedef struct orc_cfg {
     float rope_theta;
     int32_t gemm_fp8;     /* 1: the block GEMMs take fp8 operands (orc_mx_quantize_rows /
                              orc_quant_weight_cols), the HIP path's fp8 compute mode */
+    int32_t fused_adaln;  /* 1: every row of a block shares one modulation vector and the
+                             adaLN is folded into the GEMMs that read h, as the HIP path's
+                             bf16 sampler chains compute it: h W = r (x (1 + scale)) W +
+                             shift W with r = rsqrt(mean x^2 + eps) per row (with gemm_fp8
+                             the GEMM inputs x (1 + scale) and the shift row would each be
+                             quantized; the HIP fp8 mode keeps the unfolded adaLN) */
 } orc_cfg;
 
 /* One DiffusionBlock (src/model/diffusion.rs:21-28), fused inference layout

@@ -27,7 +27,7 @@ class OrcCfg(C.Structure):
         ("latent_dim", C.c_int32), ("model_dim", C.c_int32), ("num_layers", C.c_int32),
         ("num_heads", C.c_int32), ("head_dim", C.c_int32), ("mlp_hidden", C.c_int32),
         ("adaln_rank", C.c_int32), ("t_dim", C.c_int32), ("norm_eps", C.c_float),
-        ("rope_theta", C.c_float), ("gemm_fp8", C.c_int32),
+        ("rope_theta", C.c_float), ("gemm_fp8", C.c_int32), ("fused_adaln", C.c_int32),
     ]
 
 
@@ -207,22 +207,27 @@ def quant_weight_cols(w):
 
 class Oracle:
     """Oracle entry points; arrays are numpy float32 (masks uint8), shapes as in oracle.h.
-    gemm_fp8: the block GEMMs take fp8 operands (the HIP path's fp8 compute mode)."""
+    gemm_fp8: the block GEMMs take fp8 operands (the HIP path's fp8 compute mode).
+    fused_adaln: the samplers' forwards fold the adaLN into the GEMMs that read its output,
+    the algebra of the HIP path's bf16 sampler chains (orc_cfg.fused_adaln).  Every row of a
+    sampler evaluation shares one modulation vector; the plain forward and block entry
+    points, whose rows may carry different t, keep the unfolded adaLN unless asked."""
 
-    def __init__(self, precision: str = "f32", gemm_fp8: bool = False):
+    def __init__(self, precision: str = "f32", gemm_fp8: bool = False, fused_adaln: bool = False):
         assert precision in ("f32", "f64")
         self.lib = _load()
         self.p = "orc_%s_" % precision
         self.fp8 = bool(gemm_fp8)
+        self.fused = bool(fused_adaln)
 
     def _fn(self, name):
         return getattr(self.lib, self.p + name)
 
     # ---- structs -------------------------------------------------------------------
-    def cfg_struct(self, cfg) -> OrcCfg:
+    def cfg_struct(self, cfg, sampler: bool = False) -> OrcCfg:
         return OrcCfg(cfg.latent_dim, cfg.model_dim, cfg.num_layers, cfg.num_heads,
                       cfg.head_dim, cfg.mlp_hidden, cfg.adaln_rank, cfg.timestep_embed_dim,
-                      cfg.norm_eps, cfg.rope_theta, int(self.fp8))
+                      cfg.norm_eps, cfg.rope_theta, int(self.fp8), int(sampler and self.fused))
 
     @staticmethod
     def block_struct(b) -> OrcBlock:
@@ -489,17 +494,20 @@ class Oracle:
         return x
 
     # ---- model ---------------------------------------------------------------------
-    def forward(self, cfg, weights, x_t, t, ctx_k, ctx_v, ctx_mask, debug=False, latent_mask=None):
+    def forward(self, cfg, weights, x_t, t, ctx_k, ctx_v, ctx_mask, debug=False, latent_mask=None,
+                folded=False):
         """x_t [B,S,P]; t [B]; ctx_k/ctx_v [L,B,T,H,Dh]; ctx_mask [B,T] -> v [B,S,P]
         (and [L+1,B,S,D] block outputs when debug).  latent_mask [B,S] (nonzero = key
-        attends) masks latent keys (attention.rs:730-750)."""
+        attends) masks latent keys (attention.rs:730-750).  folded: the adaLN folded into
+        the GEMMs as in the samplers (with this oracle's fused_adaln), for a forward whose
+        rows share one t."""
         x_t = _c32(x_t)
         B, S, Pd = x_t.shape
         T = ctx_k.shape[2]
         blocks = (OrcBlock * cfg.num_layers)(*[self.block_struct(b) for b in weights.blocks])
         v = np.empty_like(x_t)
         dbg = np.empty((cfg.num_layers + 1, B, S, cfg.model_dim), np.float32) if debug else None
-        self._fn("forward")(C.byref(self.cfg_struct(cfg)), C.byref(self.io_struct(weights.io)),
+        self._fn("forward")(C.byref(self.cfg_struct(cfg, sampler=folded)), C.byref(self.io_struct(weights.io)),
                             blocks, B, S, _f(x_t), _f(_c32(t)), T, _f(_c32(ctx_k)),
                             _f(_c32(ctx_v)), _u8(np.ascontiguousarray(ctx_mask, np.uint8)),
                             _lat(latent_mask), _f(v), _f(dbg) if debug else None)
@@ -516,7 +524,7 @@ class Oracle:
         blocks = (OrcBlock * cfg.num_layers)(*[self.block_struct(b) for b in weights.blocks])
         out = np.empty_like(x0)
         run = self._fn("sample_rf")(
-            C.byref(self.cfg_struct(cfg)), C.byref(self.io_struct(weights.io)), blocks, U, S,
+            C.byref(self.cfg_struct(cfg, sampler=True)), C.byref(self.io_struct(weights.io)), blocks, U, S,
             _f(x0), T, _f(_c32(k)), _f(_c32(v)), _u8(np.ascontiguousarray(m, np.uint8)),
             _lat(latent_mask), C.byref(sampler), max_steps_run, _f(out))
         return out, int(run)
@@ -533,7 +541,7 @@ class Oracle:
         blocks = (OrcBlock * cfg.num_layers)(*[self.block_struct(b) for b in weights.blocks])
         out = np.empty_like(x0)
         run = self._fn("sample_joint_cfg")(
-            C.byref(self.cfg_struct(cfg)), C.byref(self.io_struct(weights.io)), blocks, U, S,
+            C.byref(self.cfg_struct(cfg, sampler=True)), C.byref(self.io_struct(weights.io)), blocks, U, S,
             _f(x0), T, _f(_c32(kc)), _f(_c32(vc)), _u8(np.ascontiguousarray(mc, np.uint8)),
             _f(_c32(ku)), _f(_c32(vu)), _u8(np.ascontiguousarray(mu, np.uint8)),
             _lat(latent_mask), num_steps,

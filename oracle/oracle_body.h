@@ -251,6 +251,51 @@ static void P(glinear)(const orc_cfg* c, const float* x, const float* w, int M, 
     free(qx); free(sx); free(qw); free(xd); free(wd); free(sw);
 }
 
+/* The input of a GEMM that reads an adaLN output h = x r (1 + scale) + shift (norm.rs:160-169):
+ * h itself, or (c->fused_adaln) its parts: xs = x (1 + scale) [M, K], r [M] and the shift rows
+ * [B, K] of the B batch rows of S tokens each. */
+typedef struct P(adaln_in) {
+    const float* h;
+    const float* xs;
+    const float* r;
+    const float* shift;
+    int B, S;
+} P(adaln_in);
+
+/* y = h @ w, or for the folded form y = r (xs @ w) + shift_b @ w — each product a block GEMM
+ * (glinear: in fp8 mode xs and the shift rows are quantized as GEMM inputs). */
+static void P(glinear_in)(const orc_cfg* c, const P(adaln_in)* in, const float* w, int M, int K, int N,
+                          float* y) {
+    if (!in->xs) {
+        P(glinear)(c, in->h, w, M, K, N, y);
+        return;
+    }
+    float* ys = (float*)malloc(sizeof(float) * (size_t)in->B * N);
+    P(glinear)(c, in->xs, w, M, K, N, y);
+    P(glinear)(c, in->shift, w, in->B, K, N, ys);
+    for (int i = 0; i < M; i++) {
+        const float* sb = ys + (size_t)(i / in->S) * N;
+        for (int n = 0; n < N; n++)
+            y[(size_t)i * N + n] = (float)((R)y[(size_t)i * N + n] * (R)in->r[i] + (R)sb[n]);
+    }
+    free(ys);
+}
+
+/* The folded adaLN's parts of x [B, S, D] for one modulation (norm.rs:160-169):
+ * xs = x (1 + scale[b]), r = 1 / sqrt(mean(x^2) + eps) per row. */
+static void P(adaln_parts)(const float* x, const float* scale, int B, int S, int D, float eps, float* xs,
+                           float* r) {
+    #pragma omp parallel for schedule(static)
+    for (int i = 0; i < B * S; i++) {
+        const int b = i / S;
+        const float* xr = x + (size_t)i * D;
+        R ss = 0;
+        for (int d = 0; d < D; d++) ss += (R)xr[d] * (R)xr[d];
+        r[i] = (float)(R_C(1.0) / SQRT(ss / (R)D + (R)eps));
+        for (int d = 0; d < D; d++) xs[(size_t)i * D + d] = (float)((R)xr[d] * (R_C(1.0) + (R)scale[(size_t)b * D + d]));
+    }
+}
+
 void P(gemm_fp8)(const float* x, const float* w, int M, int K, int N, float* y) {
     orc_cfg c;
     memset(&c, 0, sizeof c);
@@ -260,11 +305,11 @@ void P(gemm_fp8)(const float* x, const float* w, int M, int K, int N, float* y) 
 
 /* feed_forward.rs:76-85 (SwiGlu::forward_fused): u = h @ [W1|W3];
  * out = (silu(u[:, :F]) * u[:, F:]) @ W2. */
-static void P(swiglu_c)(const orc_cfg* c, const float* h, const float* w13, const float* w2, int M, int D,
+static void P(swiglu_c)(const orc_cfg* c, const P(adaln_in)* in, const float* w13, const float* w2, int M, int D,
                         int F, float* out) {
     float* u = (float*)malloc(sizeof(float) * (size_t)M * 2 * F);
     float* m = (float*)malloc(sizeof(float) * (size_t)M * F);
-    P(glinear)(c, h, w13, M, D, 2 * F, u);
+    P(glinear_in)(c, in, w13, M, D, 2 * F, u);
     #pragma omp parallel for schedule(static)
     for (int i = 0; i < M; i++)
         for (int j = 0; j < F; j++)
@@ -276,7 +321,8 @@ static void P(swiglu_c)(const orc_cfg* c, const float* h, const float* w13, cons
 
 void P(swiglu)(const float* h, const float* w13, const float* w2, int M, int D, int F,
                float* out) {
-    P(swiglu_c)(NULL, h, w13, w2, M, D, F, out);
+    P(adaln_in) in = {h, NULL, NULL, NULL, 0, 0};
+    P(swiglu_c)(NULL, &in, w13, w2, M, D, F, out);
 }
 
 /* attention.rs:272-425 (JointAttention::forward_fused with a KV cache):
@@ -285,9 +331,20 @@ void P(swiglu)(const float* h, const float* w13, const float* w2, int M, int D, 
  *   ones when absent (build_joint_mask, attention.rs:730-750);
  *   o = SDPA(q, K, V, mask, Dh^-0.5); out = (sigmoid(h @ W_gate) * o) @ W_o.
  * ctx_k/ctx_v: [B, T, H, Dh] (already k-normed, not rotated); ctx_mask: [B, T] (1 = attend). */
+static void P(joint_attention_in)(const orc_cfg* c, const orc_block* blk, const P(adaln_in)* in, int B,
+                                  int S, int T, const float* ctx_k, const float* ctx_v,
+                                  const uint8_t* ctx_mask, const uint8_t* lat_mask, const float* cos_t,
+                                  const float* sin_t, float* out);
 void P(joint_attention)(const orc_cfg* c, const orc_block* blk, const float* h, int B, int S,
                         int T, const float* ctx_k, const float* ctx_v, const uint8_t* ctx_mask,
                         const uint8_t* lat_mask, const float* cos_t, const float* sin_t, float* out) {
+    P(adaln_in) in = {h, NULL, NULL, NULL, B, S};
+    P(joint_attention_in)(c, blk, &in, B, S, T, ctx_k, ctx_v, ctx_mask, lat_mask, cos_t, sin_t, out);
+}
+static void P(joint_attention_in)(const orc_cfg* c, const orc_block* blk, const P(adaln_in)* in, int B,
+                                  int S, int T, const float* ctx_k, const float* ctx_v,
+                                  const uint8_t* ctx_mask, const uint8_t* lat_mask, const float* cos_t,
+                                  const float* sin_t, float* out) {
     int D = c->model_dim, H = c->num_heads, Dh = c->head_dim, HD = H * Dh;
     int M = B * S, Skv = S + T;
     size_t szq = (size_t)M * HD;
@@ -296,7 +353,7 @@ void P(joint_attention)(const orc_cfg* c, const orc_block* blk, const float* h, 
     float* kk = (float*)malloc(sizeof(float) * szq);
     float* vv = (float*)malloc(sizeof(float) * szq);
     float* tmp = (float*)malloc(sizeof(float) * szq);
-    P(glinear)(c, h, blk->w_qkv, M, D, 3 * HD, qkv);
+    P(glinear_in)(c, in, blk->w_qkv, M, D, 3 * HD, qkv);
     for (int i = 0; i < M; i++)
         for (int j = 0; j < HD; j++) {
             q[(size_t)i * HD + j] = qkv[(size_t)i * 3 * HD + j];
@@ -338,7 +395,7 @@ void P(joint_attention)(const orc_cfg* c, const orc_block* blk, const float* h, 
     P(sdpa)(qh, kh, vh, mk, B, H, S, Skv, Dh, (float)(R_C(1.0) / SQRT((R)Dh)), oh);
 
     /* gated = sigmoid(h @ W_gate) * o  (o back to [B, S, H*Dh]); out = gated @ W_o. */
-    P(glinear)(c, h, blk->w_gate, M, D, D, tmp);
+    P(glinear_in)(c, in, blk->w_gate, M, D, D, tmp);
     for (int b = 0; b < B; b++)
         for (int s = 0; s < S; s++)
             for (int hh = 0; hh < H; hh++)
@@ -368,21 +425,26 @@ void P(block_forward)(const orc_cfg* c, const orc_block* blk, float* x, const fl
     float* h = (float*)malloc(sizeof(float) * n);
     float* y = (float*)malloc(sizeof(float) * n);
 
+    /* c->fused_adaln: the adaLN folded into the GEMMs that read h (orc_cfg), h never formed. */
+    float* r = c->fused_adaln ? (float*)malloc(sizeof(float) * (size_t)M) : NULL;
+    P(adaln_in) in = {h, c->fused_adaln ? h : NULL, r, shift, B, S};
     P(adaln_vectors)(c, blk, 0, cond, B, shift, scale, gate);
-    P(fused_adaln)(x, scale, shift, B, S, D, c->norm_eps, h);
-    P(joint_attention)(c, blk, h, B, S, T, ctx_k, ctx_v, ctx_mask, lat_mask, cos_t, sin_t, y);
+    if (c->fused_adaln) P(adaln_parts)(x, scale, B, S, D, c->norm_eps, h, r);
+    else P(fused_adaln)(x, scale, shift, B, S, D, c->norm_eps, h);
+    P(joint_attention_in)(c, blk, &in, B, S, T, ctx_k, ctx_v, ctx_mask, lat_mask, cos_t, sin_t, y);
     for (size_t i = 0; i < n; i++) {
         int b = (int)(i / ((size_t)S * D)), d = (int)(i % D);
         x[i] = (float)((R)x[i] + (R)gate[b * D + d] * (R)y[i]);
     }
     P(adaln_vectors)(c, blk, 1, cond, B, shift, scale, gate);
-    P(fused_adaln)(x, scale, shift, B, S, D, c->norm_eps, h);
-    P(swiglu_c)(c, h, blk->w13, blk->w2, M, D, F, y);
+    if (c->fused_adaln) P(adaln_parts)(x, scale, B, S, D, c->norm_eps, h, r);
+    else P(fused_adaln)(x, scale, shift, B, S, D, c->norm_eps, h);
+    P(swiglu_c)(c, &in, blk->w13, blk->w2, M, D, F, y);
     for (size_t i = 0; i < n; i++) {
         int b = (int)(i / ((size_t)S * D)), d = (int)(i % D);
         x[i] = (float)((R)x[i] + (R)gate[b * D + d] * (R)y[i]);
     }
-    free(shift); free(scale); free(gate); free(h); free(y);
+    free(shift); free(scale); free(gate); free(h); free(y); free(r);
 }
 
 /* dit/model.rs:354-393 (forward_backbone_fused) with per-layer cached context KV

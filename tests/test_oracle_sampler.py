@@ -17,6 +17,7 @@ sys.path.insert(0, os.path.join(HERE, ".."))
 sys.path.insert(0, os.path.join(HERE, "..", "irodori-tts-burn_amd"))
 
 import irodori_hip as ih  # noqa: E402
+from conftest import rel_l2  # noqa: E402
 from oracle.oracle import Oracle, sampler_struct  # noqa: E402
 
 EULER, HEUN, PLMS = 0, 1, 2
@@ -332,3 +333,23 @@ def test_speaker_and_caption_flags_are_exclusive():
     with pytest.raises(ih.IrodoriError, match="exclusive"):
         p.validate(has_speaker=True, has_caption=True)
     p.validate(has_speaker=False, has_caption=True)
+
+
+def _joint_run(orc, cfg, w, ctx, x0, steps=3):
+    c, u = ctx.rows([0]), ctx.rows([1])
+    out, _ = orc.sample_joint_cfg(cfg, w, x0, (c.k, c.v, c.mask), (u.k, u.v, u.mask), steps, 3.0)
+    return out
+
+
+def test_folded_adaln_is_the_same_function_in_exact_arithmetic():
+    # The folded adaLN of the bf16 sampler chains (h W = r (x (1 + scale)) W + shift W,
+    # norm.rs:160-169) is an algebraic identity: in float64 arithmetic it reproduces the
+    # unfolded sampler to rounding (both store their intermediates as f32, so to f32
+    # rounding: ~1e-7 over three steps; a dropped shift or a misplaced r costs ~1e-1).
+    cfg = ih.cfg_tiny()
+    w = ih.DitWeights.random(cfg, 4, std=0.05, norm_jitter=0.1)
+    ctx = ih.make_context_kv(cfg, 1, 9, 7, seed=2)
+    x0 = ih.make_noise(1, 20, cfg.latent_dim, 3)
+    plain = _joint_run(Oracle("f64"), cfg, w, ctx, x0)
+    folded = _joint_run(Oracle("f64", fused_adaln=True), cfg, w, ctx, x0)
+    assert rel_l2(folded, plain) < 1e-6
