@@ -74,7 +74,7 @@ typedef struct irodori_ctx irodori_ctx;
  * (src/config/model.rs:8-44), plus device sizing. */
 typedef struct irodori_dit_config {
     int32_t latent_dim;         /* patched latent dim P (latent_dim * latent_patch_size), <= 256 */
-    int32_t model_dim;          /* D */
+    int32_t model_dim;          /* D, a multiple of 64, <= 4096 */
     int32_t num_layers;         /* L */
     int32_t num_heads;          /* H (head_dim = D / H) */
     int32_t head_dim;           /* Dh: 64, or 128 for bf16 / f32 (fp8 compute needs 64) */

@@ -867,8 +867,8 @@ int irodori_ctx_create(int device, const irodori_dit_config* cfg, irodori_ctx** 
     IRO_REQUIRE(g.compute_dtype != IRODORI_DTYPE_FP8 || g.head_dim == 64, IRODORI_ERR_SHAPE,
                 "fp8 compute needs head_dim 64");
     IRO_REQUIRE(g.num_heads * g.head_dim == g.model_dim, IRODORI_ERR_SHAPE, "num_heads * head_dim must equal model_dim");
-    IRO_REQUIRE(g.model_dim % 64 == 0 && g.model_dim <= 2048, IRODORI_ERR_SHAPE,
-                "model_dim must be a multiple of 64 and <= 2048");
+    IRO_REQUIRE(g.model_dim % 64 == 0 && g.model_dim <= 4096, IRODORI_ERR_SHAPE,
+                "model_dim must be a multiple of 64 and <= 4096");
     IRO_REQUIRE(g.mlp_hidden > 0, IRODORI_ERR_SHAPE, "mlp_hidden must be positive");
     IRO_REQUIRE(g.latent_dim <= 256, IRODORI_ERR_SHAPE, "latent_dim (patched) must be <= 256");
     IRO_REQUIRE(g.adaln_rank > 0 && g.timestep_embed_dim > 0 && g.timestep_embed_dim % 2 == 0,

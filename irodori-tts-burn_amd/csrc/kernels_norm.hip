@@ -505,8 +505,10 @@ void launch_norm_mod(const float* x, T* h, int M, int S, int D, float eps, ModTa
         norm_mod_kernel<T, 2><<<grid, 256, 0, st>>>(x, h, M, S, D, eps, mt, layer, kind, q8, q8s);
     else if (nch <= 4)
         norm_mod_kernel<T, 4><<<grid, 256, 0, st>>>(x, h, M, S, D, eps, mt, layer, kind, q8, q8s);
-    else
+    else if (nch <= 8)
         norm_mod_kernel<T, 8><<<grid, 256, 0, st>>>(x, h, M, S, D, eps, mt, layer, kind, q8, q8s);
+    else
+        norm_mod_kernel<T, 16><<<grid, 256, 0, st>>>(x, h, M, S, D, eps, mt, layer, kind, q8, q8s);
 }
 
 template <typename T>
@@ -517,7 +519,8 @@ void launch_mod_stats(const float* x, T* h, int M, int S, int D, ModTable mt, in
     if (nch <= 1) mod_stats_kernel<T, 1><<<grid, 256, 0, st>>>(x, h, M, S, D, mt, layer, kind, rstat);
     else if (nch <= 2) mod_stats_kernel<T, 2><<<grid, 256, 0, st>>>(x, h, M, S, D, mt, layer, kind, rstat);
     else if (nch <= 4) mod_stats_kernel<T, 4><<<grid, 256, 0, st>>>(x, h, M, S, D, mt, layer, kind, rstat);
-    else mod_stats_kernel<T, 8><<<grid, 256, 0, st>>>(x, h, M, S, D, mt, layer, kind, rstat);
+    else if (nch <= 8) mod_stats_kernel<T, 8><<<grid, 256, 0, st>>>(x, h, M, S, D, mt, layer, kind, rstat);
+    else mod_stats_kernel<T, 16><<<grid, 256, 0, st>>>(x, h, M, S, D, mt, layer, kind, rstat);
 }
 template void launch_mod_stats<bf16>(const float*, bf16*, int, int, int, ModTable, int, int, float*, hipStream_t);
 
@@ -558,8 +561,11 @@ template <int PT, int NR, int FR>
 static void launch_final_cfg(const FinalArgs& a, hipStream_t st) {
     constexpr int R = NR * FR;
     const size_t lds = sizeof(float) * ((size_t)R * (a.D + a.D / 8) + (size_t)4 * R * PT + (size_t)R * PT + R);
-    // Sized for the largest model width the context accepts (D <= 2048).
-    constexpr int kMax = (int)sizeof(float) * (R * (2048 + 256) + 4 * R * PT + R * PT + R);
+    // Sized for the widest model the instantiation serves: D <= 4096 with at most 6 staged
+    // rows (the launcher keeps wider models there), D <= 2048 otherwise.
+    constexpr int kMaxD = R <= 6 ? 4096 : 2048;
+    constexpr int kMax = (int)sizeof(float) * (R * (kMaxD + kMaxD / 8) + 4 * R * PT + R * PT + R);
+    static_assert(kMax <= 160 * 1024, "staged rows fit the LDS");
     static std::once_flag once;
     static hipError_t attr_rc = hipSuccess;
     (void)set_lds_limit_once(once, attr_rc, (const void*)final_kernel<PT, NR, FR>, kMax);
@@ -582,8 +588,9 @@ static void launch_final_pt(const FinalArgs& a, hipStream_t st) {
     const int nr = a.rf.plan ? a.nrole : 2;
     const int ngroups = a.rf.plan ? a.B : (a.B + nr - 1) / nr;
     // One update element per thread: PT = 128 takes at most two frames per block, 256 one.
+    // Models wider than 2048 stage at most 6 rows (two frames of three roles).
     if constexpr (PT * 4 <= 256) {
-        if ((long)((a.S + 3) / 4) * ngroups >= 256) {
+        if (a.D <= 2048 && (long)((a.S + 3) / 4) * ngroups >= 256) {
             launch_final_fr<PT, 4>(a, st);
             return;
         }

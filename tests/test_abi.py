@@ -102,6 +102,7 @@ def test_op_shape_and_dtype_errors_before_any_device_call():
     ("compute_dtype", 9, L.ERR_DTYPE),
     ("norm_eps", 0.0, L.ERR_CONFIG),
     ("latent_dim", 257, L.ERR_SHAPE),
+    ("model_dim", 4160, L.ERR_SHAPE),
     ("max_rows", 65536, L.ERR_SHAPE),
 ])
 def test_ctx_create_config_errors(field, value, code):

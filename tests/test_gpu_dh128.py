@@ -42,19 +42,31 @@ def cfg_reference_default(layers=2):
                                mlp_hidden=5888, adaln_rank=256, timestep_embed_dim=512, norm_eps=1e-5)
 
 
+def cfg_d4096(layers=1):
+    # Wider than the reference's default: d 4096 = 32 x 128 heads, SwiGLU 4096 * 2.875 (the
+    # unfused adaLN, 16 float4 chunks per lane in its norm kernel; the output head stages at
+    # most six rows).
+    return dataclasses.replace(cfg_reference_default(layers), model_dim=4096, num_heads=32, mlp_hidden=11776)
+
+
 CASES = {
     # name: (cfg factory, seq, text, speaker, weight std, norm jitter)
     "tiny": (cfg_dh128_tiny, 40, 20, 13, 0.05, 0.1),
     "tiny_odd": (cfg_dh128_tiny, 37, 11, 9, 0.05, 0.1),
     "h3": (cfg_dh128_h3, 40, 20, 13, 0.05, 0.1),
     "ref_default": (cfg_reference_default, 48, 16, 20, 0.02, 0.05),
+    "d4096": (cfg_d4096, 24, 8, 9, 0.02, 0.05),
+    # 512 frames: the output head takes two frames per block (enough blocks to fill the chip)
+    "d4096_s512": (cfg_d4096, 512, 8, 9, 0.02, 0.05),
 }
 
 
 @pytest.mark.parametrize("backend", [F32, BF16], ids=["f32", "bf16"])
 @pytest.mark.parametrize("name", list(CASES))
-def test_forward_per_block_dh128(oracle64, name, backend):
+def test_forward_per_block_dh128(oracle64, oracle32, name, backend):
     make_cfg, S, tt, ts, std, jit = CASES[name]
+    if name == "d4096_s512":
+        oracle64 = oracle32  # 1024 rows at d 4096: the f32 oracle (per-block bars unchanged)
     cfg = make_cfg()
     assert cfg.head_dim == 128
     w = ih.DitWeights.random(cfg, 0, std=std, norm_jitter=jit)
@@ -71,7 +83,7 @@ def test_forward_per_block_dh128(oracle64, name, backend):
 
 
 @pytest.mark.parametrize("backend", [F32, BF16], ids=["f32", "bf16"])
-@pytest.mark.parametrize("name", ["tiny", "ref_default"])
+@pytest.mark.parametrize("name", ["tiny", "ref_default", "d4096"])
 def test_sample_joint_cfg_dh128(oracle64, name, backend):
     # 4 Euler steps of Joint CFG (scale 3) through the captured step graphs.
     make_cfg, S, tt, ts, std, jit = CASES[name]
