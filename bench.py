@@ -173,6 +173,27 @@ def mfma_summary(pmc_csv, M=750, D=1024, F=2816, H=16, Dh=64, T=1381):
     return "\n".join(lines + [""] + out)
 
 
+def marker_summary(marker_csv):
+    """Per-range host durations of a rocprofv3 --marker-trace CSV of this script run with
+    IRODORI_ROCTX=1 (the library's ranges carry the reference's NVTX names,
+    src/profiling.rs:29-92).  Ranges bracket host work: graph capture for the per-block ranges,
+    the per-evaluation graph launch for the sampler's."""
+    import collections
+    import csv
+    dur = collections.defaultdict(list)
+    first = {}
+    with open(marker_csv) as f:
+        for i, r in enumerate(csv.DictReader(f)):
+            name = r["Function"]
+            dur[name].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+            first.setdefault(name, (int(r["Start_Timestamp"]), i))
+    lines = ["| range | count | avg us | min us | max us |", "|---|---|---|---|---|"]
+    for name in sorted(dur, key=lambda n: first[n]):
+        v = dur[name]
+        lines.append("| %s | %d | %.1f | %.1f | %.1f |" % (name, len(v), sum(v) / len(v), min(v), max(v)))
+    return "\n".join(lines)
+
+
 def read_profile_value(path, key):
     """The number after `key:` in a committed profile summary, or None."""
     try:
@@ -323,6 +344,9 @@ def main():
                          "counter_collection.csv files of this script and exit")
     ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
                     help="print the summary of a rocprofv3 --kernel-trace CSV of this script and exit")
+    ap.add_argument("--marker-summary", metavar="MARKER_API_TRACE_CSV",
+                    help="print the roctx range summary of a rocprofv3 --marker-trace CSV of this "
+                         "script (run with IRODORI_ROCTX=1) and exit")
     ap.add_argument("--mfma-summary", metavar="COUNTER_CSV",
                     help="print the MFMA-busy summary of a rocprofv3 --pmc CSV of this script "
                          "(SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CYCLES SQ_INSTS_VALU_MFMA_MOPS_BF16 "
@@ -337,6 +361,9 @@ def main():
         return
     if args.mfma_summary:
         print(mfma_summary(args.mfma_summary))
+        return
+    if args.marker_summary:
+        print(marker_summary(args.marker_summary))
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the RF step of one model instance "
