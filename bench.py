@@ -173,6 +173,51 @@ def mfma_summary(pmc_csv, M=750, D=1024, F=2816, H=16, Dh=64, T=1381):
     return "\n".join(lines + [""] + out)
 
 
+def stall_summary(*pmc_csvs):
+    """Where the hot kernels' waves spend their resident time, from rocprofv3 --pmc runs of
+    this script (any split of SQ_WAVE_CYCLES, SQ_WAIT_ANY, SQ_WAIT_INST_ANY,
+    SQ_ACTIVE_INST_ANY, SQ_WAVES, SQ_INSTS_{VALU,SALU,MFMA,LDS,VMEM_RD},
+    SQ_LDS_BANK_CONFLICT, SQ_VALU_MFMA_COEXEC_CYCLES over the passes).  The wait and active
+    counters are wave-cycles (quad-cycle units, like SQ_WAVE_CYCLES), so their ratios to
+    SQ_WAVE_CYCLES are fractions of the waves' resident time: WAIT_ANY = waiting on a
+    dependency (s_waitcnt on memory or LDS, s_barrier), WAIT_INST_ANY = ready but not issued
+    (issue port or matrix core busy).  Instruction counts are per wave."""
+    import csv
+    per = {}
+    for path in pmc_csvs:
+        for r in csv.DictReader(open(path)):
+            key, _ = kernel_info(r["Kernel_Name"])
+            if not key:
+                continue
+            acc = per.setdefault(key, {})
+            tot = acc.setdefault(r["Counter_Name"], [0.0, set()])
+            tot[0] += float(r["Counter_Value"])
+            tot[1].add((path, r["Dispatch_Id"]))
+    def avg(acc, c):
+        v = acc.get(c)
+        return v[0] / len(v[1]) if v and v[1] else None
+    cols = ("wait dep", "wait issue", "active", "VALU/wave", "SALU/wave", "MFMA/wave", "LDS/wave",
+            "VMEM rd/wave", "LDS bank confl.")
+    lines = ["| kernel | " + " | ".join(cols) + " |", "|---|" + "---|" * len(cols)]
+    for key in ("w13_gemm", "qkvg_gemm", "resid_gemm", "attention"):
+        acc = per.get(key)
+        if not acc:
+            continue
+        wc, waves = avg(acc, "SQ_WAVE_CYCLES"), avg(acc, "SQ_WAVES")
+        def frac(c):
+            v = avg(acc, c)
+            return "%.2f" % (v / wc) if v is not None and wc else "-"
+        def pw(c):
+            v = avg(acc, c)
+            return "%.0f" % (v / waves) if v is not None and waves else "-"
+        bank = avg(acc, "SQ_LDS_BANK_CONFLICT")
+        lines.append("| %s | %s | %s | %s | %s | %s | %s | %s | %s | %s |" % (
+            key, frac("SQ_WAIT_ANY"), frac("SQ_WAIT_INST_ANY"), frac("SQ_ACTIVE_INST_ANY"),
+            pw("SQ_INSTS_VALU"), pw("SQ_INSTS_SALU"), pw("SQ_INSTS_MFMA"), pw("SQ_INSTS_LDS"),
+            pw("SQ_INSTS_VMEM_RD"), "-" if bank is None else "%.0f" % bank))
+    return "\n".join(lines)
+
+
 def marker_summary(marker_csv):
     """Per-range host durations of a rocprofv3 --marker-trace CSV of this script run with
     IRODORI_ROCTX=1 (the library's ranges carry the reference's NVTX names,
@@ -344,6 +389,9 @@ def main():
                          "counter_collection.csv files of this script and exit")
     ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
                     help="print the summary of a rocprofv3 --kernel-trace CSV of this script and exit")
+    ap.add_argument("--stall-summary", nargs="+", metavar="COUNTER_CSV",
+                    help="print the wave stall / instruction-mix summary of rocprofv3 --pmc CSVs of "
+                         "this script and exit")
     ap.add_argument("--marker-summary", metavar="MARKER_API_TRACE_CSV",
                     help="print the roctx range summary of a rocprofv3 --marker-trace CSV of this "
                          "script (run with IRODORI_ROCTX=1) and exit")
@@ -361,6 +409,9 @@ def main():
         return
     if args.mfma_summary:
         print(mfma_summary(args.mfma_summary))
+        return
+    if args.stall_summary:
+        print(stall_summary(*args.stall_summary))
         return
     if args.marker_summary:
         print(marker_summary(args.marker_summary))
