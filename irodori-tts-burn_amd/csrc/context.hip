@@ -333,7 +333,7 @@ int enqueue_mod_table(irodori_ctx* c, int nvec, bool skip_mlp, int l0 = 0, int l
     int D = g.model_dim, L = g.num_layers, r = g.adaln_rank;
     if (l1 < 0) l1 = L;
     if (!skip_mlp) {
-        RoctxRange r("cond_module");  // timestep embedding + conditioning MLP (dit/model.rs:298-302)
+        RoctxRange cond("cond_module");  // timestep embedding + conditioning MLP (dit/model.rs:298-302)
         {
             RoctxRange te("timestep_embed");
             launch_timestep_embedding(c->tvec, nvec, g.timestep_embed_dim, c->emb, c->stream);
@@ -607,19 +607,19 @@ int enqueue_layer(irodori_ctx* c, int l, int B, int S, const ModTable& mt, int r
     snprintf(name, sizeof(name), "dit_block_%d", l);
     RoctxRange block(name);  // the reference's per-block and per-half ranges (diffusion.rs:88-104)
     {
-        RoctxRange r("joint_attention_fused");
+        RoctxRange range("joint_attention_fused");
         for (int p : {PART_QKVG, PART_ATTN, PART_WO}) IRO_TRY(enqueue_part<T>(c, l, B, S, mt, p, r0, st));
     }
     {
-        RoctxRange r("adaln_mlp");
+        RoctxRange range("adaln_mlp");
         IRO_TRY(enqueue_part<T>(c, l, B, S, mt, PART_NORM_MLP, r0, st));
     }
     {
-        RoctxRange r("swiglu_mlp_fused");
+        RoctxRange range("swiglu_mlp_fused");
         for (int p : {PART_W13, PART_W2}) IRO_TRY(enqueue_part<T>(c, l, B, S, mt, p, r0, st));
     }
     {
-        RoctxRange r("adaln_attn");  // the next block's attention adaLN, from this block's output
+        RoctxRange range("adaln_attn");  // the next block's attention adaLN, from this block's output
         IRO_TRY(enqueue_part<T>(c, l, B, S, mt, PART_NORM_NEXT, r0, st));
     }
     return check_launch("layer");
@@ -1436,7 +1436,7 @@ static int forward_impl(irodori_ctx* c, int B, int S, const float* x_t, const fl
     IRO_TRY(enqueue_mod_table(c, B, false));
     ModTable mt{c->tab, c->zero_step, 0, 1, L};
     {
-        RoctxRange r("in_proj");
+        RoctxRange range("in_proj");
         IRO_TRY(enqueue_inproj(c, B, S, c->xt, B, 0, mt, c->stream));
     }
     size_t n = (size_t)B * S * D;
@@ -1448,7 +1448,7 @@ static int forward_impl(irodori_ctx* c, int B, int S, const float* x_t, const fl
                                          c->stream));
     }
     {
-        RoctxRange r("out_proj");  // out_norm folded into the head's weights (dit/model.rs:391-392)
+        RoctxRange range("out_proj");  // out_norm folded into the head's weights (dit/model.rs:391-392)
         IRO_TRY(enqueue_head(c, B, S, 0, c->stream));
     }
     IRO_HIP_CHECK(hipMemcpyAsync(v_out, c->vout, sizeof(float) * (size_t)B * S * P, hipMemcpyDeviceToHost, c->stream));
@@ -1707,13 +1707,13 @@ static int sample_device_impl(irodori_ctx* c, const irodori_sampler_params* p, i
     for (int i = 0; i < N; i++) {
         hipGraphExec_t ex = nullptr;
         {
-            RoctxRange r(eval_name(roles_of[2 * i]));
+            RoctxRange range(eval_name(roles_of[2 * i]));
             IRO_TRY(graph_for(roles_of[2 * i], 0, &ex));
             IRO_HIP_CHECK(hipGraphLaunch(ex, c->stream));
         }
         if (i == revert_step && kvs) IRO_TRY(scale_kv(false, 1.0f / p->speaker_kv_scale));
         if (heun) {
-            RoctxRange r("heun_corrector");
+            RoctxRange range("heun_corrector");
             IRO_TRY(graph_for(roles_of[2 * i + 1], 1, &ex));
             IRO_HIP_CHECK(hipGraphLaunch(ex, c->stream));
         }
