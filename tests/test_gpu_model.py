@@ -62,6 +62,11 @@ SMALL = {
     # 4000 latent + 250 context keys: 67 key tiles per row, past the 64 one word of the
     # bf16 attention's tile list holds
     "long_keys": (ih.cfg_tiny, 4000, 150, 100, 0.05, 0.1),
+    # one and three latent frames: every token pair of the V^T scatter crosses a batch row
+    # (S = 1), the QKV+gate RoPE rows step through fewer tokens than one load covers (S < 4),
+    # and the output head's frame blocks are mostly past S
+    "one_frame": (ih.cfg_tiny, 1, 20, 13, 0.05, 0.1),
+    "three_frames": (ih.cfg_tiny, 3, 20, 13, 0.05, 0.1),
 }
 
 
@@ -132,6 +137,24 @@ def test_sample_joint_cfg_wide_latent(oracle64, backend, P):
     c, u = ctx.rows([0]), ctx.rows([1])
     ref, _ = oracle64.sample_joint_cfg(cfg, w, x0, (c.k, c.v, c.mask), (u.k, u.v, u.mask), 4, 3.0)
     print(backend.value, "latent %d: final rel L2 %.2e" % (P, rel_l2(got, ref)))
+    assert rel_l2(got, ref) < TOL_FINAL[backend]
+
+
+@pytest.mark.parametrize("backend", [F32, BF16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("S", [1, 3])
+def test_sample_joint_cfg_few_frames(oracle64, backend, S):
+    # Utterances of one and three latent frames through the graph-captured sampler: 4 Euler
+    # steps of Joint CFG against the oracle.
+    cfg = ih.cfg_tiny()
+    w = ih.DitWeights.random(cfg, 0, std=0.05)
+    ctx = ih.make_context_kv(cfg, 1, 20, 13, seed=1)
+    x0 = ih.make_noise(1, S, cfg.latent_dim, 2)
+    p = joint_params(4)
+    with make_engine(cfg, backend, w, ctx, 2, S) as e:
+        got = e.sample(x0, p)
+    c, u = ctx.rows([0]), ctx.rows([1])
+    ref, _ = oracle64.sample_joint_cfg(cfg, w, x0, (c.k, c.v, c.mask), (u.k, u.v, u.mask), 4, 3.0)
+    print(backend.value, "S = %d: final rel L2 %.2e" % (S, rel_l2(got, ref)))
     assert rel_l2(got, ref) < TOL_FINAL[backend]
 
 
