@@ -40,6 +40,8 @@ CASES = {
     # name: (config, rows' valid lengths, seq)
     "text_dh128": (ih.enc_text_tiny, [20, 13, 0], 20),     # a row with no valid token
     "speaker_dh64": (ih.enc_speaker_tiny, [37, 30], 37),    # mean token, odd length
+    "text_one_token": (ih.enc_text_tiny, [1, 0], 1),        # one token, and a row with none
+    "speaker_one_frame": (ih.enc_speaker_tiny, [1, 1], 1),  # one reference frame + the mean token
 }
 
 
