@@ -521,6 +521,9 @@ def main():
     alg["resid_gemm"] = (alg["wo_gemm"] + alg["w2_gemm"]) // 2  # per launch, the two alternating
     norm_bytes = M * D * 4 + M * D * 2  # read x f32, write h bf16
     norm_gbs = norm_bytes / (kt["norm_mod_us"] * 1e-6) / 1e9
+    peak_meas = achievable_bf16_peak(torch)
+    log("achievable dense bf16 (large square GEMM): %.0f TFLOP/s = %.3f of the published peak"
+        % (peak_meas["tflops"], peak_meas["frac_of_peak"]))
 
     # Every hot kernel at the RF launch shape: event time (this run), the committed trace's
     # average over the same back-to-back launches, both as fractions of the bf16 peak, and
@@ -608,7 +611,8 @@ def main():
                                  "source": "profiles/rf_config4_kernel_trace.md (rocprofv3 kernel trace of this "
                                            "script, its irodori_profile_layer phase: the same back-to-back "
                                            "launches the event figures time)"},
-                     "hot_kernels": hot},
+                     "hot_kernels": hot,
+                     "achievable_peak": peak_meas},
         "cpu_baseline": cpu,
     }
     eng.close()
@@ -644,6 +648,30 @@ def time_on_stream(torch, fn, warmup, steps):
     e1.record(st)
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / steps
+
+
+def achievable_bf16_peak(torch, n=8192, reps=10):
+    """The dense bf16 rate a large square GEMM reaches on this GPU: torch.matmul (the ROCm
+    BLAS library) on contiguous n x n bf16 operands, HIP events over reps calls after two
+    warm-up calls.  A reference point for the roofline fractions (they stay against the
+    published peak); not part of the timed RF run."""
+    a = torch.randn((n, n), device="cuda", dtype=torch.bfloat16)
+    b = torch.randn((n, n), device="cuda", dtype=torch.bfloat16)
+    c = torch.empty((n, n), device="cuda", dtype=torch.bfloat16)
+    for _ in range(2):
+        torch.matmul(a, b, out=c)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()  # torch's current stream, the one the products run on
+    for _ in range(reps):
+        torch.matmul(a, b, out=c)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    tflops = 2.0 * n ** 3 / (ms * 1e-3) / 1e12
+    del a, b, c
+    return {"gemm": "torch.matmul bf16 %dx%dx%d (ROCm BLAS), contiguous operands" % (n, n, n),
+            "ms": round(ms, 3), "tflops": round(tflops, 1), "frac_of_peak": round(tflops / PEAK_BF16_TFLOPS, 4)}
 
 
 def run_isolated(args, np, torch, ih):
