@@ -1,8 +1,8 @@
-"""Sanitizer runs on the CPU (the reference's race / memory checking aside, SURVEY's aux
-subsystems): the oracle built with AddressSanitizer + UBSan and driven through its entry
-points (tests/sanitize/oracle_run.py), and the library's host code built likewise and
-driven through the C ABI's device-free validation paths (tests/sanitize/host_driver.cpp).
-Each must finish with no sanitizer report."""
+"""Sanitizer runs on the CPU (memory and undefined-behaviour checking of the host side; GPU
+sanitizer builds are not used): the oracle built with AddressSanitizer + UBSan and driven
+through its entry points (tests/sanitize/oracle_run.py), and the library's host code built
+likewise and driven through the C ABI's device-free validation paths
+(tests/sanitize/host_driver.cpp).  Each must finish with no sanitizer report."""
 import os
 import shutil
 import subprocess
