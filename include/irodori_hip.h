@@ -45,7 +45,10 @@ extern "C" {
 #define IRODORI_ERR_SHAPE 2       /* dimension mismatch / unsupported shape */
 #define IRODORI_ERR_DTYPE 3       /* unsupported dtype */
 #define IRODORI_ERR_HIP 4         /* HIP runtime error */
-#define IRODORI_ERR_OOM 5         /* device allocation failed */
+#define IRODORI_ERR_OOM 5         /* device allocation failed (or would pass the limit that the
+                                     environment variable IRODORI_DEVICE_ALLOC_LIMIT, a byte
+                                     count, sets on each context's, encoder's and codec's
+                                     persistent device buffers: a way to exercise this path) */
 #define IRODORI_ERR_NOT_LOADED 6  /* weights / context KV missing */
 #define IRODORI_ERR_CONFIG 7      /* invalid sampler / model configuration */
 

@@ -74,6 +74,7 @@ struct irodori_codec {
     int hop = 1, proj_p = 0, dim_p = 0, last_p = 0;
     hipStream_t stream = nullptr;
     std::vector<void*> allocs;
+    uint64_t dev_bytes = 0;  // persistent device bytes held (tracked_alloc)
     float *in_w = nullptr, *in_b = nullptr;  // [proj_p, latent_dim], [proj_p]
     void* stem_w = nullptr;                  // [dim_p, 7 * proj_p]
     float* stem_b = nullptr;                 // [dim_p] or null
@@ -91,16 +92,7 @@ struct irodori_codec {
 
 namespace {
 
-int codec_alloc(irodori_codec* c, void** p, size_t bytes) {
-    if (bytes == 0) bytes = 16;
-    hipError_t err = hipMalloc(p, bytes);
-    if (err != hipSuccess) {
-        set_last_error(std::string("hipMalloc(") + std::to_string(bytes) + "): " + hipGetErrorString(err));
-        return err == hipErrorOutOfMemory ? IRODORI_ERR_OOM : IRODORI_ERR_HIP;
-    }
-    c->allocs.push_back(*p);
-    return IRODORI_OK;
-}
+int codec_alloc(irodori_codec* c, void** p, size_t bytes) { return tracked_alloc(c->allocs, c->dev_bytes, p, bytes); }
 template <typename P>
 int codec_alloc_t(irodori_codec* c, P** p, size_t bytes) {
     return codec_alloc(c, reinterpret_cast<void**>(p), bytes);

@@ -6,6 +6,7 @@
 
 #include <mutex>
 #include <string>
+#include <vector>
 
 namespace irodori {
 
@@ -194,6 +195,13 @@ __device__ __forceinline__ int xcd_remap(int id, int n) {
 // Host-side error plumbing (thread-local last error, status codes of irodori_hip.h).
 // ---------------------------------------------------------------------------------
 void set_last_error(const std::string& msg);
+
+// Device allocation of one object's persistent buffers (a DiT context, an encoder, a codec):
+// hipMalloc, the pointer recorded in allocs (freed with the object), the bytes added to total.
+// With IRODORI_DEVICE_ALLOC_LIMIT set (a byte count, read at each call), an allocation that
+// would bring the object's total above it fails with IRODORI_ERR_OOM before hipMalloc runs,
+// so a caller can exercise its out-of-memory handling on any device.
+int tracked_alloc(std::vector<void*>& allocs, uint64_t& total, void** p, size_t bytes);
 
 // Raises a kernel's dynamic-LDS limit once per process.  The first launch of a kernel
 // variant may come from several host threads at once (one context, encoder or codec per

@@ -12,6 +12,7 @@
 // One RF step is recorded once into a hipGraph and replayed num_steps times; the step
 // index lives in device memory and is advanced by the last node of the graph.
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
@@ -33,6 +34,27 @@ namespace irodori {
 
 static thread_local std::string g_last_error;
 void set_last_error(const std::string& msg) { g_last_error = msg; }
+
+int tracked_alloc(std::vector<void*>& allocs, uint64_t& total, void** p, size_t bytes) {
+    if (bytes == 0) bytes = 16;
+    if (const char* lim = std::getenv("IRODORI_DEVICE_ALLOC_LIMIT")) {
+        const unsigned long long limit = std::strtoull(lim, nullptr, 10);
+        if (limit > 0 && total + bytes > limit) {
+            set_last_error("device allocation of " + std::to_string(bytes) + " bytes would exceed "
+                           "IRODORI_DEVICE_ALLOC_LIMIT (" + std::to_string(limit) + " bytes; " +
+                           std::to_string(total) + " already held)");
+            return IRODORI_ERR_OOM;
+        }
+    }
+    hipError_t e = hipMalloc(p, bytes);
+    if (e != hipSuccess) {
+        set_last_error(std::string("hipMalloc(") + std::to_string(bytes) + "): " + hipGetErrorString(e));
+        return e == hipErrorOutOfMemory ? IRODORI_ERR_OOM : IRODORI_ERR_HIP;
+    }
+    allocs.push_back(*p);
+    total += bytes;
+    return IRODORI_OK;
+}
 
 }  // namespace irodori
 
@@ -182,17 +204,7 @@ struct irodori_ctx {
 
 namespace {
 
-int dev_alloc(irodori_ctx* c, void** p, size_t bytes) {
-    if (bytes == 0) bytes = 16;
-    hipError_t e = hipMalloc(p, bytes);
-    if (e != hipSuccess) {
-        set_last_error(std::string("hipMalloc(") + std::to_string(bytes) + "): " + hipGetErrorString(e));
-        return e == hipErrorOutOfMemory ? IRODORI_ERR_OOM : IRODORI_ERR_HIP;
-    }
-    c->allocs.push_back(*p);
-    c->dev_bytes += bytes;
-    return IRODORI_OK;
-}
+int dev_alloc(irodori_ctx* c, void** p, size_t bytes) { return tracked_alloc(c->allocs, c->dev_bytes, p, bytes); }
 
 template <typename P>
 int dalloc(irodori_ctx* c, P** p, size_t bytes) {

@@ -41,6 +41,7 @@ struct irodori_encoder {
     size_t esz = 2;
     hipStream_t stream = nullptr;
     std::vector<void*> allocs;
+    uint64_t dev_bytes = 0;  // persistent device bytes held (tracked_alloc)
     std::vector<EncLayer> layers;
     float *embedding = nullptr, *in_w = nullptr, *in_b = nullptr, *out_norm = nullptr;
     bool io_loaded = false;
@@ -62,16 +63,7 @@ struct irodori_encoder {
 
 namespace {
 
-int enc_alloc(irodori_encoder* e, void** p, size_t bytes) {
-    if (bytes == 0) bytes = 16;
-    hipError_t err = hipMalloc(p, bytes);
-    if (err != hipSuccess) {
-        set_last_error(std::string("hipMalloc(") + std::to_string(bytes) + "): " + hipGetErrorString(err));
-        return err == hipErrorOutOfMemory ? IRODORI_ERR_OOM : IRODORI_ERR_HIP;
-    }
-    e->allocs.push_back(*p);
-    return IRODORI_OK;
-}
+int enc_alloc(irodori_encoder* e, void** p, size_t bytes) { return tracked_alloc(e->allocs, e->dev_bytes, p, bytes); }
 template <typename P>
 int enc_alloc_t(irodori_encoder* e, P** p, size_t bytes) {
     return enc_alloc(e, reinterpret_cast<void**>(p), bytes);

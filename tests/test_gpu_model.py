@@ -428,3 +428,28 @@ def test_profile_layer_reports_every_kernel(backend):
     with make_engine(cfg, F32, w, ctx, 2, 64) as e:
         with pytest.raises(ih.IrodoriError, match="Dtype"):
             e.profile_layer(1, 64, 3)
+
+
+def test_device_allocation_limit_reports_out_of_memory(monkeypatch):
+    # IRODORI_DEVICE_ALLOC_LIMIT turns a context's, encoder's or codec's persistent
+    # allocations past the limit into IRODORI_ERR_OOM (OutOfMemory) before hipMalloc runs; the
+    # partly built object is released, and objects created without the limit work.
+    cfg = ih.cfg_tiny()
+    monkeypatch.setenv("IRODORI_DEVICE_ALLOC_LIMIT", "4096")
+    with pytest.raises(ih.IrodoriError) as ei:
+        ih.HipInferenceEngine(cfg, F32, max_rows=2, max_seq=40, max_ctx=33)
+    assert ei.value.kind == "OutOfMemory" and "IRODORI_DEVICE_ALLOC_LIMIT" in str(ei.value)
+    with pytest.raises(ih.IrodoriError) as ei:
+        ih.HipEncoder(ih.enc_text_tiny(), F32, max_rows=2, max_seq=20)
+    assert ei.value.kind == "OutOfMemory"
+    with pytest.raises(ih.IrodoriError) as ei:
+        ih.HipDacVaeCodec(ih.codec_tiny(), F32, max_frames=16)
+    assert ei.value.kind == "OutOfMemory"
+    monkeypatch.delenv("IRODORI_DEVICE_ALLOC_LIMIT")
+    w = ih.DitWeights.random(cfg, 0, std=0.05)
+    ctx = ih.make_context_kv(cfg, 1, 20, 13, seed=1)
+    x = ih.make_noise(2, 40, cfg.latent_dim, 2)
+    with make_engine(cfg, F32, w, ctx, 2, 40) as e:
+        v = e.forward_with_cond_cached(x, np.array([0.9, 0.35], np.float32))
+    assert np.all(np.isfinite(v))
+
