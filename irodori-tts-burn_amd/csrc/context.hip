@@ -98,7 +98,7 @@ struct GraphKey {
     int roles;          // bit r set: role r runs (rows r*U .. r*U + U - 1)
     int method, phase;
     int latent_masked;  // the captured attention reads the latent key masks
-    int kv_scaled;      // the captured attention reads the speaker-scaled context copies
+    int kv_scaled;      // layers whose captured attention reads the speaker-scaled copies
     bool operator<(const GraphKey& o) const {
         return std::tie(U, S, T, roles, method, phase, latent_masked, kv_scaled) <
                std::tie(o.U, o.S, o.T, o.roles, o.method, o.phase, o.latent_masked, o.kv_scaled);
@@ -1681,7 +1681,7 @@ static int sample_device_impl(irodori_ctx* c, const irodori_sampler_params* p, i
 
     // One captured graph per distinct evaluation (roles, phase), replayed per step.
     auto graph_for = [&](int roles, int phase, hipGraphExec_t* out) -> int {
-        GraphKey key{U, S, c->t_ctx, roles, method, phase, lengths ? 1 : 0, c->kvs_on ? 1 : 0};
+        GraphKey key{U, S, c->t_ctx, roles, method, phase, lengths ? 1 : 0, c->kvs_on ? c->kvs_layers : 0};
         auto it = c->graphs.find(key);
         if (it != c->graphs.end()) {
             *out = it->second;

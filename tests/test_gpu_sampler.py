@@ -115,6 +115,36 @@ def test_speaker_kv_scaling_with_revert(oracle64, model, backend, mode):
     assert np.array_equal(got, again)  # the context copies are rebuilt for every call
 
 
+def test_speaker_kv_layer_count_changes_between_calls(oracle64, model):
+    # One context sampled with speaker-KV scaling in the first layer, then in both layers,
+    # then without, then in the first layer again: the captured evaluations must follow the
+    # layer count of each call (each result equals a fresh context's, bit for bit, and the
+    # oracle's).
+    cfg, w = model
+    runs = [ih.config.SpeakerKvConfig(scale=1.8, max_layers=1), ih.config.SpeakerKvConfig(scale=1.8, max_layers=2),
+            None, ih.config.SpeakerKvConfig(scale=1.8, max_layers=1)]
+    ps = [params(M.JOINT, SM.EULER, steps=3, speaker_kv=skv) for skv in runs]
+    roles = ps[0].cfg_roles(has_speaker=True)
+    ctx = ih.make_role_context(cfg, 1, TT, TA, roles, seed=3)
+    x0 = ih.make_noise(1, S, cfg.latent_dim, 4)
+
+    def engine():
+        e = ih.HipInferenceEngine(cfg, F32, max_rows=len(roles), max_seq=S, max_ctx=ctx.t_ctx)
+        e.load_weights(w)
+        e.set_context_kv(ctx)
+        return e
+
+    with engine() as e:
+        seq = [e.sample(x0, p, ctx_aux_start=TT) for p in ps]
+    for p, got in zip(ps, seq):
+        with engine() as fresh:
+            alone = fresh.sample(x0, p, ctx_aux_start=TT)
+        ref, _ = oracle64.sample_rf(cfg, w, x0, (ctx.k, ctx.v, ctx.mask), orc_params(p))
+        assert np.array_equal(got, alone)
+        assert rel_l2(got, ref) < TOL[F32]
+    assert rel_l2(seq[0], seq[1]) > 1e-5  # the layer count matters
+
+
 @pytest.mark.parametrize("backend", [F32, BF16], ids=["f32", "bf16"])
 def test_two_utterances_independent_padded(oracle64, model, backend):
     # Role-major rows with U = 2 (conditioned 0-1, text dropped 2-3, speaker dropped 4-5),
