@@ -203,13 +203,25 @@ void set_last_error(const std::string& msg);
 // so a caller can exercise its out-of-memory handling on any device.
 int tracked_alloc(std::vector<void*>& allocs, uint64_t& total, void** p, size_t bytes);
 
-// Raises a kernel's dynamic-LDS limit once per process.  The first launch of a kernel
-// variant may come from several host threads at once (one context, encoder or codec per
-// thread), so the one-time call is guarded by a once_flag owned by the caller (one static
-// per kernel instantiation); every caller sees the call's result.
-inline hipError_t set_lds_limit_once(std::once_flag& once, hipError_t& rc, const void* fn, int bytes) {
-    std::call_once(once, [&] { rc = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes); });
-    return rc;
+// Raises a kernel's dynamic-LDS limit once per process and device (the attribute belongs to
+// the kernel's code object on each device; launches run on the current device, which every
+// entry point sets to its object's).  The first launch of a kernel variant may come from
+// several host threads at once (one context, encoder or codec per thread), so the one-time
+// call is guarded by a once_flag per device, owned by the caller (one static LdsLimit per
+// kernel instantiation); every caller sees the call's result.
+struct LdsLimit {
+    static constexpr int kDevices = 64;
+    std::once_flag once[kDevices];
+    hipError_t rc[kDevices] = {};
+};
+inline hipError_t set_lds_limit_once(LdsLimit& lim, const void* fn, int bytes) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= LdsLimit::kDevices) return hipErrorInvalidDevice;
+    std::call_once(lim.once[dev],
+                   [&] { lim.rc[dev] = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes); });
+    return lim.rc[dev];
 }
 
 }  // namespace irodori

@@ -546,9 +546,8 @@ __global__ __launch_bounds__(64 * QB * KVS) __attribute__((amdgpu_waves_per_eu(1
 template <typename T, int QB, int KVS, int NT>
 int launch_attn32_cfg(const AttnArgs<T>& a, hipStream_t st) {
     const size_t lds = (size_t)4 * KVS * TILE_BYTES;
-    static std::once_flag once;
-    static hipError_t attr_rc = hipSuccess;
-    if (set_lds_limit_once(once, attr_rc, (const void*)attn32_kernel<T, QB, KVS, NT>, (int)lds) != hipSuccess)
+    static LdsLimit lds_limit;
+    if (set_lds_limit_once(lds_limit, (const void*)attn32_kernel<T, QB, KVS, NT>, (int)lds) != hipSuccess)
         return -2;
     const int nqb = (a.Sq + 32 * QB - 1) / (32 * QB);
     attn32_kernel<T, QB, KVS, NT><<<dim3(nqb * a.H * a.B), 64 * QB * KVS, lds, st>>>(a, nqb);

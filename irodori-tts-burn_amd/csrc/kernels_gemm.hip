@@ -1313,10 +1313,9 @@ int launch_cfg(const GemmArgs<T>& a, hipStream_t st) {
     constexpr int kStageLds = STAGES * (BM + BN) * 128;
     const size_t lds = (size_t)(kStageLds > kResLds ? kStageLds : kResLds) + (F8 ? (size_t)BM * (a.K / 32) : 0);
     // Per instantiation; the attribute is process-wide.
-    static std::once_flag once;
-    static hipError_t attr_rc = hipSuccess;
+    static LdsLimit lds_limit;
     constexpr int lds_max = (kStageLds > kResLds ? kStageLds : kResLds) + (F8 ? BM * (kMaxK8 / 32) : 0);
-    if (set_lds_limit_once(once, attr_rc, (const void*)gemm_kernel<T, BM, BN, WAVES_M, WAVES_N, STAGES, EPI, F8, CONV>,
+    if (set_lds_limit_once(lds_limit, (const void*)gemm_kernel<T, BM, BN, WAVES_M, WAVES_N, STAGES, EPI, F8, CONV>,
                            lds_max) != hipSuccess)
         return -2;
     gemm_kernel<T, BM, BN, WAVES_M, WAVES_N, STAGES, EPI, F8, CONV><<<tiles, 64 * WAVES_M * WAVES_N, lds, st>>>(a);

@@ -566,9 +566,8 @@ static void launch_final_cfg(const FinalArgs& a, hipStream_t st) {
     constexpr int kMaxD = R <= 6 ? 4096 : 2048;
     constexpr int kMax = (int)sizeof(float) * (R * (kMaxD + kMaxD / 8) + 4 * R * PT + R * PT + R);
     static_assert(kMax <= 160 * 1024, "staged rows fit the LDS");
-    static std::once_flag once;
-    static hipError_t attr_rc = hipSuccess;
-    (void)set_lds_limit_once(once, attr_rc, (const void*)final_kernel<PT, NR, FR>, kMax);
+    static LdsLimit lds_limit;
+    (void)set_lds_limit_once(lds_limit, (const void*)final_kernel<PT, NR, FR>, kMax);
     const int ngroups = a.rf.plan ? a.B : (a.B + NR - 1) / NR;  // <= 65535 (row limit)
     const dim3 grid((a.S + FR - 1) / FR, ngroups);
     final_kernel<PT, NR, FR><<<grid, 256, lds, st>>>(a);
