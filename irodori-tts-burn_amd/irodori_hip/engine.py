@@ -160,6 +160,11 @@ class HipInferenceEngine:
             self.ctx, row, ts.shape[0], _fp(ts), tm.ctypes.data_as(u8), t_aux,
             _fp(a) if t_aux else None, am.ctypes.data_as(u8) if t_aux else None))
 
+    def clear_context_kv(self) -> None:
+        """Forget every row's cached context (irodori_clear_ctx_kv), so that the next bundle
+        may have another length."""
+        _check(self.lib.irodori_clear_ctx_kv(self.ctx))
+
     def read_context_kv(self, layer: int, row: int, t_ctx: int):
         """The cached context of (layer, row): k, v [t_ctx, H, Dh], mask [t_ctx]."""
         H, Dh = self.cfg.num_heads, self.cfg.head_dim
