@@ -18,7 +18,7 @@ caller.
 """
 from __future__ import annotations
 
-import dataclasses
+from concurrent.futures import ThreadPoolExecutor
 from dataclasses import dataclass
 from typing import Optional
 
@@ -213,20 +213,29 @@ class InferenceEngine:
             raise IrodoriError("UnsupportedMode", "the model has no caption conditioner")
         p.validate(has_speaker=has_speaker, has_caption=has_caption)
 
-        text_state, text_m = m.text.forward(tmask, ids=ids)
-        aux_state = aux_m = None
+        aux_job = None
         if has_speaker:
             lat = np.ascontiguousarray(request.ref_latent, np.float32)
             rm = request.ref_mask if request.ref_mask is not None else np.ones(lat.shape[:2], np.uint8)
             if lat.shape[0] != B or lat.shape[1] > m.max_aux:
                 raise IrodoriError("Shape", "ref_latent must be [batch, <= %d frames, latent_dim]" % m.max_aux)
-            aux_state, aux_m = m.aux.forward(np.ascontiguousarray(rm, np.uint8), latent=lat)
+            aux_job = lambda: m.aux.forward(np.ascontiguousarray(rm, np.uint8), latent=lat)  # noqa: E731
         elif has_caption:
             cids = np.ascontiguousarray(request.caption_ids, np.int32)
             cm = request.caption_mask if request.caption_mask is not None else np.ones(cids.shape, np.uint8)
             if cids.shape[0] != B or cids.shape[1] > m.max_aux:
                 raise IrodoriError("Shape", "caption_ids must be [batch, <= %d tokens]" % m.max_aux)
-            aux_state, aux_m = m.aux.forward(np.ascontiguousarray(cm, np.uint8), ids=cids)
+            aux_job = lambda: m.aux.forward(np.ascontiguousarray(cm, np.uint8), ids=cids)  # noqa: E731
+        # The two encoders are independent objects with streams of their own, and the library
+        # calls release the GIL: the auxiliary one runs on a second host thread beside the text one.
+        aux_state = aux_m = None
+        if aux_job is None:
+            text_state, text_m = m.text.forward(tmask, ids=ids)
+        else:
+            with ThreadPoolExecutor(max_workers=1) as pool:
+                fut = pool.submit(aux_job)
+                text_state, text_m = m.text.forward(tmask, ids=ids)
+                aux_state, aux_m = fut.result()
 
         # One bundle per CFG role and utterance, role-major (row r * B + u): the role keeps or
         # drops the text and the auxiliary segment.
