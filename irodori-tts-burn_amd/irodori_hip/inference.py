@@ -174,7 +174,9 @@ class InferenceEngine:
         self.close()
 
     def with_sampling(self, params: SamplerParams) -> "InferenceEngine":
-        """A new engine with the same loaded model and other sampling parameters."""
+        """A new engine with the same loaded model and other sampling parameters.  The
+        reference's with_sampling consumes the engine; here both stay usable and share the
+        GPU model, which close() on either releases."""
         return InferenceEngine(self._config, None, params, self._device, self._backend, 0, 0, 0, 0, _model=self._m)
 
     def model_config(self) -> ModelConfig:
