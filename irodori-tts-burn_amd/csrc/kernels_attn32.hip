@@ -429,7 +429,10 @@ __global__ __launch_bounds__(64 * QB * KVS) __attribute__((amdgpu_waves_per_eu(1
     // tile's scores into the current ones).  Tile step j consumes sc (tile j's scores) and
     // leaves tile j + 1's scores in sn.
     f32x16 sn[2];
-    auto tile_step = [&](const int j, f32x16 (&sc)[2], f32x16 (&sn)[2]) {
+    // FIRST: the wavefront's first tile (j = 0), whose reference comes from the tile's own
+    // max before any exponential (the later tiles move it only when their sums overflow).
+    auto tile_step = [&](auto first_c, const int j, f32x16 (&sc)[2], f32x16 (&sn)[2]) {
+        constexpr bool FIRST = decltype(first_c)::value;
         // K_{j+1} and V_j have landed once this wave's loads are done and all waves met.
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         raw_barrier();
@@ -462,13 +465,33 @@ __global__ __launch_bounds__(64 * QB * KVS) __attribute__((amdgpu_waves_per_eu(1
         // Softmax of tile j against the current reference, on the VALU, while the scores
         // of tile j + 1 run on the matrix core.  (Those are computed unconditionally to keep
         // one scheduling region; without a next tile the slot holds stale data and the
-        // result is dropped.)  The reference is corrected afterwards, off the common path:
-        // the tile max is needed only on the wavefront's first tile, or when a lane's sum
-        // shows a probability that may exceed 2^TAU (any p > 2^TAU makes the sum exceed it;
-        // an overflow to +inf does too).
+        // result is dropped.)  The wavefront's first tile sets the reference from its max
+        // before the exponentials; later tiles correct it afterwards, off the common path,
+        // only when a lane's sum shows a probability that may exceed 2^TAU (any p > 2^TAU
+        // makes the sum exceed it; an overflow to +inf does too).
         // The next tile's scores subtract the reference in use now (qbias is updated below),
         // so a moved reference also shifts the scores already computed into sn.
         score_tile<T>(sn, kring + (((j + 1) & 1) * KVS + par) * TILE_BYTES, fr, fh, qf, ones, qbias);
+        if constexpr (FIRST) {
+            // The reference is the tile max (rounded to T; both key halves of a query), taken
+            // before the exponentials; O and l are still zero.
+            float m16[16];
+#pragma unroll
+            for (int e = 0; e < 16; e++) m16[e] = fmaxf(sc[0][e], sc[1][e]);
+#pragma unroll
+            for (int w = 8; w > 0; w >>= 1)
+#pragma unroll
+                for (int e = 0; e < w; e++) m16[e] = fmaxf(m16[e], m16[e + w]);
+            m_ref = round_to<T>(max_halves(m16[0]));
+#pragma unroll
+            for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    sc[kb][e] -= m_ref;
+                    sn[kb][e] -= m_ref;
+                }
+            if (fh == 0) qbias[0] = static_cast<T>(-m_ref);
+        }
         float psum = 0.f;
         V8 pf[4];
 #pragma unroll
@@ -486,7 +509,7 @@ __global__ __launch_bounds__(64 * QB * KVS) __attribute__((amdgpu_waves_per_eu(1
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
         }
-        const unsigned long long over = __ballot(first || !(psum <= kSumMax));
+        const unsigned long long over = FIRST ? 0ull : __ballot(!(psum <= kSumMax));
         if (over) {
             // Lanes l and l ^ 32 hold one query's two key halves: either one asks for both.
             const bool need = ((over >> lane) | (over >> (lane ^ 32))) & 1ull;
@@ -501,7 +524,7 @@ __global__ __launch_bounds__(64 * QB * KVS) __attribute__((amdgpu_waves_per_eu(1
             const float mx = max_halves(m16[0]);
             const float nref = need ? round_to<T>(m_ref + mx) : m_ref;
             const float delta = nref - m_ref;
-            const float corr = first ? 0.f : fast_exp2(-delta);
+            const float corr = fast_exp2(-delta);
             m_ref = nref;
 #pragma unroll
             for (int db = 0; db < 2; db++) o[db] *= corr;
@@ -527,9 +550,10 @@ __global__ __launch_bounds__(64 * QB * KVS) __attribute__((amdgpu_waves_per_eu(1
 #pragma unroll
             for (int g = 0; g < 4; g++) o[db] = mma32x16(vf[db][g], pf[g], o[db]);
     };
-    for (int j = 0; j < niter; j += 2) {
-        tile_step(j, s, sn);
-        if (j + 1 < niter) tile_step(j + 1, sn, s);
+    if (niter > 0) tile_step(std::true_type{}, 0, s, sn);
+    for (int j = 1; j < niter; j += 2) {
+        tile_step(std::false_type{}, j, sn, s);
+        if (j + 1 < niter) tile_step(std::false_type{}, j + 1, s, sn);
     }
 #undef ATT_ISSUE
     float m_run = first ? -INFINITY : m_ref;
