@@ -384,7 +384,7 @@ int irodori_encoder_forward(irodori_encoder* enc, int batch, int seq, const int3
 typedef struct irodori_codec irodori_codec;
 
 typedef struct irodori_codec_config {
-    int32_t latent_dim;    /* 32: codebook_dim (bottleneck.rs) */
+    int32_t latent_dim;    /* 32: codebook_dim (bottleneck.rs); <= 1024 */
     int32_t proj_dim;      /* 1024: quantizer.out_proj output channels, multiple of 8 */
     int32_t decoder_dim;   /* 1536: stem output; block i maps dim >> i to dim >> (i + 1) */
     int32_t num_blocks;    /* 4, at most IRODORI_CODEC_MAX_BLOCKS */

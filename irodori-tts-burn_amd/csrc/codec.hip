@@ -387,8 +387,8 @@ int irodori_codec_create(int device, const irodori_codec_config* cfg, irodori_co
                 "codec compute_dtype must be IRODORI_DTYPE_BF16 or IRODORI_DTYPE_F32");
     IRO_REQUIRE(g.num_blocks >= 1 && g.num_blocks <= IRODORI_CODEC_MAX_BLOCKS, IRODORI_ERR_CONFIG,
                 "codec num_blocks must be in [1, 8]");
-    IRO_REQUIRE(g.latent_dim > 0 && g.proj_dim > 0 && g.proj_dim % 8 == 0, IRODORI_ERR_SHAPE,
-                "codec latent_dim must be positive and proj_dim a positive multiple of 8");
+    IRO_REQUIRE(g.latent_dim > 0 && g.latent_dim <= 1024 && g.proj_dim > 0 && g.proj_dim % 8 == 0, IRODORI_ERR_SHAPE,
+                "codec latent_dim must be in [1, 1024] and proj_dim a positive multiple of 8");
     IRO_REQUIRE(g.decoder_dim > 0 && g.decoder_dim % (8 << g.num_blocks) == 0, IRODORI_ERR_SHAPE,
                 "codec decoder_dim must be a multiple of 8 * 2^num_blocks (the channels halve per block)");
     long hop = 1;

@@ -44,32 +44,41 @@ __device__ __forceinline__ void load8(const T* p, float (&v)[8]) {
     }
 }
 
-// quantizer.out_proj (bottleneck.rs:21-23, a k 1 Conv1d): one thread per 8 output
-// channels of an operand row: s[r] = W lat[r - halo] + b over Cl latent channels, zeros in
-// the halos.  W [Pp, Cl] and b [Pp] f32, zero past the real channels.
+// quantizer.out_proj (bottleneck.rs:21-23, a k 1 Conv1d): s[r] = W lat[r - halo] + b over
+// Cl latent channels, zeros in the halos.  W [Pp, Cl] and b [Pp] f32, zero past the real
+// channels.  A workgroup owns kCodecInRows operand rows and 256 output channels: the rows'
+// latents sit in LDS (read as broadcasts), and thread o walks weight row o once, feeding
+// every row's accumulator in the order c = 0 .. Cl - 1 before adding b[o].
+constexpr int kCodecInRows = 8;
+
 template <typename T>
 __global__ __launch_bounds__(256) void codec_in_kernel(const float* __restrict__ lat, int frames, int Cl,
                                                        const float* __restrict__ w, const float* __restrict__ b,
                                                        int Pp, int halo, T* __restrict__ s) {
-    const int c8 = Pp / 8;
-    const long idx = (long)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= (long)(frames + 2 * halo) * c8) return;
-    const int r = (int)(idx / c8), o = (int)(idx % c8) * 8;
-    const int t = r - halo;
-    float v[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) v[i] = 0.f;
-    if (t >= 0 && t < frames) {
-        const float* lr = lat + (size_t)t * Cl;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const float* wr = w + (size_t)(o + i) * Cl;
-            float acc = 0.f;
-            for (int c = 0; c < Cl; c++) acc = fmaf(wr[c], lr[c], acc);
-            v[i] = acc + b[o + i];
-        }
+    extern __shared__ float ls[];  // [kCodecInRows][Cl]
+    const int r0 = blockIdx.x * kCodecInRows, rows = frames + 2 * halo;
+    const int o = blockIdx.y * 256 + threadIdx.x;
+    for (int i = threadIdx.x; i < kCodecInRows * Cl; i += 256) {
+        const int t = r0 + i / Cl - halo;
+        ls[i] = (t >= 0 && t < frames) ? lat[(size_t)t * Cl + i % Cl] : 0.f;
     }
-    store8<T>(s + (size_t)r * Pp + o, v);
+    __syncthreads();
+    if (o >= Pp) return;
+    float acc[kCodecInRows];
+#pragma unroll
+    for (int r = 0; r < kCodecInRows; r++) acc[r] = 0.f;
+    const float* wr = w + (size_t)o * Cl;
+    for (int c = 0; c < Cl; c++) {
+        const float wc = wr[c];
+#pragma unroll
+        for (int r = 0; r < kCodecInRows; r++) acc[r] = fmaf(wc, ls[r * Cl + c], acc[r]);
+    }
+    const float bo = b[o];
+#pragma unroll
+    for (int r = 0; r < kCodecInRows; r++) {
+        const int t = r0 + r - halo;
+        if (r0 + r < rows) s[(size_t)(r0 + r) * Pp + o] = static_cast<T>(t >= 0 && t < frames ? acc[r] + bo : 0.f);
+    }
 }
 
 // WmHead (decoder.rs WmHead::forward) fused with its Snake: wav[t] = tanh(b + sum_j sum_c
@@ -152,8 +161,10 @@ inline unsigned blocks_for(long n) { return (unsigned)((n + 255) / 256); }
 template <typename T>
 void launch_codec_in(const float* lat, int frames, int Cl, const float* w, const float* b, int Pp, int halo, T* s,
                      hipStream_t st) {
-    const long n = (long)(frames + 2 * halo) * (Pp / 8);
-    if (n > 0) codec_in_kernel<T><<<blocks_for(n), 256, 0, st>>>(lat, frames, Cl, w, b, Pp, halo, s);
+    const int rows = frames + 2 * halo;
+    if (rows <= 0 || Pp <= 0) return;
+    const dim3 grid((unsigned)((rows + kCodecInRows - 1) / kCodecInRows), (unsigned)((Pp + 255) / 256));
+    codec_in_kernel<T><<<grid, 256, sizeof(float) * kCodecInRows * Cl, st>>>(lat, frames, Cl, w, b, Pp, halo, s);
 }
 
 template <typename T>

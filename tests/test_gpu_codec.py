@@ -126,6 +126,9 @@ def test_codec_errors_are_reported():
     with pytest.raises(ih.IrodoriError) as ei:
         ih.HipDacVaeCodec(ih.CodecConfig(latent_dim=4, proj_dim=32, decoder_dim=72, rates=(2, 2)), F32)
     assert ei.value.kind == "Shape"  # channels do not halve to multiples of 8
+    with pytest.raises(ih.IrodoriError) as ei:
+        ih.HipDacVaeCodec(ih.CodecConfig(latent_dim=1025, proj_dim=32, decoder_dim=64, rates=(2, 4)), F32)
+    assert ei.value.kind == "Shape" and "latent_dim" in str(ei.value)
     # At the reference widths the 192-channel stream of 6000 latent frames is 960 x 6000 x 192
     # f32 values (4.4 GB), more than one GEMM operand may span: refused at creation.
     with pytest.raises(ih.IrodoriError) as ei:
