@@ -74,7 +74,7 @@ __device__ __forceinline__ f32x16 mma32x16(f16x8 a, f16x8 b, f32x16 c) {
 constexpr int KT = 64;
 constexpr int TILE_BYTES = KT * 128;  // 64 rows x 128 bytes (bf16 Dh = 64)
 constexpr float TAU = 16.0f;          // lazy-reference slack, log2 units
-constexpr float kSumMax = 65536.0f;   // 2^TAU: a lane's tile sum above it moves the reference
+constexpr float kSumMax = (float)(1u << (int)TAU);  // a lane's tile sum above it moves the reference
 
 __device__ __forceinline__ void raw_barrier() { asm volatile("s_barrier" ::: "memory"); }
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, unsigned bytes) {
