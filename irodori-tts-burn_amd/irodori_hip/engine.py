@@ -37,6 +37,59 @@ def _c32(a) -> np.ndarray:
     return np.ascontiguousarray(a, dtype=np.float32)
 
 
+def _shaped(a, shape, what: str, dtype=np.float32) -> np.ndarray:
+    """a as a C-contiguous array of dtype with exactly `shape`: the library reads that many
+    elements through the pointer, so any other shape is refused before the call."""
+    if a is None:
+        raise IrodoriError("InvalidArg", "%s is missing" % what)
+    arr = np.ascontiguousarray(a, dtype)
+    if arr.shape != tuple(shape):
+        raise IrodoriError("Shape", "%s must be %s, got %s" % (what, tuple(shape), arr.shape))
+    return arr
+
+
+def dit_weight_shapes(cfg: DitConfig):
+    """Shapes of DitWeights (Burn [d_in, d_out] layouts): io and per-block entries; the
+    ada_* entries are [2 norms][3 chunks] lists of the given shape."""
+    D, P, F, r, HD = cfg.model_dim, cfg.latent_dim, cfg.mlp_hidden, cfg.adaln_rank, cfg.num_heads * cfg.head_dim
+    io = {"cond_w0": (cfg.timestep_embed_dim, D), "cond_w1": (D, D), "cond_w2": (D, 3 * D), "in_w": (P, D),
+          "in_b": (D,), "out_norm_w": (D,), "out_w": (D, P), "out_b": (P,)}
+    block = {"w_qkv": (D, 3 * HD), "w_gate": (D, D), "w_o": (HD, D), "q_norm": (cfg.num_heads, cfg.head_dim),
+             "k_norm": (cfg.num_heads, cfg.head_dim), "w13": (D, 2 * F), "w2": (F, D),
+             "ada_down": (D, r), "ada_up": (r, D), "ada_up_b": (D,)}
+    return io, block
+
+
+def codec_weight_shapes(cfg: CodecConfig):
+    """Shapes of CodecWeights (Burn layouts, codec/weights.rs): io entries and, per decoder
+    block, its entries (the res_* ones per residual unit).  Biases may also be None."""
+    C0, hd, P = cfg.decoder_dim, cfg.head_dim, cfg.proj_dim
+    io = {"out_proj_w": (P, cfg.latent_dim, 1), "out_proj_b": (P,), "stem_w": (C0, P, 7), "stem_b": (C0,),
+          "head_alpha": (hd,), "head_w": (1, hd, 7), "head_b": (1,)}
+    blocks = []
+    for i, r in enumerate(cfg.rates):
+        cin, cout = cfg.block_dims(i)
+        blocks.append({"alpha": (cin,), "convt_w": (cin, cout, 2 * r), "convt_b": (cout,), "res_alpha0": (cout,),
+                       "res_conv_w": (cout, cout, 7), "res_conv_b": (cout,), "res_alpha1": (cout,),
+                       "res_pw_w": (cout, cout, 1), "res_pw_b": (cout,)})
+    return io, blocks
+
+
+def encoder_weight_shapes(cfg: EncoderConfig):
+    """Shapes of EncoderWeights: io (the input embedding or projection, the output norm) and
+    per-block entries."""
+    E, F, H = cfg.dim, cfg.mlp_hidden, cfg.num_heads
+    io = {"out_norm": (E,)}
+    if cfg.vocab_size:
+        io["embedding"] = (cfg.vocab_size, E)
+    if cfg.in_dim:
+        io["in_w"] = (cfg.in_dim, E)
+        io["in_b"] = (E,)
+    block = {"attn_norm": (E,), "wq": (E, E), "wk": (E, E), "wv": (E, E), "wo": (E, E), "w_gate": (E, E),
+             "q_norm": (H, E // H), "k_norm": (H, E // H), "mlp_norm": (E,), "w13": (E, 2 * F), "w2": (F, E)}
+    return io, block
+
+
 def sampler_params_c(p: SamplerParams, has_speaker: bool = True, has_caption: bool = False,
                      ctx_aux_start: int = 0) -> L.SamplerParamsC:
     """irodori_sampler_params from the params and the request facts: whether the condition
@@ -112,49 +165,83 @@ class HipInferenceEngine:
 
     # ---- weights / context --------------------------------------------------------------
     def load_weights(self, w: DitWeights) -> None:
-        io = L.IoWeightsC(*[_fp(w.io[k]) for k in ("cond_w0", "cond_w1", "cond_w2", "in_w",
-                                                     "in_b", "out_norm_w", "out_w", "out_b")])
-        _check(self.lib.irodori_load_io_weights(self.ctx, C.byref(io)))
+        ios, bs = dit_weight_shapes(self.cfg)
+        if len(w.blocks) != self.cfg.num_layers:
+            raise IrodoriError("Shape", "%d blocks of weights for %d layers" % (len(w.blocks), self.cfg.num_layers))
+        # Every array is checked before the first upload, so a refusal loads nothing.
+        io_arrs = [_shaped(w.io.get(k), ios[k], "io." + k) for k in ("cond_w0", "cond_w1", "cond_w2", "in_w",
+                                                                     "in_b", "out_norm_w", "out_w", "out_b")]
+        plain = ("w_qkv", "w_gate", "w_o", "q_norm", "k_norm", "w13", "w2")
+        blocks = []
         for l, b in enumerate(w.blocks):
+            arrs = {k: _shaped(b.get(k), bs[k], "blocks[%d].%s" % (l, k)) for k in plain}
+            for k in ("ada_down", "ada_up", "ada_up_b"):
+                rows = b.get(k)
+                if rows is None or len(rows) != 2 or any(len(r) != 3 for r in rows):
+                    raise IrodoriError("Shape", "blocks[%d].%s must be 2 x 3 arrays" % (l, k))
+                arrs[k] = [[_shaped(rows[i][ch], bs[k], "blocks[%d].%s[%d][%d]" % (l, k, i, ch)) for ch in range(3)]
+                           for i in range(2)]
+            blocks.append(arrs)
+        io = L.IoWeightsC(*[_fp(a) for a in io_arrs])
+        _check(self.lib.irodori_load_io_weights(self.ctx, C.byref(io)))
+        for l, arrs in enumerate(blocks):
             s = L.BlockWeightsC()
-            for k in ("w_qkv", "w_gate", "w_o", "q_norm", "k_norm", "w13", "w2"):
-                setattr(s, k, _fp(b[k]))
-            for i in range(2):
-                for ch in range(3):
-                    s.ada_down[i][ch] = _fp(b["ada_down"][i][ch])
-                    s.ada_up[i][ch] = _fp(b["ada_up"][i][ch])
-                    s.ada_up_b[i][ch] = _fp(b["ada_up_b"][i][ch])
+            for k in plain:
+                setattr(s, k, _fp(arrs[k]))
+            for k in ("ada_down", "ada_up", "ada_up_b"):
+                for i in range(2):
+                    for ch in range(3):
+                        getattr(s, k)[i][ch] = _fp(arrs[k][i][ch])
             _check(self.lib.irodori_load_block_weights(self.ctx, l, C.byref(s)))
 
     def set_context_kv(self, ctx: ContextKV) -> None:
         _check(self.lib.irodori_clear_ctx_kv(self.ctx))
         Lc, B, T = ctx.k.shape[:3]
+        kv = (Lc, B, T, self.cfg.num_heads, self.cfg.head_dim)
+        ks, vs = _shaped(ctx.k, kv, "context k"), _shaped(ctx.v, kv, "context v")
+        ms = _shaped(ctx.mask, (B, T), "context mask", np.uint8)
         for l in range(Lc):
             for r in range(B):
-                k = _c32(ctx.k[l, r])
-                v = _c32(ctx.v[l, r])
-                m = np.ascontiguousarray(ctx.mask[r], np.uint8)
+                k = ks[l, r]
+                v = vs[l, r]
+                m = ms[r]
                 _check(self.lib.irodori_set_ctx_kv(self.ctx, l, r, T, _fp(k), _fp(v),
                                                    m.ctypes.data_as(C.POINTER(C.c_uint8))))
 
     def load_ctx_proj_weights(self, w: CtxProjWeights) -> None:
         """Upload every layer's context projections (wk/wv_text, wk/wv_speaker|caption)."""
-        for l, lw in enumerate(w.layers):
-            s = L.CtxProjWeightsC(_fp(lw["wk_text"]), _fp(lw["wv_text"]),
-                                  _fp(lw["wk_aux"]) if w.aux_dim else None,
-                                  _fp(lw["wv_aux"]) if w.aux_dim else None)
+        if len(w.layers) != self.cfg.num_layers:
+            raise IrodoriError("Shape", "%d layers of context projections for %d layers"
+                               % (len(w.layers), self.cfg.num_layers))
+        HD = self.cfg.num_heads * self.cfg.head_dim
+        keys = ("wk_text", "wv_text", "wk_aux", "wv_aux") if w.aux_dim else ("wk_text", "wv_text")
+        layers = [{k: _shaped(lw.get(k), (w.text_dim if k.endswith("text") else w.aux_dim, HD),
+                              "layers[%d].%s" % (l, k)) for k in keys} for l, lw in enumerate(w.layers)]
+        for l, a in enumerate(layers):
+            s = L.CtxProjWeightsC(_fp(a["wk_text"]), _fp(a["wv_text"]),
+                                  _fp(a["wk_aux"]) if w.aux_dim else None,
+                                  _fp(a["wv_aux"]) if w.aux_dim else None)
             _check(self.lib.irodori_load_ctx_proj_weights(self.ctx, l, w.text_dim, w.aux_dim,
                                                           C.byref(s)))
+        self._ctx_dims = (w.text_dim, w.aux_dim)
 
     def build_context_kv(self, row: int, text_state: np.ndarray, text_mask: np.ndarray,
                          aux_state: np.ndarray = None, aux_mask: np.ndarray = None) -> None:
         """build_kv_cache (attention.rs:431-501) of batch row `row` on the device, every layer:
         text_state [t_text, text_dim], aux_state [t_aux, aux_dim] (None: no aux keys)."""
+        text_dim, aux_dim = getattr(self, "_ctx_dims", (None, None))
+        if text_dim is None:
+            raise IrodoriError("NotLoaded", "load_ctx_proj_weights first")
         ts = _c32(text_state)
-        tm = np.ascontiguousarray(text_mask, np.uint8)
+        if ts.ndim != 2:
+            raise IrodoriError("Shape", "text_state must be [tokens, %d]" % text_dim)
+        ts = _shaped(ts, (ts.shape[0], text_dim), "text_state")
+        tm = _shaped(text_mask, (ts.shape[0],), "text_mask", np.uint8)
         t_aux = 0 if aux_state is None else aux_state.shape[0]
-        a = _c32(aux_state) if t_aux else None
-        am = np.ascontiguousarray(aux_mask, np.uint8) if t_aux else None
+        if t_aux and not aux_dim:
+            raise IrodoriError("NotLoaded", "no auxiliary context projection is loaded")
+        a = _shaped(aux_state, (t_aux, aux_dim), "aux_state") if t_aux else None
+        am = _shaped(aux_mask, (t_aux,), "aux_mask", np.uint8) if t_aux else None
         u8 = C.POINTER(C.c_uint8)
         _check(self.lib.irodori_build_ctx_kv(
             self.ctx, row, ts.shape[0], _fp(ts), tm.ctypes.data_as(u8), t_aux,
@@ -182,8 +269,11 @@ class HipInferenceEngine:
         latent_mask [B,S] (nonzero = the latent key attends) masks latent keys
         (optimized.rs:102-113, attention.rs:730-750); None = every key attends."""
         x_t = _c32(x_t)
-        t = _c32(t)
+        if x_t.ndim != 3:
+            raise IrodoriError("Shape", "x_t must be [B, S, latent_dim]")
         B, S, P = x_t.shape
+        x_t = _shaped(x_t, (B, S, self.cfg.latent_dim), "x_t")
+        t = _shaped(t, (B,), "t")
         v = np.empty_like(x_t)
         dbg = (np.empty((self.cfg.num_layers + 1, B, S, self.cfg.model_dim), np.float32)
                if debug else None)
@@ -202,8 +292,13 @@ class HipInferenceEngine:
     def block_forward(self, layer: int, x: np.ndarray, cond: np.ndarray) -> np.ndarray:
         """One DiffusionBlock::forward_fused on x [B,S,D] with cond_module output [B,3D]."""
         x = _c32(x).copy()
+        if x.ndim != 3:
+            raise IrodoriError("Shape", "x must be [B, S, model_dim]")
         B, S, _ = x.shape
-        _check(self.lib.irodori_block_forward(self.ctx, layer, B, S, _fp(x), _fp(_c32(cond))))
+        D = self.cfg.model_dim
+        x = _shaped(x, (B, S, D), "x")
+        cond = _shaped(cond, (B, 3 * D), "cond")
+        _check(self.lib.irodori_block_forward(self.ctx, layer, B, S, _fp(x), _fp(cond)))
         return x
 
     def sample(self, x0: np.ndarray, params: SamplerParams, has_speaker: bool = True,
@@ -214,7 +309,10 @@ class HipInferenceEngine:
         attends to its first lengths[u] latent frames (padded variable-length batch).
         ctx_aux_start: first aux key of the context (used by speaker-KV scaling)."""
         x0 = _c32(x0)
+        if x0.ndim != 3:
+            raise IrodoriError("Shape", "x0 must be [utterances, S, latent_dim]")
         U, S, P = x0.shape
+        x0 = _shaped(x0, (U, S, self.cfg.latent_dim), "x0")
         out = np.empty_like(x0)
         pc = sampler_params_c(params, has_speaker, has_caption, ctx_aux_start)
         if lengths is None:
@@ -304,28 +402,38 @@ class HipEncoder:
         self.close()
 
     def load_weights(self, w: EncoderWeights) -> None:
-        io = L.EncoderIoWeightsC(*[_fp(w.io[k]) if k in w.io else None
+        ios, bs = encoder_weight_shapes(self.cfg)
+        if len(w.blocks) != self.cfg.num_layers:
+            raise IrodoriError("Shape", "%d blocks of weights for %d layers" % (len(w.blocks), self.cfg.num_layers))
+        io_arrs = {k: _shaped(w.io.get(k), ios[k], "io." + k) for k in ios}
+        blocks = [[_shaped(b.get(k), bs[k], "blocks[%d].%s" % (l, k)) for k in L.ENC_BLOCK_FIELDS]
+                  for l, b in enumerate(w.blocks)]
+        io = L.EncoderIoWeightsC(*[_fp(io_arrs[k]) if k in io_arrs else None
                                    for k in ("embedding", "in_w", "in_b", "out_norm")])
         _check(self.lib.irodori_encoder_load_io_weights(self.enc, C.byref(io)))
-        for l, b in enumerate(w.blocks):
-            s = L.EncoderBlockWeightsC(*[_fp(_c32(b[k])) for k in L.ENC_BLOCK_FIELDS])
+        for l, arrs in enumerate(blocks):
+            s = L.EncoderBlockWeightsC(*[_fp(a) for a in arrs])
             _check(self.lib.irodori_encoder_load_block_weights(self.enc, l, C.byref(s)))
 
     def forward(self, mask: np.ndarray, ids: np.ndarray = None, latent: np.ndarray = None):
         """mask [B, S]; ids [B, S] (token encoder) or latent [B, S, in_dim] ->
         (state [B, S + mean_token, dim], mask_out [B, S + mean_token])."""
         mask = np.ascontiguousarray(mask, np.uint8)
+        if mask.ndim != 2:
+            raise IrodoriError("Shape", "mask must be [B, S]")
         B, S = mask.shape
+        if (ids is None) == (latent is None):
+            raise IrodoriError("InvalidArg", "give either token ids or latent frames")
         Tn = S + int(self.cfg.mean_token)
         out = np.empty((B, Tn, self.cfg.dim), np.float32)
         mo = np.empty((B, Tn), np.uint8)
         u8 = C.POINTER(C.c_uint8)
         idp = lat = None
         if ids is not None:
-            ids = np.ascontiguousarray(ids, np.int32)
+            ids = _shaped(ids, (B, S), "ids", np.int32)
             idp = ids.ctypes.data_as(C.POINTER(C.c_int32))
         if latent is not None:
-            lat = _c32(latent)
+            lat = _shaped(latent, (B, S, self.cfg.in_dim), "latent")
         _check(self.lib.irodori_encoder_forward(self.enc, B, S, idp, _fp(lat) if lat is not None else None,
                                                 mask.ctypes.data_as(u8), _fp(out), mo.ctypes.data_as(u8)))
         return out, mo
@@ -375,29 +483,44 @@ class HipDacVaeCodec:
         return int(self.lib.irodori_codec_hop_length(self.codec))
 
     def load_weights(self, w: CodecWeights) -> None:
-        def p(a):
-            return _fp(_c32(a)) if a is not None else None
-
+        """Burn layouts (codec/weights.rs); biases may be None (zero)."""
+        cfg = self.cfg
         keep = []
-        blocks = (L.CodecBlockWeightsC * self.cfg.num_blocks)()
+
+        def p(a, shape, what, optional=False):
+            if a is None and optional:
+                return None
+            keep.append(_shaped(a, shape, what))
+            return _fp(keep[-1])
+
+        if len(w.blocks) != cfg.num_blocks:
+            raise IrodoriError("Shape", "%d decoder blocks of weights for %d" % (len(w.blocks), cfg.num_blocks))
+        ios, bss = codec_weight_shapes(cfg)
+        blocks = (L.CodecBlockWeightsC * cfg.num_blocks)()
         for i, b in enumerate(w.blocks):
-            s = blocks[i]
-            s.alpha, s.convt_w, s.convt_b = p(b["alpha"]), p(b["convt_w"]), p(b["convt_b"])
+            s, bs = blocks[i], bss[i]
+            s.alpha = p(b.get("alpha"), bs["alpha"], "blocks[%d].alpha" % i)
+            s.convt_w = p(b.get("convt_w"), bs["convt_w"], "blocks[%d].convt_w" % i)
+            s.convt_b = p(b.get("convt_b"), bs["convt_b"], "blocks[%d].convt_b" % i, True)
             for k in ("res_alpha0", "res_conv_w", "res_conv_b", "res_alpha1", "res_pw_w", "res_pw_b"):
                 arr = getattr(s, k)
                 for u in range(3):
-                    arr[u] = p(b[k][u])
-            keep.append(b)
+                    arr[u] = p(b[k][u], bs[k], "blocks[%d].%s[%d]" % (i, k, u), k.endswith("_b"))
         io = w.io
-        cw = L.CodecWeightsC(p(io["out_proj_w"]), p(io["out_proj_b"]), p(io["stem_w"]), p(io["stem_b"]),
-                             blocks, p(io["head_alpha"]), p(io["head_w"]), p(io["head_b"]))
+        cw = L.CodecWeightsC(*[p(io.get(k), ios[k], "io." + k, k.endswith("_b")) for k in
+                               ("out_proj_w", "out_proj_b", "stem_w", "stem_b")],
+                             blocks, *[p(io.get(k), ios[k], "io." + k, k.endswith("_b")) for k in
+                                       ("head_alpha", "head_w", "head_b")])
         _check(self.lib.irodori_codec_load_weights(self.codec, C.byref(cw)))
         del keep
 
     def decode(self, latent: np.ndarray) -> np.ndarray:
         """latent [B, T, latent_dim] -> wav [B, 1, T * hop_length] (host arrays)."""
         lat = _c32(latent)
+        if lat.ndim != 3:
+            raise IrodoriError("Shape", "latent must be [B, T, latent_dim]")
         B, T, _ = lat.shape
+        lat = _shaped(lat, (B, T, self.cfg.latent_dim), "latent")
         wav = np.empty((B, 1, T * self.cfg.hop_length), np.float32)
         _check(self.lib.irodori_codec_decode(self.codec, B, T, _fp(lat), _fp(wav)))
         return wav
