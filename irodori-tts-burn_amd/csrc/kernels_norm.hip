@@ -91,17 +91,34 @@ __global__ __launch_bounds__(256) void norm_mod_kernel(const float* __restrict__
     const float* base = mod_base(mt, row / S, layer, kind, D);
     const float* shift = base;
     const float* scale = base + D;
+    // Every chunk's scale / shift loads go out together after the reduction, before the first
+    // store (one cache round trip per row, not one per chunk): one straight-line body when D
+    // fills the chunks, a guarded one otherwise.
+    auto body = [&](auto full_c) {
+        constexpr bool FULL = decltype(full_c)::value;
+        float4 sc[NCH], sh[NCH];
 #pragma unroll
-    for (int j = 0; j < NCH; j++) {
-        int d = lane * 4 + 256 * j;
-        if (d >= D) break;
-        float4 sc = *reinterpret_cast<const float4*>(scale + d);
-        float4 sh = *reinterpret_cast<const float4*>(shift + d);
-        const float h0 = v[j].x / rms * (1.f + sc.x) + sh.x, h1 = v[j].y / rms * (1.f + sc.y) + sh.y;
-        const float h2 = v[j].z / rms * (1.f + sc.z) + sh.z, h3 = v[j].w / rms * (1.f + sc.w) + sh.w;
-        if (h) store4<T>(h + (size_t)row * D + d, h0, h1, h2, h3);
-        if (q8) mx_store4_group8(h0, h1, h2, h3, q8 + (size_t)row * D + d, q8s + (size_t)row * (D / 32) + d / 32, lane);
-    }
+        for (int j = 0; j < NCH; j++) {
+            const int d = lane * 4 + 256 * j;
+            if (FULL || d < D) {
+                sc[j] = *reinterpret_cast<const float4*>(scale + d);
+                sh[j] = *reinterpret_cast<const float4*>(shift + d);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < NCH; j++) {
+            const int d = lane * 4 + 256 * j;
+            if (!FULL && d >= D) break;
+            const float h0 = v[j].x / rms * (1.f + sc[j].x) + sh[j].x, h1 = v[j].y / rms * (1.f + sc[j].y) + sh[j].y;
+            const float h2 = v[j].z / rms * (1.f + sc[j].z) + sh[j].z, h3 = v[j].w / rms * (1.f + sc[j].w) + sh[j].w;
+            if (h) store4<T>(h + (size_t)row * D + d, h0, h1, h2, h3);
+            if (q8)
+                mx_store4_group8(h0, h1, h2, h3, q8 + (size_t)row * D + d, q8s + (size_t)row * (D / 32) + d / 32,
+                                 lane);
+        }
+    };
+    if (D == 256 * NCH) body(std::true_type{});
+    else body(std::false_type{});
 }
 
 // The fused adaLN's operand of one (layer, kind) from the residual x: h = x (1 + scale)
