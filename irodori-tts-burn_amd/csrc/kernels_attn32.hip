@@ -471,10 +471,10 @@ __global__ __launch_bounds__(64 * QB * KVS) __attribute__((amdgpu_waves_per_eu(1
         // makes the sum exceed it; an overflow to +inf does too).
         // The next tile's scores subtract the reference in use now (qbias is updated below),
         // so a moved reference also shifts the scores already computed into sn.
-        score_tile<T>(sn, kring + (((j + 1) & 1) * KVS + par) * TILE_BYTES, fr, fh, qf, ones, qbias);
         if constexpr (FIRST) {
             // The reference is the tile max (rounded to T; both key halves of a query), taken
-            // before the exponentials; O and l are still zero.
+            // before the exponentials and before the next tile's scores, which then subtract
+            // it inside their MFMAs like every later tile's; O and l are still zero.
             float m16[16];
 #pragma unroll
             for (int e = 0; e < 16; e++) m16[e] = fmaxf(sc[0][e], sc[1][e]);
@@ -486,12 +486,10 @@ __global__ __launch_bounds__(64 * QB * KVS) __attribute__((amdgpu_waves_per_eu(1
 #pragma unroll
             for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-                for (int e = 0; e < 16; e++) {
-                    sc[kb][e] -= m_ref;
-                    sn[kb][e] -= m_ref;
-                }
+                for (int e = 0; e < 16; e++) sc[kb][e] -= m_ref;
             if (fh == 0) qbias[0] = static_cast<T>(-m_ref);
         }
+        score_tile<T>(sn, kring + (((j + 1) & 1) * KVS + par) * TILE_BYTES, fr, fh, qf, ones, qbias);
         float psum = 0.f;
         V8 pf[4];
 #pragma unroll
