@@ -930,6 +930,7 @@ void P(codec_decode)(const orc_codec* cd, int B, int T, const float* latent, flo
             if ((size_t)C * L > cap) cap = (size_t)C * L;
         }
         if ((size_t)cd->proj_dim * T > cap) cap = (size_t)cd->proj_dim * T;
+        if ((size_t)cd->latent_dim * T > cap) cap = (size_t)cd->latent_dim * T;  /* the transposed latent */
     }
     float* a = (float*)malloc(sizeof(float) * cap);
     float* b2 = (float*)malloc(sizeof(float) * cap);

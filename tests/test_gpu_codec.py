@@ -23,6 +23,9 @@ TOL = {F32: 1e-4, BF16: 2e-2}
 CONFIGS = {
     "tiny": ih.codec_tiny,  # rates 3 (odd) and 4; channels 192 -> 96 (K slices straddling taps) -> 48 (padded to 64)
     "even": lambda: ih.CodecConfig(latent_dim=4, proj_dim=32, decoder_dim=64, rates=(2, 4)),
+    # out_proj at the latent limit (its 8 staged latent rows fill 32 KB of LDS) onto 40
+    # channels padded to 64 (a channel block only partly real).
+    "wide_latent": lambda: ih.CodecConfig(latent_dim=1024, proj_dim=40, decoder_dim=64, rates=(2, 4)),
 }
 
 

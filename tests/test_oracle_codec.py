@@ -67,11 +67,14 @@ def test_snake_closed_forms(oracle32):
     assert np.allclose(got, xq[:, 0] + 1.0 / a, rtol=1e-6)
 
 
-@pytest.mark.parametrize("name", ["tiny", "even", "nobias"])
+@pytest.mark.parametrize("name", ["tiny", "even", "nobias", "wide_latent"])
 def test_codec_decode_vs_torch(oracle64, name):
+    # wide_latent: the latent (1024 channels, the library's limit) is the widest array of the
+    # decode, so the oracle's scratch must be sized by it too.
     cfg = {"tiny": ih.codec_tiny(), "even": ih.CodecConfig(latent_dim=4, proj_dim=32, decoder_dim=64,
                                                                rates=(2, 4)),
-           "nobias": ih.codec_tiny()}[name]
+           "nobias": ih.codec_tiny(),
+           "wide_latent": ih.CodecConfig(latent_dim=1024, proj_dim=40, decoder_dim=64, rates=(2, 4))}[name]
     cw = ih.CodecWeights.random(cfg, 3, bias=name != "nobias")
     lat = np.random.default_rng(5).standard_normal((2, 11, cfg.latent_dim)).astype(np.float32)
     got = oracle64.codec_decode(cfg, cw, lat)
