@@ -46,12 +46,14 @@ int tracked_alloc(std::vector<void*>& allocs, uint64_t& total, void** p, size_t 
             return IRODORI_ERR_OOM;
         }
     }
+    allocs.push_back(nullptr);  // the slot first: a throwing push_back must not strand the allocation
     hipError_t e = hipMalloc(p, bytes);
     if (e != hipSuccess) {
+        allocs.pop_back();
         set_last_error(std::string("hipMalloc(") + std::to_string(bytes) + "): " + hipGetErrorString(e));
         return e == hipErrorOutOfMemory ? IRODORI_ERR_OOM : IRODORI_ERR_HIP;
     }
-    allocs.push_back(*p);
+    allocs.back() = *p;
     total += bytes;
     return IRODORI_OK;
 }
