@@ -107,6 +107,41 @@ struct GraphKey {
     }
 };
 
+// Captured sampler graphs, least recently used first out beyond kMax (each executable holds
+// its ~120 kernel nodes and their arguments; a server cycling through many utterance lengths
+// would otherwise keep one per length).  An entry is only dropped on a cache miss, after the
+// capture's stream synchronisation, so no dropped graph is still running.
+struct GraphCache {
+    static constexpr size_t kMax = 64;
+    struct Entry {
+        hipGraphExec_t exec;
+        uint64_t last;
+    };
+    std::map<GraphKey, Entry> map;
+    uint64_t tick = 0;
+    hipGraphExec_t find(const GraphKey& k) {
+        auto it = map.find(k);
+        if (it == map.end()) return nullptr;
+        it->second.last = ++tick;
+        return it->second.exec;
+    }
+    void insert(const GraphKey& k, hipGraphExec_t e) {
+        while (map.size() >= kMax) {
+            auto old = map.begin();
+            for (auto it = map.begin(); it != map.end(); ++it)
+                if (it->second.last < old->second.last) old = it;
+            (void)hipGraphExecDestroy(old->second.exec);
+            map.erase(old);
+        }
+        map[k] = Entry{e, ++tick};
+    }
+    void clear() {
+        for (auto& kv : map) (void)hipGraphExecDestroy(kv.second.exec);
+        map.clear();
+    }
+    size_t size() const { return map.size(); }
+};
+
 struct irodori_ctx {
     int device = 0;
     irodori_dit_config cfg{};
@@ -201,7 +236,7 @@ struct irodori_ctx {
     VecLinJob* d_jobs_down = nullptr;  // L*6 jobs
     VecLinJob* d_jobs_up = nullptr;    // L*6 jobs
 
-    std::map<GraphKey, hipGraphExec_t> graphs;
+    GraphCache graphs;
 };
 
 namespace {
@@ -333,7 +368,6 @@ int ensure_nvec(irodori_ctx* c, int nvec) {
     IRO_HIP_CHECK(hipMemcpy(c->d_jobs_down, down.data(), sizeof(VecLinJob) * L * 6, hipMemcpyHostToDevice));
     IRO_HIP_CHECK(hipMemcpy(c->d_jobs_up, up.data(), sizeof(VecLinJob) * L * 6, hipMemcpyHostToDevice));
     // Cached graphs captured the old table pointers.
-    for (auto& kv : c->graphs) (void)hipGraphExecDestroy(kv.second);
     c->graphs.clear();
     return IRODORI_OK;
 }
@@ -851,7 +885,7 @@ int irodori_ctx_destroy(irodori_ctx* c) {
     if (!c) return IRODORI_OK;
     (void)hipSetDevice(c->device);
     if (c->stream) (void)hipStreamSynchronize(c->stream);
-    for (auto& kv : c->graphs) (void)hipGraphExecDestroy(kv.second);
+    c->graphs.clear();
     for (void* p : c->allocs) (void)hipFree(p);
     for (auto sd : c->side)
         if (sd) (void)hipStreamSynchronize(sd);
@@ -1113,7 +1147,6 @@ int irodori_clear_ctx_kv(irodori_ctx* c) {
     IRO_REQUIRE(c, IRODORI_ERR_INVALID_ARG, "null context");
     c->t_ctx = -1;
     for (auto& lb : c->layers) std::fill(lb.row_set.begin(), lb.row_set.end(), 0);
-    for (auto& kv : c->graphs) (void)hipGraphExecDestroy(kv.second);
     c->graphs.clear();
     return IRODORI_OK;
 }
@@ -1284,7 +1317,6 @@ int irodori_build_ctx_kv(irodori_ctx* c, int row, int t_text, const float* text_
     }
     IRO_HIP_CHECK(hipStreamSynchronize(c->stream));
     if (c->t_ctx != t_ctx) {
-        for (auto& kv : c->graphs) (void)hipGraphExecDestroy(kv.second);
         c->graphs.clear();
     }
     c->t_ctx = t_ctx;
@@ -1340,7 +1372,6 @@ int irodori_set_ctx_kv(irodori_ctx* c, int layer, int row, int t_ctx, const floa
         IRO_TRY(upload_row_mask(c, lb, row, t_ctx, mask));
     }
     if (c->t_ctx != t_ctx) {
-        for (auto& kv : c->graphs) (void)hipGraphExecDestroy(kv.second);
         c->graphs.clear();
     }
     c->t_ctx = t_ctx;
@@ -1622,7 +1653,6 @@ static int sample_device_impl(irodori_ctx* c, const irodori_sampler_params* p, i
         IRO_HIP_CHECK(hipStreamSynchronize(c->stream));
         IRO_TRY(dalloc(c, &c->plan, sizeof(RfEval) * 2 * (size_t)N));
         c->plan_cap = N;
-        for (auto& kv : c->graphs) (void)hipGraphExecDestroy(kv.second);
         c->graphs.clear();
     }
     IRO_TRY(upload(c, c->plan, plan.data(), sizeof(RfEval) * plan.size()));
@@ -1684,9 +1714,8 @@ static int sample_device_impl(irodori_ctx* c, const irodori_sampler_params* p, i
     // One captured graph per distinct evaluation (roles, phase), replayed per step.
     auto graph_for = [&](int roles, int phase, hipGraphExec_t* out) -> int {
         GraphKey key{U, S, c->t_ctx, roles, method, phase, lengths ? 1 : 0, c->kvs_on ? c->kvs_layers : 0};
-        auto it = c->graphs.find(key);
-        if (it != c->graphs.end()) {
-            *out = it->second;
+        if (hipGraphExec_t hit = c->graphs.find(key)) {
+            *out = hit;
             return IRODORI_OK;
         }
         hipGraph_t graph = nullptr;
@@ -1709,7 +1738,7 @@ static int sample_device_impl(irodori_ctx* c, const irodori_sampler_params* p, i
             set_last_error(std::string("graph instantiate: ") + hipGetErrorString(ee));
             return IRODORI_ERR_HIP;
         }
-        c->graphs[key] = exec;
+        c->graphs.insert(key, exec);
         *out = exec;
         return IRODORI_OK;
     };

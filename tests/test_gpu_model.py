@@ -453,3 +453,21 @@ def test_device_allocation_limit_reports_out_of_memory(monkeypatch):
         v = e.forward_with_cond_cached(x, np.array([0.9, 0.35], np.float32))
     assert np.all(np.isfinite(v))
 
+
+
+def test_graph_cache_eviction_keeps_results():
+    """The sampler keeps at most 64 captured graphs, least recently used out first.  70
+    distinct sequence lengths evict the first ones; running the first length again re-captures
+    its graph and gives the same bits as its first run."""
+    cfg = ih.cfg_tiny()
+    w = ih.DitWeights.random(cfg, 0)
+    ctx = ih.make_context_kv(cfg, 1, 6, 2, seed=1)
+    x0 = ih.make_noise(1, 72, cfg.latent_dim, 4)
+    p = joint_params(1)
+    with make_engine(cfg, ih.InferenceBackendKind.HIP_BF16, w, ctx, 2, 72) as e:
+        first = {S: e.sample(x0[:, :S].copy(), p, has_speaker=True) for S in (3, 4)}
+        for S in range(5, 73):
+            e.sample(x0[:, :S].copy(), p, has_speaker=True)
+        for S, ref in first.items():
+            again = e.sample(x0[:, :S].copy(), p, has_speaker=True)
+            assert np.array_equal(again, ref), S
