@@ -293,6 +293,21 @@ def test_cfg4_forward_increments_bf16(oracle32, cfg4, row):
     assert max(errs) < 1e-2 and max(inc) < 2e-2 and rel_l2(v, v_ref) < 1e-2
 
 
+def test_cfg4_sampler_is_deterministic_across_many_runs(cfg4):
+    """Twelve 40-step RF runs of the benchmark configuration, with forward calls of another
+    batch shape between them (other graphs, other cache contents), all bit-identical to the
+    first: the step counter on the device, the last-workgroup step advance and the forked
+    role chains leave no run-to-run state."""
+    cfg, w, ctx, x0 = cfg4
+    xb = np.concatenate([x0, x0])
+    with make_engine(cfg, BF16, w, ctx, 2, 750) as e:
+        first = e.sample(x0, joint_params(40))
+        for i in range(11):
+            if i % 3 == 0:
+                e.forward_with_cond_cached(xb, np.array([0.8, 0.3], np.float32))
+            assert np.array_equal(e.sample(x0, joint_params(40)), first), i
+
+
 def test_cfg4_sample_40_steps_bf16_vs_golden(cfg4):
     # Final 40-step latent against the f32 oracle's, committed by tests/golden/make_golden.py.
     path = os.path.join(HERE, "golden", "cfg4_joint40_final_latent.npy")
